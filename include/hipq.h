@@ -1,0 +1,158 @@
+/*
+ * hipq.h -- C ABI of libhipq, the MI355X (gfx950) quantized-weight matmul library.
+ *
+ * This is the drop-in boundary for Light's quantized matmul path: the
+ * functions below are what a cgo layer (kernels/rocm + internal/hiprt in a
+ * Light tree) binds in place of the CUDA launchers and internal/cudart calls
+ * for this path.  Each declaration cites the reference interface it replaces.
+ *
+ * Conventions
+ *  - Every function returns int: 0 (HQ_OK) on success, a negative HQ_E* code
+ *    for argument / support errors, or a positive hipError_t.  The message
+ *    of the last failure on the calling thread is hq_last_error(), formatted
+ *    like Light's cudart errors: "hipq: <call>: <msg> (code N)"
+ *    (internal/cudart/runtime.go:335-337).
+ *  - Pointers are device pointers unless stated; sizes are element counts.
+ *    Weights are raw GGUF block bytes (dtype/dtype.go:53-60), never repacked.
+ *  - `stream` is last; NULL means the library's current stream
+ *    (hq_stream_set_current; the null stream until set), as Light issues all
+ *    work on one process-wide current stream (internal/cudart/stream.go:22-30).
+ *    All op calls are asynchronous, as cuLaunchKernel is in Light.
+ *  - dtype codes are Light's dtype.DType values (dtype/dtype.go:13-37).
+ *  - Workspace (`ws`, `ws_bytes`): device scratch for the on-GPU q8_1
+ *    activation quantization.  Size it with the matching *_ws_bytes().
+ *    ws == NULL makes the library use a per-device buffer it allocates and
+ *    grows on demand (not capture-safe).
+ */
+#ifndef HIPQ_H
+#define HIPQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t *hq_stream_t; /* == hipStream_t */
+
+enum {
+  HQ_OK = 0,
+  HQ_EINVAL = -1,       /* bad argument (shape, dtype, pointer) */
+  HQ_EUNSUPPORTED = -2, /* dtype / layout not handled by this library */
+  HQ_ENOMEM = -3,       /* workspace too small or allocation failed */
+};
+
+/* dtype.DType codes (dtype/dtype.go:13-37). */
+enum {
+  HQ_F16 = 0, HQ_BF16 = 1, HQ_F32 = 2,
+  HQ_Q8_0 = 17, HQ_Q8_1 = 18, HQ_Q4_K = 21, HQ_Q6_K = 23,
+};
+
+/* ---- errors / version ------------------------------------------------- */
+
+/* Thread-local text of the last failure ("" if none).
+ * Replaces cudart's error rendering (internal/cudart/runtime.go:335-363). */
+const char *hq_last_error(void);
+/* Library ABI version (major*10000 + minor*100 + patch). */
+int hq_version(void);
+
+/* ---- runtime: the internal/cudart roles this path needs ---------------- */
+
+/* cudart.DeviceCount (device/cuda.go:27-39, internal/cudart/runtime.go:40-50). */
+int hq_device_count(int *count);
+/* cudart.SetDevice (internal/cudart/runtime.go:52-62). */
+int hq_set_device(int device);
+/* cudart.Malloc / Free (internal/cudart/runtime.go:64-110); Light's caching
+ * pool (storage/cuda.go:115-245) stays on the Go side. */
+int hq_malloc(void **ptr, size_t bytes);
+int hq_free(void *ptr);
+/* cudart.MemcpyHtoD / DtoH / DtoD and Memset (internal/cudart/runtime.go:150-230).
+ * h2d and d2h are synchronous with respect to `stream` (the host buffer may be
+ * reused on return), as Light's copies are. */
+int hq_memcpy_h2d(void *dst, const void *src, size_t bytes, hq_stream_t stream);
+int hq_memcpy_d2h(void *dst, const void *src, size_t bytes, hq_stream_t stream);
+int hq_memcpy_d2d(void *dst, const void *src, size_t bytes, hq_stream_t stream);
+int hq_memset(void *dst, int value, size_t bytes, hq_stream_t stream);
+/* cudart stream helpers (internal/cudart/stream.go:12-60). */
+int hq_stream_create(hq_stream_t *stream);
+int hq_stream_destroy(hq_stream_t stream);
+int hq_stream_synchronize(hq_stream_t stream);
+int hq_stream_set_current(hq_stream_t stream);
+hq_stream_t hq_stream_get_current(void);
+
+/* GPU trace spans (internal/cudart/gputrace.go:24-101): while tracing, every
+ * op call is bracketed by a pair of HIP events; hq_trace_stop synchronizes
+ * and reports, per kernel family, the call count and total microseconds.
+ * names: caller buffer of n_max * 32 chars; returns the number of entries. */
+int hq_trace_start(void);
+int hq_trace_stop(char *names, int *calls, double *total_us, int n_max);
+
+/* ---- ops ----------------------------------------------------------------- */
+
+/* Workspace bytes hq_matmul_q needs for x (M, K) and weight dtype w_dtype. */
+size_t hq_matmul_q_ws_bytes(int64_t M, int64_t K, int w_dtype);
+
+/* out (M, N) F32 = x (M, K) F32 contiguous @ dequant(w (N, K))^T.
+ * w_dtype: HQ_Q8_0, HQ_Q4_K or HQ_Q6_K.  K must be a multiple of the block
+ * size.  x is quantized on the GPU to q8_1 (see hq_quantize_q8_1) into ws,
+ * then M <= 8 runs the wave-per-row int8-dot GEMV and larger M (Q4_K) the
+ * MFMA GEMM.
+ * Replaces registry kernel "matmul_q" (ops/matmul_q.go:61-75; CUDA launcher
+ * kernels/cuda/matmul_q.go:44-91) and, since it serves every M, the M >= 8
+ * dequant + cuBLAS fallback (ops/matmul_q.go:52-59, 85-95). */
+int hq_matmul_q(const float *x, const void *w, float *out, int64_t M, int64_t N, int64_t K, int w_dtype,
+                void *ws, size_t ws_bytes, hq_stream_t stream);
+
+/* Dequantize n elements of GGUF blocks to F32 or BF16 (bit-exact with Light's
+ * CPU decoders; BF16 rounds the F32 value once, RNE).
+ * Replaces the "dequant" hook (quant/cuda_hook.go:17-69, kernels/cuda/dequant.go:39-80). */
+int hq_dequant(const void *src, void *dst, int64_t n, int src_dtype, int out_dtype, hq_stream_t stream);
+
+/* Quantize x (M, K) (F32, BF16 or F16) to q8_1 blocks (M, K/32) x 36 bytes:
+ * [f16 d][f16 s][i8 q[32]] (quant/q8_1.go:10-18) with encodeQ8_0's rounding
+ * (quant/quantize.go:70-86): d = amax/127, q = RoundToEven(v * (1/d)),
+ * s = f16(f32(sum q) * d).  No counterpart in Light (which has no q8_1
+ * encoder); bit-exact with the specification. */
+int hq_quantize_q8_1(const void *x, int x_dtype, void *dst, int64_t M, int64_t K, hq_stream_t stream);
+
+/* Workspace bytes hq_int4_matmul needs. */
+size_t hq_int4_matmul_ws_bytes(int64_t M, int64_t K, int G);
+
+/* y (M, N) = x (M, K) @ W^T for Light's canonical 4-bit layout (quant.Int4,
+ * quant/int4.go:11-34): codes U32 (N, K/8), nibble j of word c = W[n, 8c+j];
+ * scales / zeros F32 (N, K/G); W = s * (code - z).  x_dtype F32, BF16 or F16;
+ * y has x's dtype.  K % 32 == 0 and G % 32 == 0.
+ * Replaces registry kernel "int4_gemv" (ops/int4.go:87-99; kernels/cuda/int4.go:76-101)
+ * and, since it serves every M, the dequant + GEMM path (ops/int4.go:100-126). */
+int hq_int4_matmul(const void *x, int x_dtype, const uint32_t *codes, const float *scales, const float *zeros,
+                   void *y, int64_t M, int64_t N, int64_t K, int G, void *ws, size_t ws_bytes,
+                   hq_stream_t stream);
+
+/* Expand canonical 4-bit weights to (N, K) F32 or BF16 at element offset
+ * out_offset of out: s * (q - z) in F32, rounded once (bit-exact with Light).
+ * Replaces registry kernel "int4_dequant" (ops/int4.go:34-56; kernels/cuda/int4.go:43-70). */
+int hq_int4_dequant(const uint32_t *codes, const float *scales, const float *zeros, void *out, int out_dtype,
+                    int64_t N, int64_t K, int G, int64_t out_offset, hq_stream_t stream);
+
+/* Workspace bytes hq_moe_gemm_q needs for `rows` input rows of K elements. */
+size_t hq_moe_gemm_q_ws_bytes(int64_t rows, int64_t K, int w_dtype);
+
+/* Grouped expert qmatmul (ops.MoEGemmQ, ops/moe.go:242-265):
+ *   out[p, :] = w(p) * x[row(p), :] @ dequant(W[e(p)])^T  for every routed pair p,
+ * row(p) = row_per_pair ? p : p / topk, w(p) = topk_w[p] or 1 (topk_w NULL).
+ * x F32 (rows, K); W (E, N, K) GGUF blocks; sorted_pairs / sorted_expts I64 (M)
+ * expert-sorted (MoERouteFromIDs, ops/moe.go:78-99); counts I32 (E) and
+ * offsets I32 (E+1) are scratch the caller zeroes, as Light's op layer
+ * allocates them (ops/moe.go:172-179); out F32 (size_m, N) zeroed by the
+ * caller; pairs outside [0, size_m) are skipped.
+ * Replaces registry kernel "moe_gemm_q" (kernels/cuda/moe.go:78-141). */
+int hq_moe_gemm_q(const float *x, const void *w, const int64_t *sorted_pairs, const int64_t *sorted_expts,
+                  int32_t *counts, int32_t *offsets, const float *topk_w, float *out, int topk, int64_t size_m,
+                  int64_t M, int64_t rows, int64_t E, int64_t N, int64_t K, int row_per_pair, int w_dtype,
+                  void *ws, size_t ws_bytes, hq_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* HIPQ_H */

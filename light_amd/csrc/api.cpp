@@ -1,0 +1,324 @@
+// api.cpp -- libhipq's C ABI: errors, runtime wrappers, trace spans and the
+// validated op entry points.  Kernels live in the .hip translation units.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <map>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "internal.hpp"
+
+namespace hq {
+
+static thread_local char g_err[512] = "";
+static hipStream_t g_current = nullptr;
+
+int fail(int code, const char *call, const char *fmt, ...) {
+  char msg[400];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(msg, sizeof msg, fmt, ap);
+  va_end(ap);
+  snprintf(g_err, sizeof g_err, "hipq: %s: %s (code %d)", call, msg, code);
+  return code;
+}
+
+int check(hipError_t e, const char *call) {
+  if (e == hipSuccess) return HQ_OK;
+  return fail((int)e, call, "%s", hipGetErrorString(e));
+}
+
+hipStream_t resolve(hq_stream_t s) { return s ? (hipStream_t)s : g_current; }
+
+// Per-device workspace, grown on demand.  Growing frees the old buffer after a
+// device sync so no in-flight kernel still reads it.
+static std::mutex g_ws_mu;
+static std::map<int, std::pair<void *, size_t>> g_ws;
+
+int workspace(size_t bytes, hipStream_t stream, void **out, const char *call) {
+  int dev = 0;
+  if (int rc = check(hipGetDevice(&dev), call)) return rc;
+  std::lock_guard<std::mutex> lk(g_ws_mu);
+  auto &slot = g_ws[dev];
+  if (slot.second < bytes) {
+    if (slot.first) {
+      if (int rc = check(hipDeviceSynchronize(), call)) return rc;
+      if (int rc = check(hipFree(slot.first), call)) return rc;
+      slot = {nullptr, 0};
+    }
+    size_t cap = bytes < (1u << 20) ? (1u << 20) : bytes + bytes / 4;
+    void *p = nullptr;
+    if (hipMalloc(&p, cap) != hipSuccess) return fail(HQ_ENOMEM, call, "workspace of %zu bytes", cap);
+    slot = {p, cap};
+  }
+  *out = slot.first;
+  return HQ_OK;
+}
+
+// ---- trace spans ----
+struct TraceRec {
+  int calls = 0;
+  double us = 0;
+};
+static std::mutex g_tr_mu;
+static bool g_tracing = false;
+static std::vector<std::pair<std::string, std::pair<hipEvent_t, hipEvent_t>>> g_spans;
+
+TraceSpan::TraceSpan(const char *n, hipStream_t s) : name(n), stream(s) {
+  if (!g_tracing) return;
+  if (hipEventCreate(&ev0) != hipSuccess || hipEventCreate(&ev1) != hipSuccess) {
+    ev0 = ev1 = nullptr;
+    return;
+  }
+  (void)hipEventRecord(ev0, stream);
+}
+
+TraceSpan::~TraceSpan() {
+  if (!ev0) return;
+  (void)hipEventRecord(ev1, stream);
+  std::lock_guard<std::mutex> lk(g_tr_mu);
+  g_spans.push_back({name, {ev0, ev1}});
+}
+
+}  // namespace hq
+
+using namespace hq;
+
+extern "C" {
+
+const char *hq_last_error(void) { return g_err; }
+int hq_version(void) { return 100; }
+
+int hq_device_count(int *count) {
+  if (!count) return fail(HQ_EINVAL, "hq_device_count", "count is NULL");
+  return check(hipGetDeviceCount(count), "hipGetDeviceCount");
+}
+
+int hq_set_device(int device) { return check(hipSetDevice(device), "hipSetDevice"); }
+
+int hq_malloc(void **ptr, size_t bytes) {
+  if (!ptr) return fail(HQ_EINVAL, "hq_malloc", "ptr is NULL");
+  *ptr = nullptr;
+  if (bytes == 0) return HQ_OK;
+  return check(hipMalloc(ptr, bytes), "hipMalloc");
+}
+
+int hq_free(void *ptr) { return ptr ? check(hipFree(ptr), "hipFree") : HQ_OK; }
+
+int hq_memcpy_h2d(void *dst, const void *src, size_t bytes, hq_stream_t s) {
+  hipStream_t st = resolve(s);
+  if (int rc = check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, st), "hipMemcpyHtoD")) return rc;
+  return check(hipStreamSynchronize(st), "hipStreamSynchronize");
+}
+
+int hq_memcpy_d2h(void *dst, const void *src, size_t bytes, hq_stream_t s) {
+  hipStream_t st = resolve(s);
+  if (int rc = check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, st), "hipMemcpyDtoH")) return rc;
+  return check(hipStreamSynchronize(st), "hipStreamSynchronize");
+}
+
+int hq_memcpy_d2d(void *dst, const void *src, size_t bytes, hq_stream_t s) {
+  return check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, resolve(s)), "hipMemcpyDtoD");
+}
+
+int hq_memset(void *dst, int value, size_t bytes, hq_stream_t s) {
+  return check(hipMemsetAsync(dst, value, bytes, resolve(s)), "hipMemsetAsync");
+}
+
+int hq_stream_create(hq_stream_t *stream) {
+  if (!stream) return fail(HQ_EINVAL, "hq_stream_create", "stream is NULL");
+  hipStream_t s = nullptr;
+  int rc = check(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreate");
+  *stream = (hq_stream_t)s;
+  return rc;
+}
+
+int hq_stream_destroy(hq_stream_t stream) {
+  if (!stream) return HQ_OK;
+  if ((hipStream_t)stream == g_current) g_current = nullptr;
+  return check(hipStreamDestroy((hipStream_t)stream), "hipStreamDestroy");
+}
+
+int hq_stream_synchronize(hq_stream_t stream) {
+  return check(hipStreamSynchronize(resolve(stream)), "hipStreamSynchronize");
+}
+
+int hq_stream_set_current(hq_stream_t stream) {
+  g_current = (hipStream_t)stream;
+  return HQ_OK;
+}
+
+hq_stream_t hq_stream_get_current(void) { return (hq_stream_t)g_current; }
+
+int hq_trace_start(void) {
+  std::lock_guard<std::mutex> lk(g_tr_mu);
+  g_spans.clear();
+  g_tracing = true;
+  return HQ_OK;
+}
+
+int hq_trace_stop(char *names, int *calls, double *total_us, int n_max) {
+  std::vector<std::pair<std::string, std::pair<hipEvent_t, hipEvent_t>>> spans;
+  {
+    std::lock_guard<std::mutex> lk(g_tr_mu);
+    g_tracing = false;
+    spans.swap(g_spans);
+  }
+  std::map<std::string, TraceRec> agg;
+  int rc = HQ_OK;
+  for (auto &sp : spans) {
+    float ms = 0;
+    if (!rc) rc = check(hipEventSynchronize(sp.second.second), "hipEventSynchronize");
+    if (!rc) rc = check(hipEventElapsedTime(&ms, sp.second.first, sp.second.second), "hipEventElapsedTime");
+    auto &r = agg[sp.first];
+    r.calls++;
+    r.us += ms * 1000.0;
+    (void)hipEventDestroy(sp.second.first);
+    (void)hipEventDestroy(sp.second.second);
+  }
+  if (rc) return rc;
+  int i = 0;
+  for (auto &kv : agg) {
+    if (i >= n_max) break;
+    if (names) snprintf(names + 32 * i, 32, "%s", kv.first.c_str());
+    if (calls) calls[i] = kv.second.calls;
+    if (total_us) total_us[i] = kv.second.us;
+    i++;
+  }
+  return i;
+}
+
+// ---------------------------------------------------------------------------
+// ops
+// ---------------------------------------------------------------------------
+
+static bool is_gguf(int dt) { return dt == HQ_Q8_0 || dt == HQ_Q4_K || dt == HQ_Q6_K; }
+
+size_t hq_matmul_q_ws_bytes(int64_t M, int64_t K, int w_dtype) { return matmul_q_ws_bytes(M, K, w_dtype); }
+
+int hq_matmul_q(const float *x, const void *w, float *out, int64_t M, int64_t N, int64_t K, int w_dtype,
+                void *ws, size_t ws_bytes, hq_stream_t stream) {
+  const char *call = "hq_matmul_q";
+  if (!is_gguf(w_dtype)) return fail(HQ_EUNSUPPORTED, call, "weight dtype %d has no fused kernel", w_dtype);
+  if (M < 0 || N < 0 || K <= 0) return fail(HQ_EINVAL, call, "bad shape M=%lld N=%lld K=%lld", (long long)M,
+                                            (long long)N, (long long)K);
+  BlockInfo bi = block_info(w_dtype);
+  if (K % bi.elems)
+    return fail(HQ_EINVAL, call, "K=%lld not a multiple of block size %d", (long long)K, bi.elems);
+  if (M == 0 || N == 0) return HQ_OK;
+  if (!x || !w || !out) return fail(HQ_EINVAL, call, "NULL pointer");
+  if (((uintptr_t)x & 15) || ((uintptr_t)w & 15) || ((uintptr_t)out & 3))
+    return fail(HQ_EINVAL, call, "x and w must be 16-byte aligned, out 4-byte aligned");
+  hipStream_t s = resolve(stream);
+  size_t need = matmul_q_ws_bytes(M, K, w_dtype);
+  if (!ws) {
+    if (int rc = workspace(need, s, &ws, call)) return rc;
+  } else if (ws_bytes < need) {
+    return fail(HQ_ENOMEM, call, "workspace %zu bytes < %zu needed", ws_bytes, need);
+  }
+  TraceSpan span(matmul_q_kernel_name(M, w_dtype), s);
+  return launch_matmul_q(x, w, out, M, N, K, w_dtype, ws, s);
+}
+
+int hq_dequant(const void *src, void *dst, int64_t n, int src_dtype, int out_dtype, hq_stream_t stream) {
+  const char *call = "hq_dequant";
+  if (!is_gguf(src_dtype) && src_dtype != HQ_Q8_1)
+    return fail(HQ_EUNSUPPORTED, call, "source dtype %d", src_dtype);
+  if (out_dtype != HQ_F32 && out_dtype != HQ_BF16) return fail(HQ_EUNSUPPORTED, call, "out dtype %d", out_dtype);
+  BlockInfo bi = block_info(src_dtype);
+  if (n < 0 || n % bi.elems) return fail(HQ_EINVAL, call, "n=%lld not a multiple of %d", (long long)n, bi.elems);
+  if (n == 0) return HQ_OK;
+  if (!src || !dst) return fail(HQ_EINVAL, call, "NULL pointer");
+  hipStream_t s = resolve(stream);
+  TraceSpan span("dequant", s);
+  return launch_dequant(src, dst, n, src_dtype, out_dtype, s);
+}
+
+int hq_quantize_q8_1(const void *x, int x_dtype, void *dst, int64_t M, int64_t K, hq_stream_t stream) {
+  const char *call = "hq_quantize_q8_1";
+  if (x_dtype != HQ_F32 && x_dtype != HQ_BF16 && x_dtype != HQ_F16)
+    return fail(HQ_EUNSUPPORTED, call, "x dtype %d", x_dtype);
+  if (M < 0 || K < 0 || K % 32) return fail(HQ_EINVAL, call, "K=%lld not a multiple of 32", (long long)K);
+  if (M == 0 || K == 0) return HQ_OK;
+  if (!x || !dst) return fail(HQ_EINVAL, call, "NULL pointer");
+  hipStream_t s = resolve(stream);
+  TraceSpan span("quantize_q8_1", s);
+  return launch_quantize_q8_1(x, x_dtype, dst, M, K, s);
+}
+
+size_t hq_int4_matmul_ws_bytes(int64_t M, int64_t K, int G) { return int4_ws_bytes(M, K, G); }
+
+int hq_int4_matmul(const void *x, int x_dtype, const uint32_t *codes, const float *scales, const float *zeros,
+                   void *y, int64_t M, int64_t N, int64_t K, int G, void *ws, size_t ws_bytes,
+                   hq_stream_t stream) {
+  const char *call = "hq_int4_matmul";
+  if (x_dtype != HQ_F32 && x_dtype != HQ_BF16 && x_dtype != HQ_F16)
+    return fail(HQ_EUNSUPPORTED, call, "activations dtype %d, want F32, BF16 or F16", x_dtype);
+  if (M < 0 || N < 0 || K <= 0 || G <= 0 || K % G)
+    return fail(HQ_EINVAL, call, "group %d does not divide K %lld", G, (long long)K);
+  if (K % 32 || G % 32) return fail(HQ_EUNSUPPORTED, call, "K=%lld and G=%d must be multiples of 32", (long long)K, G);
+  if (M == 0 || N == 0) return HQ_OK;
+  if (!x || !codes || !scales || !zeros || !y) return fail(HQ_EINVAL, call, "NULL pointer");
+  hipStream_t s = resolve(stream);
+  size_t need = int4_ws_bytes(M, K, G);
+  if (!ws) {
+    if (int rc = workspace(need, s, &ws, call)) return rc;
+  } else if (ws_bytes < need) {
+    return fail(HQ_ENOMEM, call, "workspace %zu bytes < %zu needed", ws_bytes, need);
+  }
+  TraceSpan span("int4_matmul", s);
+  return launch_int4_matmul(x, x_dtype, codes, scales, zeros, y, M, N, K, G, ws, s);
+}
+
+int hq_int4_dequant(const uint32_t *codes, const float *scales, const float *zeros, void *out, int out_dtype,
+                    int64_t N, int64_t K, int G, int64_t out_offset, hq_stream_t stream) {
+  const char *call = "hq_int4_dequant";
+  if (G <= 0 || K <= 0 || K % G) return fail(HQ_EINVAL, call, "group %d does not divide K %lld", G, (long long)K);
+  if (K % 8) return fail(HQ_EINVAL, call, "K=%lld not a multiple of 8", (long long)K);
+  if (out_dtype != HQ_F32 && out_dtype != HQ_BF16) return fail(HQ_EUNSUPPORTED, call, "out dtype %d", out_dtype);
+  if (N < 0 || out_offset < 0) return fail(HQ_EINVAL, call, "bad N or offset");
+  if (N == 0) return HQ_OK;
+  if (!codes || !scales || !zeros || !out) return fail(HQ_EINVAL, call, "NULL pointer");
+  hipStream_t s = resolve(stream);
+  TraceSpan span("int4_dequant", s);
+  return launch_int4_dequant(codes, scales, zeros, out, out_dtype, N, K, G, out_offset, s);
+}
+
+size_t hq_moe_gemm_q_ws_bytes(int64_t rows, int64_t K, int w_dtype) {
+  if (rows <= 0 || K <= 0 || K % 32) return 0;
+  return ((size_t)rows * (size_t)(K / 32) * 36 + 255) & ~(size_t)255;
+}
+
+int hq_moe_gemm_q(const float *x, const void *w, const int64_t *sorted_pairs, const int64_t *sorted_expts,
+                  int32_t *counts, int32_t *offsets, const float *topk_w, float *out, int topk, int64_t size_m,
+                  int64_t M, int64_t rows, int64_t E, int64_t N, int64_t K, int row_per_pair, int w_dtype,
+                  void *ws, size_t ws_bytes, hq_stream_t stream) {
+  const char *call = "hq_moe_gemm_q";
+  if (!is_gguf(w_dtype)) return fail(HQ_EUNSUPPORTED, call, "weight dtype %d has no fused kernel", w_dtype);
+  if (E <= 0 || N < 0 || K <= 0 || M < 0 || size_m < 0 || rows < 0 || topk < 1)
+    return fail(HQ_EINVAL, call, "bad shape");
+  BlockInfo bi = block_info(w_dtype);
+  if (K % bi.elems) return fail(HQ_EINVAL, call, "K=%lld not a multiple of block size %d", (long long)K, bi.elems);
+  if (row_per_pair ? rows != M : rows != M / topk)
+    return fail(HQ_EINVAL, call, "input rows %lld must be M=%lld (per pair) or M/topk=%lld (per token)",
+                (long long)rows, (long long)M, (long long)(M / topk));
+  if (M == 0 || N == 0) return HQ_OK;
+  if (!x || !w || !sorted_pairs || !sorted_expts || !counts || !offsets || !out)
+    return fail(HQ_EINVAL, call, "NULL pointer");
+  hipStream_t s = resolve(stream);
+  size_t need = hq_moe_gemm_q_ws_bytes(rows, K, w_dtype);
+  if (!ws) {
+    if (int rc = workspace(need, s, &ws, call)) return rc;
+  } else if (ws_bytes < need) {
+    return fail(HQ_ENOMEM, call, "workspace %zu bytes < %zu needed", ws_bytes, need);
+  }
+  TraceSpan span("moe_gemm_q", s);
+  if (int rc = launch_quantize_q8_1(x, HQ_F32, ws, rows, K, s)) return rc;
+  return launch_moe_q(ws, w, sorted_pairs, sorted_expts, counts, offsets, topk_w, out, topk, size_m, M, E, N, K,
+                      row_per_pair, w_dtype, s);
+}
+
+}  // extern "C"

@@ -1,0 +1,58 @@
+// internal.hpp -- host-side helpers shared by the libhipq entry points.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "common.hpp"
+
+namespace hq {
+
+// Record a failure for hq_last_error() and return `code`.
+int fail(int code, const char *call, const char *fmt, ...) __attribute__((format(printf, 3, 4)));
+// Map a hipError_t to the return convention (0 or the positive HIP code).
+int check(hipError_t e, const char *call);
+// Check the most recent kernel launch.
+inline int check_launch(const char *call) { return check(hipGetLastError(), call); }
+// NULL -> the library's current stream.
+hipStream_t resolve(hq_stream_t s);
+// Library-owned, grow-on-demand device workspace of the current device.
+int workspace(size_t bytes, hipStream_t stream, void **out, const char *call);
+
+// Trace span: brackets one op call with HIP events while hq_trace_start is active.
+struct TraceSpan {
+  TraceSpan(const char *name, hipStream_t s);
+  ~TraceSpan();
+  const char *name;
+  hipStream_t stream;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+};
+
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// ---- kernel launchers (one translation unit each) ----
+int launch_quantize_q8_1(const void *x, int x_dtype, void *dst, int64_t M, int64_t K, hipStream_t s);
+int launch_dequant(const void *src, void *dst, int64_t n, int src_dtype, int out_dtype, hipStream_t s);
+// matmul_q: quantizes x into ws when the int8 path applies, then runs the GEMV
+// (M <= kGemvMaxRows) or the MFMA GEMM (Q4_K, larger M).
+constexpr int64_t kGemvMaxRows = 8;
+size_t matmul_q_ws_bytes(int64_t M, int64_t K, int dt);
+int launch_matmul_q(const float *x, const void *w, float *out, int64_t M, int64_t N, int64_t K, int dt, void *ws,
+                    hipStream_t s);
+const char *matmul_q_kernel_name(int64_t M, int dt);
+// GEMV on pre-quantized q8_1 activations (shared with the MoE path for tests).
+int launch_gemv_q8(const void *xq, const void *w, float *out, int64_t M, int64_t N, int64_t K, int dt,
+                   hipStream_t s);
+int launch_gemm_q4k(const void *xq, const void *w, float *out, int64_t M, int64_t N, int64_t K, void *ws,
+                    hipStream_t s);
+size_t gemm_q4k_ws_bytes(int64_t M, int64_t K);
+int device_cus();
+int launch_int4_dequant(const uint32_t *codes, const float *s, const float *z, void *out, int out_dtype,
+                        int64_t N, int64_t K, int G, int64_t off, hipStream_t st);
+int launch_int4_matmul(const void *x, int x_dtype, const uint32_t *codes, const float *s, const float *z, void *y,
+                       int64_t M, int64_t N, int64_t K, int G, void *ws, hipStream_t st);
+size_t int4_ws_bytes(int64_t M, int64_t K, int G);
+int launch_moe_q(const void *xq, const void *w, const int64_t *pairs, const int64_t *expts, int32_t *counts,
+                 int32_t *offsets, const float *topk_w, float *out, int topk, int64_t size_m, int64_t M,
+                 int64_t E, int64_t N, int64_t K, int row_per_pair, int dt, hipStream_t s);
+
+}  // namespace hq

@@ -1,0 +1,72 @@
+// quantize.hip -- on-GPU q8_1 activation quantizer.
+//
+// Block of 32 -> [f16 d][f16 s][i8 q[32]] (quant/q8_1.go:10-18).  Rounding follows
+// Light's encodeQ8_0 (quant/quantize.go:70-86): d = amax / 127 (f32), id = 1 / d
+// from the unrounded d, q = RoundToEven(v * id); s = f16(f32(sum q) * d).
+// Eight lanes own one block (four elements each); amax and sum q are reduced
+// with xor shuffles inside the 8-lane group.  All arithmetic is explicitly
+// rounded (__fdiv_rn / __fmul_rn) so the bytes match the CPU quantizer.
+#include "internal.hpp"
+
+namespace hq {
+
+template <int XDT>
+__device__ __forceinline__ void load4(const void *x, int64_t i, float v[4]) {
+  if constexpr (XDT == F32) {
+    float4 f = *reinterpret_cast<const float4 *>(static_cast<const float *>(x) + i);
+    v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
+  } else {
+    uint2 u = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(x) + i);
+    uint32_t h[4] = {u.x & 0xffffu, u.x >> 16, u.y & 0xffffu, u.y >> 16};
+#pragma unroll
+    for (int j = 0; j < 4; j++) v[j] = XDT == BF16 ? bf2f(h[j]) : h2f(h[j]);
+  }
+}
+
+template <int XDT>
+__global__ __launch_bounds__(256) void quantize_q8_1_kernel(const void *__restrict__ x, uint8_t *__restrict__ dst,
+                                                            int64_t nblocks) {
+  int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int64_t blk = t >> 3;
+  int sub = threadIdx.x & 7;
+  bool live = blk < nblocks;
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  if (live) load4<XDT>(x, blk * 32 + sub * 4, v);
+  float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+#pragma unroll
+  for (int o = 4; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 8));
+  float d = __fdiv_rn(amax, 127.0f);
+  float id = d != 0.f ? __fdiv_rn(1.0f, d) : 0.f;
+  int q[4], sum = 0;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    q[j] = (int)rintf(__fmul_rn(v[j], id));
+    sum += q[j];
+  }
+#pragma unroll
+  for (int o = 4; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 8);
+  if (!live) return;
+  uint8_t *o = dst + blk * 36;
+  uint32_t packed = (uint32_t)(q[0] & 0xff) | (uint32_t)(q[1] & 0xff) << 8 | (uint32_t)(q[2] & 0xff) << 16 |
+                    (uint32_t)(q[3] & 0xff) << 24;
+  reinterpret_cast<uint32_t *>(o + 4)[sub] = packed;
+  if (sub == 0) {
+    uint32_t ds = (uint32_t)f2h_rne(d) | (uint32_t)f2h_rne(__fmul_rn((float)sum, d)) << 16;
+    *reinterpret_cast<uint32_t *>(o) = ds;
+  }
+}
+
+int launch_quantize_q8_1(const void *x, int x_dtype, void *dst, int64_t M, int64_t K, hipStream_t s) {
+  int64_t nblocks = M * (K / 32);
+  dim3 grid((unsigned)cdiv(nblocks * 8, 256));
+  auto *d = static_cast<uint8_t *>(dst);
+  switch (x_dtype) {
+    case F32: quantize_q8_1_kernel<F32><<<grid, 256, 0, s>>>(x, d, nblocks); break;
+    case BF16: quantize_q8_1_kernel<BF16><<<grid, 256, 0, s>>>(x, d, nblocks); break;
+    case F16: quantize_q8_1_kernel<F16><<<grid, 256, 0, s>>>(x, d, nblocks); break;
+    default: return fail(HQ_EUNSUPPORTED, "quantize_q8_1", "x dtype %d", x_dtype);
+  }
+  return check_launch("quantize_q8_1");
+}
+
+}  // namespace hq

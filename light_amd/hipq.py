@@ -1,0 +1,224 @@
+"""ctypes binding of libhipq's C ABI (include/hipq.h) for torch device tensors.
+
+This is the Python twin of the cgo stub a Light tree would carry: it passes
+raw device pointers, sizes and Light dtype codes across the C ABI and turns a
+non-zero return into ``HipqError`` carrying ``hq_last_error()``.  There is no
+CPU fallback: if ``libhipq.so`` is missing, importing the op functions raises.
+"""
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libhipq.so")
+
+# Light dtype.DType codes (dtype/dtype.go:13-37).
+F16, BF16, F32 = 0, 1, 2
+Q8_0, Q8_1, Q4_K, Q6_K = 17, 18, 21, 23
+BLOCK = {Q8_0: (32, 34), Q8_1: (32, 36), Q4_K: (256, 144), Q6_K: (256, 210)}
+NAMES = {F16: "F16", BF16: "BF16", F32: "F32", Q8_0: "Q8_0", Q8_1: "Q8_1", Q4_K: "Q4_K", Q6_K: "Q6_K"}
+
+HQ_OK, HQ_EINVAL, HQ_EUNSUPPORTED, HQ_ENOMEM = 0, -1, -2, -3
+
+
+class HipqError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(msg)
+        self.code = code
+
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I = ctypes.c_int
+_SZ = ctypes.c_size_t
+
+# Every exported symbol with its ctypes signature; tests check this list
+# against include/hipq.h.
+SIGNATURES = {
+    "hq_last_error": (ctypes.c_char_p, []),
+    "hq_version": (_I, []),
+    "hq_device_count": (_I, [ctypes.POINTER(_I)]),
+    "hq_set_device": (_I, [_I]),
+    "hq_malloc": (_I, [ctypes.POINTER(_P), _SZ]),
+    "hq_free": (_I, [_P]),
+    "hq_memcpy_h2d": (_I, [_P, _P, _SZ, _P]),
+    "hq_memcpy_d2h": (_I, [_P, _P, _SZ, _P]),
+    "hq_memcpy_d2d": (_I, [_P, _P, _SZ, _P]),
+    "hq_memset": (_I, [_P, _I, _SZ, _P]),
+    "hq_stream_create": (_I, [ctypes.POINTER(_P)]),
+    "hq_stream_destroy": (_I, [_P]),
+    "hq_stream_synchronize": (_I, [_P]),
+    "hq_stream_set_current": (_I, [_P]),
+    "hq_stream_get_current": (_P, []),
+    "hq_trace_start": (_I, []),
+    "hq_trace_stop": (_I, [ctypes.c_char_p, ctypes.POINTER(_I), ctypes.POINTER(ctypes.c_double), _I]),
+    "hq_matmul_q_ws_bytes": (_SZ, [_I64, _I64, _I]),
+    "hq_matmul_q": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _P, _SZ, _P]),
+    "hq_dequant": (_I, [_P, _P, _I64, _I, _I, _P]),
+    "hq_quantize_q8_1": (_I, [_P, _I, _P, _I64, _I64, _P]),
+    "hq_int4_matmul_ws_bytes": (_SZ, [_I64, _I64, _I]),
+    "hq_int4_matmul": (_I, [_P, _I, _P, _P, _P, _P, _I64, _I64, _I64, _I, _P, _SZ, _P]),
+    "hq_int4_dequant": (_I, [_P, _P, _P, _P, _I, _I64, _I64, _I, _I64, _P]),
+    "hq_moe_gemm_q_ws_bytes": (_SZ, [_I64, _I64, _I]),
+    "hq_moe_gemm_q": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I,
+                           _P, _SZ, _P]),
+}
+
+_lib = None
+
+
+def lib():
+    """Load libhipq.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"libhipq.so not built at {LIB_PATH}: run light_amd.build.build()")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def last_error():
+    return lib().hq_last_error().decode()
+
+
+def check(rc):
+    if rc != 0:
+        raise HipqError(rc, last_error())
+    return rc
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(stream=None):
+    import torch
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return ctypes.c_void_p(stream.cuda_stream)
+
+
+def _torch_dtype_code(t):
+    import torch
+    return {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}[t.dtype]
+
+
+def row_bytes(dt, K):
+    be, bb = BLOCK[dt]
+    return K // be * bb
+
+
+# ---------------------------------------------------------------------------
+# Ops (device tensors in, device tensors out; all asynchronous on the stream)
+# ---------------------------------------------------------------------------
+
+def matmul_q(x, w, N, K, w_dtype, out=None, ws=None, stream=None):
+    """out (M, N) f32 = x (M, K) f32 @ dequant(w)^T; w is a uint8 tensor of GGUF blocks."""
+    import torch
+    M = x.shape[0]
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float32, device=x.device)
+    ws_bytes = 0 if ws is None else ws.numel() * ws.element_size()
+    check(lib().hq_matmul_q(_ptr(x), _ptr(w), _ptr(out), M, N, K, w_dtype, _ptr(ws), ws_bytes, _stream(stream)))
+    return out
+
+
+def matmul_q_ws_bytes(M, K, w_dtype):
+    return lib().hq_matmul_q_ws_bytes(M, K, w_dtype)
+
+
+def dequant(src, n, src_dtype, out_dtype=F32, out=None, stream=None):
+    import torch
+    if out is None:
+        out = torch.empty(n, dtype=torch.float32 if out_dtype == F32 else torch.bfloat16, device=src.device)
+    check(lib().hq_dequant(_ptr(src), _ptr(out), n, src_dtype, out_dtype, _stream(stream)))
+    return out
+
+
+def quantize_q8_1(x, out=None, stream=None):
+    import torch
+    M, K = x.shape
+    if out is None:
+        out = torch.empty(M * (K // 32) * 36, dtype=torch.uint8, device=x.device)
+    check(lib().hq_quantize_q8_1(_ptr(x), _torch_dtype_code(x), _ptr(out), M, K, _stream(stream)))
+    return out
+
+
+def int4_matmul(x, codes, scales, zeros, G, out=None, ws=None, stream=None):
+    """y (M, N) at x's dtype = x (M, K) @ W^T, W = s * (code - z) (quant.Int4 layout)."""
+    import torch
+    M, K = x.shape
+    N = codes.shape[0]
+    if out is None:
+        out = torch.empty((M, N), dtype=x.dtype, device=x.device)
+    ws_bytes = 0 if ws is None else ws.numel() * ws.element_size()
+    check(lib().hq_int4_matmul(_ptr(x), _torch_dtype_code(x), _ptr(codes), _ptr(scales), _ptr(zeros), _ptr(out),
+                               M, N, K, G, _ptr(ws), ws_bytes, _stream(stream)))
+    return out
+
+
+def int4_matmul_ws_bytes(M, K, G):
+    return lib().hq_int4_matmul_ws_bytes(M, K, G)
+
+
+def int4_dequant(codes, scales, zeros, G, out_dtype=F32, out=None, out_offset=0, stream=None):
+    import torch
+    N = codes.shape[0]
+    K = codes.shape[1] * 8
+    if out is None:
+        out = torch.empty((N, K), dtype=torch.float32 if out_dtype == F32 else torch.bfloat16, device=codes.device)
+    check(lib().hq_int4_dequant(_ptr(codes), _ptr(scales), _ptr(zeros), _ptr(out), out_dtype, N, K, G, out_offset,
+                                _stream(stream)))
+    return out
+
+
+def moe_gemm_q(x, w, sorted_pairs, sorted_expts, E, N, K, w_dtype, topk, topk_w=None, out=None, counts=None,
+               offsets=None, ws=None, stream=None):
+    """Grouped expert qmatmul with Light's MoEGemmQ contract (ops/moe.go:242-265)."""
+    import torch
+    M = sorted_pairs.numel()
+    rows = x.shape[0]
+    if rows == M:
+        rpp = 1
+    elif rows == M // topk:
+        rpp = 0
+    else:
+        raise HipqError(HQ_EINVAL, f"moe_gemm_q: input rows {rows} must be M={M} or M/topk={M // topk}")
+    dev = x.device
+    if counts is None:
+        counts = torch.zeros(E, dtype=torch.int32, device=dev)
+    if offsets is None:
+        offsets = torch.zeros(E + 1, dtype=torch.int32, device=dev)
+    if out is None:
+        out = torch.zeros((M, N), dtype=torch.float32, device=dev)
+    ws_bytes = 0 if ws is None else ws.numel() * ws.element_size()
+    check(lib().hq_moe_gemm_q(_ptr(x), _ptr(w), _ptr(sorted_pairs), _ptr(sorted_expts), _ptr(counts),
+                              _ptr(offsets), _ptr(topk_w), _ptr(out), topk, out.shape[0], M, rows, E, N, K, rpp,
+                              w_dtype, _ptr(ws), ws_bytes, _stream(stream)))
+    return out
+
+
+def moe_gemm_q_ws_bytes(rows, K, w_dtype):
+    return lib().hq_moe_gemm_q_ws_bytes(rows, K, w_dtype)
+
+
+def trace_start():
+    check(lib().hq_trace_start())
+
+
+def trace_stop(n_max=32):
+    names = ctypes.create_string_buffer(32 * n_max)
+    calls = (_I * n_max)()
+    us = (ctypes.c_double * n_max)()
+    n = lib().hq_trace_stop(names, calls, us, n_max)
+    if n < 0:
+        raise HipqError(n, last_error())
+    out = {}
+    for i in range(n):
+        nm = names.raw[32 * i:32 * (i + 1)].split(b"\0", 1)[0].decode()
+        out[nm] = (calls[i], us[i])
+    return out

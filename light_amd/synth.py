@@ -1,0 +1,145 @@
+"""Seeded synthetic inputs for the five benchmark configurations.
+
+Blocks are written directly from their fields (never produced by a quantizer),
+so every dequantized value is known exactly.  The packers follow Light's block
+layouts and its test builders (buildQ4_KBlock, quant/q4_k_test.go:20-46;
+buildQ6_KBlock, quant/q6_k_test.go:20-59).  Distributions:
+
+* Q8_0:  qs ~ U[-127, 127], d = f16(|N(0,1)| * 0.02 / 127).
+* Q4_K:  6-bit sc, m ~ U[0, 63], q ~ U[0, 15], d and dmin = f16(|N(0,1)| * 1e-3)
+         (the configs leave the Q4_K d / dmin distribution open; this is the
+         stated choice, the same law as Q6_K's d).
+* Q6_K:  raw ~ U[0, 63], int8 sc ~ U[-32, 31], d = f16(|N(0,1)| * 1e-3).
+* int4:  codes u32 uniform, s = f16(|N(0,1)| * 0.01) widened to F32,
+         z ~ U[0, 15] as F32, group 128.
+* MoE:   expert ids uniform without replacement per token, routing weights
+         softmax(N(0,1)) over the topk slots, pairs sorted by expert.
+* Activations ~ N(0,1) (F32, or F16 for int4).
+"""
+import numpy as np
+
+Q8_0, Q4_K, Q6_K = 17, 21, 23
+
+
+def rng(seed):
+    return np.random.Generator(np.random.PCG64(seed))
+
+
+def _f16_bits(v):
+    return np.asarray(v, dtype=np.float32).astype(np.float16).view(np.uint16)
+
+
+def pack_q8_0(d_bits, qs):
+    """d_bits (nb,) uint16, qs (nb, 32) int8 -> (nb*34,) uint8."""
+    nb = d_bits.shape[0]
+    out = np.empty((nb, 34), np.uint8)
+    out[:, 0:2] = d_bits.astype("<u2").view(np.uint8).reshape(nb, 2)
+    out[:, 2:] = qs.astype(np.int8).view(np.uint8)
+    return out.reshape(-1)
+
+
+def pack_q4_k(d_bits, dmin_bits, sc, mn, q):
+    """sc, mn (nb, 8) in [0, 63]; q (nb, 256) in [0, 15] -> (nb*144,) uint8."""
+    nb = d_bits.shape[0]
+    sc = sc.astype(np.uint8)
+    mn = mn.astype(np.uint8)
+    out = np.empty((nb, 144), np.uint8)
+    out[:, 0:2] = d_bits.astype("<u2").view(np.uint8).reshape(nb, 2)
+    out[:, 2:4] = dmin_bits.astype("<u2").view(np.uint8).reshape(nb, 2)
+    s12 = np.empty((nb, 12), np.uint8)
+    s12[:, 0:4] = (sc[:, 0:4] & 0x3F) | ((sc[:, 4:8] & 0x30) << 2)
+    s12[:, 4:8] = (mn[:, 0:4] & 0x3F) | ((mn[:, 4:8] & 0x30) << 2)
+    s12[:, 8:12] = (sc[:, 4:8] & 0x0F) | ((mn[:, 4:8] & 0x0F) << 4)
+    out[:, 4:16] = s12
+    q = q.astype(np.uint8).reshape(nb, 4, 2, 32)  # (p, lo/hi, l)
+    out[:, 16:] = (q[:, :, 0, :] | (q[:, :, 1, :] << 4)).reshape(nb, 128)
+    return out.reshape(-1)
+
+
+def pack_q6_k(d_bits, sc, raw):
+    """sc (nb, 16) int8; raw (nb, 256) in [0, 63] -> (nb*210,) uint8."""
+    nb = d_bits.shape[0]
+    raw = raw.astype(np.uint8).reshape(nb, 2, 4, 32)  # (half, group, l)
+    out = np.empty((nb, 210), np.uint8)
+    r1, r2, r3, r4 = raw[:, :, 0], raw[:, :, 1], raw[:, :, 2], raw[:, :, 3]
+    ql = np.empty((nb, 2, 64), np.uint8)
+    ql[:, :, :32] = (r1 & 0x0F) | ((r3 & 0x0F) << 4)
+    ql[:, :, 32:] = (r2 & 0x0F) | ((r4 & 0x0F) << 4)
+    qh = ((r1 >> 4) & 3) | (((r2 >> 4) & 3) << 2) | (((r3 >> 4) & 3) << 4) | (((r4 >> 4) & 3) << 6)
+    out[:, 0:128] = ql.reshape(nb, 128)
+    out[:, 128:192] = qh.reshape(nb, 64)
+    out[:, 192:208] = sc.astype(np.int8).view(np.uint8)
+    out[:, 208:210] = d_bits.astype("<u2").view(np.uint8).reshape(nb, 2)
+    return out.reshape(-1)
+
+
+def gguf_weight(dt, N, K, g):
+    """Random (N, K) weight in format dt with the config distributions; returns uint8 bytes."""
+    if dt == Q8_0:
+        nb = N * K // 32
+        d = _f16_bits(np.abs(g.standard_normal(nb, dtype=np.float32)) * np.float32(0.02 / 127))
+        qs = g.integers(-127, 128, size=(nb, 32), dtype=np.int8)
+        return pack_q8_0(d, qs)
+    if dt == Q4_K:
+        nb = N * K // 256
+        d = _f16_bits(np.abs(g.standard_normal(nb, dtype=np.float32)) * np.float32(1e-3))
+        dmin = _f16_bits(np.abs(g.standard_normal(nb, dtype=np.float32)) * np.float32(1e-3))
+        sc = g.integers(0, 64, size=(nb, 8), dtype=np.uint8)
+        mn = g.integers(0, 64, size=(nb, 8), dtype=np.uint8)
+        q = g.integers(0, 16, size=(nb, 256), dtype=np.uint8)
+        return pack_q4_k(d, dmin, sc, mn, q)
+    if dt == Q6_K:
+        nb = N * K // 256
+        d = _f16_bits(np.abs(g.standard_normal(nb, dtype=np.float32)) * np.float32(1e-3))
+        sc = g.integers(-32, 32, size=(nb, 16), dtype=np.int8)
+        raw = g.integers(0, 64, size=(nb, 256), dtype=np.uint8)
+        return pack_q6_k(d, sc, raw)
+    raise ValueError(f"dtype {dt}")
+
+
+def activations(M, K, g, dtype=np.float32):
+    return g.standard_normal((M, K), dtype=np.float32).astype(dtype)
+
+
+def int4_weight(N, K, G, g):
+    """Canonical quant.Int4 tensors: codes u32 (N, K/8), scales / zeros f32 (N, K/G)."""
+    codes = g.integers(0, 2 ** 32, size=(N, K // 8), dtype=np.uint64).astype(np.uint32)
+    s = (np.abs(g.standard_normal((N, K // G), dtype=np.float32)) * np.float32(0.01)).astype(np.float16)
+    s = s.astype(np.float32)
+    z = g.integers(0, 16, size=(N, K // G)).astype(np.float32)
+    return codes, s, z
+
+
+def moe_routing(T, E, topk, g):
+    """ids (T*topk,) int64 uniform without replacement per token, weights (T*topk,) f32 softmax(N(0,1))."""
+    ids = np.empty((T, topk), np.int64)
+    for t in range(T):
+        ids[t] = g.choice(E, size=topk, replace=False)
+    logits = g.standard_normal((T, topk)).astype(np.float32)
+    e = np.exp(logits - logits.max(axis=1, keepdims=True))
+    w = (e / e.sum(axis=1, keepdims=True)).astype(np.float32)
+    return ids.reshape(-1), w.reshape(-1)
+
+
+def sort_pairs(ids):
+    """Stable expert sort of the flat ids (MoERouteFromIDs): (sorted_expts, sorted_pairs)."""
+    order = np.argsort(ids, kind="stable")
+    return ids[order].astype(np.int64), order.astype(np.int64)
+
+
+# Named single-GPU workloads of the five configs (seed = config index).
+CONFIGS = {
+    "q8_0_gemv_4096x4096": dict(cfg=0, kind="gguf", dt=Q8_0, M=1, N=4096, K=4096),
+    "q4_k_gemv_gate_14336x4096": dict(cfg=1, kind="gguf", dt=Q4_K, M=1, N=14336, K=4096),
+    "q4_k_gemv_down_4096x14336": dict(cfg=1, kind="gguf", dt=Q4_K, M=1, N=4096, K=14336),
+    "q6_k_gemv_attn_out_4096x4096": dict(cfg=1, kind="gguf", dt=Q6_K, M=1, N=4096, K=4096),
+    "q6_k_gemv_lm_head_128256x4096": dict(cfg=1, kind="gguf", dt=Q6_K, M=1, N=128256, K=4096),
+    "q4_k_gemm_m512_14336x4096": dict(cfg=2, kind="gguf", dt=Q4_K, M=512, N=14336, K=4096),
+    "q4_k_gemm_m512_4096x14336": dict(cfg=2, kind="gguf", dt=Q4_K, M=512, N=4096, K=14336),
+    "int4_m1_18944x3584": dict(cfg=3, kind="int4", M=1, N=18944, K=3584, G=128),
+    "int4_m1_3584x18944": dict(cfg=3, kind="int4", M=1, N=3584, K=18944, G=128),
+    "int4_m64_18944x3584": dict(cfg=3, kind="int4", M=64, N=18944, K=3584, G=128),
+    "int4_m64_3584x18944": dict(cfg=3, kind="int4", M=64, N=3584, K=18944, G=128),
+    "moe_q4_k_t1": dict(cfg=4, kind="moe", dt=Q4_K, T=1, E=128, topk=8, H=2048, I=768),
+    "moe_q4_k_t256": dict(cfg=4, kind="moe", dt=Q4_K, T=256, E=128, topk=8, H=2048, I=768),
+}

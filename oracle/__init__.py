@@ -1,0 +1,276 @@
+"""CPU oracle for Light's quantized-matmul path -- TEST INFRASTRUCTURE ONLY.
+
+A ctypes front end over ``liboracle.so`` (built from ``oracle.c`` by the
+Makefile beside it).  Only ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may import this package, and only as the
+checker or the timed CPU baseline; the product path (``light_amd``) never
+does.
+
+Parity status of each function (how it is pinned):
+
+* ``half_to_f32`` / ``half_from_f32`` / ``bf16_from_f32``: all 65536 f16
+  patterns against numpy's IEEE conversion; f32 -> f16 / bf16 on 2^20 random
+  patterns plus ties against numpy / torch round-to-nearest-even.
+* ``decode_row`` / ``dequant`` (Q8_0, Q4_K, Q6_K): Light's known-answer tests
+  (quant/q4_k_test.go, quant/q6_k_test.go) as golden fixtures, scalar vs AVX2
+  bit identity (Light's TestAVX2DecodersExact), closed forms on special
+  blocks (q = 0, scale = 0, min = 0).
+* ``int4_row`` / ``int4_dequant``: scalar vs AVX2 bit identity; closed forms
+  (codes all equal, z = q) and the BF16 round-once rule.
+* ``dot`` / ``mattb``: intrinsics vs a lane-by-lane scalar encoding of the same
+  order (bit identity), and the f64 bound 1e-5 (1 + sum|x w|).
+* ``matmul_q`` / ``int4_matmul``: the f64 oracle with Light's own bound
+  (ops/matmul_q_cpu_test.go:66-76).
+* ``moe_gemm_q`` / ``moe_route_from_ids`` / ``moe_combine``: Light's routing
+  invariants (ops/moe_test.go:63-88) and a per-expert loop in f64.
+* ``quantize_q8_1``: specification only (Light has no q8_1 encoder): layout,
+  |q| <= 127, round trip within d/2, all-zero block, and the q8_0 encoder
+  (same rounding rule) on the same data.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+
+F16, BF16, F32 = 0, 1, 2
+Q8_0, Q8_1, Q4_K, Q6_K = 17, 18, 21, 23
+BLOCK = {Q8_0: (32, 34), Q8_1: (32, 36), Q4_K: (256, 144), Q6_K: (256, 210)}
+
+_lib = None
+
+
+def build():
+    """Compile liboracle.so with make (gcc)."""
+    import subprocess
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        _lib = ctypes.CDLL(_LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+P = ctypes.c_void_p
+I64 = ctypes.c_int64
+I = ctypes.c_int
+
+
+def _declare(L):
+    sig = {
+        "or_half_to_f32": (ctypes.c_float, [ctypes.c_uint16]),
+        "or_half_from_f32": (ctypes.c_uint16, [ctypes.c_float]),
+        "or_bf16_from_f32": (ctypes.c_uint16, [ctypes.c_float]),
+        "or_half_to_f32_avx2": (None, [P, P, I64]),
+        "or_decode_row": (I, [I, P, I64, P]),
+        "or_decode_row_avx2": (I, [I, P, I64, P]),
+        "or_int4_row": (None, [P, P, P, P, I64, I]),
+        "or_int4_row_avx2": (None, [P, P, P, P, I64, I]),
+        "or_dequant": (I, [I, P, I64, P]),
+        "or_int4_dequant": (I, [P, P, P, P, I, I64, I64, I]),
+        "or_dot_avx2": (ctypes.c_float, [P, P, I64]),
+        "or_dot_lanes": (ctypes.c_float, [P, P, I64]),
+        "or_mattb": (None, [P, I64, P, I64, P, I64, I64, I64, I64]),
+        "or_matmul_q": (I, [P, P, P, I64, I64, I64, I, I]),
+        "or_int4_matmul": (I, [P, P, P, P, P, I64, I64, I64, I, I]),
+        "or_moe_route_from_ids": (None, [P, I64, P, P]),
+        "or_moe_gemm_f32": (I, [P, P, P, P, P, P, I64, I64, I64, I64, I, I, I]),
+        "or_moe_gemm_q": (I, [P, P, I, P, P, P, P, I64, I64, I64, I64, I64, I, I, I, P]),
+        "or_moe_combine": (None, [P, P, I64, I64, I]),
+        "or_quantize_q8_0": (None, [P, I64, P]),
+        "or_quantize_q8_1": (None, [P, I64, P]),
+        "or_matmul_f64": (None, [P, P, I64, I64, I64, P, P, P, P, I]),
+        "or_hw_threads": (I, []),
+    }
+    for name, (res, args) in sig.items():
+        f = getattr(L, name)
+        f.restype = res
+        f.argtypes = args
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _c(a, dt):
+    return np.ascontiguousarray(a, dtype=dt)
+
+
+def hw_threads():
+    return lib().or_hw_threads()
+
+
+def half_to_f32(h):
+    return lib().or_half_to_f32(int(h))
+
+
+def half_from_f32(f):
+    return lib().or_half_from_f32(float(f))
+
+
+def bf16_from_f32(f):
+    return lib().or_bf16_from_f32(float(f))
+
+
+def half_to_f32_avx2(h):
+    h = _c(h, np.uint16)
+    out = np.zeros(h.size, np.float32)
+    lib().or_half_to_f32_avx2(_p(h), _p(out), h.size)
+    return out
+
+
+def decode_row(dt, raw, K, avx2=False):
+    raw = _c(raw, np.uint8)
+    out = np.zeros(K, np.float32)
+    f = lib().or_decode_row_avx2 if avx2 else lib().or_decode_row
+    if f(dt, _p(raw), K, _p(out)) != 0:
+        raise ValueError("decode_row: bad dtype or K")
+    return out
+
+
+def dequant(dt, raw, n):
+    raw = _c(raw, np.uint8)
+    out = np.zeros(n, np.float32)
+    if lib().or_dequant(dt, _p(raw), n, _p(out)) != 0:
+        raise ValueError("dequant: bad dtype or n")
+    return out
+
+
+def int4_row(codes, s, z, K, G, avx2=False):
+    codes, s, z = _c(codes, np.uint32), _c(s, np.float32), _c(z, np.float32)
+    out = np.zeros(K, np.float32)
+    f = lib().or_int4_row_avx2 if avx2 else lib().or_int4_row
+    f(_p(codes), _p(s), _p(z), _p(out), K, G)
+    return out
+
+
+def int4_dequant(codes, s, z, N, K, G, out_dt=F32):
+    codes, s, z = _c(codes, np.uint32), _c(s, np.float32), _c(z, np.float32)
+    out = np.zeros(N * K, np.float32 if out_dt == F32 else np.uint16)
+    if lib().or_int4_dequant(_p(codes), _p(s), _p(z), _p(out), out_dt, N, K, G) != 0:
+        raise ValueError("int4_dequant: bad args")
+    return out.reshape(N, K)
+
+
+def dot(a, b, lanes=False):
+    a, b = _c(a, np.float32), _c(b, np.float32)
+    f = lib().or_dot_lanes if lanes else lib().or_dot_avx2
+    return np.float32(f(_p(a), _p(b), a.size))
+
+
+def mattb(a, w):
+    """out = a @ w.T with Light's MatTB order; a (m, k), w (n, k)."""
+    a, w = _c(a, np.float32), _c(w, np.float32)
+    m, k = a.shape
+    n = w.shape[0]
+    out = np.zeros((m, n), np.float32)
+    lib().or_mattb(_p(a), k, _p(w), k, _p(out), n, m, n, k)
+    return out
+
+
+def matmul_q(x, w_raw, N, K, dt, threads=0):
+    """Light's CPU MatMulQ: x (M, K) f32 times dequant(W)^T -> (M, N) f32."""
+    x = _c(x, np.float32)
+    w_raw = _c(w_raw, np.uint8)
+    M = x.size // K
+    out = np.zeros((M, N), np.float32)
+    if lib().or_matmul_q(_p(x), _p(w_raw), _p(out), M, N, K, dt, threads) != 0:
+        raise ValueError("matmul_q: bad args")
+    return out
+
+
+def int4_matmul(x, codes, s, z, N, K, G, threads=0):
+    x = _c(x, np.float32)
+    codes, s, z = _c(codes, np.uint32), _c(s, np.float32), _c(z, np.float32)
+    M = x.size // K
+    out = np.zeros((M, N), np.float32)
+    if lib().or_int4_matmul(_p(x), _p(codes), _p(s), _p(z), _p(out), M, N, K, G, threads) != 0:
+        raise ValueError("int4_matmul: bad args")
+    return out
+
+
+def moe_route_from_ids(ids):
+    ids = _c(ids, np.int64).ravel()
+    se = np.zeros(ids.size, np.int64)
+    sp = np.zeros(ids.size, np.int64)
+    lib().or_moe_route_from_ids(_p(ids), ids.size, _p(se), _p(sp))
+    return se, sp
+
+
+def moe_gemm_q(x, w_raw, dt, E, N, K, sorted_pairs, sorted_expts, topk, topk_w=None, threads=0,
+               scratch=None):
+    """Light's CPU MoEGemmQ: dequantize the (E, N, K) stack, then moeGemmKernel."""
+    x = _c(x, np.float32)
+    w_raw = _c(w_raw, np.uint8)
+    sp, se = _c(sorted_pairs, np.int64), _c(sorted_expts, np.int64)
+    M = sp.size
+    rows = x.shape[0]
+    if rows == M:
+        rpp = 1
+    elif rows == M // topk:
+        rpp = 0
+    else:
+        raise ValueError("moe_gemm_q: input rows must be M or M/topk")
+    tw = None if topk_w is None else _c(topk_w, np.float32)
+    out = np.zeros((M, N), np.float32)
+    if scratch is not None:
+        assert scratch.dtype == np.float32 and scratch.size >= E * N * K
+    rc = lib().or_moe_gemm_q(_p(x), _p(w_raw), dt, _p(sp), _p(se), _p(tw), _p(out), M, M, E, N, K, topk, rpp,
+                             threads, _p(scratch))
+    if rc != 0:
+        raise ValueError("moe_gemm_q: bad args")
+    return out
+
+
+def moe_gemm_f32(x, w, sorted_pairs, sorted_expts, topk, topk_w=None, threads=0):
+    x, w = _c(x, np.float32), _c(w, np.float32)
+    E, N, K = w.shape
+    sp, se = _c(sorted_pairs, np.int64), _c(sorted_expts, np.int64)
+    M = sp.size
+    rpp = 1 if x.shape[0] == M else 0
+    tw = None if topk_w is None else _c(topk_w, np.float32)
+    out = np.zeros((M, N), np.float32)
+    lib().or_moe_gemm_f32(_p(x), _p(w), _p(sp), _p(se), _p(tw), _p(out), M, M, N, K, topk, rpp, threads)
+    return out
+
+
+def moe_combine(pair_out, topk):
+    pair_out = _c(pair_out, np.float32)
+    M, N = pair_out.shape
+    out = np.zeros((M // topk, N), np.float32)
+    lib().or_moe_combine(_p(pair_out), _p(out), M, N, topk)
+    return out
+
+
+def quantize_q8_0(x):
+    x = _c(x, np.float32).ravel()
+    out = np.zeros(x.size // 32 * 34, np.uint8)
+    lib().or_quantize_q8_0(_p(x), x.size, _p(out))
+    return out
+
+
+def quantize_q8_1(x):
+    x = _c(x, np.float32).ravel()
+    out = np.zeros(x.size // 32 * 36, np.uint8)
+    lib().or_quantize_q8_1(_p(x), x.size, _p(out))
+    return out
+
+
+def matmul_f64(x, w, threads=0):
+    """f64 oracle: returns (ref, mag, wnorm, xnorm) for x (M, K) and dequantized w (N, K)."""
+    x, w = _c(x, np.float32), _c(w, np.float32)
+    M, K = x.shape
+    N = w.shape[0]
+    ref = np.zeros((M, N), np.float64)
+    mag = np.zeros((M, N), np.float64)
+    wn = np.zeros(N, np.float64)
+    xn = np.zeros(M, np.float64)
+    lib().or_matmul_f64(_p(x), _p(w), M, N, K, _p(ref), _p(mag), _p(wn), _p(xn), threads)
+    return ref, mag, wn, xn

@@ -1,0 +1,163 @@
+"""GPU parity of the GGUF path through the C ABI: quantizer, dequant, MatMulQ.
+
+Bars (from the build's north star): dequantized weights and quantized
+activations bit-exact; float outputs within max |err| / (||w_n|| * ||x_m||)
+<= 1e-3 of Light's CPU qmatmul (oracle.matmul_q) and of the f64
+dequant-then-matmul oracle.  Shapes follow TestCUDAMatMulQParity
+(ops/matmul_q_test.go:105-146) plus the benchmark shapes.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from _util import norm_err, random_blocks
+from light_amd import hipq, synth
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3  # max |err| / (||w_n|| ||x_m||)
+FMTS = [hipq.Q8_0, hipq.Q4_K, hipq.Q6_K]
+
+
+def _t(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _check_matmul(dev, dt, x, w, N, K, label):
+    print(f"[case] matmul_q {label} dt={hipq.NAMES[dt]} M={x.shape[0]} N={N} K={K}", flush=True)
+    y = hipq.matmul_q(_t(x, dev), _t(w, dev), N, K, dt)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    cpu = oracle.matmul_q(x, w, N, K, dt)
+    wd = oracle.dequant(dt, w, N * K).reshape(N, K)
+    ref, _, wn, xn = oracle.matmul_f64(x, wd)
+    e_cpu = norm_err(got, cpu, wn, xn)
+    e_f64 = norm_err(got, ref, wn, xn)
+    assert np.all(np.isfinite(got))
+    assert e_cpu <= TOL, f"{label}: vs Light CPU {e_cpu:.3g}"
+    assert e_f64 <= TOL, f"{label}: vs f64 {e_f64:.3g}"
+    return e_cpu
+
+
+# ---- q8_1 activation quantizer -------------------------------------------
+
+@pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16, torch.float16])
+def test_quantize_q8_1_bit_exact(dev, xdt):
+    g = np.random.default_rng(1)
+    M, K = 7, 4096
+    x = (g.standard_normal((M, K)) * np.repeat(10.0 ** g.uniform(-9, 3, size=(M, K // 32)), 32, axis=1))
+    x = x.astype(np.float32)
+    x[0, :32] = 0.0
+    x[1, :32] = 5e-6  # d in Light's f16 flush-to-zero range
+    xt = torch.from_numpy(x).to(xdt)
+    xw = xt.float().numpy()  # the exact widened values the CPU quantizer sees
+    got = hipq.quantize_q8_1(xt.to(dev)).cpu().numpy()
+    want = oracle.quantize_q8_1(xw)
+    bad = np.nonzero(got != want)[0]
+    assert bad.size == 0, f"first mismatch at byte {bad[:8]}"
+
+
+# ---- dequant -------------------------------------------------------------
+
+@pytest.mark.parametrize("dt", FMTS)
+@pytest.mark.parametrize("odt", [hipq.F32, hipq.BF16])
+def test_dequant_bit_exact(dev, dt, odt):
+    g = np.random.default_rng(dt)
+    N, K = 33, 1024
+    raw = random_blocks(g, dt, N, K)
+    got = hipq.dequant(_t(raw, dev), N * K, dt, odt)
+    want = oracle.dequant(dt, raw, N * K)
+    if odt == hipq.F32:
+        assert np.array_equal(got.cpu().numpy().view(np.uint32), want.view(np.uint32))
+    else:
+        wb = torch.from_numpy(want).to(torch.bfloat16).view(torch.int16)
+        assert torch.equal(got.cpu().view(torch.int16), wb)
+
+
+def test_dequant_golden_known_answers(dev):
+    import json
+    import os
+    cases = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "dequant_kat.json")))["cases"]
+    for c in cases:
+        dt = {"Q4_K": hipq.Q4_K, "Q6_K": hipq.Q6_K}[c["dtype"]]
+        raw = np.frombuffer(bytes.fromhex(c["blocks"]), np.uint8).copy()
+        got = hipq.dequant(_t(raw, dev), c["n"], dt).cpu().numpy()
+        if c["checks"] == "all":
+            assert np.array_equal(got, np.array(c["want"], np.float32)), c["name"]
+        else:
+            for i, v in c["want"].items():
+                assert got[int(i)] == np.float32(v), c["name"]
+
+
+def test_dequant_q8_1_roundtrip(dev):
+    g = np.random.default_rng(9)
+    x = g.standard_normal((3, 256)).astype(np.float32)
+    q = hipq.quantize_q8_1(_t(x, dev))
+    y = hipq.dequant(q, 3 * 256, hipq.Q8_1).cpu().numpy()
+    assert np.array_equal(y, oracle.dequant(oracle.Q8_1, q.cpu().numpy(), 3 * 256))
+
+
+# ---- MatMulQ ---------------------------------------------------------------
+
+@pytest.mark.parametrize("dt", FMTS)
+@pytest.mark.parametrize("M", [1, 4, 9])
+@pytest.mark.parametrize("K", [1024, 1792])
+def test_matmul_q_parity_light_shapes(dev, dt, M, K):
+    """TestCUDAMatMulQParity shapes: M in {1,4,9}, K in {1024,1792}, N=13, random blocks."""
+    g = np.random.default_rng(5 * M + K + dt)
+    N = 13
+    if K % oracle.BLOCK[dt][0]:
+        pytest.skip("K not a block multiple")
+    x = (g.random((M, K)) * 2 - 1).astype(np.float32)
+    w = random_blocks(g, dt, N, K)
+    _check_matmul(dev, dt, x, w, N, K, "light_shapes")
+
+
+@pytest.mark.parametrize("dt", FMTS)
+@pytest.mark.parametrize("N,K", [(1, 256), (64, 512), (130, 2048), (257, 4096), (70, 6144), (65, 12288)])
+def test_matmul_q_shapes(dev, dt, N, K):
+    g = np.random.default_rng(N * 7 + K + dt)
+    x = synth.activations(1, K, g)
+    w = synth.gguf_weight(dt, N, K, g)
+    _check_matmul(dev, dt, x, w, N, K, "shapes")
+
+
+@pytest.mark.parametrize("name", ["q8_0_gemv_4096x4096", "q4_k_gemv_gate_14336x4096", "q4_k_gemv_down_4096x14336",
+                                  "q6_k_gemv_attn_out_4096x4096", "q6_k_gemv_lm_head_128256x4096"])
+def test_matmul_q_benchmark_configs(dev, name):
+    c = synth.CONFIGS[name]
+    g = synth.rng(c["cfg"])
+    w = synth.gguf_weight(c["dt"], c["N"], c["K"], g)
+    x = synth.activations(c["M"], c["K"], g)
+    _check_matmul(dev, c["dt"], x, w, c["N"], c["K"], name)
+
+
+def test_matmul_q_zero_and_large_activations(dev):
+    g = np.random.default_rng(3)
+    N, K = 40, 2048
+    w = synth.gguf_weight(hipq.Q4_K, N, K, g)
+    x = np.zeros((2, K), np.float32)
+    x[1] = g.standard_normal(K).astype(np.float32) * 1e4
+    x[1, :256] = 0
+    y = hipq.matmul_q(_t(x, dev), _t(w, dev), N, K, hipq.Q4_K).cpu().numpy()
+    assert np.all(y[0] == 0)
+    _check_matmul(dev, hipq.Q4_K, x[1:], w, N, K, "large")
+
+
+def test_matmul_q_explicit_workspace_and_stream(dev):
+    g = np.random.default_rng(4)
+    N, K = 96, 4096
+    w = _t(synth.gguf_weight(hipq.Q6_K, N, K, g), dev)
+    x = _t(synth.activations(2, K, g), dev)
+    ws = torch.empty(hipq.matmul_q_ws_bytes(2, K, hipq.Q6_K), dtype=torch.uint8, device=dev)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        y1 = hipq.matmul_q(x, w, N, K, hipq.Q6_K, ws=ws)
+    s.synchronize()
+    y2 = hipq.matmul_q(x, w, N, K, hipq.Q6_K)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+    small = torch.empty(16, dtype=torch.uint8, device=dev)
+    with pytest.raises(hipq.HipqError):
+        hipq.matmul_q(x, w, N, K, hipq.Q6_K, ws=small)
