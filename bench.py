@@ -1,0 +1,306 @@
+"""Benchmark of the MI355X quantized-matmul path (BASELINE.json metric).
+
+Headline metric: Q4_K GEMV GB/s at Llama-3-8B MLP decode shapes,
+plus the Q4_K M=512 GEMM TFLOPS.  One "step" is one MLP decode
+pass through the hot path: the gate (14336x4096), up (14336x4096) and down
+(4096x14336) Q4_K projections at M = 1, each an hq_matmul_q call (on-GPU
+q8_1 quantization + GEMV).  Inputs are synthetic (seeded, BASELINE
+distributions), resident in HBM; every weight is rotated over enough copies
+that the working set exceeds the 256 MB Infinity Cache.
+
+`value` is whole-job throughput: algorithmic bytes of a step (weights as
+stored + F32 activations + F32 outputs) / wall time of the K timed steps,
+replayed as captured HIP graphs so host launch cost is not measured.
+`roofline` is for the dominant kernel (the Q4_K GEMV), timed per launch with
+HIP events on its stream.  `cpu_baseline` is Light's AVX2 CPU qmatmul (the
+C restatement in oracle/) on the same step, on this host's cores.
+
+Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--table] [--no-cpu]
+"""
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+MFMA_PEAK_TFLOPS = {"bf16": 2500.0, "int8": 5000.0}
+MALL_BYTES = 256 << 20
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--table", action="store_true", help="also time every config (printed to stderr)")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--launches", type=int, default=200, help="per-kernel timed launches for the roofline")
+    return p.parse_args()
+
+
+def copies_for(nbytes):
+    return max(2, math.ceil(2 * MALL_BYTES / nbytes))
+
+
+class Weight:
+    """A GGUF weight with `n` rotated device copies."""
+
+    def __init__(self, raw, dt, N, K, dev):
+        import torch
+        self.raw, self.dt, self.N, self.K = raw, dt, N, K
+        base = torch.from_numpy(raw).to(dev)
+        self.copies = [base] + [base.clone() for _ in range(copies_for(raw.nbytes) - 1)]
+
+    def __getitem__(self, i):
+        return self.copies[i % len(self.copies)]
+
+
+def mlp_inputs(dev):
+    """Llama-3-8B MLP decode at M = 1, config 1 (seed 1)."""
+    import torch
+    from light_amd import hipq, synth
+    g = synth.rng(1)
+    H, I = 4096, 14336
+    gate = Weight(synth.gguf_weight(hipq.Q4_K, I, H, g), hipq.Q4_K, I, H, dev)
+    up = Weight(synth.gguf_weight(hipq.Q4_K, I, H, g), hipq.Q4_K, I, H, dev)
+    down = Weight(synth.gguf_weight(hipq.Q4_K, H, I, g), hipq.Q4_K, H, I, dev)
+    x = synth.activations(1, H, g)
+    h = synth.activations(1, I, g)
+    return gate, up, down, x, h
+
+
+def step_bytes(ws_list, M):
+    """Algorithmic bytes: weights as stored + F32 x + F32 out, per matmul."""
+    tot = 0
+    for w in ws_list:
+        tot += w.raw.nbytes + 4 * M * w.K + 4 * M * w.N
+    return tot
+
+
+def run_gpu(args):
+    import torch
+    from light_amd import hipq
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    gate, up, down, x_np, h_np = mlp_inputs(dev)
+    x = torch.from_numpy(x_np).to(dev)
+    h = torch.from_numpy(h_np).to(dev)
+    H, I = 4096, 14336
+    ws = torch.empty(max(hipq.matmul_q_ws_bytes(1, H, hipq.Q4_K), hipq.matmul_q_ws_bytes(1, I, hipq.Q4_K)),
+                     dtype=torch.uint8, device=dev)
+    yg = torch.empty((1, I), device=dev)
+    yu = torch.empty((1, I), device=dev)
+    yd = torch.empty((1, H), device=dev)
+    rot = max(len(gate.copies), len(down.copies))
+
+    def step(i):
+        hipq.matmul_q(x, gate[i], I, H, hipq.Q4_K, out=yg, ws=ws)
+        hipq.matmul_q(x, up[i], I, H, hipq.Q4_K, out=yu, ws=ws)
+        hipq.matmul_q(h, down[i], H, I, hipq.Q4_K, out=yd, ws=ws)
+
+    # Eager reference outputs of copy 0, then one graph per weight copy.
+    step(0)
+    torch.cuda.synchronize()
+    eager = (yg.clone(), yu.clone(), yd.clone())
+    # One graph holds `rot` consecutive steps (one per weight copy), so the
+    # replays amortise graph-launch cost; single-step graphs cover a remainder.
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cap):
+        full = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(full, stream=cap):
+            for i in range(rot):
+                step(i)
+        singles = []
+        for i in range(rot):
+            gph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gph, stream=cap):
+                step(i)
+            singles.append(gph)
+    torch.cuda.current_stream().wait_stream(cap)
+    for rep in range(3):  # replays must reproduce the eager result (copies hold identical bytes)
+        (full if rep % 2 else singles[rep]).replay()
+        torch.cuda.synchronize()
+        for a, b in zip((yg, yu, yd), eager):
+            if not torch.equal(a, b):
+                raise RuntimeError("graph replay differs from the eager step")
+        step(1)
+        torch.cuda.synchronize()
+
+    def run_steps(n):
+        for _ in range(n // rot):
+            full.replay()
+        for i in range(n % rot):
+            singles[i].replay()
+
+    run_steps(args.warmup)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    run_steps(args.steps)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    nbytes = step_bytes([gate, up, down], 1)
+    ms_per_step = dt * 1e3 / args.steps
+    value = nbytes * args.steps / dt / 1e9
+
+    roof = gemv_roofline(args, gate, x, dev)
+    return dict(value=value, ms_per_step=ms_per_step, step_bytes=nbytes, roofline=roof,
+                inputs=(gate, up, down, x_np, h_np))
+
+
+def time_launches(fn, n, rot):
+    """Average per-launch duration (us): one HIP event pair on torch's current stream around n
+    back-to-back launches, all queued behind a spin kernel so that host launch latency is hidden."""
+    import torch
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    for i in range(min(n, 10)):
+        fn(i)
+    torch.cuda.synchronize()
+    torch.cuda._sleep(int(2e8))
+    a.record()
+    for i in range(n):
+        fn(i)
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1e3 / n
+
+
+def gemv_roofline(args, w, x, dev):
+    """Roofline of the dominant kernel: the Q4_K GEMV (gemv_q4k_kernel) on prepared activations."""
+    import torch
+    from light_amd import hipq
+    N, K = w.N, w.K
+    act = hipq.quantize_act(x)
+    out = torch.empty((1, N), device=dev)
+    us = time_launches(lambda i: hipq.matmul_q_act(act, w[i], 1, N, K, hipq.Q4_K, out=out), args.launches,
+                       len(w.copies))
+    alg = w.raw.nbytes + K + 8 * (K // 32) + 4 * N  # weight + int8 activations and their scales + F32 out
+    achieved = alg / (us * 1e-6) / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "gemv_q4k_kernel", "shape": f"N={N} K={K} M=1", "alg_bytes_per_launch": alg,
+            "avg_launch_us": round(us, 3)}
+
+
+def table(args, dev):
+    """Per-config µs/call, GB/s, TFLOPS and roofline fraction (stderr)."""
+    import numpy as np
+    import torch
+    from light_amd import hipq, synth
+    rows = []
+    for name, c in synth.CONFIGS.items():
+        g = synth.rng(c["cfg"])
+        try:
+            if c["kind"] == "gguf":
+                M, N, K, dt = c["M"], c["N"], c["K"], c["dt"]
+                w = Weight(synth.gguf_weight(dt, N, K, g), dt, N, K, dev)
+                x = torch.from_numpy(synth.activations(M, K, g)).to(dev)
+                out = torch.empty((M, N), device=dev)
+                ws = torch.empty(hipq.matmul_q_ws_bytes(M, K, dt), dtype=torch.uint8, device=dev)
+                us = time_launches(lambda i: hipq.matmul_q(x, w[i], N, K, dt, out=out, ws=ws), 100,
+                                   len(w.copies))
+                nbytes = w.raw.nbytes + 4 * M * K + 4 * M * N
+                flops = 2 * M * N * K
+            elif c["kind"] == "int4":
+                M, N, K, G = c["M"], c["N"], c["K"], c["G"]
+                codes, s, z = synth.int4_weight(N, K, G, g)
+                xt = torch.from_numpy(synth.activations(M, K, g, np.float16)).to(dev)
+                ct, st, zt = (torch.from_numpy(a).to(dev) for a in (codes, s, z))
+                reps = copies_for(codes.nbytes)
+                cs = [ct] + [ct.clone() for _ in range(reps - 1)]
+                out = torch.empty((M, N), dtype=torch.float16, device=dev)
+                us = time_launches(lambda i: hipq.int4_matmul(xt, cs[i % reps], st, zt, G, out=out), 100, reps)
+                nbytes = codes.nbytes + s.nbytes + z.nbytes + 2 * M * K + 2 * M * N
+                flops = 2 * M * N * K
+            else:
+                continue  # MoE rows are timed by the MoE section once it lands
+        except hipq.HipqError as e:
+            rows.append(dict(config=name, error=str(e)))
+            continue
+        gbs = nbytes / (us * 1e-6) / 1e9
+        tfl = flops / (us * 1e-6) / 1e12
+        rows.append(dict(config=name, us=round(us, 2), GBs=round(gbs, 1), TFLOPS=round(tfl, 2),
+                         hbm_frac=round(gbs / HBM_PEAK_GBS, 3)))
+        torch.cuda.empty_cache()
+    return rows
+
+
+def cpu_baseline(inputs):
+    """Light's AVX2 CPU qmatmul (oracle C restatement) on the same step; median of 5 after a warm-up."""
+    import oracle
+    gate, up, down, x, h = inputs
+    threads = int(os.environ.get("OMP_NUM_THREADS", "16"))
+    threads = max(1, min(threads, oracle.hw_threads()))
+
+    def run():
+        oracle.matmul_q(x, gate.raw, gate.N, gate.K, gate.dt, threads)
+        oracle.matmul_q(x, up.raw, up.N, up.K, up.dt, threads)
+        oracle.matmul_q(h, down.raw, down.N, down.K, down.dt, threads)
+
+    run()
+    ts = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        run()
+        ts.append(time.perf_counter() - t0)
+    t = statistics.median(ts)
+    nbytes = step_bytes([gate, up, down], 1)
+    return {"value": round(nbytes / t / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"5 timed MLP decode steps (gate+up+down Q4_K, M=1), median {t * 1e3:.2f} ms/step",
+            "cpu": _cpu_model()}
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); "
+              "the multi-GPU sharding design is described in DESIGN.md", file=sys.stderr)
+        sys.exit(2)
+    res = run_gpu(args)
+    line = {
+        "metric": "Q4_K GEMV GB/s (% of HBM peak) + Q4_K M=512 GEMM TFLOPS, Llama-3-8B shapes",
+        "value": round(res["value"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(res["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_k x q8_1 -> f32 (int8 dot, f32 accumulate)",
+        "data": "synthetic (seeded, BASELINE.json distributions; weights rotated over >512 MB)",
+        "config": {"workload": "llama3_8b_mlp_decode_q4_k", "M": 1, "hidden": 4096, "intermediate": 14336,
+                   "matmuls": ["gate 14336x4096", "up 14336x4096", "down 4096x14336"],
+                   "step_bytes": res["step_bytes"]},
+        "roofline": res["roofline"],
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(res["inputs"])
+    if args.table:
+        import torch
+        print(json.dumps({"table": table(args, torch.device("cuda:0"))}), file=sys.stderr)
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

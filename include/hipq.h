@@ -104,6 +104,23 @@ size_t hq_matmul_q_ws_bytes(int64_t M, int64_t K, int w_dtype);
 int hq_matmul_q(const float *x, const void *w, float *out, int64_t M, int64_t N, int64_t K, int w_dtype,
                 void *ws, size_t ws_bytes, hq_stream_t stream);
 
+/* Prepared activations: hq_matmul_q = hq_quantize_act + hq_matmul_q_act.
+ * A caller that multiplies one activation by several weights (the SwiGLU gate
+ * and up projections, models/llama.go:1306-1328) quantizes once and reuses it.
+ * No counterpart in Light.  The act buffer (hq_act_bytes(M, K) bytes, 16-byte
+ * aligned) holds x's q8_1 quantization in a planar layout: int8 q [M][K], then
+ * f32 d [M][K/32], then f32 d*sum(q) [M][K/32]; q and d are the values
+ * hq_quantize_q8_1 produces (d before its f16 rounding). */
+size_t hq_act_bytes(int64_t M, int64_t K);
+int hq_quantize_act(const void *x, int x_dtype, void *act, int64_t M, int64_t K, hq_stream_t stream);
+/* Workspace hq_matmul_q_act needs beyond the act buffer (0 for the GEMV). */
+size_t hq_matmul_q_act_ws_bytes(int64_t M, int64_t K, int w_dtype);
+/* out (M, N) F32 = x @ dequant(w)^T from prepared activations.  For M <= 8 the
+ * weight must take the int8 GEMV (16-byte aligned, rows a multiple of 16 bytes;
+ * HQ_EUNSUPPORTED otherwise). */
+int hq_matmul_q_act(const void *act, const void *w, float *out, int64_t M, int64_t N, int64_t K, int w_dtype,
+                    void *ws, size_t ws_bytes, hq_stream_t stream);
+
 /* Dequantize n elements of GGUF blocks to F32 or BF16 (bit-exact with Light's
  * CPU decoders; BF16 rounds the F32 value once, RNE).
  * Replaces the "dequant" hook (quant/cuda_hook.go:17-69, kernels/cuda/dequant.go:39-80). */

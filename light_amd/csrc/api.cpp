@@ -223,6 +223,53 @@ int hq_matmul_q(const float *x, const void *w, float *out, int64_t M, int64_t N,
   return launch_matmul_q(x, w, out, M, N, K, w_dtype, ws, s);
 }
 
+size_t hq_act_bytes(int64_t M, int64_t K) {
+  if (M <= 0 || K <= 0 || K % 32) return 0;
+  return (size_t)act_bytes(M, K);
+}
+
+int hq_quantize_act(const void *x, int x_dtype, void *act, int64_t M, int64_t K, hq_stream_t stream) {
+  const char *call = "hq_quantize_act";
+  if (x_dtype != HQ_F32 && x_dtype != HQ_BF16 && x_dtype != HQ_F16)
+    return fail(HQ_EUNSUPPORTED, call, "x dtype %d", x_dtype);
+  if (M < 0 || K < 0 || K % 32) return fail(HQ_EINVAL, call, "K=%lld not a multiple of 32", (long long)K);
+  if (M == 0 || K == 0) return HQ_OK;
+  if (!x || !act) return fail(HQ_EINVAL, call, "NULL pointer");
+  if (((uintptr_t)x & 15) || ((uintptr_t)act & 15)) return fail(HQ_EINVAL, call, "x and act must be 16-byte aligned");
+  hipStream_t s = resolve(stream);
+  TraceSpan span("quantize_act", s);
+  return launch_quantize_act(x, x_dtype, act, M, K, s);
+}
+
+size_t hq_matmul_q_act_ws_bytes(int64_t M, int64_t K, int w_dtype) {
+  size_t all = matmul_q_ws_bytes(M, K, w_dtype), act = hq_act_bytes(M, K);
+  return all > act ? all - act : 0;
+}
+
+int hq_matmul_q_act(const void *act, const void *w, float *out, int64_t M, int64_t N, int64_t K, int w_dtype,
+                    void *ws, size_t ws_bytes, hq_stream_t stream) {
+  const char *call = "hq_matmul_q_act";
+  if (!is_gguf(w_dtype)) return fail(HQ_EUNSUPPORTED, call, "weight dtype %d has no fused kernel", w_dtype);
+  if (M < 0 || N < 0 || K <= 0) return fail(HQ_EINVAL, call, "bad shape");
+  BlockInfo bi = block_info(w_dtype);
+  if (K % bi.elems)
+    return fail(HQ_EINVAL, call, "K=%lld not a multiple of block size %d", (long long)K, bi.elems);
+  if (M == 0 || N == 0) return HQ_OK;
+  if (!act || !w || !out) return fail(HQ_EINVAL, call, "NULL pointer");
+  if (((uintptr_t)act & 15) || ((uintptr_t)out & 3)) return fail(HQ_EINVAL, call, "act must be 16-byte aligned");
+  if (M <= kGemvMaxRows && !gemv_fast_ok(w_dtype, K, w))
+    return fail(HQ_EUNSUPPORTED, call, "weight layout needs the F32 path (hq_matmul_q)");
+  hipStream_t s = resolve(stream);
+  size_t need = hq_matmul_q_act_ws_bytes(M, K, w_dtype);
+  if (need && !ws) {
+    if (int rc = workspace(need, s, &ws, call)) return rc;
+  } else if (need && ws_bytes < need) {
+    return fail(HQ_ENOMEM, call, "workspace %zu bytes < %zu needed", ws_bytes, need);
+  }
+  TraceSpan span(matmul_q_kernel_name(M, w_dtype), s);
+  return launch_matmul_act(act, w, out, M, N, K, w_dtype, ws, s);
+}
+
 int hq_dequant(const void *src, void *dst, int64_t n, int src_dtype, int out_dtype, hq_stream_t stream) {
   const char *call = "hq_dequant";
   if (!is_gguf(src_dtype) && src_dtype != HQ_Q8_1)

@@ -20,6 +20,18 @@ enum DType : int {
 
 constexpr int kWave = 64;  // CDNA wavefront width
 
+// Prepared activations ("act" layout, internal to libhipq) for x (M, K): the q8_1
+// quantization of x, stored planar so kernels can use 16-byte loads:
+//   qs  int8 [M][K]      at 0
+//   d   f32  [M][K/32]   at act_d_off(M, K)   (the f32 d, before q8_1's f16 rounding)
+//   sx  f32  [M][K/32]   at act_s_off(M, K)   (d * sum of the block's q, exact integer sum)
+// q is bit-identical to the q8_1 quants of the same x.
+__host__ __device__ constexpr int64_t act_d_off(int64_t M, int64_t K) { return (M * K + 15) & ~(int64_t)15; }
+__host__ __device__ constexpr int64_t act_s_off(int64_t M, int64_t K) { return act_d_off(M, K) + 4 * M * (K / 32); }
+__host__ __device__ constexpr int64_t act_bytes(int64_t M, int64_t K) {
+  return (act_s_off(M, K) + 4 * M * (K / 32) + 255) & ~(int64_t)255;
+}
+
 // Bytes per block / elements per block (dtype/dtype.go:53-60).
 struct BlockInfo { int elems, bytes; };
 __host__ __device__ constexpr BlockInfo block_info(int dt) {

@@ -4,26 +4,25 @@
 // kernels/cpu/quant_matmul.go:141-170); y[m, n] = sum_k x[m, k] * dequant(W)[n, k].
 //
 // Design (gfx950, wave64):
-//  * The activation row is quantized once to q8_1 (quantize.hip) and each lane
-//    keeps the int8 activations of a FIXED set of K positions in registers for
-//    the whole kernel; a wave then streams weight rows past them.  The weight
-//    is read exactly once from HBM; the activations are read once per wave.
-//  * Inner products run on v_dot4_i32_i8 (4 MACs per op), so the unpack work per
-//    weight stays far below the VALU budget needed at HBM speed.
-//  * Q4_K (144-byte blocks, 16-byte aligned): lanes load their 16-byte quant
-//    chunk straight from HBM (global_load_dwordx4, coalesced); the 16-byte block
-//    header is fetched one dword per lane and broadcast inside each 4-lane quad
-//    with DPP, so each lane issues 20 bytes of loads per 32 weights.
-//  * Q8_0 (34 B) and Q6_K (210 B) blocks are only 2-byte aligned.  A wave copies
-//    its rows' bytes into LDS with coalesced 16-byte loads and writes each block
-//    at a padded, 4/8-byte-aligned LDS slot; lanes then decode from LDS with
-//    aligned reads.
-//  * Any other shape (K beyond the register budget, rows not 16-byte multiples)
-//    takes a generic wave-per-row kernel on F32 activations that uses the
-//    bit-exact decoder of dequant.hip.
-//
-// Accuracy: activations are quantized per 32 elements (error <= d/2 per element),
-// and per-block partial sums are exact integers scaled once in F32.
+//  * x is quantized once (quantize.hip) into the planar act layout: int8 quants,
+//    f32 block scales d and f32 d * sum(q).  Every product is an exact int32
+//    v_dot4_i32_i8 chain over one 32-element block, scaled once in f32, so the
+//    per-weight VALU work stays well under what HBM speed allows.
+//  * A lane owns FIXED K positions and keeps their activations in registers for
+//    the whole kernel; weight rows stream past.  Up to MM = 4 activation rows are
+//    served per weight read.
+//  * Q4_K (144-byte blocks, 16-byte aligned): a "team" of ceil(nb*4/16)*16 lanes
+//    covers one weight row; lane = one (block, p) pair = 32 contiguous quant
+//    bytes (two global_load_dwordx4) = sub-blocks 2p (low nibbles) and 2p+1
+//    (high nibbles).  The 16-byte block header is fetched one dword per lane
+//    and broadcast inside the block's 4-lane quad with DPP.  Partial sums are
+//    reduced with DPP inside 16-lane rows and across the team in LDS.
+//    Workgroups are persistent and prefetch the next rows while computing.
+//  * Q8_0 (34 B) and Q6_K (210 B) blocks are only 2-byte aligned.  Each wave
+//    copies its rows' raw bytes into LDS with 16-byte loads and stores, and lanes
+//    read their blocks back with aligned dword reads re-aligned by v_alignbit.
+//  * Other shapes take a generic wave-per-row kernel on F32 activations built on
+//    the bit-exact decoder of dequant.hip.
 #include "decode.hpp"
 #include "internal.hpp"
 
@@ -51,17 +50,23 @@ __device__ __forceinline__ uint32_t quad_bcast(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, K * 0x55, 0xF, 0xF, false);
 }
 
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-// Streaming 16-byte load (weights are read once: non-temporal hint).
-__device__ __forceinline__ uint4 ld_stream16(const void *p) {
-  u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
-  return make_uint4(v.x, v.y, v.z, v.w);
+// Sum over each 16-lane DPP row; the result is valid in every lane of the row.
+__device__ __forceinline__ float row16_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));   // xor 1
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));   // xor 2
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));  // half mirror
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));  // mirror
+  return v;
 }
 
-__device__ __forceinline__ uint32_t byte_at(uint32_t w, int k) { return (w >> (8 * k)) & 0xffu; }
+// Full-wave sum via the four 16-lane row sums.
+__device__ __forceinline__ float wave_sum64(float v) {
+  v = row16_sum(v);
+  return __shfl(v, 0, 64) + __shfl(v, 16, 64) + __shfl(v, 32, 64) + __shfl(v, 48, 64);
+}
+
+__device__ __forceinline__ uint4 ld16g(const void *p) { return *reinterpret_cast<const uint4 *>(p); }
 __device__ __forceinline__ uint32_t ld32(const uint8_t *p) { return *reinterpret_cast<const uint32_t *>(p); }
-__device__ __forceinline__ uint32_t ld16(const uint8_t *p) { return *reinterpret_cast<const uint16_t *>(p); }
 
 // Sum of the four signed bytes of each of n dwords.
 __device__ __forceinline__ int byte_sum(const int *v, int n) {
@@ -71,226 +76,332 @@ __device__ __forceinline__ int byte_sum(const int *v, int n) {
 }
 
 // ---------------------------------------------------------------------------
-// Q4_K: one "chunk" = 16 quant bytes = 16 elements of sub-block 2p (low
-// nibbles) and 16 of sub-block 2p+1 (high nibbles); 8 chunks per block.
-// Lane l owns chunks l, l+64, ... of every row.
+// Q4_K
 // ---------------------------------------------------------------------------
-template <int CPL, int R>
-__global__ __launch_bounds__(256) void gemv_q4k_kernel(const uint8_t *__restrict__ xq, const uint8_t *__restrict__ w,
-                                                       float *__restrict__ out, int N, int nchunks,
-                                                       int64_t row_bytes, int64_t xq_row_bytes) {
-  const int lane = threadIdx.x & 63;
-  const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int nwaves = gridDim.x * 4;
-  xq += blockIdx.y * xq_row_bytes;
-  out += (int64_t)blockIdx.y * N;
+struct Q4kArgs {
+  const uint8_t *act;  // planar activations
+  const uint8_t *w;
+  float *out;
+  int M, N, K, P, TP;  // P = pairs per row (nb * 4), TP = team lanes (P rounded up to 16)
+  int64_t row_bytes, d_off, s_off;
+};
 
-  int xa[CPL][4], xb[CPL][4], qoff[CPL], hoff[CPL], kA[CPL];
-  float dA[CPL], dB[CPL], sA[CPL], sB[CPL];
-  bool lowj[CPL];
-#pragma unroll
-  for (int i = 0; i < CPL; i++) {
-    int c = lane + 64 * i;
-    bool ok = c < nchunks;
-    if (!ok) c = 0;
-    int b = c >> 3, cc = c & 7, p = cc >> 1, h = cc & 1;
-    qoff[i] = b * 144 + 16 + cc * 16;
-    hoff[i] = b * 144 + 4 * (cc & 3);
-    lowj[i] = p < 2;
-    kA[i] = (2 * p) & 3;
-    const uint8_t *pa = xq + 36 * (b * 8 + 2 * p);
-    const uint8_t *pb = pa + 36;
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-      xa[i][k] = ok ? (int)ld32(pa + 4 + 16 * h + 4 * k) : 0;
-      xb[i][k] = ok ? (int)ld32(pb + 4 + 16 * h + 4 * k) : 0;
-    }
-    dA[i] = ok ? h2f(ld16(pa)) : 0.f;
-    dB[i] = ok ? h2f(ld16(pb)) : 0.f;
-    sA[i] = dA[i] * (float)byte_sum(xa[i], 4);
-    sB[i] = dB[i] * (float)byte_sum(xb[i], 4);
-  }
+template <int R, int MM, bool PF>
+__global__ __launch_bounds__(512) void gemv_q4k_kernel(Q4kArgs a) {
+  __shared__ float part[512];
+  const int t = threadIdx.x;
+  const int RW = blockDim.x / a.TP;  // row teams per workgroup
+  const int team = t / a.TP, u = t - team * a.TP;
+  const bool active = u < a.P;
+  const int uu = active ? u : 0;
+  const int b = uu >> 2, p = uu & 3;
+  const int qoff = b * 144 + 16 + p * 32, hoff = b * 144 + 4 * p;
+  const int rows_per_group = RW * R;
+  const int ngroups = (a.N + rows_per_group - 1) / rows_per_group;
+  const int m0 = blockIdx.y * MM;
 
-  for (int64_t row0 = (int64_t)wave * R; row0 < N; row0 += (int64_t)nwaves * R) {
-    uint4 q[R][CPL];
-    uint32_t hd[R][CPL];
+  uint4 q0[R], q1[R];
+  uint32_t hd[R];
+  auto load = [&](int grp, uint4 (&x0)[R], uint4 (&x1)[R], uint32_t (&h)[R]) {
 #pragma unroll
     for (int r = 0; r < R; r++) {
-      int64_t row = row0 + r < N ? row0 + r : N - 1;
-      const uint8_t *rp = w + row * row_bytes;
-#pragma unroll
-      for (int i = 0; i < CPL; i++) {
-        q[r][i] = ld_stream16(rp + qoff[i]);
-        hd[r][i] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(rp + hoff[i]));
+      int row = grp * rows_per_group + r * RW + team;
+      row = row < a.N ? row : a.N - 1;
+      const uint8_t *rp = a.w + (int64_t)row * a.row_bytes;
+      if (active) {
+        x0[r] = ld16g(rp + qoff);
+        x1[r] = ld16g(rp + qoff + 16);
+        h[r] = ld32(rp + hoff);
+      } else {
+        x0[r] = x1[r] = make_uint4(0, 0, 0, 0);
+        h[r] = 0;
       }
     }
+  };
+  int g = blockIdx.x;
+  if (g < ngroups) load(g, q0, q1, hd);
+
+  // Activations of this lane's two sub-blocks, for MM rows of x.
+  const int ja = b * 8 + 2 * p;
+  int xa[MM][8], xb[MM][8];
+  float2 dd[MM], ss[MM];
+#pragma unroll
+  for (int mm = 0; mm < MM; mm++) {
+    const int m = m0 + mm < a.M ? m0 + mm : a.M - 1;
+    const int64_t blk = (int64_t)m * (a.K / 32) + ja;
+    const uint4 *xs = reinterpret_cast<const uint4 *>(a.act + blk * 32);
+    const uint4 v0 = xs[0], v1 = xs[1], v2 = xs[2], v3 = xs[3];
+    const int A[8] = {(int)v0.x, (int)v0.y, (int)v0.z, (int)v0.w, (int)v1.x, (int)v1.y, (int)v1.z, (int)v1.w};
+    const int B[8] = {(int)v2.x, (int)v2.y, (int)v2.z, (int)v2.w, (int)v3.x, (int)v3.y, (int)v3.z, (int)v3.w};
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      xa[mm][k] = A[k];
+      xb[mm][k] = B[k];
+    }
+    dd[mm] = *reinterpret_cast<const float2 *>(a.act + a.d_off + 4 * blk);
+    ss[mm] = *reinterpret_cast<const float2 *>(a.act + a.s_off + 4 * blk);
+  }
+  const bool lowj = p < 2;
+  const int ka = (2 * p) & 3;
+  const int lane = t & 63;
+  const int hpt = a.TP >> 4;  // 16-lane rows per team
+
+  for (; g < ngroups; g += gridDim.x) {
+    uint4 n0[R], n1[R];
+    uint32_t nh[R];
+    if (PF && g + (int)gridDim.x < ngroups) load(g + gridDim.x, n0, n1, nh);
 #pragma unroll
     for (int r = 0; r < R; r++) {
-      float acc = 0.f;
+      const uint32_t h0 = quad_bcast<0>(hd[r]), h1 = quad_bcast<1>(hd[r]);
+      const uint32_t h2 = quad_bcast<2>(hd[r]), h3 = quad_bcast<3>(hd[r]);
+      const float d = h2f(h0 & 0xffffu), dmin = h2f(h0 >> 16);
+      // 6-bit (scale, min) of sub-blocks 2p and 2p+1 (getScaleMinK4, quant/q4_k.go:83-89),
+      // unpacked two at a time: bytes ka and ka+1 of each scale dword.
+      const uint32_t t1 = (h1 >> (8 * ka)) & 0xffffu, t2 = (h2 >> (8 * ka)) & 0xffffu;
+      const uint32_t t3 = (h3 >> (8 * ka)) & 0xffffu;
+      const uint32_t scp = lowj ? (t1 & 0x3F3Fu) : ((t3 & 0x0F0Fu) | ((t1 >> 2) & 0x3030u));
+      const uint32_t mnp = lowj ? (t2 & 0x3F3Fu) : (((t3 >> 4) & 0x0F0Fu) | ((t2 >> 2) & 0x3030u));
+      const float scA = (float)(scp & 0xffu), scB = (float)(scp >> 8);
+      const float mnA = (float)(mnp & 0xffu), mnB = (float)(mnp >> 8);
+      const uint32_t qw[8] = {q0[r].x, q0[r].y, q0[r].z, q0[r].w, q1[r].x, q1[r].y, q1[r].z, q1[r].w};
+      uint32_t lo[8], hi[8];
 #pragma unroll
-      for (int i = 0; i < CPL; i++) {
-        uint32_t h0 = quad_bcast<0>(hd[r][i]), h1 = quad_bcast<1>(hd[r][i]);
-        uint32_t h2 = quad_bcast<2>(hd[r][i]), h3 = quad_bcast<3>(hd[r][i]);
-        float d = h2f(h0 & 0xffffu), dmin = h2f(h0 >> 16);
-        int ka = kA[i], kb = ka + 1;
-        uint32_t sa = byte_at(h1, ka), ma = byte_at(h2, ka), aa = byte_at(h3, ka);
-        uint32_t sb = byte_at(h1, kb), mb = byte_at(h2, kb), ab = byte_at(h3, kb);
-        int scA = lowj[i] ? (int)(sa & 63) : (int)((aa & 15) | ((sa >> 6) << 4));
-        int mnA = lowj[i] ? (int)(ma & 63) : (int)((aa >> 4) | ((ma >> 6) << 4));
-        int scB = lowj[i] ? (int)(sb & 63) : (int)((ab & 15) | ((sb >> 6) << 4));
-        int mnB = lowj[i] ? (int)(mb & 63) : (int)((ab >> 4) | ((mb >> 6) << 4));
-        const uint32_t qw[4] = {q[r][i].x, q[r][i].y, q[r][i].z, q[r][i].w};
+      for (int k = 0; k < 8; k++) {
+        lo[k] = qw[k] & 0x0F0F0F0Fu;
+        hi[k] = (qw[k] >> 4) & 0x0F0F0F0Fu;
+      }
+#pragma unroll
+      for (int mm = 0; mm < MM; mm++) {
         int dotA = 0, dotB = 0;
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-          dotA = dot4((int)(qw[k] & 0x0F0F0F0Fu), xa[i][k], dotA);
-          dotB = dot4((int)((qw[k] >> 4) & 0x0F0F0F0Fu), xb[i][k], dotB);
+        for (int k = 0; k < 8; k++) {
+          dotA = dot4((int)lo[k], xa[mm][k], dotA);
+          dotB = dot4((int)hi[k], xb[mm][k], dotB);
         }
-        float v = (float)scA * dA[i] * (float)dotA + (float)scB * dB[i] * (float)dotB;
-        float mn = (float)mnA * sA[i] + (float)mnB * sB[i];
-        acc += d * v - dmin * mn;
+        const float v = scA * (dd[mm].x * (float)dotA) + scB * (dd[mm].y * (float)dotB);
+        const float mn = mnA * ss[mm].x + mnB * ss[mm].y;
+        const float s = row16_sum(d * v - dmin * mn);
+        if ((lane & 15) == 0) part[((r * RW + team) * MM + mm) * hpt + (u >> 4)] = s;
       }
-      acc = wave_sum(acc);
-      if (lane == 0 && row0 + r < N) out[row0 + r] = acc;
+    }
+    __syncthreads();
+    if (t < rows_per_group * MM) {
+      const int slot = t / MM, mm = t - slot * MM;
+      const int r = slot / RW, tm = slot - r * RW;
+      float acc = 0.f;
+      for (int k = 0; k < hpt; k++) acc += part[t * hpt + k];
+      const int row = g * rows_per_group + r * RW + tm;
+      if (row < a.N && m0 + mm < a.M) a.out[(int64_t)(m0 + mm) * a.N + row] = acc;
+    }
+    __syncthreads();
+    if (PF) {
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        q0[r] = n0[r];
+        q1[r] = n1[r];
+        hd[r] = nh[r];
+      }
+    } else if (g + (int)gridDim.x < ngroups) {
+      load(g + gridDim.x, q0, q1, hd);
     }
   }
 }
 
 // ---------------------------------------------------------------------------
-// Q8_0 / Q6_K: LDS-staged rows.
+// Q8_0 / Q6_K: LDS-staged rows, one wave per R rows.
 // ---------------------------------------------------------------------------
-template <int DT>
-struct Staged;
-template <>
-struct Staged<Q8_0> {
-  static constexpr int BB = 34, SB = 36, LEAD = 2, UPB = 1;  // block at slot+2: d at +2, qs at +4
-};
-template <>
-struct Staged<Q6_K> {
-  static constexpr int BB = 210, SB = 216, LEAD = 0, UPB = 8;  // block at slot: ql +0, qh +128, sc +192, d +208
+struct StagedArgs {
+  const uint8_t *act;
+  const uint8_t *w;
+  float *out;
+  int M, N, K, nb;
+  int64_t row_bytes, d_off;
+  int lds_wave;  // bytes of LDS per wave
 };
 
-template <int DT, int CPL, int R>
-__global__ __launch_bounds__(256) void gemv_staged_kernel(const uint8_t *__restrict__ xq,
-                                                          const uint8_t *__restrict__ w, float *__restrict__ out,
-                                                          int N, int nblk, int64_t row_bytes, int64_t xq_row_bytes,
-                                                          int lds_wave_bytes) {
-  using S = Staged<DT>;
+// NDW dwords starting at LDS byte offset o (o even), re-aligned: out[k] = bytes [o+4k, o+4k+4).
+template <int NDW>
+__device__ __forceinline__ void lds_unaligned(const uint8_t *lds, int o, uint32_t (&out)[NDW]) {
+  const uint32_t *base = reinterpret_cast<const uint32_t *>(lds + (o & ~3));
+  const uint32_t sh = (uint32_t)(o & 3) * 8;
+  uint32_t w[NDW + 1];
+#pragma unroll
+  for (int k = 0; k <= NDW; k++) w[k] = base[k];
+#pragma unroll
+  for (int k = 0; k < NDW; k++) out[k] = __builtin_amdgcn_alignbit(w[k + 1], w[k], sh);
+}
+
+__device__ __forceinline__ void stage_rows(uint8_t *lds, const uint8_t *src, int nseg, int lane) {
+  const uint4 *s4 = reinterpret_cast<const uint4 *>(src);
+  uint4 *d4 = reinterpret_cast<uint4 *>(lds);
+  for (int s0 = lane; s0 < nseg; s0 += 256) {
+    uint4 v[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+      if (s0 + 64 * k < nseg) v[k] = s4[s0 + 64 * k];
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+      if (s0 + 64 * k < nseg) d4[s0 + 64 * k] = v[k];
+  }
+}
+
+template <int CPL, int R, int MM>
+__global__ __launch_bounds__(256) void gemv_q80_kernel(StagedArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   const int lane = threadIdx.x & 63;
   const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int nwaves = gridDim.x * 4;
-  uint8_t *lds = smem + (threadIdx.x >> 6) * lds_wave_bytes;
-  uint16_t *lds16 = reinterpret_cast<uint16_t *>(lds);
-  xq += blockIdx.y * xq_row_bytes;
-  out += (int64_t)blockIdx.y * N;
-  const int units = nblk * S::UPB;
+  uint8_t *lds = smem + (threadIdx.x >> 6) * a.lds_wave;
+  const int m0 = blockIdx.y * MM;
 
-  // Activations of this lane's units.
-  constexpr int XD = DT == Q8_0 ? 8 : 8;  // dwords of int8 activations per unit
-  int xv[CPL][XD];
-  float dx[CPL][DT == Q8_0 ? 1 : 4];
-  int s32[CPL][4];
-  int ublk[CPL], uh[CPL], ul0[CPL];
+  int xv[MM][CPL][8];
+  float dx[MM][CPL];
 #pragma unroll
-  for (int i = 0; i < CPL; i++) {
-    int u = lane + 64 * i;
-    bool ok = u < units;
-    if (!ok) u = 0;
-    if constexpr (DT == Q8_0) {
-      ublk[i] = u;
-      uh[i] = ul0[i] = 0;
-      const uint8_t *p = xq + 36 * u;
+  for (int mm = 0; mm < MM; mm++) {
+    const int m = m0 + mm < a.M ? m0 + mm : a.M - 1;
 #pragma unroll
-      for (int k = 0; k < 8; k++) xv[i][k] = ok ? (int)ld32(p + 4 + 4 * k) : 0;
-      dx[i][0] = ok ? h2f(ld16(p)) : 0.f;
-    } else {
-      int b = u >> 3, l8 = u & 7, h = l8 >> 2, l0 = (l8 & 3) * 8;
-      ublk[i] = b;
-      uh[i] = h;
-      ul0[i] = l0;
+    for (int i = 0; i < CPL; i++) {
+      const int bl = lane + 64 * i;
+      const bool ok = bl < a.nb;
+      const int64_t blk = (int64_t)m * a.nb + (ok ? bl : 0);
+      const uint4 *xs = reinterpret_cast<const uint4 *>(a.act + blk * 32);
+      const uint4 v0 = xs[0], v1 = xs[1];
+      const int V[8] = {(int)v0.x, (int)v0.y, (int)v0.z, (int)v0.w, (int)v1.x, (int)v1.y, (int)v1.z, (int)v1.w};
 #pragma unroll
-      for (int g = 0; g < 4; g++) {
-        const uint8_t *p = xq + 36 * (b * 8 + h * 4 + g);
-        xv[i][2 * g] = ok ? (int)ld32(p + 4 + l0) : 0;
-        xv[i][2 * g + 1] = ok ? (int)ld32(p + 8 + l0) : 0;
-        dx[i][g] = ok ? h2f(ld16(p)) : 0.f;
-        s32[i][g] = 32 * byte_sum(&xv[i][2 * g], 2);
-      }
+      for (int k = 0; k < 8; k++) xv[mm][i][k] = ok ? V[k] : 0;
+      dx[mm][i] = ok ? reinterpret_cast<const float *>(a.act + a.d_off)[blk] : 0.f;
     }
   }
 
-  for (int64_t row0 = (int64_t)wave * R; row0 < N; row0 += (int64_t)nwaves * R) {
-    const int nrows = (int)(N - row0 < R ? N - row0 : R);
-    const int nseg = (int)(nrows * row_bytes / 16);
-    const uint4 *src = reinterpret_cast<const uint4 *>(w + row0 * row_bytes);
-    // Stage: 16-byte coalesced loads, 2-byte scatter into padded block slots.
-    for (int s0 = lane; s0 < nseg; s0 += 256) {
-      uint4 v[4];
+  for (int64_t row0 = (int64_t)wave * R; row0 < a.N; row0 += (int64_t)nwaves * R) {
+    const int nrows = (int)(a.N - row0 < R ? a.N - row0 : R);
+    stage_rows(lds, a.w + row0 * a.row_bytes, (int)(nrows * a.row_bytes / 16), lane);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-      for (int k = 0; k < 4; k++)
-        if (s0 + 64 * k < nseg) v[k] = ld_stream16(src + s0 + 64 * k);
+    for (int r = 0; r < R; r++) {
+      if (r >= nrows) break;
+      float acc[MM];
 #pragma unroll
-      for (int k = 0; k < 4; k++) {
-        int s = s0 + 64 * k;
-        if (s >= nseg) break;
-        const uint32_t vw[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+      for (int mm = 0; mm < MM; mm++) acc[mm] = 0.f;
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-          int ob = 16 * s + 2 * j;
-          int gb = ob / S::BB;
-          lds16[(gb * S::SB + S::LEAD + ob - gb * S::BB) >> 1] = (uint16_t)(vw[j >> 1] >> (16 * (j & 1)));
+      for (int i = 0; i < CPL; i++) {
+        const int bl = lane + 64 * i;
+        const int o = r * (int)a.row_bytes + 34 * (bl < a.nb ? bl : 0);
+        const float d = h2f(*reinterpret_cast<const uint16_t *>(lds + o));
+        uint32_t qd[8];
+        lds_unaligned<8>(lds, o + 2, qd);
+#pragma unroll
+        for (int mm = 0; mm < MM; mm++) {
+          int dot = 0;
+#pragma unroll
+          for (int k = 0; k < 8; k++) dot = dot4((int)qd[k], xv[mm][i][k], dot);
+          acc[mm] += d * (dx[mm][i] * (float)dot);
         }
+      }
+#pragma unroll
+      for (int mm = 0; mm < MM; mm++) {
+        const float s = wave_sum64(acc[mm]);
+        if (lane == 0 && m0 + mm < a.M) a.out[(int64_t)(m0 + mm) * a.N + row0 + r] = s;
       }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+}
 
+// Q6_K lane unit = (block b, l8): half h = l8 >> 2, l0 = (l8 & 3) * 8; the unit covers
+// elements h*128 + g*32 + l0 + [0, 8) for g = 0..3 (quant/q6_k.go:18-27).
+template <int CPL, int R, int MM>
+__global__ __launch_bounds__(256) void gemv_q6k_kernel(StagedArgs a) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int nwaves = gridDim.x * 4;
+  uint8_t *lds = smem + (threadIdx.x >> 6) * a.lds_wave;
+  const int m0 = blockIdx.y * MM;
+  const int units = a.nb * 8;
+
+  int xv[MM][CPL][8];
+  float dx[MM][CPL][4];
+  int s32[MM][CPL][4];
+#pragma unroll
+  for (int i = 0; i < CPL; i++) {
+    const int un = lane + 64 * i;
+    const bool ok = un < units;
+    const int uu = ok ? un : 0, bl = uu >> 3, l8 = uu & 7, h = l8 >> 2, l0 = (l8 & 3) * 8;
+#pragma unroll
+    for (int mm = 0; mm < MM; mm++) {
+      const int m = m0 + mm < a.M ? m0 + mm : a.M - 1;
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        const int64_t blk = (int64_t)m * (a.K / 32) + bl * 8 + h * 4 + g;
+        const uint2 v = *reinterpret_cast<const uint2 *>(a.act + blk * 32 + l0);
+        xv[mm][i][2 * g] = ok ? (int)v.x : 0;
+        xv[mm][i][2 * g + 1] = ok ? (int)v.y : 0;
+        dx[mm][i][g] = ok ? reinterpret_cast<const float *>(a.act + a.d_off)[blk] : 0.f;
+        s32[mm][i][g] = 32 * byte_sum(&xv[mm][i][2 * g], 2);
+      }
+    }
+  }
+
+  for (int64_t row0 = (int64_t)wave * R; row0 < a.N; row0 += (int64_t)nwaves * R) {
+    const int nrows = (int)(a.N - row0 < R ? a.N - row0 : R);
+    stage_rows(lds, a.w + row0 * a.row_bytes, (int)(nrows * a.row_bytes / 16), lane);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
     for (int r = 0; r < R; r++) {
       if (r >= nrows) break;
-      float acc = 0.f;
+      float acc[MM];
+#pragma unroll
+      for (int mm = 0; mm < MM; mm++) acc[mm] = 0.f;
 #pragma unroll
       for (int i = 0; i < CPL; i++) {
-        const uint8_t *blk = lds + (r * nblk + ublk[i]) * S::SB;
-        if constexpr (DT == Q8_0) {
-          float d = h2f(ld16(blk + 2));
-          int dot = 0;
+        const int un = lane + 64 * i;
+        const int uu = un < units ? un : 0, bl = uu >> 3, l8 = uu & 7, h = l8 >> 2, l0 = (l8 & 3) * 8;
+        const int o = r * (int)a.row_bytes + 210 * bl;
+        uint32_t A[2], B[2], H[2], S[2];
+        lds_unaligned<2>(lds, o + h * 64 + l0, A);
+        lds_unaligned<2>(lds, o + h * 64 + 32 + l0, B);
+        lds_unaligned<2>(lds, o + 128 + h * 32 + l0, H);
+        lds_unaligned<2>(lds, o + 192 + h * 8, S);
+        const float d = h2f(*reinterpret_cast<const uint16_t *>(lds + o + 208));
+        const int is = l0 >> 4;
+        float scf[4];
 #pragma unroll
-          for (int k = 0; k < 8; k++) dot = dot4((int)ld32(blk + 4 + 4 * k), xv[i][k], dot);
-          acc += d * (dx[i][0] * (float)dot);
-        } else {
-          const int h = uh[i], l0 = ul0[i];
-          const uint2 qa = *reinterpret_cast<const uint2 *>(blk + h * 64 + l0);
-          const uint2 qb = *reinterpret_cast<const uint2 *>(blk + h * 64 + 32 + l0);
-          const uint2 qh = *reinterpret_cast<const uint2 *>(blk + 128 + h * 32 + l0);
-          const uint2 sc = *reinterpret_cast<const uint2 *>(blk + 192 + h * 8);
-          float d = h2f(ld16(blk + 208));
-          const uint32_t A[2] = {qa.x, qa.y}, B[2] = {qb.x, qb.y}, H[2] = {qh.x, qh.y};
-          const int is = l0 >> 4;
+        for (int g = 0; g < 4; g++) {
+          const int sidx = 2 * g + is;
+          scf[g] = (float)(int8_t)((sidx < 4 ? S[0] >> (8 * sidx) : S[1] >> (8 * (sidx - 4))) & 0xff);
+        }
+        uint32_t qv[4][2];
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+          const uint32_t hk = H[k];
+          qv[0][k] = (A[k] & 0x0F0F0F0Fu) | ((hk & 0x03030303u) << 4);
+          qv[1][k] = (B[k] & 0x0F0F0F0Fu) | (((hk >> 2) & 0x03030303u) << 4);
+          qv[2][k] = ((A[k] >> 4) & 0x0F0F0F0Fu) | (((hk >> 4) & 0x03030303u) << 4);
+          qv[3][k] = ((B[k] >> 4) & 0x0F0F0F0Fu) | (((hk >> 6) & 0x03030303u) << 4);
+        }
+#pragma unroll
+        for (int mm = 0; mm < MM; mm++) {
           float v = 0.f;
 #pragma unroll
           for (int g = 0; g < 4; g++) {
-            int dot = 0;
-#pragma unroll
-            for (int k = 0; k < 2; k++) {
-              uint32_t nib = g == 0 ? (A[k] & 0x0F0F0F0Fu)
-                           : g == 1 ? (B[k] & 0x0F0F0F0Fu)
-                           : g == 2 ? ((A[k] >> 4) & 0x0F0F0F0Fu)
-                                    : ((B[k] >> 4) & 0x0F0F0F0Fu);
-              uint32_t qv = nib | (((H[k] >> (2 * g)) & 0x03030303u) << 4);
-              dot = dot4((int)qv, xv[i][2 * g + k], dot);
-            }
-            int sidx = 2 * g + is;  // scale byte within this half's 8
-            int scv = (int)(int8_t)((sidx < 4 ? sc.x >> (8 * sidx) : sc.y >> (8 * (sidx - 4))) & 0xff);
-            v += (float)scv * (dx[i][g] * (float)(dot - s32[i][g]));
+            int dot = dot4((int)qv[g][0], xv[mm][i][2 * g], 0);
+            dot = dot4((int)qv[g][1], xv[mm][i][2 * g + 1], dot);
+            v += scf[g] * (dx[mm][i][g] * (float)(dot - s32[mm][i][g]));
           }
-          acc += d * v;
+          acc[mm] += d * v;
         }
       }
-      acc = wave_sum(acc);
-      if (lane == 0) out[row0 + r] = acc;
+#pragma unroll
+      for (int mm = 0; mm < MM; mm++) {
+        const float s = wave_sum64(acc[mm]);
+        if (lane == 0 && m0 + mm < a.M) a.out[(int64_t)(m0 + mm) * a.N + row0 + r] = s;
+      }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -316,7 +427,7 @@ __global__ __launch_bounds__(256) void gemv_generic_kernel(const float *__restri
 #pragma unroll
       for (int j = 0; j < 8; j++) acc += y[j] * xr[8 * t + j];
     }
-    acc = wave_sum(acc);
+    acc = wave_sum64(acc);
     if (lane == 0) out[blockIdx.y * N + row] = acc;
   }
 }
@@ -325,7 +436,7 @@ __global__ __launch_bounds__(256) void gemv_generic_kernel(const float *__restri
 // Launch logic
 // ---------------------------------------------------------------------------
 
-static const int kCplSteps[] = {1, 2, 3, 4, 5, 6, 7, 8, 10, 12, 14, 16};
+static const int kCplSteps[] = {1, 2, 3, 4, 6, 8};
 
 static int pick_cpl(int64_t units) {
   int64_t need = cdiv(units, 64);
@@ -334,96 +445,121 @@ static int pick_cpl(int64_t units) {
   return 0;
 }
 
-// Fast (int8) GEMV applies: K fits the register budget and rows are 16-byte multiples.
-static bool gemv_fast_ok(int dt, int64_t K, const void *w) {
-  if (((uintptr_t)w & 15) != 0) return false;
+static int64_t staged_row_bytes(int dt, int64_t K) { return K / block_info(dt).elems * block_info(dt).bytes; }
+
+// The int8 GEMV applies: rows are 16-byte multiples, w is 16-byte aligned and K fits.
+bool gemv_fast_ok(int dt, int64_t K, const void *w) {
+  if (((uintptr_t)w & 15) != 0 || K % 32) return false;
   BlockInfo bi = block_info(dt);
-  int64_t nblk = K / bi.elems, row_bytes = nblk * bi.bytes;
+  if (!bi.elems || K % bi.elems) return false;
+  int64_t nb = K / bi.elems, row_bytes = nb * bi.bytes;
   if (row_bytes % 16) return false;
-  int64_t units = dt == Q4_K ? nblk * 8 : dt == Q6_K ? nblk * 8 : nblk;
-  if (!pick_cpl(units)) return false;
-  if (dt != Q4_K) {
-    int sb = dt == Q8_0 ? Staged<Q8_0>::SB : Staged<Q6_K>::SB;
-    if (nblk * sb + 16 > 16384) return false;  // one row must fit a wave's LDS slice
-  }
-  return true;
+  if (dt == Q4_K) return nb <= 128;  // team of <= 512 lanes
+  if (!pick_cpl(dt == Q8_0 ? nb : nb * 8)) return false;
+  return staged_row_bytes(dt, K) + 16 <= 16384;  // one row must fit a wave's LDS slice
 }
 
-template <int CPL, int R>
-static void run_q4k(const uint8_t *xq, const uint8_t *w, float *out, int64_t M, int64_t N, int64_t K, hipStream_t s) {
-  int64_t nblk = K / 256;
-  int64_t wgs = cdiv(cdiv(N, R), 4);
-  int64_t cap = (int64_t)device_cus() * 16;
-  dim3 grid((unsigned)(wgs < cap ? wgs : cap), (unsigned)M);
-  gemv_q4k_kernel<CPL, R><<<grid, 256, 0, s>>>(xq, w, out, (int)N, (int)(nblk * 8), nblk * 144, (K / 32) * 36);
+template <int R, int MM, bool PF>
+static void run_q4k(const Q4kArgs &a, int rw, int cap, hipStream_t s) {
+  int ngroups = (a.N + rw * R - 1) / (rw * R);
+  int grid = ngroups < cap ? ngroups : cap;
+  dim3 g((unsigned)grid, (unsigned)cdiv(a.M, MM));
+  gemv_q4k_kernel<R, MM, PF><<<g, a.TP * rw, 0, s>>>(a);
 }
 
-template <int DT, int CPL, int R>
-static void run_staged(const uint8_t *xq, const uint8_t *w, float *out, int64_t M, int64_t N, int64_t K,
-                       hipStream_t s) {
-  using S = Staged<DT>;
-  int64_t nblk = K / block_info(DT).elems;
-  int lds_wave = (int)(((R * nblk * S::SB + 16) + 15) & ~15);
-  int64_t wgs = cdiv(cdiv(N, R), 4);
-  int64_t cap = (int64_t)device_cus() * 16;
-  dim3 grid((unsigned)(wgs < cap ? wgs : cap), (unsigned)M);
-  gemv_staged_kernel<DT, CPL, R><<<grid, 256, 4 * lds_wave, s>>>(xq, w, out, (int)N, (int)nblk,
-                                                                  nblk * block_info(DT).bytes, (K / 32) * 36,
-                                                                  lds_wave);
-}
-
-#define CPL_SWITCH(cpl, CALL)        \
-  switch (cpl) {                     \
-    case 1: { constexpr int C = 1; CALL; } break;   \
-    case 2: { constexpr int C = 2; CALL; } break;   \
-    case 3: { constexpr int C = 3; CALL; } break;   \
-    case 4: { constexpr int C = 4; CALL; } break;   \
-    case 5: { constexpr int C = 5; CALL; } break;   \
-    case 6: { constexpr int C = 6; CALL; } break;   \
-    case 7: { constexpr int C = 7; CALL; } break;   \
-    case 8: { constexpr int C = 8; CALL; } break;   \
-    case 10: { constexpr int C = 10; CALL; } break; \
-    case 12: { constexpr int C = 12; CALL; } break; \
-    case 14: { constexpr int C = 14; CALL; } break; \
-    default: { constexpr int C = 16; CALL; } break; \
-  }
-
-template <int C>
-static void run_q4k_c(const uint8_t *xq, const uint8_t *w, float *out, int64_t M, int64_t N, int64_t K, hipStream_t s) {
-  if constexpr (C <= 2)
-    run_q4k<C, 4>(xq, w, out, M, N, K, s);
-  else if constexpr (C <= 8)
-    run_q4k<C, 2>(xq, w, out, M, N, K, s);
+template <int MM>
+static void dispatch_q4k(Q4kArgs a, hipStream_t s) {
+  const int rw = a.TP >= 256 ? 1 : 256 / a.TP;
+  const int cus = device_cus();
+  if (a.TP <= 128)
+    run_q4k<1, MM, true>(a, rw, cus * 4, s);
   else
-    run_q4k<C, 1>(xq, w, out, M, N, K, s);
+    run_q4k<2, MM, false>(a, rw, cus * 2, s);
 }
 
-template <int DT, int C>
-static void run_staged_c(const uint8_t *xq, const uint8_t *w, float *out, int64_t M, int64_t N, int64_t K,
-                         hipStream_t s) {
-  using S = Staged<DT>;
-  int64_t row_lds = (K / block_info(DT).elems) * S::SB;
-  if constexpr (C <= 4) {
-    if (4 * row_lds + 16 <= 16384) return run_staged<DT, C, 4>(xq, w, out, M, N, K, s);
+template <int CPL, int R, int MM>
+static void run_staged(int dt, StagedArgs a, hipStream_t s) {
+  a.lds_wave = (int)((R * a.row_bytes + 16 + 15) & ~(int64_t)15);
+  int64_t wgs = cdiv(cdiv(a.N, R), 4), cap = (int64_t)device_cus() * 8;
+  dim3 g((unsigned)(wgs < cap ? wgs : cap), (unsigned)cdiv(a.M, MM));
+  if (dt == Q8_0)
+    gemv_q80_kernel<CPL, R, MM><<<g, 256, 4 * a.lds_wave, s>>>(a);
+  else
+    gemv_q6k_kernel<CPL, R, MM><<<g, 256, 4 * a.lds_wave, s>>>(a);
+}
+
+template <int CPL, int MM>
+static void run_staged_r(int dt, StagedArgs a, hipStream_t s) {
+  if (4 * a.row_bytes + 16 <= 16384)
+    run_staged<CPL, 4, MM>(dt, a, s);
+  else if (2 * a.row_bytes + 16 <= 16384)
+    run_staged<CPL, 2, MM>(dt, a, s);
+  else
+    run_staged<CPL, 1, MM>(dt, a, s);
+}
+
+template <int MM>
+static void run_staged_m(int dt, StagedArgs a, int cpl, hipStream_t s) {
+  switch (cpl) {
+    case 1: run_staged_r<1, MM>(dt, a, s); break;
+    case 2: run_staged_r<2, MM>(dt, a, s); break;
+    case 3: run_staged_r<3, MM>(dt, a, s); break;
+    case 4: run_staged_r<4, MM>(dt, a, s); break;
+    case 6: run_staged_r<6, MM>(dt, a, s); break;
+    default: run_staged_r<8, MM>(dt, a, s); break;
   }
-  if (2 * row_lds + 16 <= 16384) return run_staged<DT, C, 2>(xq, w, out, M, N, K, s);
-  run_staged<DT, C, 1>(xq, w, out, M, N, K, s);
 }
 
-int launch_gemv_q8(const void *xqv, const void *wv, float *out, int64_t M, int64_t N, int64_t K, int dt,
-                   hipStream_t s) {
-  auto *xq = static_cast<const uint8_t *>(xqv);
+int launch_gemv_act(const void *act, const void *wv, float *out, int64_t M, int64_t N, int64_t K, int dt,
+                    hipStream_t s) {
+  if (N > INT32_MAX || M > 65535 * 4 || K > INT32_MAX)
+    return fail(HQ_EUNSUPPORTED, "gemv", "N, M or K too large");
   auto *w = static_cast<const uint8_t *>(wv);
-  if (N > INT32_MAX) return fail(HQ_EUNSUPPORTED, "gemv", "N=%lld too large", (long long)N);
-  int64_t nblk = K / block_info(dt).elems;
-  int cpl = pick_cpl(dt == Q8_0 ? nblk : nblk * 8);
-  switch (dt) {
-    case Q4_K: CPL_SWITCH(cpl, (run_q4k_c<C>(xq, w, out, M, N, K, s))); break;
-    case Q8_0: CPL_SWITCH(cpl, (run_staged_c<Q8_0, C>(xq, w, out, M, N, K, s))); break;
-    case Q6_K: CPL_SWITCH(cpl, (run_staged_c<Q6_K, C>(xq, w, out, M, N, K, s))); break;
-    default: return fail(HQ_EUNSUPPORTED, "gemv", "dtype %d", dt);
+  auto *xa = static_cast<const uint8_t *>(act);
+  const int MMc = M >= 3 ? 4 : (int)M;
+  if (dt == Q4_K) {
+    Q4kArgs a;
+    a.act = xa;
+    a.w = w;
+    a.out = out;
+    a.M = (int)M;
+    a.N = (int)N;
+    a.K = (int)K;
+    a.P = (int)(K / 256 * 4);
+    a.TP = (a.P + 15) & ~15;
+    a.row_bytes = K / 256 * 144;
+    a.d_off = act_d_off(M, K);
+    a.s_off = act_s_off(M, K);
+    if (MMc == 1)
+      dispatch_q4k<1>(a, s);
+    else if (MMc == 2)
+      dispatch_q4k<2>(a, s);
+    else
+      dispatch_q4k<4>(a, s);
+    return check_launch("gemv_q4k");
   }
-  return check_launch("gemv_q8");
+  if (dt != Q8_0 && dt != Q6_K) return fail(HQ_EUNSUPPORTED, "gemv", "dtype %d", dt);
+  StagedArgs a;
+  a.act = xa;
+  a.w = w;
+  a.out = out;
+  a.M = (int)M;
+  a.N = (int)N;
+  a.K = (int)K;
+  a.nb = (int)(K / block_info(dt).elems);
+  a.row_bytes = staged_row_bytes(dt, K);
+  a.d_off = act_d_off(M, K);
+  a.lds_wave = 0;
+  int cpl = pick_cpl(dt == Q8_0 ? a.nb : (int64_t)a.nb * 8);
+  // Q6_K keeps 16 registers of activations per unit and row of x: cap MM at 2.
+  int mm = dt == Q6_K && MMc > 2 ? 2 : MMc;
+  if (mm == 1)
+    run_staged_m<1>(dt, a, cpl, s);
+  else if (mm == 2)
+    run_staged_m<2>(dt, a, cpl, s);
+  else
+    run_staged_m<4>(dt, a, cpl, s);
+  return check_launch(dt == Q8_0 ? "gemv_q80" : "gemv_q6k");
 }
 
 static int launch_gemv_generic(const float *x, const void *wv, float *out, int64_t M, int64_t N, int64_t K, int dt,
@@ -442,26 +578,26 @@ static int launch_gemv_generic(const float *x, const void *wv, float *out, int64
   return check_launch("gemv_generic");
 }
 
-static size_t q8_bytes(int64_t M, int64_t K) { return ((size_t)M * (size_t)(K / 32) * 36 + 255) & ~(size_t)255; }
-
 static bool use_gemm(int64_t M, int dt) { return dt == Q4_K && M > kGemvMaxRows; }
 
 size_t matmul_q_ws_bytes(int64_t M, int64_t K, int dt) {
   if (M <= 0 || K <= 0 || K % 32) return 0;
-  return q8_bytes(M, K) + (use_gemm(M, dt) ? gemm_q4k_ws_bytes(M, K) : 0);
+  return (size_t)act_bytes(M, K) + (use_gemm(M, dt) ? gemm_q4k_ws_bytes(M, K) : 0);
 }
 
 const char *matmul_q_kernel_name(int64_t M, int dt) { return use_gemm(M, dt) ? "matmul_q.gemm" : "matmul_q.gemv"; }
 
+int launch_matmul_act(const void *act, const void *w, float *out, int64_t M, int64_t N, int64_t K, int dt,
+                      void *gemm_ws, hipStream_t s) {
+  if (use_gemm(M, dt)) return launch_gemm_q4k(act, w, out, M, N, K, gemm_ws, s);
+  return launch_gemv_act(act, w, out, M, N, K, dt, s);
+}
+
 int launch_matmul_q(const float *x, const void *w, float *out, int64_t M, int64_t N, int64_t K, int dt, void *ws,
                     hipStream_t s) {
-  if (use_gemm(M, dt)) {
-    if (int rc = launch_quantize_q8_1(x, F32, ws, M, K, s)) return rc;
-    return launch_gemm_q4k(ws, w, out, M, N, K, static_cast<char *>(ws) + q8_bytes(M, K), s);
-  }
-  if (!gemv_fast_ok(dt, K, w)) return launch_gemv_generic(x, w, out, M, N, K, dt, s);
-  if (int rc = launch_quantize_q8_1(x, F32, ws, M, K, s)) return rc;
-  return launch_gemv_q8(ws, w, out, M, N, K, dt, s);
+  if (!use_gemm(M, dt) && !gemv_fast_ok(dt, K, w)) return launch_gemv_generic(x, w, out, M, N, K, dt, s);
+  if (int rc = launch_quantize_act(x, F32, ws, M, K, s)) return rc;
+  return launch_matmul_act(ws, w, out, M, N, K, dt, static_cast<char *>(ws) + act_bytes(M, K), s);
 }
 
 }  // namespace hq

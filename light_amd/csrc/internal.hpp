@@ -31,6 +31,7 @@ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // ---- kernel launchers (one translation unit each) ----
 int launch_quantize_q8_1(const void *x, int x_dtype, void *dst, int64_t M, int64_t K, hipStream_t s);
+int launch_quantize_act(const void *x, int x_dtype, void *dst, int64_t M, int64_t K, hipStream_t s);
 int launch_dequant(const void *src, void *dst, int64_t n, int src_dtype, int out_dtype, hipStream_t s);
 // matmul_q: quantizes x into ws when the int8 path applies, then runs the GEMV
 // (M <= kGemvMaxRows) or the MFMA GEMM (Q4_K, larger M).
@@ -39,9 +40,12 @@ size_t matmul_q_ws_bytes(int64_t M, int64_t K, int dt);
 int launch_matmul_q(const float *x, const void *w, float *out, int64_t M, int64_t N, int64_t K, int dt, void *ws,
                     hipStream_t s);
 const char *matmul_q_kernel_name(int64_t M, int dt);
-// GEMV on pre-quantized q8_1 activations (shared with the MoE path for tests).
-int launch_gemv_q8(const void *xq, const void *w, float *out, int64_t M, int64_t N, int64_t K, int dt,
-                   hipStream_t s);
+// GEMV / GEMM on prepared (planar q8_1) activations.
+int launch_gemv_act(const void *act, const void *w, float *out, int64_t M, int64_t N, int64_t K, int dt,
+                    hipStream_t s);
+int launch_matmul_act(const void *act, const void *w, float *out, int64_t M, int64_t N, int64_t K, int dt,
+                      void *gemm_ws, hipStream_t s);
+bool gemv_fast_ok(int dt, int64_t K, const void *w);
 int launch_gemm_q4k(const void *xq, const void *w, float *out, int64_t M, int64_t N, int64_t K, void *ws,
                     hipStream_t s);
 size_t gemm_q4k_ws_bytes(int64_t M, int64_t K);

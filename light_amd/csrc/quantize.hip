@@ -1,4 +1,4 @@
-// quantize.hip -- on-GPU q8_1 activation quantizer.
+// quantize.hip -- on-GPU q8_1 activation quantizer (q8_1 blocks or the planar act layout).
 //
 // Block of 32 -> [f16 d][f16 s][i8 q[32]] (quant/q8_1.go:10-18).  Rounding follows
 // Light's encodeQ8_0 (quant/quantize.go:70-86): d = amax / 127 (f32), id = 1 / d
@@ -23,9 +23,9 @@ __device__ __forceinline__ void load4(const void *x, int64_t i, float v[4]) {
   }
 }
 
-template <int XDT>
+template <int XDT, bool ACT>
 __global__ __launch_bounds__(256) void quantize_q8_1_kernel(const void *__restrict__ x, uint8_t *__restrict__ dst,
-                                                            int64_t nblocks) {
+                                                            int64_t nblocks, int64_t d_off, int64_t s_off) {
   int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   int64_t blk = t >> 3;
   int sub = threadIdx.x & 7;
@@ -46,27 +46,45 @@ __global__ __launch_bounds__(256) void quantize_q8_1_kernel(const void *__restri
 #pragma unroll
   for (int o = 4; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 8);
   if (!live) return;
-  uint8_t *o = dst + blk * 36;
   uint32_t packed = (uint32_t)(q[0] & 0xff) | (uint32_t)(q[1] & 0xff) << 8 | (uint32_t)(q[2] & 0xff) << 16 |
                     (uint32_t)(q[3] & 0xff) << 24;
-  reinterpret_cast<uint32_t *>(o + 4)[sub] = packed;
-  if (sub == 0) {
-    uint32_t ds = (uint32_t)f2h_rne(d) | (uint32_t)f2h_rne(__fmul_rn((float)sum, d)) << 16;
-    *reinterpret_cast<uint32_t *>(o) = ds;
+  if constexpr (ACT) {
+    reinterpret_cast<uint32_t *>(dst + blk * 32)[sub] = packed;
+    if (sub == 0) {
+      reinterpret_cast<float *>(dst + d_off)[blk] = d;
+      reinterpret_cast<float *>(dst + s_off)[blk] = __fmul_rn(d, (float)sum);
+    }
+  } else {
+    uint8_t *o = dst + blk * 36;
+    reinterpret_cast<uint32_t *>(o + 4)[sub] = packed;
+    if (sub == 0) {
+      uint32_t ds = (uint32_t)f2h_rne(d) | (uint32_t)f2h_rne(__fmul_rn((float)sum, d)) << 16;
+      *reinterpret_cast<uint32_t *>(o) = ds;
+    }
   }
 }
 
-int launch_quantize_q8_1(const void *x, int x_dtype, void *dst, int64_t M, int64_t K, hipStream_t s) {
+template <bool ACT>
+static int launch_q(const void *x, int x_dtype, void *dst, int64_t M, int64_t K, hipStream_t s) {
   int64_t nblocks = M * (K / 32);
   dim3 grid((unsigned)cdiv(nblocks * 8, 256));
   auto *d = static_cast<uint8_t *>(dst);
+  int64_t doff = act_d_off(M, K), soff = act_s_off(M, K);
   switch (x_dtype) {
-    case F32: quantize_q8_1_kernel<F32><<<grid, 256, 0, s>>>(x, d, nblocks); break;
-    case BF16: quantize_q8_1_kernel<BF16><<<grid, 256, 0, s>>>(x, d, nblocks); break;
-    case F16: quantize_q8_1_kernel<F16><<<grid, 256, 0, s>>>(x, d, nblocks); break;
-    default: return fail(HQ_EUNSUPPORTED, "quantize_q8_1", "x dtype %d", x_dtype);
+    case F32: quantize_q8_1_kernel<F32, ACT><<<grid, 256, 0, s>>>(x, d, nblocks, doff, soff); break;
+    case BF16: quantize_q8_1_kernel<BF16, ACT><<<grid, 256, 0, s>>>(x, d, nblocks, doff, soff); break;
+    case F16: quantize_q8_1_kernel<F16, ACT><<<grid, 256, 0, s>>>(x, d, nblocks, doff, soff); break;
+    default: return fail(HQ_EUNSUPPORTED, "quantize", "x dtype %d", x_dtype);
   }
-  return check_launch("quantize_q8_1");
+  return check_launch("quantize");
+}
+
+int launch_quantize_q8_1(const void *x, int x_dtype, void *dst, int64_t M, int64_t K, hipStream_t s) {
+  return launch_q<false>(x, x_dtype, dst, M, K, s);
+}
+
+int launch_quantize_act(const void *x, int x_dtype, void *dst, int64_t M, int64_t K, hipStream_t s) {
+  return launch_q<true>(x, x_dtype, dst, M, K, s);
 }
 
 }  // namespace hq

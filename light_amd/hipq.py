@@ -53,6 +53,10 @@ SIGNATURES = {
     "hq_trace_stop": (_I, [ctypes.c_char_p, ctypes.POINTER(_I), ctypes.POINTER(ctypes.c_double), _I]),
     "hq_matmul_q_ws_bytes": (_SZ, [_I64, _I64, _I]),
     "hq_matmul_q": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _P, _SZ, _P]),
+    "hq_act_bytes": (_SZ, [_I64, _I64]),
+    "hq_quantize_act": (_I, [_P, _I, _P, _I64, _I64, _P]),
+    "hq_matmul_q_act_ws_bytes": (_SZ, [_I64, _I64, _I]),
+    "hq_matmul_q_act": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _P, _SZ, _P]),
     "hq_dequant": (_I, [_P, _P, _I64, _I, _I, _P]),
     "hq_quantize_q8_1": (_I, [_P, _I, _P, _I64, _I64, _P]),
     "hq_int4_matmul_ws_bytes": (_SZ, [_I64, _I64, _I]),
@@ -124,6 +128,27 @@ def matmul_q(x, w, N, K, w_dtype, out=None, ws=None, stream=None):
         out = torch.empty((M, N), dtype=torch.float32, device=x.device)
     ws_bytes = 0 if ws is None else ws.numel() * ws.element_size()
     check(lib().hq_matmul_q(_ptr(x), _ptr(w), _ptr(out), M, N, K, w_dtype, _ptr(ws), ws_bytes, _stream(stream)))
+    return out
+
+
+def quantize_act(x, out=None, stream=None):
+    """Prepared activations of x (M, K) (planar q8_1) for matmul_q_act."""
+    import torch
+    M, K = x.shape
+    if out is None:
+        out = torch.empty(lib().hq_act_bytes(M, K), dtype=torch.uint8, device=x.device)
+    check(lib().hq_quantize_act(_ptr(x), _torch_dtype_code(x), _ptr(out), M, K, _stream(stream)))
+    return out
+
+
+def matmul_q_act(act, w, M, N, K, w_dtype, out=None, ws=None, stream=None):
+    """out (M, N) f32 from prepared activations and GGUF weight bytes w."""
+    import torch
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float32, device=w.device)
+    ws_bytes = 0 if ws is None else ws.numel() * ws.element_size()
+    check(lib().hq_matmul_q_act(_ptr(act), _ptr(w), _ptr(out), M, N, K, w_dtype, _ptr(ws), ws_bytes,
+                                _stream(stream)))
     return out
 
 

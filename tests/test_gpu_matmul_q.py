@@ -161,3 +161,38 @@ def test_matmul_q_explicit_workspace_and_stream(dev):
     small = torch.empty(16, dtype=torch.uint8, device=dev)
     with pytest.raises(hipq.HipqError):
         hipq.matmul_q(x, w, N, K, hipq.Q6_K, ws=small)
+
+
+def test_prepared_activations_match_q8_1(dev):
+    """The planar act layout holds exactly q8_1's quants; d is q8_1's d before f16 rounding."""
+    g = np.random.default_rng(12)
+    M, K = 3, 2048
+    x = (g.standard_normal((M, K)) * 3).astype(np.float32)
+    xt = _t(x, dev)
+    act = hipq.quantize_act(xt).cpu().numpy()
+    q81 = oracle.quantize_q8_1(x).reshape(-1, 36)
+    nb = M * K // 32
+    assert np.array_equal(act[:M * K].reshape(-1, 32), q81[:, 4:])
+    d_off = (M * K + 15) & ~15
+    d = act[d_off:d_off + 4 * nb].view(np.float32)
+    sx = act[d_off + 4 * nb:d_off + 8 * nb].view(np.float32)
+    amax = np.abs(x.reshape(-1, 32)).max(1)
+    assert np.array_equal(d, amax / np.float32(127))
+    assert np.array_equal(d.astype(np.float16).view(np.uint16), q81[:, 0:2].copy().view("<u2")[:, 0])
+    qsum = q81[:, 4:].view(np.int8).astype(np.int64).sum(1)
+    assert np.array_equal(sx, d * qsum.astype(np.float32))
+
+
+@pytest.mark.parametrize("dt", FMTS)
+@pytest.mark.parametrize("M", [1, 2, 3, 5, 8])
+def test_matmul_q_act_equals_matmul_q(dev, dt, M):
+    g = np.random.default_rng(M + dt)
+    N, K = 200, 4096
+    w = _t(synth.gguf_weight(dt, N, K, g), dev)
+    x = _t(synth.activations(M, K, g), dev)
+    y1 = hipq.matmul_q(x, w, N, K, dt)
+    act = hipq.quantize_act(x)
+    y2 = hipq.matmul_q_act(act, w, M, N, K, dt)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+    _check_matmul(dev, dt, x.cpu().numpy(), w.cpu().numpy(), N, K, "act")
