@@ -93,7 +93,7 @@ def run_gpu(args):
     x = torch.from_numpy(x_np).to(dev)
     h = torch.from_numpy(h_np).to(dev)
     H, I = 4096, 14336
-    ws = torch.empty(max(hipq.matmul_q_ws_bytes(1, H, hipq.Q4_K), hipq.matmul_q_ws_bytes(1, I, hipq.Q4_K)),
+    ws = torch.empty(max(hipq.matmul_q_ws_bytes(1, I, H, hipq.Q4_K), hipq.matmul_q_ws_bytes(1, H, I, hipq.Q4_K)),
                      dtype=torch.uint8, device=dev)
     yg = torch.empty((1, I), device=dev)
     yu = torch.empty((1, I), device=dev)
@@ -204,7 +204,7 @@ def table(args, dev):
                 w = Weight(synth.gguf_weight(dt, N, K, g), dt, N, K, dev)
                 x = torch.from_numpy(synth.activations(M, K, g)).to(dev)
                 out = torch.empty((M, N), device=dev)
-                ws = torch.empty(hipq.matmul_q_ws_bytes(M, K, dt), dtype=torch.uint8, device=dev)
+                ws = torch.empty(hipq.matmul_q_ws_bytes(M, N, K, dt), dtype=torch.uint8, device=dev)
                 us = time_launches(lambda i: hipq.matmul_q(x, w[i], N, K, dt, out=out, ws=ws), 100,
                                    len(w.copies))
                 nbytes = w.raw.nbytes + 4 * M * K + 4 * M * N

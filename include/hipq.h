@@ -90,14 +90,14 @@ int hq_trace_stop(char *names, int *calls, double *total_us, int n_max);
 
 /* ---- ops ----------------------------------------------------------------- */
 
-/* Workspace bytes hq_matmul_q needs for x (M, K) and weight dtype w_dtype. */
-size_t hq_matmul_q_ws_bytes(int64_t M, int64_t K, int w_dtype);
+/* Workspace bytes hq_matmul_q needs for x (M, K), a weight (N, K) and w_dtype. */
+size_t hq_matmul_q_ws_bytes(int64_t M, int64_t N, int64_t K, int w_dtype);
 
 /* out (M, N) F32 = x (M, K) F32 contiguous @ dequant(w (N, K))^T.
  * w_dtype: HQ_Q8_0, HQ_Q4_K or HQ_Q6_K.  K must be a multiple of the block
- * size.  x is quantized on the GPU to q8_1 (see hq_quantize_q8_1) into ws,
- * then M <= 8 runs the wave-per-row int8-dot GEMV and larger M (Q4_K) the
- * MFMA GEMM.
+ * size.  M <= 8 (and Q8_0 / Q6_K at any M): x is quantized on the GPU to q8_1
+ * into ws and the int8-dot GEMV runs; Q4_K with M > 8: x is rounded to bf16
+ * into ws and the bf16 MFMA GEMM runs.
  * Replaces registry kernel "matmul_q" (ops/matmul_q.go:61-75; CUDA launcher
  * kernels/cuda/matmul_q.go:44-91) and, since it serves every M, the M >= 8
  * dequant + cuBLAS fallback (ops/matmul_q.go:52-59, 85-95). */
@@ -114,7 +114,7 @@ int hq_matmul_q(const float *x, const void *w, float *out, int64_t M, int64_t N,
 size_t hq_act_bytes(int64_t M, int64_t K);
 int hq_quantize_act(const void *x, int x_dtype, void *act, int64_t M, int64_t K, hq_stream_t stream);
 /* Workspace hq_matmul_q_act needs beyond the act buffer (0 for the GEMV). */
-size_t hq_matmul_q_act_ws_bytes(int64_t M, int64_t K, int w_dtype);
+size_t hq_matmul_q_act_ws_bytes(int64_t M, int64_t N, int64_t K, int w_dtype);
 /* out (M, N) F32 = x @ dequant(w)^T from prepared activations.  For M <= 8 the
  * weight must take the int8 GEMV (16-byte aligned, rows a multiple of 16 bytes;
  * HQ_EUNSUPPORTED otherwise). */

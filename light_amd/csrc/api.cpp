@@ -197,7 +197,7 @@ int hq_trace_stop(char *names, int *calls, double *total_us, int n_max) {
 
 static bool is_gguf(int dt) { return dt == HQ_Q8_0 || dt == HQ_Q4_K || dt == HQ_Q6_K; }
 
-size_t hq_matmul_q_ws_bytes(int64_t M, int64_t K, int w_dtype) { return matmul_q_ws_bytes(M, K, w_dtype); }
+size_t hq_matmul_q_ws_bytes(int64_t M, int64_t N, int64_t K, int w_dtype) { return matmul_q_ws_bytes(M, N, K, w_dtype); }
 
 int hq_matmul_q(const float *x, const void *w, float *out, int64_t M, int64_t N, int64_t K, int w_dtype,
                 void *ws, size_t ws_bytes, hq_stream_t stream) {
@@ -213,7 +213,7 @@ int hq_matmul_q(const float *x, const void *w, float *out, int64_t M, int64_t N,
   if (((uintptr_t)x & 15) || ((uintptr_t)w & 15) || ((uintptr_t)out & 3))
     return fail(HQ_EINVAL, call, "x and w must be 16-byte aligned, out 4-byte aligned");
   hipStream_t s = resolve(stream);
-  size_t need = matmul_q_ws_bytes(M, K, w_dtype);
+  size_t need = matmul_q_ws_bytes(M, N, K, w_dtype);
   if (!ws) {
     if (int rc = workspace(need, s, &ws, call)) return rc;
   } else if (ws_bytes < need) {
@@ -241,9 +241,8 @@ int hq_quantize_act(const void *x, int x_dtype, void *act, int64_t M, int64_t K,
   return launch_quantize_act(x, x_dtype, act, M, K, s);
 }
 
-size_t hq_matmul_q_act_ws_bytes(int64_t M, int64_t K, int w_dtype) {
-  size_t all = matmul_q_ws_bytes(M, K, w_dtype), act = hq_act_bytes(M, K);
-  return all > act ? all - act : 0;
+size_t hq_matmul_q_act_ws_bytes(int64_t M, int64_t N, int64_t K, int w_dtype) {
+  return matmul_act_ws_bytes(M, N, K, w_dtype);
 }
 
 int hq_matmul_q_act(const void *act, const void *w, float *out, int64_t M, int64_t N, int64_t K, int w_dtype,
@@ -260,7 +259,7 @@ int hq_matmul_q_act(const void *act, const void *w, float *out, int64_t M, int64
   if (M <= kGemvMaxRows && !gemv_fast_ok(w_dtype, K, w))
     return fail(HQ_EUNSUPPORTED, call, "weight layout needs the F32 path (hq_matmul_q)");
   hipStream_t s = resolve(stream);
-  size_t need = hq_matmul_q_act_ws_bytes(M, K, w_dtype);
+  size_t need = hq_matmul_q_act_ws_bytes(M, N, K, w_dtype);
   if (need && !ws) {
     if (int rc = workspace(need, s, &ws, call)) return rc;
   } else if (need && ws_bytes < need) {

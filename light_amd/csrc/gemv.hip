@@ -578,26 +578,42 @@ static int launch_gemv_generic(const float *x, const void *wv, float *out, int64
   return check_launch("gemv_generic");
 }
 
-static bool use_gemm(int64_t M, int dt) { return dt == Q4_K && M > kGemvMaxRows; }
+bool use_gemm(int64_t M, int dt) { return dt == Q4_K && M > kGemvMaxRows; }
 
-size_t matmul_q_ws_bytes(int64_t M, int64_t K, int dt) {
+static size_t gemm_ws(int64_t M, int64_t N, int64_t K) { return gemm_q4k_ws_bytes(M, K) + gemm_q4k_partial_bytes(M, N, K); }
+
+size_t matmul_q_ws_bytes(int64_t M, int64_t N, int64_t K, int dt) {
   if (M <= 0 || K <= 0 || K % 32) return 0;
-  return (size_t)act_bytes(M, K) + (use_gemm(M, dt) ? gemm_q4k_ws_bytes(M, K) : 0);
+  return use_gemm(M, dt) ? gemm_ws(M, N, K) : (size_t)act_bytes(M, K);
+}
+
+size_t matmul_act_ws_bytes(int64_t M, int64_t N, int64_t K, int dt) {
+  if (M <= 0 || K <= 0 || K % 32) return 0;
+  return use_gemm(M, dt) ? gemm_ws(M, N, K) : 0;
 }
 
 const char *matmul_q_kernel_name(int64_t M, int dt) { return use_gemm(M, dt) ? "matmul_q.gemm" : "matmul_q.gemv"; }
 
-int launch_matmul_act(const void *act, const void *w, float *out, int64_t M, int64_t N, int64_t K, int dt,
-                      void *gemm_ws, hipStream_t s) {
-  if (use_gemm(M, dt)) return launch_gemm_q4k(act, w, out, M, N, K, gemm_ws, s);
+static int run_gemm(const void *src, bool from_act, const void *w, float *out, int64_t M, int64_t N, int64_t K,
+                    void *ws, hipStream_t s) {
+  auto *xb = static_cast<uint16_t *>(ws);
+  float *partials = reinterpret_cast<float *>(static_cast<char *>(ws) + gemm_q4k_ws_bytes(M, K));
+  if (int rc = launch_to_bf16(src, from_act, xb, M, K, s)) return rc;
+  return launch_gemm_q4k_bf16(xb, w, out, partials, M, N, K, s);
+}
+
+int launch_matmul_act(const void *act, const void *w, float *out, int64_t M, int64_t N, int64_t K, int dt, void *ws,
+                      hipStream_t s) {
+  if (use_gemm(M, dt)) return run_gemm(act, true, w, out, M, N, K, ws, s);
   return launch_gemv_act(act, w, out, M, N, K, dt, s);
 }
 
 int launch_matmul_q(const float *x, const void *w, float *out, int64_t M, int64_t N, int64_t K, int dt, void *ws,
                     hipStream_t s) {
-  if (!use_gemm(M, dt) && !gemv_fast_ok(dt, K, w)) return launch_gemv_generic(x, w, out, M, N, K, dt, s);
+  if (use_gemm(M, dt)) return run_gemm(x, false, w, out, M, N, K, ws, s);
+  if (!gemv_fast_ok(dt, K, w)) return launch_gemv_generic(x, w, out, M, N, K, dt, s);
   if (int rc = launch_quantize_act(x, F32, ws, M, K, s)) return rc;
-  return launch_matmul_act(ws, w, out, M, N, K, dt, static_cast<char *>(ws) + act_bytes(M, K), s);
+  return launch_gemv_act(ws, w, out, M, N, K, dt, s);
 }
 
 }  // namespace hq

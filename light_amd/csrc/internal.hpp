@@ -33,10 +33,12 @@ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 int launch_quantize_q8_1(const void *x, int x_dtype, void *dst, int64_t M, int64_t K, hipStream_t s);
 int launch_quantize_act(const void *x, int x_dtype, void *dst, int64_t M, int64_t K, hipStream_t s);
 int launch_dequant(const void *src, void *dst, int64_t n, int src_dtype, int out_dtype, hipStream_t s);
-// matmul_q: quantizes x into ws when the int8 path applies, then runs the GEMV
-// (M <= kGemvMaxRows) or the MFMA GEMM (Q4_K, larger M).
+// matmul_q: quantizes x (GEMV, M <= kGemvMaxRows) or converts it to bf16 (Q4_K MFMA GEMM)
+// in ws, then runs the kernel.
 constexpr int64_t kGemvMaxRows = 8;
-size_t matmul_q_ws_bytes(int64_t M, int64_t K, int dt);
+bool use_gemm(int64_t M, int dt);
+size_t matmul_q_ws_bytes(int64_t M, int64_t N, int64_t K, int dt);
+size_t matmul_act_ws_bytes(int64_t M, int64_t N, int64_t K, int dt);
 int launch_matmul_q(const float *x, const void *w, float *out, int64_t M, int64_t N, int64_t K, int dt, void *ws,
                     hipStream_t s);
 const char *matmul_q_kernel_name(int64_t M, int dt);
@@ -44,11 +46,14 @@ const char *matmul_q_kernel_name(int64_t M, int dt);
 int launch_gemv_act(const void *act, const void *w, float *out, int64_t M, int64_t N, int64_t K, int dt,
                     hipStream_t s);
 int launch_matmul_act(const void *act, const void *w, float *out, int64_t M, int64_t N, int64_t K, int dt,
-                      void *gemm_ws, hipStream_t s);
+                      void *ws, hipStream_t s);
 bool gemv_fast_ok(int dt, int64_t K, const void *w);
-int launch_gemm_q4k(const void *xq, const void *w, float *out, int64_t M, int64_t N, int64_t K, void *ws,
-                    hipStream_t s);
+// Q4_K MFMA GEMM on bf16 activations; partials: split-K scratch (gemm_q4k_partial_bytes).
+int launch_gemm_q4k_bf16(const uint16_t *xb, const void *w, float *out, float *partials, int64_t M, int64_t N,
+                         int64_t K, hipStream_t s);
 size_t gemm_q4k_ws_bytes(int64_t M, int64_t K);
+size_t gemm_q4k_partial_bytes(int64_t M, int64_t N, int64_t K);
+int launch_to_bf16(const void *src, bool from_act, uint16_t *dst, int64_t M, int64_t K, hipStream_t s);
 int device_cus();
 int launch_int4_dequant(const uint32_t *codes, const float *s, const float *z, void *out, int out_dtype,
                         int64_t N, int64_t K, int G, int64_t off, hipStream_t st);

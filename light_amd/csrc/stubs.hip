@@ -1,10 +1,6 @@
 // stubs.hip -- entry points not yet implemented on the GPU.
 #include "internal.hpp"
 namespace hq {
-size_t gemm_q4k_ws_bytes(int64_t, int64_t) { return 0; }
-int launch_gemm_q4k(const void *xq, const void *w, float *out, int64_t M, int64_t N, int64_t K, void *, hipStream_t s) {
-  return launch_gemv_act(xq, w, out, M, N, K, Q4_K, s);
-}
 size_t int4_ws_bytes(int64_t, int64_t, int) { return 0; }
 int launch_int4_dequant(const uint32_t *, const float *, const float *, void *, int, int64_t, int64_t, int, int64_t, hipStream_t) {
   return fail(HQ_EUNSUPPORTED, "int4_dequant", "not built");

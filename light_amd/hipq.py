@@ -51,11 +51,11 @@ SIGNATURES = {
     "hq_stream_get_current": (_P, []),
     "hq_trace_start": (_I, []),
     "hq_trace_stop": (_I, [ctypes.c_char_p, ctypes.POINTER(_I), ctypes.POINTER(ctypes.c_double), _I]),
-    "hq_matmul_q_ws_bytes": (_SZ, [_I64, _I64, _I]),
+    "hq_matmul_q_ws_bytes": (_SZ, [_I64, _I64, _I64, _I]),
     "hq_matmul_q": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _P, _SZ, _P]),
     "hq_act_bytes": (_SZ, [_I64, _I64]),
     "hq_quantize_act": (_I, [_P, _I, _P, _I64, _I64, _P]),
-    "hq_matmul_q_act_ws_bytes": (_SZ, [_I64, _I64, _I]),
+    "hq_matmul_q_act_ws_bytes": (_SZ, [_I64, _I64, _I64, _I]),
     "hq_matmul_q_act": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _P, _SZ, _P]),
     "hq_dequant": (_I, [_P, _P, _I64, _I, _I, _P]),
     "hq_quantize_q8_1": (_I, [_P, _I, _P, _I64, _I64, _P]),
@@ -152,8 +152,8 @@ def matmul_q_act(act, w, M, N, K, w_dtype, out=None, ws=None, stream=None):
     return out
 
 
-def matmul_q_ws_bytes(M, K, w_dtype):
-    return lib().hq_matmul_q_ws_bytes(M, K, w_dtype)
+def matmul_q_ws_bytes(M, N, K, w_dtype):
+    return lib().hq_matmul_q_ws_bytes(M, N, K, w_dtype)
 
 
 def dequant(src, n, src_dtype, out_dtype=F32, out=None, stream=None):

@@ -63,7 +63,7 @@ def test_matmul_q_empty_is_ok_and_null_is_error():
 
 def test_matmul_q_workspace_too_small():
     L = hipq.lib()
-    need = L.hq_matmul_q_ws_bytes(3, 4096, hipq.Q4_K)
+    need = L.hq_matmul_q_ws_bytes(3, 4, 4096, hipq.Q4_K)
     assert need >= 3 * 128 * 36
     rc = L.hq_matmul_q(1 << 12, 1 << 12, 1 << 12, 3, 4, 4096, hipq.Q4_K, 1 << 12, need - 1, None)
     assert rc == hipq.HQ_ENOMEM

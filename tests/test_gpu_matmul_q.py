@@ -150,7 +150,7 @@ def test_matmul_q_explicit_workspace_and_stream(dev):
     N, K = 96, 4096
     w = _t(synth.gguf_weight(hipq.Q6_K, N, K, g), dev)
     x = _t(synth.activations(2, K, g), dev)
-    ws = torch.empty(hipq.matmul_q_ws_bytes(2, K, hipq.Q6_K), dtype=torch.uint8, device=dev)
+    ws = torch.empty(hipq.matmul_q_ws_bytes(2, N, K, hipq.Q6_K), dtype=torch.uint8, device=dev)
     s = torch.cuda.Stream()
     with torch.cuda.stream(s):
         y1 = hipq.matmul_q(x, w, N, K, hipq.Q6_K, ws=ws)
@@ -196,3 +196,48 @@ def test_matmul_q_act_equals_matmul_q(dev, dt, M):
     torch.cuda.synchronize()
     assert torch.equal(y1, y2)
     _check_matmul(dev, dt, x.cpu().numpy(), w.cpu().numpy(), N, K, "act")
+
+
+# ---- Q4_K prefill GEMM (MFMA) ----------------------------------------------
+
+@pytest.mark.parametrize("M,N,K", [(9, 13, 1024), (17, 128, 256), (100, 200, 2048), (256, 256, 4096),
+                                   (300, 130, 1024), (64, 4096, 4096), (513, 384, 2560)])
+def test_gemm_q4_k_shapes(dev, M, N, K):
+    g = np.random.default_rng(M * 31 + N + K)
+    x = synth.activations(M, K, g)
+    w = synth.gguf_weight(hipq.Q4_K, N, K, g)
+    _check_matmul(dev, hipq.Q4_K, x, w, N, K, "gemm")
+
+
+@pytest.mark.parametrize("name", ["q4_k_gemm_m512_14336x4096", "q4_k_gemm_m512_4096x14336"])
+def test_gemm_q4_k_benchmark_configs(dev, name):
+    """Full M=512 configs on the GPU; Light's CPU path and the f64 oracle on a sample of 48 rows."""
+    c = synth.CONFIGS[name]
+    g = synth.rng(c["cfg"])
+    M, N, K = c["M"], c["N"], c["K"]
+    w = synth.gguf_weight(hipq.Q4_K, N, K, g)
+    x = synth.activations(M, K, g)
+    print(f"[case] gemm {name}", flush=True)
+    y = hipq.matmul_q(_t(x, dev), _t(w, dev), N, K, hipq.Q4_K).cpu().numpy()
+    rows = np.sort(np.random.default_rng(0).choice(M, 48, replace=False))
+    cpu = oracle.matmul_q(x[rows], w, N, K, hipq.Q4_K)
+    wd = oracle.dequant(hipq.Q4_K, w, N * K).reshape(N, K)
+    ref, _, wn, xn = oracle.matmul_f64(x[rows], wd)
+    assert norm_err(y[rows], cpu, wn, xn) <= TOL
+    assert norm_err(y[rows], ref, wn, xn) <= TOL
+    assert np.all(np.isfinite(y))
+
+
+def test_gemm_act_path_matches(dev):
+    """hq_matmul_q_act at M > 8 (act -> bf16 -> GEMM) stays within tolerance of the F32 path."""
+    g = np.random.default_rng(77)
+    M, N, K = 40, 300, 2048
+    x = synth.activations(M, K, g)
+    w = synth.gguf_weight(hipq.Q4_K, N, K, g)
+    xt, wt = _t(x, dev), _t(w, dev)
+    act = hipq.quantize_act(xt)
+    ws = torch.empty(hipq.lib().hq_matmul_q_act_ws_bytes(M, N, K, hipq.Q4_K), dtype=torch.uint8, device=dev)
+    y = hipq.matmul_q_act(act, wt, M, N, K, hipq.Q4_K, ws=ws).cpu().numpy()
+    wd = oracle.dequant(hipq.Q4_K, w, N * K).reshape(N, K)
+    ref, _, wn, xn = oracle.matmul_f64(x, wd)
+    assert norm_err(y, ref, wn, xn) <= TOL
