@@ -133,13 +133,16 @@ int hq_dequant(const void *src, void *dst, int64_t n, int src_dtype, int out_dty
  * encoder); bit-exact with the specification. */
 int hq_quantize_q8_1(const void *x, int x_dtype, void *dst, int64_t M, int64_t K, hq_stream_t stream);
 
-/* Workspace bytes hq_int4_matmul needs. */
-size_t hq_int4_matmul_ws_bytes(int64_t M, int64_t K, int G);
+/* Workspace bytes hq_int4_matmul needs (x (M, K) of x_dtype, weight (N, K), group G). */
+size_t hq_int4_matmul_ws_bytes(int64_t M, int64_t N, int64_t K, int G, int x_dtype);
 
 /* y (M, N) = x (M, K) @ W^T for Light's canonical 4-bit layout (quant.Int4,
  * quant/int4.go:11-34): codes U32 (N, K/8), nibble j of word c = W[n, 8c+j];
  * scales / zeros F32 (N, K/G); W = s * (code - z).  x_dtype F32, BF16 or F16;
- * y has x's dtype.  K % 32 == 0 and G % 32 == 0.
+ * y has x's dtype (F16 is an extension: Light takes F32 or BF16, ops/int4.go:70-72).
+ * K % 32 == 0 and G % 32 == 0.  M <= 8 (or G % 64 != 0): x is quantized to q8_1
+ * into ws and the int8-dot GEMV runs; otherwise x is rounded to bf16 into ws and
+ * the bf16 MFMA GEMM runs.
  * Replaces registry kernel "int4_gemv" (ops/int4.go:87-99; kernels/cuda/int4.go:76-101)
  * and, since it serves every M, the dequant + GEMM path (ops/int4.go:100-126). */
 int hq_int4_matmul(const void *x, int x_dtype, const uint32_t *codes, const float *scales, const float *zeros,

@@ -295,7 +295,9 @@ int hq_quantize_q8_1(const void *x, int x_dtype, void *dst, int64_t M, int64_t K
   return launch_quantize_q8_1(x, x_dtype, dst, M, K, s);
 }
 
-size_t hq_int4_matmul_ws_bytes(int64_t M, int64_t K, int G) { return int4_ws_bytes(M, K, G); }
+size_t hq_int4_matmul_ws_bytes(int64_t M, int64_t N, int64_t K, int G, int x_dtype) {
+  return int4_ws_bytes(M, N, K, G, x_dtype);
+}
 
 int hq_int4_matmul(const void *x, int x_dtype, const uint32_t *codes, const float *scales, const float *zeros,
                    void *y, int64_t M, int64_t N, int64_t K, int G, void *ws, size_t ws_bytes,
@@ -309,7 +311,8 @@ int hq_int4_matmul(const void *x, int x_dtype, const uint32_t *codes, const floa
   if (M == 0 || N == 0) return HQ_OK;
   if (!x || !codes || !scales || !zeros || !y) return fail(HQ_EINVAL, call, "NULL pointer");
   hipStream_t s = resolve(stream);
-  size_t need = int4_ws_bytes(M, K, G);
+  if (((uintptr_t)x & 15)) return fail(HQ_EINVAL, call, "x must be 16-byte aligned");
+  size_t need = int4_ws_bytes(M, N, K, G, x_dtype);
   if (!ws) {
     if (int rc = workspace(need, s, &ws, call)) return rc;
   } else if (ws_bytes < need) {

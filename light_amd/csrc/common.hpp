@@ -20,14 +20,17 @@ enum DType : int {
 
 constexpr int kWave = 64;  // CDNA wavefront width
 
-// Prepared activations ("act" layout, internal to libhipq) for x (M, K): the q8_1
-// quantization of x, stored planar so kernels can use 16-byte loads:
-//   qs  int8 [M][K]      at 0
-//   d   f32  [M][K/32]   at act_d_off(M, K)   (the f32 d, before q8_1's f16 rounding)
-//   sx  f32  [M][K/32]   at act_s_off(M, K)   (d * sum of the block's q, exact integer sum)
-// q is bit-identical to the q8_1 quants of the same x.
-__host__ __device__ constexpr int64_t act_d_off(int64_t M, int64_t K) { return (M * K + 15) & ~(int64_t)15; }
-__host__ __device__ constexpr int64_t act_s_off(int64_t M, int64_t K) { return act_d_off(M, K) + 4 * M * (K / 32); }
+// Prepared activations ("act" layout, internal to libhipq) for x (M, K): a two-level
+// int8 quantization of x, stored planar so kernels can use 16-byte loads:
+//   q1  int8   [M][K]      at 0                 q8_1's quants of x (d = amax / 127)
+//   q2  int8   [M][K]      at act_q2_off(M, K)  quants of the residual x - d*q1, step e = d / 254
+//   de  f32x2  [M][K/32]   at act_d_off(M, K)   (d, e) per 32-block (d before q8_1's f16 rounding)
+//   sx  f32    [M][K/32]   at act_s_off(M, K)   sum of the block's x (f32)
+// x ~= d*q1 + e*q2 with |error| <= e/2: about 2^-15 of the block's amax.  q1 and d are
+// bit-identical to the q8_1 quantization of the same x.
+__host__ __device__ constexpr int64_t act_q2_off(int64_t M, int64_t K) { return (M * K + 255) & ~(int64_t)255; }
+__host__ __device__ constexpr int64_t act_d_off(int64_t M, int64_t K) { return 2 * act_q2_off(M, K); }
+__host__ __device__ constexpr int64_t act_s_off(int64_t M, int64_t K) { return act_d_off(M, K) + 8 * M * (K / 32); }
 __host__ __device__ constexpr int64_t act_bytes(int64_t M, int64_t K) {
   return (act_s_off(M, K) + 4 * M * (K / 32) + 255) & ~(int64_t)255;
 }

@@ -79,11 +79,11 @@ __device__ __forceinline__ int byte_sum(const int *v, int n) {
 // Q4_K
 // ---------------------------------------------------------------------------
 struct Q4kArgs {
-  const uint8_t *act;  // planar activations
+  const uint8_t *act;  // planar two-level activations
   const uint8_t *w;
   float *out;
   int M, N, K, P, TP;  // P = pairs per row (nb * 4), TP = team lanes (P rounded up to 16)
-  int64_t row_bytes, d_off, s_off;
+  int64_t row_bytes, q2_off, d_off, s_off;
 };
 
 template <int R, int MM, bool PF>
@@ -121,24 +121,31 @@ __global__ __launch_bounds__(512) void gemv_q4k_kernel(Q4kArgs a) {
   int g = blockIdx.x;
   if (g < ngroups) load(g, q0, q1, hd);
 
-  // Activations of this lane's two sub-blocks, for MM rows of x.
+  // Activations of this lane's two sub-blocks (both levels), for MM rows of x.
   const int ja = b * 8 + 2 * p;
-  int xa[MM][8], xb[MM][8];
-  float2 dd[MM], ss[MM];
+  int xa[MM][8], xb[MM][8], ya[MM][8], yb[MM][8];
+  float4 de[MM];  // (dA, eA, dB, eB)
+  float2 ss[MM];  // block sums of x
 #pragma unroll
   for (int mm = 0; mm < MM; mm++) {
     const int m = m0 + mm < a.M ? m0 + mm : a.M - 1;
     const int64_t blk = (int64_t)m * (a.K / 32) + ja;
     const uint4 *xs = reinterpret_cast<const uint4 *>(a.act + blk * 32);
+    const uint4 *x2 = reinterpret_cast<const uint4 *>(a.act + a.q2_off + blk * 32);
     const uint4 v0 = xs[0], v1 = xs[1], v2 = xs[2], v3 = xs[3];
+    const uint4 u0 = x2[0], u1 = x2[1], u2 = x2[2], u3 = x2[3];
     const int A[8] = {(int)v0.x, (int)v0.y, (int)v0.z, (int)v0.w, (int)v1.x, (int)v1.y, (int)v1.z, (int)v1.w};
     const int B[8] = {(int)v2.x, (int)v2.y, (int)v2.z, (int)v2.w, (int)v3.x, (int)v3.y, (int)v3.z, (int)v3.w};
+    const int C[8] = {(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w, (int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
+    const int D[8] = {(int)u2.x, (int)u2.y, (int)u2.z, (int)u2.w, (int)u3.x, (int)u3.y, (int)u3.z, (int)u3.w};
 #pragma unroll
     for (int k = 0; k < 8; k++) {
       xa[mm][k] = A[k];
       xb[mm][k] = B[k];
+      ya[mm][k] = C[k];
+      yb[mm][k] = D[k];
     }
-    dd[mm] = *reinterpret_cast<const float2 *>(a.act + a.d_off + 4 * blk);
+    de[mm] = *reinterpret_cast<const float4 *>(a.act + a.d_off + 8 * blk);
     ss[mm] = *reinterpret_cast<const float2 *>(a.act + a.s_off + 4 * blk);
   }
   const bool lowj = p < 2;
@@ -172,13 +179,16 @@ __global__ __launch_bounds__(512) void gemv_q4k_kernel(Q4kArgs a) {
       }
 #pragma unroll
       for (int mm = 0; mm < MM; mm++) {
-        int dotA = 0, dotB = 0;
+        int dotA = 0, dotB = 0, dotA2 = 0, dotB2 = 0;
 #pragma unroll
         for (int k = 0; k < 8; k++) {
           dotA = dot4((int)lo[k], xa[mm][k], dotA);
           dotB = dot4((int)hi[k], xb[mm][k], dotB);
+          dotA2 = dot4((int)lo[k], ya[mm][k], dotA2);
+          dotB2 = dot4((int)hi[k], yb[mm][k], dotB2);
         }
-        const float v = scA * (dd[mm].x * (float)dotA) + scB * (dd[mm].y * (float)dotB);
+        const float v = scA * (de[mm].x * (float)dotA + de[mm].y * (float)dotA2) +
+                        scB * (de[mm].z * (float)dotB + de[mm].w * (float)dotB2);
         const float mn = mnA * ss[mm].x + mnB * ss[mm].y;
         const float s = row16_sum(d * v - dmin * mn);
         if ((lane & 15) == 0) part[((r * RW + team) * MM + mm) * hpt + (u >> 4)] = s;
@@ -215,7 +225,7 @@ struct StagedArgs {
   const uint8_t *w;
   float *out;
   int M, N, K, nb;
-  int64_t row_bytes, d_off;
+  int64_t row_bytes, q2_off, d_off;
   int lds_wave;  // bytes of LDS per wave
 };
 
@@ -231,17 +241,19 @@ __device__ __forceinline__ void lds_unaligned(const uint8_t *lds, int o, uint32_
   for (int k = 0; k < NDW; k++) out[k] = __builtin_amdgcn_alignbit(w[k + 1], w[k], sh);
 }
 
+// Copy nseg 16-byte segments src -> lds; lanes take segments lane, lane + 64, ...
+// Loads are clamped to the last segment so every load is in bounds and unconditional.
 __device__ __forceinline__ void stage_rows(uint8_t *lds, const uint8_t *src, int nseg, int lane) {
   const uint4 *s4 = reinterpret_cast<const uint4 *>(src);
   uint4 *d4 = reinterpret_cast<uint4 *>(lds);
   for (int s0 = lane; s0 < nseg; s0 += 256) {
-    uint4 v[4];
-#pragma unroll
-    for (int k = 0; k < 4; k++)
-      if (s0 + 64 * k < nseg) v[k] = s4[s0 + 64 * k];
-#pragma unroll
-    for (int k = 0; k < 4; k++)
-      if (s0 + 64 * k < nseg) d4[s0 + 64 * k] = v[k];
+    const int i1 = s0 + 64 < nseg ? s0 + 64 : nseg - 1, i2 = s0 + 128 < nseg ? s0 + 128 : nseg - 1;
+    const int i3 = s0 + 192 < nseg ? s0 + 192 : nseg - 1;
+    const uint4 v0 = s4[s0], v1 = s4[i1], v2 = s4[i2], v3 = s4[i3];
+    d4[s0] = v0;
+    d4[i1] = v1;  // a clamped index rewrites the last segment with its own bytes
+    d4[i2] = v2;
+    d4[i3] = v3;
   }
 }
 
@@ -254,8 +266,8 @@ __global__ __launch_bounds__(256) void gemv_q80_kernel(StagedArgs a) {
   uint8_t *lds = smem + (threadIdx.x >> 6) * a.lds_wave;
   const int m0 = blockIdx.y * MM;
 
-  int xv[MM][CPL][8];
-  float dx[MM][CPL];
+  int xv[MM][CPL][8], yv[MM][CPL][8];
+  float2 dx[MM][CPL];
 #pragma unroll
   for (int mm = 0; mm < MM; mm++) {
     const int m = m0 + mm < a.M ? m0 + mm : a.M - 1;
@@ -265,11 +277,16 @@ __global__ __launch_bounds__(256) void gemv_q80_kernel(StagedArgs a) {
       const bool ok = bl < a.nb;
       const int64_t blk = (int64_t)m * a.nb + (ok ? bl : 0);
       const uint4 *xs = reinterpret_cast<const uint4 *>(a.act + blk * 32);
-      const uint4 v0 = xs[0], v1 = xs[1];
+      const uint4 *x2 = reinterpret_cast<const uint4 *>(a.act + a.q2_off + blk * 32);
+      const uint4 v0 = xs[0], v1 = xs[1], u0 = x2[0], u1 = x2[1];
       const int V[8] = {(int)v0.x, (int)v0.y, (int)v0.z, (int)v0.w, (int)v1.x, (int)v1.y, (int)v1.z, (int)v1.w};
+      const int U[8] = {(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w, (int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
 #pragma unroll
-      for (int k = 0; k < 8; k++) xv[mm][i][k] = ok ? V[k] : 0;
-      dx[mm][i] = ok ? reinterpret_cast<const float *>(a.act + a.d_off)[blk] : 0.f;
+      for (int k = 0; k < 8; k++) {
+        xv[mm][i][k] = ok ? V[k] : 0;
+        yv[mm][i][k] = ok ? U[k] : 0;
+      }
+      dx[mm][i] = ok ? reinterpret_cast<const float2 *>(a.act + a.d_off)[blk] : make_float2(0.f, 0.f);
     }
   }
 
@@ -294,10 +311,13 @@ __global__ __launch_bounds__(256) void gemv_q80_kernel(StagedArgs a) {
         lds_unaligned<8>(lds, o + 2, qd);
 #pragma unroll
         for (int mm = 0; mm < MM; mm++) {
-          int dot = 0;
+          int dot = 0, dot2 = 0;
 #pragma unroll
-          for (int k = 0; k < 8; k++) dot = dot4((int)qd[k], xv[mm][i][k], dot);
-          acc[mm] += d * (dx[mm][i] * (float)dot);
+          for (int k = 0; k < 8; k++) {
+            dot = dot4((int)qd[k], xv[mm][i][k], dot);
+            dot2 = dot4((int)qd[k], yv[mm][i][k], dot2);
+          }
+          acc[mm] += d * (dx[mm][i].x * (float)dot + dx[mm][i].y * (float)dot2);
         }
       }
 #pragma unroll
@@ -323,9 +343,9 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(StagedArgs a) {
   const int m0 = blockIdx.y * MM;
   const int units = a.nb * 8;
 
-  int xv[MM][CPL][8];
-  float dx[MM][CPL][4];
-  int s32[MM][CPL][4];
+  int xv[MM][CPL][8], yv[MM][CPL][8];
+  float2 dx[MM][CPL][4];
+  int s32[MM][CPL][4], t32[MM][CPL][4];
 #pragma unroll
   for (int i = 0; i < CPL; i++) {
     const int un = lane + 64 * i;
@@ -338,10 +358,14 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(StagedArgs a) {
       for (int g = 0; g < 4; g++) {
         const int64_t blk = (int64_t)m * (a.K / 32) + bl * 8 + h * 4 + g;
         const uint2 v = *reinterpret_cast<const uint2 *>(a.act + blk * 32 + l0);
+        const uint2 v2 = *reinterpret_cast<const uint2 *>(a.act + a.q2_off + blk * 32 + l0);
         xv[mm][i][2 * g] = ok ? (int)v.x : 0;
         xv[mm][i][2 * g + 1] = ok ? (int)v.y : 0;
-        dx[mm][i][g] = ok ? reinterpret_cast<const float *>(a.act + a.d_off)[blk] : 0.f;
+        yv[mm][i][2 * g] = ok ? (int)v2.x : 0;
+        yv[mm][i][2 * g + 1] = ok ? (int)v2.y : 0;
+        dx[mm][i][g] = ok ? reinterpret_cast<const float2 *>(a.act + a.d_off)[blk] : make_float2(0.f, 0.f);
         s32[mm][i][g] = 32 * byte_sum(&xv[mm][i][2 * g], 2);
+        t32[mm][i][g] = 32 * byte_sum(&yv[mm][i][2 * g], 2);
       }
     }
   }
@@ -392,7 +416,10 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(StagedArgs a) {
           for (int g = 0; g < 4; g++) {
             int dot = dot4((int)qv[g][0], xv[mm][i][2 * g], 0);
             dot = dot4((int)qv[g][1], xv[mm][i][2 * g + 1], dot);
-            v += scf[g] * (dx[mm][i][g] * (float)(dot - s32[mm][i][g]));
+            int dot2 = dot4((int)qv[g][0], yv[mm][i][2 * g], 0);
+            dot2 = dot4((int)qv[g][1], yv[mm][i][2 * g + 1], dot2);
+            v += scf[g] * (dx[mm][i][g].x * (float)(dot - s32[mm][i][g]) +
+                           dx[mm][i][g].y * (float)(dot2 - t32[mm][i][g]));
           }
           acc[mm] += d * v;
         }
@@ -498,15 +525,25 @@ static void run_staged_r(int dt, StagedArgs a, hipStream_t s) {
     run_staged<CPL, 1, MM>(dt, a, s);
 }
 
+// Q6_K holds 16 activation registers per unit and row of x: wide rows (CPL >= 6)
+// serve one row of x per pass.
+template <int CPL, int MM>
+static void run_staged_c(int dt, StagedArgs a, hipStream_t s) {
+  if constexpr (CPL >= 6 && MM > 1) {
+    if (dt == Q6_K) return run_staged_r<CPL, 1>(dt, a, s);
+  }
+  run_staged_r<CPL, MM>(dt, a, s);
+}
+
 template <int MM>
 static void run_staged_m(int dt, StagedArgs a, int cpl, hipStream_t s) {
   switch (cpl) {
-    case 1: run_staged_r<1, MM>(dt, a, s); break;
-    case 2: run_staged_r<2, MM>(dt, a, s); break;
-    case 3: run_staged_r<3, MM>(dt, a, s); break;
-    case 4: run_staged_r<4, MM>(dt, a, s); break;
-    case 6: run_staged_r<6, MM>(dt, a, s); break;
-    default: run_staged_r<8, MM>(dt, a, s); break;
+    case 1: run_staged_c<1, MM>(dt, a, s); break;
+    case 2: run_staged_c<2, MM>(dt, a, s); break;
+    case 3: run_staged_c<3, MM>(dt, a, s); break;
+    case 4: run_staged_c<4, MM>(dt, a, s); break;
+    case 6: run_staged_c<6, MM>(dt, a, s); break;
+    default: run_staged_c<8, MM>(dt, a, s); break;
   }
 }
 
@@ -528,6 +565,7 @@ int launch_gemv_act(const void *act, const void *wv, float *out, int64_t M, int6
     a.P = (int)(K / 256 * 4);
     a.TP = (a.P + 15) & ~15;
     a.row_bytes = K / 256 * 144;
+    a.q2_off = act_q2_off(M, K);
     a.d_off = act_d_off(M, K);
     a.s_off = act_s_off(M, K);
     if (MMc == 1)
@@ -548,6 +586,7 @@ int launch_gemv_act(const void *act, const void *wv, float *out, int64_t M, int6
   a.K = (int)K;
   a.nb = (int)(K / block_info(dt).elems);
   a.row_bytes = staged_row_bytes(dt, K);
+  a.q2_off = act_q2_off(M, K);
   a.d_off = act_d_off(M, K);
   a.lds_wave = 0;
   int cpl = pick_cpl(dt == Q8_0 ? a.nb : (int64_t)a.nb * 8);
@@ -598,7 +637,7 @@ static int run_gemm(const void *src, bool from_act, const void *w, float *out, i
                     void *ws, hipStream_t s) {
   auto *xb = static_cast<uint16_t *>(ws);
   float *partials = reinterpret_cast<float *>(static_cast<char *>(ws) + gemm_q4k_ws_bytes(M, K));
-  if (int rc = launch_to_bf16(src, from_act, xb, M, K, s)) return rc;
+  if (int rc = launch_to_bf16(src, from_act ? kActSrc : F32, xb, M, K, s)) return rc;
   return launch_gemm_q4k_bf16(xb, w, out, partials, M, N, K, s);
 }
 

@@ -53,13 +53,19 @@ int launch_gemm_q4k_bf16(const uint16_t *xb, const void *w, float *out, float *p
                          int64_t K, hipStream_t s);
 size_t gemm_q4k_ws_bytes(int64_t M, int64_t K);
 size_t gemm_q4k_partial_bytes(int64_t M, int64_t N, int64_t K);
-int launch_to_bf16(const void *src, bool from_act, uint16_t *dst, int64_t M, int64_t K, hipStream_t s);
+// src_kind: F32, F16, BF16 (copy) or kActSrc (prepared activations).
+constexpr int kActSrc = -1;
+int launch_to_bf16(const void *src, int src_kind, uint16_t *dst, int64_t M, int64_t K, hipStream_t s);
+size_t gemm_x_bytes(int64_t M, int64_t K);
+size_t gemm_partial_bytes(int64_t M, int64_t N, int64_t K, bool f32_out);
+int launch_gemm_int4_bf16(const uint16_t *xb, const uint32_t *codes, const float *sc, const float *zr, void *out,
+                          int out_dtype, float *partials, int64_t M, int64_t N, int64_t K, int G, hipStream_t s);
 int device_cus();
 int launch_int4_dequant(const uint32_t *codes, const float *s, const float *z, void *out, int out_dtype,
                         int64_t N, int64_t K, int G, int64_t off, hipStream_t st);
 int launch_int4_matmul(const void *x, int x_dtype, const uint32_t *codes, const float *s, const float *z, void *y,
                        int64_t M, int64_t N, int64_t K, int G, void *ws, hipStream_t st);
-size_t int4_ws_bytes(int64_t M, int64_t K, int G);
+size_t int4_ws_bytes(int64_t M, int64_t N, int64_t K, int G, int x_dtype);
 int launch_moe_q(const void *xq, const void *w, const int64_t *pairs, const int64_t *expts, int32_t *counts,
                  int32_t *offsets, const float *topk_w, float *out, int topk, int64_t size_m, int64_t M,
                  int64_t E, int64_t N, int64_t K, int row_per_pair, int dt, hipStream_t s);

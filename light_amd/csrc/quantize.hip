@@ -1,4 +1,4 @@
-// quantize.hip -- on-GPU q8_1 activation quantizer (q8_1 blocks or the planar act layout).
+// quantize.hip -- on-GPU q8_1 activation quantizer (q8_1 blocks or the two-level planar act layout).
 //
 // Block of 32 -> [f16 d][f16 s][i8 q[32]] (quant/q8_1.go:10-18).  Rounding follows
 // Light's encodeQ8_0 (quant/quantize.go:70-86): d = amax / 127 (f32), id = 1 / d
@@ -25,7 +25,8 @@ __device__ __forceinline__ void load4(const void *x, int64_t i, float v[4]) {
 
 template <int XDT, bool ACT>
 __global__ __launch_bounds__(256) void quantize_q8_1_kernel(const void *__restrict__ x, uint8_t *__restrict__ dst,
-                                                            int64_t nblocks, int64_t d_off, int64_t s_off) {
+                                                            int64_t nblocks, int64_t q2_off, int64_t d_off,
+                                                            int64_t s_off) {
   int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   int64_t blk = t >> 3;
   int sub = threadIdx.x & 7;
@@ -45,16 +46,32 @@ __global__ __launch_bounds__(256) void quantize_q8_1_kernel(const void *__restri
   }
 #pragma unroll
   for (int o = 4; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 8);
-  if (!live) return;
   uint32_t packed = (uint32_t)(q[0] & 0xff) | (uint32_t)(q[1] & 0xff) << 8 | (uint32_t)(q[2] & 0xff) << 16 |
                     (uint32_t)(q[3] & 0xff) << 24;
   if constexpr (ACT) {
+    // Residual level: r = x - d*q1, e = d / 254, q2 = RoundToEven(r / e) (|q2| <= 127).
+    const float e = __fdiv_rn(d, 254.0f);
+    const float ie = e != 0.f ? __fdiv_rn(1.0f, e) : 0.f;
+    uint32_t packed2 = 0;
+    float bsum = (v[0] + v[1]) + (v[2] + v[3]);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const float r = __fsub_rn(v[j], __fmul_rn(d, (float)q[j]));
+      int q2 = (int)rintf(__fmul_rn(r, ie));
+      q2 = q2 > 127 ? 127 : (q2 < -127 ? -127 : q2);
+      packed2 |= (uint32_t)(q2 & 0xff) << (8 * j);
+    }
+#pragma unroll
+    for (int o = 1; o < 8; o <<= 1) bsum += __shfl_xor(bsum, o, 8);
+    if (!live) return;
     reinterpret_cast<uint32_t *>(dst + blk * 32)[sub] = packed;
+    reinterpret_cast<uint32_t *>(dst + q2_off + blk * 32)[sub] = packed2;
     if (sub == 0) {
-      reinterpret_cast<float *>(dst + d_off)[blk] = d;
-      reinterpret_cast<float *>(dst + s_off)[blk] = __fmul_rn(d, (float)sum);
+      reinterpret_cast<float2 *>(dst + d_off)[blk] = make_float2(d, e);
+      reinterpret_cast<float *>(dst + s_off)[blk] = bsum;
     }
   } else {
+    if (!live) return;
     uint8_t *o = dst + blk * 36;
     reinterpret_cast<uint32_t *>(o + 4)[sub] = packed;
     if (sub == 0) {
@@ -69,11 +86,11 @@ static int launch_q(const void *x, int x_dtype, void *dst, int64_t M, int64_t K,
   int64_t nblocks = M * (K / 32);
   dim3 grid((unsigned)cdiv(nblocks * 8, 256));
   auto *d = static_cast<uint8_t *>(dst);
-  int64_t doff = act_d_off(M, K), soff = act_s_off(M, K);
+  int64_t q2off = act_q2_off(M, K), doff = act_d_off(M, K), soff = act_s_off(M, K);
   switch (x_dtype) {
-    case F32: quantize_q8_1_kernel<F32, ACT><<<grid, 256, 0, s>>>(x, d, nblocks, doff, soff); break;
-    case BF16: quantize_q8_1_kernel<BF16, ACT><<<grid, 256, 0, s>>>(x, d, nblocks, doff, soff); break;
-    case F16: quantize_q8_1_kernel<F16, ACT><<<grid, 256, 0, s>>>(x, d, nblocks, doff, soff); break;
+    case F32: quantize_q8_1_kernel<F32, ACT><<<grid, 256, 0, s>>>(x, d, nblocks, q2off, doff, soff); break;
+    case BF16: quantize_q8_1_kernel<BF16, ACT><<<grid, 256, 0, s>>>(x, d, nblocks, q2off, doff, soff); break;
+    case F16: quantize_q8_1_kernel<F16, ACT><<<grid, 256, 0, s>>>(x, d, nblocks, q2off, doff, soff); break;
     default: return fail(HQ_EUNSUPPORTED, "quantize", "x dtype %d", x_dtype);
   }
   return check_launch("quantize");

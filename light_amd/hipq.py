@@ -59,7 +59,7 @@ SIGNATURES = {
     "hq_matmul_q_act": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _P, _SZ, _P]),
     "hq_dequant": (_I, [_P, _P, _I64, _I, _I, _P]),
     "hq_quantize_q8_1": (_I, [_P, _I, _P, _I64, _I64, _P]),
-    "hq_int4_matmul_ws_bytes": (_SZ, [_I64, _I64, _I]),
+    "hq_int4_matmul_ws_bytes": (_SZ, [_I64, _I64, _I64, _I, _I]),
     "hq_int4_matmul": (_I, [_P, _I, _P, _P, _P, _P, _I64, _I64, _I64, _I, _P, _SZ, _P]),
     "hq_int4_dequant": (_I, [_P, _P, _P, _P, _I, _I64, _I64, _I, _I64, _P]),
     "hq_moe_gemm_q_ws_bytes": (_SZ, [_I64, _I64, _I]),
@@ -186,8 +186,8 @@ def int4_matmul(x, codes, scales, zeros, G, out=None, ws=None, stream=None):
     return out
 
 
-def int4_matmul_ws_bytes(M, K, G):
-    return lib().hq_int4_matmul_ws_bytes(M, K, G)
+def int4_matmul_ws_bytes(M, N, K, G, x_dtype):
+    return lib().hq_int4_matmul_ws_bytes(M, N, K, G, x_dtype)
 
 
 def int4_dequant(codes, scales, zeros, G, out_dtype=F32, out=None, out_offset=0, stream=None):

@@ -1,0 +1,114 @@
+"""GPU parity of the GPTQ / AWQ int4 path (Light's quant.Int4) through the C ABI.
+
+Mirrors TestDequantizeInt4 (ops/int4_test.go:47-81: bit-exact F32 and BF16) and
+TestMatMulInt4 (ops/int4_test.go:83-145: M in {1, 3, 8, 9}) plus the
+Qwen2.5-7B MLP shapes of the benchmark.  Float bar: max |err| / (||w_n|| ||x_m||)
+<= 1e-3 against Light's CPU int4MatMulCPU (oracle.int4_matmul) and the f64
+oracle, plus the output dtype's rounding (half an ulp of |y|) for BF16 / F16 y.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from _util import norm_err
+from light_amd import hipq, synth
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+TDT = {hipq.F32: torch.float32, hipq.BF16: torch.bfloat16, hipq.F16: torch.float16}
+ULP = {hipq.F32: 0.0, hipq.BF16: 2.0 ** -8, hipq.F16: 2.0 ** -11}
+
+
+def _t(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def light_int4(rng, N, K, G):
+    """randomInt4 (ops/int4_test.go:15-31): codes uniform, s in [1e-3, 0.021), z in [0, 15]."""
+    codes = rng.integers(0, 2 ** 32, size=(N, K // 8), dtype=np.uint64).astype(np.uint32)
+    s = (rng.random((N, K // G)) * 0.02 + 1e-3).astype(np.float32)
+    z = rng.integers(0, 16, size=(N, K // G)).astype(np.float32)
+    return codes, s, z
+
+
+def _check(dev, x, codes, s, z, G, xdt, rows=None):
+    M, K = x.shape
+    N = codes.shape[0]
+    print(f"[case] int4 M={M} N={N} K={K} G={G} x={hipq.NAMES[xdt]}", flush=True)
+    xt = torch.from_numpy(x).to(TDT[xdt])
+    xw = xt.float().numpy()  # exact widened activations
+    y = hipq.int4_matmul(xt.to(dev), _t(codes, dev), _t(s, dev), _t(z, dev), G)
+    torch.cuda.synchronize()
+    assert y.dtype == TDT[xdt] and tuple(y.shape) == (M, N)
+    got = y.float().cpu().numpy()
+    if rows is not None:
+        got, xw = got[rows], xw[rows]
+    cpu = oracle.int4_matmul(xw, codes, s, z, N, K, G)
+    wd = oracle.int4_dequant(codes, s, z, N, K, G)
+    ref, _, wn, xn = oracle.matmul_f64(xw, wd)
+    slack = ULP[xdt] * np.abs(ref) / np.maximum(np.outer(xn, wn), 1e-30)
+    e = np.abs(got - ref) / np.maximum(np.outer(xn, wn), 1e-30) - slack
+    assert np.all(np.isfinite(got))
+    assert float(e.max()) <= TOL, f"vs f64 {e.max():.3g}"
+    e2 = np.abs(got - cpu) / np.maximum(np.outer(xn, wn), 1e-30) - slack
+    assert float(e2.max()) <= TOL, f"vs Light CPU {e2.max():.3g}"
+
+
+@pytest.mark.parametrize("odt", [hipq.F32, hipq.BF16])
+def test_dequantize_int4_bit_exact(dev, odt):
+    rng = np.random.default_rng(3)
+    N, K, G = 24, 256, 64
+    codes, s, z = light_int4(rng, N, K, G)
+    got = hipq.int4_dequant(_t(codes, dev), _t(s, dev), _t(z, dev), G, odt).cpu()
+    want = oracle.int4_dequant(codes, s, z, N, K, G, odt)
+    if odt == hipq.F32:
+        assert np.array_equal(got.numpy().view(np.uint32), want.view(np.uint32))
+    else:
+        assert np.array_equal(got.view(torch.int16).numpy().view(np.uint16), want)
+
+
+def test_dequantize_int4_offset_slot(dev):
+    """The offset argument writes one slot of a stacked buffer (ops/int4.go:31-56)."""
+    rng = np.random.default_rng(5)
+    N, K, G = 8, 128, 32
+    codes, s, z = light_int4(rng, N, K, G)
+    out = torch.full((3 * N * K,), -1.0, device=dev)
+    hipq.int4_dequant(_t(codes, dev), _t(s, dev), _t(z, dev), G, hipq.F32, out=out, out_offset=N * K)
+    o = out.cpu().numpy()
+    assert np.all(o[:N * K] == -1) and np.all(o[2 * N * K:] == -1)
+    assert np.array_equal(o[N * K:2 * N * K], oracle.int4_dequant(codes, s, z, N, K, G).ravel())
+
+
+@pytest.mark.parametrize("M", [1, 3, 8, 9])
+@pytest.mark.parametrize("xdt", [hipq.F32, hipq.BF16, hipq.F16])
+def test_matmul_int4_light_shapes(dev, M, xdt):
+    """TestMatMulInt4 shapes: N=96, K=256, G=64."""
+    rng = np.random.default_rng(4 + M)
+    N, K, G = 96, 256, 64
+    codes, s, z = light_int4(rng, N, K, G)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    _check(dev, x, codes, s, z, G, xdt)
+
+
+@pytest.mark.parametrize("M,N,K,G", [(1, 1, 32, 32), (2, 300, 512, 32), (5, 77, 1024, 128), (16, 256, 4096, 128),
+                                     (33, 130, 2048, 64), (64, 512, 3584, 128), (70, 200, 1536, 96),
+                                     (4, 64, 32768, 128)])
+def test_matmul_int4_shapes(dev, M, N, K, G):
+    rng = np.random.default_rng(M * 7 + N + K)
+    codes, s, z = light_int4(rng, N, K, G)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    _check(dev, x, codes, s, z, G, hipq.F32)
+
+
+@pytest.mark.parametrize("name", ["int4_m1_18944x3584", "int4_m1_3584x18944", "int4_m64_18944x3584",
+                                  "int4_m64_3584x18944"])
+def test_matmul_int4_benchmark_configs(dev, name):
+    c = synth.CONFIGS[name]
+    g = synth.rng(c["cfg"])
+    M, N, K, G = c["M"], c["N"], c["K"], c["G"]
+    codes, s, z = synth.int4_weight(N, K, G, g)
+    x = synth.activations(M, K, g)
+    rows = None if M == 1 else np.arange(0, M, 4)
+    _check(dev, x, codes, s, z, G, hipq.F16, rows=rows)

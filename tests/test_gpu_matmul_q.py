@@ -164,23 +164,34 @@ def test_matmul_q_explicit_workspace_and_stream(dev):
 
 
 def test_prepared_activations_match_q8_1(dev):
-    """The planar act layout holds exactly q8_1's quants; d is q8_1's d before f16 rounding."""
+    """The act layout: level 1 is exactly q8_1 (quants and f32 d), level 2 quantizes the
+    residual at e = d / 254, and sx is the block sum of x."""
     g = np.random.default_rng(12)
     M, K = 3, 2048
     x = (g.standard_normal((M, K)) * 3).astype(np.float32)
+    x[1, :32] = 0.0
     xt = _t(x, dev)
     act = hipq.quantize_act(xt).cpu().numpy()
     q81 = oracle.quantize_q8_1(x).reshape(-1, 36)
     nb = M * K // 32
-    assert np.array_equal(act[:M * K].reshape(-1, 32), q81[:, 4:])
-    d_off = (M * K + 15) & ~15
-    d = act[d_off:d_off + 4 * nb].view(np.float32)
-    sx = act[d_off + 4 * nb:d_off + 8 * nb].view(np.float32)
+    q2_off = (M * K + 255) & ~255
+    d_off = 2 * q2_off
+    s_off = d_off + 8 * nb
+    q1 = act[:M * K].reshape(-1, 32)
+    q2 = act[q2_off:q2_off + M * K].view(np.int8).reshape(-1, 32).astype(np.float64)
+    de = act[d_off:d_off + 8 * nb].view(np.float32).reshape(-1, 2)
+    sx = act[s_off:s_off + 4 * nb].view(np.float32)
+    assert np.array_equal(q1, q81[:, 4:])
     amax = np.abs(x.reshape(-1, 32)).max(1)
-    assert np.array_equal(d, amax / np.float32(127))
-    assert np.array_equal(d.astype(np.float16).view(np.uint16), q81[:, 0:2].copy().view("<u2")[:, 0])
-    qsum = q81[:, 4:].view(np.int8).astype(np.int64).sum(1)
-    assert np.array_equal(sx, d * qsum.astype(np.float32))
+    assert np.array_equal(de[:, 0], amax / np.float32(127))
+    assert np.array_equal(de[:, 0].astype(np.float16).view(np.uint16), q81[:, 0:2].copy().view("<u2")[:, 0])
+    assert np.array_equal(de[:, 1], de[:, 0] / np.float32(254))
+    assert np.all(np.abs(q2) <= 127)
+    recon = q1.view(np.int8).astype(np.float64) * de[:, :1] + q2 * de[:, 1:]
+    err = np.abs(recon - x.reshape(-1, 32))
+    assert np.all(err <= de[:, 1:] * 0.5 * (1 + 1e-3) + 1e-30)
+    assert np.allclose(sx, x.reshape(-1, 32).sum(1), rtol=1e-5, atol=1e-5)
+    assert np.all(de[32 // 32 * (K // 32)] == 0)  # the all-zero block
 
 
 @pytest.mark.parametrize("dt", FMTS)
