@@ -35,6 +35,9 @@ namespace hq {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+// Native 4 x u32 vector: unlike HIP's uint4 (a struct over a union, copied with
+// memcpy) arrays of it stay in registers.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int GBN = 128, GBK = 64, GLD = GBK + 8;  // LDS row stride in bf16
 
@@ -69,12 +72,12 @@ struct GemmArgs {
 // ---- weight policies: registers for one K step and the LDS write ----------
 
 struct Q4kPolicy {
-  uint4 q, h;
+  u32x4 q, h;
   __device__ __forceinline__ void load(const GemmArgs &a, int row, int half, int k0) {
     const uint8_t *bp = a.w + (int64_t)row * (a.K / 256) * 144 + (int64_t)(k0 >> 8) * 144;
     const int p = (k0 >> 6) & 3;
-    q = *reinterpret_cast<const uint4 *>(bp + 16 + 32 * p + 16 * half);
-    h = *reinterpret_cast<const uint4 *>(bp);
+    q = *reinterpret_cast<const u32x4 *>(bp + 16 + 32 * p + 16 * half);
+    h = *reinterpret_cast<const u32x4 *>(bp);
   }
   // Low nibbles: sub-block 2p, k = 16*half + i; high nibbles: sub-block 2p+1, k = 32 + 16*half + i.
   __device__ __forceinline__ void store(uint8_t *brow, int half, int k0) const {
@@ -94,21 +97,21 @@ struct Q4kPolicy {
       hi[2 * k] = pack_bf16(dB * (float)(hh & 0xff) - mB, dB * (float)((hh >> 8) & 0xff) - mB);
       hi[2 * k + 1] = pack_bf16(dB * (float)((hh >> 16) & 0xff) - mB, dB * (float)(hh >> 24) - mB);
     }
-    uint4 *bd = reinterpret_cast<uint4 *>(brow + 32 * half);
-    bd[0] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-    bd[1] = make_uint4(lo[4], lo[5], lo[6], lo[7]);
-    uint4 *bh = reinterpret_cast<uint4 *>(brow + 64 + 32 * half);
-    bh[0] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-    bh[1] = make_uint4(hi[4], hi[5], hi[6], hi[7]);
+    u32x4 *bd = reinterpret_cast<u32x4 *>(brow + 32 * half);
+    bd[0] = u32x4{lo[0], lo[1], lo[2], lo[3]};
+    bd[1] = u32x4{lo[4], lo[5], lo[6], lo[7]};
+    u32x4 *bh = reinterpret_cast<u32x4 *>(brow + 64 + 32 * half);
+    bh[0] = u32x4{hi[0], hi[1], hi[2], hi[3]};
+    bh[1] = u32x4{hi[4], hi[5], hi[6], hi[7]};
   }
 };
 
 struct Int4Policy {
-  uint4 q;
+  u32x4 q;
   float s, z;
   // Codes of k in [k0 + 32*half, +32): words k0/8 + 4*half .. +4.
   __device__ __forceinline__ void load(const GemmArgs &a, int row, int half, int k0) {
-    q = *reinterpret_cast<const uint4 *>(a.w + (int64_t)row * (a.K / 2) + (k0 >> 1) + 16 * half);
+    q = *reinterpret_cast<const u32x4 *>(a.w + (int64_t)row * (a.K / 2) + (k0 >> 1) + 16 * half);
     const int64_t gi = (int64_t)row * (a.K / a.G) + k0 / a.G;
     s = a.s[gi];
     z = a.z[gi];
@@ -122,9 +125,9 @@ struct Int4Policy {
       for (int j = 0; j < 8; j += 2)
         o[4 * k + j / 2] = pack_bf16(s * ((float)((qw[k] >> (4 * j)) & 15) - z),
                                      s * ((float)((qw[k] >> (4 * j + 4)) & 15) - z));
-    uint4 *bd = reinterpret_cast<uint4 *>(brow + 64 * half);
+    u32x4 *bd = reinterpret_cast<u32x4 *>(brow + 64 * half);
 #pragma unroll
-    for (int k = 0; k < 4; k++) bd[k] = make_uint4(o[4 * k], o[4 * k + 1], o[4 * k + 2], o[4 * k + 3]);
+    for (int k = 0; k < 4; k++) bd[k] = u32x4{o[4 * k], o[4 * k + 1], o[4 * k + 2], o[4 * k + 3]};
   }
 };
 
@@ -165,16 +168,16 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
 
-  uint4 ra[T::ALOADS];
+  u32x4 ra[T::ALOADS];
   WP wp;
   if (nsteps > 0) {
     const int k0 = st0 * GBK;
 #pragma unroll
-    for (int i = 0; i < T::ALOADS; i++) ra[i] = *reinterpret_cast<const uint4 *>(xrow[i] + k0);
+    for (int i = 0; i < T::ALOADS; i++) ra[i] = *reinterpret_cast<const u32x4 *>(xrow[i] + k0);
     wp.load(a, wrow, wh, k0);
     uint8_t *ad = smem + ((t >> 3) * GLD + acol * 8) * 2;
 #pragma unroll
-    for (int i = 0; i < T::ALOADS; i++) *reinterpret_cast<uint4 *>(ad + i * 32 * GLD * 2) = ra[i];
+    for (int i = 0; i < T::ALOADS; i++) *reinterpret_cast<u32x4 *>(ad + i * 32 * GLD * 2) = ra[i];
     wp.store(smem + T::A_BYTES + wr * GLD * 2, wh, k0);
   }
   __syncthreads();
@@ -184,7 +187,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
     const int kn = (st0 + s + 1) * GBK;
     if (s + 1 < nsteps) {
 #pragma unroll
-      for (int i = 0; i < T::ALOADS; i++) ra[i] = *reinterpret_cast<const uint4 *>(xrow[i] + kn);
+      for (int i = 0; i < T::ALOADS; i++) ra[i] = *reinterpret_cast<const u32x4 *>(xrow[i] + kn);
       wp.load(a, wrow, wh, kn);
     }
     const uint8_t *sa = smem + buf * T::STAGE;
@@ -208,7 +211,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
       uint8_t *na = smem + (buf ^ 1) * T::STAGE;
       uint8_t *ad = na + ((t >> 3) * GLD + acol * 8) * 2;
 #pragma unroll
-      for (int i = 0; i < T::ALOADS; i++) *reinterpret_cast<uint4 *>(ad + i * 32 * GLD * 2) = ra[i];
+      for (int i = 0; i < T::ALOADS; i++) *reinterpret_cast<u32x4 *>(ad + i * 32 * GLD * 2) = ra[i];
       wp.store(na + T::A_BYTES + wr * GLD * 2, wh, kn);
     }
     __syncthreads();
