@@ -336,10 +336,7 @@ int hq_int4_dequant(const uint32_t *codes, const float *scales, const float *zer
   return launch_int4_dequant(codes, scales, zeros, out, out_dtype, N, K, G, out_offset, s);
 }
 
-size_t hq_moe_gemm_q_ws_bytes(int64_t rows, int64_t K, int w_dtype) {
-  if (rows <= 0 || K <= 0 || K % 32) return 0;
-  return ((size_t)rows * (size_t)(K / 32) * 36 + 255) & ~(size_t)255;
-}
+size_t hq_moe_gemm_q_ws_bytes(int64_t rows, int64_t K, int w_dtype) { return moe_ws_bytes(rows, K, w_dtype); }
 
 int hq_moe_gemm_q(const float *x, const void *w, const int64_t *sorted_pairs, const int64_t *sorted_expts,
                   int32_t *counts, int32_t *offsets, const float *topk_w, float *out, int topk, int64_t size_m,
@@ -358,16 +355,16 @@ int hq_moe_gemm_q(const float *x, const void *w, const int64_t *sorted_pairs, co
   if (!x || !w || !sorted_pairs || !sorted_expts || !counts || !offsets || !out)
     return fail(HQ_EINVAL, call, "NULL pointer");
   hipStream_t s = resolve(stream);
-  size_t need = hq_moe_gemm_q_ws_bytes(rows, K, w_dtype);
-  if (!ws) {
+  if (((uintptr_t)x & 15)) return fail(HQ_EINVAL, call, "x must be 16-byte aligned");
+  size_t need = moe_ws_bytes(rows, K, w_dtype);
+  if (need && !ws) {
     if (int rc = workspace(need, s, &ws, call)) return rc;
-  } else if (ws_bytes < need) {
+  } else if (need && ws_bytes < need) {
     return fail(HQ_ENOMEM, call, "workspace %zu bytes < %zu needed", ws_bytes, need);
   }
   TraceSpan span("moe_gemm_q", s);
-  if (int rc = launch_quantize_q8_1(x, HQ_F32, ws, rows, K, s)) return rc;
-  return launch_moe_q(ws, w, sorted_pairs, sorted_expts, counts, offsets, topk_w, out, topk, size_m, M, E, N, K,
-                      row_per_pair, w_dtype, s);
+  return launch_moe_q(x, w, sorted_pairs, sorted_expts, counts, offsets, topk_w, out, topk, size_m, M, rows, E, N, K,
+                      row_per_pair, w_dtype, ws, s);
 }
 
 }  // extern "C"

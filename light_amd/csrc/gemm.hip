@@ -233,6 +233,124 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
     }
 }
 
+// ---- MoE grouped GEMM ---------------------------------------------------------
+// out[p, n] = w(p) * x[row(p)] . dequant(W[e])[n] for the expert-sorted pairs of
+// expert e = blockIdx.y; blockIdx.x is the 128-wide weight-row tile.  The expert's
+// pairs are processed in chunks of 32 gathered activation rows (BM = 32, 4 waves of
+// 32 x 32), each chunk running the full K loop of gemm_kernel.
+struct MoeGemmArgs {
+  GemmArgs g;  // x = bf16 rows of x, w = expert stack, N, K
+  const int64_t *pairs;
+  const int32_t *offsets;
+  const float *topk_w;
+  float *out;
+  int64_t size_m, expert_bytes;
+  int topk, rpp;
+};
+
+template <class WP>
+__global__ __launch_bounds__(256) void moe_gemm_kernel(MoeGemmArgs ma) {
+  using T = GTile<32>;
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int e = blockIdx.y;
+  const int seg0 = ma.offsets[e], seg1 = ma.offsets[e + 1];
+  if (seg0 >= seg1) return;
+  GemmArgs a = ma.g;
+  a.w += (int64_t)e * ma.expert_bytes;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int wn = wave;  // 4 waves along N, 32 columns each
+  const int n0 = blockIdx.x * GBN;
+  const int ksteps = a.K / GBK;
+  const int acol = t & 7, arow = t >> 3;  // A: 32 rows x 128 B per step, one 16-byte load per thread
+  const int wr = t >> 1, wh = t & 1;
+  const int wrow = n0 + wr < a.N ? n0 + wr : a.N - 1;
+  const int fr = lane & 31, fk = (lane >> 5) * 8;
+
+  for (int c0 = seg0; c0 < seg1; c0 += 32) {
+    // Gathered activation row of this thread's A slot.
+    int64_t pp = c0 + arow < seg1 ? ma.pairs[c0 + arow] : -1;
+    const int64_t xr = (pp < 0 || pp >= ma.size_m) ? 0 : (ma.rpp ? pp : pp / ma.topk);
+    const uint16_t *xrow = a.x + xr * a.K + acol * 8;
+
+    f32x16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[r] = 0.f;
+    u32x4 ra;
+    WP wp;
+    ra = *reinterpret_cast<const u32x4 *>(xrow);
+    wp.load(a, wrow, wh, 0);
+    *reinterpret_cast<u32x4 *>(smem + (arow * GLD + acol * 8) * 2) = ra;
+    wp.store(smem + T::A_BYTES + wr * GLD * 2, wh, 0);
+    __syncthreads();
+    for (int s = 0; s < ksteps; s++) {
+      const int buf = s & 1;
+      const int kn = (s + 1) * GBK;
+      if (s + 1 < ksteps) {
+        ra = *reinterpret_cast<const u32x4 *>(xrow + kn);
+        wp.load(a, wrow, wh, kn);
+      }
+      const uint8_t *sa = smem + buf * T::STAGE;
+      const uint8_t *sb = sa + T::A_BYTES;
+#pragma unroll
+      for (int kk = 0; kk < GBK / 16; kk++) {
+        const bf16x8 af = *reinterpret_cast<const bf16x8 *>(sa + (fr * GLD + kk * 16 + fk) * 2);
+        const bf16x8 bfr = *reinterpret_cast<const bf16x8 *>(sb + ((wn * 32 + fr) * GLD + kk * 16 + fk) * 2);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bfr, acc, 0, 0, 0);
+      }
+      if (s + 1 < ksteps) {
+        uint8_t *na = smem + (buf ^ 1) * T::STAGE;
+        *reinterpret_cast<u32x4 *>(na + (arow * GLD + acol * 8) * 2) = ra;
+        wp.store(na + T::A_BYTES + wr * GLD * 2, wh, kn);
+      }
+      __syncthreads();
+    }
+    const int col = n0 + wn * 32 + (lane & 31);
+    if (col < a.N) {
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int lr = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int i = c0 + lr;
+        if (i >= seg1) continue;
+        const int64_t p = ma.pairs[i];
+        if (p < 0 || p >= ma.size_m) continue;
+        ma.out[p * a.N + col] = acc[r] * (ma.topk_w ? ma.topk_w[p] : 1.f);
+      }
+    }
+  }
+}
+
+int launch_moe_gemm_q4k(const uint16_t *xb, const void *w, const int64_t *pairs, const int32_t *offsets,
+                        const float *topk_w, float *out, int topk, int64_t size_m, int64_t E, int64_t N, int64_t K,
+                        int rpp, hipStream_t s) {
+  using T = GTile<32>;
+  static bool attr_set[64] = {false};
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  if (dev >= 0 && dev < 64 && !attr_set[dev]) {
+    if (int rc = check(hipFuncSetAttribute((const void *)moe_gemm_kernel<Q4kPolicy>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, T::LDS),
+                       "hipFuncSetAttribute"))
+      return rc;
+    attr_set[dev] = true;
+  }
+  MoeGemmArgs ma = {};
+  ma.g.x = xb;
+  ma.g.w = static_cast<const uint8_t *>(w);
+  ma.g.N = (int)N;
+  ma.g.K = (int)K;
+  ma.pairs = pairs;
+  ma.offsets = offsets;
+  ma.topk_w = topk_w;
+  ma.out = out;
+  ma.size_m = size_m;
+  ma.expert_bytes = N * (K / 256) * 144;
+  ma.topk = topk;
+  ma.rpp = rpp;
+  dim3 grid((unsigned)cdiv(N, GBN), (unsigned)E);
+  moe_gemm_kernel<Q4kPolicy><<<grid, 256, T::LDS, s>>>(ma);
+  return check_launch("moe_gemm_q4k");
+}
+
 // out[i] = sum_z part[z][i] in split order, converted to the output dtype.
 template <int ODT>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restrict__ part, void *__restrict__ out,

@@ -218,6 +218,193 @@ __global__ __launch_bounds__(512) void gemv_q4k_kernel(Q4kArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// MoE grouped Q4_K GEMV: the Q4_K kernel above with an expert dimension
+// (grid.y) and the expert's routed pairs as the rows of x (ops/moe.go:101-111):
+// out[p, n] = w(p) * x[row(p)] . dequant(W[e])[n], row(p) = rpp ? p : p / topk.
+// ---------------------------------------------------------------------------
+struct MoeQ4kArgs {
+  Q4kArgs base;  // act / w / out / N / K / P / TP / offsets; base.M = rows of x
+  const int64_t *pairs;
+  const int32_t *offsets;
+  const float *topk_w;
+  int64_t size_m, expert_bytes;
+  int topk, rpp;
+};
+
+template <int R, int MM>
+__global__ __launch_bounds__(512) void moe_gemv_q4k_kernel(MoeQ4kArgs ma) {
+  __shared__ float part[512];
+  const Q4kArgs &a = ma.base;
+  const int e = blockIdx.y;
+  const int seg0 = ma.offsets[e], seg1 = ma.offsets[e + 1];
+  if (seg0 >= seg1) return;
+  const uint8_t *wexp = a.w + (int64_t)e * ma.expert_bytes;
+  const int t = threadIdx.x;
+  const int RW = blockDim.x / a.TP;
+  const int team = t / a.TP, u = t - team * a.TP;
+  const bool active = u < a.P;
+  const int uu = active ? u : 0;
+  const int b = uu >> 2, p = uu & 3;
+  const int qoff = b * 144 + 16 + p * 32, hoff = b * 144 + 4 * p;
+  const int rows_per_group = RW * R;
+  const int ngroups = (a.N + rows_per_group - 1) / rows_per_group;
+  const int ja = b * 8 + 2 * p;
+  const bool lowj = p < 2;
+  const int ka = (2 * p) & 3;
+  const int lane = t & 63;
+  const int hpt = a.TP >> 4;
+
+  for (int c0 = seg0; c0 < seg1; c0 += MM) {
+    int64_t pid[MM];
+    int xa[MM][8], xb[MM][8], ya[MM][8], yb[MM][8];
+    float4 de[MM];
+    float2 ss[MM];
+#pragma unroll
+    for (int mm = 0; mm < MM; mm++) {
+      const int i = c0 + mm;
+      int64_t pp = i < seg1 ? ma.pairs[i] : -1;
+      if (pp < 0 || pp >= ma.size_m) pp = -1;
+      pid[mm] = pp;
+      const int64_t row = pp < 0 ? 0 : (ma.rpp ? pp : pp / ma.topk);
+      const int64_t blk = row * (a.K / 32) + ja;
+      const uint4 *xs = reinterpret_cast<const uint4 *>(a.act + blk * 32);
+      const uint4 *x2 = reinterpret_cast<const uint4 *>(a.act + a.q2_off + blk * 32);
+      const uint4 v0 = xs[0], v1 = xs[1], v2 = xs[2], v3 = xs[3];
+      const uint4 w0 = x2[0], w1 = x2[1], w2 = x2[2], w3 = x2[3];
+      const int A[8] = {(int)v0.x, (int)v0.y, (int)v0.z, (int)v0.w, (int)v1.x, (int)v1.y, (int)v1.z, (int)v1.w};
+      const int B[8] = {(int)v2.x, (int)v2.y, (int)v2.z, (int)v2.w, (int)v3.x, (int)v3.y, (int)v3.z, (int)v3.w};
+      const int C[8] = {(int)w0.x, (int)w0.y, (int)w0.z, (int)w0.w, (int)w1.x, (int)w1.y, (int)w1.z, (int)w1.w};
+      const int D[8] = {(int)w2.x, (int)w2.y, (int)w2.z, (int)w2.w, (int)w3.x, (int)w3.y, (int)w3.z, (int)w3.w};
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        xa[mm][k] = A[k];
+        xb[mm][k] = B[k];
+        ya[mm][k] = C[k];
+        yb[mm][k] = D[k];
+      }
+      de[mm] = *reinterpret_cast<const float4 *>(a.act + a.d_off + 8 * blk);
+      ss[mm] = *reinterpret_cast<const float2 *>(a.act + a.s_off + 4 * blk);
+    }
+    for (int g = blockIdx.x; g < ngroups; g += gridDim.x) {
+      uint4 q0[R], q1[R];
+      uint32_t hd[R];
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        int row = g * rows_per_group + r * RW + team;
+        row = row < a.N ? row : a.N - 1;
+        const uint8_t *rp = wexp + (int64_t)row * a.row_bytes;
+        if (active) {
+          q0[r] = ld16g(rp + qoff);
+          q1[r] = ld16g(rp + qoff + 16);
+          hd[r] = ld32(rp + hoff);
+        } else {
+          q0[r] = q1[r] = make_uint4(0, 0, 0, 0);
+          hd[r] = 0;
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        const uint32_t h0 = quad_bcast<0>(hd[r]), h1 = quad_bcast<1>(hd[r]);
+        const uint32_t h2 = quad_bcast<2>(hd[r]), h3 = quad_bcast<3>(hd[r]);
+        const float d = h2f(h0 & 0xffffu), dmin = h2f(h0 >> 16);
+        const uint32_t t1 = (h1 >> (8 * ka)) & 0xffffu, t2 = (h2 >> (8 * ka)) & 0xffffu;
+        const uint32_t t3 = (h3 >> (8 * ka)) & 0xffffu;
+        const uint32_t scp = lowj ? (t1 & 0x3F3Fu) : ((t3 & 0x0F0Fu) | ((t1 >> 2) & 0x3030u));
+        const uint32_t mnp = lowj ? (t2 & 0x3F3Fu) : (((t3 >> 4) & 0x0F0Fu) | ((t2 >> 2) & 0x3030u));
+        const float scA = (float)(scp & 0xffu), scB = (float)(scp >> 8);
+        const float mnA = (float)(mnp & 0xffu), mnB = (float)(mnp >> 8);
+        const uint32_t qw[8] = {q0[r].x, q0[r].y, q0[r].z, q0[r].w, q1[r].x, q1[r].y, q1[r].z, q1[r].w};
+        uint32_t lo[8], hi[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+          lo[k] = qw[k] & 0x0F0F0F0Fu;
+          hi[k] = (qw[k] >> 4) & 0x0F0F0F0Fu;
+        }
+#pragma unroll
+        for (int mm = 0; mm < MM; mm++) {
+          int dA1 = 0, dB1 = 0, dA2 = 0, dB2 = 0;
+#pragma unroll
+          for (int k = 0; k < 8; k++) {
+            dA1 = dot4((int)lo[k], xa[mm][k], dA1);
+            dB1 = dot4((int)hi[k], xb[mm][k], dB1);
+            dA2 = dot4((int)lo[k], ya[mm][k], dA2);
+            dB2 = dot4((int)hi[k], yb[mm][k], dB2);
+          }
+          const float v = scA * (de[mm].x * (float)dA1 + de[mm].y * (float)dA2) +
+                          scB * (de[mm].z * (float)dB1 + de[mm].w * (float)dB2);
+          const float mn = mnA * ss[mm].x + mnB * ss[mm].y;
+          const float s = row16_sum(d * v - dmin * mn);
+          if ((lane & 15) == 0) part[((r * RW + team) * MM + mm) * hpt + (u >> 4)] = s;
+        }
+      }
+      __syncthreads();
+      if (t < rows_per_group * MM) {
+        const int slot = t / MM, mm = t - slot * MM;
+        const int r = slot / RW, tm = slot - r * RW;
+        float acc = 0.f;
+        for (int k = 0; k < hpt; k++) acc += part[t * hpt + k];
+        const int row = g * rows_per_group + r * RW + tm;
+        const int64_t pp = pid[mm];
+        if (row < a.N && pp >= 0) a.out[pp * a.N + row] = acc * (ma.topk_w ? ma.topk_w[pp] : 1.f);
+      }
+      __syncthreads();
+    }
+  }
+}
+
+template <int MM>
+static void run_moe_q4k(MoeQ4kArgs ma, int64_t active, hipStream_t s) {
+  Q4kArgs &a = ma.base;
+  const int rw = a.TP >= 256 ? 1 : 256 / a.TP;
+  const int R = a.TP <= 128 ? 1 : 2;
+  const int ngroups = (a.N + rw * R - 1) / (rw * R);
+  // At most `active` experts have pairs: give each enough workgroups to fill the chip
+  // (the workgroups of experts without pairs exit at once).
+  const int64_t cap = cdiv((int64_t)device_cus() * 4, active);
+  dim3 grid((unsigned)(ngroups < cap ? ngroups : cap), (unsigned)a.M /* experts */);
+  if (R == 1)
+    moe_gemv_q4k_kernel<1, MM><<<grid, a.TP * rw, 0, s>>>(ma);
+  else
+    moe_gemv_q4k_kernel<2, MM><<<grid, a.TP * rw, 0, s>>>(ma);
+}
+
+int launch_moe_gemv_q4k(const void *act, const void *w, const int64_t *pairs, const int32_t *offsets,
+                        const float *topk_w, float *out, int topk, int64_t size_m, int64_t M, int64_t rows,
+                        int64_t E, int64_t N, int64_t K, int rpp, hipStream_t s) {
+  MoeQ4kArgs ma;
+  Q4kArgs &a = ma.base;
+  a.act = static_cast<const uint8_t *>(act);
+  a.w = static_cast<const uint8_t *>(w);
+  a.out = out;
+  a.M = (int)E;  // grid.y: experts
+  a.N = (int)N;
+  a.K = (int)K;
+  a.P = (int)(K / 256 * 4);
+  a.TP = (a.P + 15) & ~15;
+  a.row_bytes = K / 256 * 144;
+  a.q2_off = act_q2_off(rows, K);
+  a.d_off = act_d_off(rows, K);
+  a.s_off = act_s_off(rows, K);
+  ma.pairs = pairs;
+  ma.offsets = offsets;
+  ma.topk_w = topk_w;
+  ma.size_m = size_m;
+  ma.expert_bytes = N * a.row_bytes;
+  ma.topk = topk;
+  ma.rpp = rpp;
+  // Pairs per expert: about M / E on average; serve up to 4 per weight pass.
+  const int64_t active = M < E ? M : E;
+  const int64_t avg = (M + active - 1) / active;
+  if (avg <= 1)
+    run_moe_q4k<1>(ma, active, s);
+  else if (avg <= 2)
+    run_moe_q4k<2>(ma, active, s);
+  else
+    run_moe_q4k<4>(ma, active, s);
+  return check_launch("moe_gemv_q4k");
+}
+
+// ---------------------------------------------------------------------------
 // Q8_0 / Q6_K: LDS-staged rows, one wave per R rows.
 // ---------------------------------------------------------------------------
 struct StagedArgs {

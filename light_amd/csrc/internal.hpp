@@ -66,8 +66,15 @@ int launch_int4_dequant(const uint32_t *codes, const float *s, const float *z, v
 int launch_int4_matmul(const void *x, int x_dtype, const uint32_t *codes, const float *s, const float *z, void *y,
                        int64_t M, int64_t N, int64_t K, int G, void *ws, hipStream_t st);
 size_t int4_ws_bytes(int64_t M, int64_t N, int64_t K, int G, int x_dtype);
-int launch_moe_q(const void *xq, const void *w, const int64_t *pairs, const int64_t *expts, int32_t *counts,
-                 int32_t *offsets, const float *topk_w, float *out, int topk, int64_t size_m, int64_t M,
-                 int64_t E, int64_t N, int64_t K, int row_per_pair, int dt, hipStream_t s);
+size_t moe_ws_bytes(int64_t rows, int64_t K, int dt);
+int launch_moe_q(const float *x, const void *w, const int64_t *pairs, const int64_t *expts, int32_t *counts,
+                 int32_t *offsets, const float *topk_w, float *out, int topk, int64_t size_m, int64_t M, int64_t rows,
+                 int64_t E, int64_t N, int64_t K, int rpp, int dt, void *ws, hipStream_t s);
+int launch_moe_gemv_q4k(const void *act, const void *w, const int64_t *pairs, const int32_t *offsets,
+                        const float *topk_w, float *out, int topk, int64_t size_m, int64_t M, int64_t rows,
+                        int64_t E, int64_t N, int64_t K, int rpp, hipStream_t s);
+int launch_moe_gemm_q4k(const uint16_t *xb, const void *w, const int64_t *pairs, const int32_t *offsets,
+                        const float *topk_w, float *out, int topk, int64_t size_m, int64_t E, int64_t N, int64_t K,
+                        int rpp, hipStream_t s);
 
 }  // namespace hq

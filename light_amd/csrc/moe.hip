@@ -1,0 +1,114 @@
+// moe.hip -- MoE grouped expert qmatmul (Light's ops.MoEGemmQ, ops/moe.go:242-265).
+//
+//   out[p, :] = w(p) * x[row(p), :] @ dequant(W[e(p)])^T   for every routed pair p
+//
+// with the pairs sorted by expert (MoERouteFromIDs, ops/moe.go:78-99),
+// row(p) = rowPerPair ? p : p / topk and w(p) = topkW[p] or 1.
+//
+//  * Expert segments: offsets[e] = first sorted position with expert >= e, found by
+//    a binary search over the sorted expert ids (one thread per expert; no atomics,
+//    deterministic); counts[e] = offsets[e+1] - offsets[e].  This fills the counts /
+//    offsets scratch Light's launcher computes with an atomic histogram and a serial
+//    scan (kernels/cuda/src/moe.cu:28-42).
+//  * Q4_K, few pairs per expert (decode): grouped int8-dot GEMV (gemv.hip), up to 4
+//    pairs per weight pass.
+//  * Q4_K, many pairs per expert (prefill): grouped bf16 MFMA GEMM (gemm.hip) over
+//    32-pair chunks.
+//  * Other formats / shapes: a generic grouped kernel on F32 activations with the
+//    bit-exact block decoder (one wave per weight row).
+#include "decode.hpp"
+#include "internal.hpp"
+
+namespace hq {
+
+__global__ __launch_bounds__(256) void moe_offsets_kernel(const int64_t *__restrict__ expts, int64_t M, int E,
+                                                          int32_t *__restrict__ counts, int32_t *__restrict__ offsets) {
+  const int e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (e > E) return;
+  auto lower = [&](int64_t v) {
+    int64_t lo = 0, hi = M;
+    while (lo < hi) {
+      const int64_t mid = (lo + hi) >> 1;
+      if (expts[mid] < v) lo = mid + 1; else hi = mid;
+    }
+    return lo;
+  };
+  const int64_t a = lower(e);
+  offsets[e] = (int32_t)a;
+  if (e < E) counts[e] = (int32_t)(lower(e + 1) - a);
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void moe_generic_kernel(const float *__restrict__ x, const uint8_t *__restrict__ w,
+                                                          const int64_t *__restrict__ pairs,
+                                                          const int32_t *__restrict__ offsets,
+                                                          const float *__restrict__ topk_w, float *__restrict__ out,
+                                                          int64_t size_m, int64_t N, int64_t K, int topk, int rpp) {
+  const int e = blockIdx.y;
+  const int seg0 = offsets[e], seg1 = offsets[e + 1];
+  if (seg0 >= seg1) return;
+  const BlockInfo bi = block_info(DT);
+  const int64_t row_bytes = K / bi.elems * bi.bytes;
+  const int lane = threadIdx.x & 63;
+  const int64_t nwaves = (int64_t)gridDim.x * 4;
+  for (int64_t n = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); n < N; n += nwaves) {
+    const uint8_t *rp = w + ((int64_t)e * N + n) * row_bytes;
+    for (int i = seg0; i < seg1; i++) {
+      const int64_t p = pairs[i];
+      if (p < 0 || p >= size_m) continue;
+      const float *xr = x + (rpp ? p : p / topk) * K;
+      float acc = 0.f;
+      for (int64_t t = lane; t < K / 8; t += 64) {
+        float y[8];
+        decode8<DT>(rp, t, y);
+#pragma unroll
+        for (int j = 0; j < 8; j++) acc += y[j] * xr[8 * t + j];
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+      if (lane == 0) out[p * N + n] = acc * (topk_w ? topk_w[p] : 1.f);
+    }
+  }
+}
+
+static bool moe_q4k_fast(int dt, int64_t K, const void *w) {
+  return dt == Q4_K && ((uintptr_t)w & 15) == 0 && K / 256 <= 128;
+}
+
+static bool moe_use_mfma(int64_t M, int64_t E) { return M > 4 * E; }
+
+size_t moe_ws_bytes(int64_t rows, int64_t K, int dt) {
+  if (rows <= 0 || K <= 0 || K % 32) return 0;
+  return dt == Q4_K ? (size_t)act_bytes(rows, K) : 0;
+}
+
+int launch_moe_q(const float *x, const void *w, const int64_t *pairs, const int64_t *expts, int32_t *counts,
+                 int32_t *offsets, const float *topk_w, float *out, int topk, int64_t size_m, int64_t M, int64_t rows,
+                 int64_t E, int64_t N, int64_t K, int rpp, int dt, void *ws, hipStream_t s) {
+  if (E > INT32_MAX - 1 || M > INT32_MAX || N > INT32_MAX) return fail(HQ_EUNSUPPORTED, "moe_gemm_q", "too large");
+  moe_offsets_kernel<<<(unsigned)cdiv(E + 1, 256), 256, 0, s>>>(expts, M, (int)E, counts, offsets);
+  if (int rc = check_launch("moe_offsets")) return rc;
+  if (moe_q4k_fast(dt, K, w)) {
+    if (moe_use_mfma(M, E)) {
+      auto *xb = static_cast<uint16_t *>(ws);
+      if (int rc = launch_to_bf16(x, F32, xb, rows, K, s)) return rc;
+      return launch_moe_gemm_q4k(xb, w, pairs, offsets, topk_w, out, topk, size_m, E, N, K, rpp, s);
+    }
+    if (int rc = launch_quantize_act(x, F32, ws, rows, K, s)) return rc;
+    return launch_moe_gemv_q4k(ws, w, pairs, offsets, topk_w, out, topk, size_m, M, rows, E, N, K, rpp, s);
+  }
+  const int64_t active = M < E ? M : E;
+  const int64_t cap = cdiv((int64_t)device_cus() * 8, active > 0 ? active : 1);
+  const int64_t wgs = cdiv(N, 4);
+  dim3 grid((unsigned)(wgs < cap ? wgs : cap), (unsigned)E);
+  auto *wb = static_cast<const uint8_t *>(w);
+  switch (dt) {
+    case Q4_K: moe_generic_kernel<Q4_K><<<grid, 256, 0, s>>>(x, wb, pairs, offsets, topk_w, out, size_m, N, K, topk, rpp); break;
+    case Q8_0: moe_generic_kernel<Q8_0><<<grid, 256, 0, s>>>(x, wb, pairs, offsets, topk_w, out, size_m, N, K, topk, rpp); break;
+    case Q6_K: moe_generic_kernel<Q6_K><<<grid, 256, 0, s>>>(x, wb, pairs, offsets, topk_w, out, size_m, N, K, topk, rpp); break;
+    default: return fail(HQ_EUNSUPPORTED, "moe_gemm_q", "dtype %d", dt);
+  }
+  return check_launch("moe_generic");
+}
+
+}  // namespace hq
