@@ -41,6 +41,9 @@ def parse():
     p.add_argument("--table", action="store_true", help="also time every config (printed to stderr)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--launches", type=int, default=200, help="per-kernel timed launches for the roofline")
+    p.add_argument("--probe", action="store_true",
+                   help="counter probe for rocprofv3 --pmc: a 64 MiB device copy, then 20 launches of the "
+                        "dominant GEMV (no timing, no JSON line)")
     return p.parse_args()
 
 
@@ -185,9 +188,21 @@ def gemv_roofline(args, w, x, dev):
     alg = w.raw.nbytes + K + 8 * (K // 32) + 4 * N  # weight + int8 activations and their scales + F32 out
     achieved = alg / (us * 1e-6) / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(f"N={N} K={K} M=1"),
             "kernel": "gemv_q4k_kernel", "shape": f"N={N} K={K} M=1", "alg_bytes_per_launch": alg,
             "avg_launch_us": round(us, 3)}
+
+
+def measured_traffic(shape):
+    """HBM bytes per launch of gemv_q4k_kernel from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+    runs (profiles/gemv_q4k_gate_traffic.md gives the commands and the copy-kernel scaling)."""
+    path = os.path.join(ROOT, "profiles", "gemv_q4k_gate_traffic.json")
+    try:
+        with open(path) as f:
+            d = json.load(f)
+    except (OSError, ValueError):
+        return None
+    return d.get("traffic_bytes") if d.get("shape") == shape else None
 
 
 def table(args, dev):
@@ -221,7 +236,8 @@ def table(args, dev):
                 nbytes = codes.nbytes + s.nbytes + z.nbytes + 2 * M * K + 2 * M * N
                 flops = 2 * M * N * K
             else:
-                continue  # MoE rows are timed by the MoE section once it lands
+                rows.extend(moe_rows(c, name, g, dev))
+                continue
         except hipq.HipqError as e:
             rows.append(dict(config=name, error=str(e)))
             continue
@@ -231,6 +247,49 @@ def table(args, dev):
                          hbm_frac=round(gbs / HBM_PEAK_GBS, 3)))
         torch.cuda.empty_cache()
     return rows
+
+
+def moe_rows(c, name, g, dev):
+    """MoE gate/up (per token) and down (per pair, weighted) Q4_K grouped GEMMs of one layer.
+    Routing rotates over 16 draws so consecutive calls touch different experts (the stacks,
+    340 MB, then exceed the 256 MB Infinity Cache)."""
+    import numpy as np
+    import torch
+    from light_amd import hipq, synth
+    E, topk, H, I, T = c["E"], c["topk"], c["H"], c["I"], c["T"]
+    dt = hipq.Q4_K
+    wgu_np = synth.gguf_weight(dt, E * 2 * I, H, g)
+    wdn_np = synth.gguf_weight(dt, E * H, I, g)
+    wgu, wdn = torch.from_numpy(wgu_np).to(dev), torch.from_numpy(wdn_np).to(dev)
+    routes = []
+    for _ in range(16):
+        ids, tw = synth.moe_routing(T, E, topk, g)
+        se, sp = synth.sort_pairs(ids)
+        routes.append((ids, torch.from_numpy(se).to(dev), torch.from_numpy(sp).to(dev), torch.from_numpy(tw).to(dev)))
+    M = T * topk
+    x = torch.from_numpy(synth.activations(T, H, g)).to(dev)
+    h = torch.from_numpy(synth.activations(M, I, g)).to(dev)
+    ogu = torch.zeros((M, 2 * I), device=dev)
+    odn = torch.zeros((M, H), device=dev)
+    counts = torch.zeros(E, dtype=torch.int32, device=dev)
+    offsets = torch.zeros(E + 1, dtype=torch.int32, device=dev)
+    ws = torch.empty(max(hipq.moe_gemm_q_ws_bytes(T, H, dt), hipq.moe_gemm_q_ws_bytes(M, I, dt), 256),
+                     dtype=torch.uint8, device=dev)
+    ebytes_gu, ebytes_dn = 2 * I * (H // 256) * 144, H * (I // 256) * 144
+    out = []
+    for leg, fn, eb, flops_n, flops_k, xb, ob in (
+            ("gate_up", lambda r: hipq.moe_gemm_q(x, wgu, r[2], r[1], E, 2 * I, H, dt, topk, out=ogu, counts=counts,
+                                                   offsets=offsets, ws=ws), ebytes_gu, 2 * I, H, 4 * T * H, 4 * M * 2 * I),
+            ("down", lambda r: hipq.moe_gemm_q(h, wdn, r[2], r[1], E, H, I, dt, topk, topk_w=r[3], out=odn,
+                                                counts=counts, offsets=offsets, ws=ws), ebytes_dn, H, I, 4 * M * I, 4 * M * H)):
+        us = time_launches(lambda i: fn(routes[i % 16]), 64, 16)
+        used = float(np.mean([len(np.unique(r[0])) for r in routes]))
+        nbytes = used * eb + xb + ob
+        flops = 2.0 * M * flops_n * flops_k
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out.append(dict(config=f"{name}_{leg}", us=round(us, 2), GBs=round(gbs, 1),
+                        TFLOPS=round(flops / (us * 1e-6) / 1e12, 2), hbm_frac=round(gbs / HBM_PEAK_GBS, 3)))
+    return out
 
 
 def cpu_baseline(inputs):
@@ -268,8 +327,30 @@ def _cpu_model():
     return "unknown"
 
 
+def probe(dev):
+    """Known-size copy (reference for the counters' scale) followed by the dominant kernel."""
+    import torch
+    from light_amd import hipq
+    src = torch.ones(64 << 18, dtype=torch.float32, device=dev)  # 64 MiB
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    gate, _, _, x_np, _ = mlp_inputs(dev)
+    x = torch.from_numpy(x_np).to(dev)
+    act = hipq.quantize_act(x)
+    out = torch.empty((1, gate.N), device=dev)
+    for i in range(20):
+        hipq.matmul_q_act(act, gate[i], 1, gate.N, gate.K, hipq.Q4_K, out=out)
+    torch.cuda.synchronize()
+    print(f"probe: copy 67108864 B x3; gemv_q4k N={gate.N} K={gate.K} x20", file=sys.stderr)
+
+
 def main():
     args = parse()
+    if args.probe:
+        import torch
+        probe(torch.device("cuda:0"))
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); "
