@@ -172,6 +172,17 @@ int hq_moe_gemm_q(const float *x, const void *w, const int64_t *sorted_pairs, co
                   int64_t M, int64_t rows, int64_t E, int64_t N, int64_t K, int row_per_pair, int w_dtype,
                   void *ws, size_t ws_bytes, hq_stream_t stream);
 
+/* MoECombine (ops/moe.go:206-240): out (M/topk, N) F32, out[t] = sum of the topk
+ * slot rows of pair_out (M, N) F32, added in slot order as Light's chain of Add ops
+ * does (bit-identical). */
+int hq_moe_combine(const float *pair_out, float *out, int64_t M, int64_t N, int topk, hq_stream_t stream);
+
+/* y (M, K) = x[:, idx] for 2- or 4-byte elements (ops.gatherColumns, ops/int4.go:129-147):
+ * the act-order (desc_act) permutation of quant.Int4.Perm applied to the activations.
+ * Indices outside [0, K) give zeros. */
+int hq_gather_cols(const void *x, const int64_t *idx, void *y, int64_t M, int64_t K, int elem_bytes,
+                   hq_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

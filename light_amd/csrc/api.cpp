@@ -367,4 +367,26 @@ int hq_moe_gemm_q(const float *x, const void *w, const int64_t *sorted_pairs, co
                       row_per_pair, w_dtype, ws, s);
 }
 
+int hq_moe_combine(const float *pair_out, float *out, int64_t M, int64_t N, int topk, hq_stream_t stream) {
+  const char *call = "hq_moe_combine";
+  if (topk < 1 || M < 0 || N < 0 || M % topk)
+    return fail(HQ_EINVAL, call, "%lld rows not divisible by topk %d", (long long)M, topk);
+  if (M == 0 || N == 0) return HQ_OK;
+  if (!pair_out || !out) return fail(HQ_EINVAL, call, "NULL pointer");
+  hipStream_t s = resolve(stream);
+  TraceSpan span("moe_combine", s);
+  return launch_moe_combine(pair_out, out, M / topk, N, topk, s);
+}
+
+int hq_gather_cols(const void *x, const int64_t *idx, void *y, int64_t M, int64_t K, int elem_bytes,
+                   hq_stream_t stream) {
+  const char *call = "hq_gather_cols";
+  if (elem_bytes != 2 && elem_bytes != 4) return fail(HQ_EINVAL, call, "element size %d", elem_bytes);
+  if (M < 0 || K < 0) return fail(HQ_EINVAL, call, "bad shape");
+  if (M == 0 || K == 0) return HQ_OK;
+  if (!x || !idx || !y) return fail(HQ_EINVAL, call, "NULL pointer");
+  hipStream_t s = resolve(stream);
+  return launch_gather_cols(x, idx, y, M, K, elem_bytes, s);
+}
+
 }  // extern "C"

@@ -53,6 +53,29 @@ int launch_int4_dequant(const uint32_t *codes, const float *s, const float *z, v
   return check_launch("int4_dequant");
 }
 
+// ---- act-order gather -----------------------------------------------------------
+// y[m, k] = x[m, idx[k]] (ops.gatherColumns, ops/int4.go:129-147: act-order GPTQ stores
+// the weight's K axis sorted by group; x's columns are gathered the same way).
+template <typename T>
+__global__ __launch_bounds__(256) void gather_cols_kernel(const T *__restrict__ x, const int64_t *__restrict__ idx,
+                                                          T *__restrict__ y, int64_t M, int64_t K) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= M * K) return;
+  const int64_t m = i / K, k = i - m * K;
+  const int64_t j = idx[k];
+  y[i] = (j >= 0 && j < K) ? x[m * K + j] : T(0);
+}
+
+int launch_gather_cols(const void *x, const int64_t *idx, void *y, int64_t M, int64_t K, int elem_bytes,
+                       hipStream_t s) {
+  dim3 g((unsigned)cdiv(M * K, 256));
+  if (elem_bytes == 4)
+    gather_cols_kernel<uint32_t><<<g, 256, 0, s>>>(static_cast<const uint32_t *>(x), idx, static_cast<uint32_t *>(y), M, K);
+  else
+    gather_cols_kernel<uint16_t><<<g, 256, 0, s>>>(static_cast<const uint16_t *>(x), idx, static_cast<uint16_t *>(y), M, K);
+  return check_launch("gather_cols");
+}
+
 // ---- GEMV -----------------------------------------------------------------------
 
 __device__ __forceinline__ float row16_sum_i4(float v) {

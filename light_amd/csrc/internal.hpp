@@ -65,8 +65,11 @@ int launch_int4_dequant(const uint32_t *codes, const float *s, const float *z, v
                         int64_t N, int64_t K, int G, int64_t off, hipStream_t st);
 int launch_int4_matmul(const void *x, int x_dtype, const uint32_t *codes, const float *s, const float *z, void *y,
                        int64_t M, int64_t N, int64_t K, int G, void *ws, hipStream_t st);
+int launch_gather_cols(const void *x, const int64_t *idx, void *y, int64_t M, int64_t K, int elem_bytes,
+                       hipStream_t s);
 size_t int4_ws_bytes(int64_t M, int64_t N, int64_t K, int G, int x_dtype);
 size_t moe_ws_bytes(int64_t rows, int64_t K, int dt);
+int launch_moe_combine(const float *pair, float *out, int64_t T, int64_t N, int topk, hipStream_t s);
 int launch_moe_q(const float *x, const void *w, const int64_t *pairs, const int64_t *expts, int32_t *counts,
                  int32_t *offsets, const float *topk_w, float *out, int topk, int64_t size_m, int64_t M, int64_t rows,
                  int64_t E, int64_t N, int64_t K, int rpp, int dt, void *ws, hipStream_t s);

@@ -71,6 +71,24 @@ __global__ __launch_bounds__(256) void moe_generic_kernel(const float *__restric
   }
 }
 
+// MoECombine (ops/moe.go:209-240): out[t, n] = ((p[t*topk] + p[t*topk+1]) + ...) in slot
+// order, the order of Light's chain of Add ops, so F32 results are bit-identical.
+__global__ __launch_bounds__(256) void moe_combine_kernel(const float *__restrict__ pair, float *__restrict__ out,
+                                                          int64_t T, int64_t N, int topk) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= T * N) return;
+  const int64_t t = i / N, n = i - t * N;
+  const float *p = pair + t * topk * N + n;
+  float acc = p[0];
+  for (int s = 1; s < topk; s++) acc = __fadd_rn(acc, p[(int64_t)s * N]);
+  out[i] = acc;
+}
+
+int launch_moe_combine(const float *pair, float *out, int64_t T, int64_t N, int topk, hipStream_t s) {
+  moe_combine_kernel<<<(unsigned)cdiv(T * N, 256), 256, 0, s>>>(pair, out, T, N, topk);
+  return check_launch("moe_combine");
+}
+
 static bool moe_q4k_fast(int dt, int64_t K, const void *w) {
   return dt == Q4_K && ((uintptr_t)w & 15) == 0 && K / 256 <= 128;
 }

@@ -63,6 +63,8 @@ SIGNATURES = {
     "hq_int4_matmul": (_I, [_P, _I, _P, _P, _P, _P, _I64, _I64, _I64, _I, _P, _SZ, _P]),
     "hq_int4_dequant": (_I, [_P, _P, _P, _P, _I, _I64, _I64, _I, _I64, _P]),
     "hq_moe_gemm_q_ws_bytes": (_SZ, [_I64, _I64, _I]),
+    "hq_moe_combine": (_I, [_P, _P, _I64, _I64, _I, _P]),
+    "hq_gather_cols": (_I, [_P, _P, _P, _I64, _I64, _I, _P]),
     "hq_moe_gemm_q": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I,
                            _P, _SZ, _P]),
 }
@@ -224,6 +226,16 @@ def moe_gemm_q(x, w, sorted_pairs, sorted_expts, E, N, K, w_dtype, topk, topk_w=
     check(lib().hq_moe_gemm_q(_ptr(x), _ptr(w), _ptr(sorted_pairs), _ptr(sorted_expts), _ptr(counts),
                               _ptr(offsets), _ptr(topk_w), _ptr(out), topk, out.shape[0], M, rows, E, N, K, rpp,
                               w_dtype, _ptr(ws), ws_bytes, _stream(stream)))
+    return out
+
+
+def moe_combine(pair_out, topk, out=None, stream=None):
+    """(M, N) pair rows -> (M/topk, N): slot rows summed in slot order."""
+    import torch
+    M, N = pair_out.shape
+    if out is None:
+        out = torch.empty((M // topk, N), dtype=torch.float32, device=pair_out.device)
+    check(lib().hq_moe_combine(_ptr(pair_out), _ptr(out), M, N, topk, _stream(stream)))
     return out
 
 

@@ -1,0 +1,65 @@
+// kernels_rocm.cpp -- registry entries of the ROCm backend (the role of Light's
+// kernels/cuda/*.go init() registrations: matmul_q.go:35-39, int4.go:15-20,
+// moe.go:78-82, dequant.go:15-17).  Each kernel unpacks its Context and calls one
+// libhipq C-ABI entry point on the library's current stream.
+#include "../../include/hipq.h"
+#include "registry.hpp"
+
+namespace light {
+namespace {
+
+const DType kGGUF[] = {DType::Q8_0, DType::Q4_K, DType::Q6_K};
+
+void matmul_q(Context &c) {
+  const Tensor &x = c.in(0), &w = c.in(1);
+  Check(hq_matmul_q(static_cast<const float *>(x.data()), w.data(), static_cast<float *>(c.output.data()), x.Dim(0),
+                    w.Dim(0), x.Dim(1), (int)w.dtype(), nullptr, 0, nullptr));
+}
+
+void int4_gemv(Context &c) {
+  const Tensor &x = c.in(0), &codes = c.in(1), &s = c.in(2), &z = c.in(3);
+  Check(hq_int4_matmul(x.data(), (int)x.dtype(), static_cast<const uint32_t *>(codes.data()),
+                       static_cast<const float *>(s.data()), static_cast<const float *>(z.data()), c.output.data(),
+                       x.Dim(0), codes.Dim(0), x.Dim(1), (int)c.attr("group"), nullptr, 0, nullptr));
+}
+
+void int4_dequant(Context &c) {
+  const Tensor &codes = c.in(0), &s = c.in(1), &z = c.in(2);
+  Check(hq_int4_dequant(static_cast<const uint32_t *>(codes.data()), static_cast<const float *>(s.data()),
+                        static_cast<const float *>(z.data()), c.output.data(), (int)c.output.dtype(), codes.Dim(0),
+                        codes.Dim(1) * 8, (int)c.attr("group"), c.attr("offset"), nullptr));
+}
+
+void moe_gemm_q(Context &c) {
+  const Tensor &x = c.in(0), &w = c.in(1), &pairs = c.in(2), &expts = c.in(3), &counts = c.in(4),
+               &offsets = c.in(5);
+  const float *tw = c.has(6) ? static_cast<const float *>(c.in(6).data()) : nullptr;
+  const int topk = (int)c.attr("topk");
+  Check(hq_moe_gemm_q(static_cast<const float *>(x.data()), w.data(), static_cast<const int64_t *>(pairs.data()),
+                      static_cast<const int64_t *>(expts.data()), static_cast<int32_t *>(counts.data()),
+                      static_cast<int32_t *>(offsets.data()), tw, static_cast<float *>(c.output.data()), topk,
+                      c.output.Dim(0), pairs.Dim(0), x.Dim(0), w.Dim(0), w.Dim(1), w.Dim(2),
+                      (int)c.attr("row_per_pair"), (int)w.dtype(), nullptr, 0, nullptr));
+}
+
+void dequant(Context &c) {
+  const Tensor &w = c.in(0);
+  Check(hq_dequant(w.data(), c.output.data(), w.NumElements(), (int)w.dtype(), HQ_F32, nullptr));
+}
+
+struct Registrar {
+  Registrar() {
+    for (DType dt : kGGUF) {
+      Register(Key{"matmul_q", DeviceKind::ROCm, dt}, matmul_q);
+      Register(Key{"moe_gemm_q", DeviceKind::ROCm, dt}, moe_gemm_q);
+      Register(Key{"dequant", DeviceKind::ROCm, dt}, dequant);
+    }
+    Register(Key{"dequant", DeviceKind::ROCm, DType::Q8_1}, dequant);
+    for (DType dt : {DType::F32, DType::BF16, DType::F16}) Register(Key{"int4_gemv", DeviceKind::ROCm, dt}, int4_gemv);
+    for (DType dt : {DType::F32, DType::BF16}) Register(Key{"int4_dequant", DeviceKind::ROCm, dt}, int4_dequant);
+  }
+};
+const Registrar registrar;
+
+}  // namespace
+}  // namespace light

@@ -1,0 +1,202 @@
+// ops.cpp -- MatMulQ, MatMulInt4, DequantizeInt4, MoERouteFromIDs, MoEGemmQ, MoECombine,
+// Dequantize: validation, output allocation and registry dispatch as in Light's ops package.
+#include "ops.hpp"
+
+#include <algorithm>
+#include <numeric>
+
+#include "../../include/hipq.h"
+#include "registry.hpp"
+
+namespace light {
+namespace ops {
+
+static bool same_device(const Tensor &a, const Tensor &b) { return a.device().SameAs(b.device()); }
+
+// ---- MatMulQ (ops/matmul_q.go:27-76) ----
+
+Tensor MatMulQ(const Tensor &x, const Tensor &w) {
+  if (x.Rank() != 2 || w.Rank() != 2)
+    Fail("MatMulQ: want x (M,K) and w (N,K); got %s, %s", x.ShapeStr().c_str(), w.ShapeStr().c_str());
+  if (x.dtype() != DType::F32) Fail("MatMulQ: x must be F32, got %s", DTypeName(x.dtype()));
+  if (!IsQuantized(w.dtype())) Fail("MatMulQ: w must be a quantized dtype, got %s", DTypeName(w.dtype()));
+  if (!same_device(x, w)) Fail("MatMulQ: x on %s, w on %s", x.device().str().c_str(), w.device().str().c_str());
+  const int64_t M = x.Dim(0), K = x.Dim(1), N = w.Dim(0);
+  if (w.Dim(1) != K) Fail("MatMulQ: inner dim mismatch (x K=%lld, w K=%lld)", (long long)K, (long long)w.Dim(1));
+  if (K % BlockElems(w.dtype()))
+    Fail("MatMulQ: K=%lld not a multiple of %s block size %d", (long long)K, DTypeName(w.dtype()),
+         BlockElems(w.dtype()));
+  // Light's CUDA-only M >= MatMulQDequantMinRows fallback (:52-59) does not apply: the
+  // ROCm kernel serves every M (GEMV for decode, MFMA GEMM for prefill).
+  Kernel k = Lookup(Key{"matmul_q", x.device().kind, w.dtype()});
+  Tensor out = Tensor::Empty(DType::F32, {M, N}, x.device());
+  Context ctx;
+  ctx.inputs = {x, w};
+  ctx.output = out;
+  k(ctx);
+  return out;
+}
+
+bool MatMulQFusedOn(DeviceKind kind, DType dt) {
+  try {
+    Lookup(Key{"matmul_q", kind, dt});
+    return true;
+  } catch (const Error &e) {
+    if (e.IsKernelNotFound()) return false;
+    throw;
+  }
+}
+
+// ---- int4 (ops/int4.go) ----
+
+static void dequantize_int4_at(const Int4 &w, const Tensor &out, int64_t off) {
+  if (w.group <= 0 || w.K() % w.group)
+    Fail("ops.DequantizeInt4: group %d does not divide K %lld", w.group, (long long)w.K());
+  Kernel k = Lookup(Key{"int4_dequant", w.codes.device().kind, out.dtype()});
+  Context ctx;
+  ctx.inputs = {w.codes, w.scales, w.zeros};
+  ctx.output = out;
+  ctx.attrs = {{"group", Attr::Int(w.group)}, {"offset", Attr::Int(off)}};
+  k(ctx);
+}
+
+Tensor DequantizeInt4(const Int4 &w, DType out_dt) {
+  Tensor out = Tensor::Zeros(out_dt, {w.N(), w.K()}, w.codes.device());
+  dequantize_int4_at(w, out, 0);
+  return out;
+}
+
+constexpr int64_t kInt4GEMVMaxM = 8;  // ops/int4.go:58-59
+
+Tensor MatMulInt4(const Tensor &x, const Int4 &w) {
+  if (x.Rank() != 2 || x.Dim(1) != w.K())
+    Fail("ops.MatMulInt4: x %s, weight (%lld, %lld)", x.ShapeStr().c_str(), (long long)w.N(), (long long)w.K());
+  // Light takes F32 or BF16 (:70-72); F16 activations are this library's extension.
+  if (x.dtype() != DType::F32 && x.dtype() != DType::BF16 && x.dtype() != DType::F16)
+    Fail("ops.MatMulInt4: activations %s, want F32, BF16 or F16", DTypeName(x.dtype()));
+  const int64_t M = x.Dim(0), N = w.N();
+  Tensor xc = x;
+  if (w.perm) {
+    // Act-order GPTQ: gather x's columns into the weight's K order (x[:, Perm]).
+    xc = Tensor::Empty(x.dtype(), x.shape(), x.device());
+    if (x.device().kind != DeviceKind::ROCm) Fail("ops.MatMulInt4: act-order gather needs a ROCm device");
+    Check(hq_gather_cols(x.data(), static_cast<const int64_t *>(w.perm->data()), xc.data(), M, w.K(),
+                         x.dtype() == DType::F32 ? 4 : 2, nullptr));
+  }
+  // Light runs the fused kernel for M <= 8 on GPUs (:87-99); the ROCm kernel also serves
+  // larger M (its MFMA leg), so ROCm takes it for every M.
+  const bool fused_ok = w.K() % 32 == 0 && w.group % 32 == 0;
+  if (fused_ok && (M <= kInt4GEMVMaxM || x.device().kind != DeviceKind::CUDA)) {
+    Kernel k = Lookup(Key{"int4_gemv", x.device().kind, x.dtype()});
+    Tensor out = Tensor::Zeros(x.dtype(), {M, N}, x.device());
+    Context ctx;
+    ctx.inputs = {xc, w.codes, w.scales, w.zeros};
+    ctx.output = out;
+    ctx.attrs = {{"group", Attr::Int(w.group)}};
+    k(ctx);
+    return out;
+  }
+  Fail("ops.MatMulInt4: K=%lld, group %d: no fused kernel (K and the group must be multiples of 32)",
+       (long long)w.K(), w.group);
+}
+
+// ---- MoE (ops/moe.go) ----
+
+MoERouting MoERouteFromIDs(const std::vector<int64_t> &ids, const std::vector<float> &weights, int64_t T,
+                           int topk, Device dev) {
+  const int64_t M = T * topk;
+  if ((int64_t)ids.size() != M || (int64_t)weights.size() != M)
+    Fail("moe_route: %zu ids / %zu weights for %lld × %d", ids.size(), weights.size(), (long long)T, topk);
+  // Sort(flat, false): a stable ascending sort (kernels/cpu/shape_ops.go:156-184).
+  std::vector<int64_t> order(M);
+  std::iota(order.begin(), order.end(), 0);
+  std::stable_sort(order.begin(), order.end(), [&](int64_t a, int64_t b) { return ids[a] < ids[b]; });
+  std::vector<int64_t> sorted(M);
+  for (int64_t i = 0; i < M; i++) sorted[i] = ids[order[i]];
+  MoERouting r;
+  r.topk_ids = Tensor::FromHost(ids.data(), 8 * M, DType::I64, {T, topk}, dev);
+  r.weights = Tensor::FromHost(weights.data(), 4 * M, DType::F32, {M}, dev);
+  r.sorted_pairs = Tensor::FromHost(order.data(), 8 * M, DType::I64, {M}, dev);
+  r.sorted_expts = Tensor::FromHost(sorted.data(), 8 * M, DType::I64, {M}, dev);
+  return r;
+}
+
+// moeGemmDispatch (ops/moe.go:122-204) for op "moe_gemm_q".
+static Tensor moe_gemm_dispatch(const char *op, DType key_dt, const Tensor &input, const Tensor &weights,
+                                const MoERouting &routing, const Tensor *topk_weights, int topk) {
+  if (input.Rank() != 2 || weights.Rank() != 3)
+    Fail("%s: input (rows, K) and weights (E, N, K) required, got %s / %s", op, input.ShapeStr().c_str(),
+         weights.ShapeStr().c_str());
+  if (!same_device(input, weights) || !same_device(input, routing.sorted_pairs)) Fail("%s: device mismatch", op);
+  const int64_t E = weights.Dim(0), N = weights.Dim(1), K = weights.Dim(2);
+  if (input.Dim(1) != K) Fail("%s: input K %lld != weights K %lld", op, (long long)input.Dim(1), (long long)K);
+  const int64_t M = routing.sorted_pairs.Dim(0);
+  if (routing.sorted_expts.Dim(0) != M || routing.sorted_pairs.dtype() != DType::I64 ||
+      routing.sorted_expts.dtype() != DType::I64)
+    Fail("%s: routing must hold M I64 pair ids and M I64 expert ids", op);
+  bool row_per_pair;
+  if (input.Dim(0) == M)
+    row_per_pair = true;
+  else if (input.Dim(0) == M / topk)
+    row_per_pair = false;
+  else
+    Fail("%s: input rows %lld must be M=%lld (per pair) or M/topk=%lld (per token)", op, (long long)input.Dim(0),
+         (long long)M, (long long)(M / topk));
+  if (topk_weights) {
+    if (topk_weights->dtype() != DType::F32 || topk_weights->NumElements() != M)
+      Fail("%s: topkWeights must be F32 with %lld elements", op, (long long)M);
+    if (!same_device(*topk_weights, input)) Fail("%s: topkWeights device mismatch", op);
+  }
+  Tensor counts = Tensor::Zeros(DType::I32, {E}, input.device());
+  Tensor offsets = Tensor::Zeros(DType::I32, {E + 1}, input.device());
+  Tensor out = Tensor::Zeros(input.dtype(), {M, N}, input.device());
+  Kernel k = Lookup(Key{op, input.device().kind, key_dt});
+  Context ctx;
+  ctx.inputs = {input, weights, routing.sorted_pairs, routing.sorted_expts, counts, offsets};
+  if (topk_weights) ctx.inputs.push_back(*topk_weights);
+  ctx.output = out;
+  ctx.attrs = {{"topk", Attr::Int(topk)}, {"row_per_pair", Attr::Bool(row_per_pair)}};
+  k(ctx);
+  return out;
+}
+
+Tensor MoEGemmQ(const Tensor &x, const Tensor &w, const MoERouting &routing, const Tensor *topk_weights, int topk) {
+  if (x.dtype() != DType::F32) Fail("moe_gemm_q: x must be F32, got %s", DTypeName(x.dtype()));
+  if (!IsQuantized(w.dtype()) || w.Rank() != 3)
+    Fail("moe_gemm_q: w must be a quantized (E, N, K) tensor, got %s %s", DTypeName(w.dtype()), w.ShapeStr().c_str());
+  if (w.Dim(2) % BlockElems(w.dtype()))
+    Fail("moe_gemm_q: K=%lld not a multiple of %s block size %d", (long long)w.Dim(2), DTypeName(w.dtype()),
+         BlockElems(w.dtype()));
+  return moe_gemm_dispatch("moe_gemm_q", w.dtype(), x, w, routing, topk_weights, topk);
+}
+
+Tensor MoECombine(const Tensor &pair_out, int topk) {
+  const int64_t M = pair_out.Dim(0), N = pair_out.Dim(1);
+  if (topk < 1 || M % topk) Fail("moe_combine: %lld rows not divisible by topk %d", (long long)M, topk);
+  if (pair_out.dtype() != DType::F32) Fail("moe_combine: %s rows, want F32", DTypeName(pair_out.dtype()));
+  if (pair_out.device().kind != DeviceKind::ROCm)
+    Fail("moe_combine: device %s is not supported by this build", pair_out.device().str().c_str());
+  Tensor out = Tensor::Empty(DType::F32, {M / topk, N}, pair_out.device());
+  Check(hq_moe_combine(static_cast<const float *>(pair_out.data()), static_cast<float *>(out.data()), M, N, topk,
+                       nullptr));
+  return out;
+}
+
+// ---- Dequantize (quant/dequant.go:10-42, dispatchRegistry quant/cuda_hook.go:51-69) ----
+
+Tensor Dequantize(const Tensor &w) {
+  if (!IsQuantized(w.dtype())) Fail("quant.Dequantize: %s is not a quantized dtype", DTypeName(w.dtype()));
+  if (w.NumElements() % BlockElems(w.dtype()))
+    Fail("quant.Dequantize: element count %lld not a multiple of %s block size %d", (long long)w.NumElements(),
+         DTypeName(w.dtype()), BlockElems(w.dtype()));
+  Kernel k = Lookup(Key{"dequant", w.device().kind, w.dtype()});
+  Tensor out = Tensor::Empty(DType::F32, w.shape(), w.device());
+  Context ctx;
+  ctx.inputs = {w};
+  ctx.output = out;
+  k(ctx);
+  return out;
+}
+
+}  // namespace ops
+}  // namespace light

@@ -1,0 +1,51 @@
+// ops.hpp -- Light's public ops for the quantized matmul path (package ops), restated in C++.
+//
+// Each op validates like Light's Go function (same checks, same messages), allocates its
+// output as Light's op layer does, and runs the kernel registered for
+// (op, device kind, dtype) -- on ROCm the libhipq kernels of kernels_rocm.cpp.
+#pragma once
+
+#include <optional>
+#include <vector>
+
+#include "light.hpp"
+
+namespace light {
+namespace ops {
+
+// ops.MatMulQ (ops/matmul_q.go:14-76): x F32 (M, K) times a GGUF-quantized weight (N, K)^T -> F32 (M, N).
+Tensor MatMulQ(const Tensor &x, const Tensor &w);
+// ops.MatMulQFusedOn (ops/matmul_q.go:102-106).
+bool MatMulQFusedOn(DeviceKind kind, DType dt);
+
+// quant.Int4 (quant/int4.go:11-34): Codes U32 (N, K/8), Scales / Zeros F32 (N, K/G), Group,
+// Perm I64 (K,) for act-order checkpoints.
+struct Int4 {
+  Tensor codes, scales, zeros;
+  int group = 0;
+  std::optional<Tensor> perm;
+  int64_t N() const { return codes.Dim(0); }
+  int64_t K() const { return codes.Dim(1) * 8; }
+};
+// ops.DequantizeInt4 (ops/int4.go:13-56).
+Tensor DequantizeInt4(const Int4 &w, DType out_dt);
+// ops.MatMulInt4 (ops/int4.go:61-127).
+Tensor MatMulInt4(const Tensor &x, const Int4 &w);
+
+// ops.MoERouting (ops/moe.go:13-22).
+struct MoERouting {
+  Tensor topk_ids, weights, sorted_pairs, sorted_expts;
+};
+// ops.MoERouteFromIDs (ops/moe.go:73-99).
+MoERouting MoERouteFromIDs(const std::vector<int64_t> &ids, const std::vector<float> &weights, int64_t T,
+                           int topk, Device dev);
+// ops.MoEGemmQ (ops/moe.go:242-265); topk_weights may be absent.
+Tensor MoEGemmQ(const Tensor &x, const Tensor &w, const MoERouting &routing, const Tensor *topk_weights, int topk);
+// ops.MoECombine (ops/moe.go:206-240).
+Tensor MoECombine(const Tensor &pair_out, int topk);
+
+// quant.Dequantize (quant/dequant.go:10-42) through the "dequant" registry key.
+Tensor Dequantize(const Tensor &w);
+
+}  // namespace ops
+}  // namespace light
