@@ -108,9 +108,13 @@ int hq_matmul_q(const float *x, const void *w, float *out, int64_t M, int64_t N,
  * A caller that multiplies one activation by several weights (the SwiGLU gate
  * and up projections, models/llama.go:1306-1328) quantizes once and reuses it.
  * No counterpart in Light.  The act buffer (hq_act_bytes(M, K) bytes, 16-byte
- * aligned) holds x's q8_1 quantization in a planar layout: int8 q [M][K], then
- * f32 d [M][K/32], then f32 d*sum(q) [M][K/32]; q and d are the values
- * hq_quantize_q8_1 produces (d before its f16 rounding). */
+ * aligned) holds a two-level int8 quantization of x in a planar layout:
+ *   q1 int8 [M][K]            q8_1's quants (d = amax/127), as hq_quantize_q8_1
+ *   q2 int8 [M][K]            quants of the residual x - d*q1 at step e = d/254
+ *   (d, e) f32 pairs [M][K/32] (d before q8_1's f16 rounding)
+ *   sx f32 [M][K/32]          the block sum of x
+ * so x = d*q1 + e*q2 to within e/2 (about 2^-15 of the block's amax); offsets are
+ * rounded up to 256 bytes.  The layout is internal and may change with the version. */
 size_t hq_act_bytes(int64_t M, int64_t K);
 int hq_quantize_act(const void *x, int x_dtype, void *act, int64_t M, int64_t K, hq_stream_t stream);
 /* Workspace hq_matmul_q_act needs beyond the act buffer (0 for the GEMV). */
