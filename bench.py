@@ -1,19 +1,22 @@
 """Benchmark of the MI355X quantized-matmul path (BASELINE.json metric).
 
 Headline metric: Q4_K GEMV GB/s at Llama-3-8B MLP decode shapes,
-plus the Q4_K M=512 GEMM TFLOPS.  One "step" is one MLP decode
-pass through the hot path: the gate (14336x4096), up (14336x4096) and down
-(4096x14336) Q4_K projections at M = 1, each an hq_matmul_q call (on-GPU
-q8_1 quantization + GEMV).  Inputs are synthetic (seeded, BASELINE
-distributions), resident in HBM; every weight is rotated over enough copies
-that the working set exceeds the 256 MB Infinity Cache.
+plus the Q4_K M=512 GEMM TFLOPS (configs[2], in --table).  One "step" is one
+MLP decode pass through the hot path at M = 1, as Light's decoder runs it
+(models/llama.go:1306-1333), one hq_mlp_q call = two kernels:
+    h = SiLU(x . Wgate^T) * (x . Wup^T)     gate/up 14336x4096 Q4_K (h emitted quantized)
+    y = h . Wdown^T                          down 4096x14336 Q4_K
+Inputs are synthetic (seeded, BASELINE distributions), resident in HBM; every
+weight is rotated over enough copies that the working set exceeds the 256 MB
+Infinity Cache.
 
-`value` is whole-job throughput: algorithmic bytes of a step (weights as
-stored + F32 activations + F32 outputs) / wall time of the K timed steps,
+`value` is whole-job throughput: algorithmic bytes of a step (the three weights
+as stored + F32 x in + F32 y out) / wall time of the K timed steps,
 replayed as captured HIP graphs so host launch cost is not measured.
-`roofline` is for the dominant kernel (the Q4_K GEMV), timed per launch with
-HIP events on its stream.  `cpu_baseline` is Light's AVX2 CPU qmatmul (the
-C restatement in oracle/) on the same step, on this host's cores.
+`roofline` is for the dominant kernel (the fused gate/up Q4_K GEMV), timed
+per launch with HIP events on its stream.  `cpu_baseline` is Light's AVX2 CPU
+path (the C restatement in oracle/: MatMulQ, MatMulQ, SiLU, Mul, MatMulQ) on
+the same step, on this host's cores.
 
 Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--table] [--no-cpu]
 """
@@ -78,12 +81,10 @@ def mlp_inputs(dev):
     return gate, up, down, x, h
 
 
-def step_bytes(ws_list, M):
-    """Algorithmic bytes: weights as stored + F32 x + F32 out, per matmul."""
-    tot = 0
-    for w in ws_list:
-        tot += w.raw.nbytes + 4 * M * w.K + 4 * M * w.N
-    return tot
+def step_bytes(gate, up, down, M=1):
+    """Algorithmic bytes of one MLP decode step: the three weights as stored, F32 x in and
+    F32 y out (h stays inside the step)."""
+    return gate.raw.nbytes + up.raw.nbytes + down.raw.nbytes + 4 * M * gate.K + 4 * M * down.N
 
 
 def run_gpu(args):
@@ -94,24 +95,18 @@ def run_gpu(args):
     torch.cuda.set_device(dev)
     gate, up, down, x_np, h_np = mlp_inputs(dev)
     x = torch.from_numpy(x_np).to(dev)
-    h = torch.from_numpy(h_np).to(dev)
     H, I = 4096, 14336
-    ws = torch.empty(max(hipq.matmul_q_ws_bytes(1, I, H, hipq.Q4_K), hipq.matmul_q_ws_bytes(1, H, I, hipq.Q4_K)),
-                     dtype=torch.uint8, device=dev)
-    yg = torch.empty((1, I), device=dev)
-    yu = torch.empty((1, I), device=dev)
-    yd = torch.empty((1, H), device=dev)
+    ws = torch.empty(hipq.mlp_q_ws_bytes(1, H, I, hipq.Q4_K), dtype=torch.uint8, device=dev)
+    y = torch.empty((1, H), device=dev)
     rot = max(len(gate.copies), len(down.copies))
 
     def step(i):
-        hipq.matmul_q(x, gate[i], I, H, hipq.Q4_K, out=yg, ws=ws)
-        hipq.matmul_q(x, up[i], I, H, hipq.Q4_K, out=yu, ws=ws)
-        hipq.matmul_q(h, down[i], H, I, hipq.Q4_K, out=yd, ws=ws)
+        hipq.mlp_q(x, gate[i], up[i], down[i], H, I, hipq.Q4_K, act=hipq.ACT_SILU, out=y, ws=ws)
 
     # Eager reference outputs of copy 0, then one graph per weight copy.
     step(0)
     torch.cuda.synchronize()
-    eager = (yg.clone(), yu.clone(), yd.clone())
+    eager = (y.clone(),)
     # One graph holds `rot` consecutive steps (one per weight copy), so the
     # replays amortise graph-launch cost; single-step graphs cover a remainder.
     cap = torch.cuda.Stream()
@@ -131,7 +126,7 @@ def run_gpu(args):
     for rep in range(3):  # replays must reproduce the eager result (copies hold identical bytes)
         (full if rep % 2 else singles[rep]).replay()
         torch.cuda.synchronize()
-        for a, b in zip((yg, yu, yd), eager):
+        for a, b in zip((y,), eager):
             if not torch.equal(a, b):
                 raise RuntimeError("graph replay differs from the eager step")
         step(1)
@@ -149,12 +144,14 @@ def run_gpu(args):
     run_steps(args.steps)
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
-    nbytes = step_bytes([gate, up, down], 1)
+    nbytes = step_bytes(gate, up, down)
     ms_per_step = dt * 1e3 / args.steps
     value = nbytes * args.steps / dt / 1e9
 
-    roof = gemv_roofline(args, gate, x, dev)
-    return dict(value=value, ms_per_step=ms_per_step, step_bytes=nbytes, roofline=roof,
+    roof = gemv_roofline(args, gate, up, x, dev)
+    h = torch.from_numpy(h_np).to(dev)
+    down_k = down_kernel(args, down, h, dev)
+    return dict(value=value, ms_per_step=ms_per_step, step_bytes=nbytes, roofline=roof, down=down_k,
                 inputs=(gate, up, down, x_np, h_np))
 
 
@@ -176,27 +173,43 @@ def time_launches(fn, n, rot):
     return a.elapsed_time(b) * 1e3 / n
 
 
-def gemv_roofline(args, w, x, dev):
-    """Roofline of the dominant kernel: the Q4_K GEMV (gemv_q4k_kernel) on prepared activations."""
+def gemv_roofline(args, gate, up, x, dev):
+    """Roofline of the dominant kernel: the fused gate/up Q4_K GEMV (gemv_q4kx_kernel<1, true, D>),
+    x F32 quantized inside the kernel."""
     import torch
     from light_amd import hipq
-    N, K = w.N, w.K
-    act = hipq.quantize_act(x)
+    N, K = gate.N, gate.K
     out = torch.empty((1, N), device=dev)
-    us = time_launches(lambda i: hipq.matmul_q_act(act, w[i], 1, N, K, hipq.Q4_K, out=out), args.launches,
-                       len(w.copies))
-    alg = w.raw.nbytes + K + 8 * (K // 32) + 4 * N  # weight + int8 activations and their scales + F32 out
+    us = time_launches(lambda i: hipq.matmul_q_gated(x, gate[i], up[i], N, K, hipq.Q4_K, out=out), args.launches,
+                       len(gate.copies))
+    alg = gate.raw.nbytes + up.raw.nbytes + 4 * K + 4 * N  # both weights + F32 x + F32 h
     achieved = alg / (us * 1e-6) / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(f"N={N} K={K} M=1"),
-            "kernel": "gemv_q4k_kernel", "shape": f"N={N} K={K} M=1", "alg_bytes_per_launch": alg,
-            "avg_launch_us": round(us, 3)}
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(f"gated N={N} K={K} M=1"),
+            "kernel": "gemv_q4kx_kernel (gated)", "shape": f"gate+up N={N} K={K} M=1",
+            "alg_bytes_per_launch": alg, "avg_launch_us": round(us, 3)}
+
+
+def down_kernel(args, down, h, dev):
+    """The step's second kernel: the down projection GEMV on prepared activations
+    (gemv_q4kx_kernel, act input)."""
+    import torch
+    from light_amd import hipq
+    N, K = down.N, down.K
+    out = torch.empty((1, N), device=dev)
+    act = hipq.quantize_act(h)
+    us = time_launches(lambda i: hipq.matmul_q_act(act, down[i], 1, N, K, hipq.Q4_K, out=out), args.launches,
+                       len(down.copies))
+    alg = down.raw.nbytes + hipq.lib().hq_act_bytes(1, K) + 4 * N
+    gbs = alg / (us * 1e-6) / 1e9
+    return {"kernel": "gemv_q4kx_kernel (act input)", "shape": f"down N={N} K={K} M=1", "avg_launch_us": round(us, 3),
+            "achieved": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
 def measured_traffic(shape):
-    """HBM bytes per launch of gemv_q4k_kernel from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
-    runs (profiles/gemv_q4k_gate_traffic.md gives the commands and the copy-kernel scaling)."""
-    path = os.path.join(ROOT, "profiles", "gemv_q4k_gate_traffic.json")
+    """HBM bytes per launch of the fused gate/up kernel from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE runs (profiles/gemv_q4k_gated_traffic.md gives the commands and the copy-kernel scaling)."""
+    path = os.path.join(ROOT, "profiles", "gemv_q4k_gated_traffic.json")
     try:
         with open(path) as f:
             d = json.load(f)
@@ -293,15 +306,17 @@ def moe_rows(c, name, g, dev):
 
 
 def cpu_baseline(inputs):
-    """Light's AVX2 CPU qmatmul (oracle C restatement) on the same step; median of 5 after a warm-up."""
+    """Light's AVX2 CPU path (oracle C restatement: MatMulQ, MatMulQ, SiLU, Mul, MatMulQ) on the same
+    step; median of 5 after a warm-up."""
     import oracle
-    gate, up, down, x, h = inputs
+    gate, up, down, x, _ = inputs
     threads = int(os.environ.get("OMP_NUM_THREADS", "16"))
     threads = max(1, min(threads, oracle.hw_threads()))
 
     def run():
-        oracle.matmul_q(x, gate.raw, gate.N, gate.K, gate.dt, threads)
-        oracle.matmul_q(x, up.raw, up.N, up.K, up.dt, threads)
+        g = oracle.matmul_q(x, gate.raw, gate.N, gate.K, gate.dt, threads)
+        u = oracle.matmul_q(x, up.raw, up.N, up.K, up.dt, threads)
+        h = oracle.gated(g, u, 0)
         oracle.matmul_q(h, down.raw, down.N, down.K, down.dt, threads)
 
     run()
@@ -311,9 +326,9 @@ def cpu_baseline(inputs):
         run()
         ts.append(time.perf_counter() - t0)
     t = statistics.median(ts)
-    nbytes = step_bytes([gate, up, down], 1)
+    nbytes = step_bytes(gate, up, down)
     return {"value": round(nbytes / t / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"5 timed MLP decode steps (gate+up+down Q4_K, M=1), median {t * 1e3:.2f} ms/step",
+            "sample": f"5 timed MLP decode steps (gate, up, SiLU*up, down; Q4_K, M=1), median {t * 1e3:.2f} ms/step",
             "cpu": _cpu_model()}
 
 
@@ -335,14 +350,13 @@ def probe(dev):
     dst = torch.empty_like(src)
     for _ in range(3):
         dst.copy_(src)
-    gate, _, _, x_np, _ = mlp_inputs(dev)
+    gate, up, _, x_np, _ = mlp_inputs(dev)
     x = torch.from_numpy(x_np).to(dev)
-    act = hipq.quantize_act(x)
     out = torch.empty((1, gate.N), device=dev)
     for i in range(20):
-        hipq.matmul_q_act(act, gate[i], 1, gate.N, gate.K, hipq.Q4_K, out=out)
+        hipq.matmul_q_gated(x, gate[i], up[i], gate.N, gate.K, hipq.Q4_K, out=out)
     torch.cuda.synchronize()
-    print(f"probe: copy 67108864 B x3; gemv_q4k N={gate.N} K={gate.K} x20", file=sys.stderr)
+    print(f"probe: copy 67108864 B x3; gemv_q4k gated N={gate.N} K={gate.K} x20", file=sys.stderr)
 
 
 def main():
@@ -371,9 +385,11 @@ def main():
         "dtype": "q4_k x q8_1 -> f32 (int8 dot, f32 accumulate)",
         "data": "synthetic (seeded, BASELINE.json distributions; weights rotated over >512 MB)",
         "config": {"workload": "llama3_8b_mlp_decode_q4_k", "M": 1, "hidden": 4096, "intermediate": 14336,
-                   "matmuls": ["gate 14336x4096", "up 14336x4096", "down 4096x14336"],
+                   "matmuls": ["gate+up 2x14336x4096 (fused, SiLU*up, h quantized in the epilogue)",
+                               "down 4096x14336"],
                    "step_bytes": res["step_bytes"]},
         "roofline": res["roofline"],
+        "second_kernel": res["down"],
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(res["inputs"])

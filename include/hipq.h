@@ -95,16 +95,44 @@ size_t hq_matmul_q_ws_bytes(int64_t M, int64_t N, int64_t K, int w_dtype);
 
 /* out (M, N) F32 = x (M, K) F32 contiguous @ dequant(w (N, K))^T.
  * w_dtype: HQ_Q8_0, HQ_Q4_K or HQ_Q6_K.  K must be a multiple of the block
- * size.  M <= 8 (and Q8_0 / Q6_K at any M): x is quantized on the GPU to q8_1
- * into ws and the int8-dot GEMV runs; Q4_K with M > 8: x is rounded to bf16
- * into ws and the bf16 MFMA GEMM runs.
+ * size.  M <= 8 (and Q8_0 / Q6_K at any M): the int8-dot GEMV runs on x quantized
+ * on the GPU to q8_1 (Q4_K: inside the GEMV's workgroups; Q8_0 / Q6_K: into ws
+ * first); Q4_K with M > 8: x is rounded to bf16 into ws and the bf16 MFMA GEMM runs.
  * Replaces registry kernel "matmul_q" (ops/matmul_q.go:61-75; CUDA launcher
  * kernels/cuda/matmul_q.go:44-91) and, since it serves every M, the M >= 8
  * dequant + cuBLAS fallback (ops/matmul_q.go:52-59, 85-95). */
 int hq_matmul_q(const float *x, const void *w, float *out, int64_t M, int64_t N, int64_t K, int w_dtype,
                 void *ws, size_t ws_bytes, hq_stream_t stream);
 
-/* Prepared activations: hq_matmul_q = hq_quantize_act + hq_matmul_q_act.
+/* Gated MLP projection (the SwiGLU / GeGLU decode step):
+ *   out (M, N) F32 = act(x @ dequant(wg)^T) * (x @ dequant(wu)^T),
+ * act HQ_ACT_SILU (x / (1 + exp(-x))) or HQ_ACT_GELU_ERF (0.5 x (1 + erf(x / sqrt 2))).
+ * Same x / weight / workspace rules as hq_matmul_q; wg and wu share dtype and shape.
+ * For Q4_K with M <= 8 one kernel reads both weights (x quantized in LDS, no workspace
+ * used); other cases run the two matmuls and an elementwise epilogue.
+ * Light computes this as MatMulQ, MatMulQ, SiLU / GeluErf and Mul (models/llama.go:1306-1328;
+ * kernels/cpu/unary.go:216-222); its fused dense counterpart is ops.GatedLinear
+ * (ops/gemv.go:80-130).  No quantized counterpart in Light. */
+enum { HQ_ACT_SILU = 0, HQ_ACT_GELU_ERF = 1 };
+size_t hq_matmul_q_gated_ws_bytes(int64_t M, int64_t N, int64_t K, int w_dtype);
+int hq_matmul_q_gated(const float *x, const void *wg, const void *wu, float *out, int64_t M, int64_t N, int64_t K,
+                      int w_dtype, int act, void *ws, size_t ws_bytes, hq_stream_t stream);
+
+/* The gated MLP block of a decoder layer:
+ *   out (M, H) F32 = (act(x @ dequant(wg)^T) * (x @ dequant(wu)^T)) @ dequant(wd)^T
+ * with x (M, H) F32, wg and wu (I, H), wd (H, I), all of w_dtype; act as above.
+ * For Q4_K with M <= 8 this is two launches: the gated gate/up GEMV, which writes its
+ * output already quantized for the next matmul into ws, and the down GEMV on it.  Other
+ * cases run hq_matmul_q_gated into ws and then hq_matmul_q.
+ * Light: models/llama.go:1306-1333 (GatedLinear or MatMulQ/SiLU/Mul, then DownProj).
+ * No counterpart op in Light. */
+size_t hq_mlp_q_ws_bytes(int64_t M, int64_t H, int64_t I, int w_dtype);
+int hq_mlp_q(const float *x, const void *wg, const void *wu, const void *wd, float *out, int64_t M, int64_t H,
+             int64_t I, int w_dtype, int act, void *ws, size_t ws_bytes, hq_stream_t stream);
+
+/* Prepared activations: hq_matmul_q = hq_quantize_act + hq_matmul_q_act (bit for bit
+ * for Q8_0 / Q6_K; the Q4_K GEMV quantizes x inside its own workgroups with
+ * reciprocal-based scales, so there the two agree to the activation rounding).
  * A caller that multiplies one activation by several weights (the SwiGLU gate
  * and up projections, models/llama.go:1306-1328) quantizes once and reuses it.
  * No counterpart in Light.  The act buffer (hq_act_bytes(M, K) bytes, 16-byte

@@ -223,6 +223,64 @@ int hq_matmul_q(const float *x, const void *w, float *out, int64_t M, int64_t N,
   return launch_matmul_q(x, w, out, M, N, K, w_dtype, ws, s);
 }
 
+size_t hq_matmul_q_gated_ws_bytes(int64_t M, int64_t N, int64_t K, int w_dtype) {
+  return matmul_q_gated_ws_bytes(M, N, K, w_dtype);
+}
+
+int hq_matmul_q_gated(const float *x, const void *wg, const void *wu, float *out, int64_t M, int64_t N, int64_t K,
+                      int w_dtype, int act, void *ws, size_t ws_bytes, hq_stream_t stream) {
+  const char *call = "hq_matmul_q_gated";
+  if (!is_gguf(w_dtype)) return fail(HQ_EUNSUPPORTED, call, "weight dtype %d has no fused kernel", w_dtype);
+  if (act != HQ_ACT_SILU && act != HQ_ACT_GELU_ERF) return fail(HQ_EINVAL, call, "activation %d", act);
+  if (M < 0 || N < 0 || K <= 0) return fail(HQ_EINVAL, call, "bad shape M=%lld N=%lld K=%lld", (long long)M,
+                                            (long long)N, (long long)K);
+  BlockInfo bi = block_info(w_dtype);
+  if (K % bi.elems)
+    return fail(HQ_EINVAL, call, "K=%lld not a multiple of block size %d", (long long)K, bi.elems);
+  if (M == 0 || N == 0) return HQ_OK;
+  if (!x || !wg || !wu || !out) return fail(HQ_EINVAL, call, "NULL pointer");
+  if (((uintptr_t)x & 15) || ((uintptr_t)wg & 15) || ((uintptr_t)wu & 15) || ((uintptr_t)out & 3))
+    return fail(HQ_EINVAL, call, "x, wg and wu must be 16-byte aligned, out 4-byte aligned");
+  hipStream_t s = resolve(stream);
+  size_t need = matmul_q_gated_ws_bytes(M, N, K, w_dtype);
+  if (!ws) {
+    if (int rc = workspace(need, s, &ws, call)) return rc;
+  } else if (ws_bytes < need) {
+    return fail(HQ_ENOMEM, call, "workspace %zu bytes < %zu needed", ws_bytes, need);
+  }
+  TraceSpan span("matmul_q_gated", s);
+  return launch_matmul_q_gated(x, wg, wu, out, M, N, K, w_dtype, act, ws, s);
+}
+
+size_t hq_mlp_q_ws_bytes(int64_t M, int64_t H, int64_t I, int w_dtype) { return mlp_q_ws_bytes(M, H, I, w_dtype); }
+
+int hq_mlp_q(const float *x, const void *wg, const void *wu, const void *wd, float *out, int64_t M, int64_t H,
+             int64_t I, int w_dtype, int act, void *ws, size_t ws_bytes, hq_stream_t stream) {
+  const char *call = "hq_mlp_q";
+  if (!is_gguf(w_dtype)) return fail(HQ_EUNSUPPORTED, call, "weight dtype %d has no fused kernel", w_dtype);
+  if (act != HQ_ACT_SILU && act != HQ_ACT_GELU_ERF) return fail(HQ_EINVAL, call, "activation %d", act);
+  if (M < 0 || H <= 0 || I <= 0)
+    return fail(HQ_EINVAL, call, "bad shape M=%lld H=%lld I=%lld", (long long)M, (long long)H, (long long)I);
+  BlockInfo bi = block_info(w_dtype);
+  if (H % bi.elems || I % bi.elems)
+    return fail(HQ_EINVAL, call, "H=%lld, I=%lld not multiples of block size %d", (long long)H, (long long)I,
+                bi.elems);
+  if (M == 0) return HQ_OK;
+  if (!x || !wg || !wu || !wd || !out) return fail(HQ_EINVAL, call, "NULL pointer");
+  if (((uintptr_t)x & 15) || ((uintptr_t)wg & 15) || ((uintptr_t)wu & 15) || ((uintptr_t)wd & 15) ||
+      ((uintptr_t)out & 3))
+    return fail(HQ_EINVAL, call, "x and the weights must be 16-byte aligned, out 4-byte aligned");
+  hipStream_t s = resolve(stream);
+  size_t need = mlp_q_ws_bytes(M, H, I, w_dtype);
+  if (!ws) {
+    if (int rc = workspace(need, s, &ws, call)) return rc;
+  } else if (ws_bytes < need) {
+    return fail(HQ_ENOMEM, call, "workspace %zu bytes < %zu needed", ws_bytes, need);
+  }
+  TraceSpan span("mlp_q", s);
+  return launch_mlp_q(x, wg, wu, wd, out, M, H, I, w_dtype, act, ws, s);
+}
+
 size_t hq_act_bytes(int64_t M, int64_t K) {
   if (M <= 0 || K <= 0 || K % 32) return 0;
   return (size_t)act_bytes(M, K);

@@ -23,6 +23,7 @@
 //    read their blocks back with aligned dword reads re-aligned by v_alignbit.
 //  * Other shapes take a generic wave-per-row kernel on F32 activations built on
 //    the bit-exact decoder of dequant.hip.
+#include "actq.hpp"
 #include "decode.hpp"
 #include "internal.hpp"
 
@@ -187,10 +188,7 @@ __global__ __launch_bounds__(512) void gemv_q4k_kernel(Q4kArgs a) {
           dotA2 = dot4((int)lo[k], ya[mm][k], dotA2);
           dotB2 = dot4((int)hi[k], yb[mm][k], dotB2);
         }
-        const float v = scA * (de[mm].x * (float)dotA + de[mm].y * (float)dotA2) +
-                        scB * (de[mm].z * (float)dotB + de[mm].w * (float)dotB2);
-        const float mn = mnA * ss[mm].x + mnB * ss[mm].y;
-        const float s = row16_sum(d * v - dmin * mn);
+        const float s = row16_sum(q4k_pair(d, dmin, scA, scB, mnA, mnB, de[mm], ss[mm], dotA, dotA2, dotB, dotB2));
         if ((lane & 15) == 0) part[((r * RW + team) * MM + mm) * hpt + (u >> 4)] = s;
       }
     }
@@ -330,10 +328,7 @@ __global__ __launch_bounds__(512) void moe_gemv_q4k_kernel(MoeQ4kArgs ma) {
             dA2 = dot4((int)lo[k], ya[mm][k], dA2);
             dB2 = dot4((int)hi[k], yb[mm][k], dB2);
           }
-          const float v = scA * (de[mm].x * (float)dA1 + de[mm].y * (float)dA2) +
-                          scB * (de[mm].z * (float)dB1 + de[mm].w * (float)dB2);
-          const float mn = mnA * ss[mm].x + mnB * ss[mm].y;
-          const float s = row16_sum(d * v - dmin * mn);
+          const float s = row16_sum(q4k_pair(d, dmin, scA, scB, mnA, mnB, de[mm], ss[mm], dA1, dA2, dB1, dB2));
           if ((lane & 15) == 0) part[((r * RW + team) * MM + mm) * hpt + (u >> 4)] = s;
         }
       }
@@ -741,6 +736,7 @@ int launch_gemv_act(const void *act, const void *wv, float *out, int64_t M, int6
   auto *w = static_cast<const uint8_t *>(wv);
   auto *xa = static_cast<const uint8_t *>(act);
   const int MMc = M >= 3 ? 4 : (int)M;
+  if (dt == Q4_K && q4kx_ok(M, N, K, w, nullptr, act)) return launch_gemv_q4kx_act(act, w, out, M, N, K, s);
   if (dt == Q4_K) {
     Q4kArgs a;
     a.act = xa;
@@ -837,6 +833,8 @@ int launch_matmul_act(const void *act, const void *w, float *out, int64_t M, int
 int launch_matmul_q(const float *x, const void *w, float *out, int64_t M, int64_t N, int64_t K, int dt, void *ws,
                     hipStream_t s) {
   if (use_gemm(M, dt)) return run_gemm(x, false, w, out, M, N, K, ws, s);
+  if (dt == Q4_K && q4kx_ok(M, N, K, w, nullptr, x) && !getenv("HQ_Q4K_SPLIT_QUANT"))
+    return launch_gemv_q4kx(x, w, nullptr, out, M, N, K, 0, s);
   if (!gemv_fast_ok(dt, K, w)) return launch_gemv_generic(x, w, out, M, N, K, dt, s);
   if (int rc = launch_quantize_act(x, F32, ws, M, K, s)) return rc;
   return launch_gemv_act(ws, w, out, M, N, K, dt, s);

@@ -61,6 +61,20 @@ size_t gemm_partial_bytes(int64_t M, int64_t N, int64_t K, bool f32_out);
 int launch_gemm_int4_bf16(const uint16_t *xb, const uint32_t *codes, const float *sc, const float *zr, void *out,
                           int out_dtype, float *partials, int64_t M, int64_t N, int64_t K, int G, hipStream_t s);
 int device_cus();
+// Q4_K GEMV on F32 x quantized in LDS (M <= kGemvMaxRows); w1 != NULL: gated pair,
+// out = act(x.w0) * (x.w1), act 0 = SiLU, 1 = GELU (erf).
+// x: F32 x or prepared activations (16-byte aligned); w1 may be NULL.
+bool q4kx_ok(int64_t M, int64_t N, int64_t K, const void *w0, const void *w1, const void *x);
+int launch_gemv_q4kx(const float *x, const void *w0, const void *w1, float *out, int64_t M, int64_t N, int64_t K,
+                     int act, hipStream_t s);
+int launch_gemv_q4kx_act(const void *act_in, const void *w, float *out, int64_t M, int64_t N, int64_t K,
+                         hipStream_t s);
+size_t matmul_q_gated_ws_bytes(int64_t M, int64_t N, int64_t K, int dt);
+size_t mlp_q_ws_bytes(int64_t M, int64_t H, int64_t I, int dt);
+int launch_mlp_q(const float *x, const void *wg, const void *wu, const void *wd, float *out, int64_t M, int64_t H,
+                 int64_t I, int dt, int act, void *ws, hipStream_t s);
+int launch_matmul_q_gated(const float *x, const void *wg, const void *wu, float *out, int64_t M, int64_t N, int64_t K,
+                          int dt, int act, void *ws, hipStream_t s);
 int launch_int4_dequant(const uint32_t *codes, const float *s, const float *z, void *out, int out_dtype,
                         int64_t N, int64_t K, int G, int64_t off, hipStream_t st);
 int launch_int4_matmul(const void *x, int x_dtype, const uint32_t *codes, const float *s, const float *z, void *y,

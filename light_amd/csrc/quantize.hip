@@ -3,9 +3,9 @@
 // Block of 32 -> [f16 d][f16 s][i8 q[32]] (quant/q8_1.go:10-18).  Rounding follows
 // Light's encodeQ8_0 (quant/quantize.go:70-86): d = amax / 127 (f32), id = 1 / d
 // from the unrounded d, q = RoundToEven(v * id); s = f16(f32(sum q) * d).
-// Eight lanes own one block (four elements each); amax and sum q are reduced
-// with xor shuffles inside the 8-lane group.  All arithmetic is explicitly
-// rounded (__fdiv_rn / __fmul_rn) so the bytes match the CPU quantizer.
+// Eight lanes own one block (four elements each; act_quant8 in actq.hpp); all
+// arithmetic is explicitly rounded so the bytes match the CPU quantizer.
+#include "actq.hpp"
 #include "internal.hpp"
 
 namespace hq {
@@ -33,49 +33,20 @@ __global__ __launch_bounds__(256) void quantize_q8_1_kernel(const void *__restri
   bool live = blk < nblocks;
   float v[4] = {0.f, 0.f, 0.f, 0.f};
   if (live) load4<XDT>(x, blk * 32 + sub * 4, v);
-  float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-#pragma unroll
-  for (int o = 4; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 8));
-  float d = __fdiv_rn(amax, 127.0f);
-  float id = d != 0.f ? __fdiv_rn(1.0f, d) : 0.f;
-  int q[4], sum = 0;
-#pragma unroll
-  for (int j = 0; j < 4; j++) {
-    q[j] = (int)rintf(__fmul_rn(v[j], id));
-    sum += q[j];
-  }
-#pragma unroll
-  for (int o = 4; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 8);
-  uint32_t packed = (uint32_t)(q[0] & 0xff) | (uint32_t)(q[1] & 0xff) << 8 | (uint32_t)(q[2] & 0xff) << 16 |
-                    (uint32_t)(q[3] & 0xff) << 24;
+  const ActQ q = act_quant8(v);
+  if (!live) return;
   if constexpr (ACT) {
-    // Residual level: r = x - d*q1, e = d / 254, q2 = RoundToEven(r / e) (|q2| <= 127).
-    const float e = __fdiv_rn(d, 254.0f);
-    const float ie = e != 0.f ? __fdiv_rn(1.0f, e) : 0.f;
-    uint32_t packed2 = 0;
-    float bsum = (v[0] + v[1]) + (v[2] + v[3]);
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const float r = __fsub_rn(v[j], __fmul_rn(d, (float)q[j]));
-      int q2 = (int)rintf(__fmul_rn(r, ie));
-      q2 = q2 > 127 ? 127 : (q2 < -127 ? -127 : q2);
-      packed2 |= (uint32_t)(q2 & 0xff) << (8 * j);
-    }
-#pragma unroll
-    for (int o = 1; o < 8; o <<= 1) bsum += __shfl_xor(bsum, o, 8);
-    if (!live) return;
-    reinterpret_cast<uint32_t *>(dst + blk * 32)[sub] = packed;
-    reinterpret_cast<uint32_t *>(dst + q2_off + blk * 32)[sub] = packed2;
+    reinterpret_cast<uint32_t *>(dst + blk * 32)[sub] = q.q1;
+    reinterpret_cast<uint32_t *>(dst + q2_off + blk * 32)[sub] = q.q2;
     if (sub == 0) {
-      reinterpret_cast<float2 *>(dst + d_off)[blk] = make_float2(d, e);
-      reinterpret_cast<float *>(dst + s_off)[blk] = bsum;
+      reinterpret_cast<float2 *>(dst + d_off)[blk] = make_float2(q.d, q.e);
+      reinterpret_cast<float *>(dst + s_off)[blk] = q.sum;
     }
   } else {
-    if (!live) return;
     uint8_t *o = dst + blk * 36;
-    reinterpret_cast<uint32_t *>(o + 4)[sub] = packed;
+    reinterpret_cast<uint32_t *>(o + 4)[sub] = q.q1;
     if (sub == 0) {
-      uint32_t ds = (uint32_t)f2h_rne(d) | (uint32_t)f2h_rne(__fmul_rn((float)sum, d)) << 16;
+      uint32_t ds = (uint32_t)f2h_rne(q.d) | (uint32_t)f2h_rne(__fmul_rn((float)q.qsum, q.d)) << 16;
       *reinterpret_cast<uint32_t *>(o) = ds;
     }
   }

@@ -53,6 +53,10 @@ SIGNATURES = {
     "hq_trace_stop": (_I, [ctypes.c_char_p, ctypes.POINTER(_I), ctypes.POINTER(ctypes.c_double), _I]),
     "hq_matmul_q_ws_bytes": (_SZ, [_I64, _I64, _I64, _I]),
     "hq_matmul_q": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _P, _SZ, _P]),
+    "hq_matmul_q_gated_ws_bytes": (_SZ, [_I64, _I64, _I64, _I]),
+    "hq_matmul_q_gated": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _P, _SZ, _P]),
+    "hq_mlp_q_ws_bytes": (_SZ, [_I64, _I64, _I64, _I]),
+    "hq_mlp_q": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _P, _SZ, _P]),
     "hq_act_bytes": (_SZ, [_I64, _I64]),
     "hq_quantize_act": (_I, [_P, _I, _P, _I64, _I64, _P]),
     "hq_matmul_q_act_ws_bytes": (_SZ, [_I64, _I64, _I64, _I]),
@@ -133,6 +137,37 @@ def matmul_q(x, w, N, K, w_dtype, out=None, ws=None, stream=None):
     return out
 
 
+ACT_SILU, ACT_GELU_ERF = 0, 1
+
+
+def matmul_q_gated(x, wg, wu, N, K, w_dtype, act=ACT_SILU, out=None, ws=None, stream=None):
+    """out (M, N) f32 = act(x @ dequant(wg)^T) * (x @ dequant(wu)^T)."""
+    import torch
+    M = x.shape[0]
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float32, device=x.device)
+    ws_bytes = 0 if ws is None else ws.numel() * ws.element_size()
+    check(lib().hq_matmul_q_gated(_ptr(x), _ptr(wg), _ptr(wu), _ptr(out), M, N, K, w_dtype, act, _ptr(ws),
+                                  ws_bytes, _stream(stream)))
+    return out
+
+
+def mlp_q(x, wg, wu, wd, H, I, w_dtype, act=ACT_SILU, out=None, ws=None, stream=None):
+    """out (M, H) f32 = (act(x @ wg^T) * (x @ wu^T)) @ wd^T for GGUF weights wg, wu (I, H), wd (H, I)."""
+    import torch
+    M = x.shape[0]
+    if out is None:
+        out = torch.empty((M, H), dtype=torch.float32, device=x.device)
+    ws_bytes = 0 if ws is None else ws.numel() * ws.element_size()
+    check(lib().hq_mlp_q(_ptr(x), _ptr(wg), _ptr(wu), _ptr(wd), _ptr(out), M, H, I, w_dtype, act, _ptr(ws),
+                         ws_bytes, _stream(stream)))
+    return out
+
+
+def mlp_q_ws_bytes(M, H, I, w_dtype):
+    return lib().hq_mlp_q_ws_bytes(M, H, I, w_dtype)
+
+
 def quantize_act(x, out=None, stream=None):
     """Prepared activations of x (M, K) (planar q8_1) for matmul_q_act."""
     import torch
@@ -156,6 +191,10 @@ def matmul_q_act(act, w, M, N, K, w_dtype, out=None, ws=None, stream=None):
 
 def matmul_q_ws_bytes(M, N, K, w_dtype):
     return lib().hq_matmul_q_ws_bytes(M, N, K, w_dtype)
+
+
+def matmul_q_gated_ws_bytes(M, N, K, w_dtype):
+    return lib().hq_matmul_q_gated_ws_bytes(M, N, K, w_dtype)
 
 
 def dequant(src, n, src_dtype, out_dtype=F32, out=None, stream=None):

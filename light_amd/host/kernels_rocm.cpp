@@ -16,6 +16,13 @@ void matmul_q(Context &c) {
                     w.Dim(0), x.Dim(1), (int)w.dtype(), nullptr, 0, nullptr));
 }
 
+void matmul_q_gated(Context &c) {
+  const Tensor &x = c.in(0), &wg = c.in(1), &wu = c.in(2);
+  Check(hq_matmul_q_gated(static_cast<const float *>(x.data()), wg.data(), wu.data(),
+                          static_cast<float *>(c.output.data()), x.Dim(0), wg.Dim(0), x.Dim(1), (int)wg.dtype(),
+                          c.attr("gelu") ? HQ_ACT_GELU_ERF : HQ_ACT_SILU, nullptr, 0, nullptr));
+}
+
 void int4_gemv(Context &c) {
   const Tensor &x = c.in(0), &codes = c.in(1), &s = c.in(2), &z = c.in(3);
   Check(hq_int4_matmul(x.data(), (int)x.dtype(), static_cast<const uint32_t *>(codes.data()),
@@ -51,6 +58,7 @@ struct Registrar {
   Registrar() {
     for (DType dt : kGGUF) {
       Register(Key{"matmul_q", DeviceKind::ROCm, dt}, matmul_q);
+      Register(Key{"matmul_q_gated", DeviceKind::ROCm, dt}, matmul_q_gated);
       Register(Key{"moe_gemm_q", DeviceKind::ROCm, dt}, moe_gemm_q);
       Register(Key{"dequant", DeviceKind::ROCm, dt}, dequant);
     }

@@ -37,6 +37,29 @@ Tensor MatMulQ(const Tensor &x, const Tensor &w) {
   return out;
 }
 
+Tensor MatMulQGated(const Tensor &x, const Tensor &wg, const Tensor &wu, bool gelu) {
+  if (x.Rank() != 2 || x.dtype() != DType::F32)
+    Fail("MatMulQGated: x must be (M, K) F32, got %s %s", DTypeName(x.dtype()), x.ShapeStr().c_str());
+  const int64_t M = x.Dim(0), K = x.Dim(1);
+  for (const Tensor *w : {&wg, &wu}) {
+    if (w->Rank() != 2 || w->Dim(1) != K || w->Dim(0) != wg.Dim(0) || w->dtype() != wg.dtype() ||
+        !IsQuantized(w->dtype()) || !same_device(*w, x))
+      Fail("MatMulQGated: weights must be (N, %lld) %s on %s, got %s / %s", (long long)K, DTypeName(wg.dtype()),
+           x.device().str().c_str(), wg.ShapeStr().c_str(), wu.ShapeStr().c_str());
+  }
+  if (K % BlockElems(wg.dtype()))
+    Fail("MatMulQGated: K=%lld not a multiple of %s block size %d", (long long)K, DTypeName(wg.dtype()),
+         BlockElems(wg.dtype()));
+  Kernel k = Lookup(Key{"matmul_q_gated", x.device().kind, wg.dtype()});
+  Tensor out = Tensor::Empty(DType::F32, {M, wg.Dim(0)}, x.device());
+  Context ctx;
+  ctx.inputs = {x, wg, wu};
+  ctx.output = out;
+  ctx.attrs = {{"gelu", Attr::Bool(gelu)}};
+  k(ctx);
+  return out;
+}
+
 bool MatMulQFusedOn(DeviceKind kind, DType dt) {
   try {
     Lookup(Key{"matmul_q", kind, dt});

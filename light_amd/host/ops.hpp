@@ -17,6 +17,10 @@ namespace ops {
 Tensor MatMulQ(const Tensor &x, const Tensor &w);
 // ops.MatMulQFusedOn (ops/matmul_q.go:102-106).
 bool MatMulQFusedOn(DeviceKind kind, DType dt);
+// Gated projection on quantized weights: act(x . wg^T) * (x . wu^T), act = SiLU or GELU (erf)
+// -- ops.GatedLinear's contract (ops/gemv.go:80-130: Inputs [x, wg, wu], Attrs {"gelu"}) for
+// GGUF weights and F32 x of any M, registry key "matmul_q_gated" keyed by the weight dtype.
+Tensor MatMulQGated(const Tensor &x, const Tensor &wg, const Tensor &wu, bool gelu);
 
 // quant.Int4 (quant/int4.go:11-34): Codes U32 (N, K/8), Scales / Zeros F32 (N, K/G), Group,
 // Perm I64 (K,) for act-order checkpoints.

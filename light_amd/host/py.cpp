@@ -146,6 +146,7 @@ PYBIND11_MODULE(_light, m) {
 
   // ops
   m.def("matmul_q", &ops::MatMulQ);
+  m.def("matmul_q_gated", &ops::MatMulQGated, py::arg("x"), py::arg("wg"), py::arg("wu"), py::arg("gelu") = false);
   m.def("matmul_q_fused_on", [](const std::string &kind, const std::string &dt) {
     return ops::MatMulQFusedOn(parse_kind(kind), parse_dtype(dt));
   });

@@ -23,6 +23,8 @@ Parity status of each function (how it is pinned):
   (ops/matmul_q_cpu_test.go:66-76).
 * ``moe_gemm_q`` / ``moe_route_from_ids`` / ``moe_combine``: Light's routing
   invariants (ops/moe_test.go:63-88) and a per-expert loop in f64.
+* ``gated``: SiLU against x * sigmoid(x) in f64 and GELU against scipy's erf
+  (closed forms), at special points (0, large |x|) and on random data.
 * ``quantize_q8_1``: specification only (Light has no q8_1 encoder): layout,
   |q| <= 127, round trip within d/2, all-zero block, and the q8_0 encoder
   (same rounding rule) on the same data.
@@ -84,6 +86,7 @@ def _declare(L):
         "or_moe_gemm_f32": (I, [P, P, P, P, P, P, I64, I64, I64, I64, I, I, I]),
         "or_moe_gemm_q": (I, [P, P, I, P, P, P, P, I64, I64, I64, I64, I64, I, I, I, P]),
         "or_moe_combine": (None, [P, P, I64, I64, I]),
+        "or_gated": (None, [P, P, P, I64, I]),
         "or_quantize_q8_0": (None, [P, I64, P]),
         "or_quantize_q8_1": (None, [P, I64, P]),
         "or_matmul_f64": (None, [P, P, I64, I64, I64, P, P, P, P, I]),
@@ -246,6 +249,15 @@ def moe_combine(pair_out, topk):
     M, N = pair_out.shape
     out = np.zeros((M // topk, N), np.float32)
     lib().or_moe_combine(_p(pair_out), _p(out), M, N, topk)
+    return out
+
+
+def gated(g, u, act=0):
+    """Light's unfused gated tail: SiLU (act 0) or GeluErf (act 1) of g, times u, in f32."""
+    g = _c(g, np.float32)
+    u = _c(u, np.float32)
+    out = np.empty_like(g)
+    lib().or_gated(_p(g), _p(u), _p(out), g.size, act)
     return out
 
 

@@ -611,6 +611,20 @@ void or_moe_combine(const float *pair_out, float *out, int64_t M, int64_t N, int
     }
 }
 
+/* The unfused gated MLP tail: SiLU (kernels/cpu/unary.go:219-222, f32: a / (1 + f32(exp(f64(-a)))))
+ * or GeluErf (:216, :263-265, f64 0.5 x (1 + erf(x / sqrt 2)) rounded to f32), then Mul (f32). */
+void or_gated(const float *g, const float *u, float *out, int64_t n, int act) {
+  for (int64_t i = 0; i < n; i++) {
+    const float a = g[i];
+    float h;
+    if (act == 1)
+      h = (float)(0.5 * (double)a * (1.0 + erf((double)a / sqrt(2.0))));
+    else
+      h = a / (1.0f + (float)exp(-(double)a));
+    out[i] = h * u[i];
+  }
+}
+
 /* ------------------------------------------------------------------ */
 /* Quantizers                                                          */
 /* ------------------------------------------------------------------ */

@@ -76,6 +76,8 @@ int or_moe_gemm_q(const float *x, const uint8_t *w, int dt, const int64_t *pairs
                   int64_t K, int topk, int row_per_pair, int threads, float *w_scratch);
 /* MoECombine (ops/moe.go:209-240): sum the topk slot rows in slot order. */
 void or_moe_combine(const float *pair_out, float *out, int64_t M, int64_t N, int topk);
+/* SiLU (act 0) or GeluErf (act 1) of g, times u (kernels/cpu/unary.go:216-222; Mul). */
+void or_gated(const float *g, const float *u, float *out, int64_t n, int act);
 
 /* Activation quantizers. */
 void or_quantize_q8_0(const float *x, int64_t n, uint8_t *dst);  /* encodeQ8_0, quant/quantize.go:70-86 */

@@ -103,3 +103,22 @@ def test_moe_pipeline(dt, T, E, topk):
     out = L.moe_combine(pair_out, topk)
     assert out.shape == [T, N]
     assert np.array_equal(out.numpy().view(np.uint32), oracle.moe_combine(po, topk).view(np.uint32))
+
+
+@pytest.mark.parametrize("gelu", [False, True])
+def test_matmul_q_gated(gelu):
+    g = synth.rng(600 + gelu)
+    N, K = 300, 2048
+    wg = synth.gguf_weight(hipq.Q4_K, N, K, g)
+    wu = synth.gguf_weight(hipq.Q4_K, N, K, g)
+    x = synth.activations(2, K, g)
+    got = L.matmul_q_gated(dev_t(x, "F32", (2, K)), dev_t(wg, "Q4_K", (N, K)), dev_t(wu, "Q4_K", (N, K)), gelu).numpy()
+    gr = oracle.matmul_q(x, wg, N, K, hipq.Q4_K)
+    ur = oracle.matmul_q(x, wu, N, K, hipq.Q4_K)
+    want = oracle.gated(gr, ur, int(gelu))
+    xn = np.linalg.norm(x.astype(np.float64), axis=1)[:, None]
+    ng = np.linalg.norm(oracle.dequant(hipq.Q4_K, wg, N * K).reshape(N, K).astype(np.float64), axis=1)[None, :]
+    nu = np.linalg.norm(oracle.dequant(hipq.Q4_K, wu, N * K).reshape(N, K).astype(np.float64), axis=1)[None, :]
+    hg = oracle.gated(gr, np.ones_like(gr), int(gelu)).astype(np.float64)
+    bound = TOL * (1.13 * np.abs(ur) * ng * xn + np.abs(hg) * nu * xn) + 1e-30
+    assert np.max(np.abs(got - want) / bound) <= 1.0

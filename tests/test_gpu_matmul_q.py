@@ -24,11 +24,12 @@ def _t(a, dev):
     return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
 
 
-def _check_matmul(dev, dt, x, w, N, K, label):
+def _check_matmul(dev, dt, x, w, N, K, label, got=None):
     print(f"[case] matmul_q {label} dt={hipq.NAMES[dt]} M={x.shape[0]} N={N} K={K}", flush=True)
-    y = hipq.matmul_q(_t(x, dev), _t(w, dev), N, K, dt)
-    torch.cuda.synchronize()
-    got = y.cpu().numpy()
+    if got is None:
+        y = hipq.matmul_q(_t(x, dev), _t(w, dev), N, K, dt)
+        torch.cuda.synchronize()
+        got = y.cpu().numpy()
     cpu = oracle.matmul_q(x, w, N, K, dt)
     wd = oracle.dequant(dt, w, N * K).reshape(N, K)
     ref, _, wn, xn = oracle.matmul_f64(x, wd)
@@ -205,8 +206,15 @@ def test_matmul_q_act_equals_matmul_q(dev, dt, M):
     act = hipq.quantize_act(x)
     y2 = hipq.matmul_q_act(act, w, M, N, K, dt)
     torch.cuda.synchronize()
-    assert torch.equal(y1, y2)
+    if dt != hipq.Q4_K:
+        assert torch.equal(y1, y2)
+    else:
+        # The Q4_K GEMV quantizes x inside its workgroups (reciprocal-based scales): the two
+        # paths agree to the activation quantization's own error, far inside the bar.
+        ref = torch.from_numpy(oracle.matmul_q(x.cpu().numpy(), w.cpu().numpy(), N, K, dt)).to(dev)
+        assert ((y1 - y2).abs().max() <= 1e-4 * ref.abs().max()).item()
     _check_matmul(dev, dt, x.cpu().numpy(), w.cpu().numpy(), N, K, "act")
+    _check_matmul(dev, dt, x.cpu().numpy(), w.cpu().numpy(), N, K, "act", got=y2.cpu().numpy())
 
 
 # ---- Q4_K prefill GEMM (MFMA) ----------------------------------------------

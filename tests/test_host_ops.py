@@ -28,7 +28,7 @@ GGUF = ["Q8_0", "Q4_K", "Q6_K"]
 def test_registered_rocm_keys():
     keys = set(L.registered())
     for dt in GGUF:
-        for op in ("matmul_q", "moe_gemm_q", "dequant"):
+        for op in ("matmul_q", "matmul_q_gated", "moe_gemm_q", "dequant"):
             assert f"{op}/ROCm/{dt}" in keys
     for dt in ("F32", "BF16", "F16"):
         assert f"int4_gemv/ROCm/{dt}" in keys
@@ -138,3 +138,13 @@ def test_moe_combine_and_dequantize_validation():
         L.dequantize(f32(4))
     with pytest.raises(L.KernelNotFound, match="dequant/CPU/Q6_K"):
         L.dequantize(q("Q6_K", 1, 256))
+
+
+def test_matmul_q_gated_validation():
+    x, w = f32(1, 256), q("Q4_K", 8, 256)
+    with pytest.raises(L.Error, match=r"MatMulQGated: x must be \(M, K\) F32"):
+        L.matmul_q_gated(f32(256), w, w)
+    with pytest.raises(L.Error, match=r"MatMulQGated: weights must be \(N, 256\) Q4_K on CPU"):
+        L.matmul_q_gated(x, w, q("Q4_K", 16, 256))
+    with pytest.raises(L.KernelNotFound, match="matmul_q_gated/CPU/Q4_K"):
+        L.matmul_q_gated(x, w, w)

@@ -318,3 +318,20 @@ def test_quantize_q8_1_spec():
     exact = q.sum(1).astype(np.float64) * dd
     assert np.all(np.abs(s - exact) <= np.abs(exact) * 2.0 ** -11 + 2.0 ** -25)
     assert np.all(np.abs(d - dd) <= dd * 2.0 ** -11 + 2.0 ** -25)
+
+
+def test_gated_tail_closed_forms():
+    """or_gated: SiLU = x * sigmoid(x) and GELU = 0.5 x (1 + erf(x / sqrt 2)) (f64 closed forms)."""
+    from scipy.special import erf
+    g = np.concatenate([np.array([0.0, -0.0, 1e-30, 30.0, -30.0, 88.0, -88.0], np.float32),
+                        (np.random.default_rng(5).standard_normal(4096) * 4).astype(np.float32)])
+    u = np.random.default_rng(6).standard_normal(g.size).astype(np.float32)
+    g64, u64 = g.astype(np.float64), u.astype(np.float64)
+    silu = oracle.gated(g, u, 0)
+    want = g64 / (1.0 + np.exp(-g64)) * u64
+    assert np.allclose(silu, want, rtol=2e-6, atol=1e-30)
+    gelu = oracle.gated(g, u, 1)
+    want = 0.5 * g64 * (1.0 + erf(g64 / np.sqrt(2.0))) * u64
+    assert np.allclose(gelu, want, rtol=2e-6, atol=1e-30)
+    assert silu[0] == 0.0 and gelu[0] == 0.0
+    assert abs(silu[4]) < 1e-10 and gelu[4] == 0.0  # x = -30: SiLU ~ -2.8e-12 * u, GELU underflows to 0
