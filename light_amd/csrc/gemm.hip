@@ -30,6 +30,8 @@
 //    also converts to the output dtype.
 #include "internal.hpp"
 
+#include <algorithm>
+
 namespace hq {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -367,6 +369,16 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restr
     static_cast<uint16_t *>(out)[i] = f2h_rne(s);
 }
 
+int launch_splitk_reduce(const float *part, void *out, int out_dtype, int64_t n, int splits, hipStream_t s) {
+  dim3 rg((unsigned)cdiv(n, 256));
+  switch (out_dtype) {
+    case F32: splitk_reduce_kernel<F32><<<rg, 256, 0, s>>>(part, out, n, splits); break;
+    case BF16: splitk_reduce_kernel<BF16><<<rg, 256, 0, s>>>(part, out, n, splits); break;
+    default: splitk_reduce_kernel<F16><<<rg, 256, 0, s>>>(part, out, n, splits); break;
+  }
+  return check_launch("splitk_reduce");
+}
+
 // x (F32 or F16) -> bf16 (RNE).
 template <int XDT>
 __global__ __launch_bounds__(256) void to_bf16_kernel(const void *__restrict__ x, uint16_t *__restrict__ y,
@@ -413,10 +425,18 @@ int gemm_splits(int64_t M, int64_t N, int64_t K) {
 
 size_t gemm_x_bytes(int64_t M, int64_t K) { return ((size_t)M * (size_t)K * 2 + 255) & ~(size_t)255; }
 
+size_t gemm_ws_partial_bytes(int64_t M, int64_t N, int64_t K, bool f32_out);
+
 size_t gemm_partial_bytes(int64_t M, int64_t N, int64_t K, bool f32_out) {
   int s = gemm_splits(M, N, K);
-  return (s > 1 || !f32_out) ? (size_t)s * (size_t)M * (size_t)N * 4 : 0;
+  const size_t old = (s > 1 || !f32_out) ? (size_t)s * (size_t)M * (size_t)N * 4 : 0;
+  return std::max(old, gemm_ws_partial_bytes(M, N, K, f32_out));
 }
+
+int launch_gemm_ws_q4k(const uint16_t *xb, const void *w, float *out, float *partials, int64_t M, int64_t N,
+                       int64_t K, hipStream_t s);
+int launch_gemm_ws_int4(const uint16_t *xb, const uint32_t *codes, const float *sc, const float *zr, void *out,
+                        int out_dtype, float *partials, int64_t M, int64_t N, int64_t K, int G, hipStream_t s);
 
 template <class WP, int BM>
 static int launch_gemm_t(const GemmArgs &a0, int out_dtype, void *out, float *partials, hipStream_t s) {
@@ -461,6 +481,8 @@ static int launch_gemm_p(const GemmArgs &a, int out_dtype, void *out, float *par
 
 int launch_gemm_q4k_bf16(const uint16_t *xb, const void *w, float *out, float *partials, int64_t M, int64_t N,
                          int64_t K, hipStream_t s) {
+  // M > 64: the warp-specialised kernel (gemm_ws.hip); small M keeps the 64-row tile.
+  if (M > 64) return launch_gemm_ws_q4k(xb, w, out, partials, M, N, K, s);
   GemmArgs a = {};
   a.x = xb;
   a.w = static_cast<const uint8_t *>(w);
@@ -473,6 +495,7 @@ int launch_gemm_q4k_bf16(const uint16_t *xb, const void *w, float *out, float *p
 
 int launch_gemm_int4_bf16(const uint16_t *xb, const uint32_t *codes, const float *sc, const float *zr, void *out,
                           int out_dtype, float *partials, int64_t M, int64_t N, int64_t K, int G, hipStream_t s) {
+  if (M > 64) return launch_gemm_ws_int4(xb, codes, sc, zr, out, out_dtype, partials, M, N, K, G, s);
   GemmArgs a = {};
   a.x = xb;
   a.w = reinterpret_cast<const uint8_t *>(codes);

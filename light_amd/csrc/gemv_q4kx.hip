@@ -14,8 +14,8 @@
 //    + one header dword, broadcast in the block's 4-lane quad by DPP.  A team of TP lanes
 //    covers a row; a workgroup holds RW teams; each lane keeps its pair's activations in
 //    registers for the whole kernel.
-//  * Workgroups are persistent.  A ring of D register slots keeps D row groups of loads in
-//    flight; every load is unconditional (inactive lanes and rows past N read valid
+//  * Workgroups are persistent (two per CU).  A ring of D register slots (D = 1) keeps the
+//    next row group's loads in flight while the current one is reduced; every load is unconditional (inactive lanes and rows past N read valid
 //    addresses and their sums are dropped), so no load sits in a branch and the compiler's
 //    wait counts stay exact.
 //  * Team sums: DPP row sums, then v_readlane over the wave's four rows; teams wider than a
@@ -335,11 +335,6 @@ __global__ __launch_bounds__(512) void gemv_q4kx_kernel(Q4kxArgs a) {
 // Launch
 // ---------------------------------------------------------------------------
 
-static int env_int(const char *name, int dflt) {
-  const char *v = getenv(name);
-  return v && *v ? atoi(v) : dflt;
-}
-
 // Team geometry: P = K/64 lanes per row; TP = 16, 32 or 64 when P fits a wave, else a
 // multiple of 64 (up to 512); RW = teams per 512-lane workgroup.
 static bool q4kx_geom(int64_t K, int *P, int *TP, int *RW) {
@@ -387,8 +382,9 @@ static int run_q4kx(const Q4kxArgs &a, hipStream_t s) {
   }
   const int ngroups = (a.N + a.RW - 1) / a.RW;
   const int units = AOUT ? (ngroups + 32 / a.RW - 1) / (32 / a.RW) : ngroups;
-  const int per_cu = env_int("HQ_Q4KX_WG_PER_CU", 2);
-  const int cap = device_cus() * per_cu;
+  // Two persistent workgroups per CU, one row group in flight per wave: measured faster
+  // than deeper per-wave prefetch (more loads per wave) or more workgroups.
+  const int cap = device_cus() * 2;
   dim3 grid((unsigned)(units < cap ? units : cap), (unsigned)cdiv(a.M, MM));
   kern<<<grid, a.TP * a.RW, lds, s>>>(a);
   return check_launch(GATED ? "gemv_q4k_gated" : "gemv_q4kx");
@@ -397,10 +393,8 @@ static int run_q4kx(const Q4kxArgs &a, hipStream_t s) {
 template <bool GATED, bool XIN, bool AOUT>
 static int dispatch_q4kx(const Q4kxArgs &a, hipStream_t s) {
   const int MMc = mm_of(a.M);
-  if (MMc == 1)
-    return env_int("HQ_Q4KX_DEPTH", 1) == 1 ? run_q4kx<1, GATED, 1, XIN, AOUT>(a, s)
-                                            : run_q4kx<1, GATED, 2, XIN, AOUT>(a, s);
-  if (MMc == 2) return run_q4kx<2, GATED, 2, XIN, AOUT>(a, s);
+  if (MMc == 1) return run_q4kx<1, GATED, 1, XIN, AOUT>(a, s);
+  if (MMc == 2) return run_q4kx<2, GATED, 1, XIN, AOUT>(a, s);
   return run_q4kx<4, GATED, 1, XIN, AOUT>(a, s);
 }
 
