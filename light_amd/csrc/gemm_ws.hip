@@ -21,6 +21,7 @@
 //    lane l's 16 bytes at l*16, so its reads are contiguous.
 //  * One barrier per K step.  Workgroup -> tile mapping keeps the M tiles of a
 //    weight tile on one XCD (its L2 serves the second read of the weights).
+#include "dma.hpp"
 #include "internal.hpp"
 
 namespace hq {
@@ -56,26 +57,6 @@ __device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
   uint32_t u;
   __builtin_memcpy(&u, &v, 4);
   return u;
-}
-
-// 16 bytes from global memory to LDS at lds_base + lane * 16 (lds_base wave-uniform).
-__device__ __forceinline__ void dma16(const void *g, uint32_t lds_base) {
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_base) : "memory", "m0");
-#pragma clang diagnostic pop
-}
-// 4 bytes from global memory to LDS at lds_base + lane * 4.
-__device__ __forceinline__ void dma4(const void *g, uint32_t lds_base) {
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds_base) : "memory", "m0");
-#pragma clang diagnostic pop
-}
-
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
 }  // namespace

@@ -19,11 +19,13 @@
 //    reduced with DPP inside 16-lane rows and across the team in LDS.
 //    Workgroups are persistent and prefetch the next rows while computing.
 //  * Q8_0 (34 B) and Q6_K (210 B) blocks are only 2-byte aligned.  Each wave
-//    copies its rows' raw bytes into LDS with 16-byte loads and stores, and lanes
-//    read their blocks back with aligned dword reads re-aligned by v_alignbit.
+//    streams its rows' raw bytes into LDS with direct global->LDS loads (two slices,
+//    the next row group loading while the current one is computed), and lanes read
+//    their blocks back with aligned dword reads re-aligned by v_alignbit.
 //  * Other shapes take a generic wave-per-row kernel on F32 activations built on
 //    the bit-exact decoder of dequant.hip.
 #include "actq.hpp"
+#include "dma.hpp"
 #include "decode.hpp"
 #include "internal.hpp"
 
@@ -423,19 +425,17 @@ __device__ __forceinline__ void lds_unaligned(const uint8_t *lds, int o, uint32_
   for (int k = 0; k < NDW; k++) out[k] = __builtin_amdgcn_alignbit(w[k + 1], w[k], sh);
 }
 
-// Copy nseg 16-byte segments src -> lds; lanes take segments lane, lane + 64, ...
-// Loads are clamped to the last segment so every load is in bounds and unconditional.
-__device__ __forceinline__ void stage_rows(uint8_t *lds, const uint8_t *src, int nseg, int lane) {
-  const uint4 *s4 = reinterpret_cast<const uint4 *>(src);
-  uint4 *d4 = reinterpret_cast<uint4 *>(lds);
-  for (int s0 = lane; s0 < nseg; s0 += 256) {
-    const int i1 = s0 + 64 < nseg ? s0 + 64 : nseg - 1, i2 = s0 + 128 < nseg ? s0 + 128 : nseg - 1;
-    const int i3 = s0 + 192 < nseg ? s0 + 192 : nseg - 1;
-    const uint4 v0 = s4[s0], v1 = s4[i1], v2 = s4[i2], v3 = s4[i3];
-    d4[s0] = v0;
-    d4[i1] = v1;  // a clamped index rewrites the last segment with its own bytes
-    d4[i2] = v2;
-    d4[i3] = v3;
+// Direct loads of the row group starting at row r0 into an LDS slice: ni = lds_wave / 1 KB
+// loads of 1 KB, byte offsets clamped into the weight (a group past the end, or the slice's
+// tail past the group, reloads valid bytes that are never read).
+__device__ __forceinline__ void staged_issue(const StagedArgs &a, uint8_t *slice, int64_t r0, int lane) {
+  const int64_t total = (int64_t)a.N * a.row_bytes;
+  const int64_t base = (r0 < a.N ? r0 : a.N - 1) * a.row_bytes;
+  const uint32_t dst = (uint32_t)(uintptr_t)slice;
+  for (int i = 0; i < (a.lds_wave >> 10); i++) {
+    int64_t off = base + i * 1024 + lane * 16;
+    off = off < total - 16 ? off : total - 16;
+    dma16(a.w + off, __builtin_amdgcn_readfirstlane(dst + i * 1024));
   }
 }
 
@@ -445,7 +445,6 @@ __global__ __launch_bounds__(256) void gemv_q80_kernel(StagedArgs a) {
   const int lane = threadIdx.x & 63;
   const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int nwaves = gridDim.x * 4;
-  uint8_t *lds = smem + (threadIdx.x >> 6) * a.lds_wave;
   const int m0 = blockIdx.y * MM;
 
   int xv[MM][CPL][8], yv[MM][CPL][8];
@@ -472,12 +471,19 @@ __global__ __launch_bounds__(256) void gemv_q80_kernel(StagedArgs a) {
     }
   }
 
-  for (int64_t row0 = (int64_t)wave * R; row0 < a.N; row0 += (int64_t)nwaves * R) {
+  // Two LDS slices per wave, filled by direct loads one row group ahead.
+  uint8_t *lds2 = smem + (threadIdx.x >> 6) * 2 * a.lds_wave;
+  const int ni = a.lds_wave >> 10;
+  const int64_t stride = (int64_t)nwaves * R;
+  staged_issue(a, lds2, (int64_t)wave * R, lane);
+  int cur = 0;
+  for (int64_t row0 = (int64_t)wave * R; row0 < a.N; row0 += stride, cur ^= 1) {
     const int nrows = (int)(a.N - row0 < R ? a.N - row0 : R);
-    stage_rows(lds, a.w + row0 * a.row_bytes, (int)(nrows * a.row_bytes / 16), lane);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    uint8_t *lds = lds2 + cur * a.lds_wave;
+    // Next row group into the other slice, then wait for this one (its ni loads are
+    // followed only by the next group's ni).
+    staged_issue(a, lds2 + (cur ^ 1) * a.lds_wave, row0 + stride, lane);
+    wait_vm_rt(ni);
 #pragma unroll
     for (int r = 0; r < R; r++) {
       if (r >= nrows) break;
@@ -508,9 +514,8 @@ __global__ __launch_bounds__(256) void gemv_q80_kernel(StagedArgs a) {
         if (lane == 0 && m0 + mm < a.M) a.out[(int64_t)(m0 + mm) * a.N + row0 + r] = s;
       }
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
   }
+  wait_vm<0>();
 }
 
 // Q6_K lane unit = (block b, l8): half h = l8 >> 2, l0 = (l8 & 3) * 8; the unit covers
@@ -521,7 +526,6 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(StagedArgs a) {
   const int lane = threadIdx.x & 63;
   const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int nwaves = gridDim.x * 4;
-  uint8_t *lds = smem + (threadIdx.x >> 6) * a.lds_wave;
   const int m0 = blockIdx.y * MM;
   const int units = a.nb * 8;
 
@@ -552,12 +556,19 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(StagedArgs a) {
     }
   }
 
-  for (int64_t row0 = (int64_t)wave * R; row0 < a.N; row0 += (int64_t)nwaves * R) {
+  // Two LDS slices per wave, filled by direct loads one row group ahead.
+  uint8_t *lds2 = smem + (threadIdx.x >> 6) * 2 * a.lds_wave;
+  const int ni = a.lds_wave >> 10;
+  const int64_t stride = (int64_t)nwaves * R;
+  staged_issue(a, lds2, (int64_t)wave * R, lane);
+  int cur = 0;
+  for (int64_t row0 = (int64_t)wave * R; row0 < a.N; row0 += stride, cur ^= 1) {
     const int nrows = (int)(a.N - row0 < R ? a.N - row0 : R);
-    stage_rows(lds, a.w + row0 * a.row_bytes, (int)(nrows * a.row_bytes / 16), lane);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    uint8_t *lds = lds2 + cur * a.lds_wave;
+    // Next row group into the other slice, then wait for this one (its ni loads are
+    // followed only by the next group's ni).
+    staged_issue(a, lds2 + (cur ^ 1) * a.lds_wave, row0 + stride, lane);
+    wait_vm_rt(ni);
 #pragma unroll
     for (int r = 0; r < R; r++) {
       if (r >= nrows) break;
@@ -612,9 +623,8 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(StagedArgs a) {
         if (lane == 0 && m0 + mm < a.M) a.out[(int64_t)(m0 + mm) * a.N + row0 + r] = s;
       }
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
   }
+  wait_vm<0>();
 }
 
 // ---------------------------------------------------------------------------
@@ -688,20 +698,31 @@ static void dispatch_q4k(Q4kArgs a, hipStream_t s) {
 
 template <int CPL, int R, int MM>
 static void run_staged(int dt, StagedArgs a, hipStream_t s) {
-  a.lds_wave = (int)((R * a.row_bytes + 16 + 15) & ~(int64_t)15);
-  int64_t wgs = cdiv(cdiv(a.N, R), 4), cap = (int64_t)device_cus() * 8;
+  // Two slices per wave of R rows (+16 bytes read past the last block), whole KB each.
+  a.lds_wave = (int)((R * a.row_bytes + 16 + 1023) & ~(int64_t)1023);
+  const int lds = 8 * a.lds_wave;
+  static bool attr_done = false;
+  if (!attr_done) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_q80_kernel<CPL, R, MM>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_q6k_kernel<CPL, R, MM>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    attr_done = true;
+  }
+  const int per_cu = (160 * 1024) / lds;
+  int64_t wgs = cdiv(cdiv(a.N, R), 4), cap = (int64_t)device_cus() * (per_cu < 2 ? per_cu : 2);
   dim3 g((unsigned)(wgs < cap ? wgs : cap), (unsigned)cdiv(a.M, MM));
   if (dt == Q8_0)
-    gemv_q80_kernel<CPL, R, MM><<<g, 256, 4 * a.lds_wave, s>>>(a);
+    gemv_q80_kernel<CPL, R, MM><<<g, 256, lds, s>>>(a);
   else
-    gemv_q6k_kernel<CPL, R, MM><<<g, 256, 4 * a.lds_wave, s>>>(a);
+    gemv_q6k_kernel<CPL, R, MM><<<g, 256, lds, s>>>(a);
 }
 
 template <int CPL, int MM>
 static void run_staged_r(int dt, StagedArgs a, hipStream_t s) {
-  if (4 * a.row_bytes + 16 <= 16384)
+  if (4 * a.row_bytes + 16 <= 8192)
     run_staged<CPL, 4, MM>(dt, a, s);
-  else if (2 * a.row_bytes + 16 <= 16384)
+  else if (2 * a.row_bytes + 16 <= 8192)
     run_staged<CPL, 2, MM>(dt, a, s);
   else
     run_staged<CPL, 1, MM>(dt, a, s);
