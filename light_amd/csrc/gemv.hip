@@ -854,7 +854,7 @@ int launch_matmul_act(const void *act, const void *w, float *out, int64_t M, int
 int launch_matmul_q(const float *x, const void *w, float *out, int64_t M, int64_t N, int64_t K, int dt, void *ws,
                     hipStream_t s) {
   if (use_gemm(M, dt)) return run_gemm(x, false, w, out, M, N, K, ws, s);
-  if (dt == Q4_K && q4kx_ok(M, N, K, w, nullptr, x))
+  if (dt == Q4_K && q4kx_ok(M, N, K, w, nullptr, x) && q4kx_xin(K))
     return launch_gemv_q4kx(x, w, nullptr, out, M, N, K, 0, s);
   if (!gemv_fast_ok(dt, K, w)) return launch_gemv_generic(x, w, out, M, N, K, dt, s);
   if (int rc = launch_quantize_act(x, F32, ws, M, K, s)) return rc;

@@ -1,23 +1,25 @@
-// gemv_q4kx.hip -- Q4_K decode GEMV (M <= 8): plain, gated (SwiGLU / GELU-erf) and the
-// two-launch MLP (gated gate/up emitting quantized h, then down).
+// gemv_q4kx.hip -- decode GEMV (M <= 8) for Q4_K and int4 weights: plain, gated (SwiGLU /
+// GELU-erf) and the two-launch MLP (gated gate/up emitting quantized h, then down).
 //
-// Role: Light's matmul_q for small M (ops/matmul_q.go:61-75, kernels/cuda/matmul_q.go:44-91)
-// and the gated MLP decode out = act(x . Wg^T) * (x . Wu^T) followed by the down projection,
-// which Light computes as MatMulQ, MatMulQ, SiLU / GeluErf, Mul, MatMulQ
-// (models/llama.go:1306-1333; the dense BF16 analogue is ops.GatedLinear, ops/gemv.go:80-130).
+// Role: Light's matmul_q for small M (ops/matmul_q.go:61-75, kernels/cuda/matmul_q.go:44-91),
+// its int4_gemv (ops/int4.go:87-99, kernels/cuda/int4.go:76-101), and the gated MLP decode
+// out = act(x . Wg^T) * (x . Wu^T) followed by the down projection, which Light computes as
+// MatMulQ, MatMulQ, SiLU / GeluErf, Mul, MatMulQ (models/llama.go:1306-1333; the dense BF16
+// analogue is ops.GatedLinear, ops/gemv.go:80-130).
 //
 // Design (gfx950, wave64):
 //  * Activations are two-level int8 (the act layout of common.hpp).  They come either
-//    prepared from global memory (XIN = false) or from F32 x that each workgroup quantizes
-//    into LDS itself (XIN = true, act_quant8_fast), which saves a launch.
-//  * Lane = one (block, 64-element pair) of a weight row: 32 quant bytes (two 16-byte loads)
-//    + one header dword, broadcast in the block's 4-lane quad by DPP.  A team of TP lanes
-//    covers a row; a workgroup holds RW teams; each lane keeps its pair's activations in
-//    registers for the whole kernel.
+//    prepared from global memory (XIN = false) or from x (F32 / BF16 / F16) that each
+//    workgroup quantizes into LDS itself (XIN = true, act_quant8_fast), saving a launch.
+//  * A lane owns one 64-element unit of a weight row (a weight-format policy: Q4kUnit =
+//    one (super-block, 64-element pair) of Q4_K, Int4Unit = two 32-element code blocks of
+//    quant.Int4) and keeps the unit's activations in registers for the whole kernel.  A
+//    team of TP lanes covers a row; a workgroup holds RW teams.  Products are exact
+//    v_dot4_i32_i8 chains scaled once per 32-block.
 //  * Workgroups are persistent (two per CU).  A ring of D register slots (D = 1) keeps the
-//    next row group's loads in flight while the current one is reduced; every load is unconditional (inactive lanes and rows past N read valid
-//    addresses and their sums are dropped), so no load sits in a branch and the compiler's
-//    wait counts stay exact.
+//    next row group's loads in flight while the current one is reduced; every load is
+//    unconditional (inactive lanes and rows past N read valid addresses and their sums are
+//    dropped), so no load sits in a branch and the compiler's wait counts stay exact.
 //  * Team sums: DPP row sums, then v_readlane over the wave's four rows; teams wider than a
 //    wave add their 16-lane row sums through LDS (one barrier per group).  Row sums are added
 //    in row order in both cases.
@@ -35,12 +37,14 @@ namespace hq {
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 struct Q4kxArgs {
-  const float *x;          // XIN: (M, K) F32
+  const void *x;           // XIN: (M, K) of x dtype
   const uint8_t *ain;      // !XIN: prepared activations of (M, K)
-  const uint8_t *w0, *w1;  // (N, K) Q4_K; w1 = up projection (gated mode only)
-  float *out;              // (M, N) F32, may be NULL with AOUT
+  const uint8_t *w0, *w1;  // weights (N, K); w1 = up projection (gated mode only)
+  const float *s0, *z0, *s1, *z1;  // int4 scales / zeros (N, K/G) of w0 / w1
+  void *out;               // (M, N) of the output dtype, may be NULL with AOUT
   uint8_t *aout;           // AOUT: act layout of the (M, N) output
-  int M, N, K, P, TP, RW;  // P: pairs per row (K/64); TP: team lanes; RW: teams per workgroup
+  int M, N, K, P, TP, RW;  // P: units per row (K/64); TP: team lanes; RW: teams per workgroup
+  int G;                   // int4 group size
   int64_t row_bytes;
   int64_t in_q2, in_d, in_s;     // act offsets of (M, K)
   int64_t out_q2, out_d, out_s;  // act offsets of (M, N)
@@ -79,24 +83,220 @@ __device__ __forceinline__ float gate_act(float g, int act) {
 //      hbuf [2][MM][32]                                                  (AOUT only)
 __host__ __device__ constexpr int64_t q4kx_act_lds(int MM, int64_t K) { return MM * (2 * K + 12 * (K / 32)); }
 
-// Byte offsets are 32-bit (the host checks N * row_bytes < 2^32), so loads take the
-// scalar-base + vector-offset form.
-#define Q4KX_LOAD(S, GRP)                                                             \
-  do {                                                                                \
-    int row_ = (GRP) * RW + team;                                                     \
-    row_ = row_ < a.N ? row_ : a.N - 1;                                               \
-    const uint32_t ro_ = (uint32_t)row_ * (uint32_t)a.row_bytes;                      \
-    wq0[S][0] = *reinterpret_cast<const u32x4_t *>(a.w0 + (ro_ + qoff));              \
-    wq1[S][0] = *reinterpret_cast<const u32x4_t *>(a.w0 + (ro_ + qoff + 16));         \
-    wh[S][0] = *reinterpret_cast<const uint32_t *>(a.w0 + (ro_ + hoff));              \
-    if (GATED) {                                                                      \
-      wq0[S][NW - 1] = *reinterpret_cast<const u32x4_t *>(a.w1 + (ro_ + qoff));       \
-      wq1[S][NW - 1] = *reinterpret_cast<const u32x4_t *>(a.w1 + (ro_ + qoff + 16));  \
-      wh[S][NW - 1] = *reinterpret_cast<const uint32_t *>(a.w1 + (ro_ + hoff));       \
-    }                                                                                 \
-  } while (0)
+// ---- weight-unit policies --------------------------------------------------------
+// Activations of one unit (two 32-blocks of one row of x), as each policy wants them.
 
-template <int MM, bool GATED, int D, bool XIN, bool AOUT>
+// Q4_K unit: super-block b = u / 4, pair p = u % 4 -> 32 quant bytes (low nibbles =
+// sub-block 2p, high = 2p+1) and the block header, broadcast in the block's 4-lane quad.
+struct Q4kUnit {
+  struct Lane {
+    uint32_t qoff, hoff;  // byte offsets of the quant chunk / this lane's header dword
+    int ja;               // first 32-block of x
+    uint32_t sel, mlo, mhi;
+    int ka;
+  };
+  struct W {
+    u32x4_t q0, q1;
+    uint32_t h;
+  };
+  struct X {
+    uint32_t xa[8], xb[8], ya[8], yb[8];
+    float4 de;  // (dA, eA, dB, eB)
+    float2 ss;  // block sums of x
+  };
+  __device__ static Lane lane(int u) {
+    Lane L;
+    const int b = u >> 2, p = u & 3;
+    L.qoff = b * 144 + 16 + p * 32;
+    L.hoff = b * 144 + 4 * p;
+    L.ja = b * 8 + 2 * p;
+    const bool lowj = p < 2;
+    L.sel = lowj ? ~0u : 0u;
+    L.mlo = lowj ? 0x3F3Fu : 0x0F0Fu;
+    L.mhi = lowj ? 0u : 0x3030u;
+    L.ka = (2 * p) & 3;
+    return L;
+  }
+  // Byte offsets are 32-bit (the host checks N * row_bytes < 2^32), so the loads take the
+  // scalar-base + vector-offset form.
+  __device__ static void load(const uint8_t *w, const float *, const float *, const Q4kxArgs &a, int row,
+                              const Lane &L, W &r) {
+    const uint32_t ro = (uint32_t)row * (uint32_t)a.row_bytes;
+    r.q0 = *reinterpret_cast<const u32x4_t *>(w + (ro + L.qoff));
+    r.q1 = *reinterpret_cast<const u32x4_t *>(w + (ro + L.qoff + 16));
+    r.h = *reinterpret_cast<const uint32_t *>(w + (ro + L.hoff));
+  }
+  __device__ static void load_x(const uint8_t *q1, const uint8_t *q2, const uint8_t *de, const uint8_t *sx,
+                                int64_t blk, X &x) {
+    const u32x4_t *s1 = reinterpret_cast<const u32x4_t *>(q1 + blk * 32);
+    const u32x4_t *s2 = reinterpret_cast<const u32x4_t *>(q2 + blk * 32);
+    const u32x4_t v0 = s1[0], v1 = s1[1], v2 = s1[2], v3 = s1[3];
+    const u32x4_t w0 = s2[0], w1 = s2[1], w2 = s2[2], w3 = s2[3];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      x.xa[k] = v0[k], x.xa[k + 4] = v1[k], x.xb[k] = v2[k], x.xb[k + 4] = v3[k];
+      x.ya[k] = w0[k], x.ya[k + 4] = w1[k], x.yb[k] = w2[k], x.yb[k + 4] = w3[k];
+    }
+    x.de = *reinterpret_cast<const float4 *>(de + 8 * blk);
+    x.ss = *reinterpret_cast<const float2 *>(sx + 4 * blk);
+  }
+  template <int MM>
+  __device__ static void dot(const W &w, const X (&x)[MM], const Lane &L, float (&out)[MM]) {
+    const uint32_t h0 = qb<0>(w.h), h1 = qb<1>(w.h), h2 = qb<2>(w.h), h3 = qb<3>(w.h);
+    const float d = h2f(h0 & 0xffffu), dmin = h2f(h0 >> 16);
+    // 6-bit (scale, min) of sub-blocks 2p and 2p+1 (getScaleMinK4, quant/q4_k.go:83-89),
+    // selected branch-free with lane constants: p < 2 takes the low six bits of
+    // scales[j] / scales[j+4]; p >= 2 combines nibbles of scales[j+4] with the top two bits
+    // of scales[j-4] / scales[j].
+    const uint32_t t1 = (h1 >> (8 * L.ka)) & 0xffffu, t2 = (h2 >> (8 * L.ka)) & 0xffffu;
+    const uint32_t t3 = (h3 >> (8 * L.ka)) & 0xffffu;
+    const uint32_t srcS = (t1 & L.sel) | (t3 & ~L.sel), srcM = (t2 & L.sel) | ((t3 >> 4) & ~L.sel);
+    const uint32_t scp = (srcS & L.mlo) | ((t1 >> 2) & L.mhi), mnp = (srcM & L.mlo) | ((t2 >> 2) & L.mhi);
+    const float scA = (float)(scp & 0xffu), scB = (float)(scp >> 8);
+    const float mnA = (float)(mnp & 0xffu), mnB = (float)(mnp >> 8);
+    uint32_t lo[8], hi[8];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      lo[k] = w.q0[k] & 0x0F0F0F0Fu;
+      hi[k] = (w.q0[k] >> 4) & 0x0F0F0F0Fu;
+      lo[k + 4] = w.q1[k] & 0x0F0F0F0Fu;
+      hi[k + 4] = (w.q1[k] >> 4) & 0x0F0F0F0Fu;
+    }
+#pragma unroll
+    for (int mm = 0; mm < MM; mm++) {
+      int dA = 0, dB = 0, dA2 = 0, dB2 = 0;
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        dA = dot4((int)lo[k], (int)x[mm].xa[k], dA);
+        dB = dot4((int)hi[k], (int)x[mm].xb[k], dB);
+        dA2 = dot4((int)lo[k], (int)x[mm].ya[k], dA2);
+        dB2 = dot4((int)hi[k], (int)x[mm].yb[k], dB2);
+      }
+      out[mm] = q4k_pair(d, dmin, scA, scB, mnA, mnB, x[mm].de, x[mm].ss, dA, dA2, dB, dB2);
+    }
+  }
+};
+
+// int4 unit (quant.Int4, quant/int4.go:11-34): 64 elements = code words 8u .. 8u+7 (two
+// 32-blocks A, B); nibble j of word c is element 8c + j, so the low / high nibbles of a
+// word are its even / odd elements and the lane's activations are stored even / odd
+// permuted (v_perm_b32) once.  Per block: s * (d * sum(q q1) + e * sum(q q2) - z * sx).
+struct Int4Unit {
+  struct Lane {
+    uint32_t coff;  // byte offset of the unit's codes in a row
+    int ja, gA, gB;  // first 32-block of x; group index of blocks A, B
+  };
+  struct W {
+    u32x4_t q0, q1;
+    float sA, zA, sB, zB;
+  };
+  struct X {
+    int ev[8], od[8], ev2[8], od2[8];  // blocks A (0..3) and B (4..7)
+    float4 de;
+    float2 ss;
+  };
+  __device__ static Lane lane(int u, int G) {
+    Lane L;
+    L.coff = 32 * u;
+    L.ja = 2 * u;
+    L.gA = (64 * u) / G;
+    L.gB = (64 * u + 32) / G;
+    return L;
+  }
+  __device__ static void load(const uint8_t *w, const float *s, const float *z, const Q4kxArgs &a, int row,
+                              const Lane &L, W &r) {
+    const uint32_t ro = (uint32_t)row * (uint32_t)a.row_bytes;
+    r.q0 = *reinterpret_cast<const u32x4_t *>(w + (ro + L.coff));
+    r.q1 = *reinterpret_cast<const u32x4_t *>(w + (ro + L.coff + 16));
+    const int64_t gr = (int64_t)row * (a.K / a.G);
+    r.sA = s[gr + L.gA];
+    r.zA = z[gr + L.gA];
+    r.sB = s[gr + L.gB];
+    r.zB = z[gr + L.gB];
+  }
+  __device__ static void load_x(const uint8_t *q1, const uint8_t *q2, const uint8_t *de, const uint8_t *sx,
+                                int64_t blk, X &x) {
+    const u32x4_t *s1 = reinterpret_cast<const u32x4_t *>(q1 + blk * 32);
+    const u32x4_t *s2 = reinterpret_cast<const u32x4_t *>(q2 + blk * 32);
+    const u32x4_t v[4] = {s1[0], s1[1], s1[2], s1[3]};
+    const u32x4_t y[4] = {s2[0], s2[1], s2[2], s2[3]};
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const uint32_t a0 = v[k >> 1][2 * (k & 1)], a1 = v[k >> 1][2 * (k & 1) + 1];
+      const uint32_t b0 = y[k >> 1][2 * (k & 1)], b1 = y[k >> 1][2 * (k & 1) + 1];
+      x.ev[k] = (int)__builtin_amdgcn_perm(a1, a0, 0x06040200u);
+      x.od[k] = (int)__builtin_amdgcn_perm(a1, a0, 0x07050301u);
+      x.ev2[k] = (int)__builtin_amdgcn_perm(b1, b0, 0x06040200u);
+      x.od2[k] = (int)__builtin_amdgcn_perm(b1, b0, 0x07050301u);
+    }
+    x.de = *reinterpret_cast<const float4 *>(de + 8 * blk);
+    x.ss = *reinterpret_cast<const float2 *>(sx + 4 * blk);
+  }
+  template <int MM>
+  __device__ static void dot(const W &w, const X (&x)[MM], const Lane &, float (&out)[MM]) {
+    uint32_t lo[8], hi[8];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      lo[k] = w.q0[k] & 0x0F0F0F0Fu;
+      hi[k] = (w.q0[k] >> 4) & 0x0F0F0F0Fu;
+      lo[k + 4] = w.q1[k] & 0x0F0F0F0Fu;
+      hi[k + 4] = (w.q1[k] >> 4) & 0x0F0F0F0Fu;
+    }
+#pragma unroll
+    for (int mm = 0; mm < MM; mm++) {
+      int dA = 0, dA2 = 0, dB = 0, dB2 = 0;
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        dA = dot4((int)lo[k], x[mm].ev[k], dA);
+        dA = dot4((int)hi[k], x[mm].od[k], dA);
+        dA2 = dot4((int)lo[k], x[mm].ev2[k], dA2);
+        dA2 = dot4((int)hi[k], x[mm].od2[k], dA2);
+        dB = dot4((int)lo[4 + k], x[mm].ev[4 + k], dB);
+        dB = dot4((int)hi[4 + k], x[mm].od[4 + k], dB);
+        dB2 = dot4((int)lo[4 + k], x[mm].ev2[4 + k], dB2);
+        dB2 = dot4((int)hi[4 + k], x[mm].od2[4 + k], dB2);
+      }
+      const float4 de = x[mm].de;
+      const float yA = __fmaf_rn(-w.zA, x[mm].ss.x, __fmaf_rn(de.y, (float)dA2, __fmul_rn(de.x, (float)dA)));
+      const float yB = __fmaf_rn(-w.zB, x[mm].ss.y, __fmaf_rn(de.w, (float)dB2, __fmul_rn(de.z, (float)dB)));
+      out[mm] = __fmaf_rn(w.sB, yB, __fmul_rn(w.sA, yA));
+    }
+  }
+};
+
+template <class U>
+__device__ __forceinline__ typename U::Lane unit_lane(int u, int G) {
+  if constexpr (__is_same(U, Int4Unit))
+    return U::lane(u, G);
+  else
+    return U::lane(u);
+}
+
+template <int XDT>
+__device__ __forceinline__ float4 load_x4(const void *x, int64_t i) {
+  if constexpr (XDT == F32) {
+    return *reinterpret_cast<const float4 *>(static_cast<const float *>(x) + i);
+  } else {
+    const uint2 u = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(x) + i);
+    const uint32_t h[4] = {u.x & 0xffffu, u.x >> 16, u.y & 0xffffu, u.y >> 16};
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) v[j] = XDT == BF16 ? bf2f(h[j]) : h2f(h[j]);
+    return make_float4(v[0], v[1], v[2], v[3]);
+  }
+}
+
+template <int ODT>
+__device__ __forceinline__ void store_out(void *out, int64_t i, float y) {
+  if constexpr (ODT == F32)
+    static_cast<float *>(out)[i] = y;
+  else if constexpr (ODT == BF16)
+    static_cast<uint16_t *>(out)[i] = f2bf_rne(y);
+  else
+    static_cast<uint16_t *>(out)[i] = f2h_rne(y);
+}
+
+template <class U, int MM, bool GATED, bool XIN, bool AOUT, int XDT, int ODT>
 __global__ __launch_bounds__(512) void gemv_q4kx_kernel(Q4kxArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   constexpr int NW = GATED ? 2 : 1;
@@ -104,9 +304,7 @@ __global__ __launch_bounds__(512) void gemv_q4kx_kernel(Q4kxArgs a) {
   const int RW = a.RW, KB = a.K >> 5;
   const int team = t / a.TP, u = t - team * a.TP;
   const bool active = u < a.P;
-  const int uu = active ? u : 0;
-  const int b = uu >> 2, p = uu & 3;
-  const uint32_t qoff = b * 144 + 16 + p * 32, hoff = b * 144 + 4 * p;
+  const typename U::Lane L = unit_lane<U>(active ? u : 0, a.G);
   const int ngroups = (a.N + RW - 1) / RW;
   const int m0 = blockIdx.y * MM;
   const int G = gridDim.x;
@@ -116,16 +314,18 @@ __global__ __launch_bounds__(512) void gemv_q4kx_kernel(Q4kxArgs a) {
   const int nchunks = (ngroups + CG - 1) / CG;
   const int niter = ((nchunks - (int)blockIdx.x + G - 1) / G) * CG;
 #define Q4KX_GRP(I) (((int)blockIdx.x + ((I) / CG) * G) * CG + (I) % CG)
+#define Q4KX_LOAD(SLOT, GRP)                                                  \
+  do {                                                                        \
+    int row_ = (GRP) * RW + team;                                             \
+    row_ = row_ < a.N ? row_ : a.N - 1;                                       \
+    U::load(a.w0, a.s0, a.z0, a, row_, L, wr[SLOT][0]);                        \
+    if (GATED) U::load(a.w1, a.s1, a.z1, a, row_, L, wr[SLOT][NW - 1]);        \
+  } while (0)
 
-  u32x4_t wq0[D][NW], wq1[D][NW];
-  uint32_t wh[D][NW];
-#pragma unroll
-  for (int s = 0; s < D; s++) Q4KX_LOAD(s, Q4KX_GRP(s));
+  typename U::W wr[1][NW];
+  Q4KX_LOAD(0, Q4KX_GRP(0));
 
-  const int ja = b * 8 + 2 * p;  // this lane's first 32-block in a row of x
-  uint32_t xa[MM][8], xb[MM][8], ya[MM][8], yb[MM][8];
-  float4 de[MM];
-  float2 ss[MM];
+  typename U::X xr[MM];
   const int64_t lds_act = XIN ? q4kx_act_lds(MM, a.K) : 0;
   if constexpr (XIN) {
     // Quantize this workgroup's MM rows of x into LDS (8 lanes per 32-block).  A chunk's
@@ -143,7 +343,7 @@ __global__ __launch_bounds__(512) void gemv_q4kx_kernel(Q4kxArgs a) {
         task = task < ntask ? task : ntask - 1;
         const int blk = task >> 3, sub = task & 7, mm = blk / KB, kb = blk - mm * KB;
         const int m = m0 + mm < a.M ? m0 + mm : a.M - 1;
-        xv[i] = *reinterpret_cast<const float4 *>(a.x + (int64_t)m * a.K + kb * 32 + sub * 4);
+        xv[i] = load_x4<XDT>(a.x, (int64_t)m * a.K + kb * 32 + sub * 4);
       }
 #pragma unroll
       for (int i = 0; i < XT; i++) {
@@ -163,182 +363,122 @@ __global__ __launch_bounds__(512) void gemv_q4kx_kernel(Q4kxArgs a) {
     }
     __syncthreads();
 #pragma unroll
-    for (int mm = 0; mm < MM; mm++) {
-      const int blk = mm * KB + ja;
-      const u32x4_t *s1 = reinterpret_cast<const u32x4_t *>(lq1 + blk * 32);
-      const u32x4_t *s2 = reinterpret_cast<const u32x4_t *>(lq2 + blk * 32);
-      const u32x4_t v0 = s1[0], v1 = s1[1], v2 = s1[2], v3 = s1[3];
-      const u32x4_t w0 = s2[0], w1 = s2[1], w2 = s2[2], w3 = s2[3];
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        xa[mm][k] = v0[k], xa[mm][k + 4] = v1[k], xb[mm][k] = v2[k], xb[mm][k + 4] = v3[k];
-        ya[mm][k] = w0[k], ya[mm][k + 4] = w1[k], yb[mm][k] = w2[k], yb[mm][k + 4] = w3[k];
-      }
-      de[mm] = *reinterpret_cast<const float4 *>(lde + blk);
-      ss[mm] = *reinterpret_cast<const float2 *>(lsx + blk);
-    }
+    for (int mm = 0; mm < MM; mm++)
+      U::load_x(lq1, lq2, reinterpret_cast<const uint8_t *>(lde), reinterpret_cast<const uint8_t *>(lsx),
+                mm * KB + L.ja, xr[mm]);
   } else {
 #pragma unroll
     for (int mm = 0; mm < MM; mm++) {
       const int m = m0 + mm < a.M ? m0 + mm : a.M - 1;
-      const int64_t blk = (int64_t)m * KB + ja;
-      const u32x4_t *s1 = reinterpret_cast<const u32x4_t *>(a.ain + blk * 32);
-      const u32x4_t *s2 = reinterpret_cast<const u32x4_t *>(a.ain + a.in_q2 + blk * 32);
-      const u32x4_t v0 = s1[0], v1 = s1[1], v2 = s1[2], v3 = s1[3];
-      const u32x4_t w0 = s2[0], w1 = s2[1], w2 = s2[2], w3 = s2[3];
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        xa[mm][k] = v0[k], xa[mm][k + 4] = v1[k], xb[mm][k] = v2[k], xb[mm][k + 4] = v3[k];
-        ya[mm][k] = w0[k], ya[mm][k + 4] = w1[k], yb[mm][k] = w2[k], yb[mm][k + 4] = w3[k];
-      }
-      de[mm] = *reinterpret_cast<const float4 *>(a.ain + a.in_d + 8 * blk);
-      ss[mm] = *reinterpret_cast<const float2 *>(a.ain + a.in_s + 4 * blk);
+      U::load_x(a.ain, a.ain + a.in_q2, a.ain + a.in_d, a.ain + a.in_s, (int64_t)m * KB + L.ja, xr[mm]);
     }
   }
 
-  const bool lowj = p < 2;
-  const uint32_t sel = lowj ? ~0u : 0u, mlo = lowj ? 0x3F3Fu : 0x0F0Fu, mhi = lowj ? 0u : 0x3030u;
-  const int ka = (2 * p) & 3;
   const int wpt = a.TP >> 6;  // waves per team (0 when a team is narrower than a wave)
   const int hpt = a.TP >> 4;  // 16-lane rows per team
   float *part = reinterpret_cast<float *>(smem + lds_act);
   float *hbuf = part + (wpt > 1 ? 2 * RW * NW * MM * hpt : 0);
 
-  for (int i0 = 0; i0 < niter; i0 += D) {
+  for (int it = 0; it < niter; it++) {
+    const int grp = Q4KX_GRP(it);
+    float res[NW][MM];
 #pragma unroll
-    for (int s = 0; s < D; s++) {
-      const int it = i0 + s;
-      const int grp = Q4KX_GRP(it);
-      float res[NW][MM];
+    for (int j = 0; j < NW; j++) {
+      float c[MM];
+      U::template dot<MM>(wr[0][j], xr, L, c);
 #pragma unroll
-      for (int j = 0; j < NW; j++) {
-        const uint32_t hd = wh[s][j];
-        const uint32_t h0 = qb<0>(hd), h1 = qb<1>(hd), h2 = qb<2>(hd), h3 = qb<3>(hd);
-        const float d = h2f(h0 & 0xffffu), dmin = h2f(h0 >> 16);
-        // 6-bit (scale, min) of sub-blocks 2p and 2p+1 (getScaleMinK4, quant/q4_k.go:83-89).
-        const uint32_t t1 = (h1 >> (8 * ka)) & 0xffffu, t2 = (h2 >> (8 * ka)) & 0xffffu;
-        const uint32_t t3 = (h3 >> (8 * ka)) & 0xffffu;
-        // Branch-free select with lane constants (v_bfi / v_and_or): p < 2 takes the low six
-        // bits of scales[j] / scales[j+4]; p >= 2 combines nibbles of scales[j+4] with the top
-        // two bits of scales[j-4] / scales[j].
-        const uint32_t srcS = (t1 & sel) | (t3 & ~sel), srcM = (t2 & sel) | ((t3 >> 4) & ~sel);
-        const uint32_t scp = (srcS & mlo) | ((t1 >> 2) & mhi), mnp = (srcM & mlo) | ((t2 >> 2) & mhi);
-        const float scA = (float)(scp & 0xffu), scB = (float)(scp >> 8);
-        const float mnA = (float)(mnp & 0xffu), mnB = (float)(mnp >> 8);
-        uint32_t lo[8], hi[8];
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-          lo[k] = wq0[s][j][k] & 0x0F0F0F0Fu;
-          hi[k] = (wq0[s][j][k] >> 4) & 0x0F0F0F0Fu;
-          lo[k + 4] = wq1[s][j][k] & 0x0F0F0F0Fu;
-          hi[k + 4] = (wq1[s][j][k] >> 4) & 0x0F0F0F0Fu;
-        }
-#pragma unroll
-        for (int mm = 0; mm < MM; mm++) {
-          int dA = 0, dB = 0, dA2 = 0, dB2 = 0;
-#pragma unroll
-          for (int k = 0; k < 8; k++) {
-            dA = dot4((int)lo[k], (int)xa[mm][k], dA);
-            dB = dot4((int)hi[k], (int)xb[mm][k], dB);
-            dA2 = dot4((int)lo[k], (int)ya[mm][k], dA2);
-            dB2 = dot4((int)hi[k], (int)yb[mm][k], dB2);
-          }
-          const float c = q4k_pair(d, dmin, scA, scB, mnA, mnB, de[mm], ss[mm], dA, dA2, dB, dB2);
-          res[j][mm] = rsum16(active ? c : 0.f);
-        }
-      }
-      // The slot is consumed: refill it with the group D iterations ahead (unconditionally).
-      Q4KX_LOAD(s, Q4KX_GRP(it + D));
-      if (it >= niter) break;
+      for (int mm = 0; mm < MM; mm++) res[j][mm] = rsum16(active ? c[mm] : 0.f);
+    }
+    // The slot is consumed: refill it with the next group (unconditionally).
+    Q4KX_LOAD(0, Q4KX_GRP(it + 1));
 
-      const int row = grp * RW + team;
-      float *hb = hbuf + ((it / CG) & 1) * (MM * 32);
-      if (wpt <= 1) {
-        // Team within one wave (TP in {16, 32, 64}): add its 16-lane rows in order.
+    const int row = grp * RW + team;
+    float *hb = hbuf + ((it / CG) & 1) * (MM * 32);
+    if (wpt <= 1) {
+      // Team within one wave (TP in {16, 32, 64}): add its 16-lane rows in order.
 #pragma unroll
-        for (int mm = 0; mm < MM; mm++) {
-          float tot[NW];
-#pragma unroll
-          for (int j = 0; j < NW; j++) {
-            const float r0 = rl(res[j][mm], 0), r1 = rl(res[j][mm], 16);
-            const float r2 = rl(res[j][mm], 32), r3 = rl(res[j][mm], 48);
-            if (a.TP == 64)
-              tot[j] = ((r0 + r1) + r2) + r3;
-            else if (a.TP == 32)
-              tot[j] = lane < 32 ? r0 + r1 : r2 + r3;
-            else
-              tot[j] = lane < 16 ? r0 : (lane < 32 ? r1 : (lane < 48 ? r2 : r3));
-          }
-          if (u == 0 && row < a.N) {
-            float y = tot[0];
-            if (GATED) y = gate_act(tot[0], a.act) * tot[NW - 1];
-            if (a.out && m0 + mm < a.M) a.out[(int64_t)(m0 + mm) * a.N + row] = y;
-            if (AOUT) hb[mm * 32 + (row & 31)] = y;
-          }
-        }
-      } else {
-        // Team of wpt waves: 16-lane row sums through LDS, added in row order.
-        float *pp = part + (it & 1) * (RW * NW * MM * hpt);
+      for (int mm = 0; mm < MM; mm++) {
+        float tot[NW];
 #pragma unroll
         for (int j = 0; j < NW; j++) {
-#pragma unroll
-          for (int mm = 0; mm < MM; mm++)
-            if ((lane & 15) == 0) pp[((team * NW + j) * MM + mm) * hpt + (u >> 4)] = res[j][mm];
+          const float r0 = rl(res[j][mm], 0), r1 = rl(res[j][mm], 16);
+          const float r2 = rl(res[j][mm], 32), r3 = rl(res[j][mm], 48);
+          if (a.TP == 64)
+            tot[j] = ((r0 + r1) + r2) + r3;
+          else if (a.TP == 32)
+            tot[j] = lane < 32 ? r0 + r1 : r2 + r3;
+          else
+            tot[j] = lane < 16 ? r0 : (lane < 32 ? r1 : (lane < 48 ? r2 : r3));
         }
-        __syncthreads();
-        if (t < RW * MM) {
-          const int tm = t / MM, mm = t - tm * MM;
-          float tot[NW];
-#pragma unroll
-          for (int j = 0; j < NW; j++) {
-            float acc = 0.f;
-            for (int k = 0; k < hpt; k++) acc += pp[((tm * NW + j) * MM + mm) * hpt + k];
-            tot[j] = acc;
-          }
-          const int r2 = grp * RW + tm;
-          if (r2 < a.N) {
-            float y = tot[0];
-            if (GATED) y = gate_act(tot[0], a.act) * tot[NW - 1];
-            if (a.out && m0 + mm < a.M) a.out[(int64_t)(m0 + mm) * a.N + r2] = y;
-            if (AOUT) hb[mm * 32 + (r2 & 31)] = y;
-          }
+        if (u == 0 && row < a.N) {
+          float y = tot[0];
+          if (GATED) y = gate_act(tot[0], a.act) * tot[NW - 1];
+          if (a.out && m0 + mm < a.M) store_out<ODT>(a.out, (int64_t)(m0 + mm) * a.N + row, y);
+          if (AOUT) hb[mm * 32 + (row & 31)] = y;
         }
       }
-      if (AOUT && it % CG == CG - 1) {
-        // The chunk's 32 rows are complete: quantize them into the act layout of (M, N).
-        __syncthreads();
-        const int chunk = grp / CG;
-        if (t < 8 * MM) {
-          const int mm = t >> 3, sub = t & 7;
-          const float v[4] = {hb[mm * 32 + sub * 4], hb[mm * 32 + sub * 4 + 1], hb[mm * 32 + sub * 4 + 2],
-                              hb[mm * 32 + sub * 4 + 3]};
-          const ActQ q = act_quant8_fast(v);
-          if (m0 + mm < a.M && chunk * 32 < a.N) {
-            const int64_t blk = (int64_t)(m0 + mm) * (a.N >> 5) + chunk;
-            reinterpret_cast<uint32_t *>(a.aout + blk * 32)[sub] = q.q1;
-            reinterpret_cast<uint32_t *>(a.aout + a.out_q2 + blk * 32)[sub] = q.q2;
-            if (sub == 0) {
-              reinterpret_cast<float2 *>(a.aout + a.out_d)[blk] = make_float2(q.d, q.e);
-              reinterpret_cast<float *>(a.aout + a.out_s)[blk] = q.sum;
-            }
+    } else {
+      // Team of wpt waves: 16-lane row sums through LDS, added in row order.
+      float *pp = part + (it & 1) * (RW * NW * MM * hpt);
+#pragma unroll
+      for (int j = 0; j < NW; j++) {
+#pragma unroll
+        for (int mm = 0; mm < MM; mm++)
+          if ((lane & 15) == 0) pp[((team * NW + j) * MM + mm) * hpt + (u >> 4)] = res[j][mm];
+      }
+      __syncthreads();
+      if (t < RW * MM) {
+        const int tm = t / MM, mm = t - tm * MM;
+        float tot[NW];
+#pragma unroll
+        for (int j = 0; j < NW; j++) {
+          float acc = 0.f;
+          for (int k = 0; k < hpt; k++) acc += pp[((tm * NW + j) * MM + mm) * hpt + k];
+          tot[j] = acc;
+        }
+        const int r2 = grp * RW + tm;
+        if (r2 < a.N) {
+          float y = tot[0];
+          if (GATED) y = gate_act(tot[0], a.act) * tot[NW - 1];
+          if (a.out && m0 + mm < a.M) store_out<ODT>(a.out, (int64_t)(m0 + mm) * a.N + r2, y);
+          if (AOUT) hb[mm * 32 + (r2 & 31)] = y;
+        }
+      }
+    }
+    if (AOUT && it % CG == CG - 1) {
+      // The chunk's 32 rows are complete: quantize them into the act layout of (M, N).
+      __syncthreads();
+      const int chunk = grp / CG;
+      if (t < 8 * MM) {
+        const int mm = t >> 3, sub = t & 7;
+        const float v[4] = {hb[mm * 32 + sub * 4], hb[mm * 32 + sub * 4 + 1], hb[mm * 32 + sub * 4 + 2],
+                            hb[mm * 32 + sub * 4 + 3]};
+        const ActQ q = act_quant8_fast(v);
+        if (m0 + mm < a.M && chunk * 32 < a.N) {
+          const int64_t blk = (int64_t)(m0 + mm) * (a.N >> 5) + chunk;
+          reinterpret_cast<uint32_t *>(a.aout + blk * 32)[sub] = q.q1;
+          reinterpret_cast<uint32_t *>(a.aout + a.out_q2 + blk * 32)[sub] = q.q2;
+          if (sub == 0) {
+            reinterpret_cast<float2 *>(a.aout + a.out_d)[blk] = make_float2(q.d, q.e);
+            reinterpret_cast<float *>(a.aout + a.out_s)[blk] = q.sum;
           }
         }
       }
     }
   }
+#undef Q4KX_LOAD
 #undef Q4KX_GRP
 }
-
-#undef Q4KX_LOAD
 
 // ---------------------------------------------------------------------------
 // Launch
 // ---------------------------------------------------------------------------
 
-// Team geometry: P = K/64 lanes per row; TP = 16, 32 or 64 when P fits a wave, else a
-// multiple of 64 (up to 512); RW = teams per 512-lane workgroup.
-static bool q4kx_geom(int64_t K, int *P, int *TP, int *RW) {
-  if (K % 256 || K > 32768) return false;
+// Team geometry: P = K/64 lanes (units) per row; TP = 16, 32 or 64 when P fits a wave,
+// else a multiple of 64 (up to 512); RW = teams per 512-lane workgroup.  `kblock` is the
+// K granularity of the format (256 for Q4_K, 64 for int4).
+static bool q4kx_geom(int64_t K, int kblock, int *P, int *TP, int *RW) {
+  if (K % kblock || K > 32768) return false;
   *P = (int)(K / 64);
   if (*P <= 16)
     *TP = 16;
@@ -352,6 +492,11 @@ static bool q4kx_geom(int64_t K, int *P, int *TP, int *RW) {
 
 static int mm_of(int64_t M) { return M >= 3 ? 4 : (int)M; }
 
+// Quantize x inside the GEMV's workgroups (saves a launch) only for rows up to 8192: each
+// workgroup quantizes all of x, which costs ~1 us at K = 4096 but ~4.5 us at K = 14336,
+// more than the separate quantize launch.
+bool q4kx_xin(int64_t K) { return K <= 8192; }
+
 static size_t q4kx_lds(int MM, int64_t K, int TP, int RW, bool gated, bool xin, bool aout) {
   size_t b = xin ? (size_t)q4kx_act_lds(MM, K) : 0;
   if (TP > 64) b += 2 * 4 * (size_t)(RW * (TP >> 4) * (gated ? 2 : 1) * MM);
@@ -361,15 +506,15 @@ static size_t q4kx_lds(int MM, int64_t K, int TP, int RW, bool gated, bool xin, 
 
 bool q4kx_ok(int64_t M, int64_t N, int64_t K, const void *w0, const void *w1, const void *x) {
   int P, TP, RW;
-  if (M < 1 || M > kGemvMaxRows || !q4kx_geom(K, &P, &TP, &RW)) return false;
+  if (M < 1 || M > kGemvMaxRows || !q4kx_geom(K, 256, &P, &TP, &RW)) return false;
   if (N > INT32_MAX / 2 || N * (K / 256 * 144) > UINT32_MAX) return false;
   if (((uintptr_t)w0 & 15) || (w1 && ((uintptr_t)w1 & 15)) || ((uintptr_t)x & 15)) return false;
   return q4kx_lds(mm_of(M), K, TP, RW, w1 != nullptr, true, true) <= 160 * 1024;
 }
 
-template <int MM, bool GATED, int D, bool XIN, bool AOUT>
+template <class U, int MM, bool GATED, bool XIN, bool AOUT, int XDT, int ODT>
 static int run_q4kx(const Q4kxArgs &a, hipStream_t s) {
-  auto *kern = &gemv_q4kx_kernel<MM, GATED, D, XIN, AOUT>;
+  auto *kern = &gemv_q4kx_kernel<U, MM, GATED, XIN, AOUT, XDT, ODT>;
   const size_t lds = q4kx_lds(MM, a.K, a.TP, a.RW, GATED, XIN, AOUT);
   if (lds > 64 * 1024) {
     static bool attr_done = false;
@@ -390,26 +535,29 @@ static int run_q4kx(const Q4kxArgs &a, hipStream_t s) {
   return check_launch(GATED ? "gemv_q4k_gated" : "gemv_q4kx");
 }
 
-template <bool GATED, bool XIN, bool AOUT>
+template <class U, bool GATED, bool XIN, bool AOUT, int XDT = F32, int ODT = F32>
 static int dispatch_q4kx(const Q4kxArgs &a, hipStream_t s) {
   const int MMc = mm_of(a.M);
-  if (MMc == 1) return run_q4kx<1, GATED, 1, XIN, AOUT>(a, s);
-  if (MMc == 2) return run_q4kx<2, GATED, 1, XIN, AOUT>(a, s);
-  return run_q4kx<4, GATED, 1, XIN, AOUT>(a, s);
+  if (MMc == 1) return run_q4kx<U, 1, GATED, XIN, AOUT, XDT, ODT>(a, s);
+  if (MMc == 2) return run_q4kx<U, 2, GATED, XIN, AOUT, XDT, ODT>(a, s);
+  return run_q4kx<U, 4, GATED, XIN, AOUT, XDT, ODT>(a, s);
 }
 
-static int q4kx_setup(Q4kxArgs &a, int64_t M, int64_t N, int64_t K, const char *call) {
-  if (!q4kx_geom(K, &a.P, &a.TP, &a.RW) || N > INT32_MAX / 2 || M > 65535 || N * (K / 256 * 144) > UINT32_MAX)
+static int q4kx_setup(Q4kxArgs &a, int64_t M, int64_t N, int64_t K, int kblock, int64_t row_bytes,
+                      const char *call) {
+  if (!q4kx_geom(K, kblock, &a.P, &a.TP, &a.RW) || N > INT32_MAX / 2 || M > 65535 || N * row_bytes > UINT32_MAX)
     return fail(HQ_EUNSUPPORTED, call, "K=%lld N=%lld", (long long)K, (long long)N);
   a.x = nullptr;
   a.ain = nullptr;
   a.w0 = a.w1 = nullptr;
+  a.s0 = a.z0 = a.s1 = a.z1 = nullptr;
   a.out = nullptr;
   a.aout = nullptr;
   a.M = (int)M;
   a.N = (int)N;
   a.K = (int)K;
-  a.row_bytes = K / 256 * 144;
+  a.G = 0;
+  a.row_bytes = row_bytes;
   a.in_q2 = act_q2_off(M, K);
   a.in_d = act_d_off(M, K);
   a.in_s = act_s_off(M, K);
@@ -423,23 +571,61 @@ static int q4kx_setup(Q4kxArgs &a, int64_t M, int64_t N, int64_t K, const char *
 int launch_gemv_q4kx(const float *x, const void *w0, const void *w1, float *out, int64_t M, int64_t N, int64_t K,
                      int act, hipStream_t s) {
   Q4kxArgs a;
-  if (int rc = q4kx_setup(a, M, N, K, "gemv_q4kx")) return rc;
+  if (int rc = q4kx_setup(a, M, N, K, 256, K / 256 * 144, "gemv_q4kx")) return rc;
   a.x = x;
   a.w0 = static_cast<const uint8_t *>(w0);
   a.w1 = static_cast<const uint8_t *>(w1);
   a.out = out;
   a.act = act;
-  return w1 ? dispatch_q4kx<true, true, false>(a, s) : dispatch_q4kx<false, true, false>(a, s);
+  return w1 ? dispatch_q4kx<Q4kUnit, true, true, false>(a, s) : dispatch_q4kx<Q4kUnit, false, true, false>(a, s);
 }
 
 int launch_gemv_q4kx_act(const void *act_in, const void *w, float *out, int64_t M, int64_t N, int64_t K,
                          hipStream_t s) {
   Q4kxArgs a;
-  if (int rc = q4kx_setup(a, M, N, K, "gemv_q4kx")) return rc;
+  if (int rc = q4kx_setup(a, M, N, K, 256, K / 256 * 144, "gemv_q4kx")) return rc;
   a.ain = static_cast<const uint8_t *>(act_in);
   a.w0 = static_cast<const uint8_t *>(w);
   a.out = out;
-  return dispatch_q4kx<false, false, false>(a, s);
+  return dispatch_q4kx<Q4kUnit, false, false, false>(a, s);
+}
+
+// int4 GEMV on x (F32 / BF16 / F16) quantized in the kernel; y at x's dtype.
+bool int4x_ok(int64_t M, int64_t N, int64_t K, int G, const void *codes, const void *x) {
+  int P, TP, RW;
+  if (M < 1 || M > kGemvMaxRows || G <= 0 || G % 32 || K % G || !q4kx_geom(K, 64, &P, &TP, &RW)) return false;
+  if (N > INT32_MAX / 2 || N * (K / 2) > UINT32_MAX) return false;
+  if (((uintptr_t)codes & 15) || ((uintptr_t)x & 15)) return false;
+  return q4kx_lds(mm_of(M), K, TP, RW, false, true, false) <= 160 * 1024;
+}
+
+int launch_gemv_int4x(const void *x, int x_dtype, const uint32_t *codes, const float *sc, const float *zr, void *y,
+                      int64_t M, int64_t N, int64_t K, int G, void *ws, hipStream_t s) {
+  Q4kxArgs a;
+  if (int rc = q4kx_setup(a, M, N, K, 64, K / 2, "int4_gemv")) return rc;
+  a.w0 = reinterpret_cast<const uint8_t *>(codes);
+  a.s0 = sc;
+  a.z0 = zr;
+  a.G = G;
+  a.out = y;
+  if (!q4kx_xin(K)) {
+    // Long rows: one quantize launch beats every workgroup quantizing all of x.
+    if (int rc = launch_quantize_act(x, x_dtype, ws, M, K, s)) return rc;
+    a.ain = static_cast<const uint8_t *>(ws);
+    switch (x_dtype) {
+      case F32: return dispatch_q4kx<Int4Unit, false, false, false, F32, F32>(a, s);
+      case BF16: return dispatch_q4kx<Int4Unit, false, false, false, F32, BF16>(a, s);
+      case F16: return dispatch_q4kx<Int4Unit, false, false, false, F32, F16>(a, s);
+      default: return fail(HQ_EUNSUPPORTED, "int4_gemv", "x dtype %d", x_dtype);
+    }
+  }
+  a.x = x;
+  switch (x_dtype) {
+    case F32: return dispatch_q4kx<Int4Unit, false, true, false, F32, F32>(a, s);
+    case BF16: return dispatch_q4kx<Int4Unit, false, true, false, BF16, BF16>(a, s);
+    case F16: return dispatch_q4kx<Int4Unit, false, true, false, F16, F16>(a, s);
+    default: return fail(HQ_EUNSUPPORTED, "int4_gemv", "x dtype %d", x_dtype);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -463,7 +649,18 @@ size_t matmul_q_gated_ws_bytes(int64_t M, int64_t N, int64_t K, int dt) {
 
 int launch_matmul_q_gated(const float *x, const void *wg, const void *wu, float *out, int64_t M, int64_t N, int64_t K,
                           int dt, int act, void *ws, hipStream_t s) {
-  if (dt == Q4_K && q4kx_ok(M, N, K, wg, wu, x)) return launch_gemv_q4kx(x, wg, wu, out, M, N, K, act, s);
+  if (dt == Q4_K && q4kx_ok(M, N, K, wg, wu, x)) {
+    if (q4kx_xin(K)) return launch_gemv_q4kx(x, wg, wu, out, M, N, K, act, s);
+    Q4kxArgs a;
+    if (int rc = q4kx_setup(a, M, N, K, 256, K / 256 * 144, "gemv_q4k_gated")) return rc;
+    if (int rc = launch_quantize_act(x, F32, ws, M, K, s)) return rc;
+    a.ain = static_cast<const uint8_t *>(ws);
+    a.w0 = static_cast<const uint8_t *>(wg);
+    a.w1 = static_cast<const uint8_t *>(wu);
+    a.out = out;
+    a.act = act;
+    return dispatch_q4kx<Q4kUnit, true, false, false>(a, s);
+  }
   float *g = static_cast<float *>(ws);
   float *u = reinterpret_cast<float *>(static_cast<char *>(ws) + al256(4 * M * N));
   void *inner = static_cast<char *>(ws) + 2 * al256(4 * M * N);
@@ -479,8 +676,8 @@ static bool mlp_fused_ok(int64_t M, int64_t H, int64_t I, int dt, const void *wg
                          const float *x) {
   int P, TP, RW;
   if (dt != Q4_K || I % 256 || !q4kx_ok(M, I, H, wg, wu, x) || !q4kx_ok(M, H, I, wd, nullptr, x)) return false;
-  if (!q4kx_geom(H, &P, &TP, &RW) || 32 % RW) return false;
-  return q4kx_geom(I, &P, &TP, &RW);
+  if (!q4kx_geom(H, 256, &P, &TP, &RW) || 32 % RW) return false;
+  return q4kx_geom(I, 256, &P, &TP, &RW);
 }
 
 size_t mlp_q_ws_bytes(int64_t M, int64_t H, int64_t I, int dt) {
@@ -496,13 +693,13 @@ int launch_mlp_q(const float *x, const void *wg, const void *wu, const void *wd,
   if (mlp_fused_ok(M, H, I, dt, wg, wu, wd, x)) {
     // Launch 1: gated gate/up on x, output quantized straight into ws (act layout of (M, I)).
     Q4kxArgs a;
-    if (int rc = q4kx_setup(a, M, I, H, "mlp_q")) return rc;
+    if (int rc = q4kx_setup(a, M, I, H, 256, H / 256 * 144, "mlp_q")) return rc;
     a.x = x;
     a.w0 = static_cast<const uint8_t *>(wg);
     a.w1 = static_cast<const uint8_t *>(wu);
     a.aout = static_cast<uint8_t *>(ws);
     a.act = act;
-    if (int rc = dispatch_q4kx<true, true, true>(a, s)) return rc;
+    if (int rc = dispatch_q4kx<Q4kUnit, true, true, true>(a, s)) return rc;
     // Launch 2: down projection on the prepared h.
     return launch_gemv_q4kx_act(ws, wd, out, M, H, I, s);
   }

@@ -295,6 +295,7 @@ int launch_int4_matmul(const void *x, int x_dtype, const uint32_t *codes, const 
     }
     return launch_gemm_int4_bf16(xb, codes, s, z, y, x_dtype, reinterpret_cast<float *>(rest), M, N, K, G, st);
   }
+  if (int4x_ok(M, N, K, G, codes, x)) return launch_gemv_int4x(x, x_dtype, codes, s, z, y, M, N, K, G, ws, st);
   if (int rc = launch_quantize_act(x, x_dtype, ws, M, K, st)) return rc;
   I4Args a;
   a.act = static_cast<const uint8_t *>(ws);

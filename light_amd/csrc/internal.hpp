@@ -69,6 +69,12 @@ int launch_gemv_q4kx(const float *x, const void *w0, const void *w1, float *out,
                      int act, hipStream_t s);
 int launch_gemv_q4kx_act(const void *act_in, const void *w, float *out, int64_t M, int64_t N, int64_t K,
                          hipStream_t s);
+// int4 GEMV on x quantized in the kernel (M <= kGemvMaxRows, G % 32 == 0, K % 64 == 0).
+bool int4x_ok(int64_t M, int64_t N, int64_t K, int G, const void *codes, const void *x);
+int launch_gemv_int4x(const void *x, int x_dtype, const uint32_t *codes, const float *sc, const float *zr, void *y,
+                      int64_t M, int64_t N, int64_t K, int G, void *ws, hipStream_t s);
+// Whether the decode GEMVs quantize x inside their workgroups at this K.
+bool q4kx_xin(int64_t K);
 size_t matmul_q_gated_ws_bytes(int64_t M, int64_t N, int64_t K, int dt);
 size_t mlp_q_ws_bytes(int64_t M, int64_t H, int64_t I, int dt);
 int launch_mlp_q(const float *x, const void *wg, const void *wu, const void *wd, float *out, int64_t M, int64_t H,
