@@ -471,6 +471,188 @@ __global__ __launch_bounds__(512) void gemv_q4kx_kernel(Q4kxArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// MoE grouped decode GEMV (ops.MoEGemmQ, ops/moe.go:101-111, 242-265):
+//   out[p, n] = w(p) * x[row(p)] . dequant(W[e(p)])[n],  row(p) = rpp ? p : p / topk,
+// for the expert-sorted pairs.  grid.y = expert.  Each workgroup finds its expert's pair
+// segment by binary search over the sorted expert ids (the workgroups with blockIdx.x == 0
+// also write Light's counts / offsets scratch), quantizes the x rows of up to MM pairs at
+// a time into LDS, and streams the expert's weight rows as the dense GEMV does.  Teams
+// fit in one wave (K <= 4096).
+// ---------------------------------------------------------------------------
+struct MoeXArgs {
+  Q4kxArgs g;  // w0 = expert stack, N, K, P, TP, RW, row_bytes; x = F32 rows of x
+  const int64_t *pairs, *expts;
+  int32_t *counts, *offsets;
+  const float *topk_w;
+  int64_t size_m, expert_bytes, rows, npairs;
+  int E, topk, rpp;
+};
+
+// Segment j of the sorted expert ids (segment starts: i == 0 or v[i] != v[i-1]), found by
+// one wave: 256 ids per round as four independent loads per lane, ballots of the start
+// flags, and the lane whose start rank is j.  Returns [seg0, seg1), the segment's expert e
+// and the expert before it (eprev, -1 for the first); seg0 = -1 when there is no segment j.
+struct Seg {
+  int64_t seg0, seg1;
+  int e, eprev;
+};
+
+__device__ __forceinline__ Seg find_segment(const int64_t *__restrict__ v, int64_t n, int j, int lane) {
+  Seg sg{-1, n, -1, -1};
+  const uint64_t lt = (1ull << lane) - 1;
+  int64_t cnt = 0;
+  for (int64_t base = 0; base < n; base += 256) {
+    int cur[4], prv[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      int64_t i = base + 64 * c + lane;
+      i = i < n ? i : n - 1;
+      cur[c] = (int)v[i];
+      prv[c] = (int)v[i > 0 ? i - 1 : 0];
+    }
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const int64_t i = base + 64 * c + lane;
+      const bool st = i < n && (i == 0 || cur[c] != prv[c]);
+      const uint64_t m = __ballot(st);
+      const int64_t rank = cnt + __popcll(m & lt);
+      if (sg.seg0 < 0) {
+        const uint64_t hit = __ballot(st && rank == j);
+        if (hit) {
+          const int pos = __ffsll((unsigned long long)hit) - 1;
+          sg.seg0 = base + 64 * c + pos;
+          sg.e = __shfl(cur[c], pos);
+          sg.eprev = sg.seg0 == 0 ? -1 : __shfl(prv[c], pos);
+        }
+      }
+      const uint64_t nxt = __ballot(st && rank == (int64_t)j + 1);
+      if (nxt && sg.seg1 == n) sg.seg1 = base + 64 * c + (__ffsll((unsigned long long)nxt) - 1);
+      cnt += __popcll(m);
+    }
+    if (sg.seg1 < n || cnt > j + 1) break;  // wave-uniform
+  }
+  return sg;
+}
+
+template <class U, int MM>
+__global__ __launch_bounds__(512) void moe_gemv_x_kernel(MoeXArgs ma) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  const Q4kxArgs &a = ma.g;
+  const int t = threadIdx.x, lane = t & 63;
+  const Seg sg = find_segment(ma.expts, ma.npairs, (int)blockIdx.y, lane);
+  if (sg.seg0 < 0) return;
+  const int64_t seg0 = sg.seg0, seg1 = sg.seg1;
+  const int e = sg.e;
+  if (blockIdx.x == 0) {
+    // counts / offsets of the experts (eprev, e], and of (e, E) after the last segment.
+    const int lo = sg.eprev + 1 > 0 ? sg.eprev + 1 : 0;
+    const int hi = seg1 == ma.npairs ? ma.E - 1 : (e < ma.E ? e : ma.E - 1);
+    for (int x = lo + t; x <= hi; x += blockDim.x) {
+      ma.counts[x] = x == e ? (int32_t)(seg1 - seg0) : 0;
+      ma.offsets[x] = x <= e ? (int32_t)seg0 : (int32_t)seg1;
+    }
+    if (seg1 == ma.npairs && t == 0) ma.offsets[ma.E] = (int32_t)seg1;
+  }
+  if (e < 0 || e >= ma.E) return;
+  const uint8_t *w = a.w0 + (int64_t)e * ma.expert_bytes;
+  const int RW = a.RW, KB = a.K >> 5;
+  const int team = t / a.TP, u = t - team * a.TP;
+  const bool active = u < a.P;
+  const typename U::Lane L = unit_lane<U>(active ? u : 0, a.G);
+  const int ngroups = (a.N + RW - 1) / RW;
+  const int G = gridDim.x;
+  const int niter = (ngroups - (int)blockIdx.x + G - 1) / G;
+  if (niter <= 0) return;
+  uint8_t *lq1 = smem, *lq2 = smem + (int64_t)MM * a.K;
+  float2 *lde = reinterpret_cast<float2 *>(smem + 2 * (int64_t)MM * a.K);
+  float *lsx = reinterpret_cast<float *>(smem + 2 * (int64_t)MM * a.K + 8 * (int64_t)MM * KB);
+
+  for (int64_t c0 = seg0; c0 < seg1; c0 += MM) {
+    int64_t pid[MM], xrow[MM];
+#pragma unroll
+    for (int mm = 0; mm < MM; mm++) {
+      int64_t p = c0 + mm < seg1 ? ma.pairs[c0 + mm] : -1;
+      if (p < 0 || p >= ma.size_m) p = -1;
+      pid[mm] = p;
+      int64_t r = p < 0 ? 0 : (ma.rpp ? p : p / ma.topk);
+      xrow[mm] = r < ma.rows ? r : ma.rows - 1;
+    }
+    typename U::W wr;
+    {
+      int row = (int)blockIdx.x * RW + team;
+      row = row < a.N ? row : a.N - 1;
+      U::load(w, a.s0, a.z0, a, row, L, wr);
+    }
+    if (c0 != seg0) __syncthreads();  // every lane has its activations of the previous chunk
+    constexpr int XT = 4;
+    const int ntask = MM * KB * 8;
+    const float *x = static_cast<const float *>(a.x);
+    for (int base = 0; base < ntask; base += XT * (int)blockDim.x) {
+      float4 xv[XT];
+#pragma unroll
+      for (int i = 0; i < XT; i++) {
+        int task = base + i * (int)blockDim.x + t;
+        task = task < ntask ? task : ntask - 1;
+        const int blk = task >> 3, sub = task & 7, mm = blk / KB, kb = blk - mm * KB;
+        int64_t r = 0;
+#pragma unroll
+        for (int k = 0; k < MM; k++) r = k == mm ? xrow[k] : r;
+        xv[i] = *reinterpret_cast<const float4 *>(x + r * a.K + kb * 32 + sub * 4);
+      }
+#pragma unroll
+      for (int i = 0; i < XT; i++) {
+        const int task = base + i * (int)blockDim.x + t;
+        const int blk = task >> 3, sub = task & 7;
+        const float v[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
+        const ActQ q = act_quant8_fast(v);
+        if (task < ntask) {
+          reinterpret_cast<uint32_t *>(lq1 + blk * 32)[sub] = q.q1;
+          reinterpret_cast<uint32_t *>(lq2 + blk * 32)[sub] = q.q2;
+          if (sub == 0) {
+            lde[blk] = make_float2(q.d, q.e);
+            lsx[blk] = q.sum;
+          }
+        }
+      }
+    }
+    __syncthreads();
+    typename U::X xr[MM];
+#pragma unroll
+    for (int mm = 0; mm < MM; mm++)
+      U::load_x(lq1, lq2, reinterpret_cast<const uint8_t *>(lde), reinterpret_cast<const uint8_t *>(lsx),
+                mm * KB + L.ja, xr[mm]);
+    float wp[MM];
+#pragma unroll
+    for (int mm = 0; mm < MM; mm++) wp[mm] = pid[mm] >= 0 && ma.topk_w ? ma.topk_w[pid[mm]] : 1.f;
+
+    for (int it = 0; it < niter; it++) {
+      const int grp = (int)blockIdx.x + it * G;
+      float c[MM];
+      U::template dot<MM>(wr, xr, L, c);
+      {
+        int row = (grp + G) * RW + team;
+        row = row < a.N ? row : a.N - 1;
+        U::load(w, a.s0, a.z0, a, row, L, wr);
+      }
+      const int row = grp * RW + team;
+#pragma unroll
+      for (int mm = 0; mm < MM; mm++) {
+        const float r16 = rsum16(active ? c[mm] : 0.f);
+        const float r0 = rl(r16, 0), r1 = rl(r16, 16), r2 = rl(r16, 32), r3 = rl(r16, 48);
+        float tot;
+        if (a.TP == 64)
+          tot = ((r0 + r1) + r2) + r3;
+        else if (a.TP == 32)
+          tot = lane < 32 ? r0 + r1 : r2 + r3;
+        else
+          tot = lane < 16 ? r0 : (lane < 32 ? r1 : (lane < 48 ? r2 : r3));
+        if (u == 0 && row < a.N && pid[mm] >= 0) static_cast<float *>(a.out)[pid[mm] * a.N + row] = tot * wp[mm];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Launch
 // ---------------------------------------------------------------------------
 
@@ -707,6 +889,55 @@ int launch_mlp_q(const float *x, const void *wg, const void *wu, const void *wd,
   void *inner = static_cast<char *>(ws) + al256(4 * M * I);
   if (int rc = launch_matmul_q_gated(x, wg, wu, h, M, I, H, dt, act, inner, s)) return rc;
   return launch_matmul_q(h, wd, out, M, H, I, dt, inner, s);
+}
+
+bool moe_x_ok(int64_t K, int dt, const void *w, const void *x) {
+  int P, TP, RW;
+  if (dt != Q4_K || !q4kx_geom(K, 256, &P, &TP, &RW) || TP > 64) return false;
+  return ((uintptr_t)w & 15) == 0 && ((uintptr_t)x & 15) == 0;
+}
+
+template <int MM>
+static int run_moe_x(MoeXArgs &ma, int64_t active, hipStream_t s) {
+  const Q4kxArgs &a = ma.g;
+  const size_t lds = (size_t)q4kx_act_lds(MM, a.K);
+  const int ngroups = (a.N + a.RW - 1) / a.RW;
+  // Enough workgroups per active expert to fill the chip (those of empty experts exit).
+  // grid.y = segment slot (at most min(pairs, E) segments); grid.x balanced so that every
+  // workgroup of a slot takes the same number of row groups.
+  int64_t per = cdiv((int64_t)device_cus() * 2, active);
+  per = per < ngroups ? per : ngroups;
+  per = cdiv(ngroups, cdiv(ngroups, per));
+  dim3 grid((unsigned)per, (unsigned)active);
+  moe_gemv_x_kernel<Q4kUnit, MM><<<grid, a.TP * a.RW, lds, s>>>(ma);
+  return check_launch("moe_gemv_x");
+}
+
+int launch_moe_gemv_x(const float *x, const void *w, const int64_t *pairs, const int64_t *expts, int32_t *counts,
+                      int32_t *offsets, const float *topk_w, float *out, int topk, int64_t size_m, int64_t M,
+                      int64_t rows, int64_t E, int64_t N, int64_t K, int rpp, hipStream_t s) {
+  MoeXArgs ma;
+  if (int rc = q4kx_setup(ma.g, 1, N, K, 256, K / 256 * 144, "moe_gemv")) return rc;
+  ma.g.x = x;
+  ma.g.w0 = static_cast<const uint8_t *>(w);
+  ma.g.out = out;
+  ma.pairs = pairs;
+  ma.expts = expts;
+  ma.counts = counts;
+  ma.offsets = offsets;
+  ma.topk_w = topk_w;
+  ma.size_m = size_m;
+  ma.expert_bytes = N * (K / 256 * 144);
+  ma.rows = rows;
+  ma.npairs = M;
+  ma.E = (int)E;
+  ma.topk = topk;
+  ma.rpp = rpp;
+  const int64_t active = M < E ? M : E;
+  const int64_t avg = active > 0 ? (M + active - 1) / active : 1;
+  if (avg <= 1) return run_moe_x<1>(ma, active, s);
+  if (avg <= 2) return run_moe_x<2>(ma, active, s);
+  return run_moe_x<4>(ma, active, s);
 }
 
 }  // namespace hq

@@ -104,6 +104,10 @@ int launch_moe_q(const float *x, const void *w, const int64_t *pairs, const int6
                  int32_t *offsets, const float *topk_w, float *out, int topk, int64_t size_m, int64_t M, int64_t rows,
                  int64_t E, int64_t N, int64_t K, int rpp, int dt, void *ws, hipStream_t s) {
   if (E > INT32_MAX - 1 || M > INT32_MAX || N > INT32_MAX) return fail(HQ_EUNSUPPORTED, "moe_gemm_q", "too large");
+  // Decode: one launch finds the segments, writes counts / offsets, quantizes x and streams.
+  if (M > 0 && E <= 65535 && moe_q4k_fast(dt, K, w) && !moe_use_mfma(M, E) && moe_x_ok(K, dt, w, x))
+    return launch_moe_gemv_x(x, w, pairs, expts, counts, offsets, topk_w, out, topk, size_m, M, rows, E, N, K, rpp,
+                             s);
   moe_offsets_kernel<<<(unsigned)cdiv(E + 1, 256), 256, 0, s>>>(expts, M, (int)E, counts, offsets);
   if (int rc = check_launch("moe_offsets")) return rc;
   if (moe_q4k_fast(dt, K, w)) {

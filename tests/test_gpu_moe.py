@@ -72,7 +72,10 @@ def test_moe_gemm_q_light_shapes(dev, dt, E, weighted):
 
 
 @pytest.mark.parametrize("T,E,topk,N,K", [(1, 8, 2, 64, 512), (5, 32, 4, 300, 1024), (64, 16, 2, 128, 2048),
-                                          (33, 64, 8, 256, 768), (200, 8, 2, 96, 256)])
+                                          (33, 64, 8, 256, 768), (200, 8, 2, 96, 256),
+                                          # decode kernel: several chunks of pairs per expert; K=4096
+                                          # (one-wave teams); K=5120 (falls back to the act GEMV)
+                                          (13, 4, 1, 72, 512), (3, 8, 2, 128, 4096), (2, 4, 2, 40, 5120)])
 def test_moe_gemm_q4_k_shapes(dev, T, E, topk, N, K):
     g = synth.rng(T * 13 + E + N + K)
     w = synth.gguf_weight(hipq.Q4_K, E * N, K, g)
