@@ -46,7 +46,7 @@ enum {
 /* dtype.DType codes (dtype/dtype.go:13-37). */
 enum {
   HQ_F16 = 0, HQ_BF16 = 1, HQ_F32 = 2,
-  HQ_Q8_0 = 17, HQ_Q8_1 = 18, HQ_Q4_K = 21, HQ_Q6_K = 23,
+  HQ_Q4_0 = 13, HQ_Q5_0 = 15, HQ_Q8_0 = 17, HQ_Q8_1 = 18, HQ_Q4_K = 21, HQ_Q5_K = 22, HQ_Q6_K = 23,
 };
 
 /* ---- errors / version ------------------------------------------------- */

@@ -195,7 +195,9 @@ int hq_trace_stop(char *names, int *calls, double *total_us, int n_max) {
 // ops
 // ---------------------------------------------------------------------------
 
-static bool is_gguf(int dt) { return dt == HQ_Q8_0 || dt == HQ_Q4_K || dt == HQ_Q6_K; }
+static bool is_gguf(int dt) {
+  return dt == HQ_Q4_0 || dt == HQ_Q5_0 || dt == HQ_Q8_0 || dt == HQ_Q4_K || dt == HQ_Q5_K || dt == HQ_Q6_K;
+}
 
 size_t hq_matmul_q_ws_bytes(int64_t M, int64_t N, int64_t K, int w_dtype) { return matmul_q_ws_bytes(M, N, K, w_dtype); }
 

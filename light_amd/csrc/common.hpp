@@ -1,7 +1,8 @@
 // common.hpp -- shared definitions for libhipq (gfx950 / CDNA4 only).
 //
 // Formats are GGUF block layouts exactly as Light stores them (dtype/dtype.go:53-60,
-// quant/q8_0.go:10-17, quant/q4_k.go:14-24, quant/q6_k.go:10-20, quant/q8_1.go:10-18):
+// quant/q4_0.go:18-27, quant/q5_0.go:11-20, quant/q8_0.go:10-17, quant/q4_k.go:14-24,
+// quant/q5_k.go:11-22, quant/q6_k.go:10-20, quant/q8_1.go:10-18):
 // the library never repacks a weight, so a tensor's bytes are the GGUF bytes.
 #pragma once
 
@@ -15,7 +16,7 @@ namespace hq {
 // Light's dtype.DType codes (dtype/dtype.go:13-37).
 enum DType : int {
   F16 = HQ_F16, BF16 = HQ_BF16, F32 = HQ_F32,
-  Q8_0 = HQ_Q8_0, Q8_1 = HQ_Q8_1, Q4_K = HQ_Q4_K, Q6_K = HQ_Q6_K,
+  Q4_0 = HQ_Q4_0, Q5_0 = HQ_Q5_0, Q8_0 = HQ_Q8_0, Q8_1 = HQ_Q8_1, Q4_K = HQ_Q4_K, Q5_K = HQ_Q5_K, Q6_K = HQ_Q6_K,
 };
 
 constexpr int kWave = 64;  // CDNA wavefront width
@@ -38,9 +39,12 @@ __host__ __device__ constexpr int64_t act_bytes(int64_t M, int64_t K) {
 // Bytes per block / elements per block (dtype/dtype.go:53-60).
 struct BlockInfo { int elems, bytes; };
 __host__ __device__ constexpr BlockInfo block_info(int dt) {
-  return dt == Q8_0 ? BlockInfo{32, 34}
+  return dt == Q4_0 ? BlockInfo{32, 18}
+       : dt == Q5_0 ? BlockInfo{32, 22}
+       : dt == Q8_0 ? BlockInfo{32, 34}
        : dt == Q8_1 ? BlockInfo{32, 36}
        : dt == Q4_K ? BlockInfo{256, 144}
+       : dt == Q5_K ? BlockInfo{256, 176}
        : dt == Q6_K ? BlockInfo{256, 210}
        : BlockInfo{0, 0};
 }

@@ -4,6 +4,9 @@
 // one 16-byte BF16 store).  The arithmetic is Light's CPU decoders', operation
 // for operation and explicitly rounded, so no multiply-add is fused:
 //   Q8_0  y = d * q                         (kernels/cpu/quant_matmul.go:29-34)
+//   Q4_0  y = d * (q - 8)                   (kernels/cpu/quant_matmul.go:35-42)
+//   Q5_0  y = d * (q5 - 16)                 (kernels/cpu/quant_matmul.go:43-53)
+//   Q5_K  y = (d * sc) * q5 - (dmin * m)    (quant/q5_k.go:50-83)
 //   Q4_K  y = (d * sc) * q - (dmin * m)     (kernels/cpu/quant_matmul.go:54-68)
 //   Q6_K  y = (d * int8 sc) * (raw - 32)    (kernels/cpu/quant_matmul.go:69-87)
 //   Q8_1  y = d * q                         (quant/q8_1.go:21-57)
@@ -47,6 +50,9 @@ static void launch_dt(const uint8_t *w, void *out, int64_t n, int odt, hipStream
 int launch_dequant(const void *src, void *dst, int64_t n, int src_dtype, int out_dtype, hipStream_t s) {
   auto *w = static_cast<const uint8_t *>(src);
   switch (src_dtype) {
+    case Q4_0: launch_dt<Q4_0>(w, dst, n, out_dtype, s); break;
+    case Q5_0: launch_dt<Q5_0>(w, dst, n, out_dtype, s); break;
+    case Q5_K: launch_dt<Q5_K>(w, dst, n, out_dtype, s); break;
     case Q8_0: launch_dt<Q8_0>(w, dst, n, out_dtype, s); break;
     case Q8_1: launch_dt<Q8_1>(w, dst, n, out_dtype, s); break;
     case Q4_K: launch_dt<Q4_K>(w, dst, n, out_dtype, s); break;

@@ -402,14 +402,14 @@ int launch_moe_gemv_q4k(const void *act, const void *w, const int64_t *pairs, co
 }
 
 // ---------------------------------------------------------------------------
-// Q8_0 / Q6_K: LDS-staged rows, one wave per R rows.
+// Q8_0 / Q4_0 / Q5_0 / Q6_K: LDS-staged rows, one wave per R rows.
 // ---------------------------------------------------------------------------
 struct StagedArgs {
   const uint8_t *act;
   const uint8_t *w;
   float *out;
   int M, N, K, nb;
-  int64_t row_bytes, q2_off, d_off;
+  int64_t row_bytes, q2_off, d_off, s_off;
   int lds_wave;  // bytes of LDS per wave
 };
 
@@ -439,9 +439,38 @@ __device__ __forceinline__ void staged_issue(const StagedArgs &a, uint8_t *slice
   }
 }
 
-template <int CPL, int R, int MM>
+// Bit j of n (j < 4) to bit 0 of byte j.
+__device__ __forceinline__ uint32_t spread4(uint32_t n) { return (n * 0x00204081u) & 0x01010101u; }
+
+// 32-element blocks (Q8_0, Q4_0, Q5_0): lane unit = one block.  The block's 32 weights as
+// eight dwords of bytes in element order; Q4_0 / Q5_0 give the unsigned stored values
+// (the offset 8 / 16 is taken off through the block sum of x).
+template <int DT>
+__device__ __forceinline__ void b32_quants(const uint8_t *lds, int o, uint32_t (&qd)[8]) {
+  if constexpr (DT == Q8_0) {
+    lds_unaligned<8>(lds, o + 2, qd);
+  } else {
+    uint32_t qs[4];
+    lds_unaligned<4>(lds, o + (DT == Q4_0 ? 2 : 6), qs);
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      qd[k] = qs[k] & 0x0F0F0F0Fu;
+      qd[4 + k] = (qs[k] >> 4) & 0x0F0F0F0Fu;
+    }
+    if constexpr (DT == Q5_0) {
+      uint32_t qh[1];
+      lds_unaligned<1>(lds, o + 2, qh);
+#pragma unroll
+      for (int k = 0; k < 8; k++) qd[k] |= spread4((qh[0] >> (4 * k)) & 15u) << 4;
+    }
+  }
+}
+
+template <int DT, int CPL, int R, int MM>
 __global__ __launch_bounds__(256) void gemv_q80_kernel(StagedArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
+  constexpr int BB = DT == Q8_0 ? 34 : DT == Q4_0 ? 18 : 22;
+  constexpr float OFF = DT == Q8_0 ? 0.f : DT == Q4_0 ? 8.f : 16.f;
   const int lane = threadIdx.x & 63;
   const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int nwaves = gridDim.x * 4;
@@ -449,6 +478,7 @@ __global__ __launch_bounds__(256) void gemv_q80_kernel(StagedArgs a) {
 
   int xv[MM][CPL][8], yv[MM][CPL][8];
   float2 dx[MM][CPL];
+  float ox[MM][CPL];  // OFF * (sum of the block's x)
 #pragma unroll
   for (int mm = 0; mm < MM; mm++) {
     const int m = m0 + mm < a.M ? m0 + mm : a.M - 1;
@@ -468,6 +498,8 @@ __global__ __launch_bounds__(256) void gemv_q80_kernel(StagedArgs a) {
         yv[mm][i][k] = ok ? U[k] : 0;
       }
       dx[mm][i] = ok ? reinterpret_cast<const float2 *>(a.act + a.d_off)[blk] : make_float2(0.f, 0.f);
+      ox[mm][i] = 0.f;
+      if constexpr (DT != Q8_0) ox[mm][i] = ok ? OFF * reinterpret_cast<const float *>(a.act + a.s_off)[blk] : 0.f;
     }
   }
 
@@ -493,10 +525,10 @@ __global__ __launch_bounds__(256) void gemv_q80_kernel(StagedArgs a) {
 #pragma unroll
       for (int i = 0; i < CPL; i++) {
         const int bl = lane + 64 * i;
-        const int o = r * (int)a.row_bytes + 34 * (bl < a.nb ? bl : 0);
+        const int o = r * (int)a.row_bytes + BB * (bl < a.nb ? bl : 0);
         const float d = h2f(*reinterpret_cast<const uint16_t *>(lds + o));
         uint32_t qd[8];
-        lds_unaligned<8>(lds, o + 2, qd);
+        b32_quants<DT>(lds, o, qd);
 #pragma unroll
         for (int mm = 0; mm < MM; mm++) {
           int dot = 0, dot2 = 0;
@@ -505,7 +537,9 @@ __global__ __launch_bounds__(256) void gemv_q80_kernel(StagedArgs a) {
             dot = dot4((int)qd[k], xv[mm][i][k], dot);
             dot2 = dot4((int)qd[k], yv[mm][i][k], dot2);
           }
-          acc[mm] += d * (dx[mm][i].x * (float)dot + dx[mm][i].y * (float)dot2);
+          float v = dx[mm][i].x * (float)dot + dx[mm][i].y * (float)dot2;
+          if constexpr (DT != Q8_0) v -= ox[mm][i];
+          acc[mm] += d * v;
         }
       }
 #pragma unroll
@@ -673,8 +707,8 @@ bool gemv_fast_ok(int dt, int64_t K, const void *w) {
   if (!bi.elems || K % bi.elems) return false;
   int64_t nb = K / bi.elems, row_bytes = nb * bi.bytes;
   if (row_bytes % 16) return false;
-  if (dt == Q4_K) return nb <= 128;  // team of <= 512 lanes
-  if (!pick_cpl(dt == Q8_0 ? nb : nb * 8)) return false;
+  if (dt == Q4_K || dt == Q5_K) return nb <= 128;  // team of <= 512 lanes
+  if (!pick_cpl(dt == Q6_K ? nb * 8 : nb)) return false;
   return staged_row_bytes(dt, K) + 16 <= 16384;  // one row must fit a wave's LDS slice
 }
 
@@ -703,7 +737,11 @@ static void run_staged(int dt, StagedArgs a, hipStream_t s) {
   const int lds = 8 * a.lds_wave;
   static bool attr_done = false;
   if (!attr_done) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_q80_kernel<CPL, R, MM>),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_q80_kernel<Q8_0, CPL, R, MM>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_q80_kernel<Q4_0, CPL, R, MM>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_q80_kernel<Q5_0, CPL, R, MM>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_q6k_kernel<CPL, R, MM>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
@@ -712,10 +750,12 @@ static void run_staged(int dt, StagedArgs a, hipStream_t s) {
   const int per_cu = (160 * 1024) / lds;
   int64_t wgs = cdiv(cdiv(a.N, R), 4), cap = (int64_t)device_cus() * (per_cu < 2 ? per_cu : 2);
   dim3 g((unsigned)(wgs < cap ? wgs : cap), (unsigned)cdiv(a.M, MM));
-  if (dt == Q8_0)
-    gemv_q80_kernel<CPL, R, MM><<<g, 256, lds, s>>>(a);
-  else
-    gemv_q6k_kernel<CPL, R, MM><<<g, 256, lds, s>>>(a);
+  switch (dt) {
+    case Q8_0: gemv_q80_kernel<Q8_0, CPL, R, MM><<<g, 256, lds, s>>>(a); break;
+    case Q4_0: gemv_q80_kernel<Q4_0, CPL, R, MM><<<g, 256, lds, s>>>(a); break;
+    case Q5_0: gemv_q80_kernel<Q5_0, CPL, R, MM><<<g, 256, lds, s>>>(a); break;
+    default: gemv_q6k_kernel<CPL, R, MM><<<g, 256, lds, s>>>(a); break;
+  }
 }
 
 template <int CPL, int MM>
@@ -757,7 +797,7 @@ int launch_gemv_act(const void *act, const void *wv, float *out, int64_t M, int6
   auto *w = static_cast<const uint8_t *>(wv);
   auto *xa = static_cast<const uint8_t *>(act);
   const int MMc = M >= 3 ? 4 : (int)M;
-  if (dt == Q4_K && q4kx_ok(M, N, K, w, nullptr, act)) return launch_gemv_q4kx_act(act, w, out, M, N, K, s);
+  if (dt == Q4_K && q4kx_ok(M, N, K, w, nullptr, act, Q4_K)) return launch_gemv_q4kx_act(act, w, out, M, N, K, Q4_K, s);
   if (dt == Q4_K) {
     Q4kArgs a;
     a.act = xa;
@@ -780,7 +820,10 @@ int launch_gemv_act(const void *act, const void *wv, float *out, int64_t M, int6
       dispatch_q4k<4>(a, s);
     return check_launch("gemv_q4k");
   }
-  if (dt != Q8_0 && dt != Q6_K) return fail(HQ_EUNSUPPORTED, "gemv", "dtype %d", dt);
+  // Q5_K at any M: the act-input kernel tiles M over grid.y (geometry checked at one row).
+  if (dt == Q5_K && q4kx_ok(1, N, K, w, nullptr, act, Q5_K))
+    return launch_gemv_q4kx_act(act, w, out, M, N, K, Q5_K, s);
+  if (dt != Q8_0 && dt != Q4_0 && dt != Q5_0 && dt != Q6_K) return fail(HQ_EUNSUPPORTED, "gemv", "dtype %d", dt);
   StagedArgs a;
   a.act = xa;
   a.w = w;
@@ -792,8 +835,9 @@ int launch_gemv_act(const void *act, const void *wv, float *out, int64_t M, int6
   a.row_bytes = staged_row_bytes(dt, K);
   a.q2_off = act_q2_off(M, K);
   a.d_off = act_d_off(M, K);
+  a.s_off = act_s_off(M, K);
   a.lds_wave = 0;
-  int cpl = pick_cpl(dt == Q8_0 ? a.nb : (int64_t)a.nb * 8);
+  int cpl = pick_cpl(dt == Q6_K ? (int64_t)a.nb * 8 : a.nb);
   // Q6_K keeps 16 registers of activations per unit and row of x: cap MM at 2.
   int mm = dt == Q6_K && MMc > 2 ? 2 : MMc;
   if (mm == 1)
@@ -802,7 +846,7 @@ int launch_gemv_act(const void *act, const void *wv, float *out, int64_t M, int6
     run_staged_m<2>(dt, a, cpl, s);
   else
     run_staged_m<4>(dt, a, cpl, s);
-  return check_launch(dt == Q8_0 ? "gemv_q80" : "gemv_q6k");
+  return check_launch(dt == Q6_K ? "gemv_q6k" : "gemv_q80");
 }
 
 static int launch_gemv_generic(const float *x, const void *wv, float *out, int64_t M, int64_t N, int64_t K, int dt,
@@ -815,6 +859,9 @@ static int launch_gemv_generic(const float *x, const void *wv, float *out, int64
   switch (dt) {
     case Q4_K: gemv_generic_kernel<Q4_K><<<grid, 256, 0, s>>>(x, w, out, N, K, row_bytes); break;
     case Q8_0: gemv_generic_kernel<Q8_0><<<grid, 256, 0, s>>>(x, w, out, N, K, row_bytes); break;
+    case Q4_0: gemv_generic_kernel<Q4_0><<<grid, 256, 0, s>>>(x, w, out, N, K, row_bytes); break;
+    case Q5_0: gemv_generic_kernel<Q5_0><<<grid, 256, 0, s>>>(x, w, out, N, K, row_bytes); break;
+    case Q5_K: gemv_generic_kernel<Q5_K><<<grid, 256, 0, s>>>(x, w, out, N, K, row_bytes); break;
     case Q6_K: gemv_generic_kernel<Q6_K><<<grid, 256, 0, s>>>(x, w, out, N, K, row_bytes); break;
     default: return fail(HQ_EUNSUPPORTED, "gemv", "dtype %d", dt);
   }
@@ -854,9 +901,10 @@ int launch_matmul_act(const void *act, const void *w, float *out, int64_t M, int
 int launch_matmul_q(const float *x, const void *w, float *out, int64_t M, int64_t N, int64_t K, int dt, void *ws,
                     hipStream_t s) {
   if (use_gemm(M, dt)) return run_gemm(x, false, w, out, M, N, K, ws, s);
-  if (dt == Q4_K && q4kx_ok(M, N, K, w, nullptr, x) && q4kx_xin(K))
-    return launch_gemv_q4kx(x, w, nullptr, out, M, N, K, 0, s);
-  if (!gemv_fast_ok(dt, K, w)) return launch_gemv_generic(x, w, out, M, N, K, dt, s);
+  if ((dt == Q4_K || dt == Q5_K) && q4kx_ok(M, N, K, w, nullptr, x, dt) && q4kx_xin(K))
+    return launch_gemv_q4kx(x, w, nullptr, out, M, N, K, 0, dt, s);
+  if (!gemv_fast_ok(dt, K, w) || (dt == Q5_K && !q4kx_ok(1, N, K, w, nullptr, x, dt)))
+    return launch_gemv_generic(x, w, out, M, N, K, dt, s);
   if (int rc = launch_quantize_act(x, F32, ws, M, K, s)) return rc;
   return launch_gemv_act(ws, w, out, M, N, K, dt, s);
 }

@@ -86,17 +86,22 @@ __host__ __device__ constexpr int64_t q4kx_act_lds(int MM, int64_t K) { return M
 // ---- weight-unit policies --------------------------------------------------------
 // Activations of one unit (two 32-blocks of one row of x), as each policy wants them.
 
-// Q4_K unit: super-block b = u / 4, pair p = u % 4 -> 32 quant bytes (low nibbles =
+// Q4_K / Q5_K unit: super-block b = u / 4, pair p = u % 4 -> 32 quant bytes (low nibbles =
 // sub-block 2p, high = 2p+1) and the block header, broadcast in the block's 4-lane quad.
-struct Q4kUnit {
+// Q5_K (quant/q5_k.go:11-22) adds the 32 qh bytes of the block: bit 2p / 2p+1 of qh[l] is
+// the fifth bit of the pair's low / high element l.
+template <bool Q5>
+struct QkUnit {
+  static constexpr int BB = Q5 ? 176 : 144, QO = Q5 ? 48 : 16;
   struct Lane {
-    uint32_t qoff, hoff;  // byte offsets of the quant chunk / this lane's header dword
-    int ja;               // first 32-block of x
+    uint32_t qoff, hoff, qhoff;  // byte offsets of the quant chunk / this lane's header dword / qh
+    int ja;                      // first 32-block of x
     uint32_t sel, mlo, mhi;
-    int ka;
+    int ka, sh;
   };
   struct W {
     u32x4_t q0, q1;
+    u32x4_t h0, h1;  // Q5_K only
     uint32_t h;
   };
   struct X {
@@ -107,14 +112,16 @@ struct Q4kUnit {
   __device__ static Lane lane(int u) {
     Lane L;
     const int b = u >> 2, p = u & 3;
-    L.qoff = b * 144 + 16 + p * 32;
-    L.hoff = b * 144 + 4 * p;
+    L.qoff = b * BB + QO + p * 32;
+    L.hoff = b * BB + 4 * p;
+    L.qhoff = b * BB + 16;
     L.ja = b * 8 + 2 * p;
     const bool lowj = p < 2;
     L.sel = lowj ? ~0u : 0u;
     L.mlo = lowj ? 0x3F3Fu : 0x0F0Fu;
     L.mhi = lowj ? 0u : 0x3030u;
     L.ka = (2 * p) & 3;
+    L.sh = 2 * p;
     return L;
   }
   // Byte offsets are 32-bit (the host checks N * row_bytes < 2^32), so the loads take the
@@ -124,6 +131,10 @@ struct Q4kUnit {
     const uint32_t ro = (uint32_t)row * (uint32_t)a.row_bytes;
     r.q0 = *reinterpret_cast<const u32x4_t *>(w + (ro + L.qoff));
     r.q1 = *reinterpret_cast<const u32x4_t *>(w + (ro + L.qoff + 16));
+    if constexpr (Q5) {
+      r.h0 = *reinterpret_cast<const u32x4_t *>(w + (ro + L.qhoff));
+      r.h1 = *reinterpret_cast<const u32x4_t *>(w + (ro + L.qhoff + 16));
+    }
     r.h = *reinterpret_cast<const uint32_t *>(w + (ro + L.hoff));
   }
   __device__ static void load_x(const uint8_t *q1, const uint8_t *q2, const uint8_t *de, const uint8_t *sx,
@@ -161,6 +172,12 @@ struct Q4kUnit {
       hi[k] = (w.q0[k] >> 4) & 0x0F0F0F0Fu;
       lo[k + 4] = w.q1[k] & 0x0F0F0F0Fu;
       hi[k + 4] = (w.q1[k] >> 4) & 0x0F0F0F0Fu;
+      if constexpr (Q5) {
+        lo[k] |= ((w.h0[k] >> L.sh) & 0x01010101u) << 4;
+        hi[k] |= ((w.h0[k] >> (L.sh + 1)) & 0x01010101u) << 4;
+        lo[k + 4] |= ((w.h1[k] >> L.sh) & 0x01010101u) << 4;
+        hi[k + 4] |= ((w.h1[k] >> (L.sh + 1)) & 0x01010101u) << 4;
+      }
     }
 #pragma unroll
     for (int mm = 0; mm < MM; mm++) {
@@ -176,6 +193,8 @@ struct Q4kUnit {
     }
   }
 };
+using Q4kUnit = QkUnit<false>;
+using Q5kUnit = QkUnit<true>;
 
 // int4 unit (quant.Int4, quant/int4.go:11-34): 64 elements = code words 8u .. 8u+7 (two
 // 32-blocks A, B); nibble j of word c is element 8c + j, so the low / high nibbles of a
@@ -686,10 +705,10 @@ static size_t q4kx_lds(int MM, int64_t K, int TP, int RW, bool gated, bool xin, 
   return b;
 }
 
-bool q4kx_ok(int64_t M, int64_t N, int64_t K, const void *w0, const void *w1, const void *x) {
+bool q4kx_ok(int64_t M, int64_t N, int64_t K, const void *w0, const void *w1, const void *x, int dt) {
   int P, TP, RW;
-  if (M < 1 || M > kGemvMaxRows || !q4kx_geom(K, 256, &P, &TP, &RW)) return false;
-  if (N > INT32_MAX / 2 || N * (K / 256 * 144) > UINT32_MAX) return false;
+  if ((dt != Q4_K && dt != Q5_K) || M < 1 || M > kGemvMaxRows || !q4kx_geom(K, 256, &P, &TP, &RW)) return false;
+  if (N > INT32_MAX / 2 || N * (K / 256 * block_info(dt).bytes) > UINT32_MAX) return false;
   if (((uintptr_t)w0 & 15) || (w1 && ((uintptr_t)w1 & 15)) || ((uintptr_t)x & 15)) return false;
   return q4kx_lds(mm_of(M), K, TP, RW, w1 != nullptr, true, true) <= 160 * 1024;
 }
@@ -751,24 +770,27 @@ static int q4kx_setup(Q4kxArgs &a, int64_t M, int64_t N, int64_t K, int kblock, 
 }
 
 int launch_gemv_q4kx(const float *x, const void *w0, const void *w1, float *out, int64_t M, int64_t N, int64_t K,
-                     int act, hipStream_t s) {
+                     int act, int dt, hipStream_t s) {
   Q4kxArgs a;
-  if (int rc = q4kx_setup(a, M, N, K, 256, K / 256 * 144, "gemv_q4kx")) return rc;
+  if (int rc = q4kx_setup(a, M, N, K, 256, K / 256 * block_info(dt).bytes, "gemv_q4kx")) return rc;
   a.x = x;
   a.w0 = static_cast<const uint8_t *>(w0);
   a.w1 = static_cast<const uint8_t *>(w1);
   a.out = out;
   a.act = act;
+  if (dt == Q5_K)
+    return w1 ? dispatch_q4kx<Q5kUnit, true, true, false>(a, s) : dispatch_q4kx<Q5kUnit, false, true, false>(a, s);
   return w1 ? dispatch_q4kx<Q4kUnit, true, true, false>(a, s) : dispatch_q4kx<Q4kUnit, false, true, false>(a, s);
 }
 
-int launch_gemv_q4kx_act(const void *act_in, const void *w, float *out, int64_t M, int64_t N, int64_t K,
+int launch_gemv_q4kx_act(const void *act_in, const void *w, float *out, int64_t M, int64_t N, int64_t K, int dt,
                          hipStream_t s) {
   Q4kxArgs a;
-  if (int rc = q4kx_setup(a, M, N, K, 256, K / 256 * 144, "gemv_q4kx")) return rc;
+  if (int rc = q4kx_setup(a, M, N, K, 256, K / 256 * block_info(dt).bytes, "gemv_q4kx")) return rc;
   a.ain = static_cast<const uint8_t *>(act_in);
   a.w0 = static_cast<const uint8_t *>(w);
   a.out = out;
+  if (dt == Q5_K) return dispatch_q4kx<Q5kUnit, false, false, false>(a, s);
   return dispatch_q4kx<Q4kUnit, false, false, false>(a, s);
 }
 
@@ -831,16 +853,17 @@ size_t matmul_q_gated_ws_bytes(int64_t M, int64_t N, int64_t K, int dt) {
 
 int launch_matmul_q_gated(const float *x, const void *wg, const void *wu, float *out, int64_t M, int64_t N, int64_t K,
                           int dt, int act, void *ws, hipStream_t s) {
-  if (dt == Q4_K && q4kx_ok(M, N, K, wg, wu, x)) {
-    if (q4kx_xin(K)) return launch_gemv_q4kx(x, wg, wu, out, M, N, K, act, s);
+  if (q4kx_ok(M, N, K, wg, wu, x, dt)) {
+    if (q4kx_xin(K)) return launch_gemv_q4kx(x, wg, wu, out, M, N, K, act, dt, s);
     Q4kxArgs a;
-    if (int rc = q4kx_setup(a, M, N, K, 256, K / 256 * 144, "gemv_q4k_gated")) return rc;
+    if (int rc = q4kx_setup(a, M, N, K, 256, K / 256 * block_info(dt).bytes, "gemv_q4k_gated")) return rc;
     if (int rc = launch_quantize_act(x, F32, ws, M, K, s)) return rc;
     a.ain = static_cast<const uint8_t *>(ws);
     a.w0 = static_cast<const uint8_t *>(wg);
     a.w1 = static_cast<const uint8_t *>(wu);
     a.out = out;
     a.act = act;
+    if (dt == Q5_K) return dispatch_q4kx<Q5kUnit, true, false, false>(a, s);
     return dispatch_q4kx<Q4kUnit, true, false, false>(a, s);
   }
   float *g = static_cast<float *>(ws);
@@ -852,12 +875,12 @@ int launch_matmul_q_gated(const float *x, const void *wg, const void *wu, float 
   return check_launch("gated_epilogue");
 }
 
-// The two-launch MLP applies: Q4_K, M <= 8, aligned, I a multiple of 256 (the down
+// The two-launch MLP applies: Q4_K / Q5_K, M <= 8, aligned, I a multiple of 256 (the down
 // projection's K) and the gate/up workgroup's teams tile 32-row chunks.
 static bool mlp_fused_ok(int64_t M, int64_t H, int64_t I, int dt, const void *wg, const void *wu, const void *wd,
                          const float *x) {
   int P, TP, RW;
-  if (dt != Q4_K || I % 256 || !q4kx_ok(M, I, H, wg, wu, x) || !q4kx_ok(M, H, I, wd, nullptr, x)) return false;
+  if (I % 256 || !q4kx_ok(M, I, H, wg, wu, x, dt) || !q4kx_ok(M, H, I, wd, nullptr, x, dt)) return false;
   if (!q4kx_geom(H, 256, &P, &TP, &RW) || 32 % RW) return false;
   return q4kx_geom(I, 256, &P, &TP, &RW);
 }
@@ -875,15 +898,17 @@ int launch_mlp_q(const float *x, const void *wg, const void *wu, const void *wd,
   if (mlp_fused_ok(M, H, I, dt, wg, wu, wd, x)) {
     // Launch 1: gated gate/up on x, output quantized straight into ws (act layout of (M, I)).
     Q4kxArgs a;
-    if (int rc = q4kx_setup(a, M, I, H, 256, H / 256 * 144, "mlp_q")) return rc;
+    if (int rc = q4kx_setup(a, M, I, H, 256, H / 256 * block_info(dt).bytes, "mlp_q")) return rc;
     a.x = x;
     a.w0 = static_cast<const uint8_t *>(wg);
     a.w1 = static_cast<const uint8_t *>(wu);
     a.aout = static_cast<uint8_t *>(ws);
     a.act = act;
-    if (int rc = dispatch_q4kx<Q4kUnit, true, true, true>(a, s)) return rc;
+    const int rc = dt == Q5_K ? dispatch_q4kx<Q5kUnit, true, true, true>(a, s)
+                              : dispatch_q4kx<Q4kUnit, true, true, true>(a, s);
+    if (rc) return rc;
     // Launch 2: down projection on the prepared h.
-    return launch_gemv_q4kx_act(ws, wd, out, M, H, I, s);
+    return launch_gemv_q4kx_act(ws, wd, out, M, H, I, dt, s);
   }
   float *h = static_cast<float *>(ws);
   void *inner = static_cast<char *>(ws) + al256(4 * M * I);
@@ -893,11 +918,11 @@ int launch_mlp_q(const float *x, const void *wg, const void *wu, const void *wd,
 
 bool moe_x_ok(int64_t K, int dt, const void *w, const void *x) {
   int P, TP, RW;
-  if (dt != Q4_K || !q4kx_geom(K, 256, &P, &TP, &RW) || TP > 64) return false;
+  if ((dt != Q4_K && dt != Q5_K) || !q4kx_geom(K, 256, &P, &TP, &RW) || TP > 64) return false;
   return ((uintptr_t)w & 15) == 0 && ((uintptr_t)x & 15) == 0;
 }
 
-template <int MM>
+template <class U, int MM>
 static int run_moe_x(MoeXArgs &ma, int64_t active, hipStream_t s) {
   const Q4kxArgs &a = ma.g;
   const size_t lds = (size_t)q4kx_act_lds(MM, a.K);
@@ -909,15 +934,16 @@ static int run_moe_x(MoeXArgs &ma, int64_t active, hipStream_t s) {
   per = per < ngroups ? per : ngroups;
   per = cdiv(ngroups, cdiv(ngroups, per));
   dim3 grid((unsigned)per, (unsigned)active);
-  moe_gemv_x_kernel<Q4kUnit, MM><<<grid, a.TP * a.RW, lds, s>>>(ma);
+  moe_gemv_x_kernel<U, MM><<<grid, a.TP * a.RW, lds, s>>>(ma);
   return check_launch("moe_gemv_x");
 }
 
 int launch_moe_gemv_x(const float *x, const void *w, const int64_t *pairs, const int64_t *expts, int32_t *counts,
                       int32_t *offsets, const float *topk_w, float *out, int topk, int64_t size_m, int64_t M,
-                      int64_t rows, int64_t E, int64_t N, int64_t K, int rpp, hipStream_t s) {
+                      int64_t rows, int64_t E, int64_t N, int64_t K, int rpp, int dt, hipStream_t s) {
   MoeXArgs ma;
-  if (int rc = q4kx_setup(ma.g, 1, N, K, 256, K / 256 * 144, "moe_gemv")) return rc;
+  const int64_t row_bytes = K / 256 * block_info(dt).bytes;
+  if (int rc = q4kx_setup(ma.g, 1, N, K, 256, row_bytes, "moe_gemv")) return rc;
   ma.g.x = x;
   ma.g.w0 = static_cast<const uint8_t *>(w);
   ma.g.out = out;
@@ -927,7 +953,7 @@ int launch_moe_gemv_x(const float *x, const void *w, const int64_t *pairs, const
   ma.offsets = offsets;
   ma.topk_w = topk_w;
   ma.size_m = size_m;
-  ma.expert_bytes = N * (K / 256 * 144);
+  ma.expert_bytes = N * row_bytes;
   ma.rows = rows;
   ma.npairs = M;
   ma.E = (int)E;
@@ -935,9 +961,14 @@ int launch_moe_gemv_x(const float *x, const void *w, const int64_t *pairs, const
   ma.rpp = rpp;
   const int64_t active = M < E ? M : E;
   const int64_t avg = active > 0 ? (M + active - 1) / active : 1;
-  if (avg <= 1) return run_moe_x<1>(ma, active, s);
-  if (avg <= 2) return run_moe_x<2>(ma, active, s);
-  return run_moe_x<4>(ma, active, s);
+  if (dt == Q5_K) {
+    if (avg <= 1) return run_moe_x<Q5kUnit, 1>(ma, active, s);
+    if (avg <= 2) return run_moe_x<Q5kUnit, 2>(ma, active, s);
+    return run_moe_x<Q5kUnit, 4>(ma, active, s);
+  }
+  if (avg <= 1) return run_moe_x<Q4kUnit, 1>(ma, active, s);
+  if (avg <= 2) return run_moe_x<Q4kUnit, 2>(ma, active, s);
+  return run_moe_x<Q4kUnit, 4>(ma, active, s);
 }
 
 }  // namespace hq

@@ -64,10 +64,10 @@ int device_cus();
 // Q4_K GEMV on F32 x quantized in LDS (M <= kGemvMaxRows); w1 != NULL: gated pair,
 // out = act(x.w0) * (x.w1), act 0 = SiLU, 1 = GELU (erf).
 // x: F32 x or prepared activations (16-byte aligned); w1 may be NULL.
-bool q4kx_ok(int64_t M, int64_t N, int64_t K, const void *w0, const void *w1, const void *x);
+bool q4kx_ok(int64_t M, int64_t N, int64_t K, const void *w0, const void *w1, const void *x, int dt);
 int launch_gemv_q4kx(const float *x, const void *w0, const void *w1, float *out, int64_t M, int64_t N, int64_t K,
-                     int act, hipStream_t s);
-int launch_gemv_q4kx_act(const void *act_in, const void *w, float *out, int64_t M, int64_t N, int64_t K,
+                     int act, int dt, hipStream_t s);
+int launch_gemv_q4kx_act(const void *act_in, const void *w, float *out, int64_t M, int64_t N, int64_t K, int dt,
                          hipStream_t s);
 // int4 GEMV on x quantized in the kernel (M <= kGemvMaxRows, G % 32 == 0, K % 64 == 0).
 bool int4x_ok(int64_t M, int64_t N, int64_t K, int G, const void *codes, const void *x);
@@ -96,7 +96,7 @@ int launch_moe_q(const float *x, const void *w, const int64_t *pairs, const int6
 bool moe_x_ok(int64_t K, int dt, const void *w, const void *x);
 int launch_moe_gemv_x(const float *x, const void *w, const int64_t *pairs, const int64_t *expts, int32_t *counts,
                       int32_t *offsets, const float *topk_w, float *out, int topk, int64_t size_m, int64_t M,
-                      int64_t rows, int64_t E, int64_t N, int64_t K, int rpp, hipStream_t s);
+                      int64_t rows, int64_t E, int64_t N, int64_t K, int rpp, int dt, hipStream_t s);
 int launch_moe_gemv_q4k(const void *act, const void *w, const int64_t *pairs, const int32_t *offsets,
                         const float *topk_w, float *out, int topk, int64_t size_m, int64_t M, int64_t rows,
                         int64_t E, int64_t N, int64_t K, int rpp, hipStream_t s);

@@ -105,9 +105,10 @@ int launch_moe_q(const float *x, const void *w, const int64_t *pairs, const int6
                  int64_t E, int64_t N, int64_t K, int rpp, int dt, void *ws, hipStream_t s) {
   if (E > INT32_MAX - 1 || M > INT32_MAX || N > INT32_MAX) return fail(HQ_EUNSUPPORTED, "moe_gemm_q", "too large");
   // Decode: one launch finds the segments, writes counts / offsets, quantizes x and streams.
-  if (M > 0 && E <= 65535 && moe_q4k_fast(dt, K, w) && !moe_use_mfma(M, E) && moe_x_ok(K, dt, w, x))
+  // (Q5_K takes it at every M: it has no grouped MFMA kernel.)
+  if (M > 0 && E <= 65535 && (dt == Q5_K || !moe_use_mfma(M, E)) && moe_x_ok(K, dt, w, x))
     return launch_moe_gemv_x(x, w, pairs, expts, counts, offsets, topk_w, out, topk, size_m, M, rows, E, N, K, rpp,
-                             s);
+                             dt, s);
   moe_offsets_kernel<<<(unsigned)cdiv(E + 1, 256), 256, 0, s>>>(expts, M, (int)E, counts, offsets);
   if (int rc = check_launch("moe_offsets")) return rc;
   if (moe_q4k_fast(dt, K, w)) {
@@ -127,6 +128,9 @@ int launch_moe_q(const float *x, const void *w, const int64_t *pairs, const int6
   switch (dt) {
     case Q4_K: moe_generic_kernel<Q4_K><<<grid, 256, 0, s>>>(x, wb, pairs, offsets, topk_w, out, size_m, N, K, topk, rpp); break;
     case Q8_0: moe_generic_kernel<Q8_0><<<grid, 256, 0, s>>>(x, wb, pairs, offsets, topk_w, out, size_m, N, K, topk, rpp); break;
+    case Q4_0: moe_generic_kernel<Q4_0><<<grid, 256, 0, s>>>(x, wb, pairs, offsets, topk_w, out, size_m, N, K, topk, rpp); break;
+    case Q5_0: moe_generic_kernel<Q5_0><<<grid, 256, 0, s>>>(x, wb, pairs, offsets, topk_w, out, size_m, N, K, topk, rpp); break;
+    case Q5_K: moe_generic_kernel<Q5_K><<<grid, 256, 0, s>>>(x, wb, pairs, offsets, topk_w, out, size_m, N, K, topk, rpp); break;
     case Q6_K: moe_generic_kernel<Q6_K><<<grid, 256, 0, s>>>(x, wb, pairs, offsets, topk_w, out, size_m, N, K, topk, rpp); break;
     default: return fail(HQ_EUNSUPPORTED, "moe_gemm_q", "dtype %d", dt);
   }

@@ -13,9 +13,11 @@ LIB_PATH = os.path.join(_HERE, "libhipq.so")
 
 # Light dtype.DType codes (dtype/dtype.go:13-37).
 F16, BF16, F32 = 0, 1, 2
-Q8_0, Q8_1, Q4_K, Q6_K = 17, 18, 21, 23
-BLOCK = {Q8_0: (32, 34), Q8_1: (32, 36), Q4_K: (256, 144), Q6_K: (256, 210)}
-NAMES = {F16: "F16", BF16: "BF16", F32: "F32", Q8_0: "Q8_0", Q8_1: "Q8_1", Q4_K: "Q4_K", Q6_K: "Q6_K"}
+Q4_0, Q5_0, Q8_0, Q8_1, Q4_K, Q5_K, Q6_K = 13, 15, 17, 18, 21, 22, 23
+BLOCK = {Q4_0: (32, 18), Q5_0: (32, 22), Q8_0: (32, 34), Q8_1: (32, 36), Q4_K: (256, 144), Q5_K: (256, 176),
+         Q6_K: (256, 210)}
+NAMES = {F16: "F16", BF16: "BF16", F32: "F32", Q4_0: "Q4_0", Q5_0: "Q5_0", Q8_0: "Q8_0", Q8_1: "Q8_1",
+         Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K"}
 
 HQ_OK, HQ_EINVAL, HQ_EUNSUPPORTED, HQ_ENOMEM = 0, -1, -2, -3
 

@@ -8,7 +8,8 @@
 namespace light {
 namespace {
 
-const DType kGGUF[] = {DType::Q8_0, DType::Q4_K, DType::Q6_K};
+// The six formats Light fuses on CUDA (kernels/cuda/matmul_q.go:17-24, moe.go:78-82).
+const DType kGGUF[] = {DType::Q4_0, DType::Q5_0, DType::Q8_0, DType::Q4_K, DType::Q5_K, DType::Q6_K};
 
 void matmul_q(Context &c) {
   const Tensor &x = c.in(0), &w = c.in(1);

@@ -10,6 +10,9 @@ buildQ6_KBlock, quant/q6_k_test.go:20-59).  Distributions:
          (the configs leave the Q4_K d / dmin distribution open; this is the
          stated choice, the same law as Q6_K's d).
 * Q6_K:  raw ~ U[0, 63], int8 sc ~ U[-32, 31], d = f16(|N(0,1)| * 1e-3).
+* Q4_0 / Q5_0 (not benchmark configs; parity cases): q ~ U over the format's
+         range, d = f16(|N(0,1)| * 0.02 / 8) and f16(|N(0,1)| * 0.02 / 16).
+* Q5_K:  as Q4_K with q5 ~ U[0, 31].
 * int4:  codes u32 uniform, s = f16(|N(0,1)| * 0.01) widened to F32,
          z ~ U[0, 15] as F32, group 128.
 * MoE:   expert ids uniform without replacement per token, routing weights
@@ -18,7 +21,7 @@ buildQ6_KBlock, quant/q6_k_test.go:20-59).  Distributions:
 """
 import numpy as np
 
-Q8_0, Q4_K, Q6_K = 17, 21, 23
+Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K = 13, 15, 17, 21, 22, 23
 
 
 def rng(seed):
@@ -53,6 +56,43 @@ def pack_q4_k(d_bits, dmin_bits, sc, mn, q):
     out[:, 4:16] = s12
     q = q.astype(np.uint8).reshape(nb, 4, 2, 32)  # (p, lo/hi, l)
     out[:, 16:] = (q[:, :, 0, :] | (q[:, :, 1, :] << 4)).reshape(nb, 128)
+    return out.reshape(-1)
+
+
+def pack_q4_0(d_bits, q):
+    """q (nb, 32) in [0, 15] (stored nibbles; value = q - 8) -> (nb*18,) uint8 (quant/q4_0.go:18-27)."""
+    nb = d_bits.shape[0]
+    q = q.astype(np.uint8)
+    out = np.empty((nb, 18), np.uint8)
+    out[:, 0:2] = d_bits.astype("<u2").view(np.uint8).reshape(nb, 2)
+    out[:, 2:] = (q[:, :16] & 0x0F) | ((q[:, 16:] & 0x0F) << 4)
+    return out.reshape(-1)
+
+
+def pack_q5_0(d_bits, q):
+    """q (nb, 32) in [0, 31] (value = q - 16) -> (nb*22,) uint8 (quant/q5_0.go:11-20)."""
+    nb = d_bits.shape[0]
+    q = q.astype(np.uint32)
+    out = np.empty((nb, 22), np.uint8)
+    out[:, 0:2] = d_bits.astype("<u2").view(np.uint8).reshape(nb, 2)
+    qh = (((q >> 4) & 1) << np.arange(32, dtype=np.uint32)[None, :]).sum(axis=1).astype("<u4")
+    out[:, 2:6] = qh.view(np.uint8).reshape(nb, 4)
+    out[:, 6:] = ((q[:, :16] & 0x0F) | ((q[:, 16:] & 0x0F) << 4)).astype(np.uint8)
+    return out.reshape(-1)
+
+
+def pack_q5_k(d_bits, dmin_bits, sc, mn, q):
+    """q (nb, 256) in [0, 31] -> (nb*176,) uint8: Q4_K's header, qh[32], Q4_K's qs (quant/q5_k.go:11-22)."""
+    nb = d_bits.shape[0]
+    q = q.astype(np.uint8)
+    q4 = pack_q4_k(d_bits, dmin_bits, sc, mn, q & 0x0F).reshape(nb, 144)
+    hb = ((q >> 4) & 1).reshape(nb, 4, 2, 32)  # (p, lo/hi, l) -> bit 2p + lo/hi of qh[l]
+    sh = (2 * np.arange(4)[:, None] + np.arange(2)[None, :]).astype(np.uint8)
+    qh = (hb << sh[None, :, :, None]).sum(axis=(1, 2)).astype(np.uint8)
+    out = np.empty((nb, 176), np.uint8)
+    out[:, 0:16] = q4[:, 0:16]
+    out[:, 16:48] = qh
+    out[:, 48:] = q4[:, 16:]
     return out.reshape(-1)
 
 
@@ -94,6 +134,20 @@ def gguf_weight(dt, N, K, g):
         sc = g.integers(-32, 32, size=(nb, 16), dtype=np.int8)
         raw = g.integers(0, 64, size=(nb, 256), dtype=np.uint8)
         return pack_q6_k(d, sc, raw)
+    if dt in (Q4_0, Q5_0):
+        nb = N * K // 32
+        hi = 16 if dt == Q4_0 else 32
+        d = _f16_bits(np.abs(g.standard_normal(nb, dtype=np.float32)) * np.float32(0.02 / (hi // 2)))
+        q = g.integers(0, hi, size=(nb, 32), dtype=np.uint8)
+        return pack_q4_0(d, q) if dt == Q4_0 else pack_q5_0(d, q)
+    if dt == Q5_K:
+        nb = N * K // 256
+        d = _f16_bits(np.abs(g.standard_normal(nb, dtype=np.float32)) * np.float32(1e-3))
+        dmin = _f16_bits(np.abs(g.standard_normal(nb, dtype=np.float32)) * np.float32(1e-3))
+        sc = g.integers(0, 64, size=(nb, 8), dtype=np.uint8)
+        mn = g.integers(0, 64, size=(nb, 8), dtype=np.uint8)
+        q = g.integers(0, 32, size=(nb, 256), dtype=np.uint8)
+        return pack_q5_k(d, dmin, sc, mn, q)
     raise ValueError(f"dtype {dt}")
 
 

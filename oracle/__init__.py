@@ -11,10 +11,12 @@ Parity status of each function (how it is pinned):
 * ``half_to_f32`` / ``half_from_f32`` / ``bf16_from_f32``: all 65536 f16
   patterns against numpy's IEEE conversion; f32 -> f16 / bf16 on 2^20 random
   patterns plus ties against numpy / torch round-to-nearest-even.
-* ``decode_row`` / ``dequant`` (Q8_0, Q4_K, Q6_K): Light's known-answer tests
-  (quant/q4_k_test.go, quant/q6_k_test.go) as golden fixtures, scalar vs AVX2
-  bit identity (Light's TestAVX2DecodersExact), closed forms on special
-  blocks (q = 0, scale = 0, min = 0).
+* ``decode_row`` / ``dequant`` (Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K): Light's
+  known-answer tests (quant/q4_0_test.go, quant/others_test.go,
+  quant/q4_k_test.go, quant/q5_k_test.go, quant/q6_k_test.go) as golden
+  fixtures, scalar vs AVX2 bit identity (Light's TestAVX2DecodersExact),
+  closed forms on special blocks (q = 0, scale = 0, min = 0), and Q5_K with
+  every fifth bit clear against Q4_K on the same header and nibbles.
 * ``int4_row`` / ``int4_dequant``: scalar vs AVX2 bit identity; closed forms
   (codes all equal, z = q) and the BF16 round-once rule.
 * ``dot`` / ``mattb``: intrinsics vs a lane-by-lane scalar encoding of the same
@@ -38,8 +40,9 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "liboracle.so")
 
 F16, BF16, F32 = 0, 1, 2
-Q8_0, Q8_1, Q4_K, Q6_K = 17, 18, 21, 23
-BLOCK = {Q8_0: (32, 34), Q8_1: (32, 36), Q4_K: (256, 144), Q6_K: (256, 210)}
+Q4_0, Q5_0, Q8_0, Q8_1, Q4_K, Q5_K, Q6_K = 13, 15, 17, 18, 21, 22, 23
+BLOCK = {Q4_0: (32, 18), Q5_0: (32, 22), Q8_0: (32, 34), Q8_1: (32, 36), Q4_K: (256, 144), Q5_K: (256, 176),
+         Q6_K: (256, 210)}
 
 _lib = None
 

@@ -119,6 +119,54 @@ static void dec_q8_0(const uint8_t *b, float *dst) {
   for (int i = 0; i < 32; i++) dst[i] = d * (float)(int8_t)b[2 + i];
 }
 
+/* Q4_0: kernels/cpu/quant_matmul.go:35-42 (= quant/q4_0.go dequantQ4_0CPU); y = d*(q - 8). */
+static void dec_q4_0(const uint8_t *b, float *dst) {
+  float d = f16le(b);
+  for (int j = 0; j < 16; j++) {
+    uint8_t q = b[2 + j];
+    dst[j] = d * (float)((int)(q & 15) - 8);
+    dst[j + 16] = d * (float)((int)(q >> 4) - 8);
+  }
+}
+
+/* Q5_0: kernels/cpu/quant_matmul.go:43-53 (= quant/q5_0.go:56-67); fifth bit of element j is
+ * bit j of the little-endian u32 qh; y = d*(q5 - 16). */
+static void dec_q5_0(const uint8_t *b, float *dst) {
+  float d = f16le(b);
+  uint32_t qh = (uint32_t)b[2] | (uint32_t)b[3] << 8 | (uint32_t)b[4] << 16 | (uint32_t)b[5] << 24;
+  for (int j = 0; j < 16; j++) {
+    uint8_t q = b[6 + j];
+    int lo = (q & 15) | (int)((qh >> j) & 1) << 4;
+    int hi = (q >> 4) | (int)((qh >> (j + 16)) & 1) << 4;
+    dst[j] = d * (float)(lo - 16);
+    dst[j + 16] = d * (float)(hi - 16);
+  }
+}
+
+/* Q5_K: quant/q5_k.go:50-83 (DequantQ5_K; Light's CPU matmul_q has no Q5_K decoder):
+ * Q4_K's header, qh[32] where bit 2p / 2p+1 of qh[l] is the fifth bit of element
+ * p*64+l / p*64+32+l, then Q4_K's qs; y = (d*sc)*q5 - dmin*m, unfused. */
+static void dec_q5_k(const uint8_t *b, float *dst) {
+  float d = f16le(b), dmin = f16le(b + 2);
+  const uint8_t *scales = b + 4, *qh = b + 16, *qs = b + 48;
+  for (int p = 0; p < 4; p++) {
+    uint8_t sc0, m0, sc1, m1;
+    scale_min_k4(2 * p, scales, &sc0, &m0);
+    scale_min_k4(2 * p + 1, scales, &sc1, &m1);
+    float d1 = d * (float)sc0, mo1 = dmin * (float)m0;
+    float d2 = d * (float)sc1, mo2 = dmin * (float)m1;
+    for (int l = 0; l < 32; l++) {
+      uint8_t q = qs[p * 32 + l];
+      int lo = (q & 15) | ((qh[l] >> (2 * p)) & 1) << 4;
+      int hi = (q >> 4) | ((qh[l] >> (2 * p + 1)) & 1) << 4;
+      float a = d1 * (float)lo;
+      float c = d2 * (float)hi;
+      dst[p * 64 + l] = a - mo1;
+      dst[p * 64 + 32 + l] = c - mo2;
+    }
+  }
+}
+
 /* Q4_K: kernels/cpu/quant_matmul.go:54-68; y = (d*sc)*q - dmin*m, unfused. */
 static void dec_q4_k(const uint8_t *b, float *dst) {
   float d = f16le(b), dmin = f16le(b + 2);
@@ -170,9 +218,12 @@ static void dec_q8_1(const uint8_t *b, float *dst) {
 
 static int block_info(int dt, int *elems, int *bytes) {
   switch (dt) {
+    case OR_Q4_0: *elems = 32; *bytes = 18; return 0;
+    case OR_Q5_0: *elems = 32; *bytes = 22; return 0;
     case OR_Q8_0: *elems = 32; *bytes = 34; return 0;
     case OR_Q8_1: *elems = 32; *bytes = 36; return 0;
     case OR_Q4_K: *elems = 256; *bytes = 144; return 0;
+    case OR_Q5_K: *elems = 256; *bytes = 176; return 0;
     case OR_Q6_K: *elems = 256; *bytes = 210; return 0;
   }
   return -1;
@@ -185,6 +236,9 @@ int or_decode_row(int dt, const uint8_t *raw, int64_t K, float *dst) {
     const uint8_t *blk = raw + b * bb;
     float *o = dst + b * be;
     switch (dt) {
+      case OR_Q4_0: dec_q4_0(blk, o); break;
+      case OR_Q5_0: dec_q5_0(blk, o); break;
+      case OR_Q5_K: dec_q5_k(blk, o); break;
       case OR_Q8_0: dec_q8_0(blk, o); break;
       case OR_Q8_1: dec_q8_1(blk, o); break;
       case OR_Q4_K: dec_q4_k(blk, o); break;
@@ -206,6 +260,35 @@ int or_decode_row_avx2(int dt, const uint8_t *raw, int64_t K, float *dst) {
       for (int c = 0; c < 4; c++) {
         __m256i v = _mm256_cvtepi8_epi32(_mm_loadl_epi64((const __m128i *)(s + 2 + 8 * c)));
         _mm256_storeu_ps(dst + b * 32 + 8 * c, _mm256_mul_ps(d, _mm256_cvtepi32_ps(v)));
+      }
+    }
+    return 0;
+  }
+  if (dt == OR_Q4_0 || dt == OR_Q5_0) {
+    /* q4_0RowAVX2 / q5_0RowAVX2 (qdecode_amd64.s:68-158): per 8-element half, the low and
+     * high nibbles (plus the qh bit for Q5_0) minus the offset, converted, times d. */
+    if (K % 32) return -1;
+    const int q5 = dt == OR_Q5_0, bb = q5 ? 22 : 18, qo = q5 ? 6 : 2;
+    const __m256i m15 = _mm256_set1_epi32(15), one = _mm256_set1_epi32(1);
+    const __m256i off = _mm256_set1_epi32(q5 ? 16 : 8), sh0 = _mm256_setr_epi32(0, 1, 2, 3, 4, 5, 6, 7);
+    for (int64_t b = 0; b < K / 32; b++) {
+      const uint8_t *s = raw + b * bb;
+      __m256 d = _mm256_set1_ps(f16le(s));
+      uint32_t qhv = q5 ? ((uint32_t)s[2] | (uint32_t)s[3] << 8 | (uint32_t)s[4] << 16 | (uint32_t)s[5] << 24) : 0;
+      __m256i qh = _mm256_set1_epi32((int)qhv);
+      for (int h = 0; h < 2; h++) {
+        __m256i v = _mm256_cvtepu8_epi32(_mm_loadl_epi64((const __m128i *)(s + qo + 8 * h)));
+        __m256i lo = _mm256_and_si256(v, m15), hi = _mm256_srli_epi32(v, 4);
+        if (q5) {
+          __m256i shl = _mm256_add_epi32(sh0, _mm256_set1_epi32(8 * h));
+          __m256i shh = _mm256_add_epi32(sh0, _mm256_set1_epi32(16 + 8 * h));
+          lo = _mm256_or_si256(lo, _mm256_slli_epi32(_mm256_and_si256(_mm256_srlv_epi32(qh, shl), one), 4));
+          hi = _mm256_or_si256(hi, _mm256_slli_epi32(_mm256_and_si256(_mm256_srlv_epi32(qh, shh), one), 4));
+        }
+        lo = _mm256_sub_epi32(lo, off);
+        hi = _mm256_sub_epi32(hi, off);
+        _mm256_storeu_ps(dst + b * 32 + 8 * h, _mm256_mul_ps(_mm256_cvtepi32_ps(lo), d));
+        _mm256_storeu_ps(dst + b * 32 + 16 + 8 * h, _mm256_mul_ps(_mm256_cvtepi32_ps(hi), d));
       }
     }
     return 0;
@@ -503,10 +586,38 @@ static void gguf_decode(void *p, int64_t n, float *dst) {
   or_decode_row_avx2(c->dt, c->w + n * c->row_bytes, c->K, dst);
 }
 
+/* matmulF32Fast's x * W^T case, kernels/cpu/matmul_f32.go:30-48: parallel over output
+ * columns with grain max(1, 32768 / (K*M + 1)), MatTB over tiles of 48 weight rows. */
+typedef struct {
+  const float *x, *w;
+  float *out;
+  int64_t M, K, N;
+} mmt_ctx;
+
+static void mmt_range(void *p, int64_t lo, int64_t hi) {
+  mmt_ctx *c = (mmt_ctx *)p;
+  for (int64_t j0 = lo; j0 < hi; j0 += TILE_ROWS) {
+    int64_t j1 = j0 + TILE_ROWS < hi ? j0 + TILE_ROWS : hi;
+    or_mattb(c->x, c->K, c->w + j0 * c->K, c->K, c->out + j0, c->N, c->M, j1 - j0, c->K);
+  }
+}
+
 int or_matmul_q(const float *x, const uint8_t *w, float *out, int64_t M, int64_t N, int64_t K, int dt,
                 int threads) {
   int be, bb;
   if (block_info(dt, &be, &bb) || dt == OR_Q8_1 || K % be) return -1;
+  if (dt == OR_Q5_K) {
+    /* No CPU matmul_q kernel for Q5_K: ops.MatMulQ falls back to quant.Dequantize + MatMul
+     * (ops/matmul_q.go:60-66, 85-95). */
+    float *wf = (float *)malloc(sizeof(float) * (size_t)(N * K));
+    if (!wf) return -2;
+    or_dequant(dt, w, N * K, wf);
+    mmt_ctx c = {x, wf, out, M, K, N};
+    int64_t grain = 32768 / (K * M + 1);
+    par_for(N, grain < 1 ? 1 : grain, threads, mmt_range, &c);
+    free(wf);
+    return 0;
+  }
   gguf_dctx d = {w, K / be * bb, K, dt};
   rows_times_x(x, out, M, K, N, gguf_decode, &d, threads);
   return 0;

@@ -28,7 +28,7 @@ extern "C" {
 
 enum {
   OR_F16 = 0, OR_BF16 = 1, OR_F32 = 2,
-  OR_Q8_0 = 17, OR_Q8_1 = 18, OR_Q4_K = 21, OR_Q6_K = 23,
+  OR_Q4_0 = 13, OR_Q5_0 = 15, OR_Q8_0 = 17, OR_Q8_1 = 18, OR_Q4_K = 21, OR_Q5_K = 22, OR_Q6_K = 23,
 };
 
 /* dtype/half.go */

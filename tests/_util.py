@@ -27,7 +27,7 @@ def max_rel(got, want):
 
 def random_blocks(rng, dt, N, K):
     """Light's randomQuantBlocks (ops/matmul_q_test.go:16-56): random bytes, f16 scale fields in [2^-6, 2^-5)."""
-    be, bb = {17: (32, 34), 21: (256, 144), 23: (256, 210)}[dt]
+    be, bb = {13: (32, 18), 15: (32, 22), 17: (32, 34), 21: (256, 144), 22: (256, 176), 23: (256, 210)}[dt]
     nb = N * K // be
     buf = rng.integers(0, 256, size=(nb, bb), dtype=np.uint8)
 
@@ -35,9 +35,9 @@ def random_blocks(rng, dt, N, K):
         v = (0x2400 | rng.integers(0, 0x400, size=nb)).astype("<u2")
         return v.view(np.uint8).reshape(nb, 2)
 
-    if dt == 17:
+    if dt in (13, 15, 17):
         buf[:, 0:2] = small()
-    elif dt == 21:
+    elif dt in (21, 22):
         buf[:, 0:2] = small()
         buf[:, 2:4] = small()
     else:

@@ -47,7 +47,7 @@ def test_gated_q4_k_fused(dev, act, M, K):
     _check(dev, hipq.Q4_K, M, 333, K, act, seed=M * 7 + K + act)
 
 
-@pytest.mark.parametrize("dt", [hipq.Q8_0, hipq.Q6_K])
+@pytest.mark.parametrize("dt", [hipq.Q4_0, hipq.Q5_0, hipq.Q8_0, hipq.Q5_K, hipq.Q6_K])
 @pytest.mark.parametrize("M", [1, 4])
 def test_gated_other_formats(dev, dt, M):
     _check(dev, dt, M, 200, 1024, hipq.ACT_SILU, seed=dt + M)
@@ -99,11 +99,16 @@ def test_mlp_q4_k_fused(dev, M, act):
     _check_mlp(dev, hipq.Q4_K, M, 1024, 2816, act, seed=300 + M + act)
 
 
+@pytest.mark.parametrize("M", [1, 5])
+def test_mlp_q5_k_fused(dev, M):
+    _check_mlp(dev, hipq.Q5_K, M, 1024, 2816, hipq.ACT_SILU, seed=500 + M)
+
+
 @pytest.mark.parametrize("H,I", [(4096, 14336), (2048, 768), (512, 256), (256, 1024)])
 def test_mlp_q4_k_shapes(dev, H, I):
     _check_mlp(dev, hipq.Q4_K, 1, H, I, hipq.ACT_SILU, seed=H + I)
 
 
-@pytest.mark.parametrize("dt,M", [(hipq.Q8_0, 1), (hipq.Q6_K, 2), (hipq.Q4_K, 12)])
+@pytest.mark.parametrize("dt,M", [(hipq.Q8_0, 1), (hipq.Q6_K, 2), (hipq.Q4_K, 12), (hipq.Q4_0, 1), (hipq.Q5_0, 3)])
 def test_mlp_unfused_paths(dev, dt, M):
     _check_mlp(dev, dt, M, 512, 768, hipq.ACT_SILU, seed=dt * 3 + M)

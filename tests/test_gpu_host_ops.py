@@ -18,14 +18,14 @@ pytestmark = pytest.mark.gpu
 
 DEV = "ROCm(0)"
 TOL = 1e-3
-NAME = {hipq.Q8_0: "Q8_0", hipq.Q4_K: "Q4_K", hipq.Q6_K: "Q6_K"}
+NAME = hipq.NAMES
 
 
 def dev_t(a, dt, shape):
     return L.from_numpy(np.ascontiguousarray(a), dt, list(shape), DEV)
 
 
-@pytest.mark.parametrize("dt", [hipq.Q8_0, hipq.Q4_K, hipq.Q6_K])
+@pytest.mark.parametrize("dt", [hipq.Q4_0, hipq.Q5_0, hipq.Q8_0, hipq.Q4_K, hipq.Q5_K, hipq.Q6_K])
 @pytest.mark.parametrize("M", [1, 5, 40])
 def test_matmul_q(dt, M):
     print(f"[case] host MatMulQ {NAME[dt]} M={M}", flush=True)
@@ -41,7 +41,7 @@ def test_matmul_q(dt, M):
     assert norm_err(got, want, np.linalg.norm(wd, axis=1), np.linalg.norm(x, axis=1)) <= TOL
 
 
-@pytest.mark.parametrize("dt", [hipq.Q8_0, hipq.Q4_K, hipq.Q6_K])
+@pytest.mark.parametrize("dt", [hipq.Q4_0, hipq.Q5_0, hipq.Q8_0, hipq.Q4_K, hipq.Q5_K, hipq.Q6_K])
 def test_dequantize_bit_exact(dt):
     g = synth.rng(200 + dt)
     N, K = 16, 512
@@ -80,7 +80,7 @@ def test_matmul_int4(M, act_order):
     assert norm_err(y.numpy(), want, np.linalg.norm(wd, axis=1), np.linalg.norm(xg, axis=1)) <= TOL
 
 
-@pytest.mark.parametrize("dt", [hipq.Q4_K, hipq.Q6_K])
+@pytest.mark.parametrize("dt", [hipq.Q4_0, hipq.Q5_0, hipq.Q4_K, hipq.Q5_K, hipq.Q6_K])
 @pytest.mark.parametrize("T,E,topk", [(1, 8, 2), (40, 4, 2)])
 def test_moe_pipeline(dt, T, E, topk):
     """MoERouteFromIDs -> MoEGemmQ (per-token rows, routing weights) -> MoECombine."""

@@ -17,7 +17,7 @@ from light_amd import hipq, synth
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-3  # max |err| / (||w_n|| ||x_m||)
-FMTS = [hipq.Q8_0, hipq.Q4_K, hipq.Q6_K]
+FMTS = [hipq.Q4_0, hipq.Q5_0, hipq.Q8_0, hipq.Q4_K, hipq.Q5_K, hipq.Q6_K]
 
 
 def _t(a, dev):
@@ -81,7 +81,7 @@ def test_dequant_golden_known_answers(dev):
     import os
     cases = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "dequant_kat.json")))["cases"]
     for c in cases:
-        dt = {"Q4_K": hipq.Q4_K, "Q6_K": hipq.Q6_K}[c["dtype"]]
+        dt = {n: d for d, n in hipq.NAMES.items()}[c["dtype"]]
         raw = np.frombuffer(bytes.fromhex(c["blocks"]), np.uint8).copy()
         got = hipq.dequant(_t(raw, dev), c["n"], dt).cpu().numpy()
         if c["checks"] == "all":
@@ -206,15 +206,44 @@ def test_matmul_q_act_equals_matmul_q(dev, dt, M):
     act = hipq.quantize_act(x)
     y2 = hipq.matmul_q_act(act, w, M, N, K, dt)
     torch.cuda.synchronize()
-    if dt != hipq.Q4_K:
+    if dt not in (hipq.Q4_K, hipq.Q5_K):
         assert torch.equal(y1, y2)
     else:
-        # The Q4_K GEMV quantizes x inside its workgroups (reciprocal-based scales): the two
+        # The Q4_K / Q5_K GEMV quantizes x inside its workgroups (reciprocal-based scales): the two
         # paths agree to the activation quantization's own error, far inside the bar.
         ref = torch.from_numpy(oracle.matmul_q(x.cpu().numpy(), w.cpu().numpy(), N, K, dt)).to(dev)
         assert ((y1 - y2).abs().max() <= 1e-4 * ref.abs().max()).item()
     _check_matmul(dev, dt, x.cpu().numpy(), w.cpu().numpy(), N, K, "act")
     _check_matmul(dev, dt, x.cpu().numpy(), w.cpu().numpy(), N, K, "act", got=y2.cpu().numpy())
+
+
+@pytest.mark.parametrize("dt", [hipq.Q4_0, hipq.Q5_0, hipq.Q5_K])
+@pytest.mark.parametrize("M", [1, 3, 8, 12, 40])
+def test_matmul_q_added_formats_rows(dev, dt, M):
+    """Q4_0 / Q5_0 / Q5_K (kernels/cuda/matmul_q.go:17-24) at decode and small prefill rows,
+    against Light's CPU path (Q5_K: its dequant + MatMul fallback)."""
+    g = np.random.default_rng(70 + M + dt)
+    N, K = 96, 2048
+    w = synth.gguf_weight(dt, N, K, g)
+    x = synth.activations(M, K, g)
+    _check_matmul(dev, dt, x, w, N, K, "added_formats")
+
+
+def test_matmul_q_q5_0_high_bits_only(dev):
+    """Q5_0 with zero nibbles and every fifth bit set (q5 = 16 -> 0) or clear (-16): pins the
+    qh bit order in the GEMV against the closed form."""
+    g = np.random.default_rng(4)
+    N, K = 8, 256
+    nb = N * K // 32
+    q = 16 * g.integers(0, 2, size=(nb, 32))
+    d = synth._f16_bits(np.full(nb, 0.5, np.float32))
+    w = synth.pack_q5_0(d, q)
+    x = synth.activations(1, K, g)
+    wd = 0.5 * (q.reshape(N, K) - 16).astype(np.float64)
+    want = wd @ x[0].astype(np.float64)
+    got = hipq.matmul_q(_t(x, dev), _t(w, dev), N, K, hipq.Q5_0).cpu().numpy()[0]
+    assert np.max(np.abs(got - want) / (np.linalg.norm(wd, axis=1) * np.linalg.norm(x[0]))) <= TOL
+    _check_matmul(dev, hipq.Q5_0, x, w, N, K, "q5_0_high_bits")
 
 
 # ---- Q4_K prefill GEMM (MFMA) ----------------------------------------------

@@ -57,7 +57,7 @@ def _check(dev, x, w, dt, E, N, K, ids, tw, topk, weighted, sample=None):
     assert np.all(np.isfinite(got))
 
 
-@pytest.mark.parametrize("dt", [hipq.Q4_K, hipq.Q8_0, hipq.Q6_K])
+@pytest.mark.parametrize("dt", [hipq.Q4_K, hipq.Q8_0, hipq.Q6_K, hipq.Q4_0, hipq.Q5_0, hipq.Q5_K])
 @pytest.mark.parametrize("E", [3, 16])  # E=3: 42 pairs > 4E -> MFMA path for Q4_K; E=16: grouped GEMV
 @pytest.mark.parametrize("weighted", [False, True])
 def test_moe_gemm_q_light_shapes(dev, dt, E, weighted):

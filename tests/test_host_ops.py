@@ -22,7 +22,7 @@ def q(dt, N, K):
     return L.from_numpy(np.zeros(L.byte_size(dt, N * K), np.uint8), dt, [N, K])
 
 
-GGUF = ["Q8_0", "Q4_K", "Q6_K"]
+GGUF = ["Q4_0", "Q5_0", "Q8_0", "Q4_K", "Q5_K", "Q6_K"]
 
 
 def test_registered_rocm_keys():
@@ -56,7 +56,8 @@ def test_matmul_q_fused_on():
     for dt in GGUF:
         assert L.matmul_q_fused_on("ROCm", dt)
         assert not L.matmul_q_fused_on("CPU", dt)
-    assert not L.matmul_q_fused_on("ROCm", "Q5_K")
+    for dt in ("Q4_1", "Q5_1", "Q2_K", "Q3_K", "Q8_K"):  # no fused kernel: ops.MatMulQ falls back
+        assert not L.matmul_q_fused_on("ROCm", dt)
 
 
 def test_tensor_roundtrip_and_sizes():
@@ -65,6 +66,7 @@ def test_tensor_roundtrip_and_sizes():
     assert t.shape == [3, 4] and t.dtype == "F32" and t.device == "CPU"
     assert np.array_equal(t.numpy(), a)
     assert L.byte_size("Q4_K", 512) == 288 and L.byte_size("Q8_0", 64) == 68 and L.byte_size("Q6_K", 256) == 210
+    assert L.byte_size("Q4_0", 64) == 36 and L.byte_size("Q5_0", 64) == 44 and L.byte_size("Q5_K", 512) == 352
     with pytest.raises(L.Error, match="bytes for F32"):
         L.from_numpy(a, "F32", [4, 4])
     assert t.reshape([2, 6]).shape == [2, 6]

@@ -16,7 +16,8 @@ import oracle
 from _util import light_bound_ok, max_rel, random_blocks
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "dequant_kat.json")
-DT = {"Q8_0": oracle.Q8_0, "Q4_K": oracle.Q4_K, "Q6_K": oracle.Q6_K}
+DT = {"Q4_0": oracle.Q4_0, "Q5_0": oracle.Q5_0, "Q8_0": oracle.Q8_0, "Q4_K": oracle.Q4_K, "Q5_K": oracle.Q5_K,
+      "Q6_K": oracle.Q6_K}
 
 
 # ---- dtype/half.go -------------------------------------------------------
@@ -92,7 +93,7 @@ def test_dequant_known_answers(case, avx2):
 
 # ---- decoders: scalar vs AVX2 bit identity + closed forms ---------------
 
-@pytest.mark.parametrize("dt", [oracle.Q8_0, oracle.Q4_K, oracle.Q6_K])
+@pytest.mark.parametrize("dt", [oracle.Q4_0, oracle.Q5_0, oracle.Q8_0, oracle.Q4_K, oracle.Q6_K])
 def test_avx2_decoders_exact(dt):
     """TestAVX2DecodersExact (kernels/cpu/qdecode_test.go:38-82)."""
     g = np.random.default_rng(dt)
@@ -135,6 +136,45 @@ def test_q6_k_closed_forms():
     i = np.arange(256)
     want = (np.float32(0.5) * (i // 16 - 8).astype(np.float32)) * ((i % 64) - 32).astype(np.float32)
     assert np.array_equal(y, want.astype(np.float32))
+
+
+def test_q4_0_q5_0_closed_forms():
+    """Element order (low nibbles 0..15, high 16..31; qh bit j = element j) pinned by q = index."""
+    from light_amd import synth
+    d = np.array([np.float16(0.375).view(np.uint16)])
+    q = np.arange(32).reshape(1, 32)
+    y = oracle.decode_row(oracle.Q4_0, synth.pack_q4_0(d, q % 16), 32)
+    assert np.array_equal(y, np.float32(0.375) * ((q[0] % 16) - 8).astype(np.float32))
+    y = oracle.decode_row(oracle.Q5_0, synth.pack_q5_0(d, q), 32)
+    assert np.array_equal(y, np.float32(0.375) * (q[0] - 16).astype(np.float32))
+    # qh bits only: q = 16 * (index odd) -> every odd element 0, even -16 d.
+    q = (16 * (np.arange(32) % 2)).reshape(1, 32)
+    y = oracle.decode_row(oracle.Q5_0, synth.pack_q5_0(d, q), 32, avx2=True)
+    assert np.array_equal(y, np.float32(0.375) * (q[0] - 16).astype(np.float32))
+
+
+def test_q5_k_reduces_to_q4_k():
+    """Q5_K with every fifth bit clear equals Q4_K on the same header and nibbles; a set fifth
+    bit adds exactly 16 (d sc) before the min is subtracted."""
+    from light_amd import synth
+    g = np.random.default_rng(9)
+    nb = 6
+    d = synth._f16_bits(np.abs(g.standard_normal(nb)) * 1e-2)
+    dmin = synth._f16_bits(np.abs(g.standard_normal(nb)) * 1e-2)
+    sc = g.integers(0, 64, size=(nb, 8))
+    mn = g.integers(0, 64, size=(nb, 8))
+    q = g.integers(0, 16, size=(nb, 256))
+    a = oracle.decode_row(oracle.Q5_K, synth.pack_q5_k(d, dmin, sc, mn, q), nb * 256)
+    b = oracle.decode_row(oracle.Q4_K, synth.pack_q4_k(d, dmin, sc, mn, q), nb * 256)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    c = oracle.decode_row(oracle.Q5_K, synth.pack_q5_k(d, dmin, sc, mn, q + 16), nb * 256)
+    df = d.view(np.float16).astype(np.float32)
+    dm = dmin.view(np.float16).astype(np.float32)
+    j = np.arange(256) // 32
+    for b_ in range(nb):
+        ds = df[b_] * sc[b_, j].astype(np.float32)
+        want = ds * (q[b_] + 16).astype(np.float32) - dm[b_] * mn[b_, j].astype(np.float32)
+        assert np.array_equal(c[b_ * 256:(b_ + 1) * 256], want.astype(np.float32))
 
 
 def test_q8_0_closed_form():
@@ -204,7 +244,7 @@ def test_mattb_tiles_match_dot():
 
 # ---- Light's CPU qmatmul ------------------------------------------------
 
-@pytest.mark.parametrize("dt", [oracle.Q8_0, oracle.Q4_K, oracle.Q6_K])
+@pytest.mark.parametrize("dt", [oracle.Q4_0, oracle.Q5_0, oracle.Q8_0, oracle.Q4_K, oracle.Q5_K, oracle.Q6_K])
 @pytest.mark.parametrize("M", [1, 9])
 def test_matmul_q_vs_f64(dt, M):
     """TestMatMulQCPUKernels (ops/matmul_q_cpu_test.go:19-81): N=37, K=512, bound 1e-5 (1 + sum|xw|)."""
@@ -218,7 +258,7 @@ def test_matmul_q_vs_f64(dt, M):
     assert light_bound_ok(y, ref, mag)
 
 
-@pytest.mark.parametrize("dt", [oracle.Q8_0, oracle.Q4_K, oracle.Q6_K])
+@pytest.mark.parametrize("dt", [oracle.Q4_0, oracle.Q5_0, oracle.Q8_0, oracle.Q4_K, oracle.Q5_K, oracle.Q6_K])
 def test_matmul_q_matches_dequant_matmul(dt):
     """TestMatMulQCPUMatchesDequant (ops/matmul_q_test.go:75-103): rel 1e-5 vs dequant + MatMul."""
     g = np.random.default_rng(3 + dt)
