@@ -224,7 +224,7 @@ def table(args, dev):
     import torch
     from light_amd import hipq, synth
     rows = []
-    for name, c in synth.CONFIGS.items():
+    for name, c in list(synth.CONFIGS.items()) + list(synth.EXTRA_CONFIGS.items()):
         g = synth.rng(c["cfg"])
         try:
             if c["kind"] == "gguf":

@@ -35,11 +35,11 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int WBN = 128, WBK = 64;
 constexpr int NR = 4;                 // raw weight stages (loads issued NR-1 steps ahead)
-constexpr int R_WAVE = 2048;          // raw bytes per producer wave per stage (1 KB + 1 KB)
-constexpr int R_STAGE = 4 * R_WAVE;
 constexpr int B_STAGE = WBN * WBK * 2;  // 16 KB of bf16 B, two stages
 
-template <int BM>
+// WF::R_WAVE: raw bytes per producer wave per stage.  WF::DIRECT: the raw stage already is
+// bf16 B in fragment order (no dequant step, no separate B stages).
+template <int BM, class WF>
 struct WsTile {
   static constexpr int A_STAGE = BM * WBK * 2;         // bf16 A per step
   static constexpr int NA = BM == 256 ? 3 : 5;          // A stages (loads issued NA-1 steps ahead)
@@ -47,9 +47,10 @@ struct WsTile {
   static constexpr int A_PER_WAVE = A_BLOCKS / 4;       // direct loads per producer wave per step
   static constexpr int WM = BM == 256 ? 2 : 2, WN = 2;  // consumer waves along M / N
   static constexpr int MT = BM / WM / 32, NT = WBN / WN / 32;
+  static constexpr int R_STAGE = 4 * WF::R_WAVE;
   static constexpr int R_OFF = NA * A_STAGE;
   static constexpr int B_OFF = R_OFF + NR * R_STAGE;
-  static constexpr int LDS = B_OFF + 2 * B_STAGE;
+  static constexpr int LDS = B_OFF + (WF::DIRECT ? 0 : 2 * B_STAGE);
 };
 
 __device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
@@ -77,6 +78,8 @@ struct WsArgs {
 // (32h + r) * 16; [1 KB, 2 KB) headers, row r at 1024 + 16 r.
 struct WsQ4k {
   static constexpr int RAW_LOADS = 2;  // direct loads per producer wave per step
+  static constexpr int R_WAVE = 2048;  // 1 KB qs + 1 KB headers
+  static constexpr bool DIRECT = false;
   __device__ static void issue_raw(const WsArgs &a, int row_base, int lane, int k0, uint32_t dst) {
     const int p = (k0 >> 6) & 3;
     const int64_t blk = (int64_t)(k0 >> 8) * 144;
@@ -117,6 +120,8 @@ struct WsQ4k {
 // [1 KB, 1 KB + 128) scales, [1 KB + 128, 1 KB + 256) zeros.
 struct WsInt4 {
   static constexpr int RAW_LOADS = 2;
+  static constexpr int R_WAVE = 2048;
+  static constexpr bool DIRECT = false;
   __device__ static void issue_raw(const WsArgs &a, int row_base, int lane, int k0, uint32_t dst) {
     int r = row_base + (lane & 31);
     r = r < a.N ? r : a.N - 1;
@@ -146,9 +151,27 @@ struct WsInt4 {
   }
 };
 
+// bf16 weights (N, K) row-major (a GGUF format dequantized once, bit-exact, to bf16): the
+// wave's 32 rows x 64 k land by direct loads straight in MFMA fragment order, 1 KB per
+// 16-k piece kk: lane l holds row l % 32, k = 16 kk + 8 (l / 32) .. + 8.
+struct WsBf16 {
+  static constexpr int RAW_LOADS = 4;
+  static constexpr int R_WAVE = 4096;
+  static constexpr bool DIRECT = true;
+  __device__ static void issue_raw(const WsArgs &a, int row_base, int lane, int k0, uint32_t dst) {
+#pragma unroll
+    for (int kk = 0; kk < 4; kk++) {
+      int r = row_base + (lane & 31);
+      r = r < a.N ? r : a.N - 1;
+      dma16(a.w + (int64_t)r * a.row_bytes + 2 * (k0 + 16 * kk + 8 * (lane >> 5)), dst + 1024 * kk);
+    }
+  }
+  __device__ static void dequant(const WsArgs &, const uint8_t *, int, int, int, float *, float *) {}
+};
+
 template <class WF, int BM>
 __global__ __launch_bounds__(512) void gemm_ws_kernel(WsArgs a) {
-  using T = WsTile<BM>;
+  using T = WsTile<BM, WF>;
   extern __shared__ __align__(16) uint8_t smem[];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
@@ -177,7 +200,8 @@ __global__ __launch_bounds__(512) void gemm_ws_kernel(WsArgs a) {
     auto issue = [&](int st) {
       // Raw weights of step st, then A of step st - (NR - T::NA) ... both at fixed counts.
       const int k0 = kofs(st);
-      WF::issue_raw(a, n0 + pw * 32, lane, k0, __builtin_amdgcn_readfirstlane(lds0 + T::R_OFF + (st % NR) * R_STAGE + pw * R_WAVE));
+      WF::issue_raw(a, n0 + pw * 32, lane, k0,
+                    __builtin_amdgcn_readfirstlane(lds0 + T::R_OFF + (st % NR) * T::R_STAGE + pw * WF::R_WAVE));
     };
     auto issue_a = [&](int st) {
       const int k0 = kofs(st);
@@ -193,7 +217,8 @@ __global__ __launch_bounds__(512) void gemm_ws_kernel(WsArgs a) {
       }
     };
     auto dequant = [&](int st) {
-      const uint8_t *raw = smem + T::R_OFF + (st % NR) * R_STAGE + pw * R_WAVE;
+      if constexpr (WF::DIRECT) return;
+      const uint8_t *raw = smem + T::R_OFF + (st % NR) * T::R_STAGE + pw * WF::R_WAVE;
       float lo[16], hi[16];
       WF::dequant(a, raw, rrow, bh, kofs(st), lo, hi);
       uint8_t *bs = smem + T::B_OFF + (st & 1) * B_STAGE;
@@ -242,7 +267,7 @@ __global__ __launch_bounds__(512) void gemm_ws_kernel(WsArgs a) {
       if (s + 1 < nsteps) {
         // raw(s+1) was issued NR-2 iterations ago; its A part and the later iterations follow.
         wait_vm<T::A_PER_WAVE + PER_IT * (NR - 2)>();
-        dequant(s + 1);
+        dequant(s + 1);  // (DIRECT: nothing to convert; the wait alone publishes B(s+1))
       }
       // A(s+1): issued NA-2 iterations ago, followed by the later iterations' loads.
       wait_vm<PER_IT * (T::NA - 2)>();
@@ -264,7 +289,7 @@ __global__ __launch_bounds__(512) void gemm_ws_kernel(WsArgs a) {
     const int fr = lane & 31, fh = lane >> 5;
     for (int s = 0; s < nsteps; s++) {
       const uint8_t *sa = smem + (s % T::NA) * T::A_STAGE;
-      const uint8_t *sb = smem + T::B_OFF + (s & 1) * B_STAGE;
+      const uint8_t *sb = WF::DIRECT ? smem + T::R_OFF + (s % NR) * T::R_STAGE : smem + T::B_OFF + (s & 1) * B_STAGE;
       bf16x8 af[2][T::MT], bfr[2][T::NT];
 #define WS_LOAD_FRAGS(BUF, KK)                                                                          \
   do {                                                                                                  \
@@ -326,7 +351,7 @@ int launch_splitk_reduce(const float *part, void *out, int out_dtype, int64_t n,
 
 template <class WF, int BM>
 static int launch_ws_t(WsArgs a, int out_dtype, void *out, float *partials, hipStream_t s) {
-  using T = WsTile<BM>;
+  using T = WsTile<BM, WF>;
   static bool attr_set[64] = {false};
   int dev = 0;
   (void)hipGetDevice(&dev);
@@ -368,6 +393,19 @@ int launch_gemm_ws_q4k(const uint16_t *xb, const void *w, float *out, float *par
   a.G = 256;
   a.row_bytes = K / 256 * 144;
   return launch_ws<WsQ4k>(a, F32, out, partials, s);
+}
+
+int launch_gemm_ws_bf16(const uint16_t *xb, const uint16_t *wb, float *out, float *partials, int64_t M, int64_t N,
+                        int64_t K, hipStream_t s) {
+  WsArgs a = {};
+  a.x = xb;
+  a.w = reinterpret_cast<const uint8_t *>(wb);
+  a.M = (int)M;
+  a.N = (int)N;
+  a.K = (int)K;
+  a.G = 0;
+  a.row_bytes = K * 2;
+  return launch_ws<WsBf16>(a, F32, out, partials, s);
 }
 
 int launch_gemm_ws_int4(const uint16_t *xb, const uint32_t *codes, const float *sc, const float *zr, void *out,

@@ -868,39 +868,54 @@ static int launch_gemv_generic(const float *x, const void *wv, float *out, int64
   return check_launch("gemv_generic");
 }
 
-bool use_gemm(int64_t M, int dt) { return dt == Q4_K && M > kGemvMaxRows; }
+// Many rows: the MFMA GEMM.  Q4_K dequantizes inside the GEMM; the other formats are
+// dequantized once, bit-exact, to bf16 in the workspace and run the same GEMM on bf16 B.
+// The K argument is checked where it is known (K % 64 for the 64-wide K step).
+bool use_gemm(int64_t M, int dt) { return M > kGemvMaxRows; }
 
-static size_t gemm_ws(int64_t M, int64_t N, int64_t K) { return gemm_q4k_ws_bytes(M, K) + gemm_q4k_partial_bytes(M, N, K); }
+static bool gemm_k_ok(int64_t K) { return K % 64 == 0; }
+
+static int64_t al256(int64_t b) { return (b + 255) & ~(int64_t)255; }
+
+static size_t gemm_ws(int64_t M, int64_t N, int64_t K, int dt) {
+  const size_t wb = dt == Q4_K ? 0 : (size_t)al256(N * K * 2);
+  return al256((int64_t)gemm_q4k_ws_bytes(M, K)) + al256((int64_t)gemm_q4k_partial_bytes(M, N, K)) + wb;
+}
 
 size_t matmul_q_ws_bytes(int64_t M, int64_t N, int64_t K, int dt) {
   if (M <= 0 || K <= 0 || K % 32) return 0;
-  return use_gemm(M, dt) ? gemm_ws(M, N, K) : (size_t)act_bytes(M, K);
+  return use_gemm(M, dt) && gemm_k_ok(K) ? gemm_ws(M, N, K, dt) : (size_t)act_bytes(M, K);
 }
 
 size_t matmul_act_ws_bytes(int64_t M, int64_t N, int64_t K, int dt) {
   if (M <= 0 || K <= 0 || K % 32) return 0;
-  return use_gemm(M, dt) ? gemm_ws(M, N, K) : 0;
+  return use_gemm(M, dt) && gemm_k_ok(K) ? gemm_ws(M, N, K, dt) : 0;
 }
 
 const char *matmul_q_kernel_name(int64_t M, int dt) { return use_gemm(M, dt) ? "matmul_q.gemm" : "matmul_q.gemv"; }
 
 static int run_gemm(const void *src, bool from_act, const void *w, float *out, int64_t M, int64_t N, int64_t K,
-                    void *ws, hipStream_t s) {
-  auto *xb = static_cast<uint16_t *>(ws);
-  float *partials = reinterpret_cast<float *>(static_cast<char *>(ws) + gemm_q4k_ws_bytes(M, K));
+                    int dt, void *ws, hipStream_t s) {
+  char *base = static_cast<char *>(ws);
+  auto *xb = reinterpret_cast<uint16_t *>(base);
+  float *partials = reinterpret_cast<float *>(base + al256((int64_t)gemm_q4k_ws_bytes(M, K)));
   if (int rc = launch_to_bf16(src, from_act ? kActSrc : F32, xb, M, K, s)) return rc;
-  return launch_gemm_q4k_bf16(xb, w, out, partials, M, N, K, s);
+  if (dt == Q4_K) return launch_gemm_q4k_bf16(xb, w, out, partials, M, N, K, s);
+  auto *wb = reinterpret_cast<uint16_t *>(base + al256((int64_t)gemm_q4k_ws_bytes(M, K)) +
+                                          al256((int64_t)gemm_q4k_partial_bytes(M, N, K)));
+  if (int rc = launch_dequant(w, wb, N * K, dt, BF16, s)) return rc;
+  return launch_gemm_ws_bf16(xb, wb, out, partials, M, N, K, s);
 }
 
 int launch_matmul_act(const void *act, const void *w, float *out, int64_t M, int64_t N, int64_t K, int dt, void *ws,
                       hipStream_t s) {
-  if (use_gemm(M, dt)) return run_gemm(act, true, w, out, M, N, K, ws, s);
+  if (use_gemm(M, dt) && gemm_k_ok(K)) return run_gemm(act, true, w, out, M, N, K, dt, ws, s);
   return launch_gemv_act(act, w, out, M, N, K, dt, s);
 }
 
 int launch_matmul_q(const float *x, const void *w, float *out, int64_t M, int64_t N, int64_t K, int dt, void *ws,
                     hipStream_t s) {
-  if (use_gemm(M, dt)) return run_gemm(x, false, w, out, M, N, K, ws, s);
+  if (use_gemm(M, dt) && gemm_k_ok(K)) return run_gemm(x, false, w, out, M, N, K, dt, ws, s);
   if ((dt == Q4_K || dt == Q5_K) && q4kx_ok(M, N, K, w, nullptr, x, dt) && q4kx_xin(K))
     return launch_gemv_q4kx(x, w, nullptr, out, M, N, K, 0, dt, s);
   if (!gemv_fast_ok(dt, K, w) || (dt == Q5_K && !q4kx_ok(1, N, K, w, nullptr, x, dt)))

@@ -37,6 +37,8 @@ int launch_dequant(const void *src, void *dst, int64_t n, int src_dtype, int out
 // in ws, then runs the kernel.
 constexpr int64_t kGemvMaxRows = 8;
 bool use_gemm(int64_t M, int dt);
+int launch_gemm_ws_bf16(const uint16_t *xb, const uint16_t *wb, float *out, float *partials, int64_t M, int64_t N,
+                        int64_t K, hipStream_t s);
 size_t matmul_q_ws_bytes(int64_t M, int64_t N, int64_t K, int dt);
 size_t matmul_act_ws_bytes(int64_t M, int64_t N, int64_t K, int dt);
 int launch_matmul_q(const float *x, const void *w, float *out, int64_t M, int64_t N, int64_t K, int dt, void *ws,

@@ -197,3 +197,14 @@ CONFIGS = {
     "moe_q4_k_t1": dict(cfg=4, kind="moe", dt=Q4_K, T=1, E=128, topk=8, H=2048, I=768),
     "moe_q4_k_t256": dict(cfg=4, kind="moe", dt=Q4_K, T=256, E=128, topk=8, H=2048, I=768),
 }
+
+# Not benchmark configurations: the remaining fused formats at the Llama-3-8B gate shape
+# (decode) and Q8_0 / Q6_K / Q5_K prefill, timed by bench.py --table only.
+EXTRA_CONFIGS = {
+    "q4_0_gemv_14336x4096": dict(cfg=5, kind="gguf", dt=Q4_0, M=1, N=14336, K=4096),
+    "q5_0_gemv_14336x4096": dict(cfg=5, kind="gguf", dt=Q5_0, M=1, N=14336, K=4096),
+    "q5_k_gemv_14336x4096": dict(cfg=5, kind="gguf", dt=Q5_K, M=1, N=14336, K=4096),
+    "q8_0_gemm_m512_14336x4096": dict(cfg=5, kind="gguf", dt=Q8_0, M=512, N=14336, K=4096),
+    "q6_k_gemm_m512_14336x4096": dict(cfg=5, kind="gguf", dt=Q6_K, M=512, N=14336, K=4096),
+    "q5_k_gemm_m512_14336x4096": dict(cfg=5, kind="gguf", dt=Q5_K, M=512, N=14336, K=4096),
+}

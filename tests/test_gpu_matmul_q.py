@@ -229,6 +229,27 @@ def test_matmul_q_added_formats_rows(dev, dt, M):
     _check_matmul(dev, dt, x, w, N, K, "added_formats")
 
 
+@pytest.mark.parametrize("dt", [hipq.Q4_0, hipq.Q5_0, hipq.Q8_0, hipq.Q5_K, hipq.Q6_K])
+@pytest.mark.parametrize("M,N,K", [(9, 13, 1024), (100, 200, 2048), (300, 130, 512), (512, 256, 4096)])
+def test_gemm_dequant_bf16_formats(dev, dt, M, N, K):
+    """M > 8, formats without an in-GEMM dequant: bit-exact bf16 dequant into the workspace,
+    then the MFMA GEMM on bf16 weights (Light's prefill is dequant + GEMM too,
+    ops/matmul_q.go:52-59)."""
+    g = np.random.default_rng(M + N + K + dt)
+    w = synth.gguf_weight(dt, N, K, g)
+    x = synth.activations(M, K, g)
+    _check_matmul(dev, dt, x, w, N, K, "gemm_bf16")
+
+
+def test_matmul_q_many_rows_k_not_64(dev):
+    """K % 64 != 0 (Q8_0 K = 96) keeps the GEMV at M > 8."""
+    g = np.random.default_rng(12)
+    N, K, M = 20, 96, 12
+    w = synth.gguf_weight(hipq.Q8_0, N, K, g)
+    x = synth.activations(M, K, g)
+    _check_matmul(dev, hipq.Q8_0, x, w, N, K, "k96")
+
+
 def test_matmul_q_q5_0_high_bits_only(dev):
     """Q5_0 with zero nibbles and every fifth bit set (q5 = 16 -> 0) or clear (-16): pins the
     qh bit order in the GEMV against the closed form."""
