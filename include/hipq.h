@@ -209,6 +209,39 @@ int hq_moe_gemm_q(const float *x, const void *w, const int64_t *sorted_pairs, co
  * does (bit-identical). */
 int hq_moe_combine(const float *pair_out, float *out, int64_t M, int64_t N, int topk, hq_stream_t stream);
 
+/* On-device MoERoute (ops/moe.go:29-71): probs F32 (T, E) -> topk_ids I64 (T, topk), weights
+ * F32 (T*topk) (renormalised per token when normalize != 0: den = left-to-right f32 sum of
+ * the k values, then value / den), and the stable expert sort of the T*topk pairs:
+ * sorted_pairs / sorted_expts I64 (T*topk).  Top-k ties keep index order (Light's stable
+ * descending sort, kernels/cpu/topk.go:52-68); probs must be finite.  counts I32 (E) and
+ * offsets I32 (E+1) (nullable) receive moe_gemm_q's scratch for the same routing.
+ * Limits: 1 <= topk <= min(E, 64), E <= 1024, T*topk <= 65535 and
+ * 2 T topk + 2 ceil(T topk / 64) E + 4 E <= 160 KiB (the sort runs in one workgroup).
+ * Replaces ops.MoERoute's TopK / Sum / Div / Sort dispatches (kernels/cuda). */
+int hq_moe_route(const float *probs, int64_t T, int64_t E, int topk, int normalize, int64_t *topk_ids,
+                 float *weights, int64_t *sorted_pairs, int64_t *sorted_expts, int32_t *counts, int32_t *offsets,
+                 hq_stream_t stream);
+
+/* The sort of MoERouteFromIDs (ops/moe.go:78-99: Sort(flat ids, ascending), stable) on the
+ * device: ids I64 (M) in [0, E) -> sorted_pairs / sorted_expts I64 (M), plus counts /
+ * offsets (nullable) as hq_moe_route.  Same limits with T*topk = M. */
+int hq_moe_sort_ids(const int64_t *ids, int64_t M, int64_t E, int64_t *sorted_pairs, int64_t *sorted_expts,
+                    int32_t *counts, int32_t *offsets, hq_stream_t stream);
+
+/* Workspace bytes hq_moe_gemm_q_gated needs. */
+size_t hq_moe_gemm_q_gated_ws_bytes(int64_t size_m, int64_t rows, int64_t I, int64_t K, int w_dtype);
+
+/* Routed gated gate/up of nn.SparseMoE.runExperts (nn/moe.go:196-236): w is the stacked
+ * GateUp (E, 2I, K) quantized (gate rows [0, I), up rows [I, 2I) of each expert), and
+ * out (size_m, I) F32 gets h[p] = act(x_row(p) . Wg[e(p)]) * (x_row(p) . Wu[e(p)]) -- the
+ * MoEGemmQ, Narrow, SiLU / GeluErf and Mul of that function in one op (one kernel for
+ * Q4_K / Q5_K decode).  Routing arguments as hq_moe_gemm_q; act HQ_ACT_SILU or
+ * HQ_ACT_GELU_ERF.  No counterpart kernel in Light: the fusion of (f) row 4. */
+int hq_moe_gemm_q_gated(const float *x, const void *w, const int64_t *sorted_pairs, const int64_t *sorted_expts,
+                        int32_t *counts, int32_t *offsets, float *out, int topk, int64_t size_m, int64_t M,
+                        int64_t rows, int64_t E, int64_t I, int64_t K, int row_per_pair, int w_dtype, int act,
+                        void *ws, size_t ws_bytes, hq_stream_t stream);
+
 /* y (M, K) = x[:, idx] for 2- or 4-byte elements (ops.gatherColumns, ops/int4.go:129-147):
  * the act-order (desc_act) permutation of quant.Int4.Perm applied to the activations.
  * Indices outside [0, K) give zeros. */

@@ -438,6 +438,71 @@ int hq_moe_combine(const float *pair_out, float *out, int64_t M, int64_t N, int 
   return launch_moe_combine(pair_out, out, M / topk, N, topk, s);
 }
 
+int hq_moe_route(const float *probs, int64_t T, int64_t E, int topk, int normalize, int64_t *topk_ids,
+                 float *weights, int64_t *sorted_pairs, int64_t *sorted_expts, int32_t *counts, int32_t *offsets,
+                 hq_stream_t stream) {
+  const char *call = "hq_moe_route";
+  if (T < 0 || E < 1) return fail(HQ_EINVAL, call, "probs must be (T, E), got (%lld, %lld)", (long long)T, (long long)E);
+  if (topk < 1 || topk > E) return fail(HQ_EINVAL, call, "topk %d out of range [1, %lld]", topk, (long long)E);
+  if (T == 0) return HQ_OK;
+  if (topk > 64 || !moe_route_fits(T * topk, E))
+    return fail(HQ_EUNSUPPORTED, call, "T=%lld E=%lld topk=%d beyond the one-workgroup sort", (long long)T,
+                (long long)E, topk);
+  if (!probs || !topk_ids || !weights || !sorted_pairs || !sorted_expts) return fail(HQ_EINVAL, call, "NULL pointer");
+  hipStream_t s = resolve(stream);
+  TraceSpan span("moe_route", s);
+  return launch_moe_route(probs, T, E, topk, normalize, topk_ids, weights, sorted_pairs, sorted_expts, counts,
+                          offsets, s);
+}
+
+int hq_moe_sort_ids(const int64_t *ids, int64_t M, int64_t E, int64_t *sorted_pairs, int64_t *sorted_expts,
+                    int32_t *counts, int32_t *offsets, hq_stream_t stream) {
+  const char *call = "hq_moe_sort_ids";
+  if (M < 0 || E < 1) return fail(HQ_EINVAL, call, "bad shape");
+  if (M == 0) return HQ_OK;
+  if (!moe_route_fits(M, E))
+    return fail(HQ_EUNSUPPORTED, call, "M=%lld E=%lld beyond the one-workgroup sort", (long long)M, (long long)E);
+  if (!ids || !sorted_pairs || !sorted_expts) return fail(HQ_EINVAL, call, "NULL pointer");
+  hipStream_t s = resolve(stream);
+  TraceSpan span("moe_sort", s);
+  return launch_moe_sort_ids(ids, M, E, sorted_pairs, sorted_expts, counts, offsets, s);
+}
+
+size_t hq_moe_gemm_q_gated_ws_bytes(int64_t size_m, int64_t rows, int64_t I, int64_t K, int w_dtype) {
+  if (size_m < 0 || rows < 0 || I < 0 || K <= 0) return 0;
+  return moe_gated_ws_bytes(size_m, rows, I, K, w_dtype);
+}
+
+int hq_moe_gemm_q_gated(const float *x, const void *w, const int64_t *sorted_pairs, const int64_t *sorted_expts,
+                        int32_t *counts, int32_t *offsets, float *out, int topk, int64_t size_m, int64_t M,
+                        int64_t rows, int64_t E, int64_t I, int64_t K, int row_per_pair, int w_dtype, int act,
+                        void *ws, size_t ws_bytes, hq_stream_t stream) {
+  const char *call = "hq_moe_gemm_q_gated";
+  if (!is_gguf(w_dtype)) return fail(HQ_EUNSUPPORTED, call, "weight dtype %d has no fused kernel", w_dtype);
+  if (act != HQ_ACT_SILU && act != HQ_ACT_GELU_ERF) return fail(HQ_EINVAL, call, "activation %d", act);
+  if (E <= 0 || I < 0 || K <= 0 || M < 0 || size_m < 0 || rows < 0 || topk < 1)
+    return fail(HQ_EINVAL, call, "bad shape");
+  BlockInfo bi = block_info(w_dtype);
+  if (K % bi.elems) return fail(HQ_EINVAL, call, "K=%lld not a multiple of block size %d", (long long)K, bi.elems);
+  if (row_per_pair ? rows != M : rows != M / topk)
+    return fail(HQ_EINVAL, call, "input rows %lld must be M=%lld (per pair) or M/topk=%lld (per token)",
+                (long long)rows, (long long)M, (long long)(M / topk));
+  if (M == 0 || I == 0) return HQ_OK;
+  if (!x || !w || !sorted_pairs || !sorted_expts || !counts || !offsets || !out)
+    return fail(HQ_EINVAL, call, "NULL pointer");
+  if (((uintptr_t)x & 15)) return fail(HQ_EINVAL, call, "x must be 16-byte aligned");
+  hipStream_t s = resolve(stream);
+  const size_t need = moe_gated_ws_bytes(size_m, rows, I, K, w_dtype);
+  if (!ws) {
+    if (int rc = workspace(need, s, &ws, call)) return rc;
+  } else if (ws_bytes < need) {
+    return fail(HQ_ENOMEM, call, "workspace %zu bytes < %zu needed", ws_bytes, need);
+  }
+  TraceSpan span("moe_gemm_q_gated", s);
+  return launch_moe_q_gated(x, w, sorted_pairs, sorted_expts, counts, offsets, out, topk, size_m, M, rows, E, I, K,
+                            row_per_pair, w_dtype, act, ws, s);
+}
+
 int hq_gather_cols(const void *x, const int64_t *idx, void *y, int64_t M, int64_t K, int elem_bytes,
                    hq_stream_t stream) {
   const char *call = "hq_gather_cols";

@@ -104,4 +104,11 @@ __device__ __forceinline__ void q4k_scale_min(int j, uint32_t s0, uint32_t s1, u
   }
 }
 
+// Light's SiLU (kernels/cpu/unary.go:219-222) and exact GELU (:216, :263-265), the gate
+// activation of the gated MLP (HQ_ACT_SILU = 0, HQ_ACT_GELU_ERF = 1).
+__device__ __forceinline__ float gate_act(float g, int act) {
+  if (act == 1) return 0.5f * g * (1.0f + erff(g * 0.70710678118654752f));
+  return g / (1.0f + expf(-g));
+}
+
 }  // namespace hq

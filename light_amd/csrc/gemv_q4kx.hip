@@ -70,12 +70,6 @@ __device__ __forceinline__ float rl(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
-// Light's SiLU (kernels/cpu/unary.go:219-222) and exact GELU (:216, :263-265).
-__device__ __forceinline__ float gate_act(float g, int act) {
-  if (act == 1) return 0.5f * g * (1.0f + erff(g * 0.70710678118654752f));
-  return g / (1.0f + expf(-g));
-}
-
 }  // namespace
 
 // LDS: act [MM][K] q1 | [MM][K] q2 | (d, e) [MM][K/32] | sx [MM][K/32]  (XIN only)
@@ -504,7 +498,8 @@ struct MoeXArgs {
   int32_t *counts, *offsets;
   const float *topk_w;
   int64_t size_m, expert_bytes, rows, npairs;
-  int E, topk, rpp;
+  int64_t up_off;  // GATED: byte offset of the up rows inside an expert (I rows after gate)
+  int E, topk, rpp, act;
 };
 
 // Segment j of the sorted expert ids (segment starts: i == 0 or v[i] != v[i-1]), found by
@@ -553,7 +548,7 @@ __device__ __forceinline__ Seg find_segment(const int64_t *__restrict__ v, int64
   return sg;
 }
 
-template <class U, int MM>
+template <class U, int MM, bool GATED>
 __global__ __launch_bounds__(512) void moe_gemv_x_kernel(MoeXArgs ma) {
   extern __shared__ __align__(16) uint8_t smem[];
   const Q4kxArgs &a = ma.g;
@@ -596,11 +591,13 @@ __global__ __launch_bounds__(512) void moe_gemv_x_kernel(MoeXArgs ma) {
       int64_t r = p < 0 ? 0 : (ma.rpp ? p : p / ma.topk);
       xrow[mm] = r < ma.rows ? r : ma.rows - 1;
     }
-    typename U::W wr;
+    constexpr int NW = GATED ? 2 : 1;
+    typename U::W wr[NW];
     {
       int row = (int)blockIdx.x * RW + team;
       row = row < a.N ? row : a.N - 1;
-      U::load(w, a.s0, a.z0, a, row, L, wr);
+      U::load(w, a.s0, a.z0, a, row, L, wr[0]);
+      if (GATED) U::load(w + ma.up_off, a.s0, a.z0, a, row, L, wr[NW - 1]);
     }
     if (c0 != seg0) __syncthreads();  // every lane has its activations of the previous chunk
     constexpr int XT = 4;
@@ -646,26 +643,32 @@ __global__ __launch_bounds__(512) void moe_gemv_x_kernel(MoeXArgs ma) {
 
     for (int it = 0; it < niter; it++) {
       const int grp = (int)blockIdx.x + it * G;
-      float c[MM];
-      U::template dot<MM>(wr, xr, L, c);
+      float c[NW][MM];
+#pragma unroll
+      for (int j = 0; j < NW; j++) U::template dot<MM>(wr[j], xr, L, c[j]);
       {
         int row = (grp + G) * RW + team;
         row = row < a.N ? row : a.N - 1;
-        U::load(w, a.s0, a.z0, a, row, L, wr);
+        U::load(w, a.s0, a.z0, a, row, L, wr[0]);
+        if (GATED) U::load(w + ma.up_off, a.s0, a.z0, a, row, L, wr[NW - 1]);
       }
       const int row = grp * RW + team;
 #pragma unroll
       for (int mm = 0; mm < MM; mm++) {
-        const float r16 = rsum16(active ? c[mm] : 0.f);
-        const float r0 = rl(r16, 0), r1 = rl(r16, 16), r2 = rl(r16, 32), r3 = rl(r16, 48);
-        float tot;
-        if (a.TP == 64)
-          tot = ((r0 + r1) + r2) + r3;
-        else if (a.TP == 32)
-          tot = lane < 32 ? r0 + r1 : r2 + r3;
-        else
-          tot = lane < 16 ? r0 : (lane < 32 ? r1 : (lane < 48 ? r2 : r3));
-        if (u == 0 && row < a.N && pid[mm] >= 0) static_cast<float *>(a.out)[pid[mm] * a.N + row] = tot * wp[mm];
+        float tot[NW];
+#pragma unroll
+        for (int j = 0; j < NW; j++) {
+          const float r16 = rsum16(active ? c[j][mm] : 0.f);
+          const float r0 = rl(r16, 0), r1 = rl(r16, 16), r2 = rl(r16, 32), r3 = rl(r16, 48);
+          if (a.TP == 64)
+            tot[j] = ((r0 + r1) + r2) + r3;
+          else if (a.TP == 32)
+            tot[j] = lane < 32 ? r0 + r1 : r2 + r3;
+          else
+            tot[j] = lane < 16 ? r0 : (lane < 32 ? r1 : (lane < 48 ? r2 : r3));
+        }
+        const float y = GATED ? gate_act(tot[0], ma.act) * tot[NW - 1] : tot[0] * wp[mm];
+        if (u == 0 && row < a.N && pid[mm] >= 0) static_cast<float *>(a.out)[pid[mm] * a.N + row] = y;
       }
     }
   }
@@ -922,7 +925,7 @@ bool moe_x_ok(int64_t K, int dt, const void *w, const void *x) {
   return ((uintptr_t)w & 15) == 0 && ((uintptr_t)x & 15) == 0;
 }
 
-template <class U, int MM>
+template <class U, int MM, bool GATED>
 static int run_moe_x(MoeXArgs &ma, int64_t active, hipStream_t s) {
   const Q4kxArgs &a = ma.g;
   const size_t lds = (size_t)q4kx_act_lds(MM, a.K);
@@ -934,16 +937,18 @@ static int run_moe_x(MoeXArgs &ma, int64_t active, hipStream_t s) {
   per = per < ngroups ? per : ngroups;
   per = cdiv(ngroups, cdiv(ngroups, per));
   dim3 grid((unsigned)per, (unsigned)active);
-  moe_gemv_x_kernel<U, MM><<<grid, a.TP * a.RW, lds, s>>>(ma);
+  moe_gemv_x_kernel<U, MM, GATED><<<grid, a.TP * a.RW, lds, s>>>(ma);
   return check_launch("moe_gemv_x");
 }
 
 int launch_moe_gemv_x(const float *x, const void *w, const int64_t *pairs, const int64_t *expts, int32_t *counts,
                       int32_t *offsets, const float *topk_w, float *out, int topk, int64_t size_m, int64_t M,
-                      int64_t rows, int64_t E, int64_t N, int64_t K, int rpp, int dt, hipStream_t s) {
+                      int64_t rows, int64_t E, int64_t N, int64_t K, int rpp, int dt, int act, hipStream_t s) {
   MoeXArgs ma;
   const int64_t row_bytes = K / 256 * block_info(dt).bytes;
-  if (int rc = q4kx_setup(ma.g, 1, N, K, 256, row_bytes, "moe_gemv")) return rc;
+  const bool gated = act >= 0;  // N = I; the expert holds gate rows [0, I) then up rows [I, 2I)
+  if (int rc = q4kx_setup(ma.g, 1, gated ? 2 * N : N, K, 256, row_bytes, "moe_gemv")) return rc;
+  ma.g.N = (int)N;
   ma.g.x = x;
   ma.g.w0 = static_cast<const uint8_t *>(w);
   ma.g.out = out;
@@ -953,7 +958,9 @@ int launch_moe_gemv_x(const float *x, const void *w, const int64_t *pairs, const
   ma.offsets = offsets;
   ma.topk_w = topk_w;
   ma.size_m = size_m;
-  ma.expert_bytes = N * row_bytes;
+  ma.expert_bytes = (gated ? 2 * N : N) * row_bytes;
+  ma.up_off = gated ? N * row_bytes : 0;
+  ma.act = gated ? act : 0;
   ma.rows = rows;
   ma.npairs = M;
   ma.E = (int)E;
@@ -961,14 +968,19 @@ int launch_moe_gemv_x(const float *x, const void *w, const int64_t *pairs, const
   ma.rpp = rpp;
   const int64_t active = M < E ? M : E;
   const int64_t avg = active > 0 ? (M + active - 1) / active : 1;
-  if (dt == Q5_K) {
-    if (avg <= 1) return run_moe_x<Q5kUnit, 1>(ma, active, s);
-    if (avg <= 2) return run_moe_x<Q5kUnit, 2>(ma, active, s);
-    return run_moe_x<Q5kUnit, 4>(ma, active, s);
+  // Gated: at most two pair rows per pass (two weight rows in registers).
+  if (gated) {
+    if (dt == Q5_K) return avg <= 1 ? run_moe_x<Q5kUnit, 1, true>(ma, active, s) : run_moe_x<Q5kUnit, 2, true>(ma, active, s);
+    return avg <= 1 ? run_moe_x<Q4kUnit, 1, true>(ma, active, s) : run_moe_x<Q4kUnit, 2, true>(ma, active, s);
   }
-  if (avg <= 1) return run_moe_x<Q4kUnit, 1>(ma, active, s);
-  if (avg <= 2) return run_moe_x<Q4kUnit, 2>(ma, active, s);
-  return run_moe_x<Q4kUnit, 4>(ma, active, s);
+  if (dt == Q5_K) {
+    if (avg <= 1) return run_moe_x<Q5kUnit, 1, false>(ma, active, s);
+    if (avg <= 2) return run_moe_x<Q5kUnit, 2, false>(ma, active, s);
+    return run_moe_x<Q5kUnit, 4, false>(ma, active, s);
+  }
+  if (avg <= 1) return run_moe_x<Q4kUnit, 1, false>(ma, active, s);
+  if (avg <= 2) return run_moe_x<Q4kUnit, 2, false>(ma, active, s);
+  return run_moe_x<Q4kUnit, 4, false>(ma, active, s);
 }
 
 }  // namespace hq

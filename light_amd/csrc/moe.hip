@@ -108,7 +108,7 @@ int launch_moe_q(const float *x, const void *w, const int64_t *pairs, const int6
   // (Q5_K takes it at every M: it has no grouped MFMA kernel.)
   if (M > 0 && E <= 65535 && (dt == Q5_K || !moe_use_mfma(M, E)) && moe_x_ok(K, dt, w, x))
     return launch_moe_gemv_x(x, w, pairs, expts, counts, offsets, topk_w, out, topk, size_m, M, rows, E, N, K, rpp,
-                             dt, s);
+                             dt, -1, s);
   moe_offsets_kernel<<<(unsigned)cdiv(E + 1, 256), 256, 0, s>>>(expts, M, (int)E, counts, offsets);
   if (int rc = check_launch("moe_offsets")) return rc;
   if (moe_q4k_fast(dt, K, w)) {
@@ -135,6 +135,48 @@ int launch_moe_q(const float *x, const void *w, const int64_t *pairs, const int6
     default: return fail(HQ_EUNSUPPORTED, "moe_gemm_q", "dtype %d", dt);
   }
   return check_launch("moe_generic");
+}
+
+// Gated gate/up (the SwiGLU / GeGLU of nn.SparseMoE.runExperts, nn/moe.go:196-236):
+// h[p, n] = act(x_row(p) . Wgu[e(p)][n]) * (x_row(p) . Wgu[e(p)][I + n]) for n < I.  Decode
+// shapes run one fused launch; otherwise moe_gemm_q into the workspace (size_m, 2I), then an
+// epilogue over its two halves.
+__global__ __launch_bounds__(256) void moe_gated_split_kernel(const float *__restrict__ gu, float *__restrict__ out,
+                                                              int64_t rows, int64_t I, int act) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= rows * I) return;
+  const int64_t r = i / I, n = i - r * I;
+  out[i] = gate_act(gu[r * 2 * I + n], act) * gu[r * 2 * I + I + n];
+}
+
+__global__ __launch_bounds__(256) void zero_f32_kernel(float *__restrict__ p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = 0.f;
+}
+
+static int64_t al256m(int64_t b) { return (b + 255) & ~(int64_t)255; }
+
+size_t moe_gated_ws_bytes(int64_t size_m, int64_t rows, int64_t I, int64_t K, int dt) {
+  return (size_t)al256m(4 * size_m * 2 * I) + moe_ws_bytes(rows, K, dt);
+}
+
+int launch_moe_q_gated(const float *x, const void *w, const int64_t *pairs, const int64_t *expts, int32_t *counts,
+                       int32_t *offsets, float *out, int topk, int64_t size_m, int64_t M, int64_t rows, int64_t E,
+                       int64_t I, int64_t K, int rpp, int dt, int act, void *ws, hipStream_t s) {
+  if (E > INT32_MAX - 1 || M > INT32_MAX || 2 * I > INT32_MAX)
+    return fail(HQ_EUNSUPPORTED, "moe_gemm_q_gated", "too large");
+  if (M > 0 && E <= 65535 && (dt == Q5_K || !moe_use_mfma(M, E)) && moe_x_ok(K, dt, w, x))
+    return launch_moe_gemv_x(x, w, pairs, expts, counts, offsets, nullptr, out, topk, size_m, M, rows, E, I, K, rpp,
+                             dt, act, s);
+  float *gu = static_cast<float *>(ws);
+  void *inner = static_cast<char *>(ws) + al256m(4 * size_m * 2 * I);
+  zero_f32_kernel<<<(unsigned)cdiv(size_m * 2 * I, 256), 256, 0, s>>>(gu, size_m * 2 * I);
+  if (int rc = check_launch("zero")) return rc;
+  if (int rc = launch_moe_q(x, w, pairs, expts, counts, offsets, nullptr, gu, topk, size_m, M, rows, E, 2 * I, K, rpp,
+                            dt, inner, s))
+    return rc;
+  moe_gated_split_kernel<<<(unsigned)cdiv(size_m * I, 256), 256, 0, s>>>(gu, out, size_m, I, act);
+  return check_launch("moe_gated_split");
 }
 
 }  // namespace hq

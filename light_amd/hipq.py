@@ -70,6 +70,11 @@ SIGNATURES = {
     "hq_int4_dequant": (_I, [_P, _P, _P, _P, _I, _I64, _I64, _I, _I64, _P]),
     "hq_moe_gemm_q_ws_bytes": (_SZ, [_I64, _I64, _I]),
     "hq_moe_combine": (_I, [_P, _P, _I64, _I64, _I, _P]),
+    "hq_moe_route": (_I, [_P, _I64, _I64, _I, _I, _P, _P, _P, _P, _P, _P, _P]),
+    "hq_moe_sort_ids": (_I, [_P, _I64, _I64, _P, _P, _P, _P, _P]),
+    "hq_moe_gemm_q_gated_ws_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I]),
+    "hq_moe_gemm_q_gated": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _I,
+                                 _P, _SZ, _P]),
     "hq_gather_cols": (_I, [_P, _P, _P, _I64, _I64, _I, _P]),
     "hq_moe_gemm_q": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I,
                            _P, _SZ, _P]),
@@ -278,6 +283,56 @@ def moe_combine(pair_out, topk, out=None, stream=None):
         out = torch.empty((M // topk, N), dtype=torch.float32, device=pair_out.device)
     check(lib().hq_moe_combine(_ptr(pair_out), _ptr(out), M, N, topk, _stream(stream)))
     return out
+
+
+def moe_route(probs, topk, normalize=True, counts=None, offsets=None, stream=None):
+    """ops.MoERoute on the device: (topk_ids (T, topk) I64, weights (T*topk,) F32,
+    sorted_pairs, sorted_expts (T*topk,) I64); counts / offsets filled when given."""
+    import torch
+    T, E = probs.shape
+    dev = probs.device
+    ids = torch.empty((T, topk), dtype=torch.int64, device=dev)
+    w = torch.empty(T * topk, dtype=torch.float32, device=dev)
+    sp = torch.empty(T * topk, dtype=torch.int64, device=dev)
+    se = torch.empty(T * topk, dtype=torch.int64, device=dev)
+    check(lib().hq_moe_route(_ptr(probs), T, E, topk, int(bool(normalize)), _ptr(ids), _ptr(w), _ptr(sp), _ptr(se),
+                             _ptr(counts), _ptr(offsets), _stream(stream)))
+    return ids, w, sp, se
+
+
+def moe_sort_ids(ids, E, counts=None, offsets=None, stream=None):
+    """Stable ascending expert sort of flat ids on the device: (sorted_pairs, sorted_expts)."""
+    import torch
+    M = ids.numel()
+    sp = torch.empty(M, dtype=torch.int64, device=ids.device)
+    se = torch.empty(M, dtype=torch.int64, device=ids.device)
+    check(lib().hq_moe_sort_ids(_ptr(ids), M, E, _ptr(sp), _ptr(se), _ptr(counts), _ptr(offsets), _stream(stream)))
+    return sp, se
+
+
+def moe_gemm_q_gated(x, w, sorted_pairs, sorted_expts, E, I, K, w_dtype, topk, act=ACT_SILU, out=None,
+                     counts=None, offsets=None, ws=None, stream=None):
+    """Routed gated gate/up: w (E, 2I, K) quantized -> h (M, I) = act(g) * u."""
+    import torch
+    M = sorted_pairs.numel()
+    rows = x.shape[0]
+    rpp = 1 if rows == M else 0
+    dev = x.device
+    if counts is None:
+        counts = torch.zeros(E, dtype=torch.int32, device=dev)
+    if offsets is None:
+        offsets = torch.zeros(E + 1, dtype=torch.int32, device=dev)
+    if out is None:
+        out = torch.zeros((M, I), dtype=torch.float32, device=dev)
+    ws_bytes = 0 if ws is None else ws.numel() * ws.element_size()
+    check(lib().hq_moe_gemm_q_gated(_ptr(x), _ptr(w), _ptr(sorted_pairs), _ptr(sorted_expts), _ptr(counts),
+                                    _ptr(offsets), _ptr(out), topk, out.shape[0], M, rows, E, I, K, rpp, w_dtype, act,
+                                    _ptr(ws), ws_bytes, _stream(stream)))
+    return out
+
+
+def moe_gemm_q_gated_ws_bytes(size_m, rows, I, K, w_dtype):
+    return lib().hq_moe_gemm_q_gated_ws_bytes(size_m, rows, I, K, w_dtype)
 
 
 def moe_gemm_q_ws_bytes(rows, K, w_dtype):

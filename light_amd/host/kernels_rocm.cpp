@@ -50,6 +50,34 @@ void moe_gemm_q(Context &c) {
                       (int)c.attr("row_per_pair"), (int)w.dtype(), nullptr, 0, nullptr));
 }
 
+// ops.MoERoute: inputs {probs, topk_ids, weights, sorted_expts}, output sorted_pairs.
+void moe_route(Context &c) {
+  const Tensor &probs = c.in(0), &ids = c.in(1), &w = c.in(2), &se = c.in(3);
+  Check(hq_moe_route(static_cast<const float *>(probs.data()), probs.Dim(0), probs.Dim(1), (int)c.attr("k"),
+                     (int)c.attr("normalize"), static_cast<int64_t *>(ids.data()), static_cast<float *>(w.data()),
+                     static_cast<int64_t *>(c.output.data()), static_cast<int64_t *>(se.data()), nullptr, nullptr,
+                     nullptr));
+}
+
+// MoERouteFromIDs' Sort: inputs {ids, sorted_expts}, output sorted_pairs, attr experts.
+void moe_sort(Context &c) {
+  const Tensor &ids = c.in(0), &se = c.in(1);
+  Check(hq_moe_sort_ids(static_cast<const int64_t *>(ids.data()), ids.NumElements(), c.attr("experts"),
+                        static_cast<int64_t *>(c.output.data()), static_cast<int64_t *>(se.data()), nullptr, nullptr,
+                        nullptr));
+}
+
+void moe_gemm_q_gated(Context &c) {
+  const Tensor &x = c.in(0), &w = c.in(1), &pairs = c.in(2), &expts = c.in(3), &counts = c.in(4),
+               &offsets = c.in(5);
+  Check(hq_moe_gemm_q_gated(static_cast<const float *>(x.data()), w.data(), static_cast<const int64_t *>(pairs.data()),
+                            static_cast<const int64_t *>(expts.data()), static_cast<int32_t *>(counts.data()),
+                            static_cast<int32_t *>(offsets.data()), static_cast<float *>(c.output.data()),
+                            (int)c.attr("topk"), c.output.Dim(0), pairs.Dim(0), x.Dim(0), w.Dim(0), w.Dim(1) / 2,
+                            w.Dim(2), (int)c.attr("row_per_pair"), (int)w.dtype(),
+                            c.attr("gelu") ? HQ_ACT_GELU_ERF : HQ_ACT_SILU, nullptr, 0, nullptr));
+}
+
 void dequant(Context &c) {
   const Tensor &w = c.in(0);
   Check(hq_dequant(w.data(), c.output.data(), w.NumElements(), (int)w.dtype(), HQ_F32, nullptr));
@@ -61,9 +89,12 @@ struct Registrar {
       Register(Key{"matmul_q", DeviceKind::ROCm, dt}, matmul_q);
       Register(Key{"matmul_q_gated", DeviceKind::ROCm, dt}, matmul_q_gated);
       Register(Key{"moe_gemm_q", DeviceKind::ROCm, dt}, moe_gemm_q);
+      Register(Key{"moe_gemm_q_gated", DeviceKind::ROCm, dt}, moe_gemm_q_gated);
       Register(Key{"dequant", DeviceKind::ROCm, dt}, dequant);
     }
     Register(Key{"dequant", DeviceKind::ROCm, DType::Q8_1}, dequant);
+    Register(Key{"moe_route", DeviceKind::ROCm, DType::F32}, moe_route);
+    Register(Key{"moe_sort", DeviceKind::ROCm, DType::I64}, moe_sort);
     for (DType dt : {DType::F32, DType::BF16, DType::F16}) Register(Key{"int4_gemv", DeviceKind::ROCm, dt}, int4_gemv);
     for (DType dt : {DType::F32, DType::BF16}) Register(Key{"int4_dequant", DeviceKind::ROCm, dt}, int4_dequant);
   }

@@ -125,11 +125,50 @@ Tensor MatMulInt4(const Tensor &x, const Int4 &w) {
 
 // ---- MoE (ops/moe.go) ----
 
+MoERouting MoERoute(const Tensor &probs, int topk, bool normalize) {
+  if (probs.Rank() != 2 || probs.dtype() != DType::F32)
+    Fail("moe_route: probs must be (T, E) F32, got %s %s", probs.ShapeStr().c_str(), DTypeName(probs.dtype()));
+  const int64_t T = probs.Dim(0), E = probs.Dim(1);
+  if (topk < 1 || topk > E) Fail("moe_route: topk %d out of range [1, %lld]", topk, (long long)E);
+  Kernel k = Lookup(Key{"moe_route", probs.device().kind, DType::F32});
+  MoERouting r;
+  r.topk_ids = Tensor::Empty(DType::I64, {T, topk}, probs.device());
+  r.weights = Tensor::Empty(DType::F32, {T * topk}, probs.device());
+  r.sorted_pairs = Tensor::Empty(DType::I64, {T * topk}, probs.device());
+  r.sorted_expts = Tensor::Empty(DType::I64, {T * topk}, probs.device());
+  Context ctx;  // outputs beyond the first travel as inputs, as ops.TopK's index output does
+  ctx.inputs = {probs, r.topk_ids, r.weights, r.sorted_expts};
+  ctx.output = r.sorted_pairs;
+  ctx.attrs = {{"k", Attr::Int(topk)}, {"normalize", Attr::Bool(normalize)}};
+  k(ctx);
+  return r;
+}
+
 MoERouting MoERouteFromIDs(const std::vector<int64_t> &ids, const std::vector<float> &weights, int64_t T,
                            int topk, Device dev) {
   const int64_t M = T * topk;
   if ((int64_t)ids.size() != M || (int64_t)weights.size() != M)
     Fail("moe_route: %zu ids / %zu weights for %lld × %d", ids.size(), weights.size(), (long long)T, topk);
+  if (dev.kind == DeviceKind::ROCm && M > 0) {
+    // Sort(flat, false) on the device ("moe_sort", stable ascending).
+    int64_t emax = 0;
+    for (int64_t v : ids) {
+      if (v < 0) Fail("moe_route: expert id %lld < 0", (long long)v);
+      emax = std::max(emax, v);
+    }
+    MoERouting r;
+    r.topk_ids = Tensor::FromHost(ids.data(), 8 * M, DType::I64, {T, topk}, dev);
+    r.weights = Tensor::FromHost(weights.data(), 4 * M, DType::F32, {M}, dev);
+    r.sorted_pairs = Tensor::Empty(DType::I64, {M}, dev);
+    r.sorted_expts = Tensor::Empty(DType::I64, {M}, dev);
+    Kernel k = Lookup(Key{"moe_sort", dev.kind, DType::I64});
+    Context ctx;
+    ctx.inputs = {r.topk_ids, r.sorted_expts};
+    ctx.output = r.sorted_pairs;
+    ctx.attrs = {{"experts", Attr::Int(emax + 1)}};
+    k(ctx);
+    return r;
+  }
   // Sort(flat, false): a stable ascending sort (kernels/cpu/shape_ops.go:156-184).
   std::vector<int64_t> order(M);
   std::iota(order.begin(), order.end(), 0);
@@ -191,6 +230,38 @@ Tensor MoEGemmQ(const Tensor &x, const Tensor &w, const MoERouting &routing, con
     Fail("moe_gemm_q: K=%lld not a multiple of %s block size %d", (long long)w.Dim(2), DTypeName(w.dtype()),
          BlockElems(w.dtype()));
   return moe_gemm_dispatch("moe_gemm_q", w.dtype(), x, w, routing, topk_weights, topk);
+}
+
+Tensor MoEGemmQGated(const Tensor &x, const Tensor &w, const MoERouting &routing, int topk, bool gelu) {
+  const char *op = "moe_gemm_q_gated";
+  if (x.dtype() != DType::F32) Fail("%s: x must be F32, got %s", op, DTypeName(x.dtype()));
+  if (!IsQuantized(w.dtype()) || w.Rank() != 3 || w.Dim(1) % 2)
+    Fail("%s: w must be a quantized (E, 2I, K) tensor, got %s %s", op, DTypeName(w.dtype()), w.ShapeStr().c_str());
+  if (w.Dim(2) % BlockElems(w.dtype()))
+    Fail("%s: K=%lld not a multiple of %s block size %d", op, (long long)w.Dim(2), DTypeName(w.dtype()),
+         BlockElems(w.dtype()));
+  if (x.Rank() != 2) Fail("%s: input (rows, K) required, got %s", op, x.ShapeStr().c_str());
+  if (!same_device(x, w) || !same_device(x, routing.sorted_pairs)) Fail("%s: device mismatch", op);
+  const int64_t E = w.Dim(0), I = w.Dim(1) / 2, K = w.Dim(2), M = routing.sorted_pairs.Dim(0);
+  if (x.Dim(1) != K) Fail("%s: input K %lld != weights K %lld", op, (long long)x.Dim(1), (long long)K);
+  bool row_per_pair;
+  if (x.Dim(0) == M)
+    row_per_pair = true;
+  else if (x.Dim(0) == M / topk)
+    row_per_pair = false;
+  else
+    Fail("%s: input rows %lld must be M=%lld (per pair) or M/topk=%lld (per token)", op, (long long)x.Dim(0),
+         (long long)M, (long long)(M / topk));
+  Tensor counts = Tensor::Zeros(DType::I32, {E}, x.device());
+  Tensor offsets = Tensor::Zeros(DType::I32, {E + 1}, x.device());
+  Tensor out = Tensor::Zeros(DType::F32, {M, I}, x.device());
+  Kernel k = Lookup(Key{op, x.device().kind, w.dtype()});
+  Context ctx;
+  ctx.inputs = {x, w, routing.sorted_pairs, routing.sorted_expts, counts, offsets};
+  ctx.output = out;
+  ctx.attrs = {{"topk", Attr::Int(topk)}, {"row_per_pair", Attr::Bool(row_per_pair)}, {"gelu", Attr::Bool(gelu)}};
+  k(ctx);
+  return out;
 }
 
 Tensor MoECombine(const Tensor &pair_out, int topk) {

@@ -40,11 +40,17 @@ Tensor MatMulInt4(const Tensor &x, const Int4 &w);
 struct MoERouting {
   Tensor topk_ids, weights, sorted_pairs, sorted_expts;
 };
+// ops.MoERoute (ops/moe.go:24-71): top-k of router probabilities (T, E) F32, optional
+// renormalisation, expert sort -- one "moe_route" kernel on ROCm.
+MoERouting MoERoute(const Tensor &probs, int topk, bool normalize);
 // ops.MoERouteFromIDs (ops/moe.go:73-99).
 MoERouting MoERouteFromIDs(const std::vector<int64_t> &ids, const std::vector<float> &weights, int64_t T,
                            int topk, Device dev);
 // ops.MoEGemmQ (ops/moe.go:242-265); topk_weights may be absent.
 Tensor MoEGemmQ(const Tensor &x, const Tensor &w, const MoERouting &routing, const Tensor *topk_weights, int topk);
+// The routed gated gate/up of nn.SparseMoE.runExperts (nn/moe.go:196-236): w (E, 2I, K)
+// stacked gate/up, output (M, I) = act(gate) * up ("moe_gemm_q_gated", keyed by w's dtype).
+Tensor MoEGemmQGated(const Tensor &x, const Tensor &w, const MoERouting &routing, int topk, bool gelu);
 // ops.MoECombine (ops/moe.go:206-240).
 Tensor MoECombine(const Tensor &pair_out, int topk);
 

@@ -182,6 +182,9 @@ PYBIND11_MODULE(_light, m) {
         return ops::MoEGemmQ(x, w, r, tw ? &*tw : nullptr, topk);
       },
       py::arg("x"), py::arg("w"), py::arg("routing"), py::arg("topk_weights"), py::arg("topk"));
+  m.def("moe_route", &ops::MoERoute, py::arg("probs"), py::arg("topk"), py::arg("normalize") = true);
+  m.def("moe_gemm_q_gated", &ops::MoEGemmQGated, py::arg("x"), py::arg("w"), py::arg("routing"), py::arg("topk"),
+        py::arg("gelu") = false);
   m.def("moe_combine", &ops::MoECombine);
   m.def("dequantize", &ops::Dequantize);
 }

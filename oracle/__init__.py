@@ -25,6 +25,9 @@ Parity status of each function (how it is pinned):
   (ops/matmul_q_cpu_test.go:66-76).
 * ``moe_gemm_q`` / ``moe_route_from_ids`` / ``moe_combine``: Light's routing
   invariants (ops/moe_test.go:63-88) and a per-expert loop in f64.
+* ``moe_route``: numpy's stable argsort of -probs (top-k with index-order ties),
+  a float32 loop for the renormalisation, Light's invariants (weights sum to 1,
+  sorted experts non-decreasing, pairs a permutation), on rows with ties.
 * ``gated``: SiLU against x * sigmoid(x) in f64 and GELU against scipy's erf
   (closed forms), at special points (0, large |x|) and on random data.
 * ``quantize_q8_1``: specification only (Light has no q8_1 encoder): layout,
@@ -86,6 +89,7 @@ def _declare(L):
         "or_matmul_q": (I, [P, P, P, I64, I64, I64, I, I]),
         "or_int4_matmul": (I, [P, P, P, P, P, I64, I64, I64, I, I]),
         "or_moe_route_from_ids": (None, [P, I64, P, P]),
+        "or_moe_route": (None, [P, I64, I64, I, I, P, P, P, P]),
         "or_moe_gemm_f32": (I, [P, P, P, P, P, P, I64, I64, I64, I64, I, I, I]),
         "or_moe_gemm_q": (I, [P, P, I, P, P, P, P, I64, I64, I64, I64, I64, I, I, I, P]),
         "or_moe_combine": (None, [P, P, I64, I64, I]),
@@ -208,6 +212,18 @@ def moe_route_from_ids(ids):
     sp = np.zeros(ids.size, np.int64)
     lib().or_moe_route_from_ids(_p(ids), ids.size, _p(se), _p(sp))
     return se, sp
+
+
+def moe_route(probs, topk, normalize=True):
+    """Light's CPU MoERoute: (topk_ids (T, topk), weights (T*topk,), sorted_pairs, sorted_expts)."""
+    probs = _c(probs, np.float32)
+    T, E = probs.shape
+    ids = np.zeros((T, topk), np.int64)
+    w = np.zeros(T * topk, np.float32)
+    sp = np.zeros(T * topk, np.int64)
+    se = np.zeros(T * topk, np.int64)
+    lib().or_moe_route(_p(probs), T, E, topk, int(bool(normalize)), _p(ids), _p(w), _p(sp), _p(se))
+    return ids, w, sp, se
 
 
 def moe_gemm_q(x, w_raw, dt, E, N, K, sorted_pairs, sorted_expts, topk, topk_w=None, threads=0,

@@ -669,6 +669,34 @@ void or_moe_route_from_ids(const int64_t *ids, int64_t M, int64_t *sorted_expts,
   free(cnt);
 }
 
+/* MoERoute, ops/moe.go:29-71, on the CPU: TopK(probs, k, largest) -- a stable descending
+ * sort of each row (kernels/cpu/topk.go:52-68; an insertion sort is stable) -- then, with
+ * normalize, den = Sum over the k values from 0 left to right (kernels/cpu/reduce.go:76-87)
+ * and vals / den; then Sort(flat ids) ascending, stable (or_moe_route_from_ids). */
+void or_moe_route(const float *probs, int64_t T, int64_t E, int topk, int normalize, int64_t *topk_ids,
+                  float *weights, int64_t *sorted_pairs, int64_t *sorted_expts) {
+  int64_t *ord = (int64_t *)malloc(sizeof(int64_t) * (size_t)E);
+  for (int64_t t = 0; t < T; t++) {
+    const float *row = probs + t * E;
+    for (int64_t j = 0; j < E; j++) {
+      int64_t i = j;
+      while (i > 0 && row[j] > row[ord[i - 1]]) {
+        ord[i] = ord[i - 1];
+        i--;
+      }
+      ord[i] = j;
+    }
+    float den = 0.0f;
+    for (int s = 0; s < topk; s++) den += row[ord[s]];
+    for (int s = 0; s < topk; s++) {
+      topk_ids[t * topk + s] = ord[s];
+      weights[t * topk + s] = normalize ? row[ord[s]] / den : row[ord[s]];
+    }
+  }
+  free(ord);
+  or_moe_route_from_ids(topk_ids, T * topk, sorted_expts, sorted_pairs);
+}
+
 typedef struct {
   const float *x, *w, *topk_w;
   const int64_t *pairs, *expts;

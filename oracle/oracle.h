@@ -65,6 +65,8 @@ int or_int4_matmul(const float *x, const uint32_t *codes, const float *s, const 
 
 /* MoE: MoERouteFromIDs sort (ops/moe.go:78-99 + kernels/cpu/shape_ops.go:156-184, stable). */
 void or_moe_route_from_ids(const int64_t *ids, int64_t M, int64_t *sorted_expts, int64_t *sorted_pairs);
+void or_moe_route(const float *probs, int64_t T, int64_t E, int topk, int normalize, int64_t *topk_ids,
+                  float *weights, int64_t *sorted_pairs, int64_t *sorted_expts);
 /* moeGemmKernel F32 path (kernels/cpu/moe.go:51-96); w is F32 (E, N, K). */
 int or_moe_gemm_f32(const float *x, const float *w, const int64_t *pairs, const int64_t *expts,
                     const float *topk_w, float *out, int64_t M, int64_t size_m, int64_t N, int64_t K,

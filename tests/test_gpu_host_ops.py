@@ -122,3 +122,30 @@ def test_matmul_q_gated(gelu):
     hg = oracle.gated(gr, np.ones_like(gr), int(gelu)).astype(np.float64)
     bound = TOL * (1.13 * np.abs(ur) * ng * xn + np.abs(hg) * nu * xn) + 1e-30
     assert np.max(np.abs(got - want) / bound) <= 1.0
+
+
+@pytest.mark.parametrize("gelu", [False, True])
+def test_moe_route_and_gated_host(gelu):
+    """ops.MoERoute on ROCm, then MoEGemmQGated -> MoEGemmQ (weighted) -> MoECombine."""
+    g = synth.rng(700 + gelu)
+    T, E, topk, H, I = 3, 32, 4, 512, 256
+    logits = g.standard_normal((T, E)).astype(np.float32)
+    probs = np.exp(logits - logits.max(axis=1, keepdims=True))
+    probs = (probs / probs.sum(axis=1, keepdims=True)).astype(np.float32)
+    r = L.moe_route(dev_t(probs, "F32", (T, E)), topk, True)
+    rids, rw, rsp, rse = oracle.moe_route(probs, topk, True)
+    assert np.array_equal(r.topk_ids.numpy(), rids) and np.array_equal(r.sorted_pairs.numpy(), rsp)
+    assert np.array_equal(r.weights.numpy().view(np.uint32), rw.view(np.uint32))
+    wgu = synth.gguf_weight(hipq.Q4_K, E * 2 * I, H, g)
+    wdn = synth.gguf_weight(hipq.Q4_K, E * H, I, g)
+    x = synth.activations(T, H, g)
+    h = L.moe_gemm_q_gated(dev_t(x, "F32", (T, H)), dev_t(wgu, "Q4_K", (E, 2 * I, H)), r, topk, gelu)
+    assert h.shape == [T * topk, I]
+    act = hipq.ACT_GELU_ERF if gelu else hipq.ACT_SILU
+    gu = oracle.moe_gemm_q(x, wgu, hipq.Q4_K, E, 2 * I, H, rsp, rse, topk)
+    hr = oracle.gated(gu[:, :I], gu[:, I:], act)
+    assert np.max(np.abs(h.numpy() - hr)) <= 1e-3 * np.abs(hr).max()
+    y = L.moe_combine(L.moe_gemm_q(h, dev_t(wdn, "Q4_K", (E, H, I)), r, r.weights, topk), topk)
+    pr = oracle.moe_gemm_q(hr, wdn, hipq.Q4_K, E, H, I, rsp, rse, topk, topk_w=rw)
+    want = oracle.moe_combine(pr, topk)
+    assert np.max(np.abs(y.numpy() - want)) <= 5e-3 * np.abs(want).max()

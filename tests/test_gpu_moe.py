@@ -115,3 +115,124 @@ def test_moe_benchmark_configs(dev, T):
     sample = None if T == 1 else list(range(0, T * topk, 37))
     _check(dev, x, wgu, hipq.Q4_K, E, 2 * I, H, ids, tw, topk, False, sample=sample)
     _check(dev, h, wdn, hipq.Q4_K, E, H, I, ids, tw, topk, True, sample=sample)
+
+
+# ---- MoERoute on the device ---------------------------------------------
+
+def _probs(g, T, E, ties):
+    logits = g.standard_normal((T, E)).astype(np.float32)
+    p = np.exp(logits - logits.max(axis=1, keepdims=True))
+    p = (p / p.sum(axis=1, keepdims=True)).astype(np.float32)
+    if ties:
+        p[:, E // 2] = p[:, 0]
+        p[:, E - 1] = p[:, 1]
+    return p
+
+
+@pytest.mark.parametrize("T,E,topk", [(1, 128, 8), (1, 8, 2), (5, 60, 60), (64, 128, 8), (65, 128, 8),
+                                      (300, 256, 8), (2048, 128, 8), (3, 1000, 4)])
+@pytest.mark.parametrize("normalize", [False, True])
+def test_moe_route_bit_exact(dev, T, E, topk, normalize):
+    """hq_moe_route against Light's CPU MoERoute (TopK, Sum, Div, Sort): ids, weights and the
+    sorted pairs bit for bit, and counts / offsets as moe_gemm_q's scratch."""
+    print(f"[case] moe_route T={T} E={E} topk={topk} normalize={normalize}", flush=True)
+    g = synth.rng(T * 7 + E + topk)
+    probs = _probs(g, T, E, ties=True)
+    counts = torch.full((E,), -1, dtype=torch.int32, device=dev)
+    offsets = torch.full((E + 1,), -1, dtype=torch.int32, device=dev)
+    ids, w, sp, se = hipq.moe_route(_t(probs, dev), topk, normalize, counts=counts, offsets=offsets)
+    torch.cuda.synchronize()
+    rids, rw, rsp, rse = oracle.moe_route(probs, topk, normalize)
+    assert np.array_equal(ids.cpu().numpy(), rids)
+    assert np.array_equal(w.cpu().numpy().view(np.uint32), rw.view(np.uint32))
+    assert np.array_equal(sp.cpu().numpy(), rsp) and np.array_equal(se.cpu().numpy(), rse)
+    bc = np.bincount(rids.reshape(-1), minlength=E)
+    assert np.array_equal(counts.cpu().numpy(), bc)
+    assert np.array_equal(offsets.cpu().numpy(), np.concatenate([[0], np.cumsum(bc)]))
+
+
+@pytest.mark.parametrize("M,E", [(1, 1), (16, 4), (1000, 128), (16384, 128), (777, 1000)])
+def test_moe_sort_ids(dev, M, E):
+    """MoERouteFromIDs' Sort on the device: stable ascending, against the oracle's counting sort."""
+    g = synth.rng(M + E)
+    ids = g.integers(0, E, size=M).astype(np.int64)
+    counts = torch.zeros(E, dtype=torch.int32, device=dev)
+    offsets = torch.zeros(E + 1, dtype=torch.int32, device=dev)
+    sp, se = hipq.moe_sort_ids(_t(ids, dev), E, counts=counts, offsets=offsets)
+    rse, rsp = oracle.moe_route_from_ids(ids)
+    assert np.array_equal(sp.cpu().numpy(), rsp) and np.array_equal(se.cpu().numpy(), rse)
+    assert np.array_equal(counts.cpu().numpy(), np.bincount(ids, minlength=E))
+
+
+def test_moe_route_limits(dev):
+    probs = torch.rand((4, 8), device=dev)
+    with pytest.raises(hipq.HipqError, match="topk 9 out of range"):
+        hipq.moe_route(probs, 9)
+    with pytest.raises(hipq.HipqError, match="beyond the one-workgroup sort"):
+        hipq.moe_route(torch.rand((1, 2000), device=dev), 2)
+
+
+# ---- routed gated gate/up ---------------------------------------------------
+
+def _check_gated(dev, dt, T, E, topk, I, K, act, rpp=False):
+    print(f"[case] moe_gated dt={hipq.NAMES[dt]} T={T} E={E} topk={topk} I={I} K={K} act={act} rpp={rpp}",
+          flush=True)
+    g = synth.rng(T * 31 + E + I + K + dt + act)
+    w = synth.gguf_weight(dt, E * 2 * I, K, g)
+    ids, tw = synth.moe_routing(T, E, topk, g)
+    se, sp = synth.sort_pairs(ids)
+    rows = T * topk if rpp else T
+    x = g.standard_normal((rows, K)).astype(np.float32)
+    got = hipq.moe_gemm_q_gated(_t(x, dev), _t(w, dev), _t(sp, dev), _t(se, dev), E, I, K, dt, topk, act=act)
+    torch.cuda.synchronize()
+    got = got.cpu().numpy()
+    gu = oracle.moe_gemm_q(x, w, dt, E, 2 * I, K, sp, se, topk)
+    want = oracle.gated(gu[:, :I], gu[:, I:], act)
+    wd = oracle.dequant(dt, w, E * 2 * I * K).reshape(E, 2 * I, K).astype(np.float64)
+    M = T * topk
+    for p in range(M):
+        r = p if rpp else p // topk
+        xn = np.linalg.norm(x[r].astype(np.float64))
+        ng = np.linalg.norm(wd[ids[p], :I], axis=1) * xn
+        nu = np.linalg.norm(wd[ids[p], I:], axis=1) * xn
+        hg = oracle.gated(gu[p:p + 1, :I], np.ones((1, I), np.float32), act)[0].astype(np.float64)
+        bound = TOL * (1.13 * np.abs(gu[p, I:]) * ng + np.abs(hg) * nu) + 1e-30
+        err = np.abs(got[p].astype(np.float64) - want[p]) / bound
+        assert err.max() <= 1.0, f"pair {p}: {err.max():.3g}"
+
+
+@pytest.mark.parametrize("act", [hipq.ACT_SILU, hipq.ACT_GELU_ERF])
+def test_moe_gated_decode_config(dev, act):
+    """Qwen3-30B-A3B-like decode: E=128, topk=8, H=2048, I=768 -- one fused launch."""
+    _check_gated(dev, hipq.Q4_K, 1, 128, 8, 768, 2048, act)
+
+
+@pytest.mark.parametrize("dt,T,E,topk,I,K,rpp", [(hipq.Q4_K, 5, 16, 4, 96, 512, False),
+                                                 (hipq.Q5_K, 3, 8, 2, 64, 1024, True),
+                                                 (hipq.Q4_K, 40, 4, 2, 64, 256, False),   # M > 4E: MFMA + split
+                                                 (hipq.Q8_0, 4, 8, 2, 48, 256, False),    # generic + split
+                                                 (hipq.Q4_K, 2, 4, 2, 32, 5120, False)])  # K > 4096: fallback
+def test_moe_gated_shapes(dev, dt, T, E, topk, I, K, rpp):
+    _check_gated(dev, dt, T, E, topk, I, K, hipq.ACT_SILU, rpp)
+
+
+def test_moe_decode_pipeline_on_device(dev):
+    """Router probs -> hq_moe_route -> gated gate/up -> down (weighted) -> combine, all on the
+    device, against Light's CPU chain (MoERoute, MoEGemmQ, SiLU * up, MoEGemmQ, MoECombine)."""
+    T, E, topk, H, I = 2, 64, 8, 1024, 512
+    g = synth.rng(77)
+    wgu = synth.gguf_weight(hipq.Q4_K, E * 2 * I, H, g)
+    wdn = synth.gguf_weight(hipq.Q4_K, E * H, I, g)
+    x = g.standard_normal((T, H)).astype(np.float32)
+    probs = _probs(g, T, E, ties=False)
+    ids, w, sp, se = hipq.moe_route(_t(probs, dev), topk, True)
+    h = hipq.moe_gemm_q_gated(_t(x, dev), _t(wgu, dev), sp, se, E, I, H, hipq.Q4_K, topk)
+    pair = hipq.moe_gemm_q(h, _t(wdn, dev), sp, se, E, H, I, hipq.Q4_K, topk, topk_w=w)
+    y = hipq.moe_combine(pair, topk).cpu().numpy()
+    rids, rw, rsp, rse = oracle.moe_route(probs, topk, True)
+    gu = oracle.moe_gemm_q(x, wgu, hipq.Q4_K, E, 2 * I, H, rsp, rse, topk)
+    hr = oracle.gated(gu[:, :I], gu[:, I:], hipq.ACT_SILU)
+    pr = oracle.moe_gemm_q(hr, wdn, hipq.Q4_K, E, H, I, rsp, rse, topk, topk_w=rw)
+    want = oracle.moe_combine(pr, topk)
+    scale = np.abs(pr).reshape(T, topk, H).sum(axis=1).max() + 1e-30
+    assert np.max(np.abs(y - want)) <= 5e-3 * scale

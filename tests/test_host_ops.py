@@ -28,13 +28,14 @@ GGUF = ["Q4_0", "Q5_0", "Q8_0", "Q4_K", "Q5_K", "Q6_K"]
 def test_registered_rocm_keys():
     keys = set(L.registered())
     for dt in GGUF:
-        for op in ("matmul_q", "matmul_q_gated", "moe_gemm_q", "dequant"):
+        for op in ("matmul_q", "matmul_q_gated", "moe_gemm_q", "moe_gemm_q_gated", "dequant"):
             assert f"{op}/ROCm/{dt}" in keys
     for dt in ("F32", "BF16", "F16"):
         assert f"int4_gemv/ROCm/{dt}" in keys
     for dt in ("F32", "BF16"):
         assert f"int4_dequant/ROCm/{dt}" in keys
     assert "dequant/ROCm/Q8_1" in keys
+    assert "moe_route/ROCm/F32" in keys and "moe_sort/ROCm/I64" in keys
 
 
 def test_duplicate_registration_fails():
@@ -150,3 +151,13 @@ def test_matmul_q_gated_validation():
         L.matmul_q_gated(x, w, q("Q4_K", 16, 256))
     with pytest.raises(L.KernelNotFound, match="matmul_q_gated/CPU/Q4_K"):
         L.matmul_q_gated(x, w, w)
+
+
+def test_moe_route_checks():
+    """ops.MoERoute's argument checks (ops/moe.go:29-37), then the registry lookup."""
+    with pytest.raises(L.Error, match=r"moe_route: probs must be \(T, E\) F32"):
+        L.moe_route(L.from_numpy(np.zeros(8, np.float32), "F32", [8]), 2)
+    with pytest.raises(L.Error, match=r"moe_route: topk 5 out of range \[1, 4\]"):
+        L.moe_route(f32(3, 4), 5)
+    with pytest.raises(L.KernelNotFound, match="moe_route/CPU/F32"):
+        L.moe_route(f32(3, 4), 2)

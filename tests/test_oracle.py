@@ -375,3 +375,33 @@ def test_gated_tail_closed_forms():
     assert np.allclose(gelu, want, rtol=2e-6, atol=1e-30)
     assert silu[0] == 0.0 and gelu[0] == 0.0
     assert abs(silu[4]) < 1e-10 and gelu[4] == 0.0  # x = -30: SiLU ~ -2.8e-12 * u, GELU underflows to 0
+
+
+# ---- MoERoute -------------------------------------------------------------
+
+@pytest.mark.parametrize("T,E,topk", [(1, 8, 2), (7, 4, 2), (33, 128, 8), (5, 60, 60)])
+@pytest.mark.parametrize("normalize", [False, True])
+def test_moe_route_pinned(T, E, topk, normalize):
+    """TestMoEGemmMatchesExpertLoop's routing checks (ops/moe_test.go:63-88) plus an independent
+    encoding: numpy's stable argsort of -probs (TopK keeps index order on ties), a float32
+    loop for Sum, and numpy's stable argsort of the flat ids (Sort)."""
+    g = np.random.default_rng(T * 100 + E + topk)
+    logits = g.standard_normal((T, E)).astype(np.float32)
+    probs = np.exp(logits - logits.max(axis=1, keepdims=True))
+    probs = (probs / probs.sum(axis=1, keepdims=True)).astype(np.float32)
+    probs[:, E // 2] = probs[:, 0]  # ties
+    ids, w, sp, se = oracle.moe_route(probs, topk, normalize)
+    want_ids = np.argsort(-probs, axis=1, kind="stable")[:, :topk]
+    assert np.array_equal(ids, want_ids)
+    vals = np.take_along_axis(probs, want_ids, axis=1)
+    if normalize:
+        for t in range(T):
+            den = np.float32(0)
+            for j in range(topk):
+                den = np.float32(den + vals[t, j])
+            vals[t] = vals[t] / den
+        assert np.allclose(w.reshape(T, topk).sum(axis=1), 1, atol=1e-5)
+    assert np.array_equal(w.view(np.uint32), vals.reshape(-1).view(np.uint32))
+    order = np.argsort(ids.reshape(-1), kind="stable")
+    assert np.array_equal(sp, order) and np.array_equal(se, ids.reshape(-1)[order])
+    assert np.all(np.diff(se) >= 0) and np.array_equal(np.sort(sp), np.arange(T * topk))
