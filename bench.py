@@ -302,6 +302,29 @@ def moe_rows(c, name, g, dev):
         gbs = nbytes / (us * 1e-6) / 1e9
         out.append(dict(config=f"{name}_{leg}", us=round(us, 2), GBs=round(gbs, 1),
                         TFLOPS=round(flops / (us * 1e-6) / 1e12, 2), hbm_frac=round(gbs / HBM_PEAK_GBS, 3)))
+    # The whole routed block on the device: router probs -> hq_moe_route -> gated gate/up
+    # (SiLU * up) -> down (routing-weighted) -> combine.  Probs rotate over 16 draws.
+    probs = []
+    for _ in range(16):
+        lg = torch.from_numpy(g.standard_normal((T, E)).astype(np.float32))
+        probs.append(torch.softmax(lg, dim=1).to(dev))
+    hg = torch.zeros((M, I), device=dev)
+    ws_g = torch.empty(max(hipq.moe_gemm_q_gated_ws_bytes(M, T, I, H, dt), 256), dtype=torch.uint8, device=dev)
+    yb = torch.empty((T, H), device=dev)
+
+    def block(i):
+        _, w, sp, se = hipq.moe_route(probs[i % 16], topk, True)
+        hipq.moe_gemm_q_gated(x, wgu, sp, se, E, I, H, dt, topk, out=hg, counts=counts, offsets=offsets, ws=ws_g)
+        hipq.moe_gemm_q(hg, wdn, sp, se, E, H, I, dt, topk, topk_w=w, out=odn, counts=counts, offsets=offsets, ws=ws)
+        hipq.moe_combine(odn, topk, out=yb)
+
+    us = time_launches(block, 64, 16)
+    used = float(np.mean([len(np.unique(torch.topk(p_, topk, dim=1).indices.cpu().numpy())) for p_ in probs]))
+    nbytes = used * (ebytes_gu + ebytes_dn) + 4 * T * E + 4 * T * H * 2
+    gbs = nbytes / (us * 1e-6) / 1e9
+    out.append(dict(config=f"{name}_block", us=round(us, 2), GBs=round(gbs, 1),
+                    TFLOPS=round(2.0 * M * (2 * I * H + H * I) / (us * 1e-6) / 1e12, 2),
+                    hbm_frac=round(gbs / HBM_PEAK_GBS, 3)))
     return out
 
 

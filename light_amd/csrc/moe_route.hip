@@ -37,73 +37,102 @@ struct RouteArgs {
   int T, E, topk, normalize, M, W;
 };
 
-__device__ __forceinline__ bool better(float va, int ia, float vb, int ib) {
-  return va > vb || (va == vb && ia < ib);
+// Selection key: the value mapped to an order-preserving u32 (high half; -0 taken as +0,
+// as Light's comparisons do) and the complement of the index (low half), so the largest key
+// is the largest value at the lowest index.  0 marks a taken or absent slot.
+__device__ __forceinline__ uint32_t ord_f32(float v) {
+  uint32_t u = __float_as_uint(v == 0.f ? 0.f : v);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float unord_f32(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
 
-// Top-k of one row by one wave; lane j < topk ends with the j-th selection (value, index).
-__device__ void topk_row(const float *__restrict__ row, int E, int topk, int lane, float &sel_v, int &sel_i) {
-  float v[kTopkVpl];
+template <int CTRL>
+__device__ __forceinline__ void kmax_dpp(uint32_t &hi, uint32_t &lo) {
+  const uint32_t oh = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)hi, CTRL, 0xF, 0xF, false);
+  const uint32_t ol = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)lo, CTRL, 0xF, 0xF, false);
+  const bool take = oh > hi || (oh == hi && ol > lo);
+  hi = take ? oh : hi;
+  lo = take ? ol : lo;
+}
+
+// Top-k of one row of E <= 64 VPL values by one wave: k rounds of a wave-wide key max (DPP
+// within 16-lane rows, then the four row maxima by readlane).  Lane j < topk ends with the
+// j-th selection; den is the left-to-right f32 sum of the selected values (uniform).
+template <int VPL>
+__device__ void topk_row(const float *__restrict__ row, int E, int topk, int lane, float &sel_v, int &sel_i,
+                         float &den) {
+  uint32_t kh[VPL], kl[VPL];
 #pragma unroll
-  for (int j = 0; j < kTopkVpl; j++) {
+  for (int j = 0; j < VPL; j++) {
     const int e = lane + 64 * j;
-    v[j] = e < E ? row[e] : 0.f;
+    kh[j] = e < E ? ord_f32(row[e]) : 0u;
+    kl[j] = e < E ? 0xffffffffu - (uint32_t)e : 0u;
   }
-  uint32_t taken = 0;
-#pragma unroll
-  for (int j = 0; j < kTopkVpl; j++)
-    if (lane + 64 * j >= E) taken |= 1u << j;
   sel_v = 0.f;
   sel_i = -1;
+  den = 0.f;
   for (int r = 0; r < topk; r++) {
-    float bv = 0.f;
-    int bi = 0x7fffffff;
-    bool have = false;
+    uint32_t hi = kh[0], lo = kl[0];
 #pragma unroll
-    for (int j = 0; j < kTopkVpl; j++) {
-      const int e = lane + 64 * j;
-      if (!(taken >> j & 1u) && (!have || better(v[j], e, bv, bi))) {
-        bv = v[j];
-        bi = e;
-        have = true;
-      }
+    for (int j = 1; j < VPL; j++) {
+      const bool take = kh[j] > hi || (kh[j] == hi && kl[j] > lo);
+      hi = take ? kh[j] : hi;
+      lo = take ? kl[j] : lo;
     }
-    // Wave argmax, ties to the lower index; lanes with nothing left carry index INT_MAX.
+    kmax_dpp<0xB1>(hi, lo);   // quad_perm [1,0,3,2]
+    kmax_dpp<0x4E>(hi, lo);   // quad_perm [2,3,0,1]
+    kmax_dpp<0x141>(hi, lo);  // row_half_mirror
+    kmax_dpp<0x140>(hi, lo);  // row_mirror
+    uint32_t bh = (uint32_t)__builtin_amdgcn_readlane((int)hi, 0), bl = (uint32_t)__builtin_amdgcn_readlane((int)lo, 0);
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-      const float ov = __shfl_xor(bv, off);
-      const int oi = __shfl_xor(bi, off);
-      const bool ohave = oi != 0x7fffffff;
-      if (ohave && (bi == 0x7fffffff || better(ov, oi, bv, bi))) {
-        bv = ov;
-        bi = oi;
-      }
+    for (int q = 16; q < 64; q += 16) {
+      const uint32_t h2 = (uint32_t)__builtin_amdgcn_readlane((int)hi, q);
+      const uint32_t l2 = (uint32_t)__builtin_amdgcn_readlane((int)lo, q);
+      const bool take = h2 > bh || (h2 == bh && l2 > bl);
+      bh = take ? h2 : bh;
+      bl = take ? l2 : bl;
     }
-    if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+    const int idx = (int)(0xffffffffu - bl);
+    const float v = unord_f32(bh);
+    den = __fadd_rn(den, v);  // Sum over the selected values in slot order
+#pragma unroll
+    for (int j = 0; j < VPL; j++)
+      if (lane + 64 * j == idx) kh[j] = kl[j] = 0u;
     if (lane == r) {
-      sel_v = bv;
-      sel_i = bi;
+      sel_v = v;
+      sel_i = idx;
     }
   }
 }
 
 // Top-k of token t by one wave, renormalised if asked; writes topk_ids and weights.
-__device__ void route_token(const RouteArgs &a, int t, int lane, uint16_t *lid) {
-  float sv;
+template <int VPL>
+__device__ void route_token_v(const RouteArgs &a, int t, int lane, uint16_t *lid) {
+  float sv, den;
   int si;
-  topk_row(a.probs + (int64_t)t * a.E, a.E, a.topk, lane, sv, si);
-  float w = sv;
-  if (a.normalize) {
-    float den = 0.f;  // Sum over the k selected values, slot order
-    for (int j = 0; j < a.topk; j++) den = __fadd_rn(den, __shfl(sv, j));
-    w = __fdiv_rn(sv, den);
-  }
+  topk_row<VPL>(a.probs + (int64_t)t * a.E, a.E, a.topk, lane, sv, si, den);
+  const float w = a.normalize ? __fdiv_rn(sv, den) : sv;
   if (lane < a.topk) {
     const int64_t p = (int64_t)t * a.topk + lane;
     a.topk_ids[p] = si;
     a.weights[p] = w;
     if (lid) lid[p] = (uint16_t)si;
   }
+}
+
+__device__ __forceinline__ void route_token(const RouteArgs &a, int t, int lane, uint16_t *lid) {
+  if (a.E <= 64)
+    route_token_v<1>(a, t, lane, lid);
+  else if (a.E <= 128)
+    route_token_v<2>(a, t, lane, lid);
+  else if (a.E <= 256)
+    route_token_v<4>(a, t, lane, lid);
+  else if (a.E <= 512)
+    route_token_v<8>(a, t, lane, lid);
+  else
+    route_token_v<16>(a, t, lane, lid);
 }
 
 // Mask of lanes holding the same id as this lane (among valid lanes).
@@ -121,15 +150,16 @@ template <bool TOPK>
 __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(RouteArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int nthr = blockDim.x, nwav = nthr >> 6;
   uint16_t *lid = reinterpret_cast<uint16_t *>(smem);                                   // [M]
   uint16_t *wcnt = lid + ((a.M + 7) & ~7);                                              // [W][E]
   uint32_t *base = reinterpret_cast<uint32_t *>(wcnt + (((int64_t)a.W * a.E + 7) & ~7));  // [E]
 
-  for (int64_t i = t; i < (int64_t)a.W * a.E; i += kRouteThreads) wcnt[i] = 0;
+  for (int64_t i = t; i < (int64_t)a.W * a.E; i += nthr) wcnt[i] = 0;
   if constexpr (TOPK) {
-    for (int tok = wave; tok < a.T; tok += kRouteWaves) route_token(a, tok, lane, lid);
+    for (int tok = wave; tok < a.T; tok += nwav) route_token(a, tok, lane, lid);
   } else {
-    for (int p = t; p < a.M; p += kRouteThreads) {
+    for (int p = t; p < a.M; p += nthr) {
       int64_t id = a.ids_in[p];
       id = id < 0 ? 0 : (id >= a.E ? a.E - 1 : id);  // ids are in [0, E); clamped for memory safety
       lid[p] = (uint16_t)id;
@@ -141,7 +171,7 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(RouteArgs a) {
   while ((1 << nbits) < a.E) nbits++;
   const uint64_t lt = (1ull << lane) - 1;
   // Phase A: per-chunk counts.
-  for (int w = wave; w < a.W; w += kRouteWaves) {
+  for (int w = wave; w < a.W; w += nwav) {
     const int p = 64 * w + lane;
     const bool valid = p < a.M;
     const int id = valid ? lid[p] : 0;
@@ -150,7 +180,7 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(RouteArgs a) {
   }
   __syncthreads();
   // Phase B: per expert, chunk counts -> exclusive offsets; totals into base.
-  for (int e = t; e < a.E; e += kRouteThreads) {
+  for (int e = t; e < a.E; e += nthr) {
     uint32_t run = 0;
     for (int w = 0; w < a.W; w++) {
       const uint32_t c = wcnt[w * a.E + e];
@@ -183,7 +213,7 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(RouteArgs a) {
   }
   __syncthreads();
   // Phase C: placement.
-  for (int w = wave; w < a.W; w += kRouteWaves) {
+  for (int w = wave; w < a.W; w += nwav) {
     const int p = 64 * w + lane;
     const bool valid = p < a.M;
     const int id = valid ? lid[p] : 0;
@@ -218,7 +248,10 @@ int run_route(bool topk, const RouteArgs &a, hipStream_t s) {
       return rc;
     attr_done[topk] = true;
   }
-  kern<<<1, kRouteThreads, lds, s>>>(a);
+  // One wave per chunk of 64 pairs (and per token for the top-k), up to 16 waves.
+  int64_t waves = a.W > a.T ? a.W : a.T;
+  waves = waves < 1 ? 1 : (waves > kRouteWaves ? kRouteWaves : waves);
+  kern<<<1, (unsigned)(64 * waves), lds, s>>>(a);
   return check_launch("moe_route");
 }
 
