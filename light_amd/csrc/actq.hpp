@@ -99,6 +99,53 @@ __device__ __forceinline__ ActQ act_quant8_fast(const float v[4]) {
   return r;
 }
 
+// Two-level quantization of one 32-element block held by two adjacent lanes (lanes 2i,
+// 2i+1), sixteen elements each: the work per element is four VALU operations.  Same
+// scales as act_quant8_fast (d = amax / 127, e = d / 254, reciprocal-based); rounding to
+// nearest-even by the magic-number add (2^23 + 2^22: the float's low byte is the rounded
+// integer).  |v * id| <= 127 (1 + 2^-22) and |r * ie| <= 127 (1 + 2^-20), so no level
+// needs a clamp.  q1 / q2: the lane's sixteen quants per level, little-endian bytes.
+struct ActQ16 {
+  uint32_t q1[4], q2[4];
+  float d, e, sum;
+};
+
+__device__ __forceinline__ uint32_t pack_lo_bytes(float a, float b, float c, float d) {
+  const uint32_t ab = __builtin_amdgcn_perm(__float_as_uint(b), __float_as_uint(a), 0x0c0c0400u);
+  const uint32_t cd = __builtin_amdgcn_perm(__float_as_uint(d), __float_as_uint(c), 0x04000c0cu);
+  return ab | cd;
+}
+
+__device__ __forceinline__ ActQ16 act_quant16_fast(const float (&v)[16]) {
+  constexpr float MAGIC = 12582912.0f;  // 1.5 * 2^23
+  float amax = 0.f;
+#pragma unroll
+  for (int j = 0; j < 16; j += 2) amax = __builtin_fmaxf(amax, __builtin_fmaxf(fabsf(v[j]), fabsf(v[j + 1])));
+  amax = fmaxf(amax, dpp8f<0xB1>(amax));
+  ActQ16 r;
+  const float ra = amax > 0.f ? __builtin_amdgcn_rcpf(amax) : 0.f;
+  r.d = amax * (1.0f / 127.0f);
+  r.e = r.d * (1.0f / 254.0f);
+  const float id = 127.0f * ra, ie = 254.0f * id;
+  float f1[16], f2[16];
+#pragma unroll
+  for (int j = 0; j < 16; j++) {
+    f1[j] = __fmaf_rn(v[j], id, MAGIC);
+    const float res = __fmaf_rn(-r.d, f1[j] - MAGIC, v[j]);
+    f2[j] = __fmaf_rn(res, ie, MAGIC);
+  }
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    r.q1[k] = pack_lo_bytes(f1[4 * k], f1[4 * k + 1], f1[4 * k + 2], f1[4 * k + 3]);
+    r.q2[k] = pack_lo_bytes(f2[4 * k], f2[4 * k + 1], f2[4 * k + 2], f2[4 * k + 3]);
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < 16; j += 4) s += (v[j] + v[j + 1]) + (v[j + 2] + v[j + 3]);
+  r.sum = s + dpp8f<0xB1>(s);
+  return r;
+}
+
 // One lane's Q4_K contribution from its two sub-blocks A (low nibbles) and B (high
 // nibbles) of a 64-element pair: d * sum_s sc_s (d1_s dot1_s + e_s dot2_s)
 // - dmin * sum_s m_s sx_s, with de = (dA, eA, dB, eB) and ss = (sxA, sxB).  Every
@@ -107,6 +154,20 @@ __device__ __forceinline__ float q4k_pair(float d, float dmin, float scA, float 
                                           float2 ss, int dA, int dA2, int dB, int dB2) {
   const float va = __fmaf_rn(de.y, (float)dA2, __fmul_rn(de.x, (float)dA));
   const float vb = __fmaf_rn(de.w, (float)dB2, __fmul_rn(de.z, (float)dB));
+  const float v = __fmaf_rn(scB, vb, __fmul_rn(scA, va));
+  const float mn = __fmaf_rn(mnB, ss.y, __fmul_rn(mnA, ss.x));
+  return __fmaf_rn(d, v, -__fmul_rn(dmin, mn));
+}
+
+// q4k_pair with sub-block B's dots taken on 16 * (q - 8) (high nibbles masked in place with
+// the sign bit flipped): sum(q x) = dot / 16 + 8 * sum(x), with the exact block sum sx of x
+// standing in for the quantized one (the difference is below the activations' own
+// quantization error, e/2 per element).
+__device__ __forceinline__ float q4k_pair_h16(float d, float dmin, float scA, float scB, float mnA, float mnB,
+                                              float4 de, float2 ss, int dA, int dA2, int dB16, int dB216) {
+  const float va = __fmaf_rn(de.y, (float)dA2, __fmul_rn(de.x, (float)dA));
+  const float vb16 = __fmaf_rn(de.w, (float)dB216, __fmul_rn(de.z, (float)dB16));
+  const float vb = __fmaf_rn(vb16, 0.0625f, __fmul_rn(8.0f, ss.y));
   const float v = __fmaf_rn(scB, vb, __fmul_rn(scA, va));
   const float mn = __fmaf_rn(mnB, ss.y, __fmul_rn(mnA, ss.x));
   return __fmaf_rn(d, v, -__fmul_rn(dmin, mn));

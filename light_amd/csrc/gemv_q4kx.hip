@@ -10,16 +10,19 @@
 // Design (gfx950, wave64):
 //  * Activations are two-level int8 (the act layout of common.hpp).  They come either
 //    prepared from global memory (XIN = false) or from x (F32 / BF16 / F16) that each
-//    workgroup quantizes into LDS itself (XIN = true, act_quant8_fast), saving a launch.
+//    workgroup quantizes into LDS itself (XIN = true, act_quant16_fast: two lanes per
+//    32-block), saving a launch.
 //  * A lane owns one 64-element unit of a weight row (a weight-format policy: Q4kUnit =
 //    one (super-block, 64-element pair) of Q4_K, Int4Unit = two 32-element code blocks of
 //    quant.Int4) and keeps the unit's activations in registers for the whole kernel.  A
 //    team of TP lanes covers a row; a workgroup holds RW teams.  Products are exact
 //    v_dot4_i32_i8 chains scaled once per 32-block.
-//  * Workgroups are persistent (two per CU).  A ring of D register slots (D = 1) keeps the
-//    next row group's loads in flight while the current one is reduced; every load is
-//    unconditional (inactive lanes and rows past N read valid addresses and their sums are
-//    dropped), so no load sits in a branch and the compiler's wait counts stay exact.
+//  * Workgroups are persistent (two per CU).  One register slot keeps the next row group's
+//    loads in flight while the current one is reduced; every load is unconditional
+//    (inactive lanes and rows past N read valid addresses and their sums are dropped), so
+//    no load sits in a branch and the compiler's wait counts stay exact.
+//  * Q4_K high nibbles are masked in place with the sign bit flipped (16 * (q - 8) as a
+//    signed byte, one and-xor per dword); the -8 folds into the block-sum term.
 //  * Team sums: DPP row sums, then v_readlane over the wave's four rows; teams wider than a
 //    wave add their 16-lane row sums through LDS (one barrier per group).  Row sums are added
 //    in row order in both cases.
@@ -53,11 +56,6 @@ struct Q4kxArgs {
 
 namespace {
 
-template <int K>
-__device__ __forceinline__ uint32_t qb(uint32_t v) {
-  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, K * 0x55, 0xF, 0xF, false);
-}
-
 __device__ __forceinline__ float rsum16(float v) {
   v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
   v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
@@ -88,7 +86,7 @@ template <bool Q5>
 struct QkUnit {
   static constexpr int BB = Q5 ? 176 : 144, QO = Q5 ? 48 : 16;
   struct Lane {
-    uint32_t qoff, hoff, qhoff;  // byte offsets of the quant chunk / this lane's header dword / qh
+    uint32_t qoff, hoff, qhoff;  // byte offsets of the quant chunk / the block header / qh
     int ja;                      // first 32-block of x
     uint32_t sel, mlo, mhi;
     int ka, sh;
@@ -96,7 +94,7 @@ struct QkUnit {
   struct W {
     u32x4_t q0, q1;
     u32x4_t h0, h1;  // Q5_K only
-    uint32_t h;
+    u32x4_t hd;      // the block header (d, dmin, scales[12]); the quad's four lanes load the same 16 B
   };
   struct X {
     uint32_t xa[8], xb[8], ya[8], yb[8];
@@ -107,7 +105,7 @@ struct QkUnit {
     Lane L;
     const int b = u >> 2, p = u & 3;
     L.qoff = b * BB + QO + p * 32;
-    L.hoff = b * BB + 4 * p;
+    L.hoff = b * BB;
     L.qhoff = b * BB + 16;
     L.ja = b * 8 + 2 * p;
     const bool lowj = p < 2;
@@ -129,7 +127,7 @@ struct QkUnit {
       r.h0 = *reinterpret_cast<const u32x4_t *>(w + (ro + L.qhoff));
       r.h1 = *reinterpret_cast<const u32x4_t *>(w + (ro + L.qhoff + 16));
     }
-    r.h = *reinterpret_cast<const uint32_t *>(w + (ro + L.hoff));
+    r.hd = *reinterpret_cast<const u32x4_t *>(w + (ro + L.hoff));
   }
   __device__ static void load_x(const uint8_t *q1, const uint8_t *q2, const uint8_t *de, const uint8_t *sx,
                                 int64_t blk, X &x) {
@@ -147,7 +145,7 @@ struct QkUnit {
   }
   template <int MM>
   __device__ static void dot(const W &w, const X (&x)[MM], const Lane &L, float (&out)[MM]) {
-    const uint32_t h0 = qb<0>(w.h), h1 = qb<1>(w.h), h2 = qb<2>(w.h), h3 = qb<3>(w.h);
+    const uint32_t h0 = w.hd[0], h1 = w.hd[1], h2 = w.hd[2], h3 = w.hd[3];
     const float d = h2f(h0 & 0xffffu), dmin = h2f(h0 >> 16);
     // 6-bit (scale, min) of sub-blocks 2p and 2p+1 (getScaleMinK4, quant/q4_k.go:83-89),
     // selected branch-free with lane constants: p < 2 takes the low six bits of
@@ -163,14 +161,19 @@ struct QkUnit {
 #pragma unroll
     for (int k = 0; k < 4; k++) {
       lo[k] = w.q0[k] & 0x0F0F0F0Fu;
-      hi[k] = (w.q0[k] >> 4) & 0x0F0F0F0Fu;
       lo[k + 4] = w.q1[k] & 0x0F0F0F0Fu;
-      hi[k + 4] = (w.q1[k] >> 4) & 0x0F0F0F0Fu;
       if constexpr (Q5) {
+        hi[k] = (w.q0[k] >> 4) & 0x0F0F0F0Fu;
+        hi[k + 4] = (w.q1[k] >> 4) & 0x0F0F0F0Fu;
         lo[k] |= ((w.h0[k] >> L.sh) & 0x01010101u) << 4;
         hi[k] |= ((w.h0[k] >> (L.sh + 1)) & 0x01010101u) << 4;
         lo[k + 4] |= ((w.h1[k] >> L.sh) & 0x01010101u) << 4;
         hi[k + 4] |= ((w.h1[k] >> (L.sh + 1)) & 0x01010101u) << 4;
+      } else {
+        // High nibbles in place, top bit flipped: the signed byte is 16 * (q - 8), one
+        // and-xor per dword instead of a shift and a mask.
+        hi[k] = (w.q0[k] & 0xF0F0F0F0u) ^ 0x80808080u;
+        hi[k + 4] = (w.q1[k] & 0xF0F0F0F0u) ^ 0x80808080u;
       }
     }
 #pragma unroll
@@ -183,7 +186,10 @@ struct QkUnit {
         dA2 = dot4((int)lo[k], (int)x[mm].ya[k], dA2);
         dB2 = dot4((int)hi[k], (int)x[mm].yb[k], dB2);
       }
-      out[mm] = q4k_pair(d, dmin, scA, scB, mnA, mnB, x[mm].de, x[mm].ss, dA, dA2, dB, dB2);
+      if constexpr (Q5)
+        out[mm] = q4k_pair(d, dmin, scA, scB, mnA, mnB, x[mm].de, x[mm].ss, dA, dA2, dB, dB2);
+      else
+        out[mm] = q4k_pair_h16(d, dmin, scA, scB, mnA, mnB, x[mm].de, x[mm].ss, dA, dA2, dB, dB2);
     }
   }
 };
@@ -322,7 +328,7 @@ __global__ __launch_bounds__(512) void gemv_q4kx_kernel(Q4kxArgs a) {
   const int m0 = blockIdx.y * MM;
   const int G = gridDim.x;
   // Iteration i of this workgroup -> row group: whole chunks of CG groups (32 rows with
-  // AOUT), chunks strided over the grid.
+  // AOUT), chunks strided over the grid.  Groups past the end clamp to row N - 1.
   const int CG = AOUT ? 32 / RW : 1;
   const int nchunks = (ngroups + CG - 1) / CG;
   const int niter = ((nchunks - (int)blockIdx.x + G - 1) / G) * CG;
@@ -335,44 +341,61 @@ __global__ __launch_bounds__(512) void gemv_q4kx_kernel(Q4kxArgs a) {
     if (GATED) U::load(a.w1, a.s1, a.z1, a, row_, L, wr[SLOT][NW - 1]);        \
   } while (0)
 
+  // One register slot: the next group's loads go out once the current one is reduced.
+  // (Deeper rings -- two to four groups in flight per wave -- were measured slower: this
+  // kernel is bound by VALU issue as much as by HBM, and more outstanding rows only spread
+  // the DRAM traffic.)
   typename U::W wr[1][NW];
   Q4KX_LOAD(0, Q4KX_GRP(0));
 
   typename U::X xr[MM];
   const int64_t lds_act = XIN ? q4kx_act_lds(MM, a.K) : 0;
   if constexpr (XIN) {
-    // Quantize this workgroup's MM rows of x into LDS (8 lanes per 32-block).  A chunk's
-    // loads are all issued before its quantization.
+    // Quantize this workgroup's MM rows of x into LDS: a task is half a 32-block (sixteen
+    // elements) on one lane, two lanes per block (act_quant16_fast).
     uint8_t *lq1 = smem, *lq2 = smem + (int64_t)MM * a.K;
     float2 *lde = reinterpret_cast<float2 *>(smem + 2 * (int64_t)MM * a.K);
     float *lsx = reinterpret_cast<float *>(smem + 2 * (int64_t)MM * a.K + 8 * (int64_t)MM * KB);
-    constexpr int XT = 4;
-    const int ntask = MM * KB * 8;
-    for (int base = 0; base < ntask; base += XT * (int)blockDim.x) {
-      float4 xv[XT];
-#pragma unroll
-      for (int i = 0; i < XT; i++) {
-        int task = base + i * (int)blockDim.x + t;
-        task = task < ntask ? task : ntask - 1;
-        const int blk = task >> 3, sub = task & 7, mm = blk / KB, kb = blk - mm * KB;
-        const int m = m0 + mm < a.M ? m0 + mm : a.M - 1;
-        xv[i] = load_x4<XDT>(a.x, (int64_t)m * a.K + kb * 32 + sub * 4);
-      }
-#pragma unroll
-      for (int i = 0; i < XT; i++) {
-        const int task = base + i * (int)blockDim.x + t;
-        const int blk = task >> 3, sub = task & 7;
-        const float v[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
-        const ActQ q = act_quant8_fast(v);
-        if (task < ntask) {  // uniform over each aligned 8-lane group
-          reinterpret_cast<uint32_t *>(lq1 + blk * 32)[sub] = q.q1;
-          reinterpret_cast<uint32_t *>(lq2 + blk * 32)[sub] = q.q2;
-          if (sub == 0) {
-            lde[blk] = make_float2(q.d, q.e);
-            lsx[blk] = q.sum;
-          }
+    const int ntask = MM * KB * 2, bd = (int)blockDim.x;
+    // Element index of task i (clamped into range): rows of x are whole blocks, so the
+    // tasks of (mm, block, half) are contiguous in x.
+    auto xidx = [&](int i) __attribute__((always_inline)) {
+      i = i < ntask ? i : ntask - 1;
+      const int mm = MM == 1 ? 0 : i / (2 * KB);
+      const int m = m0 + mm < a.M ? m0 + mm : a.M - 1;
+      return (int64_t)m * a.K + (int64_t)(i - mm * 2 * KB) * 16;
+    };
+    auto quant_store = [&](const float (&v)[16], int task) __attribute__((always_inline)) {
+      const ActQ16 q = act_quant16_fast(v);
+      if (task < ntask) {  // both lanes of a block agree (ntask is even)
+        const int blk = task >> 1, half = task & 1;
+        *reinterpret_cast<u32x4_t *>(lq1 + blk * 32 + half * 16) = u32x4_t{q.q1[0], q.q1[1], q.q1[2], q.q1[3]};
+        *reinterpret_cast<u32x4_t *>(lq2 + blk * 32 + half * 16) = u32x4_t{q.q2[0], q.q2[1], q.q2[2], q.q2[3]};
+        if (half == 0) {
+          lde[blk] = make_float2(q.d, q.e);
+          lsx[blk] = q.sum;
         }
       }
+    };
+    constexpr int XR = XDT == F32 ? 4 : 2;  // 16-byte pieces of a task's sixteen elements
+    auto to_f32 = [&](const u32x4_t (&raw)[XR], float (&v)[16]) __attribute__((always_inline)) {
+#pragma unroll
+      for (int j = 0; j < 16; j++) {
+        const uint32_t w32 = raw[XDT == F32 ? j / 4 : j / 8][XDT == F32 ? j % 4 : (j % 8) / 2];
+        if constexpr (XDT == F32)
+          v[j] = __uint_as_float(w32);
+        else
+          v[j] = XDT == BF16 ? bf2f((j & 1) ? w32 >> 16 : w32 & 0xffffu) : h2f((j & 1) ? w32 >> 16 : w32 & 0xffffu);
+      }
+    };
+    for (int base = 0; base < ntask; base += bd) {
+      u32x4_t raw[XR];
+      const uint8_t *xp = static_cast<const uint8_t *>(a.x) + xidx(base + t) * (XDT == F32 ? 4 : 2);
+#pragma unroll
+      for (int r = 0; r < XR; r++) raw[r] = *reinterpret_cast<const u32x4_t *>(xp + 16 * r);
+      float v[16];
+      to_f32(raw, v);
+      if (base + t < ntask) quant_store(v, base + t);
     }
     __syncthreads();
 #pragma unroll
@@ -392,6 +415,9 @@ __global__ __launch_bounds__(512) void gemv_q4kx_kernel(Q4kxArgs a) {
   float *part = reinterpret_cast<float *>(smem + lds_act);
   float *hbuf = part + (wpt > 1 ? 2 * RW * NW * MM * hpt : 0);
 
+  // One iteration: wait for the slot (straight-line form), reduce the group's rows, refill
+  // the slot with the group D iterations ahead, write the outputs.  VALID is
+  // workgroup-uniform; REFILL is a compile-time constant in the straight-line form.
   for (int it = 0; it < niter; it++) {
     const int grp = Q4KX_GRP(it);
     float res[NW][MM];
@@ -404,7 +430,6 @@ __global__ __launch_bounds__(512) void gemv_q4kx_kernel(Q4kxArgs a) {
     }
     // The slot is consumed: refill it with the next group (unconditionally).
     Q4KX_LOAD(0, Q4KX_GRP(it + 1));
-
     const int row = grp * RW + team;
     float *hb = hbuf + ((it / CG) & 1) * (MM * 32);
     if (wpt <= 1) {
