@@ -11,6 +11,7 @@
 #include <cctype>
 #include <cstring>
 
+#include "gguf.hpp"
 #include "light.hpp"
 #include "ops.hpp"
 #include "registry.hpp"
@@ -90,6 +91,31 @@ ops::Int4 make_int4(const Tensor &codes, const Tensor &scales, const Tensor &zer
   w.group = group;
   w.perm = std::move(perm);
   return w;
+}
+
+// GGUF strings are byte strings: decoded as UTF-8, with undecodable bytes kept by
+// surrogateescape so every key and value round-trips.
+py::str gguf_str(const std::string &s) {
+  PyObject *o = PyUnicode_DecodeUTF8(s.data(), (Py_ssize_t)s.size(), "surrogateescape");
+  if (!o) throw py::error_already_set();
+  return py::reinterpret_steal<py::str>(o);
+}
+
+py::object value_to_py(const gguf::Value &v) {
+  switch (v.type) {
+    case gguf::TypeUInt8: case gguf::TypeUInt16: case gguf::TypeUInt32: case gguf::TypeUInt64:
+      return py::int_(v.u);
+    case gguf::TypeInt8: case gguf::TypeInt16: case gguf::TypeInt32: case gguf::TypeInt64:
+      return py::int_(v.i);
+    case gguf::TypeFloat32: case gguf::TypeFloat64: return py::float_(v.f);
+    case gguf::TypeBool: return py::bool_(v.b);
+    case gguf::TypeString: return gguf_str(v.s);
+    default: {
+      py::list l;
+      for (const gguf::Value &e : v.arr) l.append(value_to_py(e));
+      return l;
+    }
+  }
 }
 
 }  // namespace
@@ -187,4 +213,66 @@ PYBIND11_MODULE(_light, m) {
         py::arg("gelu") = false);
   m.def("moe_combine", &ops::MoECombine);
   m.def("dequantize", &ops::Dequantize);
+
+  // GGUF byte path
+  py::class_<gguf::TensorInfo>(m, "GGUFTensorInfo")
+      .def_readonly("name", &gguf::TensorInfo::name)
+      .def_property_readonly("dtype", [](const gguf::TensorInfo &t) { return std::string(DTypeName(t.dtype)); })
+      .def_readonly("dims", &gguf::TensorInfo::dims)
+      .def_readonly("offset", &gguf::TensorInfo::offset)
+      .def_readonly("bytes", &gguf::TensorInfo::bytes);
+  py::class_<gguf::File, std::shared_ptr<gguf::File>>(m, "GGUFFile")
+      .def_readonly("version", &gguf::File::version)
+      .def_readonly("order", &gguf::File::order)
+      .def_readonly("key_order", &gguf::File::key_order)
+      .def_readonly("data_base", &gguf::File::data_base)
+      .def_property_readonly("meta",
+                             [](const gguf::File &f) {
+                               py::dict d;
+                               for (const auto &kv : f.meta) d[gguf_str(kv.first)] = value_to_py(kv.second);
+                               return d;
+                             })
+      .def("info", &gguf::File::Info, py::return_value_policy::copy)
+      .def("tensor_bytes",
+           [](const gguf::File &f, const std::string &n) {
+             std::vector<uint8_t> b = f.TensorBytes(n);
+             return py::bytes((const char *)b.data(), b.size());
+           })
+      .def("load_tensor", [](const gguf::File &f, const std::string &n,
+                             const std::string &dev) { return f.LoadTensor(n, parse_device(dev)); },
+           py::arg("name"), py::arg("device") = "cpu")
+      .def("tensor_row_major", [](const gguf::File &f, const std::string &n,
+                                  const std::string &dev) { return f.TensorRowMajor(n, parse_device(dev)); },
+           py::arg("name"), py::arg("device") = "cpu")
+      .def("string", [](const gguf::File &f, const std::string &k) -> py::object {
+        std::string s;
+        if (!f.String(k, &s)) return py::none();
+        return py::str(s);
+      })
+      .def("int64", [](const gguf::File &f, const std::string &k) -> py::object {
+        int64_t v;
+        if (!f.Int64(k, &v)) return py::none();
+        return py::int_(v);
+      })
+      .def("float64", [](const gguf::File &f, const std::string &k) -> py::object {
+        double v;
+        if (!f.Float64(k, &v)) return py::none();
+        return py::float_(v);
+      });
+  m.def(
+      "gguf_open_bytes",
+      [](py::bytes b, bool sized) {
+        std::string s = b;
+        return gguf::File::Open(gguf::MemorySource(std::vector<uint8_t>(s.begin(), s.end()), sized));
+      },
+      py::arg("data"), py::arg("sized") = true);
+  m.def("gguf_open", [](const std::string &path) { return gguf::File::Open(gguf::FileSource(path)); });
+  m.def(
+      "gguf_load_experts",
+      [](const gguf::File &f, const std::string &prefix, const std::string &dev) {
+        gguf::ExpertStacks e = gguf::LoadExperts(f, prefix, parse_device(dev));
+        return py::make_tuple(e.gate_up, e.down);
+      },
+      py::arg("file"), py::arg("prefix"), py::arg("device") = "cpu");
+  m.def("dtype_from_ggml", [](uint32_t t) { return std::string(DTypeName(gguf::DTypeFromGGML(t))); });
 }
