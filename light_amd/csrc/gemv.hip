@@ -21,7 +21,10 @@
 //  * Q8_0 (34 B) and Q6_K (210 B) blocks are only 2-byte aligned.  Each wave
 //    streams its rows' raw bytes into LDS with direct global->LDS loads (two slices,
 //    the next row group loading while the current one is computed), and lanes read
-//    their blocks back with aligned dword reads re-aligned by v_alignbit.
+//    their blocks back with aligned dword reads re-aligned by v_alignbit.  The first
+//    group's loads are issued before anything waits on x.  Up to K = 8192 the workgroup
+//    quantizes its own F32 x rows into LDS (two lanes per 32-block), which saves the
+//    separate quantize launch.
 //  * Other shapes take a generic wave-per-row kernel on F32 activations built on
 //    the bit-exact decoder of dequant.hip.
 #include "actq.hpp"
@@ -406,6 +409,7 @@ int launch_moe_gemv_q4k(const void *act, const void *w, const int64_t *pairs, co
 // ---------------------------------------------------------------------------
 struct StagedArgs {
   const uint8_t *act;
+  const float *x;  // XIN: F32 x (M, K), quantized by each workgroup into LDS
   const uint8_t *w;
   float *out;
   int M, N, K, nb;
@@ -426,17 +430,63 @@ __device__ __forceinline__ void lds_unaligned(const uint8_t *lds, int o, uint32_
 }
 
 // Direct loads of the row group starting at row r0 into an LDS slice: ni = lds_wave / 1 KB
-// loads of 1 KB, byte offsets clamped into the weight (a group past the end, or the slice's
-// tail past the group, reloads valid bytes that are never read).
-__device__ __forceinline__ void staged_issue(const StagedArgs &a, uint8_t *slice, int64_t r0, int lane) {
+// loads of 1 KB, byte offsets clamped into the weight (the slice's tail past the group
+// reloads valid bytes that are never read).  A group past the end issues nothing -- clamping
+// it would aim every idle wave at the same last row, one L2 channel -- and the return
+// value is the number of loads issued (wave-uniform), for the wait that follows.
+__device__ __forceinline__ int staged_issue(const StagedArgs &a, uint8_t *slice, int64_t r0, int lane) {
+  if (r0 >= a.N) return 0;
   const int64_t total = (int64_t)a.N * a.row_bytes;
-  const int64_t base = (r0 < a.N ? r0 : a.N - 1) * a.row_bytes;
+  const int64_t base = r0 * a.row_bytes;
   const uint32_t dst = (uint32_t)(uintptr_t)slice;
-  for (int i = 0; i < (a.lds_wave >> 10); i++) {
+  const int ni = a.lds_wave >> 10;
+  for (int i = 0; i < ni; i++) {
     int64_t off = base + i * 1024 + lane * 16;
     off = off < total - 16 ? off : total - 16;
     dma16(a.w + off, __builtin_amdgcn_readfirstlane(dst + i * 1024));
   }
+  return ni;
+}
+
+// XIN: the workgroup quantizes x rows m0 .. m0+MM-1 (clamped to M-1) into LDS at xs, in the
+// act layout of an MM-row activation: q1 [MM][K] | q2 [MM][K] | (d, e) [MM][K/32] | sx
+// [MM][K/32].  Two lanes per 32-block, sixteen elements each (act_quant16_fast: reciprocal
+// scales, four VALU operations per element), as the Q4_K GEMV quantizes its own x.
+struct ActView {
+  const uint8_t *p;
+  int64_t q2, d, s;  // byte offsets of q2, (d, e) and sx from p
+};
+
+__host__ __device__ constexpr int64_t staged_xin_lds(int MM, int64_t K) { return MM * (2 * K + 12 * (K / 32)); }
+
+template <int MM>
+__device__ __forceinline__ ActView staged_quantize_x(const StagedArgs &a, uint8_t *xs, int m0) {
+  const int nb = a.K >> 5, ntask = MM * nb * 2;
+  const int64_t q2 = (int64_t)MM * a.K, d = 2 * q2, so = d + 8 * (int64_t)MM * nb;
+  for (int base = 0; base < ntask; base += 256) {
+    const int t = base + (int)threadIdx.x;
+    const int tc = t < ntask ? t : ntask - 1;  // ntask is even: both lanes of a block agree
+    const int blk = tc >> 1, half = tc & 1, mm = MM == 1 ? 0 : blk / nb;
+    const int m = m0 + mm < a.M ? m0 + mm : a.M - 1;
+    const float4 *xp = reinterpret_cast<const float4 *>(a.x + (int64_t)m * a.K + (int64_t)(blk - mm * nb) * 32 + half * 16);
+    float v[16];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const float4 f = xp[r];
+      v[4 * r] = f.x, v[4 * r + 1] = f.y, v[4 * r + 2] = f.z, v[4 * r + 3] = f.w;
+    }
+    const ActQ16 q = act_quant16_fast(v);
+    if (t < ntask) {
+      *reinterpret_cast<uint4 *>(xs + blk * 32 + half * 16) = make_uint4(q.q1[0], q.q1[1], q.q1[2], q.q1[3]);
+      *reinterpret_cast<uint4 *>(xs + q2 + blk * 32 + half * 16) = make_uint4(q.q2[0], q.q2[1], q.q2[2], q.q2[3]);
+      if (half == 0) {
+        reinterpret_cast<float2 *>(xs + d)[blk] = make_float2(q.d, q.e);
+        reinterpret_cast<float *>(xs + so)[blk] = q.sum;
+      }
+    }
+  }
+  __syncthreads();
+  return ActView{xs, q2, d, so};
 }
 
 // Bit j of n (j < 4) to bit 0 of byte j.
@@ -466,7 +516,7 @@ __device__ __forceinline__ void b32_quants(const uint8_t *lds, int o, uint32_t (
   }
 }
 
-template <int DT, int CPL, int R, int MM>
+template <int DT, int CPL, int R, int MM, bool XIN>
 __global__ __launch_bounds__(256) void gemv_q80_kernel(StagedArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   constexpr int BB = DT == Q8_0 ? 34 : DT == Q4_0 ? 18 : 22;
@@ -476,19 +526,28 @@ __global__ __launch_bounds__(256) void gemv_q80_kernel(StagedArgs a) {
   const int nwaves = gridDim.x * 4;
   const int m0 = blockIdx.y * MM;
 
+  // The first row group's weight bytes are requested before anything waits on x.
+  uint8_t *lds2 = smem + (threadIdx.x >> 6) * 2 * a.lds_wave;
+  staged_issue(a, lds2, (int64_t)wave * R, lane);
+  ActView av;
+  if constexpr (XIN)
+    av = staged_quantize_x<MM>(a, smem + 8 * a.lds_wave, m0);
+  else
+    av = ActView{a.act, a.q2_off, a.d_off, a.s_off};
+
   int xv[MM][CPL][8], yv[MM][CPL][8];
   float2 dx[MM][CPL];
   float ox[MM][CPL];  // OFF * (sum of the block's x)
 #pragma unroll
   for (int mm = 0; mm < MM; mm++) {
-    const int m = m0 + mm < a.M ? m0 + mm : a.M - 1;
+    const int m = XIN ? mm : (m0 + mm < a.M ? m0 + mm : a.M - 1);
 #pragma unroll
     for (int i = 0; i < CPL; i++) {
       const int bl = lane + 64 * i;
       const bool ok = bl < a.nb;
       const int64_t blk = (int64_t)m * a.nb + (ok ? bl : 0);
-      const uint4 *xs = reinterpret_cast<const uint4 *>(a.act + blk * 32);
-      const uint4 *x2 = reinterpret_cast<const uint4 *>(a.act + a.q2_off + blk * 32);
+      const uint4 *xs = reinterpret_cast<const uint4 *>(av.p + blk * 32);
+      const uint4 *x2 = reinterpret_cast<const uint4 *>(av.p + av.q2 + blk * 32);
       const uint4 v0 = xs[0], v1 = xs[1], u0 = x2[0], u1 = x2[1];
       const int V[8] = {(int)v0.x, (int)v0.y, (int)v0.z, (int)v0.w, (int)v1.x, (int)v1.y, (int)v1.z, (int)v1.w};
       const int U[8] = {(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w, (int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
@@ -497,25 +556,21 @@ __global__ __launch_bounds__(256) void gemv_q80_kernel(StagedArgs a) {
         xv[mm][i][k] = ok ? V[k] : 0;
         yv[mm][i][k] = ok ? U[k] : 0;
       }
-      dx[mm][i] = ok ? reinterpret_cast<const float2 *>(a.act + a.d_off)[blk] : make_float2(0.f, 0.f);
+      dx[mm][i] = ok ? reinterpret_cast<const float2 *>(av.p + av.d)[blk] : make_float2(0.f, 0.f);
       ox[mm][i] = 0.f;
-      if constexpr (DT != Q8_0) ox[mm][i] = ok ? OFF * reinterpret_cast<const float *>(a.act + a.s_off)[blk] : 0.f;
+      if constexpr (DT != Q8_0) ox[mm][i] = ok ? OFF * reinterpret_cast<const float *>(av.p + av.s)[blk] : 0.f;
     }
   }
 
   // Two LDS slices per wave, filled by direct loads one row group ahead.
-  uint8_t *lds2 = smem + (threadIdx.x >> 6) * 2 * a.lds_wave;
-  const int ni = a.lds_wave >> 10;
   const int64_t stride = (int64_t)nwaves * R;
-  staged_issue(a, lds2, (int64_t)wave * R, lane);
   int cur = 0;
   for (int64_t row0 = (int64_t)wave * R; row0 < a.N; row0 += stride, cur ^= 1) {
     const int nrows = (int)(a.N - row0 < R ? a.N - row0 : R);
     uint8_t *lds = lds2 + cur * a.lds_wave;
-    // Next row group into the other slice, then wait for this one (its ni loads are
-    // followed only by the next group's ni).
-    staged_issue(a, lds2 + (cur ^ 1) * a.lds_wave, row0 + stride, lane);
-    wait_vm_rt(ni);
+    // Next row group into the other slice, then wait for this one (its loads are followed
+    // only by the next group's, if any).
+    wait_vm_rt(staged_issue(a, lds2 + (cur ^ 1) * a.lds_wave, row0 + stride, lane));
 #pragma unroll
     for (int r = 0; r < R; r++) {
       if (r >= nrows) break;
@@ -554,7 +609,7 @@ __global__ __launch_bounds__(256) void gemv_q80_kernel(StagedArgs a) {
 
 // Q6_K lane unit = (block b, l8): half h = l8 >> 2, l0 = (l8 & 3) * 8; the unit covers
 // elements h*128 + g*32 + l0 + [0, 8) for g = 0..3 (quant/q6_k.go:18-27).
-template <int CPL, int R, int MM>
+template <int CPL, int R, int MM, bool XIN>
 __global__ __launch_bounds__(256) void gemv_q6k_kernel(StagedArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   const int lane = threadIdx.x & 63;
@@ -562,6 +617,15 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(StagedArgs a) {
   const int nwaves = gridDim.x * 4;
   const int m0 = blockIdx.y * MM;
   const int units = a.nb * 8;
+
+  // The first row group's weight bytes are requested before anything waits on x.
+  uint8_t *lds2 = smem + (threadIdx.x >> 6) * 2 * a.lds_wave;
+  staged_issue(a, lds2, (int64_t)wave * R, lane);
+  ActView av;
+  if constexpr (XIN)
+    av = staged_quantize_x<MM>(a, smem + 8 * a.lds_wave, m0);
+  else
+    av = ActView{a.act, a.q2_off, a.d_off, a.s_off};
 
   int xv[MM][CPL][8], yv[MM][CPL][8];
   float2 dx[MM][CPL][4];
@@ -573,17 +637,17 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(StagedArgs a) {
     const int uu = ok ? un : 0, bl = uu >> 3, l8 = uu & 7, h = l8 >> 2, l0 = (l8 & 3) * 8;
 #pragma unroll
     for (int mm = 0; mm < MM; mm++) {
-      const int m = m0 + mm < a.M ? m0 + mm : a.M - 1;
+      const int m = XIN ? mm : (m0 + mm < a.M ? m0 + mm : a.M - 1);
 #pragma unroll
       for (int g = 0; g < 4; g++) {
         const int64_t blk = (int64_t)m * (a.K / 32) + bl * 8 + h * 4 + g;
-        const uint2 v = *reinterpret_cast<const uint2 *>(a.act + blk * 32 + l0);
-        const uint2 v2 = *reinterpret_cast<const uint2 *>(a.act + a.q2_off + blk * 32 + l0);
+        const uint2 v = *reinterpret_cast<const uint2 *>(av.p + blk * 32 + l0);
+        const uint2 v2 = *reinterpret_cast<const uint2 *>(av.p + av.q2 + blk * 32 + l0);
         xv[mm][i][2 * g] = ok ? (int)v.x : 0;
         xv[mm][i][2 * g + 1] = ok ? (int)v.y : 0;
         yv[mm][i][2 * g] = ok ? (int)v2.x : 0;
         yv[mm][i][2 * g + 1] = ok ? (int)v2.y : 0;
-        dx[mm][i][g] = ok ? reinterpret_cast<const float2 *>(a.act + a.d_off)[blk] : make_float2(0.f, 0.f);
+        dx[mm][i][g] = ok ? reinterpret_cast<const float2 *>(av.p + av.d)[blk] : make_float2(0.f, 0.f);
         s32[mm][i][g] = 32 * byte_sum(&xv[mm][i][2 * g], 2);
         t32[mm][i][g] = 32 * byte_sum(&yv[mm][i][2 * g], 2);
       }
@@ -591,18 +655,14 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(StagedArgs a) {
   }
 
   // Two LDS slices per wave, filled by direct loads one row group ahead.
-  uint8_t *lds2 = smem + (threadIdx.x >> 6) * 2 * a.lds_wave;
-  const int ni = a.lds_wave >> 10;
   const int64_t stride = (int64_t)nwaves * R;
-  staged_issue(a, lds2, (int64_t)wave * R, lane);
   int cur = 0;
   for (int64_t row0 = (int64_t)wave * R; row0 < a.N; row0 += stride, cur ^= 1) {
     const int nrows = (int)(a.N - row0 < R ? a.N - row0 : R);
     uint8_t *lds = lds2 + cur * a.lds_wave;
-    // Next row group into the other slice, then wait for this one (its ni loads are
-    // followed only by the next group's ni).
-    staged_issue(a, lds2 + (cur ^ 1) * a.lds_wave, row0 + stride, lane);
-    wait_vm_rt(ni);
+    // Next row group into the other slice, then wait for this one (its loads are followed
+    // only by the next group's, if any).
+    wait_vm_rt(staged_issue(a, lds2 + (cur ^ 1) * a.lds_wave, row0 + stride, lane));
 #pragma unroll
     for (int r = 0; r < R; r++) {
       if (r >= nrows) break;
@@ -691,6 +751,10 @@ __global__ __launch_bounds__(256) void gemv_generic_kernel(const float *__restri
 
 static const int kCplSteps[] = {1, 2, 3, 4, 6, 8};
 
+// The staged kernels quantize F32 x themselves up to this K (each workgroup re-reads x from
+// L2; beyond it one quantize launch is cheaper).
+static constexpr int64_t kStagedXinMaxK = 8192;
+
 static int pick_cpl(int64_t units) {
   int64_t need = cdiv(units, 64);
   for (int c : kCplSteps)
@@ -730,64 +794,115 @@ static void dispatch_q4k(Q4kArgs a, hipStream_t s) {
     run_q4k<2, MM, false>(a, rw, cus * 2, s);
 }
 
-template <int CPL, int R, int MM>
+template <typename K>
+static void allow_big_lds(K *kern) {
+  (void)hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            160 * 1024);
+}
+
+template <int CPL, int R, int MM, bool XIN>
 static void run_staged(int dt, StagedArgs a, hipStream_t s) {
-  // Two slices per wave of R rows (+16 bytes read past the last block), whole KB each.
+  // Two slices per wave of R rows (+16 bytes read past the last block), whole KB each;
+  // XIN adds the workgroup's quantized x rows.
   a.lds_wave = (int)((R * a.row_bytes + 16 + 1023) & ~(int64_t)1023);
-  const int lds = 8 * a.lds_wave;
+  const int lds = 8 * a.lds_wave + (XIN ? (int)staged_xin_lds(MM, a.K) : 0);
   static bool attr_done = false;
   if (!attr_done) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_q80_kernel<Q8_0, CPL, R, MM>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_q80_kernel<Q4_0, CPL, R, MM>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_q80_kernel<Q5_0, CPL, R, MM>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_q6k_kernel<CPL, R, MM>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    allow_big_lds(&gemv_q80_kernel<Q8_0, CPL, R, MM, XIN>);
+    allow_big_lds(&gemv_q80_kernel<Q4_0, CPL, R, MM, XIN>);
+    allow_big_lds(&gemv_q80_kernel<Q5_0, CPL, R, MM, XIN>);
+    allow_big_lds(&gemv_q6k_kernel<CPL, R, MM, XIN>);
     attr_done = true;
   }
   const int per_cu = (160 * 1024) / lds;
-  int64_t wgs = cdiv(cdiv(a.N, R), 4), cap = (int64_t)device_cus() * (per_cu < 2 ? per_cu : 2);
+  // At least two row groups per wave where N allows (the workgroup's x quantization and the
+  // activation set-up are paid once per workgroup); at most two workgroups per CU.
+  int64_t wgs = cdiv(cdiv(a.N, R), 4 * 2), cap = (int64_t)device_cus() * (per_cu < 2 ? per_cu : 2);
   dim3 g((unsigned)(wgs < cap ? wgs : cap), (unsigned)cdiv(a.M, MM));
   switch (dt) {
-    case Q8_0: gemv_q80_kernel<Q8_0, CPL, R, MM><<<g, 256, lds, s>>>(a); break;
-    case Q4_0: gemv_q80_kernel<Q4_0, CPL, R, MM><<<g, 256, lds, s>>>(a); break;
-    case Q5_0: gemv_q80_kernel<Q5_0, CPL, R, MM><<<g, 256, lds, s>>>(a); break;
-    default: gemv_q6k_kernel<CPL, R, MM><<<g, 256, lds, s>>>(a); break;
+    case Q8_0: gemv_q80_kernel<Q8_0, CPL, R, MM, XIN><<<g, 256, lds, s>>>(a); break;
+    case Q4_0: gemv_q80_kernel<Q4_0, CPL, R, MM, XIN><<<g, 256, lds, s>>>(a); break;
+    case Q5_0: gemv_q80_kernel<Q5_0, CPL, R, MM, XIN><<<g, 256, lds, s>>>(a); break;
+    default: gemv_q6k_kernel<CPL, R, MM, XIN><<<g, 256, lds, s>>>(a); break;
   }
 }
 
-template <int CPL, int MM>
+template <int CPL, int MM, bool XIN>
 static void run_staged_r(int dt, StagedArgs a, hipStream_t s) {
   if (4 * a.row_bytes + 16 <= 8192)
-    run_staged<CPL, 4, MM>(dt, a, s);
+    run_staged<CPL, 4, MM, XIN>(dt, a, s);
   else if (2 * a.row_bytes + 16 <= 8192)
-    run_staged<CPL, 2, MM>(dt, a, s);
+    run_staged<CPL, 2, MM, XIN>(dt, a, s);
   else
-    run_staged<CPL, 1, MM>(dt, a, s);
+    run_staged<CPL, 1, MM, XIN>(dt, a, s);
 }
 
 // Q6_K holds 16 activation registers per unit and row of x: wide rows (CPL >= 6)
 // serve one row of x per pass.
-template <int CPL, int MM>
+template <int CPL, int MM, bool XIN>
 static void run_staged_c(int dt, StagedArgs a, hipStream_t s) {
   if constexpr (CPL >= 6 && MM > 1) {
-    if (dt == Q6_K) return run_staged_r<CPL, 1>(dt, a, s);
+    if (dt == Q6_K) return run_staged_r<CPL, 1, XIN>(dt, a, s);
   }
-  run_staged_r<CPL, MM>(dt, a, s);
+  run_staged_r<CPL, MM, XIN>(dt, a, s);
 }
 
-template <int MM>
+// XIN serves K <= kStagedXinMaxK only, so CPL <= 4 there.
+template <int MM, bool XIN>
 static void run_staged_m(int dt, StagedArgs a, int cpl, hipStream_t s) {
   switch (cpl) {
-    case 1: run_staged_c<1, MM>(dt, a, s); break;
-    case 2: run_staged_c<2, MM>(dt, a, s); break;
-    case 3: run_staged_c<3, MM>(dt, a, s); break;
-    case 4: run_staged_c<4, MM>(dt, a, s); break;
-    case 6: run_staged_c<6, MM>(dt, a, s); break;
-    default: run_staged_c<8, MM>(dt, a, s); break;
+    case 1: run_staged_c<1, MM, XIN>(dt, a, s); break;
+    case 2: run_staged_c<2, MM, XIN>(dt, a, s); break;
+    case 3: run_staged_c<3, MM, XIN>(dt, a, s); break;
+    case 4: run_staged_c<4, MM, XIN>(dt, a, s); break;
+    default:
+      if constexpr (!XIN) {
+        if (cpl == 6)
+          run_staged_c<6, MM, XIN>(dt, a, s);
+        else
+          run_staged_c<8, MM, XIN>(dt, a, s);
+      }
   }
+}
+
+// The staged formats (Q8_0, Q4_0, Q5_0, Q6_K) on prepared activations (act != NULL) or on
+// F32 x quantized inside the kernel (x != NULL, K <= kStagedXinMaxK).
+static int launch_staged(const void *act, const float *x, const uint8_t *w, float *out, int64_t M, int64_t N,
+                         int64_t K, int dt, hipStream_t s) {
+  StagedArgs a;
+  a.act = static_cast<const uint8_t *>(act);
+  a.x = x;
+  a.w = w;
+  a.out = out;
+  a.M = (int)M;
+  a.N = (int)N;
+  a.K = (int)K;
+  a.nb = (int)(K / block_info(dt).elems);
+  a.row_bytes = staged_row_bytes(dt, K);
+  a.q2_off = act_q2_off(M, K);
+  a.d_off = act_d_off(M, K);
+  a.s_off = act_s_off(M, K);
+  a.lds_wave = 0;
+  const int MMc = M >= 3 ? 4 : (int)M;
+  int cpl = pick_cpl(dt == Q6_K ? (int64_t)a.nb * 8 : a.nb);
+  // Q6_K keeps 16 registers of activations per unit and row of x: cap MM at 2.
+  int mm = dt == Q6_K && MMc > 2 ? 2 : MMc;
+  if (x) {
+    if (mm == 1)
+      run_staged_m<1, true>(dt, a, cpl, s);
+    else if (mm == 2)
+      run_staged_m<2, true>(dt, a, cpl, s);
+    else
+      run_staged_m<4, true>(dt, a, cpl, s);
+  } else {
+    if (mm == 1)
+      run_staged_m<1, false>(dt, a, cpl, s);
+    else if (mm == 2)
+      run_staged_m<2, false>(dt, a, cpl, s);
+    else
+      run_staged_m<4, false>(dt, a, cpl, s);
+  }
+  return check_launch(dt == Q6_K ? "gemv_q6k" : "gemv_q80");
 }
 
 int launch_gemv_act(const void *act, const void *wv, float *out, int64_t M, int64_t N, int64_t K, int dt,
@@ -824,29 +939,7 @@ int launch_gemv_act(const void *act, const void *wv, float *out, int64_t M, int6
   if (dt == Q5_K && q4kx_ok(1, N, K, w, nullptr, act, Q5_K))
     return launch_gemv_q4kx_act(act, w, out, M, N, K, Q5_K, s);
   if (dt != Q8_0 && dt != Q4_0 && dt != Q5_0 && dt != Q6_K) return fail(HQ_EUNSUPPORTED, "gemv", "dtype %d", dt);
-  StagedArgs a;
-  a.act = xa;
-  a.w = w;
-  a.out = out;
-  a.M = (int)M;
-  a.N = (int)N;
-  a.K = (int)K;
-  a.nb = (int)(K / block_info(dt).elems);
-  a.row_bytes = staged_row_bytes(dt, K);
-  a.q2_off = act_q2_off(M, K);
-  a.d_off = act_d_off(M, K);
-  a.s_off = act_s_off(M, K);
-  a.lds_wave = 0;
-  int cpl = pick_cpl(dt == Q6_K ? (int64_t)a.nb * 8 : a.nb);
-  // Q6_K keeps 16 registers of activations per unit and row of x: cap MM at 2.
-  int mm = dt == Q6_K && MMc > 2 ? 2 : MMc;
-  if (mm == 1)
-    run_staged_m<1>(dt, a, cpl, s);
-  else if (mm == 2)
-    run_staged_m<2>(dt, a, cpl, s);
-  else
-    run_staged_m<4>(dt, a, cpl, s);
-  return check_launch(dt == Q6_K ? "gemv_q6k" : "gemv_q80");
+  return launch_staged(act, nullptr, w, out, M, N, K, dt, s);
 }
 
 static int launch_gemv_generic(const float *x, const void *wv, float *out, int64_t M, int64_t N, int64_t K, int dt,
@@ -920,6 +1013,8 @@ int launch_matmul_q(const float *x, const void *w, float *out, int64_t M, int64_
     return launch_gemv_q4kx(x, w, nullptr, out, M, N, K, 0, dt, s);
   if (!gemv_fast_ok(dt, K, w) || (dt == Q5_K && !q4kx_ok(1, N, K, w, nullptr, x, dt)))
     return launch_gemv_generic(x, w, out, M, N, K, dt, s);
+  if (dt != Q4_K && dt != Q5_K && K <= kStagedXinMaxK && ((uintptr_t)x & 15) == 0)
+    return launch_staged(nullptr, x, static_cast<const uint8_t *>(w), out, M, N, K, dt, s);
   if (int rc = launch_quantize_act(x, F32, ws, M, K, s)) return rc;
   return launch_gemv_act(ws, w, out, M, N, K, dt, s);
 }

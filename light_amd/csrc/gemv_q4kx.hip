@@ -75,6 +75,21 @@ __device__ __forceinline__ float rl(float v, int lane) {
 //      hbuf [2][MM][32]                                                  (AOUT only)
 __host__ __device__ constexpr int64_t q4kx_act_lds(int MM, int64_t K) { return MM * (2 * K + 12 * (K / 32)); }
 
+// Weight loads are buffer loads over a resource that spans exactly the matrix (N rows).  A
+// row group past the end loads "row N": every offset lies outside the resource, so the
+// load returns zeros without a memory request.  The loads stay unconditional (no branch,
+// exact compiler wait counts) and idle teams cost no bandwidth -- clamping them to a valid
+// row instead would aim every workgroup's final prefetch at the same bytes, one L2 channel.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t span_rsrc(const void *p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ u32x4_t bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
+__device__ __forceinline__ float bload_f32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+
 // ---- weight-unit policies --------------------------------------------------------
 // Activations of one unit (two 32-blocks of one row of x), as each policy wants them.
 
@@ -116,18 +131,18 @@ struct QkUnit {
     L.sh = 2 * p;
     return L;
   }
-  // Byte offsets are 32-bit (the host checks N * row_bytes < 2^32), so the loads take the
-  // scalar-base + vector-offset form.
+  // Byte offsets are 32-bit: the host checks (N + 1) * row_bytes < 2^32, row N included.
   __device__ static void load(const uint8_t *w, const float *, const float *, const Q4kxArgs &a, int row,
                               const Lane &L, W &r) {
+    const __amdgpu_buffer_rsrc_t rs = span_rsrc(w, (uint32_t)a.N * (uint32_t)a.row_bytes);
     const uint32_t ro = (uint32_t)row * (uint32_t)a.row_bytes;
-    r.q0 = *reinterpret_cast<const u32x4_t *>(w + (ro + L.qoff));
-    r.q1 = *reinterpret_cast<const u32x4_t *>(w + (ro + L.qoff + 16));
+    r.q0 = bload16(rs, ro + L.qoff);
+    r.q1 = bload16(rs, ro + L.qoff + 16);
     if constexpr (Q5) {
-      r.h0 = *reinterpret_cast<const u32x4_t *>(w + (ro + L.qhoff));
-      r.h1 = *reinterpret_cast<const u32x4_t *>(w + (ro + L.qhoff + 16));
+      r.h0 = bload16(rs, ro + L.qhoff);
+      r.h1 = bload16(rs, ro + L.qhoff + 16);
     }
-    r.hd = *reinterpret_cast<const u32x4_t *>(w + (ro + L.hoff));
+    r.hd = bload16(rs, ro + L.hoff);
   }
   __device__ static void load_x(const uint8_t *q1, const uint8_t *q2, const uint8_t *de, const uint8_t *sx,
                                 int64_t blk, X &x) {
@@ -224,14 +239,17 @@ struct Int4Unit {
   }
   __device__ static void load(const uint8_t *w, const float *s, const float *z, const Q4kxArgs &a, int row,
                               const Lane &L, W &r) {
+    const __amdgpu_buffer_rsrc_t rs = span_rsrc(w, (uint32_t)a.N * (uint32_t)a.row_bytes);
+    const uint32_t gbytes = (uint32_t)a.N * (uint32_t)(a.K / a.G) * 4u;
+    const __amdgpu_buffer_rsrc_t rsc = span_rsrc(s, gbytes), rz = span_rsrc(z, gbytes);
     const uint32_t ro = (uint32_t)row * (uint32_t)a.row_bytes;
-    r.q0 = *reinterpret_cast<const u32x4_t *>(w + (ro + L.coff));
-    r.q1 = *reinterpret_cast<const u32x4_t *>(w + (ro + L.coff + 16));
-    const int64_t gr = (int64_t)row * (a.K / a.G);
-    r.sA = s[gr + L.gA];
-    r.zA = z[gr + L.gA];
-    r.sB = s[gr + L.gB];
-    r.zB = z[gr + L.gB];
+    r.q0 = bload16(rs, ro + L.coff);
+    r.q1 = bload16(rs, ro + L.coff + 16);
+    const uint32_t go = (uint32_t)row * (uint32_t)(a.K / a.G) * 4u;
+    r.sA = bload_f32(rsc, go + 4u * L.gA);
+    r.zA = bload_f32(rz, go + 4u * L.gA);
+    r.sB = bload_f32(rsc, go + 4u * L.gB);
+    r.zB = bload_f32(rz, go + 4u * L.gB);
   }
   __device__ static void load_x(const uint8_t *q1, const uint8_t *q2, const uint8_t *de, const uint8_t *sx,
                                 int64_t blk, X &x) {
@@ -328,7 +346,7 @@ __global__ __launch_bounds__(512) void gemv_q4kx_kernel(Q4kxArgs a) {
   const int m0 = blockIdx.y * MM;
   const int G = gridDim.x;
   // Iteration i of this workgroup -> row group: whole chunks of CG groups (32 rows with
-  // AOUT), chunks strided over the grid.  Groups past the end clamp to row N - 1.
+  // AOUT), chunks strided over the grid.  Groups past the end load row N (zeros, no traffic).
   const int CG = AOUT ? 32 / RW : 1;
   const int nchunks = (ngroups + CG - 1) / CG;
   const int niter = ((nchunks - (int)blockIdx.x + G - 1) / G) * CG;
@@ -336,7 +354,7 @@ __global__ __launch_bounds__(512) void gemv_q4kx_kernel(Q4kxArgs a) {
 #define Q4KX_LOAD(SLOT, GRP)                                                  \
   do {                                                                        \
     int row_ = (GRP) * RW + team;                                             \
-    row_ = row_ < a.N ? row_ : a.N - 1;                                       \
+    row_ = row_ < a.N ? row_ : a.N;                                           \
     U::load(a.w0, a.s0, a.z0, a, row_, L, wr[SLOT][0]);                        \
     if (GATED) U::load(a.w1, a.s1, a.z1, a, row_, L, wr[SLOT][NW - 1]);        \
   } while (0)
@@ -620,7 +638,7 @@ __global__ __launch_bounds__(512) void moe_gemv_x_kernel(MoeXArgs ma) {
     typename U::W wr[NW];
     {
       int row = (int)blockIdx.x * RW + team;
-      row = row < a.N ? row : a.N - 1;
+      row = row < a.N ? row : a.N;
       U::load(w, a.s0, a.z0, a, row, L, wr[0]);
       if (GATED) U::load(w + ma.up_off, a.s0, a.z0, a, row, L, wr[NW - 1]);
     }
@@ -673,7 +691,7 @@ __global__ __launch_bounds__(512) void moe_gemv_x_kernel(MoeXArgs ma) {
       for (int j = 0; j < NW; j++) U::template dot<MM>(wr[j], xr, L, c[j]);
       {
         int row = (grp + G) * RW + team;
-        row = row < a.N ? row : a.N - 1;
+        row = row < a.N ? row : a.N;
         U::load(w, a.s0, a.z0, a, row, L, wr[0]);
         if (GATED) U::load(w + ma.up_off, a.s0, a.z0, a, row, L, wr[NW - 1]);
       }
@@ -736,7 +754,7 @@ static size_t q4kx_lds(int MM, int64_t K, int TP, int RW, bool gated, bool xin, 
 bool q4kx_ok(int64_t M, int64_t N, int64_t K, const void *w0, const void *w1, const void *x, int dt) {
   int P, TP, RW;
   if ((dt != Q4_K && dt != Q5_K) || M < 1 || M > kGemvMaxRows || !q4kx_geom(K, 256, &P, &TP, &RW)) return false;
-  if (N > INT32_MAX / 2 || N * (K / 256 * block_info(dt).bytes) > UINT32_MAX) return false;
+  if (N > INT32_MAX / 2 || (N + 1) * (K / 256 * block_info(dt).bytes) > UINT32_MAX) return false;
   if (((uintptr_t)w0 & 15) || (w1 && ((uintptr_t)w1 & 15)) || ((uintptr_t)x & 15)) return false;
   return q4kx_lds(mm_of(M), K, TP, RW, w1 != nullptr, true, true) <= 160 * 1024;
 }
@@ -774,7 +792,7 @@ static int dispatch_q4kx(const Q4kxArgs &a, hipStream_t s) {
 
 static int q4kx_setup(Q4kxArgs &a, int64_t M, int64_t N, int64_t K, int kblock, int64_t row_bytes,
                       const char *call) {
-  if (!q4kx_geom(K, kblock, &a.P, &a.TP, &a.RW) || N > INT32_MAX / 2 || M > 65535 || N * row_bytes > UINT32_MAX)
+  if (!q4kx_geom(K, kblock, &a.P, &a.TP, &a.RW) || N > INT32_MAX / 2 || M > 65535 || (N + 1) * row_bytes > UINT32_MAX)
     return fail(HQ_EUNSUPPORTED, call, "K=%lld N=%lld", (long long)K, (long long)N);
   a.x = nullptr;
   a.ain = nullptr;
@@ -826,7 +844,7 @@ int launch_gemv_q4kx_act(const void *act_in, const void *w, float *out, int64_t 
 bool int4x_ok(int64_t M, int64_t N, int64_t K, int G, const void *codes, const void *x) {
   int P, TP, RW;
   if (M < 1 || M > kGemvMaxRows || G <= 0 || G % 32 || K % G || !q4kx_geom(K, 64, &P, &TP, &RW)) return false;
-  if (N > INT32_MAX / 2 || N * (K / 2) > UINT32_MAX) return false;
+  if (N > INT32_MAX / 2 || (N + 1) * (K / 2) > UINT32_MAX) return false;
   if (((uintptr_t)codes & 15) || ((uintptr_t)x & 15)) return false;
   return q4kx_lds(mm_of(M), K, TP, RW, false, true, false) <= 160 * 1024;
 }

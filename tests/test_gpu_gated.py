@@ -112,3 +112,24 @@ def test_mlp_q4_k_shapes(dev, H, I):
 @pytest.mark.parametrize("dt,M", [(hipq.Q8_0, 1), (hipq.Q6_K, 2), (hipq.Q4_K, 12), (hipq.Q4_0, 1), (hipq.Q5_0, 3)])
 def test_mlp_unfused_paths(dev, dt, M):
     _check_mlp(dev, dt, M, 512, 768, hipq.ACT_SILU, seed=dt * 3 + M)
+
+
+def test_mlp_repeated_calls_agree(dev):
+    """Calls at different M (one and two grid rows) interleave on the same weights, and every
+    repeat of a call reproduces its first result bit for bit (the decode kernels keep no state
+    between calls and sum in a fixed order)."""
+    print("[case] mlp repeated calls", flush=True)
+    g = synth.rng(77)
+    H, I = 1024, 2816
+    t = lambda a: torch.from_numpy(a).to(dev)
+    wg, wu, wd = (t(synth.gguf_weight(hipq.Q4_K, r, c, g)) for r, c in ((I, H), (I, H), (H, I)))
+    xs = {M: t(synth.activations(M, H, g)) for M in (1, 8, 3)}
+    first = {}
+    for rep in range(3):
+        for M, x in xs.items():
+            y = hipq.mlp_q(x, wg, wu, wd, H, I, hipq.Q4_K, act=hipq.ACT_SILU)
+            torch.cuda.synchronize()
+            if rep == 0:
+                first[M] = y.clone()
+            else:
+                assert torch.equal(y, first[M]), (rep, M)

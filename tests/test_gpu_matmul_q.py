@@ -206,13 +206,10 @@ def test_matmul_q_act_equals_matmul_q(dev, dt, M):
     act = hipq.quantize_act(x)
     y2 = hipq.matmul_q_act(act, w, M, N, K, dt)
     torch.cuda.synchronize()
-    if dt not in (hipq.Q4_K, hipq.Q5_K):
-        assert torch.equal(y1, y2)
-    else:
-        # The Q4_K / Q5_K GEMV quantizes x inside its workgroups (reciprocal-based scales): the two
-        # paths agree to the activation quantization's own error, far inside the bar.
-        ref = torch.from_numpy(oracle.matmul_q(x.cpu().numpy(), w.cpu().numpy(), N, K, dt)).to(dev)
-        assert ((y1 - y2).abs().max() <= 1e-4 * ref.abs().max()).item()
+    # At K <= 8192 the decode GEMVs quantize x inside their workgroups (reciprocal-based
+    # scales): the two paths agree to the activation quantization's own error, far inside the bar.
+    ref = torch.from_numpy(oracle.matmul_q(x.cpu().numpy(), w.cpu().numpy(), N, K, dt)).to(dev)
+    assert ((y1 - y2).abs().max() <= 1e-4 * ref.abs().max()).item()
     _check_matmul(dev, dt, x.cpu().numpy(), w.cpu().numpy(), N, K, "act")
     _check_matmul(dev, dt, x.cpu().numpy(), w.cpu().numpy(), N, K, "act", got=y2.cpu().numpy())
 
