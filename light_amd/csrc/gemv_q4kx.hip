@@ -333,30 +333,35 @@ __device__ __forceinline__ void store_out(void *out, int64_t i, float y) {
     static_cast<uint16_t *>(out)[i] = f2h_rne(y);
 }
 
-template <class U, int MM, bool GATED, bool XIN, bool AOUT, int XDT, int ODT>
-__global__ __launch_bounds__(512) void gemv_q4kx_kernel(Q4kxArgs a) {
-  extern __shared__ __align__(16) uint8_t smem[];
-  constexpr int NW = GATED ? 2 : 1;
+// The kernel body for workgroup bx of G persistent workgroups (grid row blockIdx.y).  PAIR
+// (plain GEMV only): a team carries two rows per iteration, rows g*2RW + team and + RW, so
+// twice the bytes are in flight and the per-iteration reduction is paid once per two rows.
+template <class U, int MM, bool GATED, bool XIN, bool AOUT, int XDT, int ODT, bool PAIR = false>
+__device__ __forceinline__ void q4kx_body(const Q4kxArgs &a, uint8_t *smem, const int bx, const int G) {
+  static_assert(!(PAIR && (GATED || AOUT)), "PAIR is for the plain GEMV");
+  constexpr int NW = GATED || PAIR ? 2 : 1;
   const int t = threadIdx.x, lane = t & 63;
   const int RW = a.RW, KB = a.K >> 5;
   const int team = t / a.TP, u = t - team * a.TP;
   const bool active = u < a.P;
   const typename U::Lane L = unit_lane<U>(active ? u : 0, a.G);
-  const int ngroups = (a.N + RW - 1) / RW;
+  const int SPAN = PAIR ? 2 * RW : RW;  // rows per group
+  const int ngroups = (a.N + SPAN - 1) / SPAN;
   const int m0 = blockIdx.y * MM;
-  const int G = gridDim.x;
   // Iteration i of this workgroup -> row group: whole chunks of CG groups (32 rows with
   // AOUT), chunks strided over the grid.  Groups past the end load row N (zeros, no traffic).
   const int CG = AOUT ? 32 / RW : 1;
   const int nchunks = (ngroups + CG - 1) / CG;
-  const int niter = ((nchunks - (int)blockIdx.x + G - 1) / G) * CG;
-#define Q4KX_GRP(I) (((int)blockIdx.x + ((I) / CG) * G) * CG + (I) % CG)
+  const int niter = ((nchunks - bx + G - 1) / G) * CG;
+#define Q4KX_GRP(I) ((bx + ((I) / CG) * G) * CG + (I) % CG)
 #define Q4KX_LOAD(SLOT, GRP)                                                  \
   do {                                                                        \
-    int row_ = (GRP) * RW + team;                                             \
+    int row_ = (GRP) * SPAN + team, rowb_ = row_ + RW;                        \
     row_ = row_ < a.N ? row_ : a.N;                                           \
+    rowb_ = rowb_ < a.N ? rowb_ : a.N;                                        \
     U::load(a.w0, a.s0, a.z0, a, row_, L, wr[SLOT][0]);                        \
     if (GATED) U::load(a.w1, a.s1, a.z1, a, row_, L, wr[SLOT][NW - 1]);        \
+    if (PAIR) U::load(a.w0, a.s0, a.z0, a, rowb_, L, wr[SLOT][NW - 1]);        \
   } while (0)
 
   // One register slot: the next group's loads go out once the current one is reduced.
@@ -448,7 +453,7 @@ __global__ __launch_bounds__(512) void gemv_q4kx_kernel(Q4kxArgs a) {
     }
     // The slot is consumed: refill it with the next group (unconditionally).
     Q4KX_LOAD(0, Q4KX_GRP(it + 1));
-    const int row = grp * RW + team;
+    const int row = grp * SPAN + team;
     float *hb = hbuf + ((it / CG) & 1) * (MM * 32);
     if (wpt <= 1) {
       // Team within one wave (TP in {16, 32, 64}): add its 16-lane rows in order.
@@ -472,6 +477,8 @@ __global__ __launch_bounds__(512) void gemv_q4kx_kernel(Q4kxArgs a) {
           if (a.out && m0 + mm < a.M) store_out<ODT>(a.out, (int64_t)(m0 + mm) * a.N + row, y);
           if (AOUT) hb[mm * 32 + (row & 31)] = y;
         }
+        if (PAIR && u == 0 && row + RW < a.N && a.out && m0 + mm < a.M)
+          store_out<ODT>(a.out, (int64_t)(m0 + mm) * a.N + row + RW, tot[NW - 1]);
       }
     } else {
       // Team of wpt waves: 16-lane row sums through LDS, added in row order.
@@ -492,13 +499,15 @@ __global__ __launch_bounds__(512) void gemv_q4kx_kernel(Q4kxArgs a) {
           for (int k = 0; k < hpt; k++) acc += pp[((tm * NW + j) * MM + mm) * hpt + k];
           tot[j] = acc;
         }
-        const int r2 = grp * RW + tm;
+        const int r2 = grp * SPAN + tm;
         if (r2 < a.N) {
           float y = tot[0];
           if (GATED) y = gate_act(tot[0], a.act) * tot[NW - 1];
           if (a.out && m0 + mm < a.M) store_out<ODT>(a.out, (int64_t)(m0 + mm) * a.N + r2, y);
           if (AOUT) hb[mm * 32 + (r2 & 31)] = y;
         }
+        if (PAIR && r2 + RW < a.N && a.out && m0 + mm < a.M)
+          store_out<ODT>(a.out, (int64_t)(m0 + mm) * a.N + r2 + RW, tot[NW - 1]);
       }
     }
     if (AOUT && it % CG == CG - 1) {
@@ -524,6 +533,12 @@ __global__ __launch_bounds__(512) void gemv_q4kx_kernel(Q4kxArgs a) {
   }
 #undef Q4KX_LOAD
 #undef Q4KX_GRP
+}
+
+template <class U, int MM, bool GATED, bool XIN, bool AOUT, int XDT, int ODT, bool PAIR = false>
+__global__ __launch_bounds__(512) void gemv_q4kx_kernel(Q4kxArgs a) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  q4kx_body<U, MM, GATED, XIN, AOUT, XDT, ODT, PAIR>(a, smem, (int)blockIdx.x, (int)gridDim.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -759,10 +774,10 @@ bool q4kx_ok(int64_t M, int64_t N, int64_t K, const void *w0, const void *w1, co
   return q4kx_lds(mm_of(M), K, TP, RW, w1 != nullptr, true, true) <= 160 * 1024;
 }
 
-template <class U, int MM, bool GATED, bool XIN, bool AOUT, int XDT, int ODT>
+template <class U, int MM, bool GATED, bool XIN, bool AOUT, int XDT, int ODT, bool PAIR = false>
 static int run_q4kx(const Q4kxArgs &a, hipStream_t s) {
-  auto *kern = &gemv_q4kx_kernel<U, MM, GATED, XIN, AOUT, XDT, ODT>;
-  const size_t lds = q4kx_lds(MM, a.K, a.TP, a.RW, GATED, XIN, AOUT);
+  auto *kern = &gemv_q4kx_kernel<U, MM, GATED, XIN, AOUT, XDT, ODT, PAIR>;
+  const size_t lds = q4kx_lds(MM, a.K, a.TP, a.RW, GATED || PAIR, XIN, AOUT);
   if (lds > 64 * 1024) {
     static bool attr_done = false;
     if (!attr_done) {
@@ -772,7 +787,8 @@ static int run_q4kx(const Q4kxArgs &a, hipStream_t s) {
       attr_done = true;
     }
   }
-  const int ngroups = (a.N + a.RW - 1) / a.RW;
+  const int span = PAIR ? 2 * a.RW : a.RW;
+  const int ngroups = (a.N + span - 1) / span;
   const int units = AOUT ? (ngroups + 32 / a.RW - 1) / (32 / a.RW) : ngroups;
   // Two persistent workgroups per CU, one row group in flight per wave: measured faster
   // than deeper per-wave prefetch (more loads per wave) or more workgroups.
@@ -782,12 +798,12 @@ static int run_q4kx(const Q4kxArgs &a, hipStream_t s) {
   return check_launch(GATED ? "gemv_q4k_gated" : "gemv_q4kx");
 }
 
-template <class U, bool GATED, bool XIN, bool AOUT, int XDT = F32, int ODT = F32>
+template <class U, bool GATED, bool XIN, bool AOUT, int XDT = F32, int ODT = F32, bool PAIR = false>
 static int dispatch_q4kx(const Q4kxArgs &a, hipStream_t s) {
   const int MMc = mm_of(a.M);
-  if (MMc == 1) return run_q4kx<U, 1, GATED, XIN, AOUT, XDT, ODT>(a, s);
-  if (MMc == 2) return run_q4kx<U, 2, GATED, XIN, AOUT, XDT, ODT>(a, s);
-  return run_q4kx<U, 4, GATED, XIN, AOUT, XDT, ODT>(a, s);
+  if (MMc == 1) return run_q4kx<U, 1, GATED, XIN, AOUT, XDT, ODT, PAIR>(a, s);
+  if (MMc == 2) return run_q4kx<U, 2, GATED, XIN, AOUT, XDT, ODT, PAIR>(a, s);
+  return run_q4kx<U, 4, GATED, XIN, AOUT, XDT, ODT, PAIR>(a, s);
 }
 
 static int q4kx_setup(Q4kxArgs &a, int64_t M, int64_t N, int64_t K, int kblock, int64_t row_bytes,
@@ -836,6 +852,12 @@ int launch_gemv_q4kx_act(const void *act_in, const void *w, float *out, int64_t 
   a.ain = static_cast<const uint8_t *>(act_in);
   a.w0 = static_cast<const uint8_t *>(w);
   a.out = out;
+  // Long rows (teams of several waves): two rows per team and iteration (measured 10.8 ->
+  // 10.6 us at 4096 x 14336).
+  if (a.TP > 64) {
+    if (dt == Q5_K) return dispatch_q4kx<Q5kUnit, false, false, false, F32, F32, true>(a, s);
+    return dispatch_q4kx<Q4kUnit, false, false, false, F32, F32, true>(a, s);
+  }
   if (dt == Q5_K) return dispatch_q4kx<Q5kUnit, false, false, false>(a, s);
   return dispatch_q4kx<Q4kUnit, false, false, false>(a, s);
 }
@@ -862,6 +884,12 @@ int launch_gemv_int4x(const void *x, int x_dtype, const uint32_t *codes, const f
     // Long rows: one quantize launch beats every workgroup quantizing all of x.
     if (int rc = launch_quantize_act(x, x_dtype, ws, M, K, s)) return rc;
     a.ain = static_cast<const uint8_t *>(ws);
+    if (a.TP > 64) switch (x_dtype) {  // two rows per team (15.0 -> 13.8 us at 3584 x 18944)
+      case F32: return dispatch_q4kx<Int4Unit, false, false, false, F32, F32, true>(a, s);
+      case BF16: return dispatch_q4kx<Int4Unit, false, false, false, F32, BF16, true>(a, s);
+      case F16: return dispatch_q4kx<Int4Unit, false, false, false, F32, F16, true>(a, s);
+      default: return fail(HQ_EUNSUPPORTED, "int4_gemv", "x dtype %d", x_dtype);
+    }
     switch (x_dtype) {
       case F32: return dispatch_q4kx<Int4Unit, false, false, false, F32, F32>(a, s);
       case BF16: return dispatch_q4kx<Int4Unit, false, false, false, F32, BF16>(a, s);
