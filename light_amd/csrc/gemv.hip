@@ -414,7 +414,8 @@ struct StagedArgs {
   float *out;
   int M, N, K, nb;
   int64_t row_bytes, q2_off, d_off, s_off;
-  int lds_wave;  // bytes of LDS per wave
+  int lds_wave;  // bytes of one LDS slice (one row group)
+  int ns;        // slices per wave: row groups are loaded ns - 1 ahead
 };
 
 // NDW dwords starting at LDS byte offset o (o even), re-aligned: out[k] = bytes [o+4k, o+4k+4).
@@ -527,11 +528,12 @@ __global__ __launch_bounds__(256) void gemv_q80_kernel(StagedArgs a) {
   const int m0 = blockIdx.y * MM;
 
   // The first row group's weight bytes are requested before anything waits on x.
-  uint8_t *lds2 = smem + (threadIdx.x >> 6) * 2 * a.lds_wave;
-  staged_issue(a, lds2, (int64_t)wave * R, lane);
+  uint8_t *ring = smem + (threadIdx.x >> 6) * a.ns * a.lds_wave;
+  const int64_t stride = (int64_t)nwaves * R;
+  for (int k = 0; k < a.ns - 1; k++) staged_issue(a, ring + k * a.lds_wave, (int64_t)wave * R + k * stride, lane);
   ActView av;
   if constexpr (XIN)
-    av = staged_quantize_x<MM>(a, smem + 8 * a.lds_wave, m0);
+    av = staged_quantize_x<MM>(a, smem + 4 * a.ns * a.lds_wave, m0);
   else
     av = ActView{a.act, a.q2_off, a.d_off, a.s_off};
 
@@ -562,15 +564,20 @@ __global__ __launch_bounds__(256) void gemv_q80_kernel(StagedArgs a) {
     }
   }
 
-  // Two LDS slices per wave, filled by direct loads one row group ahead.
-  const int64_t stride = (int64_t)nwaves * R;
+  // A ring of ns LDS slices per wave, filled by direct loads ns - 1 row groups ahead.
+  const int ni = a.lds_wave >> 10;
   int cur = 0;
-  for (int64_t row0 = (int64_t)wave * R; row0 < a.N; row0 += stride, cur ^= 1) {
+  for (int64_t row0 = (int64_t)wave * R; row0 < a.N; row0 += stride, cur = cur + 1 == a.ns ? 0 : cur + 1) {
     const int nrows = (int)(a.N - row0 < R ? a.N - row0 : R);
-    uint8_t *lds = lds2 + cur * a.lds_wave;
-    // Next row group into the other slice, then wait for this one (its loads are followed
-    // only by the next group's, if any).
-    wait_vm_rt(staged_issue(a, lds2 + (cur ^ 1) * a.lds_wave, row0 + stride, lane));
+    uint8_t *lds = ring + cur * a.lds_wave;
+    // The group ns - 1 ahead into the slice computed last, then wait for this group: the
+    // loads issued after it are the later groups' (those before the end).  Row stores in
+    // between only make the wait stricter.
+    const int prev = cur == 0 ? a.ns - 1 : cur - 1;
+    staged_issue(a, ring + prev * a.lds_wave, row0 + (a.ns - 1) * stride, lane);
+    int newer = 0;
+    for (int k = 1; k < a.ns; k++) newer += row0 + k * stride < a.N ? ni : 0;
+    wait_vm_rt(newer);
 #pragma unroll
     for (int r = 0; r < R; r++) {
       if (r >= nrows) break;
@@ -619,16 +626,20 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(StagedArgs a) {
   const int units = a.nb * 8;
 
   // The first row group's weight bytes are requested before anything waits on x.
-  uint8_t *lds2 = smem + (threadIdx.x >> 6) * 2 * a.lds_wave;
-  staged_issue(a, lds2, (int64_t)wave * R, lane);
+  uint8_t *ring = smem + (threadIdx.x >> 6) * a.ns * a.lds_wave;
+  const int64_t stride = (int64_t)nwaves * R;
+  for (int k = 0; k < a.ns - 1; k++) staged_issue(a, ring + k * a.lds_wave, (int64_t)wave * R + k * stride, lane);
   ActView av;
   if constexpr (XIN)
-    av = staged_quantize_x<MM>(a, smem + 8 * a.lds_wave, m0);
+    av = staged_quantize_x<MM>(a, smem + 4 * a.ns * a.lds_wave, m0);
   else
     av = ActView{a.act, a.q2_off, a.d_off, a.s_off};
 
+  // Per (row of x, unit, 32-block g): the quants of both levels, -32 * their sums (the Q6_K
+  // offset, folded into the dot chains' start) and d / 254 (the second level's step e is
+  // d / 254 to within an ulp, so d q1 + e q2 = (d / 254) (254 q1 + q2)).
   int xv[MM][CPL][8], yv[MM][CPL][8];
-  float2 dx[MM][CPL][4];
+  float fs[MM][CPL][4];
   int s32[MM][CPL][4], t32[MM][CPL][4];
 #pragma unroll
   for (int i = 0; i < CPL; i++) {
@@ -647,22 +658,27 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(StagedArgs a) {
         xv[mm][i][2 * g + 1] = ok ? (int)v.y : 0;
         yv[mm][i][2 * g] = ok ? (int)v2.x : 0;
         yv[mm][i][2 * g + 1] = ok ? (int)v2.y : 0;
-        dx[mm][i][g] = ok ? reinterpret_cast<const float2 *>(av.p + av.d)[blk] : make_float2(0.f, 0.f);
-        s32[mm][i][g] = 32 * byte_sum(&xv[mm][i][2 * g], 2);
-        t32[mm][i][g] = 32 * byte_sum(&yv[mm][i][2 * g], 2);
+        fs[mm][i][g] = ok ? reinterpret_cast<const float2 *>(av.p + av.d)[blk].x * (1.0f / 254.0f) : 0.f;
+        s32[mm][i][g] = -32 * byte_sum(&xv[mm][i][2 * g], 2);
+        t32[mm][i][g] = -32 * byte_sum(&yv[mm][i][2 * g], 2);
       }
     }
   }
 
-  // Two LDS slices per wave, filled by direct loads one row group ahead.
-  const int64_t stride = (int64_t)nwaves * R;
+  // A ring of ns LDS slices per wave, filled by direct loads ns - 1 row groups ahead.
+  const int ni = a.lds_wave >> 10;
   int cur = 0;
-  for (int64_t row0 = (int64_t)wave * R; row0 < a.N; row0 += stride, cur ^= 1) {
+  for (int64_t row0 = (int64_t)wave * R; row0 < a.N; row0 += stride, cur = cur + 1 == a.ns ? 0 : cur + 1) {
     const int nrows = (int)(a.N - row0 < R ? a.N - row0 : R);
-    uint8_t *lds = lds2 + cur * a.lds_wave;
-    // Next row group into the other slice, then wait for this one (its loads are followed
-    // only by the next group's, if any).
-    wait_vm_rt(staged_issue(a, lds2 + (cur ^ 1) * a.lds_wave, row0 + stride, lane));
+    uint8_t *lds = ring + cur * a.lds_wave;
+    // The group ns - 1 ahead into the slice computed last, then wait for this group: the
+    // loads issued after it are the later groups' (those before the end).  Row stores in
+    // between only make the wait stricter.
+    const int prev = cur == 0 ? a.ns - 1 : cur - 1;
+    staged_issue(a, ring + prev * a.lds_wave, row0 + (a.ns - 1) * stride, lane);
+    int newer = 0;
+    for (int k = 1; k < a.ns; k++) newer += row0 + k * stride < a.N ? ni : 0;
+    wait_vm_rt(newer);
 #pragma unroll
     for (int r = 0; r < R; r++) {
       if (r >= nrows) break;
@@ -680,33 +696,34 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(StagedArgs a) {
         lds_unaligned<2>(lds, o + 128 + h * 32 + l0, H);
         lds_unaligned<2>(lds, o + 192 + h * 8, S);
         const float d = h2f(*reinterpret_cast<const uint16_t *>(lds + o + 208));
+        // Sub-block scales 2g + is (int8): bytes is, is + 2 of S[0] (g = 0, 1) and of S[1].
         const int is = l0 >> 4;
-        float scf[4];
+        int sc[4];
 #pragma unroll
-        for (int g = 0; g < 4; g++) {
-          const int sidx = 2 * g + is;
-          scf[g] = (float)(int8_t)((sidx < 4 ? S[0] >> (8 * sidx) : S[1] >> (8 * (sidx - 4))) & 0xff);
-        }
+        for (int g = 0; g < 4; g++) sc[g] = __builtin_amdgcn_sbfe((int)S[g >> 1], 8 * (2 * (g & 1) + is), 8);
+        // 6-bit quants q = low nibble | 2 high bits << 4, one byte each.
         uint32_t qv[4][2];
 #pragma unroll
         for (int k = 0; k < 2; k++) {
           const uint32_t hk = H[k];
-          qv[0][k] = (A[k] & 0x0F0F0F0Fu) | ((hk & 0x03030303u) << 4);
-          qv[1][k] = (B[k] & 0x0F0F0F0Fu) | (((hk >> 2) & 0x03030303u) << 4);
-          qv[2][k] = ((A[k] >> 4) & 0x0F0F0F0Fu) | (((hk >> 4) & 0x03030303u) << 4);
-          qv[3][k] = ((B[k] >> 4) & 0x0F0F0F0Fu) | (((hk >> 6) & 0x03030303u) << 4);
+          qv[0][k] = (A[k] & 0x0F0F0F0Fu) | ((hk << 4) & 0x30303030u);
+          qv[1][k] = (B[k] & 0x0F0F0F0Fu) | ((hk << 2) & 0x30303030u);
+          qv[2][k] = ((A[k] >> 4) & 0x0F0F0F0Fu) | (hk & 0x30303030u);
+          qv[3][k] = ((B[k] >> 4) & 0x0F0F0F0Fu) | ((hk >> 2) & 0x30303030u);
         }
 #pragma unroll
         for (int mm = 0; mm < MM; mm++) {
           float v = 0.f;
 #pragma unroll
           for (int g = 0; g < 4; g++) {
-            int dot = dot4((int)qv[g][0], xv[mm][i][2 * g], 0);
+            // sum (q - 32) x over the 8 elements, both levels: |dot| <= 8 * 32 * 127, so
+            // 254 dot + dot2 stays below 2^23 and sc * (254 dot + dot2) below 2^31.
+            int dot = dot4((int)qv[g][0], xv[mm][i][2 * g], s32[mm][i][g]);
             dot = dot4((int)qv[g][1], xv[mm][i][2 * g + 1], dot);
-            int dot2 = dot4((int)qv[g][0], yv[mm][i][2 * g], 0);
+            int dot2 = dot4((int)qv[g][0], yv[mm][i][2 * g], t32[mm][i][g]);
             dot2 = dot4((int)qv[g][1], yv[mm][i][2 * g + 1], dot2);
-            v += scf[g] * (dx[mm][i][g].x * (float)(dot - s32[mm][i][g]) +
-                           dx[mm][i][g].y * (float)(dot2 - t32[mm][i][g]));
+            const int c = __mul24(sc[g], __mul24(254, dot) + dot2);
+            v = __fmaf_rn((float)c, fs[mm][i][g], v);
           }
           acc[mm] += d * v;
         }
@@ -800,12 +817,15 @@ static void allow_big_lds(K *kern) {
                             160 * 1024);
 }
 
+// Bytes of one LDS slice: R rows (+16 bytes read past the last block), whole KB.
+static int staged_slice(int R, int64_t row_bytes) { return (int)((R * row_bytes + 16 + 1023) & ~(int64_t)1023); }
+
 template <int CPL, int R, int MM, bool XIN>
-static void run_staged(int dt, StagedArgs a, hipStream_t s) {
-  // Two slices per wave of R rows (+16 bytes read past the last block), whole KB each;
-  // XIN adds the workgroup's quantized x rows.
-  a.lds_wave = (int)((R * a.row_bytes + 16 + 1023) & ~(int64_t)1023);
-  const int lds = 8 * a.lds_wave + (XIN ? (int)staged_xin_lds(MM, a.K) : 0);
+static void run_staged(int dt, StagedArgs a, int ns, hipStream_t s) {
+  // ns slices per wave; XIN adds the workgroup's quantized x rows.
+  a.lds_wave = staged_slice(R, a.row_bytes);
+  a.ns = ns;
+  const int lds = 4 * ns * a.lds_wave + (XIN ? (int)staged_xin_lds(MM, a.K) : 0);
   static bool attr_done = false;
   if (!attr_done) {
     allow_big_lds(&gemv_q80_kernel<Q8_0, CPL, R, MM, XIN>);
@@ -829,12 +849,14 @@ static void run_staged(int dt, StagedArgs a, hipStream_t s) {
 
 template <int CPL, int MM, bool XIN>
 static void run_staged_r(int dt, StagedArgs a, hipStream_t s) {
+  // Two slices per wave of up to four rows each.  (Four one-row slices, three groups in
+  // flight per wave, measured slower on every shape: per-row overheads outweigh the depth.)
   if (4 * a.row_bytes + 16 <= 8192)
-    run_staged<CPL, 4, MM, XIN>(dt, a, s);
+    run_staged<CPL, 4, MM, XIN>(dt, a, 2, s);
   else if (2 * a.row_bytes + 16 <= 8192)
-    run_staged<CPL, 2, MM, XIN>(dt, a, s);
+    run_staged<CPL, 2, MM, XIN>(dt, a, 2, s);
   else
-    run_staged<CPL, 1, MM, XIN>(dt, a, s);
+    run_staged<CPL, 1, MM, XIN>(dt, a, 2, s);
 }
 
 // Q6_K holds 16 activation registers per unit and row of x: wide rows (CPL >= 6)
@@ -883,6 +905,7 @@ static int launch_staged(const void *act, const float *x, const uint8_t *w, floa
   a.d_off = act_d_off(M, K);
   a.s_off = act_s_off(M, K);
   a.lds_wave = 0;
+  a.ns = 2;
   const int MMc = M >= 3 ? 4 : (int)M;
   int cpl = pick_cpl(dt == Q6_K ? (int64_t)a.nb * 8 : a.nb);
   // Q6_K keeps 16 registers of activations per unit and row of x: cap MM at 2.
