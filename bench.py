@@ -249,20 +249,30 @@ def table(args, dev):
                 nbytes = codes.nbytes + s.nbytes + z.nbytes + 2 * M * K + 2 * M * N
                 flops = 2 * M * N * K
             else:
-                rows.extend(moe_rows(c, name, g, dev))
+                rows.extend(moe_rows(c, name, g, dev, cpu=not args.no_cpu))
                 continue
         except hipq.HipqError as e:
             rows.append(dict(config=name, error=str(e)))
             continue
         gbs = nbytes / (us * 1e-6) / 1e9
         tfl = flops / (us * 1e-6) / 1e12
-        rows.append(dict(config=name, us=round(us, 2), GBs=round(gbs, 1), TFLOPS=round(tfl, 2),
-                         hbm_frac=round(gbs / HBM_PEAK_GBS, 3)))
+        row = dict(config=name, us=round(us, 2), GBs=round(gbs, 1), TFLOPS=round(tfl, 2),
+                   hbm_frac=round(gbs / HBM_PEAK_GBS, 3))
+        if not args.no_cpu:
+            import oracle
+            if c["kind"] == "gguf":
+                t, th, smp = cpu_gguf_row(x.cpu().numpy(), w.raw, N, K, dt)
+            else:
+                xf = xt.cpu().float().numpy()
+                th = _cpu_threads()
+                t, smp = _cpu_median(lambda: oracle.int4_matmul(xf, codes, s, z, N, K, G, th), 1), "whole call"
+            row.update(cpu_us=round(t * 1e6, 1), cpu_threads=th, cpu_sample=smp, gpu_over_cpu=round(t * 1e6 / us, 1))
+        rows.append(row)
         torch.cuda.empty_cache()
     return rows
 
 
-def moe_rows(c, name, g, dev):
+def moe_rows(c, name, g, dev, cpu=False):
     """MoE gate/up (per token) and down (per pair, weighted) Q4_K grouped GEMMs of one layer.
     Routing rotates over 16 draws so consecutive calls touch different experts (the stacks,
     340 MB, then exceed the 256 MB Infinity Cache)."""
@@ -300,8 +310,16 @@ def moe_rows(c, name, g, dev):
         nbytes = used * eb + xb + ob
         flops = 2.0 * M * flops_n * flops_k
         gbs = nbytes / (us * 1e-6) / 1e9
-        out.append(dict(config=f"{name}_{leg}", us=round(us, 2), GBs=round(gbs, 1),
-                        TFLOPS=round(flops / (us * 1e-6) / 1e12, 2), hbm_frac=round(gbs / HBM_PEAK_GBS, 3)))
+        row = dict(config=f"{name}_{leg}", us=round(us, 2), GBs=round(gbs, 1),
+                   TFLOPS=round(flops / (us * 1e-6) / 1e12, 2), hbm_frac=round(gbs / HBM_PEAK_GBS, 3))
+        if cpu:
+            ids, se_np, sp_np, tw_np = routes[0][0], *(r.cpu().numpy() for r in routes[0][1:])
+            if leg == "gate_up":
+                t, th, smp = cpu_moe_leg(x.cpu().numpy(), wgu_np, dt, E, 2 * I, H, sp_np, se_np, topk)
+            else:
+                t, th, smp = cpu_moe_leg(h.cpu().numpy(), wdn_np, dt, E, H, I, sp_np, se_np, topk, tw_np)
+            row.update(cpu_us=round(t * 1e6, 1), cpu_threads=th, cpu_sample=smp, gpu_over_cpu=round(t * 1e6 / us, 1))
+        out.append(row)
     # The whole routed block on the device: router probs -> hq_moe_route -> gated gate/up
     # (SiLU * up) -> down (routing-weighted) -> combine.  Probs rotate over 16 draws.
     probs = []
@@ -326,6 +344,61 @@ def moe_rows(c, name, g, dev):
                     TFLOPS=round(2.0 * M * (2 * I * H + H * I) / (us * 1e-6) / 1e12, 2),
                     hbm_frac=round(gbs / HBM_PEAK_GBS, 3)))
     return out
+
+
+def _cpu_threads():
+    import oracle
+    threads = int(os.environ.get("OMP_NUM_THREADS", "16"))
+    return max(1, min(threads, oracle.hw_threads()))
+
+
+def _cpu_median(fn, reps=3):
+    """Median wall time (s) of `reps` calls after one warm-up."""
+    fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
+
+
+def cpu_gguf_row(x, raw, N, K, dt):
+    """Light's CPU MatMulQ (oracle restatement) on a bounded sample of one table config: all of
+    it when it is small; a slice of the weight rows, or of the activation rows for M > 8, scaled
+    back linearly otherwise (the sample says which)."""
+    import oracle
+    M = x.shape[0]
+    th = _cpu_threads()
+    bb = oracle.BLOCK[dt][1] * (K // oracle.BLOCK[dt][0])  # bytes per weight row
+    if M > 8:
+        ms = 32
+        t = _cpu_median(lambda: oracle.matmul_q(x[:ms], raw, N, K, dt, th), 1) * (M / ms)
+        return t, th, f"M={ms} of {M} rows x {M // ms}"
+    if N * K > (64 << 20):
+        ns = N // 8
+        t = _cpu_median(lambda: oracle.matmul_q(x, raw[:ns * bb], ns, K, dt, th)) * (N / ns)
+        return t, th, f"{ns} of {N} weight rows x 8"
+    return _cpu_median(lambda: oracle.matmul_q(x, raw, N, K, dt, th)), th, "whole call"
+
+
+def cpu_moe_leg(x, w_raw, dt, E, N, K, sp, se, topk, tw=None):
+    """Light's CPU MoEGemmQ: dequantize the whole (E, N, K) stack (single thread, as
+    quant.Dequantize), then moeGemmKernel over the pairs.  The dequant is timed on 16 experts and
+    scaled to E; the pair dots run in full on a 16-expert stack with expert ids folded mod 16
+    (the same number of dot products)."""
+    import numpy as np
+    import oracle
+    th = _cpu_threads()
+    es = min(16, E)
+    nb = w_raw.size // E
+    sub = np.ascontiguousarray(w_raw.reshape(E, nb)[:es]).ravel()
+    t_deq = _cpu_median(lambda: oracle.dequant(dt, sub, es * N * K), 1) * (E / es)
+    wf = oracle.dequant(dt, sub, es * N * K).reshape(es, N, K)
+    se_f = np.asarray(se) % es
+    order = np.argsort(se_f, kind="stable")
+    t_gemm = _cpu_median(lambda: oracle.moe_gemm_f32(x, wf, np.asarray(sp)[order], se_f[order], topk, tw, th), 1)
+    return t_deq + t_gemm, th, f"dequant {t_deq * 1e3:.1f} ms (16 of {E} experts x {E // es}) + dots {t_gemm * 1e3:.1f} ms"
 
 
 def cpu_baseline(inputs):
