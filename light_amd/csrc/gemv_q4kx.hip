@@ -363,6 +363,14 @@ __device__ __forceinline__ void q4kx_body(const Q4kxArgs &a, uint8_t *smem, cons
     if (GATED) U::load(a.w1, a.s1, a.z1, a, row_, L, wr[SLOT][NW - 1]);        \
     if (PAIR) U::load(a.w0, a.s0, a.z0, a, rowb_, L, wr[SLOT][NW - 1]);        \
   } while (0)
+  // Refill of weight j of the slot alone (j = 1: the up weight, or the pair's second row).
+#define Q4KX_LOAD_J(SLOT, GRP, J)                                             \
+  do {                                                                        \
+    int row_ = (GRP) * SPAN + team + ((J) && PAIR ? RW : 0);                  \
+    row_ = row_ < a.N ? row_ : a.N;                                           \
+    U::load((J) && GATED ? a.w1 : a.w0, (J) && GATED ? a.s1 : a.s0,          \
+            (J) && GATED ? a.z1 : a.z0, a, row_, L, wr[SLOT][J]);             \
+  } while (0)
 
   // One register slot: the next group's loads go out once the current one is reduced.
   // (Deeper rings -- two to four groups in flight per wave -- were measured slower: this
@@ -433,10 +441,9 @@ __device__ __forceinline__ void q4kx_body(const Q4kxArgs &a, uint8_t *smem, cons
     }
   }
 
-  const int wpt = a.TP >> 6;  // waves per team (0 when a team is narrower than a wave)
   const int hpt = a.TP >> 4;  // 16-lane rows per team
   float *part = reinterpret_cast<float *>(smem + lds_act);
-  float *hbuf = part + (wpt > 1 ? 2 * RW * NW * MM * hpt : 0);
+  float *hbuf = part + (a.TP > 64 ? 2 * RW * NW * MM * hpt : 0);
 
   // One iteration: wait for the slot (straight-line form), reduce the group's rows, refill
   // the slot with the group D iterations ahead, write the outputs.  VALID is
@@ -448,14 +455,15 @@ __device__ __forceinline__ void q4kx_body(const Q4kxArgs &a, uint8_t *smem, cons
     for (int j = 0; j < NW; j++) {
       float c[MM];
       U::template dot<MM>(wr[0][j], xr, L, c);
+      // Weight j is consumed: refill it with the next group's (unconditionally) before the
+      // next weight's arithmetic, so the load has that much longer to arrive.
+      Q4KX_LOAD_J(0, Q4KX_GRP(it + 1), j);
 #pragma unroll
       for (int mm = 0; mm < MM; mm++) res[j][mm] = rsum16(active ? c[mm] : 0.f);
     }
-    // The slot is consumed: refill it with the next group (unconditionally).
-    Q4KX_LOAD(0, Q4KX_GRP(it + 1));
     const int row = grp * SPAN + team;
     float *hb = hbuf + ((it / CG) & 1) * (MM * 32);
-    if (wpt <= 1) {
+    if (a.TP <= 64) {
       // Team within one wave (TP in {16, 32, 64}): add its 16-lane rows in order.
 #pragma unroll
       for (int mm = 0; mm < MM; mm++) {
@@ -481,7 +489,7 @@ __device__ __forceinline__ void q4kx_body(const Q4kxArgs &a, uint8_t *smem, cons
           store_out<ODT>(a.out, (int64_t)(m0 + mm) * a.N + row + RW, tot[NW - 1]);
       }
     } else {
-      // Team of wpt waves: 16-lane row sums through LDS, added in row order.
+      // Team wider than a wave: 16-lane row sums through LDS, added in row order.
       float *pp = part + (it & 1) * (RW * NW * MM * hpt);
 #pragma unroll
       for (int j = 0; j < NW; j++) {
@@ -532,6 +540,7 @@ __device__ __forceinline__ void q4kx_body(const Q4kxArgs &a, uint8_t *smem, cons
     }
   }
 #undef Q4KX_LOAD
+#undef Q4KX_LOAD_J
 #undef Q4KX_GRP
 }
 
@@ -737,7 +746,8 @@ __global__ __launch_bounds__(512) void moe_gemv_x_kernel(MoeXArgs ma) {
 // ---------------------------------------------------------------------------
 
 // Team geometry: P = K/64 lanes (units) per row; TP = 16, 32 or 64 when P fits a wave,
-// else a multiple of 64 (up to 512); RW = teams per 512-lane workgroup.  `kblock` is the
+// else P rounded up to whole 16-lane rows (up to 512; e.g. 224 at K = 14336, so no lane of
+// the team idles); RW = teams per workgroup of at most 512 lanes.  `kblock` is the
 // K granularity of the format (256 for Q4_K, 64 for int4).
 static bool q4kx_geom(int64_t K, int kblock, int *P, int *TP, int *RW) {
   if (K % kblock || K > 32768) return false;
@@ -746,8 +756,10 @@ static bool q4kx_geom(int64_t K, int kblock, int *P, int *TP, int *RW) {
     *TP = 16;
   else if (*P <= 32)
     *TP = 32;
+  else if (*P <= 64)
+    *TP = 64;
   else
-    *TP = (*P + 63) & ~63;
+    *TP = (*P + 15) & ~15;  // several waves: whole 16-lane rows (the LDS reduction's unit)
   *RW = *TP >= 512 ? 1 : 512 / *TP;
   return true;
 }
