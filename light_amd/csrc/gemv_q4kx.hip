@@ -333,19 +333,20 @@ __device__ __forceinline__ void store_out(void *out, int64_t i, float y) {
     static_cast<uint16_t *>(out)[i] = f2h_rne(y);
 }
 
-// The kernel body for workgroup bx of G persistent workgroups (grid row blockIdx.y).  PAIR
-// (plain GEMV only): a team carries two rows per iteration, rows g*2RW + team and + RW, so
-// twice the bytes are in flight and the per-iteration reduction is paid once per two rows.
-template <class U, int MM, bool GATED, bool XIN, bool AOUT, int XDT, int ODT, bool PAIR = false>
+// The kernel body for workgroup bx of G persistent workgroups (grid row blockIdx.y).  ROWS
+// (plain GEMV only): a team carries ROWS rows per iteration, rows g*ROWS*RW + team + j*RW, so
+// ROWS times the bytes are in flight and the per-iteration reduction is paid once per ROWS
+// rows.
+template <class U, int MM, bool GATED, bool XIN, bool AOUT, int XDT, int ODT, int ROWS = 1>
 __device__ __forceinline__ void q4kx_body(const Q4kxArgs &a, uint8_t *smem, const int bx, const int G) {
-  static_assert(!(PAIR && (GATED || AOUT)), "PAIR is for the plain GEMV");
-  constexpr int NW = GATED || PAIR ? 2 : 1;
+  static_assert(ROWS == 1 || !(GATED || AOUT), "ROWS > 1 is for the plain GEMV");
+  constexpr int NW = GATED ? 2 : ROWS;  // weight rows in a register slot
   const int t = threadIdx.x, lane = t & 63;
   const int RW = a.RW, KB = a.K >> 5;
   const int team = t / a.TP, u = t - team * a.TP;
   const bool active = u < a.P;
   const typename U::Lane L = unit_lane<U>(active ? u : 0, a.G);
-  const int SPAN = PAIR ? 2 * RW : RW;  // rows per group
+  const int SPAN = ROWS * RW;  // rows per group
   const int ngroups = (a.N + SPAN - 1) / SPAN;
   const int m0 = blockIdx.y * MM;
   // Iteration i of this workgroup -> row group: whole chunks of CG groups (32 rows with
@@ -354,22 +355,18 @@ __device__ __forceinline__ void q4kx_body(const Q4kxArgs &a, uint8_t *smem, cons
   const int nchunks = (ngroups + CG - 1) / CG;
   const int niter = ((nchunks - bx + G - 1) / G) * CG;
 #define Q4KX_GRP(I) ((bx + ((I) / CG) * G) * CG + (I) % CG)
-#define Q4KX_LOAD(SLOT, GRP)                                                  \
-  do {                                                                        \
-    int row_ = (GRP) * SPAN + team, rowb_ = row_ + RW;                        \
-    row_ = row_ < a.N ? row_ : a.N;                                           \
-    rowb_ = rowb_ < a.N ? rowb_ : a.N;                                        \
-    U::load(a.w0, a.s0, a.z0, a, row_, L, wr[SLOT][0]);                        \
-    if (GATED) U::load(a.w1, a.s1, a.z1, a, row_, L, wr[SLOT][NW - 1]);        \
-    if (PAIR) U::load(a.w0, a.s0, a.z0, a, rowb_, L, wr[SLOT][NW - 1]);        \
-  } while (0)
-  // Refill of weight j of the slot alone (j = 1: the up weight, or the pair's second row).
+  // Weight j of a slot: the up weight of the same row (GATED, j = 1), else row j * RW of
+  // the group.  Rows past the end load row N (zeros, no traffic).
 #define Q4KX_LOAD_J(SLOT, GRP, J)                                             \
   do {                                                                        \
-    int row_ = (GRP) * SPAN + team + ((J) && PAIR ? RW : 0);                  \
+    int row_ = (GRP) * SPAN + team + (GATED ? 0 : (J) * RW);                  \
     row_ = row_ < a.N ? row_ : a.N;                                           \
     U::load((J) && GATED ? a.w1 : a.w0, (J) && GATED ? a.s1 : a.s0,          \
             (J) && GATED ? a.z1 : a.z0, a, row_, L, wr[SLOT][J]);             \
+  } while (0)
+#define Q4KX_LOAD(SLOT, GRP)                                                  \
+  do {                                                                        \
+    _Pragma("unroll") for (int j_ = 0; j_ < NW; j_++) Q4KX_LOAD_J(SLOT, GRP, j_); \
   } while (0)
 
   // One register slot: the next group's loads go out once the current one is reduced.
@@ -485,8 +482,10 @@ __device__ __forceinline__ void q4kx_body(const Q4kxArgs &a, uint8_t *smem, cons
           if (a.out && m0 + mm < a.M) store_out<ODT>(a.out, (int64_t)(m0 + mm) * a.N + row, y);
           if (AOUT) hb[mm * 32 + (row & 31)] = y;
         }
-        if (PAIR && u == 0 && row + RW < a.N && a.out && m0 + mm < a.M)
-          store_out<ODT>(a.out, (int64_t)(m0 + mm) * a.N + row + RW, tot[NW - 1]);
+#pragma unroll
+        for (int j = 1; j < (GATED ? 1 : NW); j++)
+          if (u == 0 && row + j * RW < a.N && a.out && m0 + mm < a.M)
+            store_out<ODT>(a.out, (int64_t)(m0 + mm) * a.N + row + j * RW, tot[j]);
       }
     } else {
       // Team wider than a wave: 16-lane row sums through LDS, added in row order.
@@ -514,8 +513,10 @@ __device__ __forceinline__ void q4kx_body(const Q4kxArgs &a, uint8_t *smem, cons
           if (a.out && m0 + mm < a.M) store_out<ODT>(a.out, (int64_t)(m0 + mm) * a.N + r2, y);
           if (AOUT) hb[mm * 32 + (r2 & 31)] = y;
         }
-        if (PAIR && r2 + RW < a.N && a.out && m0 + mm < a.M)
-          store_out<ODT>(a.out, (int64_t)(m0 + mm) * a.N + r2 + RW, tot[NW - 1]);
+#pragma unroll
+        for (int j = 1; j < (GATED ? 1 : NW); j++)
+          if (r2 + j * RW < a.N && a.out && m0 + mm < a.M)
+            store_out<ODT>(a.out, (int64_t)(m0 + mm) * a.N + r2 + j * RW, tot[j]);
       }
     }
     if (AOUT && it % CG == CG - 1) {
@@ -544,10 +545,10 @@ __device__ __forceinline__ void q4kx_body(const Q4kxArgs &a, uint8_t *smem, cons
 #undef Q4KX_GRP
 }
 
-template <class U, int MM, bool GATED, bool XIN, bool AOUT, int XDT, int ODT, bool PAIR = false>
+template <class U, int MM, bool GATED, bool XIN, bool AOUT, int XDT, int ODT, int ROWS = 1>
 __global__ __launch_bounds__(512) void gemv_q4kx_kernel(Q4kxArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
-  q4kx_body<U, MM, GATED, XIN, AOUT, XDT, ODT, PAIR>(a, smem, (int)blockIdx.x, (int)gridDim.x);
+  q4kx_body<U, MM, GATED, XIN, AOUT, XDT, ODT, ROWS>(a, smem, (int)blockIdx.x, (int)gridDim.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -771,9 +772,9 @@ static int mm_of(int64_t M) { return M >= 3 ? 4 : (int)M; }
 // more than the separate quantize launch.
 bool q4kx_xin(int64_t K) { return K <= 8192; }
 
-static size_t q4kx_lds(int MM, int64_t K, int TP, int RW, bool gated, bool xin, bool aout) {
+static size_t q4kx_lds(int MM, int64_t K, int TP, int RW, int nw, bool xin, bool aout) {
   size_t b = xin ? (size_t)q4kx_act_lds(MM, K) : 0;
-  if (TP > 64) b += 2 * 4 * (size_t)(RW * (TP >> 4) * (gated ? 2 : 1) * MM);
+  if (TP > 64) b += 2 * 4 * (size_t)(RW * (TP >> 4) * nw * MM);
   if (aout) b += 2 * 4 * 32 * (size_t)MM;
   return b;
 }
@@ -783,13 +784,13 @@ bool q4kx_ok(int64_t M, int64_t N, int64_t K, const void *w0, const void *w1, co
   if ((dt != Q4_K && dt != Q5_K) || M < 1 || M > kGemvMaxRows || !q4kx_geom(K, 256, &P, &TP, &RW)) return false;
   if (N > INT32_MAX / 2 || (N + 1) * (K / 256 * block_info(dt).bytes) > UINT32_MAX) return false;
   if (((uintptr_t)w0 & 15) || (w1 && ((uintptr_t)w1 & 15)) || ((uintptr_t)x & 15)) return false;
-  return q4kx_lds(mm_of(M), K, TP, RW, w1 != nullptr, true, true) <= 160 * 1024;
+  return q4kx_lds(mm_of(M), K, TP, RW, w1 != nullptr ? 2 : 1, true, true) <= 160 * 1024;
 }
 
-template <class U, int MM, bool GATED, bool XIN, bool AOUT, int XDT, int ODT, bool PAIR = false>
+template <class U, int MM, bool GATED, bool XIN, bool AOUT, int XDT, int ODT, int ROWS = 1>
 static int run_q4kx(const Q4kxArgs &a, hipStream_t s) {
-  auto *kern = &gemv_q4kx_kernel<U, MM, GATED, XIN, AOUT, XDT, ODT, PAIR>;
-  const size_t lds = q4kx_lds(MM, a.K, a.TP, a.RW, GATED || PAIR, XIN, AOUT);
+  auto *kern = &gemv_q4kx_kernel<U, MM, GATED, XIN, AOUT, XDT, ODT, ROWS>;
+  const size_t lds = q4kx_lds(MM, a.K, a.TP, a.RW, GATED ? 2 : ROWS, XIN, AOUT);
   if (lds > 64 * 1024) {
     static bool attr_done = false;
     if (!attr_done) {
@@ -799,7 +800,7 @@ static int run_q4kx(const Q4kxArgs &a, hipStream_t s) {
       attr_done = true;
     }
   }
-  const int span = PAIR ? 2 * a.RW : a.RW;
+  const int span = ROWS * a.RW;
   const int ngroups = (a.N + span - 1) / span;
   const int units = AOUT ? (ngroups + 32 / a.RW - 1) / (32 / a.RW) : ngroups;
   // Two persistent workgroups per CU, one row group in flight per wave: measured faster
@@ -810,12 +811,12 @@ static int run_q4kx(const Q4kxArgs &a, hipStream_t s) {
   return check_launch(GATED ? "gemv_q4k_gated" : "gemv_q4kx");
 }
 
-template <class U, bool GATED, bool XIN, bool AOUT, int XDT = F32, int ODT = F32, bool PAIR = false>
+template <class U, bool GATED, bool XIN, bool AOUT, int XDT = F32, int ODT = F32, int ROWS = 1>
 static int dispatch_q4kx(const Q4kxArgs &a, hipStream_t s) {
   const int MMc = mm_of(a.M);
-  if (MMc == 1) return run_q4kx<U, 1, GATED, XIN, AOUT, XDT, ODT, PAIR>(a, s);
-  if (MMc == 2) return run_q4kx<U, 2, GATED, XIN, AOUT, XDT, ODT, PAIR>(a, s);
-  return run_q4kx<U, 4, GATED, XIN, AOUT, XDT, ODT, PAIR>(a, s);
+  if (MMc == 1) return run_q4kx<U, 1, GATED, XIN, AOUT, XDT, ODT, ROWS>(a, s);
+  if (MMc == 2) return run_q4kx<U, 2, GATED, XIN, AOUT, XDT, ODT, ROWS>(a, s);
+  return run_q4kx<U, 4, GATED, XIN, AOUT, XDT, ODT, ROWS>(a, s);
 }
 
 static int q4kx_setup(Q4kxArgs &a, int64_t M, int64_t N, int64_t K, int kblock, int64_t row_bytes,
@@ -865,10 +866,10 @@ int launch_gemv_q4kx_act(const void *act_in, const void *w, float *out, int64_t 
   a.w0 = static_cast<const uint8_t *>(w);
   a.out = out;
   // Long rows (teams of several waves): two rows per team and iteration (measured 10.8 ->
-  // 10.6 us at 4096 x 14336).
+  // 10.6 us at 4096 x 14336; four rows, 130 registers, measured 12.2 us).
   if (a.TP > 64) {
-    if (dt == Q5_K) return dispatch_q4kx<Q5kUnit, false, false, false, F32, F32, true>(a, s);
-    return dispatch_q4kx<Q4kUnit, false, false, false, F32, F32, true>(a, s);
+    if (dt == Q5_K) return dispatch_q4kx<Q5kUnit, false, false, false, F32, F32, 2>(a, s);
+    return dispatch_q4kx<Q4kUnit, false, false, false, F32, F32, 2>(a, s);
   }
   if (dt == Q5_K) return dispatch_q4kx<Q5kUnit, false, false, false>(a, s);
   return dispatch_q4kx<Q4kUnit, false, false, false>(a, s);
@@ -880,7 +881,7 @@ bool int4x_ok(int64_t M, int64_t N, int64_t K, int G, const void *codes, const v
   if (M < 1 || M > kGemvMaxRows || G <= 0 || G % 32 || K % G || !q4kx_geom(K, 64, &P, &TP, &RW)) return false;
   if (N > INT32_MAX / 2 || (N + 1) * (K / 2) > UINT32_MAX) return false;
   if (((uintptr_t)codes & 15) || ((uintptr_t)x & 15)) return false;
-  return q4kx_lds(mm_of(M), K, TP, RW, false, true, false) <= 160 * 1024;
+  return q4kx_lds(mm_of(M), K, TP, RW, 1, true, false) <= 160 * 1024;
 }
 
 int launch_gemv_int4x(const void *x, int x_dtype, const uint32_t *codes, const float *sc, const float *zr, void *y,
@@ -897,9 +898,9 @@ int launch_gemv_int4x(const void *x, int x_dtype, const uint32_t *codes, const f
     if (int rc = launch_quantize_act(x, x_dtype, ws, M, K, s)) return rc;
     a.ain = static_cast<const uint8_t *>(ws);
     if (a.TP > 64) switch (x_dtype) {  // two rows per team (15.0 -> 13.8 us at 3584 x 18944)
-      case F32: return dispatch_q4kx<Int4Unit, false, false, false, F32, F32, true>(a, s);
-      case BF16: return dispatch_q4kx<Int4Unit, false, false, false, F32, BF16, true>(a, s);
-      case F16: return dispatch_q4kx<Int4Unit, false, false, false, F32, F16, true>(a, s);
+      case F32: return dispatch_q4kx<Int4Unit, false, false, false, F32, F32, 2>(a, s);
+      case BF16: return dispatch_q4kx<Int4Unit, false, false, false, F32, BF16, 2>(a, s);
+      case F16: return dispatch_q4kx<Int4Unit, false, false, false, F32, F16, 2>(a, s);
       default: return fail(HQ_EUNSUPPORTED, "int4_gemv", "x dtype %d", x_dtype);
     }
     switch (x_dtype) {
