@@ -621,6 +621,18 @@ __global__ __launch_bounds__(512) void moe_gemv_x_kernel(MoeXArgs ma) {
   extern __shared__ __align__(16) uint8_t smem[];
   const Q4kxArgs &a = ma.g;
   const int t = threadIdx.x, lane = t & 63;
+  // One row of x (a single token's gate/up, plain kernel): every pair reads row 0, so the first slice of
+  // x loads (all of x up to K = 2048) goes out now, beside the expert-id search instead of
+  // after it.
+  constexpr int XT = 4;
+  const bool x1 = !GATED && ma.rows == 1;  // (the gated kernel has no registers to spare)
+  const int KB0 = a.K >> 5, ntask0 = MM * KB0 * 8;
+  float4 xpre = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (x1) {
+    const int task = t < ntask0 ? t : ntask0 - 1;
+    const int blk = task >> 3, sub = task & 7, kb = blk % KB0;
+    xpre = *reinterpret_cast<const float4 *>(static_cast<const float *>(a.x) + kb * 32 + sub * 4);
+  }
   const Seg sg = find_segment(ma.expts, ma.npairs, (int)blockIdx.y, lane);
   if (sg.seg0 < 0) return;
   const int64_t seg0 = sg.seg0, seg1 = sg.seg1;
@@ -668,20 +680,25 @@ __global__ __launch_bounds__(512) void moe_gemv_x_kernel(MoeXArgs ma) {
       if (GATED) U::load(w + ma.up_off, a.s0, a.z0, a, row, L, wr[NW - 1]);
     }
     if (c0 != seg0) __syncthreads();  // every lane has its activations of the previous chunk
-    constexpr int XT = 4;
     const int ntask = MM * KB * 8;
     const float *x = static_cast<const float *>(a.x);
     for (int base = 0; base < ntask; base += XT * (int)blockDim.x) {
       float4 xv[XT];
+      {
 #pragma unroll
-      for (int i = 0; i < XT; i++) {
-        int task = base + i * (int)blockDim.x + t;
-        task = task < ntask ? task : ntask - 1;
-        const int blk = task >> 3, sub = task & 7, mm = blk / KB, kb = blk - mm * KB;
-        int64_t r = 0;
+        for (int i = 0; i < XT; i++) {
+          if (i == 0 && x1 && c0 == seg0 && base == 0) {
+            xv[0] = xpre;
+            continue;
+          }
+          int task = base + i * (int)blockDim.x + t;
+          task = task < ntask ? task : ntask - 1;
+          const int blk = task >> 3, sub = task & 7, mm = blk / KB, kb = blk - mm * KB;
+          int64_t r = 0;
 #pragma unroll
-        for (int k = 0; k < MM; k++) r = k == mm ? xrow[k] : r;
-        xv[i] = *reinterpret_cast<const float4 *>(x + r * a.K + kb * 32 + sub * 4);
+          for (int k = 0; k < MM; k++) r = k == mm ? xrow[k] : r;
+          xv[i] = *reinterpret_cast<const float4 *>(x + r * a.K + kb * 32 + sub * 4);
+        }
       }
 #pragma unroll
       for (int i = 0; i < XT; i++) {
