@@ -18,9 +18,11 @@
 //    team of TP lanes covers a row; a workgroup holds RW teams.  Products are exact
 //    v_dot4_i32_i8 chains scaled once per 32-block.
 //  * Workgroups are persistent (two per CU).  One register slot keeps the next row group's
-//    loads in flight while the current one is reduced; every load is unconditional
-//    (inactive lanes and rows past N read valid addresses and their sums are dropped), so
-//    no load sits in a branch and the compiler's wait counts stay exact.
+//    loads in flight while the current one is reduced (each weight refilled as soon as its
+//    dot is done); every load is unconditional -- inactive lanes read valid addresses and
+//    their sums are dropped, rows past N are range-checked buffer loads that fetch nothing --
+//    so no load sits in a branch and the compiler's wait counts stay exact.  Long rows carry
+//    two rows per team and iteration.
 //  * Q4_K high nibbles are masked in place with the sign bit flipped (16 * (q - 8) as a
 //    signed byte, one and-xor per dword); the -8 folds into the block-sum term.
 //  * Team sums: DPP row sums, then v_readlane over the wave's four rows; teams wider than a
