@@ -416,10 +416,12 @@ __global__ __launch_bounds__(256) void act_to_bf16_kernel(const uint8_t *__restr
 static int gemm_bm(int64_t M) { return M <= 64 ? 64 : 256; }
 
 int gemm_splits(int64_t M, int64_t N, int64_t K) {
+  // Split K until the grid fills the CUs: the 64-row tile (4 waves, 55 KB of LDS) up to two
+  // workgroups per CU (int4 M = 64, 18944 x 3584: 63 -> 46 us), at most 8 splits.
   int64_t tiles = cdiv(M, gemm_bm(M)) * cdiv(N, GBN), steps = K / GBK;
-  int target = device_cus();
+  const int target = device_cus() * (gemm_bm(M) == 64 ? 2 : 1);
   int s = 1;
-  while (tiles * (s * 2) <= target && steps / (s * 2) >= 8) s *= 2;
+  while (tiles * (s * 2) <= target && steps / (s * 2) >= 8 && s < 8) s *= 2;
   return s;
 }
 
@@ -473,10 +475,10 @@ static int launch_gemm_t(const GemmArgs &a0, int out_dtype, void *out, float *pa
   return check_launch("splitk_reduce");
 }
 
+// M <= 64 only (larger M takes the warp-specialised kernel of gemm_ws.hip).
 template <class WP>
 static int launch_gemm_p(const GemmArgs &a, int out_dtype, void *out, float *partials, hipStream_t s) {
-  if (gemm_bm(a.M) == 64) return launch_gemm_t<WP, 64>(a, out_dtype, out, partials, s);
-  return launch_gemm_t<WP, 256>(a, out_dtype, out, partials, s);
+  return launch_gemm_t<WP, 64>(a, out_dtype, out, partials, s);
 }
 
 int launch_gemm_q4k_bf16(const uint16_t *xb, const void *w, float *out, float *partials, int64_t M, int64_t N,
