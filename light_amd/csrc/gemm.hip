@@ -235,6 +235,136 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
     }
 }
 
+// ---- int4, M <= 64: weights straight into MFMA operands -------------------------
+// out[m, n] = sum_k x[m, k] * s[n, g] * (q[n, k] - z[n, g]) for up to 64 rows of x.  Each wave
+// owns 32 weight rows and streams their codes through registers, expanding each lane's 8
+// codes per 16-k slice directly into its MFMA B fragment (no LDS for the weights); the
+// workgroup shares x in LDS, 128 k per stage, double-buffered.  The two halves of a wave
+// (lanes l / 32) take the two contiguous 64-k halves of a stage -- A and B use the same
+// k permutation, so the sum is unchanged -- which makes every code load a contiguous 16 B.
+// Dequant in fma form, s * q + (-s z), rounded once to bf16 (the 64-row path is not the
+// bit-exact dequant).  Split K over grid.z; partial tiles summed by splitk_reduce_kernel.
+constexpr int SK = 128, SLD = SK + 8;  // x stage: 64 rows x 128 k (bf16), padded row stride
+
+struct SmallI4Args {
+  const uint16_t *x;       // bf16 [M][K]
+  const uint32_t *codes;   // (N, K/8)
+  const float *s, *z;      // (N, K/G)
+  float *out;              // [M][N] or split partials [S][M][N]
+  int M, N, K, G, splits;
+};
+
+template <bool G64>  // G % 64 == 0: one (scale, zero) per lane per stage
+__global__ __launch_bounds__(256) void gemm_small_int4_kernel(SmallI4Args a) {
+  __shared__ __align__(16) uint16_t xs[2][64 * SLD];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int kh = lane >> 5, fr = lane & 31;
+  const int n0 = blockIdx.x * 128 + wave * 32;
+  const int row = n0 + fr < a.N ? n0 + fr : a.N - 1;  // this lane's weight row (clamped)
+  const int nst = a.K / SK;
+  const int c0 = (int)((int64_t)nst * blockIdx.z / a.splits), c1 = (int)((int64_t)nst * (blockIdx.z + 1) / a.splits);
+  const int ng = a.K / a.G;
+  const uint32_t *crow = a.codes + (int64_t)row * (a.K / 8);
+  const float *srow = a.s + (int64_t)row * ng, *zrow = a.z + (int64_t)row * ng;
+  // x stage loads: 64 rows x 256 B; thread t -> row t / 4, 64-byte quarter t % 4.
+  const int xr = t >> 2, xq = t & 3;
+  const uint16_t *xsrc = a.x + (int64_t)(xr < a.M ? xr : a.M - 1) * a.K + xq * 32;
+
+  f32x16 acc[2];
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[i][r] = 0.f;
+  if (c0 >= c1) return;
+
+  // Stage c + 1's loads go out while stage c is computed.  (A two-stage register ring
+  // measured the same: the compiler waits for every outstanding load at the loop's back edge.)
+  u32x4 xv[4], cw[2];
+  float sc[8], zc[8];
+  auto load_stage = [&](int c) __attribute__((always_inline)) {
+    const uint16_t *xp = xsrc + (int64_t)c * SK;
+#pragma unroll
+    for (int i = 0; i < 4; i++) xv[i] = *reinterpret_cast<const u32x4 *>(xp + 8 * i);
+    const uint32_t *cp = crow + (c * SK + 64 * kh) / 8;
+    cw[0] = *reinterpret_cast<const u32x4 *>(cp);
+    cw[1] = *reinterpret_cast<const u32x4 *>(cp + 4);
+    if constexpr (G64) {
+      const int g = (c * SK + 64 * kh) / a.G;
+      sc[0] = srow[g];
+      zc[0] = zrow[g];
+    } else {
+#pragma unroll
+      for (int s8 = 0; s8 < 8; s8++) {
+        const int g = (c * SK + 64 * kh + 8 * s8) / a.G;
+        sc[s8] = srow[g];
+        zc[s8] = zrow[g];
+      }
+    }
+  };
+  auto store_x = [&](int buf) __attribute__((always_inline)) {
+    uint16_t *d = &xs[buf][xr * SLD + xq * 32];
+#pragma unroll
+    for (int i = 0; i < 4; i++) *reinterpret_cast<u32x4 *>(d + 8 * i) = xv[i];
+  };
+  load_stage(c0);
+  store_x(0);
+  u32x4 cur[2] = {cw[0], cw[1]};
+  float cs[8], cz[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    cs[i] = sc[G64 ? 0 : i];
+    cz[i] = zc[G64 ? 0 : i];
+  }
+  __syncthreads();
+  for (int c = c0; c < c1; c++) {
+    const int buf = (c - c0) & 1;
+    if (c + 1 < c1) load_stage(c + 1);
+    const uint16_t *xa = &xs[buf][0];
+#pragma unroll
+    for (int s8 = 0; s8 < 8; s8++) {
+      const uint32_t w = cur[s8 >> 2][s8 & 3];
+      const float sg = cs[G64 ? 0 : s8], nz = -sg * cz[G64 ? 0 : s8];
+      const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+      bf16x8 b;
+      b[0] = (__bf16)__fmaf_rn(sg, (float)(lo & 0xff), nz);
+      b[1] = (__bf16)__fmaf_rn(sg, (float)(hi & 0xff), nz);
+      b[2] = (__bf16)__fmaf_rn(sg, (float)((lo >> 8) & 0xff), nz);
+      b[3] = (__bf16)__fmaf_rn(sg, (float)((hi >> 8) & 0xff), nz);
+      b[4] = (__bf16)__fmaf_rn(sg, (float)((lo >> 16) & 0xff), nz);
+      b[5] = (__bf16)__fmaf_rn(sg, (float)((hi >> 16) & 0xff), nz);
+      b[6] = (__bf16)__fmaf_rn(sg, (float)(lo >> 24), nz);
+      b[7] = (__bf16)__fmaf_rn(sg, (float)(hi >> 24), nz);
+      const int kx = 64 * kh + 8 * s8;
+      const bf16x8 a0 = *reinterpret_cast<const bf16x8 *>(xa + fr * SLD + kx);
+      const bf16x8 a1 = *reinterpret_cast<const bf16x8 *>(xa + (32 + fr) * SLD + kx);
+      acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b, acc[0], 0, 0, 0);
+      acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b, acc[1], 0, 0, 0);
+    }
+    if (c + 1 < c1) {
+      store_x(buf ^ 1);
+      cur[0] = cw[0];
+      cur[1] = cw[1];
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        cs[i] = sc[G64 ? 0 : i];
+        cz[i] = zc[G64 ? 0 : i];
+      }
+    }
+    __syncthreads();
+  }
+  // Lane holds D[8*(r/4) + 4*(lane/32) + r%4][lane%32] of each 32 x 32 tile (m, n).
+  float *out = a.out + (int64_t)blockIdx.z * a.M * a.N;
+  const int col = n0 + fr;
+  if (col >= a.N) return;
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int m = 32 * i + 8 * (r >> 2) + 4 * kh + (r & 3);
+      if (m < a.M) out[(int64_t)m * a.N + col] = acc[i][r];
+    }
+}
+
 // ---- MoE grouped GEMM ---------------------------------------------------------
 // out[p, n] = w(p) * x[row(p)] . dequant(W[e])[n] for the expert-sorted pairs of
 // expert e = blockIdx.y; blockIdx.x is the 128-wide weight-row tile.  The expert's
@@ -429,10 +559,50 @@ size_t gemm_x_bytes(int64_t M, int64_t K) { return ((size_t)M * (size_t)K * 2 + 
 
 size_t gemm_ws_partial_bytes(int64_t M, int64_t N, int64_t K, bool f32_out);
 
+// int4 at M <= 64 (gemm_small_int4_kernel): split K until about two workgroups per CU,
+// keeping at least four 128-k stages per split.
+static int small_int4_splits(int64_t N, int64_t K) {
+  const int64_t tiles = cdiv(N, 128), nst = K / SK;
+  const int64_t target = 2 * (int64_t)device_cus();
+  int s = 1;
+  while (tiles * (s * 2) <= target && nst / (s * 2) >= 4 && s < 16) s *= 2;
+  return s;
+}
+
+static bool small_int4_ok(int64_t M, int64_t K, int G) { return M <= 64 && K % SK == 0 && G % 32 == 0; }
+
 size_t gemm_partial_bytes(int64_t M, int64_t N, int64_t K, bool f32_out) {
   int s = gemm_splits(M, N, K);
-  const size_t old = (s > 1 || !f32_out) ? (size_t)s * (size_t)M * (size_t)N * 4 : 0;
+  size_t old = (s > 1 || !f32_out) ? (size_t)s * (size_t)M * (size_t)N * 4 : 0;
+  if (M <= 64 && K % SK == 0) {
+    const int s2 = small_int4_splits(N, K);
+    old = std::max(old, (s2 > 1 || !f32_out) ? (size_t)s2 * (size_t)M * (size_t)N * 4 : (size_t)0);
+  }
   return std::max(old, gemm_ws_partial_bytes(M, N, K, f32_out));
+}
+
+static int launch_small_int4(const uint16_t *xb, const uint32_t *codes, const float *sc, const float *zr, void *out,
+                             int out_dtype, float *partials, int64_t M, int64_t N, int64_t K, int G, hipStream_t s) {
+  SmallI4Args a;
+  a.x = xb;
+  a.codes = codes;
+  a.s = sc;
+  a.z = zr;
+  a.M = (int)M;
+  a.N = (int)N;
+  a.K = (int)K;
+  a.G = G;
+  a.splits = small_int4_splits(N, K);
+  const bool direct = a.splits == 1 && out_dtype == F32;
+  a.out = direct ? static_cast<float *>(out) : partials;
+  dim3 grid((unsigned)cdiv(N, 128), 1, (unsigned)a.splits);
+  if (G % 64 == 0)
+    gemm_small_int4_kernel<true><<<grid, 256, 0, s>>>(a);
+  else
+    gemm_small_int4_kernel<false><<<grid, 256, 0, s>>>(a);
+  if (int rc = check_launch("gemm_small_int4")) return rc;
+  if (direct) return HQ_OK;
+  return launch_splitk_reduce(partials, out, out_dtype, M * N, a.splits, s);
 }
 
 int launch_gemm_ws_q4k(const uint16_t *xb, const void *w, float *out, float *partials, int64_t M, int64_t N,
@@ -498,6 +668,7 @@ int launch_gemm_q4k_bf16(const uint16_t *xb, const void *w, float *out, float *p
 int launch_gemm_int4_bf16(const uint16_t *xb, const uint32_t *codes, const float *sc, const float *zr, void *out,
                           int out_dtype, float *partials, int64_t M, int64_t N, int64_t K, int G, hipStream_t s) {
   if (M > 64) return launch_gemm_ws_int4(xb, codes, sc, zr, out, out_dtype, partials, M, N, K, G, s);
+  if (small_int4_ok(M, K, G)) return launch_small_int4(xb, codes, sc, zr, out, out_dtype, partials, M, N, K, G, s);
   GemmArgs a = {};
   a.x = xb;
   a.w = reinterpret_cast<const uint8_t *>(codes);
