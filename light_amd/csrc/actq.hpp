@@ -173,4 +173,19 @@ __device__ __forceinline__ float q4k_pair_h16(float d, float dmin, float scA, fl
   return __fmaf_rn(d, v, -__fmul_rn(dmin, mn));
 }
 
+// Single-level forms of q4k_pair / q4k_pair_h16: x is q1 with its step d only (q8_1).
+__device__ __forceinline__ float q4k_pair1(float d, float dmin, float scA, float scB, float mnA, float mnB, float4 de,
+                                           float2 ss, int dA, int dB) {
+  const float v = __fmaf_rn(scB, __fmul_rn(de.z, (float)dB), __fmul_rn(scA, __fmul_rn(de.x, (float)dA)));
+  const float mn = __fmaf_rn(mnB, ss.y, __fmul_rn(mnA, ss.x));
+  return __fmaf_rn(d, v, -__fmul_rn(dmin, mn));
+}
+__device__ __forceinline__ float q4k_pair1_h16(float d, float dmin, float scA, float scB, float mnA, float mnB,
+                                               float4 de, float2 ss, int dA, int dB16) {
+  const float vb = __fmaf_rn(__fmul_rn(de.z, (float)dB16), 0.0625f, __fmul_rn(8.0f, ss.y));
+  const float v = __fmaf_rn(scB, vb, __fmul_rn(scA, __fmul_rn(de.x, (float)dA)));
+  const float mn = __fmaf_rn(mnB, ss.y, __fmul_rn(mnA, ss.x));
+  return __fmaf_rn(d, v, -__fmul_rn(dmin, mn));
+}
+
 }  // namespace hq

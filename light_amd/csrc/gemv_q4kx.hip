@@ -99,9 +99,14 @@ __device__ __forceinline__ float bload_f32(__amdgpu_buffer_rsrc_t r, uint32_t of
 // sub-block 2p, high = 2p+1) and the block header, broadcast in the block's 4-lane quad.
 // Q5_K (quant/q5_k.go:11-22) adds the 32 qh bytes of the block: bit 2p / 2p+1 of qh[l] is
 // the fifth bit of the pair's low / high element l.
-template <bool Q5>
+//
+// X2 = false: single-level activations (q1 with its step d only -- exactly q8_1), for rows of
+// at least kX1MinK elements, where the int8 rounding noise of x averages out below the error
+// bar; the q2 loads and dots are skipped (4096 x 14336: 10.9 -> 9.8 us).
+template <bool Q5, bool X2 = true>
 struct QkUnit {
   static constexpr int BB = Q5 ? 176 : 144, QO = Q5 ? 48 : 16;
+  static constexpr bool kX2 = X2;
   struct Lane {
     uint32_t qoff, hoff, qhoff;  // byte offsets of the quant chunk / the block header / qh
     int ja;                      // first 32-block of x
@@ -149,13 +154,14 @@ struct QkUnit {
   __device__ static void load_x(const uint8_t *q1, const uint8_t *q2, const uint8_t *de, const uint8_t *sx,
                                 int64_t blk, X &x) {
     const u32x4_t *s1 = reinterpret_cast<const u32x4_t *>(q1 + blk * 32);
-    const u32x4_t *s2 = reinterpret_cast<const u32x4_t *>(q2 + blk * 32);
     const u32x4_t v0 = s1[0], v1 = s1[1], v2 = s1[2], v3 = s1[3];
-    const u32x4_t w0 = s2[0], w1 = s2[1], w2 = s2[2], w3 = s2[3];
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-      x.xa[k] = v0[k], x.xa[k + 4] = v1[k], x.xb[k] = v2[k], x.xb[k + 4] = v3[k];
-      x.ya[k] = w0[k], x.ya[k + 4] = w1[k], x.yb[k] = w2[k], x.yb[k + 4] = w3[k];
+    for (int k = 0; k < 4; k++) x.xa[k] = v0[k], x.xa[k + 4] = v1[k], x.xb[k] = v2[k], x.xb[k + 4] = v3[k];
+    if constexpr (X2) {
+      const u32x4_t *s2 = reinterpret_cast<const u32x4_t *>(q2 + blk * 32);
+      const u32x4_t w0 = s2[0], w1 = s2[1], w2 = s2[2], w3 = s2[3];
+#pragma unroll
+      for (int k = 0; k < 4; k++) x.ya[k] = w0[k], x.ya[k + 4] = w1[k], x.yb[k] = w2[k], x.yb[k + 4] = w3[k];
     }
     x.de = *reinterpret_cast<const float4 *>(de + 8 * blk);
     x.ss = *reinterpret_cast<const float2 *>(sx + 4 * blk);
@@ -200,10 +206,17 @@ struct QkUnit {
       for (int k = 0; k < 8; k++) {
         dA = dot4((int)lo[k], (int)x[mm].xa[k], dA);
         dB = dot4((int)hi[k], (int)x[mm].xb[k], dB);
-        dA2 = dot4((int)lo[k], (int)x[mm].ya[k], dA2);
-        dB2 = dot4((int)hi[k], (int)x[mm].yb[k], dB2);
+        if constexpr (X2) {
+          dA2 = dot4((int)lo[k], (int)x[mm].ya[k], dA2);
+          dB2 = dot4((int)hi[k], (int)x[mm].yb[k], dB2);
+        }
       }
-      if constexpr (Q5)
+      if constexpr (!X2) {
+        if constexpr (Q5)
+          out[mm] = q4k_pair1(d, dmin, scA, scB, mnA, mnB, x[mm].de, x[mm].ss, dA, dB);
+        else
+          out[mm] = q4k_pair1_h16(d, dmin, scA, scB, mnA, mnB, x[mm].de, x[mm].ss, dA, dB);
+      } else if constexpr (Q5)
         out[mm] = q4k_pair(d, dmin, scA, scB, mnA, mnB, x[mm].de, x[mm].ss, dA, dA2, dB, dB2);
       else
         out[mm] = q4k_pair_h16(d, dmin, scA, scB, mnA, mnB, x[mm].de, x[mm].ss, dA, dA2, dB, dB2);
@@ -213,11 +226,25 @@ struct QkUnit {
 using Q4kUnit = QkUnit<false>;
 using Q5kUnit = QkUnit<true>;
 
+// Rows of at least this many elements take single-level activations.
+constexpr int64_t kX1MinK = 4096;
+
+// Calls f with a default-constructed unit policy for (dt in {Q4_K, Q5_K}, K).
+template <class F>
+static int with_qk_unit(int dt, int64_t K, F &&f) {
+  const bool x1 = K >= kX1MinK;
+  if (dt == Q5_K) return x1 ? f(QkUnit<true, false>{}) : f(QkUnit<true, true>{});
+  return x1 ? f(QkUnit<false, false>{}) : f(QkUnit<false, true>{});
+}
+
 // int4 unit (quant.Int4, quant/int4.go:11-34): 64 elements = code words 8u .. 8u+7 (two
 // 32-blocks A, B); nibble j of word c is element 8c + j, so the low / high nibbles of a
 // word are its even / odd elements and the lane's activations are stored even / odd
 // permuted (v_perm_b32) once.  Per block: s * (d * sum(q q1) + e * sum(q q2) - z * sx).
-struct Int4Unit {
+// X2 = false: single-level activations, as for QkUnit.
+template <bool X2 = true>
+struct Int4UnitT {
+  static constexpr bool kX2 = X2, kInt4 = true;
   struct Lane {
     uint32_t coff;  // byte offset of the unit's codes in a row
     int ja, gA, gB;  // first 32-block of x; group index of blocks A, B
@@ -258,15 +285,20 @@ struct Int4Unit {
     const u32x4_t *s1 = reinterpret_cast<const u32x4_t *>(q1 + blk * 32);
     const u32x4_t *s2 = reinterpret_cast<const u32x4_t *>(q2 + blk * 32);
     const u32x4_t v[4] = {s1[0], s1[1], s1[2], s1[3]};
-    const u32x4_t y[4] = {s2[0], s2[1], s2[2], s2[3]};
 #pragma unroll
     for (int k = 0; k < 8; k++) {
       const uint32_t a0 = v[k >> 1][2 * (k & 1)], a1 = v[k >> 1][2 * (k & 1) + 1];
-      const uint32_t b0 = y[k >> 1][2 * (k & 1)], b1 = y[k >> 1][2 * (k & 1) + 1];
       x.ev[k] = (int)__builtin_amdgcn_perm(a1, a0, 0x06040200u);
       x.od[k] = (int)__builtin_amdgcn_perm(a1, a0, 0x07050301u);
-      x.ev2[k] = (int)__builtin_amdgcn_perm(b1, b0, 0x06040200u);
-      x.od2[k] = (int)__builtin_amdgcn_perm(b1, b0, 0x07050301u);
+    }
+    if constexpr (X2) {
+      const u32x4_t y[4] = {s2[0], s2[1], s2[2], s2[3]};
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        const uint32_t b0 = y[k >> 1][2 * (k & 1)], b1 = y[k >> 1][2 * (k & 1) + 1];
+        x.ev2[k] = (int)__builtin_amdgcn_perm(b1, b0, 0x06040200u);
+        x.od2[k] = (int)__builtin_amdgcn_perm(b1, b0, 0x07050301u);
+      }
     }
     x.de = *reinterpret_cast<const float4 *>(de + 8 * blk);
     x.ss = *reinterpret_cast<const float2 *>(sx + 4 * blk);
@@ -288,24 +320,43 @@ struct Int4Unit {
       for (int k = 0; k < 4; k++) {
         dA = dot4((int)lo[k], x[mm].ev[k], dA);
         dA = dot4((int)hi[k], x[mm].od[k], dA);
-        dA2 = dot4((int)lo[k], x[mm].ev2[k], dA2);
-        dA2 = dot4((int)hi[k], x[mm].od2[k], dA2);
         dB = dot4((int)lo[4 + k], x[mm].ev[4 + k], dB);
         dB = dot4((int)hi[4 + k], x[mm].od[4 + k], dB);
-        dB2 = dot4((int)lo[4 + k], x[mm].ev2[4 + k], dB2);
-        dB2 = dot4((int)hi[4 + k], x[mm].od2[4 + k], dB2);
+        if constexpr (X2) {
+          dA2 = dot4((int)lo[k], x[mm].ev2[k], dA2);
+          dA2 = dot4((int)hi[k], x[mm].od2[k], dA2);
+          dB2 = dot4((int)lo[4 + k], x[mm].ev2[4 + k], dB2);
+          dB2 = dot4((int)hi[4 + k], x[mm].od2[4 + k], dB2);
+        }
       }
       const float4 de = x[mm].de;
-      const float yA = __fmaf_rn(-w.zA, x[mm].ss.x, __fmaf_rn(de.y, (float)dA2, __fmul_rn(de.x, (float)dA)));
-      const float yB = __fmaf_rn(-w.zB, x[mm].ss.y, __fmaf_rn(de.w, (float)dB2, __fmul_rn(de.z, (float)dB)));
+      float yA, yB;
+      if constexpr (X2) {
+        yA = __fmaf_rn(-w.zA, x[mm].ss.x, __fmaf_rn(de.y, (float)dA2, __fmul_rn(de.x, (float)dA)));
+        yB = __fmaf_rn(-w.zB, x[mm].ss.y, __fmaf_rn(de.w, (float)dB2, __fmul_rn(de.z, (float)dB)));
+      } else {
+        yA = __fmaf_rn(-w.zA, x[mm].ss.x, __fmul_rn(de.x, (float)dA));
+        yB = __fmaf_rn(-w.zB, x[mm].ss.y, __fmul_rn(de.z, (float)dB));
+      }
       out[mm] = __fmaf_rn(w.sB, yB, __fmul_rn(w.sA, yA));
     }
   }
 };
 
+using Int4Unit = Int4UnitT<true>;
+
+template <class U, class = void>
+struct is_int4_unit {
+  static constexpr bool value = false;
+};
+template <class U>
+struct is_int4_unit<U, decltype(void(U::kInt4))> {
+  static constexpr bool value = true;
+};
+
 template <class U>
 __device__ __forceinline__ typename U::Lane unit_lane(int u, int G) {
-  if constexpr (__is_same(U, Int4Unit))
+  if constexpr (is_int4_unit<U>::value)
     return U::lane(u, G);
   else
     return U::lane(u);
@@ -375,10 +426,13 @@ __device__ __forceinline__ void q4kx_body(const Q4kxArgs &a, uint8_t *smem, cons
   // (Deeper rings -- two to four groups in flight per wave -- were measured slower: this
   // kernel is bound by VALU issue as much as by HBM, and more outstanding rows only spread
   // the DRAM traffic.)
+  // Prepared activations are loaded before the first weights (measured 0.2-0.3 us faster at
+  // 4096 x 14336: the shared x lines are not queued behind the weight stream); x quantized
+  // in the kernel goes after them, so the weights stream during the quantization.
   typename U::W wr[1][NW];
-  Q4KX_LOAD(0, Q4KX_GRP(0));
-
   typename U::X xr[MM];
+  if constexpr (XIN) Q4KX_LOAD(0, Q4KX_GRP(0));
+
   const int64_t lds_act = XIN ? q4kx_act_lds(MM, a.K) : 0;
   if constexpr (XIN) {
     // Quantize this workgroup's MM rows of x into LDS: a task is half a 32-block (sixteen
@@ -400,7 +454,8 @@ __device__ __forceinline__ void q4kx_body(const Q4kxArgs &a, uint8_t *smem, cons
       if (task < ntask) {  // both lanes of a block agree (ntask is even)
         const int blk = task >> 1, half = task & 1;
         *reinterpret_cast<u32x4_t *>(lq1 + blk * 32 + half * 16) = u32x4_t{q.q1[0], q.q1[1], q.q1[2], q.q1[3]};
-        *reinterpret_cast<u32x4_t *>(lq2 + blk * 32 + half * 16) = u32x4_t{q.q2[0], q.q2[1], q.q2[2], q.q2[3]};
+        if constexpr (U::kX2)
+          *reinterpret_cast<u32x4_t *>(lq2 + blk * 32 + half * 16) = u32x4_t{q.q2[0], q.q2[1], q.q2[2], q.q2[3]};
         if (half == 0) {
           lde[blk] = make_float2(q.d, q.e);
           lsx[blk] = q.sum;
@@ -439,6 +494,7 @@ __device__ __forceinline__ void q4kx_body(const Q4kxArgs &a, uint8_t *smem, cons
       U::load_x(a.ain, a.ain + a.in_q2, a.ain + a.in_d, a.ain + a.in_s, (int64_t)m * KB + L.ja, xr[mm]);
     }
   }
+  if constexpr (!XIN) Q4KX_LOAD(0, Q4KX_GRP(0));
 
   const int hpt = a.TP >> 4;  // 16-lane rows per team
   float *part = reinterpret_cast<float *>(smem + lds_act);
@@ -872,9 +928,10 @@ int launch_gemv_q4kx(const float *x, const void *w0, const void *w1, float *out,
   a.w1 = static_cast<const uint8_t *>(w1);
   a.out = out;
   a.act = act;
-  if (dt == Q5_K)
-    return w1 ? dispatch_q4kx<Q5kUnit, true, true, false>(a, s) : dispatch_q4kx<Q5kUnit, false, true, false>(a, s);
-  return w1 ? dispatch_q4kx<Q4kUnit, true, true, false>(a, s) : dispatch_q4kx<Q4kUnit, false, true, false>(a, s);
+  return with_qk_unit(dt, K, [&](auto unit) {
+    using U = decltype(unit);
+    return w1 ? dispatch_q4kx<U, true, true, false>(a, s) : dispatch_q4kx<U, false, true, false>(a, s);
+  });
 }
 
 int launch_gemv_q4kx_act(const void *act_in, const void *w, float *out, int64_t M, int64_t N, int64_t K, int dt,
@@ -886,12 +943,11 @@ int launch_gemv_q4kx_act(const void *act_in, const void *w, float *out, int64_t 
   a.out = out;
   // Long rows (teams of several waves): two rows per team and iteration (measured 10.8 ->
   // 10.6 us at 4096 x 14336; four rows, 130 registers, measured 12.2 us).
-  if (a.TP > 64) {
-    if (dt == Q5_K) return dispatch_q4kx<Q5kUnit, false, false, false, F32, F32, 2>(a, s);
-    return dispatch_q4kx<Q4kUnit, false, false, false, F32, F32, 2>(a, s);
-  }
-  if (dt == Q5_K) return dispatch_q4kx<Q5kUnit, false, false, false>(a, s);
-  return dispatch_q4kx<Q4kUnit, false, false, false>(a, s);
+  return with_qk_unit(dt, K, [&](auto unit) {
+    using U = decltype(unit);
+    if (a.TP > 64) return dispatch_q4kx<U, false, false, false, F32, F32, 2>(a, s);
+    return dispatch_q4kx<U, false, false, false>(a, s);
+  });
 }
 
 // int4 GEMV on x (F32 / BF16 / F16) quantized in the kernel; y at x's dtype.
@@ -916,7 +972,15 @@ int launch_gemv_int4x(const void *x, int x_dtype, const uint32_t *codes, const f
     // Long rows: one quantize launch beats every workgroup quantizing all of x.
     if (int rc = launch_quantize_act(x, x_dtype, ws, M, K, s)) return rc;
     a.ain = static_cast<const uint8_t *>(ws);
-    if (a.TP > 64) switch (x_dtype) {  // two rows per team (15.0 -> 13.8 us at 3584 x 18944)
+    // Two rows per team (15.0 -> 13.8 us at 3584 x 18944); rows of at least kX1MinK take
+    // single-level activations.
+    if (a.TP > 64 && K >= kX1MinK) switch (x_dtype) {
+      case F32: return dispatch_q4kx<Int4UnitT<false>, false, false, false, F32, F32, 2>(a, s);
+      case BF16: return dispatch_q4kx<Int4UnitT<false>, false, false, false, F32, BF16, 2>(a, s);
+      case F16: return dispatch_q4kx<Int4UnitT<false>, false, false, false, F32, F16, 2>(a, s);
+      default: return fail(HQ_EUNSUPPORTED, "int4_gemv", "x dtype %d", x_dtype);
+    }
+    if (a.TP > 64) switch (x_dtype) {
       case F32: return dispatch_q4kx<Int4Unit, false, false, false, F32, F32, 2>(a, s);
       case BF16: return dispatch_q4kx<Int4Unit, false, false, false, F32, BF16, 2>(a, s);
       case F16: return dispatch_q4kx<Int4Unit, false, false, false, F32, F16, 2>(a, s);
@@ -969,8 +1033,7 @@ int launch_matmul_q_gated(const float *x, const void *wg, const void *wu, float 
     a.w1 = static_cast<const uint8_t *>(wu);
     a.out = out;
     a.act = act;
-    if (dt == Q5_K) return dispatch_q4kx<Q5kUnit, true, false, false>(a, s);
-    return dispatch_q4kx<Q4kUnit, true, false, false>(a, s);
+    return with_qk_unit(dt, K, [&](auto unit) { return dispatch_q4kx<decltype(unit), true, false, false>(a, s); });
   }
   float *g = static_cast<float *>(ws);
   float *u = reinterpret_cast<float *>(static_cast<char *>(ws) + al256(4 * M * N));
@@ -1010,8 +1073,8 @@ int launch_mlp_q(const float *x, const void *wg, const void *wu, const void *wd,
     a.w1 = static_cast<const uint8_t *>(wu);
     a.aout = static_cast<uint8_t *>(ws);
     a.act = act;
-    const int rc = dt == Q5_K ? dispatch_q4kx<Q5kUnit, true, true, true>(a, s)
-                              : dispatch_q4kx<Q4kUnit, true, true, true>(a, s);
+    const int rc =
+        with_qk_unit(dt, H, [&](auto unit) { return dispatch_q4kx<decltype(unit), true, true, true>(a, s); });
     if (rc) return rc;
     // Launch 2: down projection on the prepared h.
     return launch_gemv_q4kx_act(ws, wd, out, M, H, I, dt, s);
