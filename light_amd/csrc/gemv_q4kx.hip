@@ -227,7 +227,7 @@ using Q4kUnit = QkUnit<false>;
 using Q5kUnit = QkUnit<true>;
 
 // Rows of at least this many elements take single-level activations.
-constexpr int64_t kX1MinK = 4096;
+constexpr int64_t kX1MinK = 8192;
 
 // Calls f with a default-constructed unit policy for (dt in {Q4_K, Q5_K}, K).
 template <class F>

@@ -307,3 +307,19 @@ def test_gemm_act_path_matches(dev):
     wd = oracle.dequant(hipq.Q4_K, w, N * K).reshape(N, K)
     ref, _, wn, xn = oracle.matmul_f64(x, wd)
     assert norm_err(y, ref, wn, xn) <= TOL
+
+
+@pytest.mark.parametrize("dt", [hipq.Q4_K, hipq.Q5_K])
+@pytest.mark.parametrize("K,amp", [(4096, 30.0), (8192, 10.0), (8192, 30.0), (14336, 10.0)])
+def test_matmul_q_single_level_outlier_blocks(dev, dt, K, amp):
+    """Rows of K >= 8192 quantize x to q1 alone (q8_1): its error is largest when one element
+    per 32-block sets the step.  One outlier of `amp` sigma in every block, 2048 rows (K = 4096
+    keeps both levels; measured single-level there: up to 6.2e-4)."""
+    g = np.random.default_rng(int(amp) + K + dt)
+    N = 2048
+    x = g.standard_normal((1, K)).astype(np.float32)
+    pos = np.arange(0, K, 32) + g.integers(0, 32, K // 32)
+    x[0, pos] = (amp * np.sign(g.standard_normal(K // 32))).astype(np.float32)
+    w = synth.gguf_weight(dt, N, K, g)
+    e = _check_matmul(dev, dt, x, w, N, K, f"outliers amp={amp}")
+    print(f"[err] single-level K={K} amp={amp}: {e:.3g}", flush=True)
