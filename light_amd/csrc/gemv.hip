@@ -68,7 +68,9 @@ __device__ __forceinline__ float row16_sum(float v) {
 // Full-wave sum via the four 16-lane row sums.
 __device__ __forceinline__ float wave_sum64(float v) {
   v = row16_sum(v);
-  return __shfl(v, 0, 64) + __shfl(v, 16, 64) + __shfl(v, 32, 64) + __shfl(v, 48, 64);
+  // v_readlane: the four row sums come straight from VGPR lanes, no LDS round trips.
+  const auto rl = [](float f, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), l)); };
+  return ((rl(v, 0) + rl(v, 16)) + rl(v, 32)) + rl(v, 48);
 }
 
 __device__ __forceinline__ uint4 ld16g(const void *p) { return *reinterpret_cast<const uint4 *>(p); }

@@ -661,8 +661,8 @@ __device__ __forceinline__ Seg find_segment(const int64_t *__restrict__ v, int64
         if (hit) {
           const int pos = __ffsll((unsigned long long)hit) - 1;
           sg.seg0 = base + 64 * c + pos;
-          sg.e = __shfl(cur[c], pos);
-          sg.eprev = sg.seg0 == 0 ? -1 : __shfl(prv[c], pos);
+          sg.e = __builtin_amdgcn_readlane(cur[c], pos);  // pos is wave-uniform
+          sg.eprev = sg.seg0 == 0 ? -1 : __builtin_amdgcn_readlane(prv[c], pos);
         }
       }
       const uint64_t nxt = __ballot(st && rank == (int64_t)j + 1);
