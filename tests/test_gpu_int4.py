@@ -94,7 +94,10 @@ def test_matmul_int4_light_shapes(dev, M, xdt):
 
 @pytest.mark.parametrize("M,N,K,G", [(1, 1, 32, 32), (2, 300, 512, 32), (5, 77, 1024, 128), (16, 256, 4096, 128),
                                      (33, 130, 2048, 64), (64, 512, 3584, 128), (70, 200, 1536, 96),
-                                     (4, 64, 32768, 128), (3, 77, 16384, 128)])
+                                     (4, 64, 32768, 128), (3, 77, 16384, 128),
+                                     # 8 < M <= 64 with G % 64 != 0 (a scale per 8-column slice),
+                                     # ragged N and M, and K split 16 ways
+                                     (24, 96, 1024, 32), (40, 136, 1536, 96), (48, 256, 8192, 32)])
 def test_matmul_int4_shapes(dev, M, N, K, G):
     rng = np.random.default_rng(M * 7 + N + K)
     codes, s, z = light_int4(rng, N, K, G)
