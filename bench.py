@@ -464,7 +464,7 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); "
-              "the multi-GPU sharding design is described in DESIGN.md", file=sys.stderr)
+              "sharding the weights' N rows across GPUs is designed but not built", file=sys.stderr)
         sys.exit(2)
     res = run_gpu(args)
     line = {
