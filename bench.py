@@ -1,25 +1,27 @@
 """Benchmark of the MI355X quantized-matmul path (BASELINE.json metric).
 
-Headline metric: Q4_K GEMV GB/s at Llama-3-8B MLP decode shapes,
-plus the Q4_K M=512 GEMM TFLOPS (configs[2], in --table).  One "step" is one
-MLP decode pass through the hot path at M = 1, as Light's decoder runs it
-(models/llama.go:1306-1333), one hq_mlp_q call = two kernels:
-    h = SiLU(x . Wgate^T) * (x . Wup^T)     gate/up 14336x4096 Q4_K (h emitted quantized)
-    y = h . Wdown^T                          down 4096x14336 Q4_K
-Inputs are synthetic (seeded, BASELINE distributions), resident in HBM; every
-weight is rotated over enough copies that the working set exceeds the 256 MB
-Infinity Cache.
+Headline metric: "Q4_K GEMV GB/s (% of HBM peak) + Q4_K M=512 GEMM TFLOPS", Llama-3-8B
+shapes.  Both halves are measured in the default run.
 
-`value` is whole-job throughput: algorithmic bytes of a step (the three weights
-as stored + F32 x in + F32 y out) / wall time of the K timed steps,
-replayed as captured HIP graphs so host launch cost is not measured.
-`roofline` is for the dominant kernel (the fused gate/up Q4_K GEMV), timed
-per launch with HIP events on its stream.  `cpu_baseline` is Light's AVX2 CPU
-path (the C restatement in oracle/: MatMulQ, MatMulQ, SiLU, Mul, MatMulQ) on
-the same step, on this host's cores.
+* `value` (GB/s): one "step" is one MLP decode pass through the hot path at M = 1, as
+  Light's decoder runs it (models/llama.go:1306-1333), one hq_mlp_q call = two kernels:
+      h = SiLU(x . Wgate^T) * (x . Wup^T)   gate/up 14336x4096 Q4_K (h emitted quantized)
+      y = h . Wdown^T                        down 4096x14336 Q4_K
+  value = algorithmic bytes of a step (the three weights as stored + F32 x in + F32 y out)
+  / wall time of the K timed steps, replayed as captured HIP graphs.
+* `roofline`: the step's dominant kernel, its first launch (hq_matmul_q_gated_act: the gated
+  GEMV with the quantized-h epilogue), timed per launch with HIP events on its stream.
+  `second_kernel` is the step's down GEMV, timed the same way.
+* `gemm`: the Q4_K M = 512 prefill GEMM at both shapes, hq_matmul_q per call
+  (the bf16 conversion of x plus the MFMA GEMM), TFLOP/s and fraction of the 2.5 PFLOP/s
+  dense bf16 MFMA peak, with Light's CPU path beside it.
+* `cpu_baseline`: Light's AVX2 CPU path (the C restatement in oracle/: MatMulQ, MatMulQ,
+  SiLU, Mul, MatMulQ) on the same step, on the host cores available to this process.
+
+Inputs are synthetic (seeded, BASELINE distributions) and resident in HBM; every weight is
+rotated over enough copies that the working set exceeds the 256 MB Infinity Cache.
 
 Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--table] [--no-cpu]
-"""
 import argparse
 import json
 import math
@@ -44,6 +46,7 @@ def parse():
     p.add_argument("--table", action="store_true", help="also time every config (printed to stderr)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--launches", type=int, default=200, help="per-kernel timed launches for the roofline")
+    p.add_argument("--gemm-launches", type=int, default=100, help="timed calls per M=512 GEMM shape")
     p.add_argument("--probe", action="store_true",
                    help="counter probe for rocprofv3 --pmc: a 64 MiB device copy, then 20 launches of the "
                         "dominant GEMV (no timing, no JSON line)")
@@ -174,19 +177,21 @@ def time_launches(fn, n, rot):
 
 
 def gemv_roofline(args, gate, up, x, dev):
-    """Roofline of the dominant kernel: the fused gate/up Q4_K GEMV (gemv_q4kx_kernel<1, true, D>),
-    x F32 quantized inside the kernel."""
+    """Roofline of the step's dominant kernel: its first launch, the fused gate/up Q4_K GEMV
+    that quantizes h into the act layout in its epilogue (hq_matmul_q_gated_act, the call
+    hq_mlp_q makes), x F32 quantized inside the kernel."""
     import torch
     from light_amd import hipq
     N, K = gate.N, gate.K
-    out = torch.empty((1, N), device=dev)
-    us = time_launches(lambda i: hipq.matmul_q_gated(x, gate[i], up[i], N, K, hipq.Q4_K, out=out), args.launches,
-                       len(gate.copies))
-    alg = gate.raw.nbytes + up.raw.nbytes + 4 * K + 4 * N  # both weights + F32 x + F32 h
+    ab = hipq.lib().hq_act_bytes(1, N)
+    out = torch.empty(ab, dtype=torch.uint8, device=dev)
+    us = time_launches(lambda i: hipq.matmul_q_gated_act(x, gate[i], up[i], N, K, hipq.Q4_K, out=out),
+                       args.launches, len(gate.copies))
+    alg = gate.raw.nbytes + up.raw.nbytes + 4 * K + ab  # both weights + F32 x + quantized h
     achieved = alg / (us * 1e-6) / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(f"gated N={N} K={K} M=1"),
-            "kernel": "gemv_q4kx_kernel (gated)", "shape": f"gate+up N={N} K={K} M=1",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(f"gated_act N={N} K={K} M=1"),
+            "kernel": "gemv_q4kx_kernel (gated, quantized-h epilogue)", "shape": f"gate+up N={N} K={K} M=1",
             "alg_bytes_per_launch": alg, "avg_launch_us": round(us, 3)}
 
 
@@ -203,7 +208,41 @@ def down_kernel(args, down, h, dev):
     alg = down.raw.nbytes + hipq.lib().hq_act_bytes(1, K) + 4 * N
     gbs = alg / (us * 1e-6) / 1e9
     return {"kernel": "gemv_q4kx_kernel (act input)", "shape": f"down N={N} K={K} M=1", "avg_launch_us": round(us, 3),
-            "achieved": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+            "achieved": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4), "alg_bytes_per_launch": alg}
+
+
+GEMM_SHAPES = ((512, 14336, 4096), (512, 4096, 14336))
+
+
+def gemm_records(args, dev, cpu=True):
+    """Q4_K prefill GEMM at M = 512, both shapes, per hq_matmul_q call (x F32 ->
+    bf16 conversion launch + the MFMA GEMM), weights rotated past the Infinity Cache."""
+    import torch
+    from light_amd import hipq, synth
+    out = []
+    for idx, (M, N, K) in enumerate(GEMM_SHAPES):
+        g = synth.rng(20 + idx)
+        w = Weight(synth.gguf_weight(hipq.Q4_K, N, K, g), hipq.Q4_K, N, K, dev)
+        x_np = synth.activations(M, K, g)
+        x = torch.from_numpy(x_np).to(dev)
+        y = torch.empty((M, N), device=dev)
+        ws = torch.empty(hipq.matmul_q_ws_bytes(M, N, K, hipq.Q4_K), dtype=torch.uint8, device=dev)
+        us = time_launches(lambda i: hipq.matmul_q(x, w[i], N, K, hipq.Q4_K, out=y, ws=ws), args.gemm_launches,
+                           len(w.copies))
+        flops = 2 * M * N * K
+        tflops = flops / (us * 1e-6) / 1e12
+        rec = {"shape": f"M={M} N={N} K={K}", "kernel": "to_bf16_kernel + gemm_ws_kernel<WsQ4k>",
+               "us_per_call": round(us, 2), "TFLOPS": round(tflops, 1), "peak": MFMA_PEAK_TFLOPS["bf16"],
+               "peak_unit": "TFLOP/s (dense bf16 MFMA)", "frac": round(tflops / MFMA_PEAK_TFLOPS["bf16"], 4),
+               "flops_per_call": flops}
+        if cpu:
+            t, th, smp = cpu_gguf_row(x_np, w.raw, N, K, hipq.Q4_K)
+            rec["cpu"] = {"us_per_call": round(t * 1e6, 1), "TFLOPS": round(flops / t / 1e12, 4), "cores": th,
+                          "kind": "port", "sample": smp}
+        out.append(rec)
+        del w, x, y, ws
+        torch.cuda.empty_cache()
+    return out
 
 
 def measured_traffic(shape):
@@ -347,9 +386,16 @@ def moe_rows(c, name, g, dev, cpu=False):
 
 
 def _cpu_threads():
-    import oracle
-    threads = int(os.environ.get("OMP_NUM_THREADS", "16"))
-    return max(1, min(threads, oracle.hw_threads()))
+    """Host cores this process may use (the GOMAXPROCS / hardware_concurrency role): the CPU
+    affinity set, capped by a cgroup CPU quota when one is set."""
+    n = len(os.sched_getaffinity(0))
+    try:
+        quota, period = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        if quota != "max":
+            n = min(n, max(1, math.ceil(int(quota) / int(period))))
+    except (OSError, ValueError):
+        pass
+    return max(1, n)
 
 
 def _cpu_median(fn, reps=3):
@@ -406,8 +452,7 @@ def cpu_baseline(inputs):
     step; median of 5 after a warm-up."""
     import oracle
     gate, up, down, x, _ = inputs
-    threads = int(os.environ.get("OMP_NUM_THREADS", "16"))
-    threads = max(1, min(threads, oracle.hw_threads()))
+    threads = _cpu_threads()
 
     def run():
         g = oracle.matmul_q(x, gate.raw, gate.N, gate.K, gate.dt, threads)
@@ -448,11 +493,11 @@ def probe(dev):
         dst.copy_(src)
     gate, up, _, x_np, _ = mlp_inputs(dev)
     x = torch.from_numpy(x_np).to(dev)
-    out = torch.empty((1, gate.N), device=dev)
+    out = torch.empty(hipq.lib().hq_act_bytes(1, gate.N), dtype=torch.uint8, device=dev)
     for i in range(20):
-        hipq.matmul_q_gated(x, gate[i], up[i], gate.N, gate.K, hipq.Q4_K, out=out)
+        hipq.matmul_q_gated_act(x, gate[i], up[i], gate.N, gate.K, hipq.Q4_K, out=out)
     torch.cuda.synchronize()
-    print(f"probe: copy 67108864 B x3; gemv_q4k gated N={gate.N} K={gate.K} x20", file=sys.stderr)
+    print(f"probe: copy 67108864 B x3; gemv_q4k gated_act N={gate.N} K={gate.K} x20", file=sys.stderr)
 
 
 def main():
@@ -487,10 +532,11 @@ def main():
         "roofline": res["roofline"],
         "second_kernel": res["down"],
     }
+    import torch
+    line["gemm"] = gemm_records(args, torch.device("cuda:0"), cpu=not args.no_cpu)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(res["inputs"])
     if args.table:
-        import torch
         print(json.dumps({"table": table(args, torch.device("cuda:0"))}), file=sys.stderr)
     print(json.dumps(line))
 

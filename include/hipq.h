@@ -21,8 +21,10 @@
  *  - dtype codes are Light's dtype.DType values (dtype/dtype.go:13-37).
  *  - Workspace (`ws`, `ws_bytes`): device scratch for the on-GPU q8_1
  *    activation quantization.  Size it with the matching *_ws_bytes().
- *    ws == NULL makes the library use a per-device buffer it allocates and
- *    grows on demand (not capture-safe).
+ *    ws == NULL makes the library use a buffer per (device, stream) that it
+ *    allocates and grows on demand; growing retires the old buffer without
+ *    freeing it (hq_workspace_release frees them).  During stream capture a
+ *    growth fails with HQ_EUNSUPPORTED: pass ws.
  */
 #ifndef HIPQ_H
 #define HIPQ_H
@@ -94,15 +96,26 @@ int hq_trace_stop(char *names, int *calls, double *total_us, int n_max);
 size_t hq_matmul_q_ws_bytes(int64_t M, int64_t N, int64_t K, int w_dtype);
 
 /* out (M, N) F32 = x (M, K) F32 contiguous @ dequant(w (N, K))^T.
- * w_dtype: HQ_Q8_0, HQ_Q4_K or HQ_Q6_K.  K must be a multiple of the block
- * size.  M <= 8 (and Q8_0 / Q6_K at any M): the int8-dot GEMV runs on x quantized
- * on the GPU to q8_1 (Q4_K: inside the GEMV's workgroups; Q8_0 / Q6_K: into ws
- * first); Q4_K with M > 8: x is rounded to bf16 into ws and the bf16 MFMA GEMM runs.
+ * w_dtype: one of the six GGUF formats Light fuses: HQ_Q4_0, HQ_Q5_0, HQ_Q8_0, HQ_Q4_K,
+ * HQ_Q5_K or HQ_Q6_K.  K must be a multiple of the block size.
+ *  - M <= 8, Q4_K / Q5_K: the persistent int8-dot GEMV, x quantized to q8_1 inside its
+ *    workgroups (K > 8192: into ws first).
+ *  - M <= 8, Q8_0 / Q4_0 / Q5_0 / Q6_K: the LDS-staged int8-dot GEMV (x quantized in its
+ *    workgroups up to K = 8192, into ws above).
+ *  - M > 8 (K % 64 == 0): the bf16 MFMA GEMM; x is rounded to bf16 in ws; Q4_K tiles are
+ *    dequantized inside the GEMM, the other formats once to a bf16 copy in ws.
+ *  - Rows that are not 16-byte aligned: a generic F32 GEMV with the bit-exact decoder.
  * Replaces registry kernel "matmul_q" (ops/matmul_q.go:61-75; CUDA launcher
  * kernels/cuda/matmul_q.go:44-91) and, since it serves every M, the M >= 8
  * dequant + cuBLAS fallback (ops/matmul_q.go:52-59, 85-95). */
 int hq_matmul_q(const float *x, const void *w, float *out, int64_t M, int64_t N, int64_t K, int w_dtype,
                 void *ws, size_t ws_bytes, hq_stream_t stream);
+
+/* Frees the library-owned workspaces (ws == NULL calls) after a device synchronisation on
+ * each device that has one.  The caller guarantees that no call or captured graph that
+ * used them still runs.  cudart has no counterpart: Light's op scratch lives in its Go
+ * storage pool (storage/cuda.go:115-245). */
+int hq_workspace_release(void);
 
 /* Gated MLP projection (the SwiGLU / GeGLU decode step):
  *   out (M, N) F32 = act(x @ dequant(wg)^T) * (x @ dequant(wu)^T),
@@ -117,6 +130,18 @@ enum { HQ_ACT_SILU = 0, HQ_ACT_GELU_ERF = 1 };
 size_t hq_matmul_q_gated_ws_bytes(int64_t M, int64_t N, int64_t K, int w_dtype);
 int hq_matmul_q_gated(const float *x, const void *wg, const void *wu, float *out, int64_t M, int64_t N, int64_t K,
                       int w_dtype, int act, void *ws, size_t ws_bytes, hq_stream_t stream);
+
+/* Gated projection that emits prepared activations for the next matmul:
+ *   act_out (hq_act_bytes(M, N) bytes) = quantize_act(act(x @ dequant(wg)^T) * (x @ dequant(wu)^T)),
+ * the same values hq_quantize_act would write for the F32 gated output.  N % 32 == 0.
+ * For Q4_K / Q5_K with M <= 8 this is one kernel: the gated GEMV quantizes each completed
+ * 32-row chunk of its output in the epilogue (the first launch of hq_mlp_q).  Other cases
+ * run hq_matmul_q_gated into ws, then the quantizer.  Feed act_out to hq_matmul_q_act (the
+ * down projection).  Light: models/llama.go:1306-1328 (gate, up, SiLU * up before
+ * DownProj); no counterpart op in Light. */
+size_t hq_matmul_q_gated_act_ws_bytes(int64_t M, int64_t N, int64_t K, int w_dtype);
+int hq_matmul_q_gated_act(const float *x, const void *wg, const void *wu, void *act_out, int64_t M, int64_t N,
+                          int64_t K, int w_dtype, int act, void *ws, size_t ws_bytes, hq_stream_t stream);
 
 /* The gated MLP block of a decoder layer:
  *   out (M, H) F32 = (act(x @ dequant(wg)^T) * (x @ dequant(wu)^T)) @ dequant(wd)^T

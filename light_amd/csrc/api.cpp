@@ -4,6 +4,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <map>
 #include <mutex>
 #include <string>
@@ -33,29 +34,55 @@ int check(hipError_t e, const char *call) {
 
 hipStream_t resolve(hq_stream_t s) { return s ? (hipStream_t)s : g_current; }
 
-// Per-device workspace, grown on demand.  Growing frees the old buffer after a
-// device sync so no in-flight kernel still reads it.
+// Library-owned workspace for calls made with ws == NULL, one buffer per (device, stream):
+// work on one stream runs in order, so a stream's buffer is never used by two kernels at
+// once, while calls on different streams get different buffers.  A buffer that has to grow
+// is replaced, and the old one is retired, not freed: a kernel enqueued from another thread,
+// or a graph captured earlier, may still hold its address.  Retired buffers are freed by
+// hq_workspace_release() (after a device synchronisation) or at process exit.
 static std::mutex g_ws_mu;
-static std::map<int, std::pair<void *, size_t>> g_ws;
+static std::map<std::pair<int, hipStream_t>, std::pair<void *, size_t>> g_ws;
+static std::vector<std::pair<int, void *>> g_ws_retired;
 
 int workspace(size_t bytes, hipStream_t stream, void **out, const char *call) {
   int dev = 0;
   if (int rc = check(hipGetDevice(&dev), call)) return rc;
   std::lock_guard<std::mutex> lk(g_ws_mu);
-  auto &slot = g_ws[dev];
+  auto &slot = g_ws[{dev, stream}];
   if (slot.second < bytes) {
-    if (slot.first) {
-      if (int rc = check(hipDeviceSynchronize(), call)) return rc;
-      if (int rc = check(hipFree(slot.first), call)) return rc;
-      slot = {nullptr, 0};
-    }
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (stream && hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+      return fail(HQ_EUNSUPPORTED, call,
+                  "stream is capturing and the library workspace must grow to %zu bytes: pass a workspace", bytes);
     size_t cap = bytes < (1u << 20) ? (1u << 20) : bytes + bytes / 4;
     void *p = nullptr;
     if (hipMalloc(&p, cap) != hipSuccess) return fail(HQ_ENOMEM, call, "workspace of %zu bytes", cap);
+    if (slot.first) g_ws_retired.push_back({dev, slot.first});
     slot = {p, cap};
   }
   *out = slot.first;
   return HQ_OK;
+}
+
+int workspace_release() {
+  std::lock_guard<std::mutex> lk(g_ws_mu);
+  int rc = HQ_OK, cur = 0;
+  if (int e = check(hipGetDevice(&cur), "hq_workspace_release")) return e;
+  auto drop = [&](int dev, void *p) {
+    if (rc) return;
+    rc = check(hipSetDevice(dev), "hipSetDevice");
+    if (!rc) rc = check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    if (!rc) rc = check(hipFree(p), "hipFree");
+  };
+  for (auto &r : g_ws_retired) drop(r.first, r.second);
+  for (auto &kv : g_ws)
+    if (kv.second.first) drop(kv.first.first, kv.second.first);
+  if (!rc) {
+    g_ws_retired.clear();
+    g_ws.clear();
+  }
+  (void)hipSetDevice(cur);
+  return rc;
 }
 
 // ---- trace spans ----
@@ -86,6 +113,16 @@ TraceSpan::~TraceSpan() {
 }  // namespace hq
 
 using namespace hq;
+
+// Byte fill: `head` bytes up to 16-byte alignment, n16 16-byte stores, then `tail` bytes.
+__global__ void fill_bytes_kernel(unsigned char *dst, size_t head, size_t n16, size_t tail, uint32_t b) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  const size_t t0 = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  uint4 *v = reinterpret_cast<uint4 *>(dst + head);
+  for (size_t i = t0; i < n16; i += stride) v[i] = make_uint4(b, b, b, b);
+  for (size_t i = t0; i < head; i += stride) dst[i] = (unsigned char)b;
+  for (size_t i = t0; i < tail; i += stride) dst[head + n16 * 16 + i] = (unsigned char)b;
+}
 
 extern "C" {
 
@@ -125,7 +162,18 @@ int hq_memcpy_d2d(void *dst, const void *src, size_t bytes, hq_stream_t s) {
 }
 
 int hq_memset(void *dst, int value, size_t bytes, hq_stream_t s) {
-  return check(hipMemsetAsync(dst, value, bytes, resolve(s)), "hipMemsetAsync");
+  if (bytes == 0) return HQ_OK;
+  if (!dst) return fail(HQ_EINVAL, "hq_memset", "dst is NULL");
+  // A fill kernel rather than hipMemsetAsync: memset nodes recorded into captured graphs
+  // are not reliable on replay, and callers may capture this.
+  const unsigned char *p = static_cast<const unsigned char *>(dst);
+  const size_t head = std::min(bytes, (size_t)((16 - ((uintptr_t)p & 15)) & 15));
+  const size_t n16 = (bytes - head) / 16, tail = bytes - head - n16 * 16;
+  const uint32_t b = (uint32_t)(value & 0xff) * 0x01010101u;
+  const size_t work = n16 + head + tail;
+  const unsigned blocks = (unsigned)std::min<size_t>((work + 255) / 256, 65536);
+  fill_bytes_kernel<<<blocks, 256, 0, resolve(s)>>>(static_cast<unsigned char *>(dst), head, n16, tail, b);
+  return check_launch("hq_memset");
 }
 
 int hq_stream_create(hq_stream_t *stream) {
@@ -225,6 +273,8 @@ int hq_matmul_q(const float *x, const void *w, float *out, int64_t M, int64_t N,
   return launch_matmul_q(x, w, out, M, N, K, w_dtype, ws, s);
 }
 
+int hq_workspace_release(void) { return workspace_release(); }
+
 size_t hq_matmul_q_gated_ws_bytes(int64_t M, int64_t N, int64_t K, int w_dtype) {
   return matmul_q_gated_ws_bytes(M, N, K, w_dtype);
 }
@@ -252,6 +302,36 @@ int hq_matmul_q_gated(const float *x, const void *wg, const void *wu, float *out
   }
   TraceSpan span("matmul_q_gated", s);
   return launch_matmul_q_gated(x, wg, wu, out, M, N, K, w_dtype, act, ws, s);
+}
+
+size_t hq_matmul_q_gated_act_ws_bytes(int64_t M, int64_t N, int64_t K, int w_dtype) {
+  return matmul_q_gated_act_ws_bytes(M, N, K, w_dtype);
+}
+
+int hq_matmul_q_gated_act(const float *x, const void *wg, const void *wu, void *act_out, int64_t M, int64_t N,
+                          int64_t K, int w_dtype, int act, void *ws, size_t ws_bytes, hq_stream_t stream) {
+  const char *call = "hq_matmul_q_gated_act";
+  if (!is_gguf(w_dtype)) return fail(HQ_EUNSUPPORTED, call, "weight dtype %d has no fused kernel", w_dtype);
+  if (act != HQ_ACT_SILU && act != HQ_ACT_GELU_ERF) return fail(HQ_EINVAL, call, "activation %d", act);
+  if (M < 0 || N < 0 || K <= 0 || N % 32)
+    return fail(HQ_EINVAL, call, "bad shape M=%lld N=%lld K=%lld (N must be a multiple of 32)", (long long)M,
+                (long long)N, (long long)K);
+  BlockInfo bi = block_info(w_dtype);
+  if (K % bi.elems)
+    return fail(HQ_EINVAL, call, "K=%lld not a multiple of block size %d", (long long)K, bi.elems);
+  if (M == 0 || N == 0) return HQ_OK;
+  if (!x || !wg || !wu || !act_out) return fail(HQ_EINVAL, call, "NULL pointer");
+  if (((uintptr_t)x & 15) || ((uintptr_t)wg & 15) || ((uintptr_t)wu & 15) || ((uintptr_t)act_out & 15))
+    return fail(HQ_EINVAL, call, "x, wg, wu and act_out must be 16-byte aligned");
+  hipStream_t s = resolve(stream);
+  size_t need = matmul_q_gated_act_ws_bytes(M, N, K, w_dtype);
+  if (!ws) {
+    if (int rc = workspace(need, s, &ws, call)) return rc;
+  } else if (ws_bytes < need) {
+    return fail(HQ_ENOMEM, call, "workspace %zu bytes < %zu needed", ws_bytes, need);
+  }
+  TraceSpan span("matmul_q_gated_act", s);
+  return launch_matmul_q_gated_act(x, wg, wu, static_cast<uint8_t *>(act_out), M, N, K, w_dtype, act, ws, s);
 }
 
 size_t hq_mlp_q_ws_bytes(int64_t M, int64_t H, int64_t I, int w_dtype) { return mlp_q_ws_bytes(M, H, I, w_dtype); }

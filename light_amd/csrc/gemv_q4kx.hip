@@ -1062,22 +1062,42 @@ size_t mlp_q_ws_bytes(int64_t M, int64_t H, int64_t I, int dt) {
   return std::max(fused, unfused);
 }
 
+size_t matmul_q_gated_act_ws_bytes(int64_t M, int64_t N, int64_t K, int dt) {
+  if (M <= 0 || N <= 0 || K <= 0 || N % 32 || K % 32) return 0;
+  return (size_t)al256(4 * M * N) + matmul_q_gated_ws_bytes(M, N, K, dt);
+}
+
+// Gated projection whose output is written as prepared activations (act layout of (M, N)).
+// Q4_K / Q5_K, M <= 8, aligned, with teams that tile 32-row chunks: one kernel (the gated
+// GEMV quantizes its own 32-row output chunks in the epilogue).  Otherwise the gated
+// projection runs into ws as F32 and a quantize launch follows.
+int launch_matmul_q_gated_act(const float *x, const void *wg, const void *wu, uint8_t *aout, int64_t M, int64_t N,
+                              int64_t K, int dt, int act, void *ws, hipStream_t s) {
+  int P, TP, RW;
+  if (N % 256 == 0 && q4kx_ok(M, N, K, wg, wu, x, dt) && q4kx_geom(K, 256, &P, &TP, &RW) && 32 % RW == 0) {
+    Q4kxArgs a;
+    if (int rc = q4kx_setup(a, M, N, K, 256, K / 256 * block_info(dt).bytes, "matmul_q_gated_act")) return rc;
+    a.x = x;
+    a.w0 = static_cast<const uint8_t *>(wg);
+    a.w1 = static_cast<const uint8_t *>(wu);
+    a.aout = aout;
+    a.act = act;
+    return with_qk_unit(dt, K, [&](auto unit) { return dispatch_q4kx<decltype(unit), true, true, true>(a, s); });
+  }
+  float *h = static_cast<float *>(ws);
+  void *inner = static_cast<char *>(ws) + al256(4 * M * N);
+  if (int rc = launch_matmul_q_gated(x, wg, wu, h, M, N, K, dt, act, inner, s)) return rc;
+  return launch_quantize_act(h, F32, aout, M, N, s);
+}
+
 int launch_mlp_q(const float *x, const void *wg, const void *wu, const void *wd, float *out, int64_t M, int64_t H,
                  int64_t I, int dt, int act, void *ws, hipStream_t s) {
   if (mlp_fused_ok(M, H, I, dt, wg, wu, wd, x)) {
     // Launch 1: gated gate/up on x, output quantized straight into ws (act layout of (M, I)).
-    Q4kxArgs a;
-    if (int rc = q4kx_setup(a, M, I, H, 256, H / 256 * block_info(dt).bytes, "mlp_q")) return rc;
-    a.x = x;
-    a.w0 = static_cast<const uint8_t *>(wg);
-    a.w1 = static_cast<const uint8_t *>(wu);
-    a.aout = static_cast<uint8_t *>(ws);
-    a.act = act;
-    const int rc =
-        with_qk_unit(dt, H, [&](auto unit) { return dispatch_q4kx<decltype(unit), true, true, true>(a, s); });
-    if (rc) return rc;
+    auto *h = static_cast<uint8_t *>(ws);
+    if (int rc = launch_matmul_q_gated_act(x, wg, wu, h, M, I, H, dt, act, nullptr, s)) return rc;
     // Launch 2: down projection on the prepared h.
-    return launch_gemv_q4kx_act(ws, wd, out, M, H, I, dt, s);
+    return launch_gemv_q4kx_act(h, wd, out, M, H, I, dt, s);
   }
   float *h = static_cast<float *>(ws);
   void *inner = static_cast<char *>(ws) + al256(4 * M * I);

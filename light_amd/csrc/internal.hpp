@@ -17,6 +17,8 @@ inline int check_launch(const char *call) { return check(hipGetLastError(), call
 hipStream_t resolve(hq_stream_t s);
 // Library-owned, grow-on-demand device workspace of the current device.
 int workspace(size_t bytes, hipStream_t stream, void **out, const char *call);
+// Frees every library-owned workspace (hq_workspace_release).
+int workspace_release();
 
 // Trace span: brackets one op call with HIP events while hq_trace_start is active.
 struct TraceSpan {
@@ -78,6 +80,9 @@ int launch_gemv_int4x(const void *x, int x_dtype, const uint32_t *codes, const f
 // Whether the decode GEMVs quantize x inside their workgroups at this K.
 bool q4kx_xin(int64_t K);
 size_t matmul_q_gated_ws_bytes(int64_t M, int64_t N, int64_t K, int dt);
+size_t matmul_q_gated_act_ws_bytes(int64_t M, int64_t N, int64_t K, int dt);
+int launch_matmul_q_gated_act(const float *x, const void *wg, const void *wu, uint8_t *aout, int64_t M, int64_t N,
+                              int64_t K, int dt, int act, void *ws, hipStream_t s);
 size_t mlp_q_ws_bytes(int64_t M, int64_t H, int64_t I, int dt);
 int launch_mlp_q(const float *x, const void *wg, const void *wu, const void *wd, float *out, int64_t M, int64_t H,
                  int64_t I, int dt, int act, void *ws, hipStream_t s);

@@ -20,6 +20,7 @@ NAMES = {F16: "F16", BF16: "BF16", F32: "F32", Q4_0: "Q4_0", Q5_0: "Q5_0", Q8_0:
          Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K"}
 
 HQ_OK, HQ_EINVAL, HQ_EUNSUPPORTED, HQ_ENOMEM = 0, -1, -2, -3
+ACT_SILU, ACT_GELU_ERF = 0, 1
 
 
 class HipqError(RuntimeError):
@@ -55,8 +56,11 @@ SIGNATURES = {
     "hq_trace_stop": (_I, [ctypes.c_char_p, ctypes.POINTER(_I), ctypes.POINTER(ctypes.c_double), _I]),
     "hq_matmul_q_ws_bytes": (_SZ, [_I64, _I64, _I64, _I]),
     "hq_matmul_q": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _P, _SZ, _P]),
+    "hq_workspace_release": (_I, []),
     "hq_matmul_q_gated_ws_bytes": (_SZ, [_I64, _I64, _I64, _I]),
     "hq_matmul_q_gated": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _P, _SZ, _P]),
+    "hq_matmul_q_gated_act_ws_bytes": (_SZ, [_I64, _I64, _I64, _I]),
+    "hq_matmul_q_gated_act": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _P, _SZ, _P]),
     "hq_mlp_q_ws_bytes": (_SZ, [_I64, _I64, _I64, _I]),
     "hq_mlp_q": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _P, _SZ, _P]),
     "hq_act_bytes": (_SZ, [_I64, _I64]),
@@ -144,7 +148,16 @@ def matmul_q(x, w, N, K, w_dtype, out=None, ws=None, stream=None):
     return out
 
 
-ACT_SILU, ACT_GELU_ERF = 0, 1
+def matmul_q_gated_act(x, wg, wu, N, K, w_dtype, act=ACT_SILU, out=None, ws=None, stream=None):
+    """Prepared activations (uint8, hq_act_bytes(M, N)) of act(x @ dequant(wg)^T) * (x @ dequant(wu)^T)."""
+    import torch
+    M = x.shape[0]
+    if out is None:
+        out = torch.empty(lib().hq_act_bytes(M, N), dtype=torch.uint8, device=x.device)
+    ws_bytes = 0 if ws is None else ws.numel() * ws.element_size()
+    check(lib().hq_matmul_q_gated_act(_ptr(x), _ptr(wg), _ptr(wu), _ptr(out), M, N, K, w_dtype, act, _ptr(ws),
+                                      ws_bytes, _stream(stream)))
+    return out
 
 
 def matmul_q_gated(x, wg, wu, N, K, w_dtype, act=ACT_SILU, out=None, ws=None, stream=None):

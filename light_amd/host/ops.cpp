@@ -26,14 +26,39 @@ Tensor MatMulQ(const Tensor &x, const Tensor &w) {
   if (K % BlockElems(w.dtype()))
     Fail("MatMulQ: K=%lld not a multiple of %s block size %d", (long long)K, DTypeName(w.dtype()),
          BlockElems(w.dtype()));
-  // Light's CUDA-only M >= MatMulQDequantMinRows fallback (:52-59) does not apply: the
-  // ROCm kernel serves every M (GEMV for decode, MFMA GEMM for prefill).
-  Kernel k = Lookup(Key{"matmul_q", x.device().kind, w.dtype()});
+  // ensureContig (:48-51) is the identity here: this layer's tensors are always dense
+  // row-major (Tensor has no strides).  Light's CUDA-only M >= MatMulQDequantMinRows
+  // fallback (:52-59) does not apply: the ROCm kernel serves every M (GEMV for decode, MFMA
+  // GEMM for prefill).  A dtype with no fused kernel takes matMulQFallback (:61-71).
+  Kernel k;
+  try {
+    k = Lookup(Key{"matmul_q", x.device().kind, w.dtype()});
+  } catch (const Error &e) {
+    if (!e.IsKernelNotFound()) throw;
+    return MatMulQFallback(x, w);
+  }
   Tensor out = Tensor::Empty(DType::F32, {M, N}, x.device());
   Context ctx;
   ctx.inputs = {x, w};
   ctx.output = out;
   k(ctx);
+  return out;
+}
+
+// matMulQFallback (ops/matmul_q.go:85-95): quant.Dequantize, then the ordinary F32 matmul
+// out = x . wf^T through the registry's "matmul" key.  This library registers neither a
+// dequant for the formats without a fused kernel nor an F32 matmul, so on ROCm the
+// fallback ends in the registry's kernel-not-found error, as Light's does on a device
+// whose backend lacks those kernels.
+Tensor MatMulQFallback(const Tensor &x, const Tensor &w) {
+  Tensor wf = Dequantize(w);
+  Kernel mm = Lookup(Key{"matmul", x.device().kind, DType::F32});
+  Tensor out = Tensor::Empty(DType::F32, {x.Dim(0), w.Dim(0)}, x.device());
+  Context ctx;
+  ctx.inputs = {x, wf};
+  ctx.output = out;
+  ctx.attrs = {{"transpose_b", Attr::Bool(true)}};
+  mm(ctx);
   return out;
 }
 

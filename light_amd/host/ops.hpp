@@ -15,6 +15,8 @@ namespace ops {
 
 // ops.MatMulQ (ops/matmul_q.go:14-76): x F32 (M, K) times a GGUF-quantized weight (N, K)^T -> F32 (M, N).
 Tensor MatMulQ(const Tensor &x, const Tensor &w);
+// matMulQFallback (ops/matmul_q.go:85-95): Dequantize, then the registry's F32 "matmul".
+Tensor MatMulQFallback(const Tensor &x, const Tensor &w);
 // ops.MatMulQFusedOn (ops/matmul_q.go:102-106).
 bool MatMulQFusedOn(DeviceKind kind, DType dt);
 // Gated projection on quantized weights: act(x . wg^T) * (x . wu^T), act = SiLU or GELU (erf)

@@ -102,3 +102,4 @@ def test_check_raises_with_message():
     with pytest.raises(hipq.HipqError) as e:
         hipq.check(_matmul_q(1, 4, 100, hipq.Q4_K))
     assert e.value.code == hipq.HQ_EINVAL
+

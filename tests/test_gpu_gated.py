@@ -133,3 +133,25 @@ def test_mlp_repeated_calls_agree(dev):
                 first[M] = y.clone()
             else:
                 assert torch.equal(y, first[M]), (rep, M)
+
+
+@pytest.mark.parametrize("dt,M,H,I", [(hipq.Q4_K, 1, 4096, 14336), (hipq.Q4_K, 3, 1024, 2816),
+                                      (hipq.Q5_K, 2, 1024, 2816), (hipq.Q8_0, 1, 512, 768)])
+def test_gated_act_then_down_equals_mlp(dev, dt, M, H, I):
+    """hq_matmul_q_gated_act followed by hq_matmul_q_act is hq_mlp_q split at its kernel
+    boundary: the same launches, so the same bits (the unfused formats run the same
+    gated-then-quantize sequence too)."""
+    print(f"[case] gated_act+down dt={hipq.NAMES[dt]} M={M} H={H} I={I}", flush=True)
+    g = synth.rng(4000 + dt + M)
+    t = lambda a: torch.from_numpy(a).to(dev)
+    wg, wu, wd = (t(synth.gguf_weight(dt, r, c, g)) for r, c in ((I, H), (I, H), (H, I)))
+    x = t(synth.activations(M, H, g))
+    want = hipq.mlp_q(x, wg, wu, wd, H, I, dt, act=hipq.ACT_SILU)
+    act = hipq.matmul_q_gated_act(x, wg, wu, I, H, dt, act=hipq.ACT_SILU)
+    got = hipq.matmul_q_act(act, wd, M, H, I, dt)
+    torch.cuda.synchronize()
+    if dt in (hipq.Q4_K, hipq.Q5_K):
+        assert torch.equal(got, want)
+    else:  # mlp_q's unfused path feeds F32 h to hq_matmul_q; here h is quantized first
+        scale = want.abs().max().item()
+        assert (got - want).abs().max().item() <= 1e-3 * scale

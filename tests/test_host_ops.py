@@ -87,7 +87,18 @@ def test_matmul_q_validation():
         L.matmul_q(x, q("Q4_K", 8, 512))
     with pytest.raises(L.Error, match="MatMulQ: K=288 not a multiple of Q4_K block size 256"):
         L.matmul_q(f32(1, 288), q("Q4_K", 8, 288))
-    with pytest.raises(L.KernelNotFound, match="matmul_q/CPU/Q4_K"):
+    # No fused CPU kernel: MatMulQ takes matMulQFallback (ops/matmul_q.go:61-71), whose
+    # Dequantize finds no CPU "dequant" kernel in this build.
+    with pytest.raises(L.KernelNotFound, match="^registry: kernel not found: dequant/CPU/Q4_K$"):
+        L.matmul_q(x, w)
+
+
+def test_matmul_q_falls_back_for_unfused_formats():
+    """A format with no fused kernel (Q3_K) goes through the dequant + matmul fallback rather
+    than failing on the matmul_q lookup (ops/matmul_q.go:65-71)."""
+    x = f32(1, 256)
+    w = q("Q3_K", 4, 256)
+    with pytest.raises(L.KernelNotFound, match="^registry: kernel not found: dequant/CPU/Q3_K$"):
         L.matmul_q(x, w)
 
 
