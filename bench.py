@@ -22,6 +22,7 @@ Inputs are synthetic (seeded, BASELINE distributions) and resident in HBM; every
 rotated over enough copies that the working set exceeds the 256 MB Infinity Cache.
 
 Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--table] [--no-cpu]
+"""
 import argparse
 import json
 import math

@@ -24,7 +24,7 @@
  *    ws == NULL makes the library use a buffer per (device, stream) that it
  *    allocates and grows on demand; growing retires the old buffer without
  *    freeing it (hq_workspace_release frees them).  During stream capture a
- *    growth fails with HQ_EUNSUPPORTED: pass ws.
+ *    growth fails with HQ_EUNSUPPORTED: pass ws, or use hq_matmul_q_noalloc.
  */
 #ifndef HIPQ_H
 #define HIPQ_H
@@ -110,6 +110,20 @@ size_t hq_matmul_q_ws_bytes(int64_t M, int64_t N, int64_t K, int w_dtype);
  * dequant + cuBLAS fallback (ops/matmul_q.go:52-59, 85-95). */
 int hq_matmul_q(const float *x, const void *w, float *out, int64_t M, int64_t N, int64_t K, int w_dtype,
                 void *ws, size_t ws_bytes, hq_stream_t stream);
+
+/* Allocation-free hq_matmul_q: the same kernels and results, with the scratch taken from a
+ * device array of HQ_NOALLOC_SCRATCH_BYTES that the library holds on each GPU it runs on
+ * (a static device symbol, present from module load until the process ends).  Calls no
+ * hipMalloc / hipFree, so it may be used under HIP graph capture, in serving loops, and by
+ * harnesses that forbid allocation.  Returns HQ_ENOMEM when hq_matmul_q_ws_bytes(M, N, K,
+ * w_dtype) exceeds HQ_NOALLOC_SCRATCH_BYTES (decode GEMVs need kilobytes; the Q4_K GEMM
+ * needs 2*M*K bytes plus split-K partials, e.g. M = 512, K = 14336 fits).  Every call on a
+ * GPU shares that GPU's scratch: calls that overlap on one GPU (two streams, or two
+ * threads) race; serialise them.  No counterpart in Light: it is for callers that cannot
+ * allocate. */
+#define HQ_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int hq_matmul_q_noalloc(const float *x, const void *w, float *out, int64_t M, int64_t N, int64_t K, int w_dtype,
+                        hq_stream_t stream);
 
 /* Frees the library-owned workspaces (ws == NULL calls) after a device synchronisation on
  * each device that has one.  The caller guarantees that no call or captured graph that

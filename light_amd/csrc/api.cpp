@@ -85,6 +85,29 @@ int workspace_release() {
   return rc;
 }
 
+// ---- allocation-free scratch ----
+// hq_matmul_q_noalloc's scratch: a file-scope device array that every GPU the library runs
+// on holds until the process ends.  Host code never passes `scratch` itself to a kernel (on
+// the host the name is only a stand-in); it uses the device address that
+// hipGetSymbolAddress returns, looked up once per device.
+static __device__ __align__(256) unsigned char scratch[HQ_NOALLOC_SCRATCH_BYTES];
+static std::mutex g_scr_mu;
+static std::map<int, void *> g_scr;
+
+static int scratch_ptr(void **out, const char *call) {
+  int dev = 0;
+  if (int rc = check(hipGetDevice(&dev), call)) return rc;
+  std::lock_guard<std::mutex> lk(g_scr_mu);
+  auto it = g_scr.find(dev);
+  if (it == g_scr.end()) {
+    void *p = nullptr;
+    if (int rc = check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress")) return rc;
+    it = g_scr.emplace(dev, p).first;
+  }
+  *out = it->second;
+  return HQ_OK;
+}
+
 // ---- trace spans ----
 struct TraceRec {
   int calls = 0;
@@ -269,6 +292,30 @@ int hq_matmul_q(const float *x, const void *w, float *out, int64_t M, int64_t N,
   } else if (ws_bytes < need) {
     return fail(HQ_ENOMEM, call, "workspace %zu bytes < %zu needed", ws_bytes, need);
   }
+  TraceSpan span(matmul_q_kernel_name(M, w_dtype), s);
+  return launch_matmul_q(x, w, out, M, N, K, w_dtype, ws, s);
+}
+
+int hq_matmul_q_noalloc(const float *x, const void *w, float *out, int64_t M, int64_t N, int64_t K, int w_dtype,
+                        hq_stream_t stream) {
+  const char *call = "hq_matmul_q_noalloc";
+  if (!is_gguf(w_dtype)) return fail(HQ_EUNSUPPORTED, call, "weight dtype %d has no fused kernel", w_dtype);
+  if (M < 0 || N < 0 || K <= 0) return fail(HQ_EINVAL, call, "bad shape M=%lld N=%lld K=%lld", (long long)M,
+                                            (long long)N, (long long)K);
+  BlockInfo bi = block_info(w_dtype);
+  if (K % bi.elems)
+    return fail(HQ_EINVAL, call, "K=%lld not a multiple of block size %d", (long long)K, bi.elems);
+  if (M == 0 || N == 0) return HQ_OK;
+  if (!x || !w || !out) return fail(HQ_EINVAL, call, "NULL pointer");
+  if (((uintptr_t)x & 15) || ((uintptr_t)w & 15) || ((uintptr_t)out & 3))
+    return fail(HQ_EINVAL, call, "x and w must be 16-byte aligned, out 4-byte aligned");
+  size_t need = matmul_q_ws_bytes(M, N, K, w_dtype);
+  if (need > HQ_NOALLOC_SCRATCH_BYTES)
+    return fail(HQ_ENOMEM, call, "needs %zu bytes of scratch, more than the %zu-byte static scratch", need,
+                (size_t)HQ_NOALLOC_SCRATCH_BYTES);
+  void *ws = nullptr;
+  if (int rc = scratch_ptr(&ws, call)) return rc;
+  hipStream_t s = resolve(stream);
   TraceSpan span(matmul_q_kernel_name(M, w_dtype), s);
   return launch_matmul_q(x, w, out, M, N, K, w_dtype, ws, s);
 }

@@ -56,6 +56,7 @@ SIGNATURES = {
     "hq_trace_stop": (_I, [ctypes.c_char_p, ctypes.POINTER(_I), ctypes.POINTER(ctypes.c_double), _I]),
     "hq_matmul_q_ws_bytes": (_SZ, [_I64, _I64, _I64, _I]),
     "hq_matmul_q": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _P, _SZ, _P]),
+    "hq_matmul_q_noalloc": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _P]),
     "hq_workspace_release": (_I, []),
     "hq_matmul_q_gated_ws_bytes": (_SZ, [_I64, _I64, _I64, _I]),
     "hq_matmul_q_gated": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _P, _SZ, _P]),
@@ -158,6 +159,21 @@ def matmul_q_gated_act(x, wg, wu, N, K, w_dtype, act=ACT_SILU, out=None, ws=None
     check(lib().hq_matmul_q_gated_act(_ptr(x), _ptr(wg), _ptr(wu), _ptr(out), M, N, K, w_dtype, act, _ptr(ws),
                                       ws_bytes, _stream(stream)))
     return out
+
+
+def matmul_q_noalloc(x, w, N, K, w_dtype, out=None, stream=None):
+    """hq_matmul_q on the library's static device scratch (no allocation inside the call)."""
+    import torch
+    M = x.shape[0]
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float32, device=x.device)
+    check(lib().hq_matmul_q_noalloc(_ptr(x), _ptr(w), _ptr(out), M, N, K, w_dtype, _stream(stream)))
+    return out
+
+
+NOALLOC_SCRATCH_BYTES = 64 << 20
+
+
 
 
 def matmul_q_gated(x, wg, wu, N, K, w_dtype, act=ACT_SILU, out=None, ws=None, stream=None):

@@ -103,3 +103,20 @@ def test_check_raises_with_message():
         hipq.check(_matmul_q(1, 4, 100, hipq.Q4_K))
     assert e.value.code == hipq.HQ_EINVAL
 
+
+def test_matmul_q_noalloc_validates_before_any_device_call():
+    """The allocation-free entry point checks arguments and its static scratch limit first."""
+    L = hipq.lib()
+    assert L.hq_matmul_q_noalloc(1 << 12, 1 << 12, 1 << 12, 1, 4, 256, hipq.F32, None) == hipq.HQ_EUNSUPPORTED
+    assert L.hq_matmul_q_noalloc(1 << 12, 1 << 12, 1 << 12, 1, 4, 255, hipq.Q4_K, None) == hipq.HQ_EINVAL
+    assert L.hq_matmul_q_noalloc(1 << 12, 1 << 12, 1 << 12, 0, 4, 256, hipq.Q4_K, None) == hipq.HQ_OK
+    assert L.hq_matmul_q_noalloc(None, 1 << 12, 1 << 12, 1, 4, 256, hipq.Q4_K, None) == hipq.HQ_EINVAL
+    # M = 4096, K = 14336 needs 117 MB of bf16 x alone: beyond the 64 MiB scratch.
+    need = L.hq_matmul_q_ws_bytes(4096, 4096, 14336, hipq.Q4_K)
+    assert need > hipq.NOALLOC_SCRATCH_BYTES
+    rc = L.hq_matmul_q_noalloc(1 << 12, 1 << 12, 1 << 12, 4096, 4096, 14336, hipq.Q4_K, None)
+    assert rc == hipq.HQ_ENOMEM
+    assert "static scratch" in hipq.last_error()
+    # The benchmark's M = 512 prefill shapes and every decode shape fit.
+    for M, N, K in ((512, 14336, 4096), (512, 4096, 14336), (1, 128256, 4096), (8, 4096, 14336)):
+        assert L.hq_matmul_q_ws_bytes(M, N, K, hipq.Q4_K) <= hipq.NOALLOC_SCRATCH_BYTES, (M, N, K)
