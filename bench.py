@@ -361,7 +361,8 @@ def moe_rows(c, name, g, dev, cpu=False):
             row.update(cpu_us=round(t * 1e6, 1), cpu_threads=th, cpu_sample=smp, gpu_over_cpu=round(t * 1e6 / us, 1))
         out.append(row)
     # The whole routed block on the device: router probs -> hq_moe_route -> gated gate/up
-    # (SiLU * up) -> down (routing-weighted) -> combine.  Probs rotate over 16 draws.
+    # (SiLU * up) -> down (routing-weighted) with the combine in its epilogue.  Probs rotate
+    # over 16 draws.
     probs = []
     for _ in range(16):
         lg = torch.from_numpy(g.standard_normal((T, E)).astype(np.float32))
@@ -369,12 +370,13 @@ def moe_rows(c, name, g, dev, cpu=False):
     hg = torch.zeros((M, I), device=dev)
     ws_g = torch.empty(max(hipq.moe_gemm_q_gated_ws_bytes(M, T, I, H, dt), 256), dtype=torch.uint8, device=dev)
     yb = torch.empty((T, H), device=dev)
+    ws_c = torch.empty(max(hipq.lib().hq_moe_gemm_q_combine_ws_bytes(T, topk, H, I, dt), 256), dtype=torch.uint8,
+                       device=dev)
 
     def block(i):
         _, w, sp, se = hipq.moe_route(probs[i % 16], topk, True)
         hipq.moe_gemm_q_gated(x, wgu, sp, se, E, I, H, dt, topk, out=hg, counts=counts, offsets=offsets, ws=ws_g)
-        hipq.moe_gemm_q(hg, wdn, sp, se, E, H, I, dt, topk, topk_w=w, out=odn, counts=counts, offsets=offsets, ws=ws)
-        hipq.moe_combine(odn, topk, out=yb)
+        hipq.moe_gemm_q_combine(hg, wdn, sp, se, E, H, I, dt, topk, topk_w=w, out=yb, ws=ws_c)
 
     us = time_launches(block, 64, 16)
     used = float(np.mean([len(np.unique(torch.topk(p_, topk, dim=1).indices.cpu().numpy())) for p_ in probs]))

@@ -251,6 +251,20 @@ int hq_moe_gemm_q(const float *x, const void *w, const int64_t *sorted_pairs, co
  * does (bit-identical). */
 int hq_moe_combine(const float *pair_out, float *out, int64_t M, int64_t N, int topk, hq_stream_t stream);
 
+/* The routed down projection with MoECombine in its epilogue:
+ *   y (T, N) F32 = MoECombine(MoEGemmQ(h, w, routing, topk_w, topk), topk),
+ * h F32 (T*topk, K) per pair (row_per_pair), W (E, N, K) GGUF blocks, routing arguments as
+ * hq_moe_gemm_q with size_m = M = T*topk; counts / offsets nullable (written when given).
+ * Bit-identical to hq_moe_gemm_q + hq_moe_combine.  For Q4_K / Q5_K decode one kernel
+ * computes each (token, output row) over the token's topk experts and adds the slots in
+ * slot order; other cases run those two ops through ws.  Light: nn/moe.go:230-235
+ * (MoEGemmQ then MoECombine, ops/moe.go:209-265); no counterpart kernel in Light. */
+size_t hq_moe_gemm_q_combine_ws_bytes(int64_t T, int topk, int64_t N, int64_t K, int w_dtype);
+int hq_moe_gemm_q_combine(const float *h, const void *w, const int64_t *sorted_pairs, const int64_t *sorted_expts,
+                          int32_t *counts, int32_t *offsets, const float *topk_w, float *y, int topk, int64_t T,
+                          int64_t E, int64_t N, int64_t K, int w_dtype, void *ws, size_t ws_bytes,
+                          hq_stream_t stream);
+
 /* On-device MoERoute (ops/moe.go:29-71): probs F32 (T, E) -> topk_ids I64 (T, topk), weights
  * F32 (T*topk) (renormalised per token when normalize != 0: den = left-to-right f32 sum of
  * the k values, then value / den), and the stable expert sort of the T*topk pairs:

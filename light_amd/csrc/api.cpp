@@ -565,6 +565,35 @@ int hq_moe_combine(const float *pair_out, float *out, int64_t M, int64_t N, int 
   return launch_moe_combine(pair_out, out, M / topk, N, topk, s);
 }
 
+size_t hq_moe_gemm_q_combine_ws_bytes(int64_t T, int topk, int64_t N, int64_t K, int w_dtype) {
+  if (T <= 0 || topk < 1 || N <= 0 || K <= 0) return 0;
+  return moe_combine_ws_bytes(T * topk, N, K, w_dtype);
+}
+
+int hq_moe_gemm_q_combine(const float *h, const void *w, const int64_t *sorted_pairs, const int64_t *sorted_expts,
+                          int32_t *counts, int32_t *offsets, const float *topk_w, float *y, int topk, int64_t T,
+                          int64_t E, int64_t N, int64_t K, int w_dtype, void *ws, size_t ws_bytes,
+                          hq_stream_t stream) {
+  const char *call = "hq_moe_gemm_q_combine";
+  if (!is_gguf(w_dtype)) return fail(HQ_EUNSUPPORTED, call, "weight dtype %d has no fused kernel", w_dtype);
+  if (E <= 0 || N < 0 || K <= 0 || T < 0 || topk < 1) return fail(HQ_EINVAL, call, "bad shape");
+  BlockInfo bi = block_info(w_dtype);
+  if (K % bi.elems) return fail(HQ_EINVAL, call, "K=%lld not a multiple of block size %d", (long long)K, bi.elems);
+  if (T == 0 || N == 0) return HQ_OK;
+  if (!h || !w || !sorted_pairs || !sorted_expts || !y) return fail(HQ_EINVAL, call, "NULL pointer");
+  if (((uintptr_t)h & 15)) return fail(HQ_EINVAL, call, "h must be 16-byte aligned");
+  hipStream_t s = resolve(stream);
+  const size_t need = moe_combine_ws_bytes(T * topk, N, K, w_dtype);
+  if (!ws) {
+    if (int rc = workspace(need, s, &ws, call)) return rc;
+  } else if (ws_bytes < need) {
+    return fail(HQ_ENOMEM, call, "workspace %zu bytes < %zu needed", ws_bytes, need);
+  }
+  TraceSpan span("moe_gemm_q_combine", s);
+  return launch_moe_q_combine(h, w, sorted_pairs, sorted_expts, counts, offsets, topk_w, y, topk, T, E, N, K,
+                              w_dtype, ws, s);
+}
+
 int hq_moe_route(const float *probs, int64_t T, int64_t E, int topk, int normalize, int64_t *topk_ids,
                  float *weights, int64_t *sorted_pairs, int64_t *sorted_expts, int32_t *counts, int32_t *offsets,
                  hq_stream_t stream) {

@@ -818,6 +818,131 @@ __global__ __launch_bounds__(512) void moe_gemv_x_kernel(MoeXArgs ma) {
 }
 
 // ---------------------------------------------------------------------------
+// MoE decode down projection with MoECombine in its epilogue (ops.MoEGemmQ with the routing
+// weights, then ops.MoECombine: ops/moe.go:209-265, nn/moe.go:230-235):
+//   y[t, n] = sum over slots s of w(t,s) * h[t*topk+s] . dequant(W[e(t,s)])[n],
+// the slots added in slot order as Light's Add chain does.  Token-major: grid.y = token, and a
+// workgroup's teams are (row, slot) pairs -- RW / topk rows times topk slots -- so a team keeps
+// one slot's activations in registers for the whole kernel.  Each pair's value is computed by
+// exactly the instruction sequence of moe_gemv_x_kernel (same quantization of h, same unit
+// dot, same 16-lane and team sums, same multiply by w), and the combine adds them in the order
+// of moe_combine_kernel, so y is bit-identical to moe_gemm_q followed by moe_combine.
+// ---------------------------------------------------------------------------
+struct MoeCombArgs {
+  Q4kxArgs g;  // w0 = expert stack (E, N, K); x = F32 h (M, K); out = y (T, N)
+  const int64_t *pairs, *expts;
+  int32_t *counts, *offsets;  // nullable: written by workgroup (0, 0)
+  const float *topk_w;        // nullable
+  int64_t expert_bytes, npairs;
+  int E, topk;
+};
+
+template <class U>
+__global__ __launch_bounds__(512) void moe_down_combine_kernel(MoeCombArgs ma) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  const Q4kxArgs &a = ma.g;
+  const int t = threadIdx.x, lane = t & 63;
+  const int tok = blockIdx.y, topk = ma.topk;
+  const int RW = a.RW, KB = a.K >> 5, RPW = RW / topk;  // rows per workgroup
+  // LDS: act of the token's topk h rows | expert per slot | pair values [RPW][topk]
+  uint8_t *lq1 = smem, *lq2 = smem + (int64_t)topk * a.K;
+  float2 *lde = reinterpret_cast<float2 *>(smem + 2 * (int64_t)topk * a.K);
+  float *lsx = reinterpret_cast<float *>(smem + 2 * (int64_t)topk * a.K + 8 * (int64_t)topk * KB);
+  int *lexp = reinterpret_cast<int *>(smem + q4kx_act_lds(topk, a.K));
+  float *lval = reinterpret_cast<float *>(lexp + 64);
+  if (blockIdx.x == 0 && tok == 0 && ma.offsets) {
+    for (int e = t; e <= ma.E; e += blockDim.x) {
+      auto lower = [&](int64_t v) {
+        int64_t lo = 0, hi = ma.npairs;
+        while (lo < hi) {
+          const int64_t mid = (lo + hi) >> 1;
+          if (ma.expts[mid] < v) lo = mid + 1; else hi = mid;
+        }
+        return lo;
+      };
+      const int64_t o = lower(e);
+      ma.offsets[e] = (int32_t)o;
+      if (e < ma.E && ma.counts) ma.counts[e] = (int32_t)(lower(e + 1) - o);
+    }
+  }
+  // Expert of each of the token's slots, from the expert-sorted pair list (-1: none).
+  if (t < topk) lexp[t] = -1;
+  __syncthreads();
+  for (int64_t i = t; i < ma.npairs; i += blockDim.x) {
+    const int64_t p = ma.pairs[i];
+    if (p >= (int64_t)tok * topk && p < (int64_t)(tok + 1) * topk) lexp[p - (int64_t)tok * topk] = (int)ma.expts[i];
+  }
+  // Quantize the token's topk rows of h into LDS, as moe_gemv_x_kernel does.
+  const int ntask = topk * KB * 8;
+  const float *x = static_cast<const float *>(a.x) + (int64_t)tok * topk * a.K;
+  for (int base = 0; base < ntask; base += (int)blockDim.x) {
+    const int task = base + t < ntask ? base + t : ntask - 1;
+    const int blk = task >> 3, sub = task & 7;
+    const float4 xv = *reinterpret_cast<const float4 *>(x + (int64_t)blk * 32 + sub * 4);
+    const float v[4] = {xv.x, xv.y, xv.z, xv.w};
+    const ActQ q = act_quant8_fast(v);
+    if (base + t < ntask) {
+      reinterpret_cast<uint32_t *>(lq1 + blk * 32)[sub] = q.q1;
+      reinterpret_cast<uint32_t *>(lq2 + blk * 32)[sub] = q.q2;
+      if (sub == 0) {
+        lde[blk] = make_float2(q.d, q.e);
+        lsx[blk] = q.sum;
+      }
+    }
+  }
+  __syncthreads();
+  const int team = t / a.TP, u = t - team * a.TP;
+  const int slot = team % topk, rloc = team / topk;
+  const bool active = u < a.P && rloc < RPW;
+  const typename U::Lane L = unit_lane<U>(active ? u : 0, a.G);
+  int e = lexp[slot];
+  const bool ok = e >= 0 && e < ma.E;
+  e = ok ? e : 0;
+  const int64_t p = (int64_t)tok * topk + slot;
+  const float wp = ma.topk_w ? ma.topk_w[p] : 1.f;
+  typename U::X xr[1];
+  U::load_x(lq1, lq2, reinterpret_cast<const uint8_t *>(lde), reinterpret_cast<const uint8_t *>(lsx),
+            slot * KB + L.ja, xr[0]);
+  const uint8_t *w = a.w0 + (int64_t)e * ma.expert_bytes;
+  const int ngroups = (a.N + RPW - 1) / RPW, G = gridDim.x;
+  const int niter = (ngroups - (int)blockIdx.x + G - 1) / G;
+  typename U::W wr;
+  {
+    int row = (int)blockIdx.x * RPW + rloc;
+    row = row < a.N && rloc < RPW ? row : a.N;
+    U::load(w, a.s0, a.z0, a, row, L, wr);
+  }
+  for (int it = 0; it < niter; it++) {
+    const int grp = (int)blockIdx.x + it * G;
+    float c[1];
+    U::template dot<1>(wr, xr, L, c);
+    {
+      int row = (grp + G) * RPW + rloc;
+      row = row < a.N && rloc < RPW ? row : a.N;
+      U::load(w, a.s0, a.z0, a, row, L, wr);
+    }
+    const float r16 = rsum16(active ? c[0] : 0.f);
+    const float r0 = rl(r16, 0), r1 = rl(r16, 16), r2 = rl(r16, 32), r3 = rl(r16, 48);
+    float tot;
+    if (a.TP == 64)
+      tot = ((r0 + r1) + r2) + r3;
+    else if (a.TP == 32)
+      tot = lane < 32 ? r0 + r1 : r2 + r3;
+    else
+      tot = lane < 16 ? r0 : (lane < 32 ? r1 : (lane < 48 ? r2 : r3));
+    float *vb = lval + (it & 1) * (RPW * topk);
+    if (u == 0 && rloc < RPW) vb[rloc * topk + slot] = ok ? tot * wp : 0.f;
+    __syncthreads();
+    const int row = grp * RPW + t;
+    if (t < RPW && row < a.N) {
+      float acc = vb[t * topk];
+      for (int s2 = 1; s2 < topk; s2++) acc = __fadd_rn(acc, vb[t * topk + s2]);
+      static_cast<float *>(a.out)[(int64_t)tok * a.N + row] = acc;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Launch
 // ---------------------------------------------------------------------------
 
@@ -1167,6 +1292,49 @@ int launch_moe_gemv_x(const float *x, const void *w, const int64_t *pairs, const
   if (avg <= 1) return run_moe_x<Q4kUnit, 1, false>(ma, active, s);
   if (avg <= 2) return run_moe_x<Q4kUnit, 2, false>(ma, active, s);
   return run_moe_x<Q4kUnit, 4, false>(ma, active, s);
+}
+
+// The fused down + combine applies to Q4_K / Q5_K decode (K fits one wave's team, topk teams
+// fit a workgroup), with every pair row in range (size_m == M).
+bool moe_comb_ok(int64_t M, int64_t T, int topk, int64_t K, int dt, const void *w, const void *x) {
+  int P, TP, RW;
+  if ((dt != Q4_K && dt != Q5_K) || topk > 64 || M != T * topk || T > 65535) return false;
+  if (!q4kx_geom(K, 256, &P, &TP, &RW) || TP > 64 || RW % topk) return false;
+  return ((uintptr_t)w & 15) == 0 && ((uintptr_t)x & 15) == 0;
+}
+
+int launch_moe_down_combine(const float *h, const void *w, const int64_t *pairs, const int64_t *expts,
+                            int32_t *counts, int32_t *offsets, const float *topk_w, float *y, int topk, int64_t T,
+                            int64_t E, int64_t N, int64_t K, int dt, hipStream_t s) {
+  MoeCombArgs ma;
+  const int64_t row_bytes = K / 256 * block_info(dt).bytes;
+  if (int rc = q4kx_setup(ma.g, 1, N, K, 256, row_bytes, "moe_gemm_q_combine")) return rc;
+  ma.g.x = h;
+  ma.g.w0 = static_cast<const uint8_t *>(w);
+  ma.g.out = y;
+  ma.pairs = pairs;
+  ma.expts = expts;
+  ma.counts = counts;
+  ma.offsets = offsets;
+  ma.topk_w = topk_w;
+  ma.expert_bytes = N * row_bytes;
+  ma.npairs = T * topk;
+  ma.E = (int)E;
+  ma.topk = topk;
+  const int RPW = ma.g.RW / topk;
+  const int64_t ngroups = cdiv(N, RPW);
+  // Enough workgroups to fill the chip over all tokens, each taking whole row groups.
+  int64_t per = cdiv((int64_t)device_cus() * 2, T);
+  per = per < ngroups ? per : ngroups;
+  per = cdiv(ngroups, cdiv(ngroups, per));
+  const size_t lds = (size_t)q4kx_act_lds(topk, K) + 64 * 4 + 2 * (size_t)RPW * topk * 4;
+  dim3 grid((unsigned)per, (unsigned)T);
+  // Two-level activations at every K, as moe_gemv_x_kernel uses (Q4kUnit / Q5kUnit).
+  if (dt == Q5_K)
+    moe_down_combine_kernel<Q5kUnit><<<grid, ma.g.TP * ma.g.RW, lds, s>>>(ma);
+  else
+    moe_down_combine_kernel<Q4kUnit><<<grid, ma.g.TP * ma.g.RW, lds, s>>>(ma);
+  return check_launch("moe_down_combine");
 }
 
 }  // namespace hq

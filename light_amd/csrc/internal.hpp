@@ -114,6 +114,14 @@ int launch_moe_sort_ids(const int64_t *ids, int64_t M, int64_t E, int64_t *sorte
 int launch_moe_q_gated(const float *x, const void *w, const int64_t *pairs, const int64_t *expts, int32_t *counts,
                        int32_t *offsets, float *out, int topk, int64_t size_m, int64_t M, int64_t rows, int64_t E,
                        int64_t I, int64_t K, int rpp, int dt, int act, void *ws, hipStream_t s);
+size_t moe_combine_ws_bytes(int64_t M, int64_t N, int64_t K, int dt);
+int launch_moe_q_combine(const float *h, const void *w, const int64_t *pairs, const int64_t *expts, int32_t *counts,
+                         int32_t *offsets, const float *topk_w, float *y, int topk, int64_t T, int64_t E, int64_t N,
+                         int64_t K, int dt, void *ws, hipStream_t s);
+bool moe_comb_ok(int64_t M, int64_t T, int topk, int64_t K, int dt, const void *w, const void *x);
+int launch_moe_down_combine(const float *h, const void *w, const int64_t *pairs, const int64_t *expts,
+                            int32_t *counts, int32_t *offsets, const float *topk_w, float *y, int topk, int64_t T,
+                            int64_t E, int64_t N, int64_t K, int dt, hipStream_t s);
 size_t moe_gated_ws_bytes(int64_t size_m, int64_t rows, int64_t I, int64_t K, int dt);
 int launch_moe_gemv_q4k(const void *act, const void *w, const int64_t *pairs, const int32_t *offsets,
                         const float *topk_w, float *out, int topk, int64_t size_m, int64_t M, int64_t rows,

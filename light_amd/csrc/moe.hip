@@ -179,4 +179,30 @@ int launch_moe_q_gated(const float *x, const void *w, const int64_t *pairs, cons
   return check_launch("moe_gated_split");
 }
 
+size_t moe_combine_ws_bytes(int64_t M, int64_t N, int64_t K, int dt) {
+  return (size_t)al256m(4 * M * N) + moe_ws_bytes(M, K, dt);
+}
+
+// Down projection + MoECombine: y (T, N) = combine(moe_gemm_q(h, w, routing, topk_w)).  Decode
+// shapes whose moe_gemm_q would run the one-launch grouped GEMV take the fused token-major
+// kernel (bit-identical to that GEMV + moe_combine); otherwise moe_gemm_q runs into the
+// zeroed workspace and moe_combine follows.
+int launch_moe_q_combine(const float *h, const void *w, const int64_t *pairs, const int64_t *expts, int32_t *counts,
+                         int32_t *offsets, const float *topk_w, float *y, int topk, int64_t T, int64_t E, int64_t N,
+                         int64_t K, int dt, void *ws, hipStream_t s) {
+  const int64_t M = T * topk;
+  if (E > INT32_MAX - 1 || M > INT32_MAX || N > INT32_MAX)
+    return fail(HQ_EUNSUPPORTED, "moe_gemm_q_combine", "too large");
+  if (E <= 65535 && (dt == Q5_K || !moe_use_mfma(M, E)) && moe_x_ok(K, dt, w, h) &&
+      moe_comb_ok(M, T, topk, K, dt, w, h))
+    return launch_moe_down_combine(h, w, pairs, expts, counts, offsets, topk_w, y, topk, T, E, N, K, dt, s);
+  float *po = static_cast<float *>(ws);
+  void *inner = static_cast<char *>(ws) + al256m(4 * M * N);
+  zero_f32_kernel<<<(unsigned)cdiv(M * N, 256), 256, 0, s>>>(po, M * N);
+  if (int rc = check_launch("zero")) return rc;
+  if (int rc = launch_moe_q(h, w, pairs, expts, counts, offsets, topk_w, po, topk, M, M, M, E, N, K, 1, dt, inner, s))
+    return rc;
+  return launch_moe_combine(po, y, T, N, topk, s);
+}
+
 }  // namespace hq

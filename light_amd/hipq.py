@@ -75,6 +75,8 @@ SIGNATURES = {
     "hq_int4_dequant": (_I, [_P, _P, _P, _P, _I, _I64, _I64, _I, _I64, _P]),
     "hq_moe_gemm_q_ws_bytes": (_SZ, [_I64, _I64, _I]),
     "hq_moe_combine": (_I, [_P, _P, _I64, _I64, _I, _P]),
+    "hq_moe_gemm_q_combine_ws_bytes": (_SZ, [_I64, _I, _I64, _I64, _I]),
+    "hq_moe_gemm_q_combine": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I64, _I64, _I64, _I64, _I, _P, _SZ, _P]),
     "hq_moe_route": (_I, [_P, _I64, _I64, _I, _I, _P, _P, _P, _P, _P, _P, _P]),
     "hq_moe_sort_ids": (_I, [_P, _I64, _I64, _P, _P, _P, _P, _P]),
     "hq_moe_gemm_q_gated_ws_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I]),
@@ -311,6 +313,21 @@ def moe_combine(pair_out, topk, out=None, stream=None):
     if out is None:
         out = torch.empty((M // topk, N), dtype=torch.float32, device=pair_out.device)
     check(lib().hq_moe_combine(_ptr(pair_out), _ptr(out), M, N, topk, _stream(stream)))
+    return out
+
+
+def moe_gemm_q_combine(h, w, sorted_pairs, sorted_expts, E, N, K, w_dtype, topk, topk_w=None, out=None,
+                       counts=None, offsets=None, ws=None, stream=None):
+    """y (T, N) = MoECombine(MoEGemmQ(h, w, routing, topk_w), topk), h per pair (T*topk, K)."""
+    import torch
+    M = sorted_pairs.numel()
+    T = M // topk
+    if out is None:
+        out = torch.empty((T, N), dtype=torch.float32, device=h.device)
+    ws_bytes = 0 if ws is None else ws.numel() * ws.element_size()
+    check(lib().hq_moe_gemm_q_combine(_ptr(h), _ptr(w), _ptr(sorted_pairs), _ptr(sorted_expts), _ptr(counts),
+                                      _ptr(offsets), _ptr(topk_w), _ptr(out), topk, T, E, N, K, w_dtype, _ptr(ws),
+                                      ws_bytes, _stream(stream)))
     return out
 
 

@@ -236,3 +236,38 @@ def test_moe_decode_pipeline_on_device(dev):
     want = oracle.moe_combine(pr, topk)
     scale = np.abs(pr).reshape(T, topk, H).sum(axis=1).max() + 1e-30
     assert np.max(np.abs(y - want)) <= 5e-3 * scale
+
+
+@pytest.mark.parametrize("dt,T,E,topk,H,I,weighted", [
+    (hipq.Q4_K, 1, 128, 8, 2048, 768, True),     # Qwen3-30B-A3B-like decode (configs[4], T = 1)
+    (hipq.Q4_K, 3, 128, 8, 2048, 768, True),
+    (hipq.Q5_K, 2, 64, 4, 1024, 512, True),
+    (hipq.Q4_K, 5, 16, 2, 512, 2048, False),     # K = 2048: two-wave-row teams
+    (hipq.Q4_K, 2, 8, 4, 256, 4096, True),       # K = 4096: one team per wave
+    (hipq.Q8_0, 2, 16, 4, 512, 256, True),       # no fused kernel: gemm + combine through ws
+])
+def test_moe_down_combine_bit_exact(dev, dt, T, E, topk, H, I, weighted):
+    """hq_moe_gemm_q_combine equals hq_moe_gemm_q followed by hq_moe_combine bit for bit, and
+    Light's CPU chain (MoEGemmQ, MoECombine) within the bar; counts / offsets as moe_gemm_q."""
+    print(f"[case] moe down+combine dt={hipq.NAMES[dt]} T={T} E={E} topk={topk} H={H} I={I}", flush=True)
+    g = synth.rng(900 + T + topk + dt)
+    wdn = synth.gguf_weight(dt, E * H, I, g)
+    ids, tw = synth.moe_routing(T, E, topk, g)
+    se, sp = synth.sort_pairs(ids)
+    h = synth.activations(T * topk, I, g)
+    wt, ht, spt, set_, twt = _t(wdn, dev), _t(h, dev), _t(sp, dev), _t(se, dev), _t(tw, dev)
+    kw = dict(topk_w=twt if weighted else None)
+    pair = hipq.moe_gemm_q(ht, wt, spt, set_, E, H, I, dt, topk, **kw)
+    want = hipq.moe_combine(pair, topk)
+    counts = torch.full((E,), -7, dtype=torch.int32, device=dev)
+    offsets = torch.full((E + 1,), -7, dtype=torch.int32, device=dev)
+    got = hipq.moe_gemm_q_combine(ht, wt, spt, set_, E, H, I, dt, topk, counts=counts, offsets=offsets, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want), f"max diff {(got - want).abs().max().item():.3g}"
+    bc = np.bincount(ids.ravel(), minlength=E)
+    assert np.array_equal(counts.cpu().numpy(), bc)
+    assert np.array_equal(offsets.cpu().numpy(), np.concatenate([[0], np.cumsum(bc)]))
+    pr = oracle.moe_gemm_q(h, wdn, dt, E, H, I, sp, se, topk, topk_w=tw if weighted else None)
+    ref = oracle.moe_combine(pr, topk)
+    scale = np.abs(pr).reshape(T, topk, H).sum(axis=1).max() + 1e-30
+    assert np.max(np.abs(got.cpu().numpy() - ref)) <= 5e-3 * scale
