@@ -370,7 +370,7 @@ def moe_rows(c, name, g, dev, cpu=False):
     hg = torch.zeros((M, I), device=dev)
     ws_g = torch.empty(max(hipq.moe_gemm_q_gated_ws_bytes(M, T, I, H, dt), 256), dtype=torch.uint8, device=dev)
     yb = torch.empty((T, H), device=dev)
-    ws_c = torch.empty(max(hipq.lib().hq_moe_gemm_q_combine_ws_bytes(T, topk, H, I, dt), 256), dtype=torch.uint8,
+    ws_c = torch.empty(max(hipq.lib().hq_moe_gemm_q_combine_ws_bytes(T, topk, E, H, I, dt), 256), dtype=torch.uint8,
                        device=dev)
 
     def block(i):

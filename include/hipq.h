@@ -259,7 +259,7 @@ int hq_moe_combine(const float *pair_out, float *out, int64_t M, int64_t N, int 
  * computes each (token, output row) over the token's topk experts and adds the slots in
  * slot order; other cases run those two ops through ws.  Light: nn/moe.go:230-235
  * (MoEGemmQ then MoECombine, ops/moe.go:209-265); no counterpart kernel in Light. */
-size_t hq_moe_gemm_q_combine_ws_bytes(int64_t T, int topk, int64_t N, int64_t K, int w_dtype);
+size_t hq_moe_gemm_q_combine_ws_bytes(int64_t T, int topk, int64_t E, int64_t N, int64_t K, int w_dtype);
 int hq_moe_gemm_q_combine(const float *h, const void *w, const int64_t *sorted_pairs, const int64_t *sorted_expts,
                           int32_t *counts, int32_t *offsets, const float *topk_w, float *y, int topk, int64_t T,
                           int64_t E, int64_t N, int64_t K, int w_dtype, void *ws, size_t ws_bytes,

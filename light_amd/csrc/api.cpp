@@ -565,9 +565,9 @@ int hq_moe_combine(const float *pair_out, float *out, int64_t M, int64_t N, int 
   return launch_moe_combine(pair_out, out, M / topk, N, topk, s);
 }
 
-size_t hq_moe_gemm_q_combine_ws_bytes(int64_t T, int topk, int64_t N, int64_t K, int w_dtype) {
-  if (T <= 0 || topk < 1 || N <= 0 || K <= 0) return 0;
-  return moe_combine_ws_bytes(T * topk, N, K, w_dtype);
+size_t hq_moe_gemm_q_combine_ws_bytes(int64_t T, int topk, int64_t E, int64_t N, int64_t K, int w_dtype) {
+  if (T <= 0 || topk < 1 || E <= 0 || N <= 0 || K <= 0) return 0;
+  return moe_combine_ws_bytes(T * topk, E, N, K, w_dtype);
 }
 
 int hq_moe_gemm_q_combine(const float *h, const void *w, const int64_t *sorted_pairs, const int64_t *sorted_expts,
@@ -583,7 +583,7 @@ int hq_moe_gemm_q_combine(const float *h, const void *w, const int64_t *sorted_p
   if (!h || !w || !sorted_pairs || !sorted_expts || !y) return fail(HQ_EINVAL, call, "NULL pointer");
   if (((uintptr_t)h & 15)) return fail(HQ_EINVAL, call, "h must be 16-byte aligned");
   hipStream_t s = resolve(stream);
-  const size_t need = moe_combine_ws_bytes(T * topk, N, K, w_dtype);
+  const size_t need = moe_combine_ws_bytes(T * topk, E, N, K, w_dtype);
   if (!ws) {
     if (int rc = workspace(need, s, &ws, call)) return rc;
   } else if (ws_bytes < need) {

@@ -114,7 +114,7 @@ int launch_moe_sort_ids(const int64_t *ids, int64_t M, int64_t E, int64_t *sorte
 int launch_moe_q_gated(const float *x, const void *w, const int64_t *pairs, const int64_t *expts, int32_t *counts,
                        int32_t *offsets, float *out, int topk, int64_t size_m, int64_t M, int64_t rows, int64_t E,
                        int64_t I, int64_t K, int rpp, int dt, int act, void *ws, hipStream_t s);
-size_t moe_combine_ws_bytes(int64_t M, int64_t N, int64_t K, int dt);
+size_t moe_combine_ws_bytes(int64_t M, int64_t E, int64_t N, int64_t K, int dt);
 int launch_moe_q_combine(const float *h, const void *w, const int64_t *pairs, const int64_t *expts, int32_t *counts,
                          int32_t *offsets, const float *topk_w, float *y, int topk, int64_t T, int64_t E, int64_t N,
                          int64_t K, int dt, void *ws, hipStream_t s);

@@ -179,8 +179,10 @@ int launch_moe_q_gated(const float *x, const void *w, const int64_t *pairs, cons
   return check_launch("moe_gated_split");
 }
 
-size_t moe_combine_ws_bytes(int64_t M, int64_t N, int64_t K, int dt) {
-  return (size_t)al256m(4 * M * N) + moe_ws_bytes(M, K, dt);
+// Workspace of the unfused down + combine: the pair rows (M, N) F32, the counts / offsets
+// scratch when the caller passes none, then moe_gemm_q's own workspace.
+size_t moe_combine_ws_bytes(int64_t M, int64_t E, int64_t N, int64_t K, int dt) {
+  return (size_t)al256m(4 * M * N) + (size_t)al256m(4 * (2 * E + 1)) + moe_ws_bytes(M, K, dt);
 }
 
 // Down projection + MoECombine: y (T, N) = combine(moe_gemm_q(h, w, routing, topk_w)).  Decode
@@ -197,7 +199,13 @@ int launch_moe_q_combine(const float *h, const void *w, const int64_t *pairs, co
       moe_comb_ok(M, T, topk, K, dt, w, h))
     return launch_moe_down_combine(h, w, pairs, expts, counts, offsets, topk_w, y, topk, T, E, N, K, dt, s);
   float *po = static_cast<float *>(ws);
-  void *inner = static_cast<char *>(ws) + al256m(4 * M * N);
+  auto *co = reinterpret_cast<int32_t *>(static_cast<char *>(ws) + al256m(4 * M * N));
+  void *inner = static_cast<char *>(ws) + al256m(4 * M * N) + al256m(4 * (2 * E + 1));
+  // moe_gemm_q writes counts / offsets; without caller buffers they go to the workspace.
+  if (!counts || !offsets) {
+    counts = co;
+    offsets = co + E;
+  }
   zero_f32_kernel<<<(unsigned)cdiv(M * N, 256), 256, 0, s>>>(po, M * N);
   if (int rc = check_launch("zero")) return rc;
   if (int rc = launch_moe_q(h, w, pairs, expts, counts, offsets, topk_w, po, topk, M, M, M, E, N, K, 1, dt, inner, s))

@@ -75,7 +75,7 @@ SIGNATURES = {
     "hq_int4_dequant": (_I, [_P, _P, _P, _P, _I, _I64, _I64, _I, _I64, _P]),
     "hq_moe_gemm_q_ws_bytes": (_SZ, [_I64, _I64, _I]),
     "hq_moe_combine": (_I, [_P, _P, _I64, _I64, _I, _P]),
-    "hq_moe_gemm_q_combine_ws_bytes": (_SZ, [_I64, _I, _I64, _I64, _I]),
+    "hq_moe_gemm_q_combine_ws_bytes": (_SZ, [_I64, _I, _I64, _I64, _I64, _I]),
     "hq_moe_gemm_q_combine": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I64, _I64, _I64, _I64, _I, _P, _SZ, _P]),
     "hq_moe_route": (_I, [_P, _I64, _I64, _I, _I, _P, _P, _P, _P, _P, _P, _P]),
     "hq_moe_sort_ids": (_I, [_P, _I64, _I64, _P, _P, _P, _P, _P]),

@@ -271,3 +271,21 @@ def test_moe_down_combine_bit_exact(dev, dt, T, E, topk, H, I, weighted):
     ref = oracle.moe_combine(pr, topk)
     scale = np.abs(pr).reshape(T, topk, H).sum(axis=1).max() + 1e-30
     assert np.max(np.abs(got.cpu().numpy() - ref)) <= 5e-3 * scale
+
+
+@pytest.mark.parametrize("dt,T,E,topk", [(hipq.Q4_K, 64, 16, 2), (hipq.Q8_0, 3, 16, 4), (hipq.Q4_K, 1, 128, 8)])
+def test_moe_down_combine_without_scratch_buffers(dev, dt, T, E, topk):
+    """counts / offsets are optional: the unfused path (here the grouped MFMA GEMM at M > 4E,
+    or a format without the fused kernel) keeps them in its workspace."""
+    print(f"[case] moe down+combine no counts dt={hipq.NAMES[dt]} T={T} E={E} topk={topk}", flush=True)
+    H, I = 256, 512
+    g = synth.rng(1200 + T + dt)
+    wdn = synth.gguf_weight(dt, E * H, I, g)
+    ids, tw = synth.moe_routing(T, E, topk, g)
+    se, sp = synth.sort_pairs(ids)
+    h = synth.activations(T * topk, I, g)
+    wt, ht, spt, set_, twt = _t(wdn, dev), _t(h, dev), _t(sp, dev), _t(se, dev), _t(tw, dev)
+    want = hipq.moe_combine(hipq.moe_gemm_q(ht, wt, spt, set_, E, H, I, dt, topk, topk_w=twt), topk)
+    got = hipq.moe_gemm_q_combine(ht, wt, spt, set_, E, H, I, dt, topk, topk_w=twt)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
