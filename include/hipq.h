@@ -298,6 +298,20 @@ int hq_moe_gemm_q_gated(const float *x, const void *w, const int64_t *sorted_pai
                         int64_t rows, int64_t E, int64_t I, int64_t K, int row_per_pair, int w_dtype, int act,
                         void *ws, size_t ws_bytes, hq_stream_t stream);
 
+/* MoERoute followed by the routed gated gate/up, the first half of the SparseMoE decode block
+ * (nn/moe.go:150-225: MoERoute, then runExperts' MoEGemmQ, Narrow, SiLU / GeluErf, Mul):
+ * probs F32 (T, E) -> topk_ids, weights, sorted_pairs, sorted_expts as hq_moe_route, and
+ * h F32 (T*topk, I) per pair as hq_moe_gemm_q_gated with x F32 (T, K) per token and the
+ * stacked GateUp w (E, 2I, K).  counts / offsets nullable.  Bit-identical to hq_moe_route +
+ * hq_moe_gemm_q_gated.  For Q4_K / Q5_K with T <= 8 and T*topk <= 64 one kernel runs both:
+ * each workgroup selects the top-k and sorts the pairs itself, so no launch sits between
+ * the router and the expert weights.  Limits as hq_moe_route.  No counterpart in Light. */
+size_t hq_moe_route_gated_ws_bytes(int64_t T, int topk, int64_t E, int64_t I, int64_t K, int w_dtype);
+int hq_moe_route_gated(const float *probs, const float *x, const void *w, float *h, int64_t T, int64_t E, int topk,
+                       int normalize, int64_t I, int64_t K, int w_dtype, int act, int64_t *topk_ids, float *weights,
+                       int64_t *sorted_pairs, int64_t *sorted_expts, int32_t *counts, int32_t *offsets, void *ws,
+                       size_t ws_bytes, hq_stream_t stream);
+
 /* y (M, K) = x[:, idx] for 2- or 4-byte elements (ops.gatherColumns, ops/int4.go:129-147):
  * the act-order (desc_act) permutation of quant.Int4.Perm applied to the activations.
  * Indices outside [0, K) give zeros. */

@@ -659,6 +659,42 @@ int hq_moe_gemm_q_gated(const float *x, const void *w, const int64_t *sorted_pai
                             row_per_pair, w_dtype, act, ws, s);
 }
 
+size_t hq_moe_route_gated_ws_bytes(int64_t T, int topk, int64_t E, int64_t I, int64_t K, int w_dtype) {
+  if (T <= 0 || topk < 1 || E <= 0 || I <= 0 || K <= 0) return 0;
+  return moe_route_gated_ws_bytes(T, topk, E, I, K, w_dtype);
+}
+
+int hq_moe_route_gated(const float *probs, const float *x, const void *w, float *h, int64_t T, int64_t E, int topk,
+                       int normalize, int64_t I, int64_t K, int w_dtype, int act, int64_t *topk_ids, float *weights,
+                       int64_t *sorted_pairs, int64_t *sorted_expts, int32_t *counts, int32_t *offsets, void *ws,
+                       size_t ws_bytes, hq_stream_t stream) {
+  const char *call = "hq_moe_route_gated";
+  if (!is_gguf(w_dtype)) return fail(HQ_EUNSUPPORTED, call, "weight dtype %d has no fused kernel", w_dtype);
+  if (act != HQ_ACT_SILU && act != HQ_ACT_GELU_ERF) return fail(HQ_EINVAL, call, "activation %d", act);
+  if (T < 0 || E < 1) return fail(HQ_EINVAL, call, "probs must be (T, E), got (%lld, %lld)", (long long)T, (long long)E);
+  if (topk < 1 || topk > E) return fail(HQ_EINVAL, call, "topk %d out of range [1, %lld]", topk, (long long)E);
+  if (I < 0 || K <= 0) return fail(HQ_EINVAL, call, "bad shape");
+  BlockInfo bi = block_info(w_dtype);
+  if (K % bi.elems) return fail(HQ_EINVAL, call, "K=%lld not a multiple of block size %d", (long long)K, bi.elems);
+  if (T == 0) return HQ_OK;
+  if (topk > 64 || !moe_route_fits(T * topk, E))
+    return fail(HQ_EUNSUPPORTED, call, "T=%lld E=%lld topk=%d beyond the one-workgroup sort", (long long)T,
+                (long long)E, topk);
+  if (!probs || !x || !w || !h || !topk_ids || !weights || !sorted_pairs || !sorted_expts)
+    return fail(HQ_EINVAL, call, "NULL pointer");
+  if (((uintptr_t)x & 15)) return fail(HQ_EINVAL, call, "x must be 16-byte aligned");
+  hipStream_t s = resolve(stream);
+  const size_t need = moe_route_gated_ws_bytes(T, topk, E, I, K, w_dtype);
+  if (!ws) {
+    if (int rc = workspace(need, s, &ws, call)) return rc;
+  } else if (ws_bytes < need) {
+    return fail(HQ_ENOMEM, call, "workspace %zu bytes < %zu needed", ws_bytes, need);
+  }
+  TraceSpan span("moe_route_gated", s);
+  return launch_moe_route_gated_any(probs, x, w, h, T, E, topk, normalize, I, K, w_dtype, act, topk_ids, weights,
+                                    sorted_pairs, sorted_expts, counts, offsets, ws, s);
+}
+
 int hq_gather_cols(const void *x, const int64_t *idx, void *y, int64_t M, int64_t K, int elem_bytes,
                    hq_stream_t stream) {
   const char *call = "hq_gather_cols";

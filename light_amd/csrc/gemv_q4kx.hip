@@ -34,6 +34,7 @@
 //    quantize launch.
 #include "actq.hpp"
 #include "internal.hpp"
+#include "route.hpp"
 
 #include <algorithm>
 
@@ -626,7 +627,46 @@ struct MoeXArgs {
   int64_t size_m, expert_bytes, rows, npairs;
   int64_t up_off;  // GATED: byte offset of the up rows inside an expert (I rows after gate)
   int E, topk, rpp, act;
+  // ROUTE: router probabilities (T, E) and MoERoute's outputs, written by workgroup (0, 0).
+  const float *probs;
+  int64_t *topk_ids, *sorted_pairs_out, *sorted_expts_out;
+  float *weights_out;
+  int T, normalize;
 };
+
+// MoERoute inside a workgroup, for T * topk <= 64 pairs and T <= 8 tokens: wave t selects
+// token t's top-k (topk_row_any, as moe_route_kernel), then wave 0 places each pair at its
+// rank in the stable expert order (pairs of one expert keep pair order).  The LDS arrays
+// end as MoERoute's outputs: re/rw per pair, se/sp in sorted order.
+__device__ void route_in_workgroup(const MoeXArgs &ma, int *re, float *rw, int *se, int *sp) {
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int M = (int)ma.npairs;
+  if (wave < ma.T) {
+    float sv, den;
+    int si;
+    topk_row_any(ma.probs + (int64_t)wave * ma.E, ma.E, ma.topk, lane, sv, si, den);
+    if (lane < ma.topk) {
+      re[wave * ma.topk + lane] = si;
+      rw[wave * ma.topk + lane] = ma.normalize ? __fdiv_rn(sv, den) : sv;
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const bool valid = lane < M;
+    const int ep = valid ? re[lane] : 0x7fffffff;
+    int pos = 0;
+    for (int q = 0; q < M; q++) {
+      const int eq = __builtin_amdgcn_readlane(ep, q);
+      pos += (eq < ep || (eq == ep && q < lane)) ? 1 : 0;
+    }
+    if (valid) {
+      se[pos] = ep;
+      sp[pos] = lane;
+    }
+  }
+  __syncthreads();
+}
+
 
 // Segment j of the sorted expert ids (segment starts: i == 0 or v[i] != v[i-1]), found by
 // one wave: 256 ids per round as four independent loads per lane, ballots of the start
@@ -674,9 +714,26 @@ __device__ __forceinline__ Seg find_segment(const int64_t *__restrict__ v, int64
   return sg;
 }
 
-template <class U, int MM, bool GATED>
+// Segment j of the expert-sorted ids held in LDS (n <= 64), as find_segment.
+__device__ __forceinline__ Seg lds_segment(const int *se, int n, int j, int lane) {
+  Seg sg{-1, n, -1, -1};
+  const bool st = lane < n && (lane == 0 || se[lane] != se[lane > 0 ? lane - 1 : 0]);
+  uint64_t m = __ballot(st);
+  for (int i = 0; i < j && m; i++) m &= m - 1;
+  if (!m) return sg;
+  sg.seg0 = __ffsll((unsigned long long)m) - 1;
+  m &= m - 1;
+  sg.seg1 = m ? __ffsll((unsigned long long)m) - 1 : n;
+  sg.e = se[sg.seg0];
+  sg.eprev = sg.seg0 == 0 ? -1 : se[sg.seg0 - 1];
+  return sg;
+}
+
+template <class U, int MM, bool GATED, bool ROUTE = false>
 __global__ __launch_bounds__(512) void moe_gemv_x_kernel(MoeXArgs ma) {
   extern __shared__ __align__(16) uint8_t smem[];
+  __shared__ int r_e[ROUTE ? 64 : 1], r_se[ROUTE ? 64 : 1], r_sp[ROUTE ? 64 : 1];
+  __shared__ float r_w[ROUTE ? 64 : 1];
   const Q4kxArgs &a = ma.g;
   const int t = threadIdx.x, lane = t & 63;
   // One row of x (a single token's gate/up, plain kernel): every pair reads row 0, so the first slice of
@@ -691,11 +748,25 @@ __global__ __launch_bounds__(512) void moe_gemv_x_kernel(MoeXArgs ma) {
     const int blk = task >> 3, sub = task & 7, kb = blk % KB0;
     xpre = *reinterpret_cast<const float4 *>(static_cast<const float *>(a.x) + kb * 32 + sub * 4);
   }
-  const Seg sg = find_segment(ma.expts, ma.npairs, (int)blockIdx.y, lane);
+  Seg sg;
+  if constexpr (ROUTE) {
+    route_in_workgroup(ma, r_e, r_w, r_se, r_sp);
+    if (blockIdx.x == 0 && blockIdx.y == 0) {
+      for (int i = t; i < (int)ma.npairs; i += blockDim.x) {
+        ma.topk_ids[i] = r_e[i];
+        ma.weights_out[i] = r_w[i];
+        ma.sorted_pairs_out[i] = r_sp[i];
+        ma.sorted_expts_out[i] = r_se[i];
+      }
+    }
+    sg = lds_segment(r_se, (int)ma.npairs, (int)blockIdx.y, lane);
+  } else {
+    sg = find_segment(ma.expts, ma.npairs, (int)blockIdx.y, lane);
+  }
   if (sg.seg0 < 0) return;
   const int64_t seg0 = sg.seg0, seg1 = sg.seg1;
   const int e = sg.e;
-  if (blockIdx.x == 0) {
+  if (blockIdx.x == 0 && ma.counts && ma.offsets) {
     // counts / offsets of the experts (eprev, e], and of (e, E) after the last segment.
     const int lo = sg.eprev + 1 > 0 ? sg.eprev + 1 : 0;
     const int hi = seg1 == ma.npairs ? ma.E - 1 : (e < ma.E ? e : ma.E - 1);
@@ -723,7 +794,7 @@ __global__ __launch_bounds__(512) void moe_gemv_x_kernel(MoeXArgs ma) {
     int64_t pid[MM], xrow[MM];
 #pragma unroll
     for (int mm = 0; mm < MM; mm++) {
-      int64_t p = c0 + mm < seg1 ? ma.pairs[c0 + mm] : -1;
+      int64_t p = c0 + mm < seg1 ? (ROUTE ? (int64_t)r_sp[c0 + mm] : ma.pairs[c0 + mm]) : -1;
       if (p < 0 || p >= ma.size_m) p = -1;
       pid[mm] = p;
       int64_t r = p < 0 ? 0 : (ma.rpp ? p : p / ma.topk);
@@ -1236,7 +1307,7 @@ bool moe_x_ok(int64_t K, int dt, const void *w, const void *x) {
   return ((uintptr_t)w & 15) == 0 && ((uintptr_t)x & 15) == 0;
 }
 
-template <class U, int MM, bool GATED>
+template <class U, int MM, bool GATED, bool ROUTE = false>
 static int run_moe_x(MoeXArgs &ma, int64_t active, hipStream_t s) {
   const Q4kxArgs &a = ma.g;
   const size_t lds = (size_t)q4kx_act_lds(MM, a.K);
@@ -1248,7 +1319,7 @@ static int run_moe_x(MoeXArgs &ma, int64_t active, hipStream_t s) {
   per = per < ngroups ? per : ngroups;
   per = cdiv(ngroups, cdiv(ngroups, per));
   dim3 grid((unsigned)per, (unsigned)active);
-  moe_gemv_x_kernel<U, MM, GATED><<<grid, a.TP * a.RW, lds, s>>>(ma);
+  moe_gemv_x_kernel<U, MM, GATED, ROUTE><<<grid, a.TP * a.RW, lds, s>>>(ma);
   return check_launch("moe_gemv_x");
 }
 
@@ -1335,6 +1406,54 @@ int launch_moe_down_combine(const float *h, const void *w, const int64_t *pairs,
   else
     moe_down_combine_kernel<Q4kUnit><<<grid, ma.g.TP * ma.g.RW, lds, s>>>(ma);
   return check_launch("moe_down_combine");
+}
+
+// MoERoute + the routed gated gate/up in one launch: every workgroup routes the T tokens
+// itself (route_in_workgroup) and takes its expert segment from that.  Applies to Q4_K /
+// Q5_K with T <= 8, T * topk <= 64, E <= 1024 and the decode GEMV's geometry.
+bool moe_route_gated_ok(int64_t T, int64_t E, int topk, int64_t K, int dt, const void *w, const void *x) {
+  const int64_t M = T * topk;
+  return T >= 1 && T <= 8 && M <= 64 && E >= 1 && E <= 1024 && topk <= E && M <= 4 * E && moe_x_ok(K, dt, w, x);
+}
+
+int launch_moe_route_gated(const float *probs, const float *x, const void *w, float *h, int64_t T, int64_t E,
+                           int topk, int normalize, int64_t I, int64_t K, int dt, int act, int64_t *topk_ids,
+                           float *weights, int64_t *sorted_pairs, int64_t *sorted_expts, int32_t *counts,
+                           int32_t *offsets, hipStream_t s) {
+  MoeXArgs ma;
+  const int64_t row_bytes = K / 256 * block_info(dt).bytes;
+  if (int rc = q4kx_setup(ma.g, 1, 2 * I, K, 256, row_bytes, "moe_route_gated")) return rc;
+  const int64_t M = T * topk;
+  ma.g.N = (int)I;
+  ma.g.x = x;
+  ma.g.w0 = static_cast<const uint8_t *>(w);
+  ma.g.out = h;
+  ma.pairs = nullptr;
+  ma.expts = nullptr;
+  ma.counts = counts;
+  ma.offsets = offsets;
+  ma.topk_w = nullptr;
+  ma.size_m = M;
+  ma.expert_bytes = 2 * I * row_bytes;
+  ma.up_off = I * row_bytes;
+  ma.act = act;
+  ma.rows = T;
+  ma.npairs = M;
+  ma.E = (int)E;
+  ma.topk = topk;
+  ma.rpp = 0;
+  ma.probs = probs;
+  ma.topk_ids = topk_ids;
+  ma.weights_out = weights;
+  ma.sorted_pairs_out = sorted_pairs;
+  ma.sorted_expts_out = sorted_expts;
+  ma.T = (int)T;
+  ma.normalize = normalize;
+  const int64_t active = M < E ? M : E;
+  const int64_t avg = (M + active - 1) / active;
+  if (dt == Q5_K)
+    return avg <= 1 ? run_moe_x<Q5kUnit, 1, true, true>(ma, active, s) : run_moe_x<Q5kUnit, 2, true, true>(ma, active, s);
+  return avg <= 1 ? run_moe_x<Q4kUnit, 1, true, true>(ma, active, s) : run_moe_x<Q4kUnit, 2, true, true>(ma, active, s);
 }
 
 }  // namespace hq

@@ -118,6 +118,16 @@ size_t moe_combine_ws_bytes(int64_t M, int64_t E, int64_t N, int64_t K, int dt);
 int launch_moe_q_combine(const float *h, const void *w, const int64_t *pairs, const int64_t *expts, int32_t *counts,
                          int32_t *offsets, const float *topk_w, float *y, int topk, int64_t T, int64_t E, int64_t N,
                          int64_t K, int dt, void *ws, hipStream_t s);
+size_t moe_route_gated_ws_bytes(int64_t T, int topk, int64_t E, int64_t I, int64_t K, int dt);
+int launch_moe_route_gated_any(const float *probs, const float *x, const void *w, float *h, int64_t T, int64_t E,
+                               int topk, int normalize, int64_t I, int64_t K, int dt, int act, int64_t *topk_ids,
+                               float *weights, int64_t *sorted_pairs, int64_t *sorted_expts, int32_t *counts,
+                               int32_t *offsets, void *ws, hipStream_t s);
+bool moe_route_gated_ok(int64_t T, int64_t E, int topk, int64_t K, int dt, const void *w, const void *x);
+int launch_moe_route_gated(const float *probs, const float *x, const void *w, float *h, int64_t T, int64_t E,
+                           int topk, int normalize, int64_t I, int64_t K, int dt, int act, int64_t *topk_ids,
+                           float *weights, int64_t *sorted_pairs, int64_t *sorted_expts, int32_t *counts,
+                           int32_t *offsets, hipStream_t s);
 bool moe_comb_ok(int64_t M, int64_t T, int topk, int64_t K, int dt, const void *w, const void *x);
 int launch_moe_down_combine(const float *h, const void *w, const int64_t *pairs, const int64_t *expts,
                             int32_t *counts, int32_t *offsets, const float *topk_w, float *y, int topk, int64_t T,

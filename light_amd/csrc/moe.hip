@@ -213,4 +213,32 @@ int launch_moe_q_combine(const float *h, const void *w, const int64_t *pairs, co
   return launch_moe_combine(po, y, T, N, topk, s);
 }
 
+size_t moe_route_gated_ws_bytes(int64_t T, int topk, int64_t E, int64_t I, int64_t K, int dt) {
+  return (size_t)al256m(4 * (2 * E + 1)) + moe_gated_ws_bytes(T * topk, T, I, K, dt);
+}
+
+// MoERoute, then the routed gated gate/up (h per pair, row(p) = p / topk).  Decode shapes run
+// both in one launch (bit-identical to moe_route + moe_gemm_q_gated); otherwise the two run
+// in sequence, with counts / offsets in the workspace when the caller passes none.
+int launch_moe_route_gated_any(const float *probs, const float *x, const void *w, float *h, int64_t T, int64_t E,
+                               int topk, int normalize, int64_t I, int64_t K, int dt, int act, int64_t *topk_ids,
+                               float *weights, int64_t *sorted_pairs, int64_t *sorted_expts, int32_t *counts,
+                               int32_t *offsets, void *ws, hipStream_t s) {
+  if (moe_route_gated_ok(T, E, topk, K, dt, w, x))
+    return launch_moe_route_gated(probs, x, w, h, T, E, topk, normalize, I, K, dt, act, topk_ids, weights,
+                                  sorted_pairs, sorted_expts, counts, offsets, s);
+  auto *co = static_cast<int32_t *>(ws);
+  void *inner = static_cast<char *>(ws) + al256m(4 * (2 * E + 1));
+  if (!counts || !offsets) {
+    counts = co;
+    offsets = co + E;
+  }
+  if (int rc = launch_moe_route(probs, T, E, topk, normalize, topk_ids, weights, sorted_pairs, sorted_expts, counts,
+                                offsets, s))
+    return rc;
+  const int64_t M = T * topk;
+  return launch_moe_q_gated(x, w, sorted_pairs, sorted_expts, counts, offsets, h, topk, M, M, T, E, I, K, 0, dt, act,
+                            inner, s);
+}
+
 }  // namespace hq

@@ -83,6 +83,9 @@ SIGNATURES = {
     "hq_moe_gemm_q_gated": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _I,
                                  _P, _SZ, _P]),
     "hq_gather_cols": (_I, [_P, _P, _P, _I64, _I64, _I, _P]),
+    "hq_moe_route_gated_ws_bytes": (_SZ, [_I64, _I, _I64, _I64, _I64, _I]),
+    "hq_moe_route_gated": (_I, [_P, _P, _P, _P, _I64, _I64, _I, _I, _I64, _I64, _I, _I, _P, _P, _P, _P, _P, _P, _P,
+                                _SZ, _P]),
     "hq_moe_gemm_q": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I,
                            _P, _SZ, _P]),
 }
@@ -329,6 +332,26 @@ def moe_gemm_q_combine(h, w, sorted_pairs, sorted_expts, E, N, K, w_dtype, topk,
                                       _ptr(offsets), _ptr(topk_w), _ptr(out), topk, T, E, N, K, w_dtype, _ptr(ws),
                                       ws_bytes, _stream(stream)))
     return out
+
+
+def moe_route_gated(probs, x, w, E, I, K, w_dtype, topk, normalize=True, act=ACT_SILU, h=None, counts=None,
+                    offsets=None, ws=None, stream=None):
+    """MoERoute + the routed gated gate/up: (topk_ids, weights, sorted_pairs, sorted_expts, h (T*topk, I))."""
+    import torch
+    T = probs.shape[0]
+    dev = probs.device
+    M = T * topk
+    ids = torch.empty((T, topk), dtype=torch.int64, device=dev)
+    wt = torch.empty(M, dtype=torch.float32, device=dev)
+    sp = torch.empty(M, dtype=torch.int64, device=dev)
+    se = torch.empty(M, dtype=torch.int64, device=dev)
+    if h is None:
+        h = torch.zeros((M, I), dtype=torch.float32, device=dev)
+    ws_bytes = 0 if ws is None else ws.numel() * ws.element_size()
+    check(lib().hq_moe_route_gated(_ptr(probs), _ptr(x), _ptr(w), _ptr(h), T, E, topk, int(bool(normalize)), I, K,
+                                   w_dtype, act, _ptr(ids), _ptr(wt), _ptr(sp), _ptr(se), _ptr(counts),
+                                   _ptr(offsets), _ptr(ws), ws_bytes, _stream(stream)))
+    return ids, wt, sp, se, h
 
 
 def moe_route(probs, topk, normalize=True, counts=None, offsets=None, stream=None):

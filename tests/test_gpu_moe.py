@@ -289,3 +289,31 @@ def test_moe_down_combine_without_scratch_buffers(dev, dt, T, E, topk):
     got = hipq.moe_gemm_q_combine(ht, wt, spt, set_, E, H, I, dt, topk, topk_w=twt)
     torch.cuda.synchronize()
     assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("dt,T,E,topk,H,I,ties", [
+    (hipq.Q4_K, 1, 128, 8, 2048, 768, False),    # configs[4] decode
+    (hipq.Q4_K, 3, 128, 8, 2048, 768, True),
+    (hipq.Q5_K, 8, 8, 4, 1024, 512, False),      # experts shared across tokens: fewer segments than slots
+    (hipq.Q4_K, 2, 64, 2, 4096, 256, True),      # K = 4096
+    (hipq.Q8_0, 2, 16, 4, 512, 256, False),      # no fused kernel: route, then the gated op
+])
+def test_moe_route_gated_bit_exact(dev, dt, T, E, topk, H, I, ties):
+    """hq_moe_route_gated equals hq_moe_route + hq_moe_gemm_q_gated bit for bit (routing
+    outputs, counts / offsets and h)."""
+    print(f"[case] moe route+gated dt={hipq.NAMES[dt]} T={T} E={E} topk={topk} H={H} I={I}", flush=True)
+    g = synth.rng(1500 + T + E + dt)
+    wgu = _t(synth.gguf_weight(dt, E * 2 * I, H, g), dev)
+    x = _t(synth.activations(T, H, g), dev)
+    probs = _t(_probs(g, T, E, ties=ties), dev)
+    c0 = torch.zeros(E, dtype=torch.int32, device=dev)
+    o0 = torch.zeros(E + 1, dtype=torch.int32, device=dev)
+    ids, w, sp, se = hipq.moe_route(probs, topk, True)
+    h0 = hipq.moe_gemm_q_gated(x, wgu, sp, se, E, I, H, dt, topk, counts=c0, offsets=o0)
+    c1 = torch.full((E,), -5, dtype=torch.int32, device=dev)
+    o1 = torch.full((E + 1,), -5, dtype=torch.int32, device=dev)
+    ids1, w1, sp1, se1, h1 = hipq.moe_route_gated(probs, x, wgu, E, I, H, dt, topk, counts=c1, offsets=o1)
+    torch.cuda.synchronize()
+    for a, b, name in ((ids, ids1, "ids"), (w, w1, "weights"), (sp, sp1, "sorted_pairs"), (se, se1, "sorted_expts"),
+                       (c0, c1, "counts"), (o0, o1, "offsets"), (h0, h1, "h")):
+        assert torch.equal(a, b), name
