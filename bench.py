@@ -360,8 +360,8 @@ def moe_rows(c, name, g, dev, cpu=False):
                 t, th, smp = cpu_moe_leg(h.cpu().numpy(), wdn_np, dt, E, H, I, sp_np, se_np, topk, tw_np)
             row.update(cpu_us=round(t * 1e6, 1), cpu_threads=th, cpu_sample=smp, gpu_over_cpu=round(t * 1e6 / us, 1))
         out.append(row)
-    # The whole routed block on the device: router probs -> hq_moe_route -> gated gate/up
-    # (SiLU * up) -> down (routing-weighted) with the combine in its epilogue.  Probs rotate
+    # The whole routed block on the device: router probs -> routing + gated gate/up (SiLU * up)
+    # in one launch -> down (routing-weighted) with the combine in its epilogue.  Probs rotate
     # over 16 draws.
     probs = []
     for _ in range(16):
@@ -373,9 +373,11 @@ def moe_rows(c, name, g, dev, cpu=False):
     ws_c = torch.empty(max(hipq.lib().hq_moe_gemm_q_combine_ws_bytes(T, topk, E, H, I, dt), 256), dtype=torch.uint8,
                        device=dev)
 
+    ws_r = torch.empty(max(hipq.lib().hq_moe_route_gated_ws_bytes(T, topk, E, I, H, dt), 256), dtype=torch.uint8,
+                       device=dev)
+
     def block(i):
-        _, w, sp, se = hipq.moe_route(probs[i % 16], topk, True)
-        hipq.moe_gemm_q_gated(x, wgu, sp, se, E, I, H, dt, topk, out=hg, counts=counts, offsets=offsets, ws=ws_g)
+        _, w, sp, se, _ = hipq.moe_route_gated(probs[i % 16], x, wgu, E, I, H, dt, topk, h=hg, ws=ws_r)
         hipq.moe_gemm_q_combine(hg, wdn, sp, se, E, H, I, dt, topk, topk_w=w, out=yb, ws=ws_c)
 
     us = time_launches(block, 64, 16)

@@ -740,7 +740,7 @@ __global__ __launch_bounds__(512) void moe_gemv_x_kernel(MoeXArgs ma) {
   // x loads (all of x up to K = 2048) goes out now, beside the expert-id search instead of
   // after it.
   constexpr int XT = 4;
-  const bool x1 = !GATED && ma.rows == 1;  // (the gated kernel has no registers to spare)
+  const bool x1 = (!GATED || ROUTE) && ma.rows == 1;  // (the plain gated kernel has no registers to spare)
   const int KB0 = a.K >> 5, ntask0 = MM * KB0 * 8;
   float4 xpre = make_float4(0.f, 0.f, 0.f, 0.f);
   if (x1) {
@@ -921,6 +921,16 @@ __global__ __launch_bounds__(512) void moe_down_combine_kernel(MoeCombArgs ma) {
   float *lsx = reinterpret_cast<float *>(smem + 2 * (int64_t)topk * a.K + 8 * (int64_t)topk * KB);
   int *lexp = reinterpret_cast<int *>(smem + q4kx_act_lds(topk, a.K));
   float *lval = reinterpret_cast<float *>(lexp + 64);
+  // The token's h rows do not depend on the routing: their first loads go out first.
+  constexpr int XT = 4;
+  const int ntask = topk * KB * 8, bd = (int)blockDim.x;
+  const float *x = static_cast<const float *>(a.x) + (int64_t)tok * topk * a.K;
+  float4 xv[XT];
+#pragma unroll
+  for (int i = 0; i < XT; i++) {
+    const int task = i * bd + t < ntask ? i * bd + t : ntask - 1;
+    xv[i] = *reinterpret_cast<const float4 *>(x + (int64_t)(task >> 3) * 32 + (task & 7) * 4);
+  }
   if (blockIdx.x == 0 && tok == 0 && ma.offsets) {
     for (int e = t; e <= ma.E; e += blockDim.x) {
       auto lower = [&](int64_t v) {
@@ -943,14 +953,38 @@ __global__ __launch_bounds__(512) void moe_down_combine_kernel(MoeCombArgs ma) {
     const int64_t p = ma.pairs[i];
     if (p >= (int64_t)tok * topk && p < (int64_t)(tok + 1) * topk) lexp[p - (int64_t)tok * topk] = (int)ma.expts[i];
   }
-  // Quantize the token's topk rows of h into LDS, as moe_gemv_x_kernel does.
-  const int ntask = topk * KB * 8;
-  const float *x = static_cast<const float *>(a.x) + (int64_t)tok * topk * a.K;
-  for (int base = 0; base < ntask; base += (int)blockDim.x) {
+  __syncthreads();
+  const int team = t / a.TP, u = t - team * a.TP;
+  const int slot = team % topk, rloc = team / topk;
+  const bool active = u < a.P && rloc < RPW;
+  const typename U::Lane L = unit_lane<U>(active ? u : 0, a.G);
+  int e = lexp[slot];
+  const bool ok = e >= 0 && e < ma.E;
+  e = ok ? e : 0;
+  const uint8_t *w = a.w0 + (int64_t)e * ma.expert_bytes;
+  const int ngroups = (a.N + RPW - 1) / RPW, G = gridDim.x;
+  const int niter = (ngroups - (int)blockIdx.x + G - 1) / G;
+  // The first weights go out as soon as the experts are known, before h is read.
+  typename U::W wr;
+  {
+    int row = (int)blockIdx.x * RPW + rloc;
+    row = row < a.N && rloc < RPW ? row : a.N;
+    U::load(w, a.s0, a.z0, a, row, L, wr);
+  }
+  // Quantize the token's topk rows of h into LDS, as moe_gemv_x_kernel does (eight lanes per
+  // 32-block; the first XT tasks per thread were loaded at the start).
+  for (int base = 0; base < ntask; base += bd) {
     const int task = base + t < ntask ? base + t : ntask - 1;
     const int blk = task >> 3, sub = task & 7;
-    const float4 xv = *reinterpret_cast<const float4 *>(x + (int64_t)blk * 32 + sub * 4);
-    const float v[4] = {xv.x, xv.y, xv.z, xv.w};
+    float4 xq;
+    if (base < XT * bd) {
+#pragma unroll
+      for (int i = 0; i < XT; i++)
+        if (base == i * bd) xq = xv[i];
+    } else {
+      xq = *reinterpret_cast<const float4 *>(x + (int64_t)blk * 32 + sub * 4);
+    }
+    const float v[4] = {xq.x, xq.y, xq.z, xq.w};
     const ActQ q = act_quant8_fast(v);
     if (base + t < ntask) {
       reinterpret_cast<uint32_t *>(lq1 + blk * 32)[sub] = q.q1;
@@ -962,27 +996,11 @@ __global__ __launch_bounds__(512) void moe_down_combine_kernel(MoeCombArgs ma) {
     }
   }
   __syncthreads();
-  const int team = t / a.TP, u = t - team * a.TP;
-  const int slot = team % topk, rloc = team / topk;
-  const bool active = u < a.P && rloc < RPW;
-  const typename U::Lane L = unit_lane<U>(active ? u : 0, a.G);
-  int e = lexp[slot];
-  const bool ok = e >= 0 && e < ma.E;
-  e = ok ? e : 0;
   const int64_t p = (int64_t)tok * topk + slot;
   const float wp = ma.topk_w ? ma.topk_w[p] : 1.f;
   typename U::X xr[1];
   U::load_x(lq1, lq2, reinterpret_cast<const uint8_t *>(lde), reinterpret_cast<const uint8_t *>(lsx),
             slot * KB + L.ja, xr[0]);
-  const uint8_t *w = a.w0 + (int64_t)e * ma.expert_bytes;
-  const int ngroups = (a.N + RPW - 1) / RPW, G = gridDim.x;
-  const int niter = (ngroups - (int)blockIdx.x + G - 1) / G;
-  typename U::W wr;
-  {
-    int row = (int)blockIdx.x * RPW + rloc;
-    row = row < a.N && rloc < RPW ? row : a.N;
-    U::load(w, a.s0, a.z0, a, row, L, wr);
-  }
   for (int it = 0; it < niter; it++) {
     const int grp = (int)blockIdx.x + it * G;
     float c[1];
