@@ -578,7 +578,7 @@ size_t gemm_partial_bytes(int64_t M, int64_t N, int64_t K, bool f32_out) {
     const int s2 = small_int4_splits(N, K);
     old = std::max(old, (s2 > 1 || !f32_out) ? (size_t)s2 * (size_t)M * (size_t)N * 4 : (size_t)0);
   }
-  return std::max(old, gemm_ws_partial_bytes(M, N, K, f32_out));
+  return std::max(std::max(old, gemm_ws_partial_bytes(M, N, K, f32_out)), gemm_q4k2_ws_bytes(M, N, K));
 }
 
 static int launch_small_int4(const uint16_t *xb, const uint32_t *codes, const float *sc, const float *zr, void *out,
@@ -653,7 +653,9 @@ static int launch_gemm_p(const GemmArgs &a, int out_dtype, void *out, float *par
 
 int launch_gemm_q4k_bf16(const uint16_t *xb, const void *w, float *out, float *partials, int64_t M, int64_t N,
                          int64_t K, hipStream_t s) {
-  // M > 64: the warp-specialised kernel (gemm_ws.hip); small M keeps the 64-row tile.
+  // M > 64: the all-waves Q4_K kernel (gemm_q4k.hip), else the warp-specialised kernel
+  // (gemm_ws.hip); small M keeps the 64-row tile.
+  if (gemm_q4k_ok(M, N, K, w, xb)) return launch_gemm_q4k2(xb, w, out, partials, M, N, K, s);
   if (M > 64) return launch_gemm_ws_q4k(xb, w, out, partials, M, N, K, s);
   GemmArgs a = {};
   a.x = xb;

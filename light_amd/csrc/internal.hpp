@@ -56,6 +56,11 @@ bool gemv_fast_ok(int dt, int64_t K, const void *w);
 int launch_gemm_q4k_bf16(const uint16_t *xb, const void *w, float *out, float *partials, int64_t M, int64_t N,
                          int64_t K, hipStream_t s);
 size_t gemm_q4k_ws_bytes(int64_t M, int64_t K);
+// The all-waves Q4_K GEMM (gemm_q4k.hip) for M > 64.
+bool gemm_q4k_ok(int64_t M, int64_t N, int64_t K, const void *w, const void *x);
+size_t gemm_q4k2_ws_bytes(int64_t M, int64_t N, int64_t K);
+int launch_gemm_q4k2(const uint16_t *xb, const void *w, float *out, void *ws, int64_t M, int64_t N, int64_t K,
+                     hipStream_t s);
 size_t gemm_q4k_partial_bytes(int64_t M, int64_t N, int64_t K);
 // src_kind: F32, F16, BF16 (copy) or kActSrc (prepared activations).
 constexpr int kActSrc = -1;
