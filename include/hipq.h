@@ -312,6 +312,23 @@ int hq_moe_route_gated(const float *probs, const float *x, const void *w, float 
                        int64_t *sorted_pairs, int64_t *sorted_expts, int32_t *counts, int32_t *offsets, void *ws,
                        size_t ws_bytes, hq_stream_t stream);
 
+/* ops.MoEInt4 (ops/int4.go:149-246): the routed gated-MLP expert block with canonical 4-bit
+ * experts (GPTQ / AWQ MoE checkpoints):
+ *   y[t] (T, H) = sum over j < topk of w[t*topk+j] * down_e(act(gate_e x[t]) * up_e x[t]),
+ *   e = topk_ids[t*topk+j], the slots added onto zero in slot order, y at x's dtype.
+ * x (T, H) F32 / BF16 / F16.  expert_tab: a DEVICE array of 6*E pointers -- the E gate-up
+ * codes (U32 (2I, H/8), gate rows then up rows), their E scales and E zeros (F32 (2I, H/G)),
+ * then the E down codes (U32 (H, I/8)), scales and zeros (F32 (H, I/G)).  topk_ids I64 and
+ * weights F32 (T*topk) are the routing (MoERouting.TopKIDs / Weights).  Only the routed
+ * experts' rows are read: nothing is expanded (Light dequantizes the used experts into its
+ * weight scratch, ops/int4.go:199-215).  An id outside [0, E) contributes zero (Light
+ * returns "expert out of range").  H and I multiples of 64 with G % 32 == 0 take the int8-dot
+ * GEMV kernels (x and h quantized in the workgroups); other shapes a generic F32 kernel. */
+size_t hq_moe_int4_ws_bytes(int64_t T, int topk, int64_t I);
+int hq_moe_int4(const void *x, int x_dtype, const void *const *expert_tab, int64_t E, const int64_t *topk_ids,
+                const float *weights, void *y, int64_t T, int topk, int64_t H, int64_t I, int G, int act, void *ws,
+                size_t ws_bytes, hq_stream_t stream);
+
 /* y (M, K) = x[:, idx] for 2- or 4-byte elements (ops.gatherColumns, ops/int4.go:129-147):
  * the act-order (desc_act) permutation of quant.Int4.Perm applied to the activations.
  * Indices outside [0, K) give zeros. */

@@ -695,6 +695,38 @@ int hq_moe_route_gated(const float *probs, const float *x, const void *w, float 
                                     sorted_pairs, sorted_expts, counts, offsets, ws, s);
 }
 
+size_t hq_moe_int4_ws_bytes(int64_t T, int topk, int64_t I) {
+  if (T <= 0 || topk < 1 || I <= 0) return 0;
+  return moe_int4_ws_bytes(T, topk, I);
+}
+
+int hq_moe_int4(const void *x, int x_dtype, const void *const *expert_tab, int64_t E, const int64_t *topk_ids,
+                const float *weights, void *y, int64_t T, int topk, int64_t H, int64_t I, int G, int act, void *ws,
+                size_t ws_bytes, hq_stream_t stream) {
+  const char *call = "hq_moe_int4";
+  if (x_dtype != HQ_F32 && x_dtype != HQ_BF16 && x_dtype != HQ_F16)
+    return fail(HQ_EUNSUPPORTED, call, "activations dtype %d, want F32, BF16 or F16", x_dtype);
+  if (act != HQ_ACT_SILU && act != HQ_ACT_GELU_ERF) return fail(HQ_EINVAL, call, "activation %d", act);
+  if (E < 1 || T < 0 || topk < 1 || H <= 0 || I <= 0 || G <= 0)
+    return fail(HQ_EINVAL, call, "x (%lld, %lld), %lld experts, topk %d, I %lld, group %d", (long long)T,
+                (long long)H, (long long)E, topk, (long long)I, G);
+  if (H % G || I % G || H % 8 || I % 8)
+    return fail(HQ_EINVAL, call, "group %d must divide hidden %lld and intermediate %lld (multiples of 8)", G,
+                (long long)H, (long long)I);
+  if (T == 0) return HQ_OK;
+  if (!x || !expert_tab || !topk_ids || !weights || !y) return fail(HQ_EINVAL, call, "NULL pointer");
+  if (((uintptr_t)x & 15) || ((uintptr_t)y & 3)) return fail(HQ_EINVAL, call, "x must be 16-byte aligned");
+  hipStream_t s = resolve(stream);
+  const size_t need = moe_int4_ws_bytes(T, topk, I);
+  if (!ws) {
+    if (int rc = workspace(need, s, &ws, call)) return rc;
+  } else if (ws_bytes < need) {
+    return fail(HQ_ENOMEM, call, "workspace %zu bytes < %zu needed", ws_bytes, need);
+  }
+  TraceSpan span("moe_int4", s);
+  return launch_moe_int4(x, x_dtype, expert_tab, E, topk_ids, weights, y, T, topk, H, I, G, act, ws, s);
+}
+
 int hq_gather_cols(const void *x, const int64_t *idx, void *y, int64_t M, int64_t K, int elem_bytes,
                    hq_stream_t stream) {
   const char *call = "hq_gather_cols";

@@ -1032,6 +1032,239 @@ __global__ __launch_bounds__(512) void moe_down_combine_kernel(MoeCombArgs ma) {
 }
 
 // ---------------------------------------------------------------------------
+// MoEInt4 (ops/int4.go:149-300): the routed gated-MLP expert block with 4-bit (GPTQ / AWQ,
+// canonical quant.Int4) experts.  Each expert is a separate quant.Int4, so the kernels read
+// per-expert (codes, scales, zeros) pointers from device tables, and only the routed experts'
+// rows are read -- nothing is expanded.  Two launches:
+//  * moe_int4_gated_kernel: grid.y = routed pair p = t * topk + j.  h[p, n] =
+//    act(x[t] . Wgu[e][n]) * (x[t] . Wgu[e][I + n]) for n < I (e = ids[p]), x[t] quantized in
+//    LDS, teams streaming gate and up rows together as the gated GEMV does.
+//  * moe_int4_down_kernel: grid.y = token, teams = (row, slot) pairs as in
+//    moe_down_combine_kernel: y[t, n] = 0 + w(t,0) dot_0 + w(t,1) dot_1 + ..., the slots added
+//    in slot order onto zero, as Light's moeInt4Rows does, stored at x's dtype.
+// ---------------------------------------------------------------------------
+struct MoeInt4Args {
+  Q4kxArgs g;                 // K, P, TP, RW, G of the launch; x / out / N set per kernel
+  const void *const *tab;     // [6][E]: gate-up codes, scales, zeros; down codes, scales, zeros
+  const int64_t *ids;         // (T * topk) expert per pair
+  const float *w;             // (T * topk) routing weights
+  float *h;                   // (T * topk, I) F32
+  int E, topk, T, I, H, act, x_dtype;
+};
+
+// Quantize `rows` rows of K elements (x dtype XDT, row r at src + r * K) into the LDS act layout
+// (eight lanes per 32-block, act_quant8_fast), rows after each other.
+template <int XDT>
+__device__ __forceinline__ void quant_rows_lds(const void *src, int rows, int K, uint8_t *smem) {
+  const int KB = K >> 5, t = threadIdx.x;
+  uint8_t *lq1 = smem, *lq2 = smem + (int64_t)rows * K;
+  float2 *lde = reinterpret_cast<float2 *>(smem + 2 * (int64_t)rows * K);
+  float *lsx = reinterpret_cast<float *>(smem + 2 * (int64_t)rows * K + 8 * (int64_t)rows * KB);
+  const int ntask = rows * KB * 8;
+  for (int base = 0; base < ntask; base += (int)blockDim.x) {
+    const int task = base + t < ntask ? base + t : ntask - 1;
+    const int blk = task >> 3, sub = task & 7;
+    const float4 xv = load_x4<XDT>(src, (int64_t)blk * 32 + sub * 4);
+    const float v[4] = {xv.x, xv.y, xv.z, xv.w};
+    const ActQ q = act_quant8_fast(v);
+    if (base + t < ntask) {
+      reinterpret_cast<uint32_t *>(lq1 + blk * 32)[sub] = q.q1;
+      reinterpret_cast<uint32_t *>(lq2 + blk * 32)[sub] = q.q2;
+      if (sub == 0) {
+        lde[blk] = make_float2(q.d, q.e);
+        lsx[blk] = q.sum;
+      }
+    }
+  }
+}
+
+template <class U, int XDT>
+__global__ __launch_bounds__(512) void moe_int4_gated_kernel(MoeInt4Args ma) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  Q4kxArgs a = ma.g;
+  const int t = threadIdx.x, lane = t & 63;
+  const int p = blockIdx.y, tok = p / ma.topk;
+  int64_t e = ma.ids[p];
+  const bool ok = e >= 0 && e < ma.E;
+  e = ok ? e : 0;
+  const uint8_t *wc = static_cast<const uint8_t *>(ma.tab[0 * ma.E + e]);
+  const float *ws = static_cast<const float *>(ma.tab[1 * ma.E + e]);
+  const float *wz = static_cast<const float *>(ma.tab[2 * ma.E + e]);
+  a.N = 2 * ma.I;  // the expert's gate-up rows (the resource spans both halves)
+  const int RW = a.RW, KB = a.K >> 5;
+  const int team = t / a.TP, u = t - team * a.TP;
+  const bool active = u < a.P;
+  const typename U::Lane L = unit_lane<U>(active ? u : 0, a.G);
+  const int ngroups = (ma.I + RW - 1) / RW, G = gridDim.x;
+  const int niter = (ngroups - (int)blockIdx.x + G - 1) / G;
+  typename U::W wr[2];
+  {
+    int row = (int)blockIdx.x * RW + team;
+    row = row < ma.I ? row : a.N;
+    U::load(wc, ws, wz, a, row, L, wr[0]);
+    U::load(wc, ws, wz, a, row < ma.I ? row + ma.I : a.N, L, wr[1]);
+  }
+  quant_rows_lds<XDT>(static_cast<const uint8_t *>(a.x) + (int64_t)tok * a.K * (XDT == F32 ? 4 : 2), 1, a.K,
+                      smem);
+  __syncthreads();
+  typename U::X xr[1];
+  U::load_x(smem, smem + a.K, smem + 2 * a.K, smem + 2 * a.K + 8 * KB, L.ja, xr[0]);
+  for (int it = 0; it < niter; it++) {
+    const int grp = (int)blockIdx.x + it * G;
+    float c[2][1];
+    U::template dot<1>(wr[0], xr, L, c[0]);
+    U::template dot<1>(wr[1], xr, L, c[1]);
+    {
+      int row = (grp + G) * RW + team;
+      const bool in = row < ma.I;
+      U::load(wc, ws, wz, a, in ? row : a.N, L, wr[0]);
+      U::load(wc, ws, wz, a, in ? row + ma.I : a.N, L, wr[1]);
+    }
+    float tot[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const float r16 = rsum16(active ? c[j][0] : 0.f);
+      const float r0 = rl(r16, 0), r1 = rl(r16, 16), r2 = rl(r16, 32), r3 = rl(r16, 48);
+      if (a.TP == 64)
+        tot[j] = ((r0 + r1) + r2) + r3;
+      else if (a.TP == 32)
+        tot[j] = lane < 32 ? r0 + r1 : r2 + r3;
+      else
+        tot[j] = lane < 16 ? r0 : (lane < 32 ? r1 : (lane < 48 ? r2 : r3));
+    }
+    const int row = grp * RW + team;
+    if (u == 0 && row < ma.I) ma.h[(int64_t)p * ma.I + row] = ok ? gate_act(tot[0], ma.act) * tot[1] : 0.f;
+  }
+}
+
+template <class U, int ODT>
+__global__ __launch_bounds__(512) void moe_int4_down_kernel(MoeInt4Args ma) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  Q4kxArgs a = ma.g;  // K = I, N = H
+  const int t = threadIdx.x, lane = t & 63;
+  const int tok = blockIdx.y, topk = ma.topk;
+  const int RW = a.RW, KB = a.K >> 5, RPW = RW / topk;
+  float *lval = reinterpret_cast<float *>(smem + q4kx_act_lds(topk, a.K));
+  const int team = t / a.TP, u = t - team * a.TP;
+  const int slot = team % topk, rloc = team / topk;
+  const bool active = u < a.P;
+  const typename U::Lane L = unit_lane<U>(active ? u : 0, a.G);
+  const int64_t p = (int64_t)tok * topk + slot;
+  int64_t e = ma.ids[p];
+  const bool ok = e >= 0 && e < ma.E;
+  e = ok ? e : 0;
+  const uint8_t *wc = static_cast<const uint8_t *>(ma.tab[3 * ma.E + e]);
+  const float *ws = static_cast<const float *>(ma.tab[4 * ma.E + e]);
+  const float *wz = static_cast<const float *>(ma.tab[5 * ma.E + e]);
+  const int ngroups = (a.N + RPW - 1) / RPW, G = gridDim.x;
+  const int niter = (ngroups - (int)blockIdx.x + G - 1) / G;
+  typename U::W wr;
+  {
+    int row = (int)blockIdx.x * RPW + rloc;
+    row = row < a.N ? row : a.N;
+    U::load(wc, ws, wz, a, row, L, wr);
+  }
+  quant_rows_lds<F32>(ma.h + (int64_t)tok * topk * a.K, topk, a.K, smem);
+  __syncthreads();
+  const float wp = ma.w[p];
+  typename U::X xr[1];
+  U::load_x(smem, smem + (int64_t)topk * a.K, smem + 2 * (int64_t)topk * a.K,
+            smem + 2 * (int64_t)topk * a.K + 8 * (int64_t)topk * KB, slot * KB + L.ja, xr[0]);
+  for (int it = 0; it < niter; it++) {
+    const int grp = (int)blockIdx.x + it * G;
+    float c[1];
+    U::template dot<1>(wr, xr, L, c);
+    {
+      int row = (grp + G) * RPW + rloc;
+      row = row < a.N ? row : a.N;
+      U::load(wc, ws, wz, a, row, L, wr);
+    }
+    const float r16 = rsum16(active ? c[0] : 0.f);
+    const float r0 = rl(r16, 0), r1 = rl(r16, 16), r2 = rl(r16, 32), r3 = rl(r16, 48);
+    float tot;
+    if (a.TP == 64)
+      tot = ((r0 + r1) + r2) + r3;
+    else if (a.TP == 32)
+      tot = lane < 32 ? r0 + r1 : r2 + r3;
+    else
+      tot = lane < 16 ? r0 : (lane < 32 ? r1 : (lane < 48 ? r2 : r3));
+    float *vb = lval + (it & 1) * (RPW * topk);
+    if (u == 0) vb[rloc * topk + slot] = ok ? __fmul_rn(wp, tot) : 0.f;
+    __syncthreads();
+    const int row = grp * RPW + t;
+    if (t < RPW && row < a.N) {
+      float acc = 0.f;
+      for (int s2 = 0; s2 < topk; s2++) acc = __fadd_rn(acc, vb[t * topk + s2]);
+      store_out<ODT>(a.out, (int64_t)tok * a.N + row, acc);
+    }
+  }
+}
+
+// Generic MoEInt4 (any H, I multiple of 8 and of G): one wave per output, F32 x, the weight
+// decoded on the fly exactly as quant.Int4.Dequant does (s * (q - z), quant/int4.go:239-261),
+// F32 products summed lane-strided then by a wave reduction.  Used where the GEMV's
+// 64-element units do not tile the shapes.
+__device__ __forceinline__ float int4_w(const uint32_t *codes, const float *sc, const float *zr, int64_t n,
+                                        int64_t k, int64_t K, int G) {
+  const uint32_t q = (codes[n * (K / 8) + k / 8] >> (4 * (k & 7))) & 15u;
+  const int64_t gi = n * (K / G) + k / G;
+  return __fmul_rn(sc[gi], __fsub_rn((float)q, zr[gi]));
+}
+
+template <int XDT>
+__global__ __launch_bounds__(256) void moe_int4_generic_gated_kernel(MoeInt4Args ma) {
+  const int lane = threadIdx.x & 63;
+  const int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // output (pair, row)
+  const int64_t M = (int64_t)ma.T * ma.topk;
+  if (gw >= M * ma.I) return;
+  const int64_t p = gw / ma.I, n = gw % ma.I, tok = p / ma.topk;
+  int64_t e = ma.ids[p];
+  const bool ok = e >= 0 && e < ma.E;
+  e = ok ? e : 0;
+  const auto *wc = static_cast<const uint32_t *>(ma.tab[0 * ma.E + e]);
+  const auto *ws = static_cast<const float *>(ma.tab[1 * ma.E + e]);
+  const auto *wz = static_cast<const float *>(ma.tab[2 * ma.E + e]);
+  float g = 0.f, u = 0.f;
+  for (int64_t k = lane; k < ma.H; k += 64) {
+    float xv;
+    if constexpr (XDT == F32)
+      xv = static_cast<const float *>(ma.g.x)[tok * ma.H + k];
+    else if constexpr (XDT == BF16)
+      xv = bf2f(static_cast<const uint16_t *>(ma.g.x)[tok * ma.H + k]);
+    else
+      xv = h2f(static_cast<const uint16_t *>(ma.g.x)[tok * ma.H + k]);
+    g = __fmaf_rn(xv, int4_w(wc, ws, wz, n, k, ma.H, ma.g.G), g);
+    u = __fmaf_rn(xv, int4_w(wc, ws, wz, n + ma.I, k, ma.H, ma.g.G), u);
+  }
+  g = wave_sum(g);
+  u = wave_sum(u);
+  if (lane == 0) ma.h[p * ma.I + n] = ok ? gate_act(g, ma.act) * u : 0.f;
+}
+
+template <int ODT>
+__global__ __launch_bounds__(256) void moe_int4_generic_down_kernel(MoeInt4Args ma) {
+  const int lane = threadIdx.x & 63;
+  const int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // output (token, row)
+  if (gw >= (int64_t)ma.T * ma.H) return;
+  const int64_t tok = gw / ma.H, n = gw % ma.H;
+  float acc = 0.f;
+  for (int j = 0; j < ma.topk; j++) {
+    const int64_t p = tok * ma.topk + j;
+    int64_t e = ma.ids[p];
+    const bool ok = e >= 0 && e < ma.E;
+    e = ok ? e : 0;
+    const auto *wc = static_cast<const uint32_t *>(ma.tab[3 * ma.E + e]);
+    const auto *ws = static_cast<const float *>(ma.tab[4 * ma.E + e]);
+    const auto *wz = static_cast<const float *>(ma.tab[5 * ma.E + e]);
+    float y = 0.f;
+    for (int64_t k = lane; k < ma.I; k += 64) y = __fmaf_rn(ma.h[p * ma.I + k], int4_w(wc, ws, wz, n, k, ma.I, ma.g.G), y);
+    y = wave_sum(y);
+    acc = __fadd_rn(acc, ok ? __fmul_rn(ma.w[p], y) : 0.f);
+  }
+  if (lane == 0) store_out<ODT>(ma.g.out, tok * ma.H + n, acc);
+}
+
+// ---------------------------------------------------------------------------
 // Launch
 // ---------------------------------------------------------------------------
 
@@ -1472,6 +1705,91 @@ int launch_moe_route_gated(const float *probs, const float *x, const void *w, fl
   if (dt == Q5_K)
     return avg <= 1 ? run_moe_x<Q5kUnit, 1, true, true>(ma, active, s) : run_moe_x<Q5kUnit, 2, true, true>(ma, active, s);
   return avg <= 1 ? run_moe_x<Q4kUnit, 1, true, true>(ma, active, s) : run_moe_x<Q4kUnit, 2, true, true>(ma, active, s);
+}
+
+// MoEInt4 on the decode GEMV machinery: H and I multiples of 64, G % 32 == 0, topk teams of
+// the down projection fit a workgroup.
+bool moe_int4_ok(int64_t H, int64_t I, int G, int topk) {
+  int P, TP, RW;
+  if (H % 64 || I % 64 || G <= 0 || G % 32 || H % G || I % G || topk < 1 || topk > 64) return false;
+  if (!q4kx_geom(H, 64, &P, &TP, &RW) || TP > 64) return false;
+  if (!q4kx_geom(I, 64, &P, &TP, &RW) || TP > 64 || RW % topk) return false;
+  return q4kx_act_lds(topk, I) + 2 * 4 * 64 <= 64 * 1024;
+}
+
+size_t moe_int4_ws_bytes(int64_t T, int topk, int64_t I) { return (size_t)(T * topk * I * 4 + 255) & ~(size_t)255; }
+
+int launch_moe_int4(const void *x, int x_dtype, const void *const *tab, int64_t E, const int64_t *ids,
+                    const float *w, void *y, int64_t T, int topk, int64_t H, int64_t I, int G, int act, void *ws,
+                    hipStream_t s) {
+  MoeInt4Args ma;
+  ma.tab = tab;
+  ma.ids = ids;
+  ma.w = w;
+  ma.h = static_cast<float *>(ws);
+  ma.E = (int)E;
+  ma.topk = topk;
+  ma.T = (int)T;
+  ma.I = (int)I;
+  ma.H = (int)H;
+  ma.act = act;
+  ma.x_dtype = x_dtype;
+  const int64_t M = T * topk;
+  if (!moe_int4_ok(H, I, G, topk)) {
+    ma.g.G = G;
+    ma.g.x = x;
+    ma.g.out = y;
+    const unsigned b1 = (unsigned)cdiv(M * I, 4), b2 = (unsigned)cdiv(T * H, 4);
+    switch (x_dtype) {
+      case F32: moe_int4_generic_gated_kernel<F32><<<b1, 256, 0, s>>>(ma); break;
+      case BF16: moe_int4_generic_gated_kernel<BF16><<<b1, 256, 0, s>>>(ma); break;
+      default: moe_int4_generic_gated_kernel<F16><<<b1, 256, 0, s>>>(ma); break;
+    }
+    if (int rc = check_launch("moe_int4_gated")) return rc;
+    switch (x_dtype) {
+      case F32: moe_int4_generic_down_kernel<F32><<<b2, 256, 0, s>>>(ma); break;
+      case BF16: moe_int4_generic_down_kernel<BF16><<<b2, 256, 0, s>>>(ma); break;
+      default: moe_int4_generic_down_kernel<F16><<<b2, 256, 0, s>>>(ma); break;
+    }
+    return check_launch("moe_int4_down");
+  }
+  // Gate / up: K = H, rows I (x2); one workgroup column per routed pair.
+  if (int rc = q4kx_setup(ma.g, 1, 2 * I, H, 64, H / 2, "moe_int4")) return rc;
+  ma.g.G = G;
+  ma.g.x = x;
+  {
+    const int ngroups = (int)cdiv(I, ma.g.RW);
+    int64_t per = cdiv((int64_t)device_cus() * 2, M);
+    per = per < ngroups ? per : ngroups;
+    per = cdiv(ngroups, cdiv(ngroups, per));
+    dim3 grid((unsigned)per, (unsigned)M);
+    const size_t lds = (size_t)q4kx_act_lds(1, H);
+    const unsigned thr = ma.g.TP * ma.g.RW;
+    switch (x_dtype) {
+      case F32: moe_int4_gated_kernel<Int4Unit, F32><<<grid, thr, lds, s>>>(ma); break;
+      case BF16: moe_int4_gated_kernel<Int4Unit, BF16><<<grid, thr, lds, s>>>(ma); break;
+      default: moe_int4_gated_kernel<Int4Unit, F16><<<grid, thr, lds, s>>>(ma); break;
+    }
+    if (int rc = check_launch("moe_int4_gated")) return rc;
+  }
+  // Down: K = I, rows H; token-major with the slots combined in the epilogue.
+  if (int rc = q4kx_setup(ma.g, 1, H, I, 64, I / 2, "moe_int4")) return rc;
+  ma.g.G = G;
+  ma.g.out = y;
+  const int RPW = ma.g.RW / topk;
+  const int64_t ngroups = cdiv(H, RPW);
+  int64_t per = cdiv((int64_t)device_cus() * 2, T);
+  per = per < ngroups ? per : ngroups;
+  per = cdiv(ngroups, cdiv(ngroups, per));
+  dim3 grid((unsigned)per, (unsigned)T);
+  const size_t lds = (size_t)q4kx_act_lds(topk, I) + 2 * (size_t)RPW * topk * 4;
+  const unsigned thr = ma.g.TP * ma.g.RW;
+  switch (x_dtype) {
+    case F32: moe_int4_down_kernel<Int4Unit, F32><<<grid, thr, lds, s>>>(ma); break;
+    case BF16: moe_int4_down_kernel<Int4Unit, BF16><<<grid, thr, lds, s>>>(ma); break;
+    default: moe_int4_down_kernel<Int4Unit, F16><<<grid, thr, lds, s>>>(ma); break;
+  }
+  return check_launch("moe_int4_down");
 }
 
 }  // namespace hq

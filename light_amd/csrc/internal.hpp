@@ -133,6 +133,11 @@ int launch_moe_route_gated(const float *probs, const float *x, const void *w, fl
                            int topk, int normalize, int64_t I, int64_t K, int dt, int act, int64_t *topk_ids,
                            float *weights, int64_t *sorted_pairs, int64_t *sorted_expts, int32_t *counts,
                            int32_t *offsets, hipStream_t s);
+bool moe_int4_ok(int64_t H, int64_t I, int G, int topk);
+size_t moe_int4_ws_bytes(int64_t T, int topk, int64_t I);
+int launch_moe_int4(const void *x, int x_dtype, const void *const *tab, int64_t E, const int64_t *ids,
+                    const float *w, void *y, int64_t T, int topk, int64_t H, int64_t I, int G, int act, void *ws,
+                    hipStream_t s);
 bool moe_comb_ok(int64_t M, int64_t T, int topk, int64_t K, int dt, const void *w, const void *x);
 int launch_moe_down_combine(const float *h, const void *w, const int64_t *pairs, const int64_t *expts,
                             int32_t *counts, int32_t *offsets, const float *topk_w, float *y, int topk, int64_t T,

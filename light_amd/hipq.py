@@ -83,6 +83,8 @@ SIGNATURES = {
     "hq_moe_gemm_q_gated": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _I,
                                  _P, _SZ, _P]),
     "hq_gather_cols": (_I, [_P, _P, _P, _I64, _I64, _I, _P]),
+    "hq_moe_int4_ws_bytes": (_SZ, [_I64, _I, _I64]),
+    "hq_moe_int4": (_I, [_P, _I, _P, _I64, _P, _P, _P, _I64, _I, _I64, _I64, _I, _I, _P, _SZ, _P]),
     "hq_moe_route_gated_ws_bytes": (_SZ, [_I64, _I, _I64, _I64, _I64, _I]),
     "hq_moe_route_gated": (_I, [_P, _P, _P, _P, _I64, _I64, _I, _I, _I64, _I64, _I, _I, _P, _P, _P, _P, _P, _P, _P,
                                 _SZ, _P]),
@@ -352,6 +354,25 @@ def moe_route_gated(probs, x, w, E, I, K, w_dtype, topk, normalize=True, act=ACT
                                    w_dtype, act, _ptr(ids), _ptr(wt), _ptr(sp), _ptr(se), _ptr(counts),
                                    _ptr(offsets), _ptr(ws), ws_bytes, _stream(stream)))
     return ids, wt, sp, se, h
+
+
+def moe_int4(x, gate_up, down, topk_ids, weights, topk, G, act=ACT_SILU, out=None, ws=None, stream=None):
+    """ops.MoEInt4: x (T, H); gate_up / down: lists of E (codes, scales, zeros) device tensors
+    (gate-up (2I, H/8) codes, down (H, I/8)); topk_ids I64 / weights F32 (T*topk)."""
+    import torch
+    T, H = x.shape
+    E = len(gate_up)
+    I = down[0][0].shape[1] * 8
+    tab = torch.tensor([t.data_ptr() for part in range(3) for t in (gu[part] for gu in gate_up)] +
+                       [t.data_ptr() for part in range(3) for t in (dn[part] for dn in down)],
+                       dtype=torch.int64).to(x.device)
+    xdt = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}[x.dtype]
+    if out is None:
+        out = torch.empty((T, H), dtype=x.dtype, device=x.device)
+    ws_bytes = 0 if ws is None else ws.numel() * ws.element_size()
+    check(lib().hq_moe_int4(_ptr(x), xdt, _ptr(tab), E, _ptr(topk_ids), _ptr(weights), _ptr(out), T, topk, H, I, G,
+                            act, _ptr(ws), ws_bytes, _stream(stream)))
+    return out
 
 
 def moe_route(probs, topk, normalize=True, counts=None, offsets=None, stream=None):

@@ -305,3 +305,33 @@ def matmul_f64(x, w, threads=0):
     xn = np.zeros(M, np.float64)
     lib().or_matmul_f64(_p(x), _p(w), M, N, K, _p(ref), _p(mag), _p(wn), _p(xn), threads)
     return ref, mag, wn, xn
+
+
+def moe_int4(x, gate_up, down, ids, w, topk, G, act=0, threads=0):
+    """Light's CPU MoEInt4 with F32 activations (moeInt4Rows, ops/int4.go:284-343): for each
+    expert in first-use order, its routed rows of x through the fused int4 MatMulInt4
+    (gate-up, (R, 2I)), act(gate) * up, MatMulInt4 with down, times the pair's weight; then
+    per token out = 0 + pair[slot 0] + pair[slot 1] + ... in slot order.
+    gate_up / down: lists of (codes, scales, zeros) numpy arrays per expert."""
+    x = _c(x, np.float32)
+    T, H = x.shape
+    ids = np.asarray(ids, np.int64).ravel()
+    w = np.asarray(w, np.float32).ravel()
+    I = down[0][0].shape[1] * 8
+    used = list(dict.fromkeys(int(e) for e in ids))
+    pair = np.zeros((ids.size, H), np.float32)
+    for e in used:
+        r = [i for i, v in enumerate(ids) if v == e]
+        xg = np.ascontiguousarray(x[[i // topk for i in r]])
+        c, sc, zr = gate_up[e]
+        gu = int4_matmul(xg, c, sc, zr, 2 * I, H, G, threads)
+        h = gated(np.ascontiguousarray(gu[:, :I]), np.ascontiguousarray(gu[:, I:]), act)
+        c, sc, zr = down[e]
+        y = int4_matmul(h, c, sc, zr, H, I, G, threads)
+        for j, i in enumerate(r):
+            pair[i] = (w[i] * y[j]).astype(np.float32)
+    out = np.zeros((T, H), np.float32)
+    for t in range(T):
+        for j in range(topk):
+            out[t] = (out[t] + pair[t * topk + j]).astype(np.float32)
+    return out

@@ -115,3 +115,48 @@ def test_matmul_int4_benchmark_configs(dev, name):
     x = synth.activations(M, K, g)
     rows = None if M == 1 else np.arange(0, M, 4)
     _check(dev, x, codes, s, z, G, hipq.F16, rows=rows)
+
+
+def _int4_experts(g, E, N, K, G, dev):
+    host = [synth.int4_weight(N, K, G, g) for _ in range(E)]
+    return host, [tuple(torch.from_numpy(a).to(dev) for a in w) for w in host]
+
+
+@pytest.mark.parametrize("T,E,topk,H,I,G,xdt", [
+    (5, 4, 2, 64, 32, 32, torch.float32),        # TestMoEInt4MatchesDense's shape: the generic kernel
+    (1, 16, 4, 2048, 768, 128, torch.float16),   # decode: the int8-dot GEMV kernels
+    (1, 16, 4, 2048, 768, 128, torch.float32),
+    (3, 8, 2, 1024, 512, 64, torch.bfloat16),
+    (2, 8, 8, 512, 256, 32, torch.float32),      # topk 8: four rows x eight slots per workgroup
+])
+def test_moe_int4_vs_light_cpu(dev, T, E, topk, H, I, G, xdt):
+    """hq_moe_int4 against the restated CPU MoEInt4 (oracle.moe_int4, ops/int4.go:284-343) and
+    an f64 dense block on the dequantized experts.  Bar: |y - y_ref| <= 5e-3 max_n |y_ref[t]|
+    per token (x and h are quantized to two-level int8 on the GPU; BF16 / F16 outputs add their
+    rounding)."""
+    print(f"[case] moe_int4 T={T} E={E} topk={topk} H={H} I={I} G={G} x={xdt}", flush=True)
+    g = synth.rng(3000 + T + H + I)
+    gu_h, gu_d = _int4_experts(g, E, 2 * I, H, G, dev)
+    dn_h, dn_d = _int4_experts(g, E, H, I, G, dev)
+    ids = np.concatenate([g.choice(E, size=topk, replace=False) for _ in range(T)]).astype(np.int64)
+    w = g.random(T * topk).astype(np.float32)
+    x = g.standard_normal((T, H)).astype(np.float32)
+    xt = torch.from_numpy(x).to(xdt)
+    xw = xt.float().numpy()
+    got = hipq.moe_int4(xt.to(dev), gu_d, dn_d, torch.from_numpy(ids).to(dev), torch.from_numpy(w).to(dev), topk, G)
+    torch.cuda.synchronize()
+    got = got.float().cpu().numpy()
+    want = oracle.moe_int4(xw, gu_h, dn_h, ids, w, topk, G)
+    tol = 5e-3 if xdt == torch.float32 else 8e-3
+    for t in range(T):
+        scale = np.abs(want[t]).max() + 1e-30
+        assert np.max(np.abs(got[t] - want[t])) <= tol * scale, t
+    # f64 dense on the dequantized experts (first token)
+    ref = np.zeros(H)
+    for j in range(topk):
+        e = ids[j]
+        wg = oracle.int4_dequant(*gu_h[e], 2 * I, H, G).astype(np.float64)
+        wd = oracle.int4_dequant(*dn_h[e], H, I, G).astype(np.float64)
+        gg, uu = wg[:I] @ xw[0].astype(np.float64), wg[I:] @ xw[0].astype(np.float64)
+        ref += float(w[j]) * (wd @ (gg / (1 + np.exp(-gg)) * uu))
+    assert np.max(np.abs(got[0] - ref)) <= tol * (np.abs(ref).max() + 1e-30)

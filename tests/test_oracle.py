@@ -405,3 +405,57 @@ def test_moe_route_pinned(T, E, topk, normalize):
     order = np.argsort(ids.reshape(-1), kind="stable")
     assert np.array_equal(sp, order) and np.array_equal(se, ids.reshape(-1)[order])
     assert np.all(np.diff(se) >= 0) and np.array_equal(np.sort(sp), np.arange(T * topk))
+
+
+def _light_int4(g, N, K, G):
+    """randomInt4 of ops/int4_test.go:16-32: random code words, s ~ U[1e-3, 2.1e-2), z ~ U{0..15}."""
+    codes = g.integers(0, 2 ** 32, size=(N, K // 8), dtype=np.uint64).astype(np.uint32)
+    s = (g.random((N, K // G)) * 0.02 + 1e-3).astype(np.float32)
+    z = g.integers(0, 16, size=(N, K // G)).astype(np.float32)
+    return codes, s, z
+
+
+@pytest.mark.parametrize("seed", [7, 8])
+def test_moe_int4_matches_dense(seed):
+    """TestMoEInt4MatchesDense (ops/int4_test.go:150-206): the restated CPU MoEInt4 against
+    sum_j w_j * down_e(silu(gate_e x) * up_e x) in f64 on the dequantized experts, within
+    Light's 1e-4 (1 + |want|)."""
+    T, H, I, E, topk, G = 5, 64, 32, 4, 2, 32
+    g = np.random.default_rng(seed)
+    gu = [_light_int4(g, 2 * I, H, G) for _ in range(E)]
+    dn = [_light_int4(g, H, I, G) for _ in range(E)]
+    x = g.standard_normal((T, H)).astype(np.float32)
+    ids = np.array([0, 2, 2, 1, 3, 0, 2, 3, 1, 2], np.int64)
+    ws = g.random(T * topk).astype(np.float32)
+    got = oracle.moe_int4(x, gu, dn, ids, ws, topk, G)
+    for t in range(T):
+        want = np.zeros(H)
+        for j in range(topk):
+            e = ids[t * topk + j]
+            wg = oracle.int4_dequant(*gu[e], 2 * I, H, G).astype(np.float64)
+            wd = oracle.int4_dequant(*dn[e], H, I, G).astype(np.float64)
+            gg = wg[:I] @ x[t].astype(np.float64)
+            uu = wg[I:] @ x[t].astype(np.float64)
+            h = gg / (1 + np.exp(-gg)) * uu
+            want += float(ws[t * topk + j]) * (wd @ h)
+        assert np.all(np.abs(got[t] - want) <= 1e-4 * (1 + np.abs(want))), t
+
+
+def test_moe_int4_slot_order_sum():
+    """The pair rows are added onto zero in slot order (moeInt4Rows' o[k] += p[k]): with one
+    expert routed twice per token the result is exactly 0 + w0 y + w1 y in f32."""
+    T, H, I, E, topk, G = 2, 64, 64, 2, 2, 32
+    g = np.random.default_rng(3)
+    gu = [_light_int4(g, 2 * I, H, G) for _ in range(E)]
+    dn = [_light_int4(g, H, I, G) for _ in range(E)]
+    x = g.standard_normal((T, H)).astype(np.float32)
+    ids = np.array([1, 1, 0, 0], np.int64)
+    ws = np.array([0.25, 0.75, 0.5, 0.125], np.float32)
+    got = oracle.moe_int4(x, gu, dn, ids, ws, topk, G)
+    for t, e in ((0, 1), (1, 0)):
+        gu_e = oracle.int4_matmul(x[t:t + 1], *gu[e], 2 * I, H, G)
+        h = oracle.gated(gu_e[:, :I].copy(), gu_e[:, I:].copy(), 0)
+        y = oracle.int4_matmul(h, *dn[e], H, I, G)[0]
+        want = (np.float32(0) + ws[2 * t] * y).astype(np.float32)
+        want = (want + ws[2 * t + 1] * y).astype(np.float32)
+        assert np.array_equal(got[t], want)
