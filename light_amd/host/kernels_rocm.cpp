@@ -78,6 +78,15 @@ void moe_gemm_q_gated(Context &c) {
                             c.attr("gelu") ? HQ_ACT_GELU_ERF : HQ_ACT_SILU, nullptr, 0, nullptr));
 }
 
+// ops.MoEInt4: inputs {x, expert pointer table U64 (6E), topk_ids, weights}.
+void moe_int4(Context &c) {
+  const Tensor &x = c.in(0), &tab = c.in(1), &ids = c.in(2), &w = c.in(3);
+  Check(hq_moe_int4(x.data(), (int)x.dtype(), static_cast<const void *const *>(tab.data()), tab.Dim(0) / 6,
+                    static_cast<const int64_t *>(ids.data()), static_cast<const float *>(w.data()), c.output.data(),
+                    x.Dim(0), (int)c.attr("topk"), x.Dim(1), c.attr("inter"), (int)c.attr("group"),
+                    c.attr("gelu") ? HQ_ACT_GELU_ERF : HQ_ACT_SILU, nullptr, 0, nullptr));
+}
+
 void dequant(Context &c) {
   const Tensor &w = c.in(0);
   Check(hq_dequant(w.data(), c.output.data(), w.NumElements(), (int)w.dtype(), HQ_F32, nullptr));
@@ -97,6 +106,7 @@ struct Registrar {
     Register(Key{"moe_sort", DeviceKind::ROCm, DType::I64}, moe_sort);
     for (DType dt : {DType::F32, DType::BF16, DType::F16}) Register(Key{"int4_gemv", DeviceKind::ROCm, dt}, int4_gemv);
     for (DType dt : {DType::F32, DType::BF16}) Register(Key{"int4_dequant", DeviceKind::ROCm, dt}, int4_dequant);
+    for (DType dt : {DType::F32, DType::BF16, DType::F16}) Register(Key{"moe_int4", DeviceKind::ROCm, dt}, moe_int4);
   }
 };
 const Registrar registrar;

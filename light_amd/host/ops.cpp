@@ -301,6 +301,50 @@ Tensor MoECombine(const Tensor &pair_out, int topk) {
   return out;
 }
 
+// ---- MoEInt4 (ops/int4.go:149-246) ----
+
+Tensor MoEInt4(const Tensor &x, const std::vector<Int4> &gate_up, const std::vector<Int4> &down,
+               const MoERouting &routing, int topk, bool gelu) {
+  if (x.Rank() != 2 || gate_up.empty() || gate_up.size() != down.size())
+    Fail("ops.MoEInt4: x %s, %zu gate-up / %zu down experts", x.ShapeStr().c_str(), gate_up.size(), down.size());
+  const int64_t T = x.Dim(0), H = x.Dim(1), I2 = gate_up[0].N(), I = down[0].K();
+  if (gate_up[0].K() != H || down[0].N() != H || I2 != 2 * I)
+    Fail("ops.MoEInt4: expert shapes gate-up (%lld, %lld), down (%lld, %lld) for hidden %lld", (long long)I2,
+         (long long)gate_up[0].K(), (long long)down[0].N(), (long long)I, (long long)H);
+  const int G = gate_up[0].group;
+  std::vector<uint64_t> tab(6 * gate_up.size());
+  const size_t E = gate_up.size();
+  for (size_t e = 0; e < E; e++) {
+    const Int4 &gu = gate_up[e], &dn = down[e];
+    // The fused kernel reads every expert with expert 0's geometry: all must share it.
+    if (gu.N() != I2 || gu.K() != H || dn.N() != H || dn.K() != I || gu.group != G || dn.group != G ||
+        gu.perm || dn.perm)
+      Fail("ops.MoEInt4: expert %zu differs from expert 0 (shapes, group or act-order)", e);
+    for (const Tensor *t : {&gu.codes, &gu.scales, &gu.zeros, &dn.codes, &dn.scales, &dn.zeros})
+      if (!same_device(*t, x)) Fail("ops.MoEInt4: expert %zu on %s, x on %s", e, t->device().str().c_str(),
+                                    x.device().str().c_str());
+    tab[0 * E + e] = (uint64_t)(uintptr_t)gu.codes.data();
+    tab[1 * E + e] = (uint64_t)(uintptr_t)gu.scales.data();
+    tab[2 * E + e] = (uint64_t)(uintptr_t)gu.zeros.data();
+    tab[3 * E + e] = (uint64_t)(uintptr_t)dn.codes.data();
+    tab[4 * E + e] = (uint64_t)(uintptr_t)dn.scales.data();
+    tab[5 * E + e] = (uint64_t)(uintptr_t)dn.zeros.data();
+  }
+  if (routing.topk_ids.NumElements() != T * topk || routing.weights.NumElements() != T * topk)
+    Fail("ops.MoEInt4: routing holds %lld ids for %lld tokens x topk %d", (long long)routing.topk_ids.NumElements(),
+         (long long)T, topk);
+  Tensor table = Tensor::FromHost(tab.data(), tab.size() * 8, DType::U64, {(int64_t)tab.size()}, x.device());
+  Kernel k = Lookup(Key{"moe_int4", x.device().kind, x.dtype()});
+  Tensor out = Tensor::Empty(x.dtype(), {T, H}, x.device());
+  Context ctx;
+  ctx.inputs = {x, table, routing.topk_ids, routing.weights};
+  ctx.output = out;
+  ctx.attrs = {{"topk", Attr::Int(topk)}, {"group", Attr::Int(G)}, {"inter", Attr::Int(I)},
+               {"gelu", Attr::Bool(gelu)}};
+  k(ctx);
+  return out;
+}
+
 // ---- Dequantize (quant/dequant.go:10-42, dispatchRegistry quant/cuda_hook.go:51-69) ----
 
 Tensor Dequantize(const Tensor &w) {

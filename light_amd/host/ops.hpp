@@ -53,6 +53,11 @@ Tensor MoEGemmQ(const Tensor &x, const Tensor &w, const MoERouting &routing, con
 // The routed gated gate/up of nn.SparseMoE.runExperts (nn/moe.go:196-236): w (E, 2I, K)
 // stacked gate/up, output (M, I) = act(gate) * up ("moe_gemm_q_gated", keyed by w's dtype).
 Tensor MoEGemmQGated(const Tensor &x, const Tensor &w, const MoERouting &routing, int topk, bool gelu);
+// ops.MoEInt4 (ops/int4.go:149-246): x (T, H) F32 / BF16 / F16, per-expert gate-up (2I, H) and
+// down (H, I) canonical 4-bit weights, the routing's TopKIDs / Weights; act = SiLU or GELU
+// (erf).  Returns (T, H) at x's dtype ("moe_int4" registry key, keyed by x's dtype).
+Tensor MoEInt4(const Tensor &x, const std::vector<Int4> &gate_up, const std::vector<Int4> &down,
+               const MoERouting &routing, int topk, bool gelu);
 // ops.MoECombine (ops/moe.go:206-240).
 Tensor MoECombine(const Tensor &pair_out, int topk);
 

@@ -212,6 +212,18 @@ PYBIND11_MODULE(_light, m) {
   m.def("moe_gemm_q_gated", &ops::MoEGemmQGated, py::arg("x"), py::arg("w"), py::arg("routing"), py::arg("topk"),
         py::arg("gelu") = false);
   m.def("moe_combine", &ops::MoECombine);
+  m.def(
+      "moe_int4",
+      [](const Tensor &x, const std::vector<std::tuple<Tensor, Tensor, Tensor>> &gate_up,
+         const std::vector<std::tuple<Tensor, Tensor, Tensor>> &down, const ops::MoERouting &routing, int topk,
+         int group, bool gelu) {
+        std::vector<ops::Int4> gu, dn;
+        for (const auto &w : gate_up) gu.push_back(make_int4(std::get<0>(w), std::get<1>(w), std::get<2>(w), group, {}));
+        for (const auto &w : down) dn.push_back(make_int4(std::get<0>(w), std::get<1>(w), std::get<2>(w), group, {}));
+        return ops::MoEInt4(x, gu, dn, routing, topk, gelu);
+      },
+      py::arg("x"), py::arg("gate_up"), py::arg("down"), py::arg("routing"), py::arg("topk"), py::arg("group"),
+      py::arg("gelu") = false);
   m.def("dequantize", &ops::Dequantize);
 
   // GGUF byte path

@@ -149,3 +149,24 @@ def test_moe_route_and_gated_host(gelu):
     pr = oracle.moe_gemm_q(hr, wdn, hipq.Q4_K, E, H, I, rsp, rse, topk, topk_w=rw)
     want = oracle.moe_combine(pr, topk)
     assert np.max(np.abs(y.numpy() - want)) <= 5e-3 * np.abs(want).max()
+
+
+@pytest.mark.parametrize("T,E,topk,H,I,G", [(5, 4, 2, 64, 32, 32), (1, 16, 4, 2048, 768, 128)])
+def test_moe_int4_host_op(T, E, topk, H, I, G):
+    """ops.MoEInt4 through the registry (ROCm "moe_int4") against Light's CPU MoEInt4 restated
+    (oracle.moe_int4); the routing comes from ops.MoERouteFromIDs."""
+    print(f"[case] host MoEInt4 T={T} E={E} topk={topk} H={H} I={I}", flush=True)
+    g = synth.rng(700 + T + H)
+    gu = [synth.int4_weight(2 * I, H, G, g) for _ in range(E)]
+    dn = [synth.int4_weight(H, I, G, g) for _ in range(E)]
+    ids = np.concatenate([g.choice(E, size=topk, replace=False) for _ in range(T)]).astype(np.int64)
+    w = g.random(T * topk).astype(np.float32)
+    x = g.standard_normal((T, H)).astype(np.float32)
+    r = L.moe_route_from_ids(ids.tolist(), w.tolist(), T, topk, DEV)
+    wrap = lambda ws: [tuple(dev_t(a, "U32" if a.dtype == np.uint32 else "F32", a.shape) for a in t) for t in ws]
+    y = L.moe_int4(dev_t(x, "F32", (T, H)), wrap(gu), wrap(dn), r, topk, G)
+    assert y.shape == [T, H] and y.dtype == "F32"
+    got = y.numpy()
+    want = oracle.moe_int4(x, gu, dn, ids, w, topk, G)
+    for t in range(T):
+        assert np.max(np.abs(got[t] - want[t])) <= 5e-3 * (np.abs(want[t]).max() + 1e-30), t

@@ -172,3 +172,21 @@ def test_moe_route_checks():
         L.moe_route(f32(3, 4), 5)
     with pytest.raises(L.KernelNotFound, match="moe_route/CPU/F32"):
         L.moe_route(f32(3, 4), 2)
+
+
+def test_moe_int4_validation():
+    """ops.MoEInt4's argument checks and messages (ops/int4.go:159-167)."""
+    x = f32(2, 64)
+    c = L.from_numpy(np.zeros((64, 8), np.uint32), "U32", [64, 8])
+    s = f32(64, 2)
+    r = L.moe_route_from_ids([0, 0], [1.0, 1.0], 2, 1, "CPU")
+    with pytest.raises(L.Error, match=r"ops.MoEInt4: x \[2 64\], 1 gate-up / 0 down experts"):
+        L.moe_int4(x, [(c, s, s)], [], r, 1, 32)
+    cd = L.from_numpy(np.zeros((64, 4), np.uint32), "U32", [64, 4])
+    sd = f32(64, 1)
+    c60 = L.from_numpy(np.zeros((60, 8), np.uint32), "U32", [60, 8])
+    with pytest.raises(L.Error, match=r"ops.MoEInt4: expert shapes gate-up \(60, 64\), down \(64, 32\) for hidden 64"):
+        L.moe_int4(x, [(c60, s, s)], [(cd, sd, sd)], r, 1, 32)
+    # Valid shapes on the CPU: this build registers the kernel for ROCm only.
+    with pytest.raises(L.KernelNotFound, match="^registry: kernel not found: moe_int4/CPU/F32$"):
+        L.moe_int4(x, [(c, s, s)], [(cd, sd, sd)], r, 1, 32)
