@@ -232,7 +232,9 @@ def gemm_records(args, dev, cpu=True):
                            len(w.copies))
         flops = 2 * M * N * K
         tflops = flops / (us * 1e-6) / 1e12
-        rec = {"shape": f"M={M} N={N} K={K}", "kernel": "to_bf16_kernel + gemm_ws_kernel<WsQ4k>",
+        kern = "to_bf16_kernel + gemm_q4k_kernel<112>" if N % 112 == 0 else \
+            "to_bf16_kernel + gemm_q4k_kernel<128> (K split 4) + splitk_reduce_kernel"
+        rec = {"shape": f"M={M} N={N} K={K}", "kernel": kern,
                "us_per_call": round(us, 2), "TFLOPS": round(tflops, 1), "peak": MFMA_PEAK_TFLOPS["bf16"],
                "peak_unit": "TFLOP/s (dense bf16 MFMA)", "frac": round(tflops / MFMA_PEAK_TFLOPS["bf16"], 4),
                "flops_per_call": flops}

@@ -561,7 +561,7 @@ size_t gemm_ws_partial_bytes(int64_t M, int64_t N, int64_t K, bool f32_out);
 
 // int4 at M <= 64 (gemm_small_int4_kernel): split K until about two workgroups per CU,
 // keeping at least four 128-k stages per split.
-static int small_int4_splits(int64_t N, int64_t K) {
+int small_int4_splits(int64_t N, int64_t K) {
   const int64_t tiles = cdiv(N, 128), nst = K / SK;
   const int64_t target = 2 * (int64_t)device_cus();
   int s = 1;
@@ -575,7 +575,7 @@ size_t gemm_partial_bytes(int64_t M, int64_t N, int64_t K, bool f32_out) {
   int s = gemm_splits(M, N, K);
   size_t old = (s > 1 || !f32_out) ? (size_t)s * (size_t)M * (size_t)N * 4 : 0;
   if (M <= 64 && K % SK == 0) {
-    const int s2 = small_int4_splits(N, K);
+    const int s2 = std::max(small_int4_splits(N, K), i4f16_splits(N, K));
     old = std::max(old, (s2 > 1 || !f32_out) ? (size_t)s2 * (size_t)M * (size_t)N * 4 : (size_t)0);
   }
   return std::max(std::max(old, gemm_ws_partial_bytes(M, N, K, f32_out)), gemm_q4k2_ws_bytes(M, N, K));

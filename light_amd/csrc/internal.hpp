@@ -99,6 +99,10 @@ int launch_int4_matmul(const void *x, int x_dtype, const uint32_t *codes, const 
                        int64_t M, int64_t N, int64_t K, int G, void *ws, hipStream_t st);
 int launch_gather_cols(const void *x, const int64_t *idx, void *y, int64_t M, int64_t K, int elem_bytes,
                        hipStream_t s);
+int i4f16_splits(int64_t N, int64_t K);
+bool i4f16_small_ok(int64_t M, int64_t N, int64_t K, int G, int x_dtype, const void *x, const void *codes);
+int launch_i4f16_small(const uint16_t *x, const uint32_t *codes, const float *s, const float *z, void *y,
+                       float *partials, int64_t M, int64_t N, int64_t K, int G, hipStream_t st);
 size_t int4_ws_bytes(int64_t M, int64_t N, int64_t K, int G, int x_dtype);
 size_t moe_ws_bytes(int64_t rows, int64_t K, int dt);
 int launch_moe_combine(const float *pair, float *out, int64_t T, int64_t N, int topk, hipStream_t s);
