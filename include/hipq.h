@@ -49,6 +49,8 @@ enum {
 enum {
   HQ_F16 = 0, HQ_BF16 = 1, HQ_F32 = 2,
   HQ_Q4_0 = 13, HQ_Q5_0 = 15, HQ_Q8_0 = 17, HQ_Q8_1 = 18, HQ_Q4_K = 21, HQ_Q5_K = 22, HQ_Q6_K = 23,
+  /* Not a Light dtype: the planar load-time layout of Q6_K that hq_repack_q6k writes. */
+  HQ_Q6_K_R = 123,
 };
 
 /* ---- errors / version ------------------------------------------------- */
@@ -97,8 +99,9 @@ size_t hq_matmul_q_ws_bytes(int64_t M, int64_t N, int64_t K, int w_dtype);
 
 /* out (M, N) F32 = x (M, K) F32 contiguous @ dequant(w (N, K))^T.
  * w_dtype: one of the six GGUF formats Light fuses: HQ_Q4_0, HQ_Q5_0, HQ_Q8_0, HQ_Q4_K,
- * HQ_Q5_K or HQ_Q6_K.  K must be a multiple of the block size.
- *  - M <= 8, Q4_K / Q5_K: the persistent int8-dot GEMV, x quantized to q8_1 inside its
+ * HQ_Q5_K or HQ_Q6_K, or HQ_Q6_K_R (a Q6_K weight after hq_repack_q6k).  K must be a
+ * multiple of the block size.
+ *  - M <= 8, Q4_K / Q5_K / Q6_K_R: the persistent int8-dot GEMV, x quantized to q8_1 inside its
  *    workgroups (K > 8192: into ws first).
  *  - M <= 8, Q8_0 / Q4_0 / Q5_0 / Q6_K: the LDS-staged int8-dot GEMV (x quantized in its
  *    workgroups up to K = 8192, into ws above).
@@ -199,6 +202,28 @@ int hq_matmul_q_act(const void *act, const void *w, float *out, int64_t M, int64
  * CPU decoders; BF16 rounds the F32 value once, RNE).
  * Replaces the "dequant" hook (quant/cuda_hook.go:17-69, kernels/cuda/dequant.go:39-80). */
 int hq_dequant(const void *src, void *dst, int64_t n, int src_dtype, int out_dtype, hq_stream_t stream);
+
+/* Bytes of the Q6_K_R copy of a Q6_K weight (N, K): N rows of ceil16(210 * K / 256) bytes. */
+size_t hq_repack_q6k_bytes(int64_t N, int64_t K);
+/* Load-time repack of a Q6_K weight (N, K) (GGUF blocks of 210 bytes, 2-byte aligned;
+ * quant/q6_k.go:10-27) into the Q6_K_R layout, which the decode GEMV reads with aligned
+ * 16-byte loads.  Per row (K = 256 nb, P = 4 nb units of 64 weights; unit u = 4 b + v of
+ * block b pairs the element groups g = v % 2 and g + 2 of half h = v / 2):
+ *   [0, 16 P)      unit u's quant bytes 0..15  (ql[64 h + 32 g + i], i < 16)
+ *   [16 P, 32 P)   its quant bytes 16..31
+ *   [32 P, 48 P)   its 2-bit highs: dword m, byte t = the highs of element 8m+t (bits 0-1)
+ *                  and 8m+4+t (bits 2-3) of group g, then the same two of group g+2
+ *   [48 P, 52 P)   its four scales: scales[8h + 2g], [8h + 2g + 1], [8h + 2g + 4], [8h + 2g + 5]
+ *   [52 P, 52 P + 2 nb)  d (f16) of each block; then zero padding to the row size.
+ * Values are unchanged: hq_dequant_rows of the copy equals hq_dequant of the original, bit
+ * for bit.  Light keeps GGUF bytes; a loader that wants the faster Q6_K GEMV calls this once
+ * per weight and passes HQ_Q6_K_R to hq_matmul_q.  No counterpart in Light. */
+int hq_repack_q6k(const void *src, void *dst, int64_t N, int64_t K, hq_stream_t stream);
+
+/* Dequantize a weight (N, K) of src_dtype (any dtype hq_dequant takes, or HQ_Q6_K_R, whose
+ * rows are padded) to F32 or BF16 (N, K), bit-exact as hq_dequant. */
+int hq_dequant_rows(const void *src, void *dst, int64_t N, int64_t K, int src_dtype, int out_dtype,
+                    hq_stream_t stream);
 
 /* Quantize x (M, K) (F32, BF16 or F16) to q8_1 blocks (M, K/32) x 36 bytes:
  * [f16 d][f16 s][i8 q[32]] (quant/q8_1.go:10-18) with encodeQ8_0's rounding

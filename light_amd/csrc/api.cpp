@@ -270,12 +270,15 @@ static bool is_gguf(int dt) {
   return dt == HQ_Q4_0 || dt == HQ_Q5_0 || dt == HQ_Q8_0 || dt == HQ_Q4_K || dt == HQ_Q5_K || dt == HQ_Q6_K;
 }
 
+// hq_matmul_q's weight formats: the GGUF six and the repacked Q6_K.
+static bool is_matmul_w(int dt) { return is_gguf(dt) || dt == HQ_Q6_K_R; }
+
 size_t hq_matmul_q_ws_bytes(int64_t M, int64_t N, int64_t K, int w_dtype) { return matmul_q_ws_bytes(M, N, K, w_dtype); }
 
 int hq_matmul_q(const float *x, const void *w, float *out, int64_t M, int64_t N, int64_t K, int w_dtype,
                 void *ws, size_t ws_bytes, hq_stream_t stream) {
   const char *call = "hq_matmul_q";
-  if (!is_gguf(w_dtype)) return fail(HQ_EUNSUPPORTED, call, "weight dtype %d has no fused kernel", w_dtype);
+  if (!is_matmul_w(w_dtype)) return fail(HQ_EUNSUPPORTED, call, "weight dtype %d has no fused kernel", w_dtype);
   if (M < 0 || N < 0 || K <= 0) return fail(HQ_EINVAL, call, "bad shape M=%lld N=%lld K=%lld", (long long)M,
                                             (long long)N, (long long)K);
   BlockInfo bi = block_info(w_dtype);
@@ -299,7 +302,7 @@ int hq_matmul_q(const float *x, const void *w, float *out, int64_t M, int64_t N,
 int hq_matmul_q_noalloc(const float *x, const void *w, float *out, int64_t M, int64_t N, int64_t K, int w_dtype,
                         hq_stream_t stream) {
   const char *call = "hq_matmul_q_noalloc";
-  if (!is_gguf(w_dtype)) return fail(HQ_EUNSUPPORTED, call, "weight dtype %d has no fused kernel", w_dtype);
+  if (!is_matmul_w(w_dtype)) return fail(HQ_EUNSUPPORTED, call, "weight dtype %d has no fused kernel", w_dtype);
   if (M < 0 || N < 0 || K <= 0) return fail(HQ_EINVAL, call, "bad shape M=%lld N=%lld K=%lld", (long long)M,
                                             (long long)N, (long long)K);
   BlockInfo bi = block_info(w_dtype);
@@ -468,6 +471,43 @@ int hq_dequant(const void *src, void *dst, int64_t n, int src_dtype, int out_dty
   hipStream_t s = resolve(stream);
   TraceSpan span("dequant", s);
   return launch_dequant(src, dst, n, src_dtype, out_dtype, s);
+}
+
+size_t hq_repack_q6k_bytes(int64_t N, int64_t K) {
+  if (N < 0 || K <= 0 || K % 256) return 0;
+  return (size_t)(N * q6kr_row_bytes(K));
+}
+
+int hq_repack_q6k(const void *src, void *dst, int64_t N, int64_t K, hq_stream_t stream) {
+  const char *call = "hq_repack_q6k";
+  if (N < 0 || K <= 0 || K % 256) return fail(HQ_EINVAL, call, "K=%lld not a positive multiple of 256", (long long)K);
+  if (N > INT32_MAX || K > INT32_MAX) return fail(HQ_EINVAL, call, "shape too large");
+  if (N == 0) return HQ_OK;
+  if (!src || !dst) return fail(HQ_EINVAL, call, "NULL pointer");
+  if (((uintptr_t)src & 1) || ((uintptr_t)dst & 15))
+    return fail(HQ_EINVAL, call, "src must be 2-byte aligned, dst 16-byte aligned");
+  hipStream_t s = resolve(stream);
+  TraceSpan span("repack_q6k", s);
+  return launch_repack_q6k(src, dst, N, K, s);
+}
+
+int hq_dequant_rows(const void *src, void *dst, int64_t N, int64_t K, int src_dtype, int out_dtype,
+                    hq_stream_t stream) {
+  const char *call = "hq_dequant_rows";
+  if (src_dtype != HQ_Q6_K_R) {
+    if (N < 0 || K < 0) return fail(HQ_EINVAL, call, "bad shape N=%lld K=%lld", (long long)N, (long long)K);
+    if (src_dtype != HQ_Q8_1 && !is_gguf(src_dtype)) return fail(HQ_EUNSUPPORTED, call, "source dtype %d", src_dtype);
+    if (K % block_info(src_dtype).elems) return fail(HQ_EINVAL, call, "K=%lld not a multiple of the block", (long long)K);
+    return hq_dequant(src, dst, N * K, src_dtype, out_dtype, stream);
+  }
+  if (out_dtype != HQ_F32 && out_dtype != HQ_BF16) return fail(HQ_EUNSUPPORTED, call, "out dtype %d", out_dtype);
+  if (N < 0 || K <= 0 || K % 256) return fail(HQ_EINVAL, call, "K=%lld not a positive multiple of 256", (long long)K);
+  if (N == 0) return HQ_OK;
+  if (!src || !dst) return fail(HQ_EINVAL, call, "NULL pointer");
+  if (((uintptr_t)src & 15) || ((uintptr_t)dst & 15)) return fail(HQ_EINVAL, call, "src and dst must be 16-byte aligned");
+  hipStream_t s = resolve(stream);
+  TraceSpan span("dequant", s);
+  return launch_dequant_q6kr(src, dst, N, K, out_dtype, s);
 }
 
 int hq_quantize_q8_1(const void *x, int x_dtype, void *dst, int64_t M, int64_t K, hq_stream_t stream) {

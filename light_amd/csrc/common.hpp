@@ -3,7 +3,8 @@
 // Formats are GGUF block layouts exactly as Light stores them (dtype/dtype.go:53-60,
 // quant/q4_0.go:18-27, quant/q5_0.go:11-20, quant/q8_0.go:10-17, quant/q4_k.go:14-24,
 // quant/q5_k.go:11-22, quant/q6_k.go:10-20, quant/q8_1.go:10-18):
-// the library never repacks a weight, so a tensor's bytes are the GGUF bytes.
+// a tensor's bytes are the GGUF bytes.  The one exception is Q6_K_R, an opt-in load-time
+// layout of Q6_K (q6k_repack.hip) that the caller asks for explicitly.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -17,6 +18,7 @@ namespace hq {
 enum DType : int {
   F16 = HQ_F16, BF16 = HQ_BF16, F32 = HQ_F32,
   Q4_0 = HQ_Q4_0, Q5_0 = HQ_Q5_0, Q8_0 = HQ_Q8_0, Q8_1 = HQ_Q8_1, Q4_K = HQ_Q4_K, Q5_K = HQ_Q5_K, Q6_K = HQ_Q6_K,
+  Q6_K_R = HQ_Q6_K_R,
 };
 
 constexpr int kWave = 64;  // CDNA wavefront width
@@ -46,8 +48,12 @@ __host__ __device__ constexpr BlockInfo block_info(int dt) {
        : dt == Q4_K ? BlockInfo{256, 144}
        : dt == Q5_K ? BlockInfo{256, 176}
        : dt == Q6_K ? BlockInfo{256, 210}
+       : dt == Q6_K_R ? BlockInfo{256, 210}
        : BlockInfo{0, 0};
 }
+
+// Row bytes of the Q6_K_R layout: the 210 bytes of each block, padded per row to 16.
+__host__ __device__ constexpr int64_t q6kr_row_bytes(int64_t K) { return (K / 256 * 210 + 15) & ~(int64_t)15; }
 
 // f16 -> f32 widening is exact for every finite pattern (v_cvt_f32_f16), which is
 // what Half.ToF32 computes (dtype/half.go:84-113).

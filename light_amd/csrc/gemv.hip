@@ -1021,7 +1021,8 @@ static int run_gemm(const void *src, bool from_act, const void *w, float *out, i
   if (dt == Q4_K) return launch_gemm_q4k_bf16(xb, w, out, partials, M, N, K, s);
   auto *wb = reinterpret_cast<uint16_t *>(base + al256((int64_t)gemm_q4k_ws_bytes(M, K)) +
                                           al256((int64_t)gemm_q4k_partial_bytes(M, N, K)));
-  if (int rc = launch_dequant(w, wb, N * K, dt, BF16, s)) return rc;
+  if (int rc = dt == Q6_K_R ? launch_dequant_q6kr(w, wb, N, K, BF16, s) : launch_dequant(w, wb, N * K, dt, BF16, s))
+    return rc;
   return launch_gemm_ws_bf16(xb, wb, out, partials, M, N, K, s);
 }
 
@@ -1034,6 +1035,15 @@ int launch_matmul_act(const void *act, const void *w, float *out, int64_t M, int
 int launch_matmul_q(const float *x, const void *w, float *out, int64_t M, int64_t N, int64_t K, int dt, void *ws,
                     hipStream_t s) {
   if (use_gemm(M, dt) && gemm_k_ok(K)) return run_gemm(x, false, w, out, M, N, K, dt, ws, s);
+  if (dt == Q6_K_R) {
+    // The planar Q6_K layout is only read by the team GEMV (and dequantized for the GEMM).
+    if (!q4kx_ok(M, N, K, w, nullptr, x, dt))
+      return fail(HQ_EUNSUPPORTED, "matmul_q", "Q6_K_R needs 16-byte aligned x and w, M <= %d, K <= 32768",
+                  (int)kGemvMaxRows);
+    if (q4kx_xin(K)) return launch_gemv_q4kx(x, w, nullptr, out, M, N, K, 0, dt, s);
+    if (int rc = launch_quantize_act(x, F32, ws, M, K, s)) return rc;
+    return launch_gemv_q4kx_act(ws, w, out, M, N, K, dt, s);
+  }
   if ((dt == Q4_K || dt == Q5_K) && q4kx_ok(M, N, K, w, nullptr, x, dt) && q4kx_xin(K))
     return launch_gemv_q4kx(x, w, nullptr, out, M, N, K, 0, dt, s);
   if (!gemv_fast_ok(dt, K, w) || (dt == Q5_K && !q4kx_ok(1, N, K, w, nullptr, x, dt)))

@@ -92,6 +92,9 @@ __device__ __forceinline__ u32x4_t bload16(__amdgpu_buffer_rsrc_t r, uint32_t of
 __device__ __forceinline__ float bload_f32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
 }
+__device__ __forceinline__ uint32_t bload_u32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
 
 // ---- weight-unit policies --------------------------------------------------------
 // Activations of one unit (two 32-blocks of one row of x), as each policy wants them.
@@ -227,17 +230,6 @@ struct QkUnit {
 using Q4kUnit = QkUnit<false>;
 using Q5kUnit = QkUnit<true>;
 
-// Rows of at least this many elements take single-level activations.
-constexpr int64_t kX1MinK = 8192;
-
-// Calls f with a default-constructed unit policy for (dt in {Q4_K, Q5_K}, K).
-template <class F>
-static int with_qk_unit(int dt, int64_t K, F &&f) {
-  const bool x1 = K >= kX1MinK;
-  if (dt == Q5_K) return x1 ? f(QkUnit<true, false>{}) : f(QkUnit<true, true>{});
-  return x1 ? f(QkUnit<false, false>{}) : f(QkUnit<false, true>{});
-}
-
 // int4 unit (quant.Int4, quant/int4.go:11-34): 64 elements = code words 8u .. 8u+7 (two
 // 32-blocks A, B); nibble j of word c is element 8c + j, so the low / high nibbles of a
 // word are its even / odd elements and the lane's activations are stored even / odd
@@ -345,6 +337,141 @@ struct Int4UnitT {
 };
 
 using Int4Unit = Int4UnitT<true>;
+
+// Q6_K_R unit (the planar Q6_K layout of q6k_repack.hip): unit u = 4 b + v of block b pairs
+// group g = v % 2 ("A", 32-block ja = 8 b + 4 h + g of x, h = v / 2) with group g + 2 ("B",
+// block ja + 2).  Three contiguous 16-byte planes (quant bytes 0..15, 16..31, 2-bit highs),
+// four int8 scales and the block's f16 d (read as the dword holding d of blocks b, b ^ 1).
+// Per 16-weight sub-block: dot chains start at -32 * (sum of x's quants) (the Q6_K offset),
+// c = 254 * dot(q1) + dot(q2) is exact below 2^24 (|dot| <= 16 * 32 * 127), and the sum is
+// d * (e_A * (scA0 c_A0 + scA1 c_A1) + e_B * (...)), with e = d_x / 254 the second level's
+// step (d_x q1 + e q2 = e (254 q1 + q2) to within an ulp of d_x).  X2 = false: one level, d_x.
+template <bool X2 = true>
+struct Q6kUnit {
+  static constexpr bool kX2 = X2;
+  struct Lane {
+    uint32_t u, dsh;
+    int ja;
+  };
+  struct W {
+    u32x4_t q0, q1, hh;
+    uint32_t sc, dd;
+  };
+  struct X {
+    uint32_t xa[8], xb[8], ya[8], yb[8];
+    float fA, fB;
+    int sA[2], sB[2], tA[2], tB[2];
+  };
+  __device__ static Lane lane(int u) {
+    Lane L;
+    const int b = u >> 2, v = u & 3;
+    L.u = (uint32_t)u;
+    L.dsh = (uint32_t)(b & 1) * 16;
+    L.ja = b * 8 + (v >> 1) * 4 + (v & 1);
+    return L;
+  }
+  __device__ static void load(const uint8_t *w, const float *, const float *, const Q4kxArgs &a, int row,
+                              const Lane &L, W &r) {
+    const __amdgpu_buffer_rsrc_t rs = span_rsrc(w, (uint32_t)a.N * (uint32_t)a.row_bytes);
+    const uint32_t ro = (uint32_t)row * (uint32_t)a.row_bytes, P16 = (uint32_t)a.K >> 2;  // 16 * K / 64
+    r.q0 = bload16(rs, ro + 16u * L.u);
+    r.q1 = bload16(rs, ro + P16 + 16u * L.u);
+    r.hh = bload16(rs, ro + 2u * P16 + 16u * L.u);
+    r.sc = bload_u32(rs, ro + 3u * P16 + 4u * L.u);
+    r.dd = bload_u32(rs, ro + 13u * (P16 >> 2) + 4u * (L.u >> 3));  // 52 P + 4 (b / 2)
+  }
+  __device__ static void load_x(const uint8_t *q1, const uint8_t *q2, const uint8_t *de, const uint8_t *,
+                                int64_t blk, X &x) {
+    const u32x4_t *a1 = reinterpret_cast<const u32x4_t *>(q1 + blk * 32);
+    const u32x4_t *b1 = reinterpret_cast<const u32x4_t *>(q1 + (blk + 2) * 32);
+    const u32x4_t va0 = a1[0], va1 = a1[1], vb0 = b1[0], vb1 = b1[1];
+#pragma unroll
+    for (int k = 0; k < 4; k++) x.xa[k] = va0[k], x.xa[k + 4] = va1[k], x.xb[k] = vb0[k], x.xb[k + 4] = vb1[k];
+    if constexpr (X2) {
+      const u32x4_t *a2 = reinterpret_cast<const u32x4_t *>(q2 + blk * 32);
+      const u32x4_t *b2 = reinterpret_cast<const u32x4_t *>(q2 + (blk + 2) * 32);
+      const u32x4_t wa0 = a2[0], wa1 = a2[1], wb0 = b2[0], wb1 = b2[1];
+#pragma unroll
+      for (int k = 0; k < 4; k++) x.ya[k] = wa0[k], x.ya[k + 4] = wa1[k], x.yb[k] = wb0[k], x.yb[k + 4] = wb1[k];
+    }
+    const float2 dA = reinterpret_cast<const float2 *>(de)[blk], dB = reinterpret_cast<const float2 *>(de)[blk + 2];
+    x.fA = X2 ? dA.y : dA.x;
+    x.fB = X2 ? dB.y : dB.x;
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+      int sa = 0, sb = 0, ta = 0, tb = 0;
+#pragma unroll
+      for (int k = 4 * s; k < 4 * s + 4; k++) {
+        sa = dot4((int)x.xa[k], 0x01010101, sa);
+        sb = dot4((int)x.xb[k], 0x01010101, sb);
+        if constexpr (X2) {
+          ta = dot4((int)x.ya[k], 0x01010101, ta);
+          tb = dot4((int)x.yb[k], 0x01010101, tb);
+        }
+      }
+      x.sA[s] = -32 * sa;
+      x.sB[s] = -32 * sb;
+      x.tA[s] = -32 * ta;
+      x.tB[s] = -32 * tb;
+    }
+  }
+  template <int MM>
+  __device__ static void dot(const W &w, const X (&x)[MM], const Lane &L, float (&out)[MM]) {
+    const float d = h2f((w.dd >> L.dsh) & 0xffffu);
+    // The signed scales pass through an empty asm so that the conversion is a plain
+    // v_cvt_f32_i32: folded with the byte extract, hipcc emitted v_cvt_f32_u32_sdwa with a
+    // sext source, which reads a negative scale as 2^32 - |sc|.
+    float sc[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      int si = __builtin_amdgcn_sbfe((int)w.sc, 8 * j, 8);
+      asm volatile("" : "+v"(si));
+      sc[j] = (float)si;
+    }
+    const uint32_t qw[8] = {w.q0[0], w.q0[1], w.q0[2], w.q0[3], w.q1[0], w.q1[1], w.q1[2], w.q1[3]};
+    uint32_t qa[8], qb[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const uint32_t hm = w.hh[k >> 1];
+      qa[k] = (qw[k] & 0x0F0F0F0Fu) | (((k & 1) ? hm << 2 : hm << 4) & 0x30303030u);
+      qb[k] = ((qw[k] >> 4) & 0x0F0F0F0Fu) | (((k & 1) ? hm >> 2 : hm) & 0x30303030u);
+    }
+#pragma unroll
+    for (int mm = 0; mm < MM; mm++) {
+      float vA = 0.f, vB = 0.f;
+#pragma unroll
+      for (int s = 0; s < 2; s++) {
+        int a1 = x[mm].sA[s], b1 = x[mm].sB[s], a2 = x[mm].tA[s], b2 = x[mm].tB[s];
+#pragma unroll
+        for (int k = 4 * s; k < 4 * s + 4; k++) {
+          a1 = dot4((int)qa[k], (int)x[mm].xa[k], a1);
+          b1 = dot4((int)qb[k], (int)x[mm].xb[k], b1);
+          if constexpr (X2) {
+            a2 = dot4((int)qa[k], (int)x[mm].ya[k], a2);
+            b2 = dot4((int)qb[k], (int)x[mm].yb[k], b2);
+          }
+        }
+        const int cA = X2 ? __mul24(254, a1) + a2 : a1, cB = X2 ? __mul24(254, b1) + b2 : b1;
+        vA = __fmaf_rn(sc[s], (float)cA, vA);
+        vB = __fmaf_rn(sc[2 + s], (float)cB, vB);
+      }
+      out[mm] = d * __fmaf_rn(x[mm].fB, vB, x[mm].fA * vA);
+    }
+  }
+};
+
+// Rows of at least this many elements take single-level activations.
+constexpr int64_t kX1MinK = 8192;
+
+// Calls f with a default-constructed unit policy for (dt in {Q4_K, Q5_K, Q6_K_R}, K).
+template <class F>
+static int with_qk_unit(int dt, int64_t K, F &&f) {
+  const bool x1 = K >= kX1MinK;
+  if (dt == Q5_K) return x1 ? f(QkUnit<true, false>{}) : f(QkUnit<true, true>{});
+  if (dt == Q6_K_R) return x1 ? f(Q6kUnit<false>{}) : f(Q6kUnit<true>{});
+  return x1 ? f(QkUnit<false, false>{}) : f(QkUnit<false, true>{});
+}
+
 
 template <class U, class = void>
 struct is_int4_unit {
@@ -1287,6 +1414,11 @@ static bool q4kx_geom(int64_t K, int kblock, int *P, int *TP, int *RW) {
   return true;
 }
 
+// Row bytes of a K-wide row of the Q4_K, Q5_K (GGUF) and Q6_K_R (padded planar) formats.
+static int64_t q4kx_row_bytes(int dt, int64_t K) {
+  return dt == Q6_K_R ? q6kr_row_bytes(K) : K / 256 * block_info(dt).bytes;
+}
+
 static int mm_of(int64_t M) { return M >= 3 ? 4 : (int)M; }
 
 // Quantize x inside the GEMV's workgroups (saves a launch) only for rows up to 8192: each
@@ -1303,8 +1435,9 @@ static size_t q4kx_lds(int MM, int64_t K, int TP, int RW, int nw, bool xin, bool
 
 bool q4kx_ok(int64_t M, int64_t N, int64_t K, const void *w0, const void *w1, const void *x, int dt) {
   int P, TP, RW;
-  if ((dt != Q4_K && dt != Q5_K) || M < 1 || M > kGemvMaxRows || !q4kx_geom(K, 256, &P, &TP, &RW)) return false;
-  if (N > INT32_MAX / 2 || (N + 1) * (K / 256 * block_info(dt).bytes) > UINT32_MAX) return false;
+  if ((dt != Q4_K && dt != Q5_K && dt != Q6_K_R) || M < 1 || M > kGemvMaxRows || !q4kx_geom(K, 256, &P, &TP, &RW))
+    return false;
+  if (N > INT32_MAX / 2 || (N + 1) * q4kx_row_bytes(dt, K) > UINT32_MAX) return false;
   if (((uintptr_t)w0 & 15) || (w1 && ((uintptr_t)w1 & 15)) || ((uintptr_t)x & 15)) return false;
   return q4kx_lds(mm_of(M), K, TP, RW, w1 != nullptr ? 2 : 1, true, true) <= 160 * 1024;
 }
@@ -1369,7 +1502,7 @@ static int q4kx_setup(Q4kxArgs &a, int64_t M, int64_t N, int64_t K, int kblock, 
 int launch_gemv_q4kx(const float *x, const void *w0, const void *w1, float *out, int64_t M, int64_t N, int64_t K,
                      int act, int dt, hipStream_t s) {
   Q4kxArgs a;
-  if (int rc = q4kx_setup(a, M, N, K, 256, K / 256 * block_info(dt).bytes, "gemv_q4kx")) return rc;
+  if (int rc = q4kx_setup(a, M, N, K, 256, q4kx_row_bytes(dt, K), "gemv_q4kx")) return rc;
   a.x = x;
   a.w0 = static_cast<const uint8_t *>(w0);
   a.w1 = static_cast<const uint8_t *>(w1);
@@ -1384,7 +1517,7 @@ int launch_gemv_q4kx(const float *x, const void *w0, const void *w1, float *out,
 int launch_gemv_q4kx_act(const void *act_in, const void *w, float *out, int64_t M, int64_t N, int64_t K, int dt,
                          hipStream_t s) {
   Q4kxArgs a;
-  if (int rc = q4kx_setup(a, M, N, K, 256, K / 256 * block_info(dt).bytes, "gemv_q4kx")) return rc;
+  if (int rc = q4kx_setup(a, M, N, K, 256, q4kx_row_bytes(dt, K), "gemv_q4kx")) return rc;
   a.ain = static_cast<const uint8_t *>(act_in);
   a.w0 = static_cast<const uint8_t *>(w);
   a.out = out;
@@ -1473,7 +1606,7 @@ int launch_matmul_q_gated(const float *x, const void *wg, const void *wu, float 
   if (q4kx_ok(M, N, K, wg, wu, x, dt)) {
     if (q4kx_xin(K)) return launch_gemv_q4kx(x, wg, wu, out, M, N, K, act, dt, s);
     Q4kxArgs a;
-    if (int rc = q4kx_setup(a, M, N, K, 256, K / 256 * block_info(dt).bytes, "gemv_q4k_gated")) return rc;
+    if (int rc = q4kx_setup(a, M, N, K, 256, q4kx_row_bytes(dt, K), "gemv_q4k_gated")) return rc;
     if (int rc = launch_quantize_act(x, F32, ws, M, K, s)) return rc;
     a.ain = static_cast<const uint8_t *>(ws);
     a.w0 = static_cast<const uint8_t *>(wg);
@@ -1523,7 +1656,7 @@ int launch_matmul_q_gated_act(const float *x, const void *wg, const void *wu, ui
   int P, TP, RW;
   if (N % 256 == 0 && q4kx_ok(M, N, K, wg, wu, x, dt) && q4kx_geom(K, 256, &P, &TP, &RW) && 32 % RW == 0) {
     Q4kxArgs a;
-    if (int rc = q4kx_setup(a, M, N, K, 256, K / 256 * block_info(dt).bytes, "matmul_q_gated_act")) return rc;
+    if (int rc = q4kx_setup(a, M, N, K, 256, q4kx_row_bytes(dt, K), "matmul_q_gated_act")) return rc;
     a.x = x;
     a.w0 = static_cast<const uint8_t *>(wg);
     a.w1 = static_cast<const uint8_t *>(wu);
@@ -1578,7 +1711,7 @@ int launch_moe_gemv_x(const float *x, const void *w, const int64_t *pairs, const
                       int32_t *offsets, const float *topk_w, float *out, int topk, int64_t size_m, int64_t M,
                       int64_t rows, int64_t E, int64_t N, int64_t K, int rpp, int dt, int act, hipStream_t s) {
   MoeXArgs ma;
-  const int64_t row_bytes = K / 256 * block_info(dt).bytes;
+  const int64_t row_bytes = q4kx_row_bytes(dt, K);
   const bool gated = act >= 0;  // N = I; the expert holds gate rows [0, I) then up rows [I, 2I)
   if (int rc = q4kx_setup(ma.g, 1, gated ? 2 * N : N, K, 256, row_bytes, "moe_gemv")) return rc;
   ma.g.N = (int)N;
@@ -1629,7 +1762,7 @@ int launch_moe_down_combine(const float *h, const void *w, const int64_t *pairs,
                             int32_t *counts, int32_t *offsets, const float *topk_w, float *y, int topk, int64_t T,
                             int64_t E, int64_t N, int64_t K, int dt, hipStream_t s) {
   MoeCombArgs ma;
-  const int64_t row_bytes = K / 256 * block_info(dt).bytes;
+  const int64_t row_bytes = q4kx_row_bytes(dt, K);
   if (int rc = q4kx_setup(ma.g, 1, N, K, 256, row_bytes, "moe_gemm_q_combine")) return rc;
   ma.g.x = h;
   ma.g.w0 = static_cast<const uint8_t *>(w);
@@ -1672,7 +1805,7 @@ int launch_moe_route_gated(const float *probs, const float *x, const void *w, fl
                            float *weights, int64_t *sorted_pairs, int64_t *sorted_expts, int32_t *counts,
                            int32_t *offsets, hipStream_t s) {
   MoeXArgs ma;
-  const int64_t row_bytes = K / 256 * block_info(dt).bytes;
+  const int64_t row_bytes = q4kx_row_bytes(dt, K);
   if (int rc = q4kx_setup(ma.g, 1, 2 * I, K, 256, row_bytes, "moe_route_gated")) return rc;
   const int64_t M = T * topk;
   ma.g.N = (int)I;

@@ -35,6 +35,9 @@ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 int launch_quantize_q8_1(const void *x, int x_dtype, void *dst, int64_t M, int64_t K, hipStream_t s);
 int launch_quantize_act(const void *x, int x_dtype, void *dst, int64_t M, int64_t K, hipStream_t s);
 int launch_dequant(const void *src, void *dst, int64_t n, int src_dtype, int out_dtype, hipStream_t s);
+// Q6_K_R (q6k_repack.hip): GGUF Q6_K (N, K) -> the planar layout, and its row-aware dequant.
+int launch_repack_q6k(const void *src, void *dst, int64_t N, int64_t K, hipStream_t s);
+int launch_dequant_q6kr(const void *src, void *dst, int64_t N, int64_t K, int out_dtype, hipStream_t s);
 // matmul_q: quantizes x (GEMV, M <= kGemvMaxRows) or converts it to bf16 (Q4_K MFMA GEMM)
 // in ws, then runs the kernel.
 constexpr int64_t kGemvMaxRows = 8;

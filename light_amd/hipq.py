@@ -14,10 +14,12 @@ LIB_PATH = os.path.join(_HERE, "libhipq.so")
 # Light dtype.DType codes (dtype/dtype.go:13-37).
 F16, BF16, F32 = 0, 1, 2
 Q4_0, Q5_0, Q8_0, Q8_1, Q4_K, Q5_K, Q6_K = 13, 15, 17, 18, 21, 22, 23
+# Not a Light dtype: the planar load-time repack of Q6_K (hq_repack_q6k).
+Q6_K_R = 123
 BLOCK = {Q4_0: (32, 18), Q5_0: (32, 22), Q8_0: (32, 34), Q8_1: (32, 36), Q4_K: (256, 144), Q5_K: (256, 176),
          Q6_K: (256, 210)}
 NAMES = {F16: "F16", BF16: "BF16", F32: "F32", Q4_0: "Q4_0", Q5_0: "Q5_0", Q8_0: "Q8_0", Q8_1: "Q8_1",
-         Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K"}
+         Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K", Q6_K_R: "Q6_K_R"}
 
 HQ_OK, HQ_EINVAL, HQ_EUNSUPPORTED, HQ_ENOMEM = 0, -1, -2, -3
 ACT_SILU, ACT_GELU_ERF = 0, 1
@@ -69,6 +71,9 @@ SIGNATURES = {
     "hq_matmul_q_act_ws_bytes": (_SZ, [_I64, _I64, _I64, _I]),
     "hq_matmul_q_act": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _P, _SZ, _P]),
     "hq_dequant": (_I, [_P, _P, _I64, _I, _I, _P]),
+    "hq_repack_q6k_bytes": (_SZ, [_I64, _I64]),
+    "hq_repack_q6k": (_I, [_P, _P, _I64, _I64, _P]),
+    "hq_dequant_rows": (_I, [_P, _P, _I64, _I64, _I, _I, _P]),
     "hq_quantize_q8_1": (_I, [_P, _I, _P, _I64, _I64, _P]),
     "hq_int4_matmul_ws_bytes": (_SZ, [_I64, _I64, _I64, _I, _I]),
     "hq_int4_matmul": (_I, [_P, _I, _P, _P, _P, _P, _I64, _I64, _I64, _I, _P, _SZ, _P]),
@@ -238,6 +243,24 @@ def matmul_q_ws_bytes(M, N, K, w_dtype):
 
 def matmul_q_gated_ws_bytes(M, N, K, w_dtype):
     return lib().hq_matmul_q_gated_ws_bytes(M, N, K, w_dtype)
+
+
+def repack_q6k(w, N, K, out=None, stream=None):
+    """The Q6_K_R copy (uint8, hq_repack_q6k_bytes(N, K)) of a Q6_K weight (N, K)."""
+    import torch
+    if out is None:
+        out = torch.empty(lib().hq_repack_q6k_bytes(N, K), dtype=torch.uint8, device=w.device)
+    check(lib().hq_repack_q6k(_ptr(w), _ptr(out), N, K, _stream(stream)))
+    return out
+
+
+def dequant_rows(src, N, K, src_dtype, out_dtype=F32, out=None, stream=None):
+    """(N, K) F32 / BF16 of a weight in any hq_dequant format or Q6_K_R."""
+    import torch
+    if out is None:
+        out = torch.empty((N, K), dtype=torch.float32 if out_dtype == F32 else torch.bfloat16, device=src.device)
+    check(lib().hq_dequant_rows(_ptr(src), _ptr(out), N, K, src_dtype, out_dtype, _stream(stream)))
+    return out
 
 
 def dequant(src, n, src_dtype, out_dtype=F32, out=None, stream=None):
