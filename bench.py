@@ -49,8 +49,8 @@ def parse():
     p.add_argument("--launches", type=int, default=200, help="per-kernel timed launches for the roofline")
     p.add_argument("--gemm-launches", type=int, default=100, help="timed calls per M=512 GEMM shape")
     p.add_argument("--probe", action="store_true",
-                   help="counter probe for rocprofv3 --pmc: a 64 MiB device copy, then 20 launches of the "
-                        "dominant GEMV (no timing, no JSON line)")
+                   help="counter probe for rocprofv3 --pmc: a 64 MiB device copy, then the step's two GEMVs "
+                        "and the M=512 GEMMs (no timing, no JSON line)")
     return p.parse_args()
 
 
@@ -209,7 +209,8 @@ def down_kernel(args, down, h, dev):
     alg = down.raw.nbytes + hipq.lib().hq_act_bytes(1, K) + 4 * N
     gbs = alg / (us * 1e-6) / 1e9
     return {"kernel": "gemv_q4kx_kernel (act input)", "shape": f"down N={N} K={K} M=1", "avg_launch_us": round(us, 3),
-            "achieved": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4), "alg_bytes_per_launch": alg}
+            "achieved": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4), "alg_bytes_per_launch": alg,
+            "traffic": measured_traffic(f"down act N={N} K={K} M=1")}
 
 
 GEMM_SHAPES = ((512, 14336, 4096), (512, 4096, 14336))
@@ -237,7 +238,8 @@ def gemm_records(args, dev, cpu=True):
         rec = {"shape": f"M={M} N={N} K={K}", "kernel": kern,
                "us_per_call": round(us, 2), "TFLOPS": round(tflops, 1), "peak": MFMA_PEAK_TFLOPS["bf16"],
                "peak_unit": "TFLOP/s (dense bf16 MFMA)", "frac": round(tflops / MFMA_PEAK_TFLOPS["bf16"], 4),
-               "flops_per_call": flops}
+               "flops_per_call": flops,
+               "traffic": measured_traffic(f"gemm M={M} N={N} K={K}" + ("" if N % 112 == 0 else " (K split 4)"))}
         if cpu:
             t, th, smp = cpu_gguf_row(x_np, w.raw, N, K, hipq.Q4_K)
             rec["cpu"] = {"us_per_call": round(t * 1e6, 1), "TFLOPS": round(flops / t / 1e12, 4), "cores": th,
@@ -249,15 +251,18 @@ def gemm_records(args, dev, cpu=True):
 
 
 def measured_traffic(shape):
-    """HBM bytes per launch of the fused gate/up kernel from the committed rocprofv3 FETCH_SIZE /
-    WRITE_SIZE runs (profiles/gemv_q4k_gated_traffic.md gives the commands and the copy-kernel scaling)."""
-    path = os.path.join(ROOT, "profiles", "gemv_q4k_gated_traffic.json")
+    """HBM bytes per launch of one reported kernel from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE runs (profiles/q4k_traffic.md gives the commands and the copy-kernel scaling)."""
+    path = os.path.join(ROOT, "profiles", "q4k_traffic.json")
     try:
         with open(path) as f:
             d = json.load(f)
     except (OSError, ValueError):
         return None
-    return d.get("traffic_bytes") if d.get("shape") == shape else None
+    for r in d.get("kernels", []):
+        if r.get("shape") == shape:
+            return r.get("traffic_bytes")
+    return None
 
 
 def table(args, dev):
@@ -491,20 +496,40 @@ def _cpu_model():
 
 
 def probe(dev):
-    """Known-size copy (reference for the counters' scale) followed by the dominant kernel."""
+    """Known-size copy (reference for the counters' scale), then the kernels the JSON line
+    reports: the step's first launch (gated GEMV, quantized-h epilogue) x20, its down GEMV on
+    prepared activations x20 and the M = 512 GEMM at both shapes x5 each."""
     import torch
-    from light_amd import hipq
+    from light_amd import hipq, synth
     src = torch.ones(64 << 18, dtype=torch.float32, device=dev)  # 64 MiB
     dst = torch.empty_like(src)
     for _ in range(3):
         dst.copy_(src)
-    gate, up, _, x_np, _ = mlp_inputs(dev)
+    gate, up, down, x_np, h_np = mlp_inputs(dev)
     x = torch.from_numpy(x_np).to(dev)
     out = torch.empty(hipq.lib().hq_act_bytes(1, gate.N), dtype=torch.uint8, device=dev)
     for i in range(20):
         hipq.matmul_q_gated_act(x, gate[i], up[i], gate.N, gate.K, hipq.Q4_K, out=out)
+    act = hipq.quantize_act(torch.from_numpy(h_np).to(dev))
+    y = torch.empty((1, down.N), device=dev)
+    for i in range(20):
+        hipq.matmul_q_act(act, down[i], 1, down.N, down.K, hipq.Q4_K, out=y)
     torch.cuda.synchronize()
-    print(f"probe: copy 67108864 B x3; gemv_q4k gated_act N={gate.N} K={gate.K} x20", file=sys.stderr)
+    del gate, up, down
+    torch.cuda.empty_cache()
+    for idx, (M, N, K) in enumerate(GEMM_SHAPES):
+        g = synth.rng(20 + idx)
+        w = Weight(synth.gguf_weight(hipq.Q4_K, N, K, g), hipq.Q4_K, N, K, dev)
+        xg = torch.from_numpy(synth.activations(M, K, g)).to(dev)
+        yg = torch.empty((M, N), device=dev)
+        ws = torch.empty(hipq.matmul_q_ws_bytes(M, N, K, hipq.Q4_K), dtype=torch.uint8, device=dev)
+        for i in range(5):
+            hipq.matmul_q(xg, w[i], N, K, hipq.Q4_K, out=yg, ws=ws)
+        torch.cuda.synchronize()
+        del w
+        torch.cuda.empty_cache()
+    print("probe: copy 67108864 B x3; gated_act N=14336 K=4096 x20; down act N=4096 K=14336 x20; "
+          "gemm M=512 (14336x4096, 4096x14336) x5 each", file=sys.stderr)
 
 
 def main():
