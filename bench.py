@@ -51,6 +51,8 @@ def parse():
     p.add_argument("--probe", action="store_true",
                    help="counter probe for rocprofv3 --pmc: a 64 MiB device copy, then the step's two GEMVs "
                         "and the M=512 GEMMs (no timing, no JSON line)")
+    p.add_argument("--probe-int4", action="store_true",
+                   help="counter probe: a 64 MiB device copy, then 5 calls of int4 M=64 at both Qwen2.5-7B shapes")
     return p.parse_args()
 
 
@@ -279,8 +281,12 @@ def table(args, dev):
                 w = Weight(synth.gguf_weight(dt, N, K, g), dt, N, K, dev)
                 x = torch.from_numpy(synth.activations(M, K, g)).to(dev)
                 out = torch.empty((M, N), device=dev)
-                ws = torch.empty(hipq.matmul_q_ws_bytes(M, N, K, dt), dtype=torch.uint8, device=dev)
-                us = time_launches(lambda i: hipq.matmul_q(x, w[i], N, K, dt, out=out, ws=ws), 100,
+                kdt = dt
+                if c.get("repack"):  # Q6_K_R: the load-time planar copy; bytes per call as stored in GGUF
+                    w.copies = [hipq.repack_q6k(cp, N, K) for cp in w.copies]
+                    kdt = hipq.Q6_K_R
+                ws = torch.empty(max(hipq.matmul_q_ws_bytes(M, N, K, kdt), 256), dtype=torch.uint8, device=dev)
+                us = time_launches(lambda i: hipq.matmul_q(x, w[i], N, K, kdt, out=out, ws=ws), 100,
                                    len(w.copies))
                 nbytes = w.raw.nbytes + 4 * M * K + 4 * M * N
                 flops = 2 * M * N * K
@@ -532,8 +538,35 @@ def probe(dev):
           "gemm M=512 (14336x4096, 4096x14336) x5 each", file=sys.stderr)
 
 
+def probe_int4(dev):
+    """Known-size copy, then configs[3]'s M = 64 int4 matmul (f16 x) at both shapes, 5 calls each."""
+    import numpy as np
+    import torch
+    from light_amd import hipq, synth
+    src = torch.ones(64 << 18, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    for name in ("int4_m64_18944x3584", "int4_m64_3584x18944"):
+        c = synth.CONFIGS[name]
+        g = synth.rng(c["cfg"])
+        M, N, K, G = c["M"], c["N"], c["K"], c["G"]
+        codes, s, z = synth.int4_weight(N, K, G, g)
+        x = torch.from_numpy(synth.activations(M, K, g, np.float16)).to(dev)
+        ct, st, zt = (torch.from_numpy(a).to(dev) for a in (codes, s, z))
+        out = torch.empty((M, N), dtype=torch.float16, device=dev)
+        for _ in range(5):
+            hipq.int4_matmul(x, ct, st, zt, G, out=out)
+        torch.cuda.synchronize()
+    print("probe: copy 67108864 B x3; int4 M=64 (18944x3584, 3584x18944) x5 each", file=sys.stderr)
+
+
 def main():
     args = parse()
+    if args.probe_int4:
+        import torch
+        probe_int4(torch.device("cuda:0"))
+        return
     if args.probe:
         import torch
         probe(torch.device("cuda:0"))

@@ -228,14 +228,22 @@ bool i4f16_small_ok(int64_t M, int64_t N, int64_t K, int G, int x_dtype, const v
 
 int launch_splitk_reduce(const float *part, void *out, int out_dtype, int64_t n, int splits, hipStream_t s);
 
-// K split: until the grid reaches two workgroups per CU, keeping at least 4 stages per split
-// (at most 16 splits).
+// K split: one workgroup fits a CU (133 registers, eight waves), so the split minimising
+// (rounds of workgroups over the CUs) x (stages per split) wins, with a 2% charge per split
+// for the partial traffic and at least 4 stages per split (18944 x 3584: 3 splits, 222
+// workgroups -- 4 splits made 296, and the 40 CUs holding two ran twice as long).
 int i4f16_splits(int64_t N, int64_t K) {
-  const int64_t tiles = cdiv(N, 256), nst = K / IK;
-  const int64_t target = 2 * (int64_t)device_cus();
-  int s = 1;
-  while (tiles * (s * 2) <= target && nst / (s * 2) >= 4 && s < 16) s *= 2;
-  return s;
+  const int64_t tiles = cdiv(N, 256), nst = K / IK, cus = device_cus();
+  int best = 1;
+  double bc = 1e300;
+  for (int s = 1; s <= 32 && nst / s >= 4; s++) {
+    const double c = (double)cdiv(tiles * s, cus) * cdiv(nst, s) * (1.0 + 0.02 * s);
+    if (c < bc) {
+      bc = c;
+      best = s;
+    }
+  }
+  return best;
 }
 
 int launch_i4f16_small(const uint16_t *x, const uint32_t *codes, const float *s, const float *z, void *y,

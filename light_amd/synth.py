@@ -188,6 +188,9 @@ CONFIGS = {
     "q4_k_gemv_down_4096x14336": dict(cfg=1, kind="gguf", dt=Q4_K, M=1, N=4096, K=14336),
     "q6_k_gemv_attn_out_4096x4096": dict(cfg=1, kind="gguf", dt=Q6_K, M=1, N=4096, K=4096),
     "q6_k_gemv_lm_head_128256x4096": dict(cfg=1, kind="gguf", dt=Q6_K, M=1, N=128256, K=4096),
+    # The same Q6_K weights after the load-time planar repack (Q6_K_R), as a model would run them.
+    "q6_k_r_gemv_attn_out_4096x4096": dict(cfg=1, kind="gguf", dt=Q6_K, M=1, N=4096, K=4096, repack=True),
+    "q6_k_r_gemv_lm_head_128256x4096": dict(cfg=1, kind="gguf", dt=Q6_K, M=1, N=128256, K=4096, repack=True),
     "q4_k_gemm_m512_14336x4096": dict(cfg=2, kind="gguf", dt=Q4_K, M=512, N=14336, K=4096),
     "q4_k_gemm_m512_4096x14336": dict(cfg=2, kind="gguf", dt=Q4_K, M=512, N=4096, K=14336),
     "int4_m1_18944x3584": dict(cfg=3, kind="int4", M=1, N=18944, K=3584, G=128),
