@@ -870,7 +870,33 @@ __global__ __launch_bounds__(512) void moe_gemv_x_kernel(MoeXArgs ma) {
   const bool x1 = (!GATED || ROUTE) && ma.rows == 1;  // (the plain gated kernel has no registers to spare)
   const int KB0 = a.K >> 5, ntask0 = MM * KB0 * 8;
   float4 xpre = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (x1) {
+  // One row of x and one pair per pass (a single token's experts): the row is quantized into
+  // LDS slot 0 once, up front -- in the routed kernel by the waves that do not route, while
+  // the routing waves select the top-k -- so it is off the path from the routing to the first
+  // dot.  (The barriers of the routing / the pass publish it.)
+  const bool xq0 = x1 && MM == 1;
+  if (xq0) {
+    const int t0 = ROUTE ? 64 * ma.T : 0;  // whole waves: act_quant8_fast works on aligned 8-lane groups
+    const int nth = (int)blockDim.x - t0;
+    if (t >= t0 && nth > 0) {
+      for (int base = 0; base < ntask0; base += nth) {
+        const int task = base + t - t0, tc = task < ntask0 ? task : ntask0 - 1;
+        const int blk = tc >> 3, sub = tc & 7;
+        const float4 xq = *reinterpret_cast<const float4 *>(static_cast<const float *>(a.x) + blk * 32 + sub * 4);
+        const float v[4] = {xq.x, xq.y, xq.z, xq.w};
+        const ActQ q = act_quant8_fast(v);
+        if (task < ntask0) {
+          reinterpret_cast<uint32_t *>(smem + blk * 32)[sub] = q.q1;
+          reinterpret_cast<uint32_t *>(smem + (int64_t)a.K + blk * 32)[sub] = q.q2;
+          if (sub == 0) {
+            reinterpret_cast<float2 *>(smem + 2 * (int64_t)a.K)[blk] = make_float2(q.d, q.e);
+            reinterpret_cast<float *>(smem + 2 * (int64_t)a.K + 8 * (int64_t)KB0)[blk] = q.sum;
+          }
+        }
+      }
+    }
+    if constexpr (!ROUTE) __syncthreads();
+  } else if (x1) {
     const int task = t < ntask0 ? t : ntask0 - 1;
     const int blk = task >> 3, sub = task & 7, kb = blk % KB0;
     xpre = *reinterpret_cast<const float4 *>(static_cast<const float *>(a.x) + kb * 32 + sub * 4);
@@ -936,7 +962,7 @@ __global__ __launch_bounds__(512) void moe_gemv_x_kernel(MoeXArgs ma) {
       if (GATED) U::load(w + ma.up_off, a.s0, a.z0, a, row, L, wr[NW - 1]);
     }
     if (c0 != seg0) __syncthreads();  // every lane has its activations of the previous chunk
-    const int ntask = MM * KB * 8;
+    const int ntask = xq0 ? 0 : MM * KB * 8;
     const float *x = static_cast<const float *>(a.x);
     for (int base = 0; base < ntask; base += XT * (int)blockDim.x) {
       float4 xv[XT];
