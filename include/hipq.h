@@ -254,6 +254,24 @@ int hq_int4_matmul(const void *x, int x_dtype, const uint32_t *codes, const floa
 int hq_int4_dequant(const uint32_t *codes, const float *scales, const float *zeros, void *out, int out_dtype,
                     int64_t N, int64_t K, int G, int64_t out_offset, hq_stream_t stream);
 
+/* GPTQ checkpoint tensors -> canonical 4-bit weights, on the device (quant.FromGPTQ,
+ * quant/int4.go:102-182).  qweight I32 (K/8, N) packed along K (nibble j of qweight[r][n] is
+ * row 8r + j); qzeros I32 (K/group, N/8) packed along N, holding zero - 1 ("gptq") or, with
+ * v2 != 0, the zero ("gptq_v2"); scales F32 (K/group, N) (the caller casts the checkpoint's
+ * F16).  perm: NULL, or I64 (K) for act-order checkpoints -- canonical column k takes input
+ * row perm[k] (Light's stable sort of K by g_idx; the host layer computes it).  Writes codes
+ * U32 (N, K/8), scales_out / zeros_out F32 (N, K/group).  K and N multiples of 8. */
+int hq_int4_from_gptq(const void *qweight, const void *qzeros, const float *scales, const int64_t *perm, int64_t K,
+                      int64_t N, int group, int v2, uint32_t *codes, float *scales_out, float *zeros_out,
+                      hq_stream_t stream);
+
+/* AutoAWQ (GEMM version) checkpoint tensors -> canonical 4-bit weights, on the device
+ * (quant.FromAWQ, quant/int4.go:184-235).  qweight I32 (K, N/8) and qzeros I32 (K/group, N/8)
+ * packed along N, nibble i of a word holding column 8c + (0, 2, 4, 6, 1, 3, 5, 7)[i]; scales
+ * F32 (K/group, N).  Writes codes U32 (N, K/8), scales_out / zeros_out F32 (N, K/group). */
+int hq_int4_from_awq(const void *qweight, const void *qzeros, const float *scales, int64_t K, int64_t N, int group,
+                     uint32_t *codes, float *scales_out, float *zeros_out, hq_stream_t stream);
+
 /* Workspace bytes hq_moe_gemm_q needs for `rows` input rows of K elements. */
 size_t hq_moe_gemm_q_ws_bytes(int64_t rows, int64_t K, int w_dtype);
 

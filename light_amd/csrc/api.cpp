@@ -549,6 +549,31 @@ int hq_int4_matmul(const void *x, int x_dtype, const uint32_t *codes, const floa
   return launch_int4_matmul(x, x_dtype, codes, scales, zeros, y, M, N, K, G, ws, s);
 }
 
+int hq_int4_from_gptq(const void *qweight, const void *qzeros, const float *scales, const int64_t *perm, int64_t K,
+                      int64_t N, int group, int v2, uint32_t *codes, float *scales_out, float *zeros_out,
+                      hq_stream_t stream) {
+  const char *call = "hq_int4_from_gptq";
+  if (K <= 0 || N <= 0 || K % 8 || N % 8) return fail(HQ_EINVAL, call, "K=%lld N=%lld (multiples of 8)", (long long)K, (long long)N);
+  if (group <= 0 || K % group) return fail(HQ_EINVAL, call, "group %d does not divide K %lld", group, (long long)K);
+  if (!qweight || !qzeros || !scales || !codes || !scales_out || !zeros_out) return fail(HQ_EINVAL, call, "NULL pointer");
+  hipStream_t s = resolve(stream);
+  TraceSpan span("int4_from_gptq", s);
+  return launch_int4_from_gptq(static_cast<const uint32_t *>(qweight), static_cast<const uint32_t *>(qzeros), scales,
+                               perm, K, N, group, v2 != 0, codes, scales_out, zeros_out, s);
+}
+
+int hq_int4_from_awq(const void *qweight, const void *qzeros, const float *scales, int64_t K, int64_t N, int group,
+                     uint32_t *codes, float *scales_out, float *zeros_out, hq_stream_t stream) {
+  const char *call = "hq_int4_from_awq";
+  if (K <= 0 || N <= 0 || K % 8 || N % 8) return fail(HQ_EINVAL, call, "K=%lld N=%lld (multiples of 8)", (long long)K, (long long)N);
+  if (group <= 0 || K % group) return fail(HQ_EINVAL, call, "group %d does not divide K %lld", group, (long long)K);
+  if (!qweight || !qzeros || !scales || !codes || !scales_out || !zeros_out) return fail(HQ_EINVAL, call, "NULL pointer");
+  hipStream_t s = resolve(stream);
+  TraceSpan span("int4_from_awq", s);
+  return launch_int4_from_awq(static_cast<const uint32_t *>(qweight), static_cast<const uint32_t *>(qzeros), scales,
+                              K, N, group, codes, scales_out, zeros_out, s);
+}
+
 int hq_int4_dequant(const uint32_t *codes, const float *scales, const float *zeros, void *out, int out_dtype,
                     int64_t N, int64_t K, int G, int64_t out_offset, hq_stream_t stream) {
   const char *call = "hq_int4_dequant";

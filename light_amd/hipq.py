@@ -78,6 +78,8 @@ SIGNATURES = {
     "hq_int4_matmul_ws_bytes": (_SZ, [_I64, _I64, _I64, _I, _I]),
     "hq_int4_matmul": (_I, [_P, _I, _P, _P, _P, _P, _I64, _I64, _I64, _I, _P, _SZ, _P]),
     "hq_int4_dequant": (_I, [_P, _P, _P, _P, _I, _I64, _I64, _I, _I64, _P]),
+    "hq_int4_from_gptq": (_I, [_P, _P, _P, _P, _I64, _I64, _I, _I, _P, _P, _P, _P]),
+    "hq_int4_from_awq": (_I, [_P, _P, _P, _I64, _I64, _I, _P, _P, _P, _P]),
     "hq_moe_gemm_q_ws_bytes": (_SZ, [_I64, _I64, _I]),
     "hq_moe_combine": (_I, [_P, _P, _I64, _I64, _I, _P]),
     "hq_moe_gemm_q_combine_ws_bytes": (_SZ, [_I64, _I, _I64, _I64, _I64, _I]),
@@ -306,6 +308,36 @@ def int4_dequant(codes, scales, zeros, G, out_dtype=F32, out=None, out_offset=0,
     check(lib().hq_int4_dequant(_ptr(codes), _ptr(scales), _ptr(zeros), _ptr(out), out_dtype, N, K, G, out_offset,
                                 _stream(stream)))
     return out
+
+
+def int4_from_gptq(qweight, qzeros, scales, group, perm=None, v2=False, stream=None):
+    """Canonical (codes U32 (N, K/8), scales, zeros F32 (N, K/G)) from GPTQ qweight (K/8, N) and
+    qzeros (K/G, N/8) int32 tensors and F32 scales (K/G, N); perm: I64 (K) for act order."""
+    import torch
+    K, N = qweight.shape[0] * 8, qweight.shape[1]
+    G = K // group
+    dev = qweight.device
+    codes = torch.empty((N, K // 8), dtype=torch.int32, device=dev)
+    so = torch.empty((N, G), dtype=torch.float32, device=dev)
+    zo = torch.empty((N, G), dtype=torch.float32, device=dev)
+    check(lib().hq_int4_from_gptq(_ptr(qweight), _ptr(qzeros), _ptr(scales), _ptr(perm) if perm is not None else None,
+                                  K, N, group, 1 if v2 else 0, _ptr(codes), _ptr(so), _ptr(zo), _stream(stream)))
+    return codes, so, zo
+
+
+def int4_from_awq(qweight, qzeros, scales, group, stream=None):
+    """Canonical (codes, scales, zeros) from AutoAWQ qweight (K, N/8), qzeros (K/G, N/8) int32
+    tensors and F32 scales (K/G, N)."""
+    import torch
+    K, N = qweight.shape[0], qweight.shape[1] * 8
+    G = K // group
+    dev = qweight.device
+    codes = torch.empty((N, K // 8), dtype=torch.int32, device=dev)
+    so = torch.empty((N, G), dtype=torch.float32, device=dev)
+    zo = torch.empty((N, G), dtype=torch.float32, device=dev)
+    check(lib().hq_int4_from_awq(_ptr(qweight), _ptr(qzeros), _ptr(scales), K, N, group, _ptr(codes), _ptr(so),
+                                 _ptr(zo), _stream(stream)))
+    return codes, so, zo
 
 
 def moe_gemm_q(x, w, sorted_pairs, sorted_expts, E, N, K, w_dtype, topk, topk_w=None, out=None, counts=None,

@@ -65,4 +65,15 @@ Tensor MoECombine(const Tensor &pair_out, int topk);
 Tensor Dequantize(const Tensor &w);
 
 }  // namespace ops
+
+namespace quant {
+// quant.FromGPTQ (quant/int4.go:102-182): AutoGPTQ / GPTQModel qweight I32 (K/8, N), qzeros
+// I32 (K/G, N/8), scales F32 (K/G, N), optional g_idx (K,) (act order -> Perm); v2 =
+// checkpoint_format "gptq_v2".  Converted on the ROCm device; the Int4 lives there.
+ops::Int4 FromGPTQ(const Tensor &qweight, const Tensor &qzeros, const Tensor &scales, const Tensor *g_idx, int group,
+                   bool v2);
+// quant.FromAWQ (quant/int4.go:184-235): AutoAWQ GEMM qweight I32 (K, N/8), qzeros I32
+// (K/G, N/8), scales F32 (K/G, N).
+ops::Int4 FromAWQ(const Tensor &qweight, const Tensor &qzeros, const Tensor &scales, int group);
+}  // namespace quant
 }  // namespace light

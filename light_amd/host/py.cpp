@@ -184,6 +184,24 @@ PYBIND11_MODULE(_light, m) {
       },
       py::arg("codes"), py::arg("scales"), py::arg("zeros"), py::arg("group"), py::arg("out_dtype"),
       py::arg("perm") = py::none());
+  auto int4_tuple = [](const ops::Int4 &w) {
+    return py::make_tuple(w.codes, w.scales, w.zeros, w.group, w.perm ? py::cast(*w.perm) : py::none());
+  };
+  m.def(
+      "from_gptq",
+      [int4_tuple](const Tensor &qweight, const Tensor &qzeros, const Tensor &scales, std::optional<Tensor> g_idx,
+                   int group, bool v2) {
+        return int4_tuple(quant::FromGPTQ(qweight, qzeros, scales, g_idx ? &*g_idx : nullptr, group, v2));
+      },
+      py::arg("qweight"), py::arg("qzeros"), py::arg("scales"), py::arg("g_idx"), py::arg("group"),
+      py::arg("v2") = false, "quant.FromGPTQ -> (codes, scales, zeros, group, perm or None)");
+  m.def(
+      "from_awq",
+      [int4_tuple](const Tensor &qweight, const Tensor &qzeros, const Tensor &scales, int group) {
+        return int4_tuple(quant::FromAWQ(qweight, qzeros, scales, group));
+      },
+      py::arg("qweight"), py::arg("qzeros"), py::arg("scales"), py::arg("group"),
+      "quant.FromAWQ -> (codes, scales, zeros, group, None)");
   m.def(
       "matmul_int4",
       [](const Tensor &x, const Tensor &codes, const Tensor &scales, const Tensor &zeros, int group,

@@ -30,6 +30,13 @@ Parity status of each function (how it is pinned):
   sorted experts non-decreasing, pairs a permutation), on rows with ties.
 * ``gated``: SiLU against x * sigmoid(x) in f64 and GELU against scipy's erf
   (closed forms), at special points (0, large |x|) and on random data.
+* ``int4_from_gptq`` / ``int4_from_awq`` (numpy restatements of quant.FromGPTQ /
+  quant.FromAWQ): PARITY UNPINNED against Light itself -- its only tests of them
+  (quant/int4_test.go:80-114) read real checkpoints, absent offline.  They are
+  checked against the producers' published packing rules (AutoGPTQ: qweight
+  packed along K, qzeros along N storing zero - 1; AutoAWQ: order
+  0, 2, 4, 6, 1, 3, 5, 7), written independently in the tests as packers, by
+  round trips and single-nibble known answers.
 * ``quantize_q8_1``: specification only (Light has no q8_1 encoder): layout,
   |q| <= 127, round trip within d/2, all-zero block, and the q8_0 encoder
   (same rounding rule) on the same data.
@@ -335,3 +342,75 @@ def moe_int4(x, gate_up, down, ids, w, topk, G, act=0, threads=0):
         for j in range(topk):
             out[t] = (out[t] + pair[t * topk + j]).astype(np.float32)
     return out
+
+
+def _gos(shape):
+    """A shape as Go's %v prints an []int."""
+    return "[" + " ".join(str(int(d)) for d in shape) + "]"
+
+
+def _nib(w, j):
+    return (np.asarray(w, np.uint32) >> np.uint32(4 * j)) & np.uint32(0xF)
+
+
+def _canon(code):
+    """Pack codes (N, K) uint8 into canonical words: nibble j of word (n, c) is code (n, 8c + j)
+    (build, quant/int4.go:75-101)."""
+    N, K = code.shape
+    c = code.reshape(N, K // 8, 8).astype(np.uint32)
+    return np.bitwise_or.reduce(c << (np.arange(8, dtype=np.uint32) * 4), axis=2).astype(np.uint32)
+
+
+def int4_from_gptq(qweight, qzeros, scales, group, g_idx=None, v2=False):
+    """quant.FromGPTQ (quant/int4.go:102-182) on numpy arrays: qweight (K/8, N) and qzeros
+    (K/G, N/8) as int32 / uint32, scales (K/G, N) F32, g_idx (K,) or None.  Returns (codes
+    (N, K/8) uint32, scales (N, K/G), zeros (N, K/G), perm (K,) int64 or None); raises
+    ValueError with Light's messages."""
+    qw = np.asarray(qweight).view(np.uint32)
+    qz = np.asarray(qzeros).view(np.uint32)
+    sc = np.asarray(scales, np.float32)
+    K, N = qw.shape[0] * 8, qw.shape[1]
+    if group <= 0:
+        group = K
+    if K % group or sc.shape != (K // group, N) or qz.shape[0] != K // group or qz.shape[1] * 8 != N:
+        raise ValueError(f"quant.FromGPTQ: qweight {_gos(qw.shape)}, qzeros {_gos(qz.shape)}, scales "
+                         f"{_gos(sc.shape)}, group {group} inconsistent")
+    perm = None
+    if g_idx is not None:
+        gi = np.asarray(g_idx).astype(np.int64).ravel()
+        if gi.size != K:
+            raise ValueError(f"quant.FromGPTQ: g_idx has {gi.size} entries for K {K}")
+        if not np.array_equal(gi, np.arange(K) // group):
+            perm = np.argsort(gi, kind="stable").astype(np.int64)
+            if not np.array_equal(gi[perm], np.arange(K) // group):
+                raise ValueError(f"quant.FromGPTQ: g_idx groups are not all of size {group}")
+    G = K // group
+    n = np.arange(N)
+    zeros = _nib(qz[:, n // 8], n % 8).astype(np.float32)  # (G, N)
+    if not v2:
+        zeros = zeros + np.float32(1)
+    src = perm if perm is not None else np.arange(K)
+    code = _nib(qw[src // 8][:, n], (src % 8)[:, None])  # (K, N): code of (n, k)
+    return _canon(code.T.astype(np.uint8)), np.ascontiguousarray(sc.T), np.ascontiguousarray(zeros.T), perm
+
+
+_AWQ_ORDER = (0, 2, 4, 6, 1, 3, 5, 7)
+
+
+def int4_from_awq(qweight, qzeros, scales, group):
+    """quant.FromAWQ (quant/int4.go:184-235) on numpy arrays: qweight (K, N/8) and qzeros
+    (K/G, N/8) int32 / uint32, scales (K/G, N) F32.  Returns (codes, scales, zeros)."""
+    qw = np.asarray(qweight).view(np.uint32)
+    qz = np.asarray(qzeros).view(np.uint32)
+    sc = np.asarray(scales, np.float32)
+    K, N = qw.shape[0], qw.shape[1] * 8
+    if group <= 0 or K % group or sc.shape != (K // group, N) or qz.shape[0] != K // group or qz.shape[1] * 8 != N:
+        raise ValueError(f"quant.FromAWQ: qweight {_gos(qw.shape)}, qzeros {_gos(qz.shape)}, scales "
+                         f"{_gos(sc.shape)}, group {group} inconsistent")
+    inv = np.zeros(8, np.int64)
+    for i, o in enumerate(_AWQ_ORDER):
+        inv[o] = i
+    n = np.arange(N)
+    zeros = _nib(qz[:, n // 8], inv[n % 8]).astype(np.float32)
+    code = _nib(qw[:, n // 8], inv[n % 8])  # (K, N)
+    return _canon(code.T.astype(np.uint8)), np.ascontiguousarray(sc.T), np.ascontiguousarray(zeros.T)
