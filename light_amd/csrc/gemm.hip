@@ -370,8 +370,30 @@ __global__ __launch_bounds__(256) void gemm_small_int4_kernel(SmallI4Args a) {
 // expert e = blockIdx.y; blockIdx.x is the 128-wide weight-row tile.  The expert's
 // pairs are processed in chunks of 32 gathered activation rows (BM = 32, 4 waves of
 // 32 x 32), each chunk running the full K loop of gemm_kernel.
+
+// ---- MoE grouped GEMM (prefill-sized routing: more than 4 pairs per expert) ------------
+//
+// out[p, :] = w(p) * x[row(p)] . dequant(W[e(p)])^T for the expert-sorted pairs (ops.MoEGemmQ,
+// ops/moe.go:242-265), Q4_K.  grid = (N / 128, E); a workgroup takes its expert's pair segment
+// in chunks of 32 gathered rows and streams the expert's 128 weight rows once per chunk.
+//
+// With only 16-32 rows per expert, each dequantized weight feeds at most 32 rows, so the
+// dequant -- not the MFMAs -- is the work: the bf16 path (convert, FMA, round, 4.4 VALU
+// instructions per weight) ran T = 256 gate/up at 108 us for 226 MB.  Here B is f16 and the
+// dequant is packed: a nibble pair becomes the f16 pair (1024 + q) with one v_perm_b32
+// against 0x64 bytes, one packed add takes away 1024 (exact), one packed FMA applies
+// d*sc and -dmin*m (one rounding), about 2 VALU instructions per weight.  x is converted to
+// f16 once per row with a power-of-two row scale (rows of |x| above 2^15 are scaled down, the
+// output row scaled back up exactly), so the f16 range never clips.
+// The raw loads of step s + MD go out while step s computes (a register ring).
+
+constexpr int MD = 3;
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2v __attribute__((ext_vector_type(2)));
+
 struct MoeGemmArgs {
-  GemmArgs g;  // x = bf16 rows of x, w = expert stack, N, K
+  GemmArgs g;          // x = f16 rows of x, w = expert stack, N, K
+  const float *xscale; // per x row: the power of two the f16 row was divided by
   const int64_t *pairs;
   const int32_t *offsets;
   const float *topk_w;
@@ -380,7 +402,94 @@ struct MoeGemmArgs {
   int topk, rpp;
 };
 
-template <class WP>
+// x (rows, K) F32 -> f16, row r divided by 2^e_r (e_r = 0 unless the row's max |x| exceeds
+// 2^15); xscale[r] = 2^e_r.  One workgroup per row.
+__global__ __launch_bounds__(256) void to_f16_rowscale_kernel(const float *__restrict__ x, _Float16 *__restrict__ y,
+                                                              float *__restrict__ xscale, int64_t K) {
+  __shared__ float red[4];
+  const int64_t r = blockIdx.x;
+  const float *xr = x + r * K;
+  float m = 0.f;
+  for (int64_t k = threadIdx.x; k < K; k += 256) m = fmaxf(m, fabsf(xr[k]));
+  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  int ex = 0;
+  (void)frexpf(m, &ex);  // m < 2^ex
+  const int e = ex > 15 && m == m && m < INFINITY ? ex - 15 : 0;
+  for (int64_t k = threadIdx.x; k < K; k += 256) y[r * K + k] = (_Float16)ldexpf(xr[k], -e);
+  if (threadIdx.x == 0) xscale[r] = ldexpf(1.f, e);
+}
+
+// The ring's loads are issued from inline asm and awaited with explicit counts: with plain
+// loads the compiler waits for every outstanding load at the K loop's back edge (vmcnt(0)),
+// which leaves one step of latency exposed per step.  The wait names the registers it
+// completes ("+v"), so nothing reads them -- or reuses them -- before it.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ u32x4 ldg16(const void *p) {
+  u32x4 r;
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r) : "v"(p) : "memory");
+  return r;
+}
+template <int N>
+__device__ __forceinline__ void wait_ring(u32x4 &a, u32x4 &b, u32x4 &c) {
+  asm volatile("s_waitcnt vmcnt(%3)" : "+v"(a), "+v"(b), "+v"(c) : "n"(N) : "memory");
+}
+#pragma clang diagnostic pop
+
+// Raw Q4_K bytes of one thread's B slot for one 64-k step: (row, half): quant bytes
+// 16 * half .. + 16 of the step's pair (low nibbles: sub-block 2p, k = 16 half + i; high:
+// sub-block 2p + 1, k = 32 + 16 half + i) and the block header.
+struct Q4kF16Slot {
+  u32x4 q, h;
+  __device__ __forceinline__ void load(const GemmArgs &a, int row, int half, int k0) {
+    const uint8_t *bp = a.w + (int64_t)row * (a.K / 256) * 144 + (int64_t)(k0 >> 8) * 144;
+    const int p = (k0 >> 6) & 3;
+    q = ldg16(bp + 16 + 32 * p + 16 * half);
+    h = ldg16(bp);
+  }
+  __device__ __forceinline__ void store(uint8_t *brow, int half, int k0) const {
+    const int p = (k0 >> 6) & 3;
+    const float d = h2f(h.x & 0xffffu), dmin = h2f(h.x >> 16);
+    int scA, mnA, scB, mnB;
+    q4k_scale_min(2 * p, h.y, h.z, h.w, scA, mnA);
+    q4k_scale_min(2 * p + 1, h.y, h.z, h.w, scB, mnB);
+    const _Float16 dA = (_Float16)(d * (float)scA), mA = (_Float16)(-(dmin * (float)mnA));
+    const _Float16 dB = (_Float16)(d * (float)scB), mB = (_Float16)(-(dmin * (float)mnB));
+    const f16x2v sa = {dA, dA}, ma = {mA, mA}, sb = {dB, dB}, mb = {mB, mB};
+    const f16x2v k1024 = {(_Float16)-1024.f, (_Float16)-1024.f};
+    constexpr uint32_t K64 = 0x64646464u;
+    uint32_t lo[8], hi[8];
+    const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const uint32_t l = qw[k] & 0x0F0F0F0Fu, hh = (qw[k] >> 4) & 0x0F0F0F0Fu;
+      const uint32_t pr[4] = {__builtin_amdgcn_perm(K64, l, 0x04010400u), __builtin_amdgcn_perm(K64, l, 0x04030402u),
+                              __builtin_amdgcn_perm(K64, hh, 0x04010400u), __builtin_amdgcn_perm(K64, hh, 0x04030402u)};
+      f16x2v v[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        f16x2v t;
+        __builtin_memcpy(&t, &pr[j], 4);
+        t = t + k1024;  // q, exact
+        v[j] = j < 2 ? __builtin_elementwise_fma(t, sa, ma) : __builtin_elementwise_fma(t, sb, mb);
+      }
+      __builtin_memcpy(&lo[2 * k], &v[0], 4);
+      __builtin_memcpy(&lo[2 * k + 1], &v[1], 4);
+      __builtin_memcpy(&hi[2 * k], &v[2], 4);
+      __builtin_memcpy(&hi[2 * k + 1], &v[3], 4);
+    }
+    u32x4 *bd = reinterpret_cast<u32x4 *>(brow + 32 * half);
+    bd[0] = u32x4{lo[0], lo[1], lo[2], lo[3]};
+    bd[1] = u32x4{lo[4], lo[5], lo[6], lo[7]};
+    u32x4 *bh = reinterpret_cast<u32x4 *>(brow + 64 + 32 * half);
+    bh[0] = u32x4{hi[0], hi[1], hi[2], hi[3]};
+    bh[1] = u32x4{hi[4], hi[5], hi[6], hi[7]};
+  }
+};
+
 __global__ __launch_bounds__(256) void moe_gemm_kernel(MoeGemmArgs ma) {
   using T = GTile<32>;
   extern __shared__ __align__(16) uint8_t smem[];
@@ -407,35 +516,54 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(MoeGemmArgs ma) {
     f32x16 acc;
 #pragma unroll
     for (int r = 0; r < 16; r++) acc[r] = 0.f;
-    u32x4 ra;
-    WP wp;
-    ra = *reinterpret_cast<const u32x4 *>(xrow);
-    wp.load(a, wrow, wh, 0);
-    *reinterpret_cast<u32x4 *>(smem + (arow * GLD + acol * 8) * 2) = ra;
-    wp.store(smem + T::A_BYTES + wr * GLD * 2, wh, 0);
+    // Ring slot i holds the raw loads of a step congruent to i mod MD; loads past the last step
+    // are clamped to it (unconditional, so the compiler's per-register waits stay exact).
+    u32x4 ra[MD];
+    Q4kF16Slot wp[MD];
+    // Three loads per step and thread (x, the quant bytes, the header), in this order.
+    auto load = [&](int st, u32x4 &r, Q4kF16Slot &w) __attribute__((always_inline)) {
+      const int k = (st < ksteps ? st : ksteps - 1) * GBK;
+      r = ldg16(xrow + k);
+      w.load(a, wrow, wh, k);
+    };
+    auto stage_in = [&](int buf, int st, const u32x4 &r, const Q4kF16Slot &w) __attribute__((always_inline)) {
+      uint8_t *na = smem + buf * T::STAGE;
+      *reinterpret_cast<u32x4 *>(na + (arow * GLD + acol * 8) * 2) = r;
+      w.store(na + T::A_BYTES + wr * GLD * 2, wh, (st < ksteps ? st : ksteps - 1) * GBK);
+    };
+#pragma unroll
+    for (int d = 0; d < MD; d++) load(d, ra[d], wp[d]);
+    // Loads issued after a slot's three when it is staged: the other MD - 1 slots' (one step
+    // each), at the prologue and in every step alike.
+    constexpr int NAFTER = 3 * (MD - 1);
+    wait_ring<NAFTER>(ra[0], wp[0].q, wp[0].h);
+    stage_in(0, 0, ra[0], wp[0]);
     __syncthreads();
-    for (int s = 0; s < ksteps; s++) {
-      const int buf = s & 1;
-      const int kn = (s + 1) * GBK;
-      if (s + 1 < ksteps) {
-        ra = *reinterpret_cast<const u32x4 *>(xrow + kn);
-        wp.load(a, wrow, wh, kn);
-      }
-      const uint8_t *sa = smem + buf * T::STAGE;
+    // Step s (ring slot s % MD, a compile-time constant): refill the slot with step s + MD,
+    // multiply step s from LDS, stage step s + 1 (slot (s + 1) % MD) into the other buffer.
+    auto step = [&](int s, auto SLOT) __attribute__((always_inline)) {
+      constexpr int slot = decltype(SLOT)::value, nslot = (slot + 1) % MD;
+      load(s + MD, ra[slot], wp[slot]);
+      wait_ring<NAFTER>(ra[nslot], wp[nslot].q, wp[nslot].h);
+      const uint8_t *sa = smem + (s & 1) * T::STAGE;
       const uint8_t *sb = sa + T::A_BYTES;
 #pragma unroll
       for (int kk = 0; kk < GBK / 16; kk++) {
-        const bf16x8 af = *reinterpret_cast<const bf16x8 *>(sa + (fr * GLD + kk * 16 + fk) * 2);
-        const bf16x8 bfr = *reinterpret_cast<const bf16x8 *>(sb + ((wn * 32 + fr) * GLD + kk * 16 + fk) * 2);
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bfr, acc, 0, 0, 0);
+        const f16x8 af = *reinterpret_cast<const f16x8 *>(sa + (fr * GLD + kk * 16 + fk) * 2);
+        const f16x8 bfr = *reinterpret_cast<const f16x8 *>(sb + ((wn * 32 + fr) * GLD + kk * 16 + fk) * 2);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bfr, acc, 0, 0, 0);
       }
-      if (s + 1 < ksteps) {
-        uint8_t *na = smem + (buf ^ 1) * T::STAGE;
-        *reinterpret_cast<u32x4 *>(na + (arow * GLD + acol * 8) * 2) = ra;
-        wp.store(na + T::A_BYTES + wr * GLD * 2, wh, kn);
-      }
+      if (s + 1 < ksteps) stage_in((s + 1) & 1, s + 1, ra[nslot], wp[nslot]);
       __syncthreads();
+    };
+    for (int s = 0; s < ksteps; s += MD) {
+      step(s, std::integral_constant<int, 0>{});
+      if (s + 1 < ksteps) step(s + 1, std::integral_constant<int, 1>{});
+      if (s + 2 < ksteps) step(s + 2, std::integral_constant<int, 2>{});
     }
+    // The ring's last (clamped) loads land before its registers can be reused.
+#pragma unroll
+    for (int d = 0; d < MD; d++) wait_ring<0>(ra[d], wp[d].q, wp[d].h);
     const int col = n0 + wn * 32 + (lane & 31);
     if (col < a.N) {
 #pragma unroll
@@ -445,31 +573,27 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(MoeGemmArgs ma) {
         if (i >= seg1) continue;
         const int64_t p = ma.pairs[i];
         if (p < 0 || p >= ma.size_m) continue;
-        ma.out[p * a.N + col] = acc[r] * (ma.topk_w ? ma.topk_w[p] : 1.f);
+        const int64_t row = ma.rpp ? p : p / ma.topk;
+        ma.out[p * a.N + col] = acc[r] * ma.xscale[row] * (ma.topk_w ? ma.topk_w[p] : 1.f);
       }
     }
   }
 }
 
-int launch_moe_gemm_q4k(const uint16_t *xb, const void *w, const int64_t *pairs, const int32_t *offsets,
-                        const float *topk_w, float *out, int topk, int64_t size_m, int64_t E, int64_t N, int64_t K,
-                        int rpp, hipStream_t s) {
+// x (rows, K) F32 in, xh = f16 rows (rows * K * 2 bytes, 16-byte aligned) and xs = row scales
+// (rows floats) in the workspace.
+int launch_moe_gemm_q4k(const float *x, uint16_t *xh, float *xs, const void *w, const int64_t *pairs,
+                        const int32_t *offsets, const float *topk_w, float *out, int topk, int64_t size_m,
+                        int64_t rows, int64_t E, int64_t N, int64_t K, int rpp, hipStream_t s) {
   using T = GTile<32>;
-  static bool attr_set[64] = {false};
-  int dev = 0;
-  (void)hipGetDevice(&dev);
-  if (dev >= 0 && dev < 64 && !attr_set[dev]) {
-    if (int rc = check(hipFuncSetAttribute((const void *)moe_gemm_kernel<Q4kPolicy>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, T::LDS),
-                       "hipFuncSetAttribute"))
-      return rc;
-    attr_set[dev] = true;
-  }
+  to_f16_rowscale_kernel<<<(unsigned)rows, 256, 0, s>>>(x, reinterpret_cast<_Float16 *>(xh), xs, K);
+  if (int rc = check_launch("to_f16_rowscale")) return rc;
   MoeGemmArgs ma = {};
-  ma.g.x = xb;
+  ma.g.x = xh;
   ma.g.w = static_cast<const uint8_t *>(w);
   ma.g.N = (int)N;
   ma.g.K = (int)K;
+  ma.xscale = xs;
   ma.pairs = pairs;
   ma.offsets = offsets;
   ma.topk_w = topk_w;
@@ -479,7 +603,7 @@ int launch_moe_gemm_q4k(const uint16_t *xb, const void *w, const int64_t *pairs,
   ma.topk = topk;
   ma.rpp = rpp;
   dim3 grid((unsigned)cdiv(N, GBN), (unsigned)E);
-  moe_gemm_kernel<Q4kPolicy><<<grid, 256, T::LDS, s>>>(ma);
+  moe_gemm_kernel<<<grid, 256, T::LDS, s>>>(ma);
   return check_launch("moe_gemm_q4k");
 }
 

@@ -158,8 +158,10 @@ size_t moe_gated_ws_bytes(int64_t size_m, int64_t rows, int64_t I, int64_t K, in
 int launch_moe_gemv_q4k(const void *act, const void *w, const int64_t *pairs, const int32_t *offsets,
                         const float *topk_w, float *out, int topk, int64_t size_m, int64_t M, int64_t rows,
                         int64_t E, int64_t N, int64_t K, int rpp, hipStream_t s);
-int launch_moe_gemm_q4k(const uint16_t *xb, const void *w, const int64_t *pairs, const int32_t *offsets,
-                        const float *topk_w, float *out, int topk, int64_t size_m, int64_t E, int64_t N, int64_t K,
-                        int rpp, hipStream_t s);
+// MoE grouped Q4_K GEMM: x (rows, K) F32 converted into xh (f16, rows * K * 2 bytes) and
+// xs (rows row scales) in the caller's workspace, then the grouped f16 MFMA kernel.
+int launch_moe_gemm_q4k(const float *x, uint16_t *xh, float *xs, const void *w, const int64_t *pairs,
+                        const int32_t *offsets, const float *topk_w, float *out, int topk, int64_t size_m,
+                        int64_t rows, int64_t E, int64_t N, int64_t K, int rpp, hipStream_t s);
 
 }  // namespace hq

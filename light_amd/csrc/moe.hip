@@ -19,6 +19,8 @@
 #include "decode.hpp"
 #include "internal.hpp"
 
+#include <algorithm>
+
 namespace hq {
 
 __global__ __launch_bounds__(256) void moe_offsets_kernel(const int64_t *__restrict__ expts, int64_t M, int E,
@@ -95,9 +97,12 @@ static bool moe_q4k_fast(int dt, int64_t K, const void *w) {
 
 static bool moe_use_mfma(int64_t M, int64_t E) { return M > 4 * E; }
 
+static int64_t al256m(int64_t b);
+
 size_t moe_ws_bytes(int64_t rows, int64_t K, int dt) {
   if (rows <= 0 || K <= 0 || K % 32) return 0;
-  return dt == Q4_K ? (size_t)act_bytes(rows, K) : 0;
+  // Q4_K: the decode path's act layout of x, or the grouped GEMM's f16 x and row scales.
+  return dt == Q4_K ? (size_t)std::max<int64_t>(act_bytes(rows, K), al256m(2 * rows * K) + 4 * rows) : 0;
 }
 
 int launch_moe_q(const float *x, const void *w, const int64_t *pairs, const int64_t *expts, int32_t *counts,
@@ -113,9 +118,9 @@ int launch_moe_q(const float *x, const void *w, const int64_t *pairs, const int6
   if (int rc = check_launch("moe_offsets")) return rc;
   if (moe_q4k_fast(dt, K, w)) {
     if (moe_use_mfma(M, E)) {
-      auto *xb = static_cast<uint16_t *>(ws);
-      if (int rc = launch_to_bf16(x, F32, xb, rows, K, s)) return rc;
-      return launch_moe_gemm_q4k(xb, w, pairs, offsets, topk_w, out, topk, size_m, E, N, K, rpp, s);
+      auto *xh = static_cast<uint16_t *>(ws);
+      auto *xs = reinterpret_cast<float *>(static_cast<char *>(ws) + al256m(2 * rows * K));
+      return launch_moe_gemm_q4k(x, xh, xs, w, pairs, offsets, topk_w, out, topk, size_m, rows, E, N, K, rpp, s);
     }
     if (int rc = launch_quantize_act(x, F32, ws, rows, K, s)) return rc;
     return launch_moe_gemv_q4k(ws, w, pairs, offsets, topk_w, out, topk, size_m, M, rows, E, N, K, rpp, s);
