@@ -86,6 +86,24 @@ def test_moe_gemm_q4_k_shapes(dev, T, E, topk, N, K):
     _check(dev, xp, w, hipq.Q4_K, E, N, K, ids, tw, topk, True)
 
 
+@pytest.mark.parametrize("big", [1e5, 3e7])
+def test_moe_grouped_gemm_rows_beyond_f16_range(dev, big):
+    """The grouped MFMA path (more than 4 pairs per expert) runs on f16 x with a power-of-two
+    scale per row: rows whose |x| exceeds the f16 range (65504) must not clip.  Rows 0 and 3
+    carry outliers of `big`; every pair is checked against the f64 oracle at the 1e-3 bar."""
+    g = synth.rng(int(big) % 1000 + 11)
+    T, E, topk, N, K = 40, 4, 2, 96, 512
+    w = synth.gguf_weight(hipq.Q4_K, E * N, K, g)
+    ids, tw = synth.moe_routing(T, E, topk, g)
+    x = g.standard_normal((T, K)).astype(np.float32)
+    x[0, 5] = big
+    x[3] *= np.float32(big / 4)
+    _check(dev, x, w, hipq.Q4_K, E, N, K, ids, tw, topk, False)
+    xp = g.standard_normal((T * topk, K)).astype(np.float32)
+    xp[7] *= np.float32(big)
+    _check(dev, xp, w, hipq.Q4_K, E, N, K, ids, tw, topk, True)
+
+
 def test_moe_pairs_outside_size_m_are_skipped(dev):
     """Pairs p >= size_m leave the output untouched (kernels/cuda/moe.go:115, moe_gguf.cu:62)."""
     g = synth.rng(3)
