@@ -4,13 +4,14 @@
 // scratch + cuBLAS), fused: y (M, N) = x (M, K) . W^T, W = s * (q - z) (quant.Int4, group G).
 //
 // Design (gfx950, 512 threads = 8 waves, 64 rows x 256 weight rows per workgroup, 128-k stages):
-//  * The weight is never rounded: the MFMA's B operand holds q - z exactly -- a nibble OR'd
-//    into the f16 exponent pattern 0x6400 is 1024 + q, and one packed f16 add of -(1024 + z)
-//    leaves the small integer q - z (zero points are the integers 0..15 of GPTQ / AWQ
-//    checkpoints) -- and the group scale multiplies the stage's f32 MFMA sum
-//    afterwards (acc += s * C, one FMA per output per group; stages never straddle a group,
-//    G % 128 == 0).  That is ~1.4 VALU instructions per weight instead of a convert, an FMA
-//    and a round per weight.
+//  * The weight is never rounded: the MFMA's B operand holds q - z exactly -- a nibble masked
+//    in place and OR'd into the f16 exponent pattern 0x6400 (one v_and_or_b32) is 1024 + q
+//    (nibbles 0, 2 of a byte pair) or 1024 + 16 q (nibbles 1, 3, whose x pairs are staged
+//    divided by 16, exact), and one packed f16 add of -(1024 + z) or -(1024 + 16 z) leaves
+//    q - z or 16 (q - z) (integral zero points, as in every GPTQ / AWQ checkpoint; other zero
+//    points take a second add, still within f16 precision) -- and the group scale multiplies
+//    the stage's f32 MFMA sum afterwards (acc += s * C, one FMA per output per group; stages
+//    never straddle a group, G % 128 == 0).  About 1.1 VALU instructions per weight.
 //  * Each lane streams its own weight row's codes (32 contiguous bytes per stage) straight
 //    into registers, three stages ahead, with its group's scale and zero; x (64 x 128 f16 per
 //    stage) is loaded three stages ahead into registers too and goes through LDS,
@@ -65,10 +66,26 @@ __device__ __forceinline__ void wait_x(u32x4 &a, u32x4 &b) {
 }
 #pragma clang diagnostic pop
 
-// (x_i, x_{i+1}) f16 pairs of an 8-k slice -> the (0, 4, 1, 5, 2, 6, 3, 7) order.
+// (x_i, x_{i+1}) f16 pairs of an 8-k slice -> the (0, 4, 1, 5, 2, 6, 3, 7) order, with the
+// pairs (1, 5) and (3, 7) divided by 16 (exact): their weights enter the MFMA as 16 (q - z).
 __device__ __forceinline__ u32x4 perm8(const u32x4 v) {
-  return u32x4{__builtin_amdgcn_perm(v[2], v[0], 0x05040100u), __builtin_amdgcn_perm(v[2], v[0], 0x07060302u),
-               __builtin_amdgcn_perm(v[3], v[1], 0x05040100u), __builtin_amdgcn_perm(v[3], v[1], 0x07060302u)};
+  const f16x2 s16 = {(_Float16)0.0625f, (_Float16)0.0625f};
+  uint32_t p1 = __builtin_amdgcn_perm(v[2], v[0], 0x07060302u), p3 = __builtin_amdgcn_perm(v[3], v[1], 0x07060302u);
+  f16x2 h1, h3;
+  __builtin_memcpy(&h1, &p1, 4);
+  __builtin_memcpy(&h3, &p3, 4);
+  h1 = h1 * s16;
+  h3 = h3 * s16;
+  __builtin_memcpy(&p1, &h1, 4);
+  __builtin_memcpy(&p3, &h3, 4);
+  return u32x4{__builtin_amdgcn_perm(v[2], v[0], 0x05040100u), p1, __builtin_amdgcn_perm(v[3], v[1], 0x05040100u), p3};
+}
+
+// (w & mask) | 0x64006400 in one instruction.
+__device__ __forceinline__ uint32_t and_or_6400(uint32_t w, uint32_t mask, uint32_t magic) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(w), "s"(mask), "v"(magic));
+  return r;
 }
 
 }  // namespace
@@ -158,33 +175,51 @@ __global__ __launch_bounds__(512) void gemm_i4f16_small_kernel(I4F16Args a) {
     const int gl = c * IK / a.G - g0, lr = wave * 32 + fr;
     const float sgv = lsz[lr * ngl + gl], zgv = lsz[256 * ngl + lr * ngl + gl];
     const uint16_t *xa = &xs[buf][0];
-    const f16x2 nz = {(_Float16)(-1024.f - zgv), (_Float16)(-1024.f - zgv)};
+    // Nibbles i = 0, 2 enter as 1024 + q, nibbles 1, 3 as 1024 + 16 q (masked in place, no
+    // shift; the x pairs they meet were staged / 16).  Integral zero points (every GPTQ / AWQ
+    // checkpoint's): one packed add of -(1024 + z) or -(1024 + 16 z) leaves q - z or 16 (q - z)
+    // exactly.  Otherwise (a wave-uniform test) -1024 first, exact, then -z or -16 z.
+    const bool zint = __all(zgv == rintf(zgv) && fabsf(zgv) <= 64.f);
+    const uint32_t magic = __builtin_amdgcn_readfirstlane(0x64006400u);
     f32x16 cacc[2];
+    auto mfma_stage = [&](auto ZI) __attribute__((always_inline)) {
+      constexpr bool zi = decltype(ZI)::value;
+      const f16x2 c0v = {(_Float16)(zi ? -1024.f - zgv : -1024.f), (_Float16)(zi ? -1024.f - zgv : -1024.f)};
+      const f16x2 c0v16 = {(_Float16)(zi ? -1024.f - 16.f * zgv : -1024.f),
+                           (_Float16)(zi ? -1024.f - 16.f * zgv : -1024.f)};
+      const f16x2 zf = {(_Float16)-zgv, (_Float16)-zgv}, zf16 = {(_Float16)(-16.f * zgv), (_Float16)(-16.f * zgv)};
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-      const uint32_t w = cw[slot][j >> 2][j & 3];
-      f16x8 b;
+      for (int j = 0; j < 8; j++) {
+        const uint32_t w = cw[slot][j >> 2][j & 3], w8 = w >> 8;
+        const uint32_t pr[4] = {and_or_6400(w, 0x000F000Fu, magic), and_or_6400(w, 0x00F000F0u, magic),
+                                and_or_6400(w8, 0x000F000Fu, magic), and_or_6400(w8, 0x00F000F0u, magic)};
+        f16x8 b;
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const uint32_t pr = ((w >> (4 * i)) & 0x000F000Fu) | 0x64006400u;  // (1024 + q_i, 1024 + q_{i+4})
-        f16x2 h;
-        __builtin_memcpy(&h, &pr, 4);
-        h = h + nz;  // (q_i - z, q_{i+4} - z), exact
-        b[2 * i] = h[0];
-        b[2 * i + 1] = h[1];
+        for (int i = 0; i < 4; i++) {
+          f16x2 h;
+          __builtin_memcpy(&h, &pr[i], 4);
+          h = h + ((i & 1) ? c0v16 : c0v);
+          if constexpr (!zi) h = h + ((i & 1) ? zf16 : zf);
+          b[2 * i] = h[0];
+          b[2 * i + 1] = h[1];
+        }
+        const int kx = 64 * kh + 8 * j;
+        const f16x8 a0 = *reinterpret_cast<const f16x8 *>(xa + fr * IXLD + kx);
+        const f16x8 a1 = *reinterpret_cast<const f16x8 *>(xa + (32 + fr) * IXLD + kx);
+        if (j == 0) {
+          const f32x16 zero = {};
+          cacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b, zero, 0, 0, 0);
+          cacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b, zero, 0, 0, 0);
+        } else {
+          cacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b, cacc[0], 0, 0, 0);
+          cacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b, cacc[1], 0, 0, 0);
+        }
       }
-      const int kx = 64 * kh + 8 * j;
-      const f16x8 a0 = *reinterpret_cast<const f16x8 *>(xa + fr * IXLD + kx);
-      const f16x8 a1 = *reinterpret_cast<const f16x8 *>(xa + (32 + fr) * IXLD + kx);
-      if (j == 0) {
-        const f32x16 zero = {};
-        cacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b, zero, 0, 0, 0);
-        cacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b, zero, 0, 0, 0);
-      } else {
-        cacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b, cacc[0], 0, 0, 0);
-        cacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b, cacc[1], 0, 0, 0);
-      }
-    }
+    };
+    if (zint)
+      mfma_stage(std::true_type{});
+    else
+      mfma_stage(std::false_type{});
     const float sc = sgv;
 #pragma unroll
     for (int i = 0; i < 2; i++)

@@ -105,6 +105,23 @@ def test_matmul_int4_shapes(dev, M, N, K, G):
     _check(dev, x, codes, s, z, G, hipq.F32)
 
 
+@pytest.mark.parametrize("zkind", ["frac", "wide"])
+def test_matmul_int4_f16_nonintegral_zeros(dev, zkind):
+    """Zero points that are not the integers 0..15 of a checkpoint (quant.Int4 holds them as
+    f32): fractional, or integral beyond 64.  The f16 MFMA path for 8 < M <= 64 takes its
+    second-add branch for these; results stay within tolerance of the f64 reference."""
+    rng = np.random.default_rng(11 if zkind == "frac" else 12)
+    M, N, K, G = 64, 512, 3584, 128
+    codes, s, _ = light_int4(rng, N, K, G)
+    if zkind == "frac":
+        z = (rng.random((N, K // G)) * 15).astype(np.float32)
+    else:
+        z = rng.integers(60, 100, size=(N, K // G)).astype(np.float32)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    x[:, ::7] *= 1e-4  # small activations: the x pairs staged / 16 go subnormal in f16
+    _check(dev, x, codes, s, z, G, hipq.F16)
+
+
 @pytest.mark.parametrize("name", ["int4_m1_18944x3584", "int4_m1_3584x18944", "int4_m64_18944x3584",
                                   "int4_m64_3584x18944"])
 def test_matmul_int4_benchmark_configs(dev, name):
