@@ -607,24 +607,60 @@ int launch_moe_gemm_q4k(const float *x, uint16_t *xh, float *xs, const void *w, 
   return check_launch("moe_gemm_q4k");
 }
 
-// out[i] = sum_z part[z][i] in split order, converted to the output dtype.
+// out[i] = sum_z part[z][i] in split order, converted to the output dtype.  Four outputs per
+// thread (16-byte loads), and the splits' loads issued eight at a time before they are added
+// (in split order): a load-add loop waits out one memory latency per split.
+template <int ODT>
+__device__ __forceinline__ void splitk_store(void *out, int64_t i, float v) {
+  if constexpr (ODT == F32)
+    static_cast<float *>(out)[i] = v;
+  else if constexpr (ODT == BF16)
+    static_cast<uint16_t *>(out)[i] = f2bf_rne(v);
+  else
+    static_cast<uint16_t *>(out)[i] = f2h_rne(v);
+}
+
 template <int ODT>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restrict__ part, void *__restrict__ out,
                                                             int64_t n, int splits) {
-  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  constexpr int U = 8;
+  const int64_t i = 4 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x);
   if (i >= n) return;
-  float s = part[i];
-  for (int z = 1; z < splits; z++) s += part[(int64_t)z * n + i];
-  if constexpr (ODT == F32)
-    static_cast<float *>(out)[i] = s;
-  else if constexpr (ODT == BF16)
-    static_cast<uint16_t *>(out)[i] = f2bf_rne(s);
-  else
-    static_cast<uint16_t *>(out)[i] = f2h_rne(s);
+  if (i + 4 <= n && (n & 3) == 0) {
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int z0 = 0; z0 < splits; z0 += U) {
+      float4 v[U];
+#pragma unroll
+      for (int u = 0; u < U; u++)
+        if (z0 + u < splits) v[u] = *reinterpret_cast<const float4 *>(part + (int64_t)(z0 + u) * n + i);
+#pragma unroll
+      for (int u = 0; u < U; u++)
+        if (z0 + u < splits) {
+          if (z0 + u == 0) {
+            acc = v[u];
+          } else {
+            acc.x += v[u].x;
+            acc.y += v[u].y;
+            acc.z += v[u].z;
+            acc.w += v[u].w;
+          }
+        }
+    }
+    splitk_store<ODT>(out, i, acc.x);
+    splitk_store<ODT>(out, i + 1, acc.y);
+    splitk_store<ODT>(out, i + 2, acc.z);
+    splitk_store<ODT>(out, i + 3, acc.w);
+    return;
+  }
+  for (int64_t e = i; e < n && e < i + 4; e++) {
+    float s = part[e];
+    for (int z = 1; z < splits; z++) s += part[(int64_t)z * n + e];
+    splitk_store<ODT>(out, e, s);
+  }
 }
 
 int launch_splitk_reduce(const float *part, void *out, int out_dtype, int64_t n, int splits, hipStream_t s) {
-  dim3 rg((unsigned)cdiv(n, 256));
+  dim3 rg((unsigned)cdiv(cdiv(n, 4), 256));
   switch (out_dtype) {
     case F32: splitk_reduce_kernel<F32><<<rg, 256, 0, s>>>(part, out, n, splits); break;
     case BF16: splitk_reduce_kernel<BF16><<<rg, 256, 0, s>>>(part, out, n, splits); break;
@@ -759,14 +795,7 @@ static int launch_gemm_t(const GemmArgs &a0, int out_dtype, void *out, float *pa
   gemm_kernel<WP, BM><<<grid, 256, T::LDS, s>>>(a);
   if (int rc = check_launch("gemm")) return rc;
   if (direct) return HQ_OK;
-  int64_t n = (int64_t)a.M * a.N;
-  dim3 rg((unsigned)cdiv(n, 256));
-  switch (out_dtype) {
-    case F32: splitk_reduce_kernel<F32><<<rg, 256, 0, s>>>(partials, out, n, a.splits); break;
-    case BF16: splitk_reduce_kernel<BF16><<<rg, 256, 0, s>>>(partials, out, n, a.splits); break;
-    default: splitk_reduce_kernel<F16><<<rg, 256, 0, s>>>(partials, out, n, a.splits); break;
-  }
-  return check_launch("splitk_reduce");
+  return launch_splitk_reduce(partials, out, out_dtype, (int64_t)a.M * a.N, a.splits, s);
 }
 
 // M <= 64 only (larger M takes the warp-specialised kernel of gemm_ws.hip).
