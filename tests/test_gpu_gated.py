@@ -136,7 +136,11 @@ def test_mlp_repeated_calls_agree(dev):
 
 
 @pytest.mark.parametrize("dt,M,H,I", [(hipq.Q4_K, 1, 4096, 14336), (hipq.Q4_K, 3, 1024, 2816),
-                                      (hipq.Q5_K, 2, 1024, 2816), (hipq.Q8_0, 1, 512, 768)])
+                                      (hipq.Q5_K, 2, 1024, 2816), (hipq.Q8_0, 1, 512, 768),
+                                      # both unit variants (two-level x below 8192, one level
+                                      # from it) on each side; fewer chunks than workgroups
+                                      (hipq.Q5_K, 1, 1024, 2816), (hipq.Q4_K, 1, 8192, 1024),
+                                      (hipq.Q4_K, 1, 256, 256), (hipq.Q4_K, 1, 2048, 768)])
 def test_gated_act_then_down_equals_mlp(dev, dt, M, H, I):
     """hq_matmul_q_gated_act followed by hq_matmul_q_act is hq_mlp_q split at its kernel
     boundary: the same launches, so the same bits (the unfused formats run the same
@@ -155,3 +159,29 @@ def test_gated_act_then_down_equals_mlp(dev, dt, M, H, I):
     else:  # mlp_q's unfused path feeds F32 h to hq_matmul_q; here h is quantized first
         scale = want.abs().max().item()
         assert (got - want).abs().max().item() <= 1e-3 * scale
+
+
+def test_mlp_streams_and_repeats(dev):
+    """hq_mlp_q without a caller workspace keeps one per stream: calls alternating over three
+    streams, repeated, reproduce the separate-launch result bit for bit every time."""
+    print("[case] mlp three streams", flush=True)
+    g = synth.rng(91)
+    H, I = 4096, 14336
+    t = lambda a: torch.from_numpy(a).to(dev)
+    wg, wu, wd = (t(synth.gguf_weight(hipq.Q4_K, r, c, g)) for r, c in ((I, H), (I, H), (H, I)))
+    xs = [t(synth.activations(1, H, g)) for _ in range(3)]
+    want = [hipq.matmul_q_act(hipq.matmul_q_gated_act(x, wg, wu, I, H, hipq.Q4_K), wd, 1, H, I, hipq.Q4_K)
+            for x in xs]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(device=dev) for _ in range(3)]
+    outs = [[None] * 3 for _ in range(3)]
+    for rep in range(20):
+        for i, st in enumerate(streams):
+            with torch.cuda.stream(st):
+                y = hipq.mlp_q(xs[i], wg, wu, wd, H, I, hipq.Q4_K, stream=st)
+            if rep < 3:
+                outs[i][rep] = y
+    torch.cuda.synchronize()
+    for i in range(3):
+        for rep in range(3):
+            assert torch.equal(outs[i][rep], want[i]), (i, rep)
