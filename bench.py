@@ -373,9 +373,9 @@ def moe_rows(c, name, g, dev, cpu=False):
                 t, th, smp = cpu_moe_leg(h.cpu().numpy(), wdn_np, dt, E, H, I, sp_np, se_np, topk, tw_np)
             row.update(cpu_us=round(t * 1e6, 1), cpu_threads=th, cpu_sample=smp, gpu_over_cpu=round(t * 1e6 / us, 1))
         out.append(row)
-    # The whole routed block on the device: router probs -> routing + gated gate/up (SiLU * up)
-    # in one launch -> down (routing-weighted) with the combine in its epilogue.  Probs rotate
-    # over 16 draws.
+    # The whole routed block on the device (hq_moe_block_q): router probs -> routing + gated
+    # gate/up (SiLU * up) -> down (routing-weighted) with the combine in its epilogue, in one
+    # launch for a single token.  Probs rotate over 16 draws.
     probs = []
     for _ in range(16):
         lg = torch.from_numpy(g.standard_normal((T, E)).astype(np.float32))
@@ -383,15 +383,12 @@ def moe_rows(c, name, g, dev, cpu=False):
     hg = torch.zeros((M, I), device=dev)
     ws_g = torch.empty(max(hipq.moe_gemm_q_gated_ws_bytes(M, T, I, H, dt), 256), dtype=torch.uint8, device=dev)
     yb = torch.empty((T, H), device=dev)
-    ws_c = torch.empty(max(hipq.lib().hq_moe_gemm_q_combine_ws_bytes(T, topk, E, H, I, dt), 256), dtype=torch.uint8,
+
+    ws_b = torch.empty(max(hipq.lib().hq_moe_block_q_ws_bytes(T, topk, E, H, I, dt), 256), dtype=torch.uint8,
                        device=dev)
 
-    ws_r = torch.empty(max(hipq.lib().hq_moe_route_gated_ws_bytes(T, topk, E, I, H, dt), 256), dtype=torch.uint8,
-                       device=dev)
-
-    def block(i):
-        _, w, sp, se, _ = hipq.moe_route_gated(probs[i % 16], x, wgu, E, I, H, dt, topk, h=hg, ws=ws_r)
-        hipq.moe_gemm_q_combine(hg, wdn, sp, se, E, H, I, dt, topk, topk_w=w, out=yb, ws=ws_c)
+    def block(i):  # hq_moe_block_q: one launch for a single token, else route-gated + combine
+        hipq.moe_block_q(probs[i % 16], x, wgu, wdn, E, H, I, dt, topk, out=yb, h=hg, ws=ws_b)
 
     us = time_launches(block, 64, 16)
     used = float(np.mean([len(np.unique(torch.topk(p_, topk, dim=1).indices.cpu().numpy())) for p_ in probs]))

@@ -355,6 +355,21 @@ int hq_moe_route_gated(const float *probs, const float *x, const void *w, float 
                        int64_t *sorted_pairs, int64_t *sorted_expts, int32_t *counts, int32_t *offsets, void *ws,
                        size_t ws_bytes, hq_stream_t stream);
 
+/* The SparseMoE decode block (nn/moe.go:150-236: MoERoute, runExperts' MoEGemmQ, Narrow,
+ * SiLU / GeluErf, Mul, MoEGemmQ with the routing weights, MoECombine): hq_moe_route_gated
+ * followed by hq_moe_gemm_q_combine, with their arguments (x F32 (T, H), w_gate_up the
+ * stacked GateUp (E, 2I, H), w_down (E, H, I), h F32 (T*topk, I) the per-pair activations it
+ * writes on the way, y F32 (T, H)) and the same bits.  For one token (T = 1) of Q4_K / Q5_K
+ * one kernel runs the whole block, with a grid barrier between the gate/up and the down
+ * projection; that kernel serves the first stream that calls this function on a device
+ * (other streams get the two launches), and graph replays of it must not run beside one
+ * another.  No counterpart kernel in Light: the fusion of (f) row 4. */
+size_t hq_moe_block_q_ws_bytes(int64_t T, int topk, int64_t E, int64_t H, int64_t I, int w_dtype);
+int hq_moe_block_q(const float *probs, const float *x, const void *w_gate_up, const void *w_down, float *h, float *y,
+                   int64_t T, int64_t E, int topk, int normalize, int64_t H, int64_t I, int w_dtype, int act,
+                   int64_t *topk_ids, float *weights, int64_t *sorted_pairs, int64_t *sorted_expts, int32_t *counts,
+                   int32_t *offsets, void *ws, size_t ws_bytes, hq_stream_t stream);
+
 /* ops.MoEInt4 (ops/int4.go:149-246): the routed gated-MLP expert block with canonical 4-bit
  * experts (GPTQ / AWQ MoE checkpoints):
  *   y[t] (T, H) = sum over j < topk of w[t*topk+j] * down_e(act(gate_e x[t]) * up_e x[t]),

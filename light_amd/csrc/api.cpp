@@ -760,6 +760,44 @@ int hq_moe_route_gated(const float *probs, const float *x, const void *w, float 
                                     sorted_pairs, sorted_expts, counts, offsets, ws, s);
 }
 
+size_t hq_moe_block_q_ws_bytes(int64_t T, int topk, int64_t E, int64_t H, int64_t I, int w_dtype) {
+  if (T <= 0 || topk < 1 || E <= 0 || H <= 0 || I <= 0) return 0;
+  return moe_block_ws_bytes(T, topk, E, H, I, w_dtype);
+}
+
+int hq_moe_block_q(const float *probs, const float *x, const void *w_gate_up, const void *w_down, float *h, float *y,
+                   int64_t T, int64_t E, int topk, int normalize, int64_t H, int64_t I, int w_dtype, int act,
+                   int64_t *topk_ids, float *weights, int64_t *sorted_pairs, int64_t *sorted_expts, int32_t *counts,
+                   int32_t *offsets, void *ws, size_t ws_bytes, hq_stream_t stream) {
+  const char *call = "hq_moe_block_q";
+  if (!is_gguf(w_dtype)) return fail(HQ_EUNSUPPORTED, call, "weight dtype %d has no fused kernel", w_dtype);
+  if (act != HQ_ACT_SILU && act != HQ_ACT_GELU_ERF) return fail(HQ_EINVAL, call, "activation %d", act);
+  if (T < 0 || E < 1) return fail(HQ_EINVAL, call, "probs must be (T, E), got (%lld, %lld)", (long long)T, (long long)E);
+  if (topk < 1 || topk > E) return fail(HQ_EINVAL, call, "topk %d out of range [1, %lld]", topk, (long long)E);
+  if (H <= 0 || I <= 0) return fail(HQ_EINVAL, call, "bad shape H=%lld I=%lld", (long long)H, (long long)I);
+  BlockInfo bi = block_info(w_dtype);
+  if (H % bi.elems || I % bi.elems)
+    return fail(HQ_EINVAL, call, "H=%lld, I=%lld not multiples of block size %d", (long long)H, (long long)I,
+                bi.elems);
+  if (T == 0) return HQ_OK;
+  if (topk > 64 || !moe_route_fits(T * topk, E))
+    return fail(HQ_EUNSUPPORTED, call, "T=%lld E=%lld topk=%d beyond the one-workgroup sort", (long long)T,
+                (long long)E, topk);
+  if (!probs || !x || !w_gate_up || !w_down || !h || !y || !topk_ids || !weights || !sorted_pairs || !sorted_expts)
+    return fail(HQ_EINVAL, call, "NULL pointer");
+  if (((uintptr_t)x & 15) || ((uintptr_t)h & 15)) return fail(HQ_EINVAL, call, "x and h must be 16-byte aligned");
+  hipStream_t s = resolve(stream);
+  const size_t need = moe_block_ws_bytes(T, topk, E, H, I, w_dtype);
+  if (!ws) {
+    if (int rc = workspace(need, s, &ws, call)) return rc;
+  } else if (ws_bytes < need) {
+    return fail(HQ_ENOMEM, call, "workspace %zu bytes < %zu needed", ws_bytes, need);
+  }
+  TraceSpan span("moe_block_q", s);
+  return launch_moe_block_any(probs, x, w_gate_up, w_down, h, y, T, E, topk, normalize, H, I, w_dtype, act, topk_ids,
+                              weights, sorted_pairs, sorted_expts, counts, offsets, ws, s);
+}
+
 size_t hq_moe_int4_ws_bytes(int64_t T, int topk, int64_t I) {
   if (T <= 0 || topk < 1 || I <= 0) return 0;
   return moe_int4_ws_bytes(T, topk, I);

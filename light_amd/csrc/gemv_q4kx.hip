@@ -37,6 +37,7 @@
 #include "route.hpp"
 
 #include <algorithm>
+#include <mutex>
 
 namespace hq {
 
@@ -856,11 +857,11 @@ __device__ __forceinline__ Seg lds_segment(const int *se, int n, int j, int lane
   return sg;
 }
 
-template <class U, int MM, bool GATED, bool ROUTE = false>
-__global__ __launch_bounds__(512) void moe_gemv_x_kernel(MoeXArgs ma) {
-  extern __shared__ __align__(16) uint8_t smem[];
-  __shared__ int r_e[ROUTE ? 64 : 1], r_se[ROUTE ? 64 : 1], r_sp[ROUTE ? 64 : 1];
-  __shared__ float r_w[ROUTE ? 64 : 1];
+// The kernel body for workgroup (bx, by) of a (G, gridDim.y) grid; r_* are the routing's LDS
+// arrays (64 entries each, ROUTE only).  A workgroup without work returns after the routing.
+template <class U, int MM, bool GATED, bool ROUTE = false, bool COH = false>
+__device__ __forceinline__ void moe_x_body(const MoeXArgs &ma, uint8_t *smem, int *r_e, float *r_w, int *r_se,
+                                           int *r_sp, const int bx, const int by, const int G) {
   const Q4kxArgs &a = ma.g;
   const int t = threadIdx.x, lane = t & 63;
   // One row of x (a single token's gate/up, plain kernel): every pair reads row 0, so the first slice of
@@ -904,7 +905,7 @@ __global__ __launch_bounds__(512) void moe_gemv_x_kernel(MoeXArgs ma) {
   Seg sg;
   if constexpr (ROUTE) {
     route_in_workgroup(ma, r_e, r_w, r_se, r_sp);
-    if (blockIdx.x == 0 && blockIdx.y == 0) {
+    if (bx == 0 && by == 0) {
       for (int i = t; i < (int)ma.npairs; i += blockDim.x) {
         ma.topk_ids[i] = r_e[i];
         ma.weights_out[i] = r_w[i];
@@ -912,14 +913,14 @@ __global__ __launch_bounds__(512) void moe_gemv_x_kernel(MoeXArgs ma) {
         ma.sorted_expts_out[i] = r_se[i];
       }
     }
-    sg = lds_segment(r_se, (int)ma.npairs, (int)blockIdx.y, lane);
+    sg = lds_segment(r_se, (int)ma.npairs, by, lane);
   } else {
-    sg = find_segment(ma.expts, ma.npairs, (int)blockIdx.y, lane);
+    sg = find_segment(ma.expts, ma.npairs, by, lane);
   }
   if (sg.seg0 < 0) return;
   const int64_t seg0 = sg.seg0, seg1 = sg.seg1;
   const int e = sg.e;
-  if (blockIdx.x == 0 && ma.counts && ma.offsets) {
+  if (bx == 0 && ma.counts && ma.offsets) {
     // counts / offsets of the experts (eprev, e], and of (e, E) after the last segment.
     const int lo = sg.eprev + 1 > 0 ? sg.eprev + 1 : 0;
     const int hi = seg1 == ma.npairs ? ma.E - 1 : (e < ma.E ? e : ma.E - 1);
@@ -936,8 +937,7 @@ __global__ __launch_bounds__(512) void moe_gemv_x_kernel(MoeXArgs ma) {
   const bool active = u < a.P;
   const typename U::Lane L = unit_lane<U>(active ? u : 0, a.G);
   const int ngroups = (a.N + RW - 1) / RW;
-  const int G = gridDim.x;
-  const int niter = (ngroups - (int)blockIdx.x + G - 1) / G;
+  const int niter = (ngroups - bx + G - 1) / G;
   if (niter <= 0) return;
   uint8_t *lq1 = smem, *lq2 = smem + (int64_t)MM * a.K;
   float2 *lde = reinterpret_cast<float2 *>(smem + 2 * (int64_t)MM * a.K);
@@ -956,7 +956,7 @@ __global__ __launch_bounds__(512) void moe_gemv_x_kernel(MoeXArgs ma) {
     constexpr int NW = GATED ? 2 : 1;
     typename U::W wr[NW];
     {
-      int row = (int)blockIdx.x * RW + team;
+      int row = bx * RW + team;
       row = row < a.N ? row : a.N;
       U::load(w, a.s0, a.z0, a, row, L, wr[0]);
       if (GATED) U::load(w + ma.up_off, a.s0, a.z0, a, row, L, wr[NW - 1]);
@@ -1009,7 +1009,7 @@ __global__ __launch_bounds__(512) void moe_gemv_x_kernel(MoeXArgs ma) {
     for (int mm = 0; mm < MM; mm++) wp[mm] = pid[mm] >= 0 && ma.topk_w ? ma.topk_w[pid[mm]] : 1.f;
 
     for (int it = 0; it < niter; it++) {
-      const int grp = (int)blockIdx.x + it * G;
+      const int grp = bx + it * G;
       float c[NW][MM];
 #pragma unroll
       for (int j = 0; j < NW; j++) U::template dot<MM>(wr[j], xr, L, c[j]);
@@ -1035,10 +1035,24 @@ __global__ __launch_bounds__(512) void moe_gemv_x_kernel(MoeXArgs ma) {
             tot[j] = lane < 16 ? r0 : (lane < 32 ? r1 : (lane < 48 ? r2 : r3));
         }
         const float y = GATED ? gate_act(tot[0], ma.act) * tot[NW - 1] : tot[0] * wp[mm];
-        if (u == 0 && row < a.N && pid[mm] >= 0) static_cast<float *>(a.out)[pid[mm] * a.N + row] = y;
+        if (u == 0 && row < a.N && pid[mm] >= 0) {
+          float *o = static_cast<float *>(a.out) + pid[mm] * a.N + row;
+          if constexpr (COH)  // read by other workgroups in the same launch: agent-coherent
+            __hip_atomic_store(o, y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          else
+            *o = y;
+        }
       }
     }
   }
+}
+
+template <class U, int MM, bool GATED, bool ROUTE = false>
+__global__ __launch_bounds__(512) void moe_gemv_x_kernel(MoeXArgs ma) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  __shared__ int r_e[ROUTE ? 64 : 1], r_se[ROUTE ? 64 : 1], r_sp[ROUTE ? 64 : 1];
+  __shared__ float r_w[ROUTE ? 64 : 1];
+  moe_x_body<U, MM, GATED, ROUTE>(ma, smem, r_e, r_w, r_se, r_sp, (int)blockIdx.x, (int)blockIdx.y, (int)gridDim.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -1061,12 +1075,21 @@ struct MoeCombArgs {
   int E, topk;
 };
 
-template <class U>
-__global__ __launch_bounds__(512) void moe_down_combine_kernel(MoeCombArgs ma) {
-  extern __shared__ __align__(16) uint8_t smem[];
+// The kernel body for workgroup bx of G (token tok).  FUSED (the one-launch MoE block): the
+// slots' experts and routing weights come from the workgroup's own routing (slot_e, slot_w),
+// the first weights go out before hook() -- which waits until h is complete -- and h is read
+// with agent-coherent loads after it.
+struct NoWait {
+  __device__ void operator()() const {}
+};
+
+template <class U, bool FUSED = false, class Hook = NoWait>
+__device__ __forceinline__ void moe_comb_body(const MoeCombArgs &ma, uint8_t *smem, const int bx, const int tok,
+                                              const int G, const int *slot_e = nullptr,
+                                              const float *slot_w = nullptr, const Hook &hook = Hook()) {
   const Q4kxArgs &a = ma.g;
   const int t = threadIdx.x, lane = t & 63;
-  const int tok = blockIdx.y, topk = ma.topk;
+  const int topk = ma.topk;
   const int RW = a.RW, KB = a.K >> 5, RPW = RW / topk;  // rows per workgroup
   // LDS: act of the token's topk h rows | expert per slot | pair values [RPW][topk]
   uint8_t *lq1 = smem, *lq2 = smem + (int64_t)topk * a.K;
@@ -1079,12 +1102,14 @@ __global__ __launch_bounds__(512) void moe_down_combine_kernel(MoeCombArgs ma) {
   const int ntask = topk * KB * 8, bd = (int)blockDim.x;
   const float *x = static_cast<const float *>(a.x) + (int64_t)tok * topk * a.K;
   float4 xv[XT];
+  if constexpr (!FUSED) {
 #pragma unroll
-  for (int i = 0; i < XT; i++) {
-    const int task = i * bd + t < ntask ? i * bd + t : ntask - 1;
-    xv[i] = *reinterpret_cast<const float4 *>(x + (int64_t)(task >> 3) * 32 + (task & 7) * 4);
+    for (int i = 0; i < XT; i++) {
+      const int task = i * bd + t < ntask ? i * bd + t : ntask - 1;
+      xv[i] = *reinterpret_cast<const float4 *>(x + (int64_t)(task >> 3) * 32 + (task & 7) * 4);
+    }
   }
-  if (blockIdx.x == 0 && tok == 0 && ma.offsets) {
+  if (!FUSED && bx == 0 && tok == 0 && ma.offsets) {
     for (int e = t; e <= ma.E; e += blockDim.x) {
       auto lower = [&](int64_t v) {
         int64_t lo = 0, hi = ma.npairs;
@@ -1100,11 +1125,15 @@ __global__ __launch_bounds__(512) void moe_down_combine_kernel(MoeCombArgs ma) {
     }
   }
   // Expert of each of the token's slots, from the expert-sorted pair list (-1: none).
-  if (t < topk) lexp[t] = -1;
-  __syncthreads();
-  for (int64_t i = t; i < ma.npairs; i += blockDim.x) {
-    const int64_t p = ma.pairs[i];
-    if (p >= (int64_t)tok * topk && p < (int64_t)(tok + 1) * topk) lexp[p - (int64_t)tok * topk] = (int)ma.expts[i];
+  if constexpr (FUSED) {
+    if (t < topk) lexp[t] = slot_e[(int64_t)tok * topk + t];
+  } else {
+    if (t < topk) lexp[t] = -1;
+    __syncthreads();
+    for (int64_t i = t; i < ma.npairs; i += blockDim.x) {
+      const int64_t p = ma.pairs[i];
+      if (p >= (int64_t)tok * topk && p < (int64_t)(tok + 1) * topk) lexp[p - (int64_t)tok * topk] = (int)ma.expts[i];
+    }
   }
   __syncthreads();
   const int team = t / a.TP, u = t - team * a.TP;
@@ -1115,14 +1144,26 @@ __global__ __launch_bounds__(512) void moe_down_combine_kernel(MoeCombArgs ma) {
   const bool ok = e >= 0 && e < ma.E;
   e = ok ? e : 0;
   const uint8_t *w = a.w0 + (int64_t)e * ma.expert_bytes;
-  const int ngroups = (a.N + RPW - 1) / RPW, G = gridDim.x;
-  const int niter = (ngroups - (int)blockIdx.x + G - 1) / G;
+  const int ngroups = (a.N + RPW - 1) / RPW;
+  const int niter = (ngroups - bx + G - 1) / G;
   // The first weights go out as soon as the experts are known, before h is read.
   typename U::W wr;
   {
-    int row = (int)blockIdx.x * RPW + rloc;
+    int row = bx * RPW + rloc;
     row = row < a.N && rloc < RPW ? row : a.N;
     U::load(w, a.s0, a.z0, a, row, L, wr);
+  }
+  // FUSED: h is read once the hook returns, agent-coherently (sc1 buffer loads over the token's
+  // rows), the first XT tasks per thread all at once.
+  __amdgpu_buffer_rsrc_t hr = span_rsrc(x, (uint32_t)ntask * 16u);
+  auto hload = [&](int task) __attribute__((always_inline)) {
+    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(hr, (uint32_t)task * 16u, 0, 16 /* sc1 */);
+    return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3]));
+  };
+  if constexpr (FUSED) {
+    hook();
+#pragma unroll
+    for (int i = 0; i < XT; i++) xv[i] = hload(i * bd + t < ntask ? i * bd + t : ntask - 1);
   }
   // Quantize the token's topk rows of h into LDS, as moe_gemv_x_kernel does (eight lanes per
   // 32-block; the first XT tasks per thread were loaded at the start).
@@ -1130,7 +1171,9 @@ __global__ __launch_bounds__(512) void moe_down_combine_kernel(MoeCombArgs ma) {
     const int task = base + t < ntask ? base + t : ntask - 1;
     const int blk = task >> 3, sub = task & 7;
     float4 xq;
-    if (base < XT * bd) {
+    if (FUSED && base >= XT * bd) {
+      xq = hload(task);
+    } else if (base < XT * bd) {
 #pragma unroll
       for (int i = 0; i < XT; i++)
         if (base == i * bd) xq = xv[i];
@@ -1150,12 +1193,12 @@ __global__ __launch_bounds__(512) void moe_down_combine_kernel(MoeCombArgs ma) {
   }
   __syncthreads();
   const int64_t p = (int64_t)tok * topk + slot;
-  const float wp = ma.topk_w ? ma.topk_w[p] : 1.f;
+  const float wp = FUSED ? slot_w[p] : (ma.topk_w ? ma.topk_w[p] : 1.f);
   typename U::X xr[1];
   U::load_x(lq1, lq2, reinterpret_cast<const uint8_t *>(lde), reinterpret_cast<const uint8_t *>(lsx),
             slot * KB + L.ja, xr[0]);
   for (int it = 0; it < niter; it++) {
-    const int grp = (int)blockIdx.x + it * G;
+    const int grp = bx + it * G;
     float c[1];
     U::template dot<1>(wr, xr, L, c);
     {
@@ -1182,6 +1225,80 @@ __global__ __launch_bounds__(512) void moe_down_combine_kernel(MoeCombArgs ma) {
       static_cast<float *>(a.out)[(int64_t)tok * a.N + row] = acc;
     }
   }
+}
+
+template <class U>
+__global__ __launch_bounds__(512) void moe_down_combine_kernel(MoeCombArgs ma) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  moe_comb_body<U>(ma, smem, (int)blockIdx.x, (int)blockIdx.y, (int)gridDim.x);
+}
+
+// ---------------------------------------------------------------------------
+// The MoE decode block in one launch (one token): MoERoute + routed gated gate/up
+// (moe_x_body, ROUTE) and then the down projection with MoECombine (moe_comb_body, FUSED),
+// with a grid barrier between them.  Every workgroup routes the token itself, so after its
+// gate/up rows it already knows the experts of the down projection: it issues its first
+// down-weight loads, waits at the barrier, and only then reads h.  h goes out as
+// agent-coherent stores (complete before the workgroup arrives) and comes back as
+// agent-coherent loads, so the barrier needs no cache-wide release or acquire.
+//
+// Barrier words (a file-scope device array; see moe_block_bar): arrival counters k < 16 at
+// 64 k (workgroup bx arrives at counter bx % 16), the top counter at 64 * 16, and 16 copies of
+// the generation at 64 * (17 + r).  A workgroup reads its copy of the generation before it
+// arrives; the last arrival at a counter resets it and arrives at the top counter; the last
+// arrival there resets it and bumps every copy; the others poll their copy.  The state
+// returns to zero counts after every launch, so graph replays work.  The wait needs the whole
+// grid resident at once (the host sizes the grid to the occupancy and serves one stream);
+// it is bounded all the same.
+// ---------------------------------------------------------------------------
+constexpr int kBarSub = 16;
+constexpr int kBarWords = 64 * (17 + kBarSub);
+constexpr uint32_t kBarSpinLimit = 1u << 26;  // s_sleep(1) rounds, far beyond a normal wait
+
+__device__ __forceinline__ void bar_arrive(uint32_t *w, int bx, int G, uint32_t gen) {
+  const int k = bx % kBarSub;
+  const uint32_t nk = (uint32_t)((G - 1 - k) / kBarSub + 1);
+  if (__hip_atomic_fetch_add(&w[64 * k], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u != nk) return;
+  __hip_atomic_store(&w[64 * k], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint32_t nsub = (uint32_t)(G < kBarSub ? G : kBarSub);
+  if (__hip_atomic_fetch_add(&w[64 * kBarSub], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u != nsub) return;
+  __hip_atomic_store(&w[64 * kBarSub], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (int r = 0; r < kBarSub; r++)
+    __hip_atomic_store(&w[64 * (17 + r)], gen + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+struct BarWait {
+  uint32_t *w;
+  uint32_t gen;
+  int bx;
+  __device__ void operator()() const {
+    if (threadIdx.x == 0) {
+      uint32_t *g = &w[64 * (17 + bx % kBarSub)];
+      for (uint32_t n = 0; n < kBarSpinLimit; n++) {
+        if (__hip_atomic_load(g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != gen) break;
+        __builtin_amdgcn_s_sleep(1);
+      }
+    }
+    __syncthreads();
+  }
+};
+
+template <class U>
+__global__ __launch_bounds__(512) void moe_block_kernel(MoeXArgs ma1, MoeCombArgs ma2, uint32_t *bar, int per,
+                                                        int nseg) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  __shared__ int r_e[64], r_se[64], r_sp[64];
+  __shared__ float r_w[64];
+  const int id = (int)blockIdx.x, G = (int)gridDim.x;
+  uint32_t gen = 0;
+  if (threadIdx.x == 0) gen = __hip_atomic_load(&bar[64 * (17 + id % kBarSub)], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // Gate/up: workgroup (id % per, id / per); ids past per * nseg only route (no segment).
+  const int by = id / per < nseg ? id / per : nseg;
+  moe_x_body<U, 1, true, true, true>(ma1, smem, r_e, r_w, r_se, r_sp, id % per, by, per);
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's h stores are complete
+  __syncthreads();
+  if (threadIdx.x == 0) bar_arrive(bar, id, G, gen);
+  moe_comb_body<U, true>(ma2, smem, id, 0, G, r_e, r_w, BarWait{bar, gen, id});
 }
 
 // ---------------------------------------------------------------------------
@@ -1864,6 +1981,120 @@ int launch_moe_route_gated(const float *probs, const float *x, const void *w, fl
   if (dt == Q5_K)
     return avg <= 1 ? run_moe_x<Q5kUnit, 1, true, true>(ma, active, s) : run_moe_x<Q5kUnit, 2, true, true>(ma, active, s);
   return avg <= 1 ? run_moe_x<Q4kUnit, 1, true, true>(ma, active, s) : run_moe_x<Q4kUnit, 2, true, true>(ma, active, s);
+}
+
+// The one-launch MoE block's barrier words: a file-scope device array (zero when the library
+// loads) that serves one stream per device -- the first to run the block; other streams take
+// the two launches (two such grids side by side could each hold CUs the other waits for).
+static __device__ __align__(256) uint32_t g_moe_bar[kBarWords];
+
+static uint32_t *moe_block_bar(hipStream_t s) {
+  static std::mutex mu;
+  static uint32_t *base[64] = {};
+  static hipStream_t owner[64] = {};
+  static bool init[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lk(mu);
+  if (!init[dev]) {
+    void *p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_moe_bar)) != hipSuccess || !p) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+    base[dev] = static_cast<uint32_t *>(p);
+    owner[dev] = s;
+    init[dev] = true;
+  }
+  return owner[dev] == s ? base[dev] : nullptr;
+}
+
+// MoERoute + gated gate/up + down + MoECombine for one token in one launch; returns 1 (and
+// launches nothing) where it does not apply: Q4_K / Q5_K, T = 1, the route_gated and
+// down-combine geometries, and a grid that fits the device at once.
+int launch_moe_block(const float *probs, const float *x, const void *wgu, const void *wdn, float *h, float *y,
+                     int64_t T, int64_t E, int topk, int normalize, int64_t H, int64_t I, int dt, int act,
+                     int64_t *topk_ids, float *weights, int64_t *sorted_pairs, int64_t *sorted_expts,
+                     int32_t *counts, int32_t *offsets, hipStream_t s) {
+  constexpr int kNo = 1;
+  if (T != 1 || (dt != Q4_K && dt != Q5_K) || topk > 64) return kNo;
+  if (!moe_route_gated_ok(T, E, topk, H, dt, wgu, x) || !moe_comb_ok(topk, T, topk, I, dt, wdn, h)) return kNo;
+  uint32_t *bar = moe_block_bar(s);
+  if (!bar) return kNo;
+  MoeXArgs ma1;
+  const int64_t rb1 = q4kx_row_bytes(dt, H), rb2 = q4kx_row_bytes(dt, I);
+  if (q4kx_setup(ma1.g, 1, 2 * I, H, 256, rb1, "moe_block")) return kNo;
+  const int64_t M = T * topk;
+  ma1.g.N = (int)I;
+  ma1.g.x = x;
+  ma1.g.w0 = static_cast<const uint8_t *>(wgu);
+  ma1.g.out = h;
+  ma1.pairs = nullptr;
+  ma1.expts = nullptr;
+  ma1.counts = counts;
+  ma1.offsets = offsets;
+  ma1.topk_w = nullptr;
+  ma1.size_m = M;
+  ma1.expert_bytes = 2 * I * rb1;
+  ma1.up_off = I * rb1;
+  ma1.act = act;
+  ma1.rows = T;
+  ma1.npairs = M;
+  ma1.E = (int)E;
+  ma1.topk = topk;
+  ma1.rpp = 0;
+  ma1.probs = probs;
+  ma1.topk_ids = topk_ids;
+  ma1.weights_out = weights;
+  ma1.sorted_pairs_out = sorted_pairs;
+  ma1.sorted_expts_out = sorted_expts;
+  ma1.T = (int)T;
+  ma1.normalize = normalize;
+  MoeCombArgs ma2;
+  if (q4kx_setup(ma2.g, 1, H, I, 256, rb2, "moe_block")) return kNo;
+  ma2.g.x = h;
+  ma2.g.w0 = static_cast<const uint8_t *>(wdn);
+  ma2.g.out = y;
+  ma2.pairs = nullptr;
+  ma2.expts = nullptr;
+  ma2.counts = nullptr;
+  ma2.offsets = nullptr;
+  ma2.topk_w = nullptr;
+  ma2.expert_bytes = H * rb2;
+  ma2.npairs = M;
+  ma2.E = (int)E;
+  ma2.topk = topk;
+  if (ma1.g.TP * ma1.g.RW > 512 || ma2.g.TP * ma2.g.RW > 512) return kNo;
+  // Gate/up grid as run_moe_x sizes it; the down projection's row groups over the same grid.
+  const int64_t nseg = M < E ? M : E;
+  const int ngroups1 = (ma1.g.N + ma1.g.RW - 1) / ma1.g.RW;
+  int64_t per = cdiv((int64_t)device_cus() * 2, nseg);
+  per = per < ngroups1 ? per : ngroups1;
+  per = cdiv(ngroups1, cdiv(ngroups1, per));
+  const size_t lds = std::max((size_t)q4kx_act_lds(1, H),
+                              (size_t)q4kx_act_lds(topk, I) + 64 * 4 + 2 * (size_t)(ma2.g.RW / topk) * topk * 4);
+  if (lds > 64 * 1024) return kNo;
+  auto *kern = dt == Q5_K ? &moe_block_kernel<Q5kUnit> : &moe_block_kernel<Q4kUnit>;
+  static int per_cu[2] = {-1, -1};
+  int &pc = per_cu[dt == Q5_K];
+  if (pc < 0) {
+    int nb = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void *>(kern), 512, lds) !=
+        hipSuccess) {
+      (void)hipGetLastError();
+      nb = 0;
+    }
+    pc = nb;
+  }
+  const int64_t resident = (int64_t)device_cus() * (pc < 2 ? pc : 2);
+  const int64_t G = std::max<int64_t>(per * nseg, device_cus() * 2);
+  if (pc < 1 || G > resident) return kNo;
+  kern<<<(unsigned)G, 512, lds, s>>>(ma1, ma2, bar, (int)per, (int)nseg);
+  if (int rc = check_launch("moe_block")) return rc;
+  return HQ_OK;
 }
 
 // MoEInt4 on the decode GEMV machinery: H and I multiples of 64, G % 32 == 0, topk teams of

@@ -145,6 +145,15 @@ int launch_moe_route_gated(const float *probs, const float *x, const void *w, fl
                            int topk, int normalize, int64_t I, int64_t K, int dt, int act, int64_t *topk_ids,
                            float *weights, int64_t *sorted_pairs, int64_t *sorted_expts, int32_t *counts,
                            int32_t *offsets, hipStream_t s);
+int launch_moe_block(const float *probs, const float *x, const void *wgu, const void *wdn, float *h, float *y,
+                     int64_t T, int64_t E, int topk, int normalize, int64_t H, int64_t I, int dt, int act,
+                     int64_t *topk_ids, float *weights, int64_t *sorted_pairs, int64_t *sorted_expts,
+                     int32_t *counts, int32_t *offsets, hipStream_t s);
+size_t moe_block_ws_bytes(int64_t T, int topk, int64_t E, int64_t H, int64_t I, int dt);
+int launch_moe_block_any(const float *probs, const float *x, const void *wgu, const void *wdn, float *h, float *y,
+                         int64_t T, int64_t E, int topk, int normalize, int64_t H, int64_t I, int dt, int act,
+                         int64_t *topk_ids, float *weights, int64_t *sorted_pairs, int64_t *sorted_expts,
+                         int32_t *counts, int32_t *offsets, void *ws, hipStream_t s);
 bool moe_int4_ok(int64_t H, int64_t I, int G, int topk);
 size_t moe_int4_ws_bytes(int64_t T, int topk, int64_t I);
 int launch_moe_int4(const void *x, int x_dtype, const void *const *tab, int64_t E, const int64_t *ids,

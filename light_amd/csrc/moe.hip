@@ -246,4 +246,26 @@ int launch_moe_route_gated_any(const float *probs, const float *x, const void *w
                             inner, s);
 }
 
+size_t moe_block_ws_bytes(int64_t T, int topk, int64_t E, int64_t H, int64_t I, int dt) {
+  return std::max(moe_route_gated_ws_bytes(T, topk, E, I, H, dt), moe_combine_ws_bytes(T * topk, E, H, I, dt));
+}
+
+// The SparseMoE decode block: MoERoute, the routed gated gate/up into h, then the down
+// projection with MoECombine into y.  One launch for a single token where it applies
+// (launch_moe_block); otherwise the route-gated launch and the combine path in sequence, on
+// the same workspace (the two do not overlap in time).  Bit-identical either way.
+int launch_moe_block_any(const float *probs, const float *x, const void *wgu, const void *wdn, float *h, float *y,
+                         int64_t T, int64_t E, int topk, int normalize, int64_t H, int64_t I, int dt, int act,
+                         int64_t *topk_ids, float *weights, int64_t *sorted_pairs, int64_t *sorted_expts,
+                         int32_t *counts, int32_t *offsets, void *ws, hipStream_t s) {
+  const int rc = launch_moe_block(probs, x, wgu, wdn, h, y, T, E, topk, normalize, H, I, dt, act, topk_ids, weights,
+                                  sorted_pairs, sorted_expts, counts, offsets, s);
+  if (rc != 1) return rc;
+  if (int r = launch_moe_route_gated_any(probs, x, wgu, h, T, E, topk, normalize, I, H, dt, act, topk_ids, weights,
+                                         sorted_pairs, sorted_expts, counts, offsets, ws, s))
+    return r;
+  return launch_moe_q_combine(h, wdn, sorted_pairs, sorted_expts, counts, offsets, weights, y, topk, T, E, H, I, dt,
+                              ws, s);
+}
+
 }  // namespace hq

@@ -93,6 +93,9 @@ SIGNATURES = {
     "hq_moe_int4_ws_bytes": (_SZ, [_I64, _I, _I64]),
     "hq_moe_int4": (_I, [_P, _I, _P, _I64, _P, _P, _P, _I64, _I, _I64, _I64, _I, _I, _P, _SZ, _P]),
     "hq_moe_route_gated_ws_bytes": (_SZ, [_I64, _I, _I64, _I64, _I64, _I]),
+    "hq_moe_block_q_ws_bytes": (_SZ, [_I64, _I, _I64, _I64, _I64, _I]),
+    "hq_moe_block_q": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I, _I, _I64, _I64, _I, _I, _P, _P, _P, _P, _P, _P,
+                            _P, _SZ, _P]),
     "hq_moe_route_gated": (_I, [_P, _P, _P, _P, _I64, _I64, _I, _I, _I64, _I64, _I, _I, _P, _P, _P, _P, _P, _P, _P,
                                 _SZ, _P]),
     "hq_moe_gemm_q": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I,
@@ -409,6 +412,28 @@ def moe_route_gated(probs, x, w, E, I, K, w_dtype, topk, normalize=True, act=ACT
                                    w_dtype, act, _ptr(ids), _ptr(wt), _ptr(sp), _ptr(se), _ptr(counts),
                                    _ptr(offsets), _ptr(ws), ws_bytes, _stream(stream)))
     return ids, wt, sp, se, h
+
+
+def moe_block_q(probs, x, w_gate_up, w_down, E, H, I, w_dtype, topk, normalize=True, act=ACT_SILU, out=None, h=None,
+                counts=None, offsets=None, ws=None, stream=None):
+    """The SparseMoE decode block: (y (T, H), topk_ids, weights, sorted_pairs, sorted_expts, h)."""
+    import torch
+    T = probs.shape[0]
+    dev = probs.device
+    M = T * topk
+    ids = torch.empty((T, topk), dtype=torch.int64, device=dev)
+    wt = torch.empty(M, dtype=torch.float32, device=dev)
+    sp = torch.empty(M, dtype=torch.int64, device=dev)
+    se = torch.empty(M, dtype=torch.int64, device=dev)
+    if h is None:
+        h = torch.zeros((M, I), dtype=torch.float32, device=dev)
+    if out is None:
+        out = torch.empty((T, H), dtype=torch.float32, device=dev)
+    ws_bytes = 0 if ws is None else ws.numel() * ws.element_size()
+    check(lib().hq_moe_block_q(_ptr(probs), _ptr(x), _ptr(w_gate_up), _ptr(w_down), _ptr(h), _ptr(out), T, E, topk,
+                               int(bool(normalize)), H, I, w_dtype, act, _ptr(ids), _ptr(wt), _ptr(sp), _ptr(se),
+                               _ptr(counts), _ptr(offsets), _ptr(ws), ws_bytes, _stream(stream)))
+    return out, ids, wt, sp, se, h
 
 
 def moe_int4(x, gate_up, down, topk_ids, weights, topk, G, act=ACT_SILU, out=None, ws=None, stream=None):

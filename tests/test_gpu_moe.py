@@ -335,3 +335,57 @@ def test_moe_route_gated_bit_exact(dev, dt, T, E, topk, H, I, ties):
     for a, b, name in ((ids, ids1, "ids"), (w, w1, "weights"), (sp, sp1, "sorted_pairs"), (se, se1, "sorted_expts"),
                        (c0, c1, "counts"), (o0, o1, "offsets"), (h0, h1, "h")):
         assert torch.equal(a, b), name
+
+
+@pytest.mark.parametrize("dt,T,E,topk,H,I", [
+    (hipq.Q4_K, 1, 128, 8, 2048, 768),   # configs[4] decode: the one-launch block
+    (hipq.Q5_K, 1, 64, 4, 1024, 512),
+    (hipq.Q4_K, 1, 16, 2, 4096, 256),    # K = 4096 gate/up, few pairs
+    (hipq.Q4_K, 3, 128, 8, 2048, 768),   # several tokens: the two launches
+    (hipq.Q8_0, 1, 16, 4, 512, 256),     # no fused kernel
+])
+def test_moe_block_equals_route_gated_then_combine(dev, dt, T, E, topk, H, I):
+    """hq_moe_block_q equals hq_moe_route_gated followed by hq_moe_gemm_q_combine bit for bit:
+    y, h, the routing outputs and counts / offsets -- in one launch (T = 1) as in two.  Three
+    calls in a row (the grid barrier's state carries over between launches) all agree."""
+    print(f"[case] moe block dt={hipq.NAMES[dt]} T={T} E={E} topk={topk} H={H} I={I}", flush=True)
+    g = synth.rng(1700 + T + E + dt)
+    wgu = _t(synth.gguf_weight(dt, E * 2 * I, H, g), dev)
+    wdn = _t(synth.gguf_weight(dt, E * H, I, g), dev)
+    x = _t(synth.activations(T, H, g), dev)
+    probs = _t(_probs(g, T, E, ties=False), dev)
+    c0 = torch.zeros(E, dtype=torch.int32, device=dev)
+    o0 = torch.zeros(E + 1, dtype=torch.int32, device=dev)
+    ids, w, sp, se, h = hipq.moe_route_gated(probs, x, wgu, E, I, H, dt, topk, counts=c0, offsets=o0)
+    y = hipq.moe_gemm_q_combine(h, wdn, sp, se, E, H, I, dt, topk, topk_w=w)
+    for rep in range(3):
+        c1 = torch.full((E,), -5, dtype=torch.int32, device=dev)
+        o1 = torch.full((E + 1,), -5, dtype=torch.int32, device=dev)
+        y1, ids1, w1, sp1, se1, h1 = hipq.moe_block_q(probs, x, wgu, wdn, E, H, I, dt, topk, counts=c1, offsets=o1)
+        torch.cuda.synchronize()
+        for a, b, name in ((y, y1, "y"), (h, h1, "h"), (ids, ids1, "ids"), (w, w1, "weights"),
+                           (sp, sp1, "sorted_pairs"), (se, se1, "sorted_expts"), (c0, c1, "counts"),
+                           (o0, o1, "offsets")):
+            assert torch.equal(a, b), (name, rep)
+
+
+def test_moe_block_second_stream_and_changing_routes(dev):
+    """The one-launch block on its stream and the two-launch path on another stream agree with
+    the separate calls, for routings that change from call to call."""
+    print("[case] moe block, two streams, 6 routings", flush=True)
+    dt, E, topk, H, I = hipq.Q4_K, 128, 8, 2048, 768
+    g = synth.rng(1777)
+    wgu = _t(synth.gguf_weight(dt, E * 2 * I, H, g), dev)
+    wdn = _t(synth.gguf_weight(dt, E * H, I, g), dev)
+    x = _t(synth.activations(1, H, g), dev)
+    other = torch.cuda.Stream(device=dev)
+    for i in range(6):
+        probs = _t(_probs(g, 1, E, ties=False), dev)
+        ids, w, sp, se, h = hipq.moe_route_gated(probs, x, wgu, E, I, H, dt, topk)
+        want = hipq.moe_gemm_q_combine(h, wdn, sp, se, E, H, I, dt, topk, topk_w=w)
+        got = hipq.moe_block_q(probs, x, wgu, wdn, E, H, I, dt, topk)[0]
+        with torch.cuda.stream(other):
+            got2 = hipq.moe_block_q(probs, x, wgu, wdn, E, H, I, dt, topk, stream=other)[0]
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), i
+        assert torch.equal(got2, want), i
