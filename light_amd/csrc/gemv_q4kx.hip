@@ -763,13 +763,70 @@ struct MoeXArgs {
 };
 
 // MoERoute inside a workgroup, for T * topk <= 64 pairs and T <= 8 tokens: wave t selects
-// token t's top-k (topk_row_any, as moe_route_kernel), then wave 0 places each pair at its
-// rank in the stable expert order (pairs of one expert keep pair order).  The LDS arrays
-// end as MoERoute's outputs: re/rw per pair, se/sp in sorted order.
+// token t's top-k (topk_row_any, as moe_route_kernel; or the rank path below), then wave 0
+// places each pair at its rank in the stable expert order (pairs of one expert keep pair
+// order).  The LDS arrays end as MoERoute's outputs: re/rw per pair, se/sp in sorted order.
+//
+// Where the workgroup has a thread per probability (T E <= blockDim.x), the top-k is found by
+// rank instead: each thread counts the keys of its row above its own (from LDS, the same
+// address for every lane of a row at a time), and the keys of rank < topk are the selection,
+// in rank order -- the order the repeated maxima find them (keys are distinct).  One pass
+// instead of topk rounds of wave-wide maxima (E = 128, topk = 8: 3 -> ~0.5 us).
 __device__ void route_in_workgroup(const MoeXArgs &ma, int *re, float *rw, int *se, int *sp) {
+  __shared__ uint64_t rkeys[512];
+  __shared__ int rpart[512];
+  __shared__ float rsel[64];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int M = (int)ma.npairs;
-  if (wave < ma.T) {
+  if (ma.T * ma.E <= (int)blockDim.x && ma.T * ma.E <= 512) {
+    const int E = ma.E, n = ma.T * E;
+    // nq threads per key, each counting over its quarter (half, ...) of the row.
+    const int nq = (int)blockDim.x / n >= 4 ? 4 : ((int)blockDim.x / n >= 2 ? 2 : 1);
+    const int ki = t % n, q = t / n;
+    const int tok = ki / E, e = ki - tok * E;
+    uint64_t key = 0;
+    if (t < n) {
+      key = ((uint64_t)ord_f32(ma.probs[t]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)e);
+      rkeys[t] = key;
+    }
+    __syncthreads();
+    if (q < nq) {
+      key = rkeys[ki];
+      const uint64_t *row = rkeys + tok * E;
+      const int j0 = E * q / nq, j1 = E * (q + 1) / nq;
+      int rank = 0, j = j0;
+      // Sixteen independent LDS reads per round (a read-compare loop waits out the LDS latency
+      // on every key).
+      for (; j + 16 <= j1; j += 16) {
+        uint64_t kk[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) kk[i] = row[j + i];
+#pragma unroll
+        for (int i = 0; i < 16; i++) rank += kk[i] > key ? 1 : 0;
+      }
+      for (; j < j1; j++) rank += row[j] > key ? 1 : 0;
+      rpart[t] = rank;
+    }
+    __syncthreads();
+    if (t < n) {
+      int rank = 0;
+      for (int qq = 0; qq < nq; qq++) rank += rpart[qq * n + t];
+      if (rank < ma.topk) {
+        re[tok * ma.topk + rank] = e;
+        rsel[tok * ma.topk + rank] = unord_f32((uint32_t)(key >> 32));
+      }
+    }
+    __syncthreads();
+    if (t < ma.T * ma.topk) {
+      // den: the left-to-right f32 sum of the token's selected values in slot order (every
+      // lane of a token adds the same values in the same order), then each slot's weight.
+      const int tk = t / ma.topk;
+      float den = 0.f;
+      for (int jj = 0; jj < ma.topk; jj++) den = __fadd_rn(den, rsel[tk * ma.topk + jj]);
+      const float v = rsel[t];
+      rw[t] = ma.normalize ? __fdiv_rn(v, den) : v;
+    }
+  } else if (wave < ma.T) {
     float sv, den;
     int si;
     topk_row_any(ma.probs + (int64_t)wave * ma.E, ma.E, ma.topk, lane, sv, si, den);
@@ -877,13 +934,32 @@ __device__ __forceinline__ void moe_x_body(const MoeXArgs &ma, uint8_t *smem, in
   // dot.  (The barriers of the routing / the pass publish it.)
   const bool xq0 = x1 && MM == 1;
   if (xq0) {
-    const int t0 = ROUTE ? 64 * ma.T : 0;  // whole waves: act_quant8_fast works on aligned 8-lane groups
+    // Whole waves (act_quant8_fast works on aligned 8-lane groups) past the routing's: one wave
+    // per token, or a thread per probability (route_in_workgroup's rank path).
+    const int rt = ma.T * ma.E <= (int)blockDim.x && ma.T * ma.E <= 512 ? (ma.T * ma.E + 63) & ~63 : 64 * ma.T;
+    const int t0 = ROUTE ? rt : 0;
     const int nth = (int)blockDim.x - t0;
     if (t >= t0 && nth > 0) {
-      for (int base = 0; base < ntask0; base += nth) {
+      // The first XP passes' loads go out together (a load-quantize loop waited out one
+      // memory latency per pass).
+      constexpr int XP = 4;
+      float4 xp[XP];
+#pragma unroll
+      for (int i = 0; i < XP; i++) {
+        const int task = i * nth + t - t0, tc = task < ntask0 ? task : ntask0 - 1;
+        xp[i] = *reinterpret_cast<const float4 *>(static_cast<const float *>(a.x) + tc * 4);
+      }
+      for (int base = 0, pass = 0; base < ntask0; base += nth, pass++) {
         const int task = base + t - t0, tc = task < ntask0 ? task : ntask0 - 1;
         const int blk = tc >> 3, sub = tc & 7;
-        const float4 xq = *reinterpret_cast<const float4 *>(static_cast<const float *>(a.x) + blk * 32 + sub * 4);
+        float4 xq = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (pass < XP) {
+#pragma unroll
+          for (int i = 0; i < XP; i++)
+            if (pass == i) xq = xp[i];
+        } else {
+          xq = *reinterpret_cast<const float4 *>(static_cast<const float *>(a.x) + blk * 32 + sub * 4);
+        }
         const float v[4] = {xq.x, xq.y, xq.z, xq.w};
         const ActQ q = act_quant8_fast(v);
         if (task < ntask0) {
