@@ -673,17 +673,26 @@ int launch_splitk_reduce(const float *part, void *out, int out_dtype, int64_t n,
 template <int XDT>
 __global__ __launch_bounds__(256) void to_bf16_kernel(const void *__restrict__ x, uint16_t *__restrict__ y,
                                                       int64_t n4) {
-  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n4) return;
-  float v[4];
-  if constexpr (XDT == F32) {
-    float4 f = static_cast<const float4 *>(x)[i];
-    v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
-  } else {
-    uint2 u = static_cast<const uint2 *>(x)[i];
-    v[0] = h2f(u.x & 0xffffu); v[1] = h2f(u.x >> 16); v[2] = h2f(u.y & 0xffffu); v[3] = h2f(u.y >> 16);
+  // Four groups of four elements per thread, the block's 1024 groups contiguous; every load
+  // goes out before the first conversion.
+  constexpr int UN = 4;
+  const int64_t i0 = (int64_t)blockIdx.x * (UN * 256) + threadIdx.x;
+  float v[UN][4];
+#pragma unroll
+  for (int k = 0; k < UN; k++) {
+    const int64_t i = i0 + k * 256 < n4 ? i0 + k * 256 : n4 - 1;
+    if constexpr (XDT == F32) {
+      const float4 f = static_cast<const float4 *>(x)[i];
+      v[k][0] = f.x; v[k][1] = f.y; v[k][2] = f.z; v[k][3] = f.w;
+    } else {
+      const uint2 u = static_cast<const uint2 *>(x)[i];
+      v[k][0] = h2f(u.x & 0xffffu); v[k][1] = h2f(u.x >> 16); v[k][2] = h2f(u.y & 0xffffu); v[k][3] = h2f(u.y >> 16);
+    }
   }
-  reinterpret_cast<uint2 *>(y)[i] = make_uint2(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
+#pragma unroll
+  for (int k = 0; k < UN; k++)
+    if (i0 + k * 256 < n4)
+      reinterpret_cast<uint2 *>(y)[i0 + k * 256] = make_uint2(pack_bf16(v[k][0], v[k][1]), pack_bf16(v[k][2], v[k][3]));
 }
 
 // Prepared activations -> bf16 of d * q1 + e * q2.
@@ -841,10 +850,10 @@ size_t gemm_q4k_partial_bytes(int64_t M, int64_t N, int64_t K) { return gemm_par
 
 int launch_to_bf16(const void *src, int src_kind, uint16_t *dst, int64_t M, int64_t K, hipStream_t s) {
   int64_t n4 = M * K / 4;
-  dim3 g((unsigned)cdiv(n4, 256));
+  dim3 g((unsigned)cdiv(n4, 256)), g4((unsigned)cdiv(n4, 1024));
   switch (src_kind) {
-    case F32: to_bf16_kernel<F32><<<g, 256, 0, s>>>(src, dst, n4); break;
-    case F16: to_bf16_kernel<F16><<<g, 256, 0, s>>>(src, dst, n4); break;
+    case F32: to_bf16_kernel<F32><<<g4, 256, 0, s>>>(src, dst, n4); break;
+    case F16: to_bf16_kernel<F16><<<g4, 256, 0, s>>>(src, dst, n4); break;
     case BF16:
       return check(hipMemcpyAsync(dst, src, (size_t)M * K * 2, hipMemcpyDeviceToDevice, s), "hipMemcpyAsync");
     default:  // prepared activations
