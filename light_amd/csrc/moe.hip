@@ -40,6 +40,31 @@ __global__ __launch_bounds__(256) void moe_offsets_kernel(const int64_t *__restr
   if (e < E) counts[e] = (int32_t)(lower(e + 1) - a);
 }
 
+// The same offsets / counts from one workgroup, for E + 1 offsets that fit in LDS: the sorted
+// ids are read once, coalesced (a binary search per expert is a chain of dependent loads),
+// and each segment start fills the offsets of the experts up to its own:
+// offsets[e] = i for e in (ids[i-1], ids[i]], and M after the last id -- the lower bound of e.
+__global__ __launch_bounds__(1024) void moe_offsets_wg_kernel(const int64_t *__restrict__ expts, int64_t M, int E,
+                                                              int32_t *__restrict__ counts,
+                                                              int32_t *__restrict__ offsets) {
+  extern __shared__ int32_t lo[];
+  const int t = threadIdx.x, nt = blockDim.x;
+  for (int e = t; e <= E; e += nt) lo[e] = (int32_t)M;  // experts past the last id
+  __syncthreads();
+  for (int64_t i = t; i < M; i += nt) {
+    const int64_t v = expts[i], p = i > 0 ? expts[i - 1] : -1;
+    if (i == 0 || v != p) {
+      const int64_t e0 = p + 1 > 0 ? p + 1 : 0, e1 = v < E ? v : E;
+      for (int64_t e = e0; e <= e1; e++) lo[e] = (int32_t)i;
+    }
+  }
+  __syncthreads();
+  for (int e = t; e <= E; e += nt) {
+    offsets[e] = lo[e];
+    if (e < E) counts[e] = lo[e + 1] - lo[e];
+  }
+}
+
 template <int DT>
 __global__ __launch_bounds__(256) void moe_generic_kernel(const float *__restrict__ x, const uint8_t *__restrict__ w,
                                                           const int64_t *__restrict__ pairs,
@@ -114,7 +139,10 @@ int launch_moe_q(const float *x, const void *w, const int64_t *pairs, const int6
   if (M > 0 && E <= 65535 && (dt == Q5_K || !moe_use_mfma(M, E)) && moe_x_ok(K, dt, w, x))
     return launch_moe_gemv_x(x, w, pairs, expts, counts, offsets, topk_w, out, topk, size_m, M, rows, E, N, K, rpp,
                              dt, -1, s);
-  moe_offsets_kernel<<<(unsigned)cdiv(E + 1, 256), 256, 0, s>>>(expts, M, (int)E, counts, offsets);
+  if (E + 1 <= 16384)
+    moe_offsets_wg_kernel<<<1, 1024, (size_t)(E + 1) * 4, s>>>(expts, M, (int)E, counts, offsets);
+  else
+    moe_offsets_kernel<<<(unsigned)cdiv(E + 1, 256), 256, 0, s>>>(expts, M, (int)E, counts, offsets);
   if (int rc = check_launch("moe_offsets")) return rc;
   if (moe_q4k_fast(dt, K, w)) {
     if (moe_use_mfma(M, E)) {
