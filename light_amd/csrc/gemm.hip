@@ -400,6 +400,7 @@ struct MoeGemmArgs {
   float *out;
   int64_t size_m, expert_bytes;
   int topk, rpp;
+  int gated_I, act;  // gated: N = 2 I stacked gate / up rows, out (size_m, I) = act(g) * u
 };
 
 // x (rows, K) F32 -> f16, row r divided by 2^e_r (e_r = 0 unless the row's max |x| exceeds
@@ -490,6 +491,11 @@ struct Q4kF16Slot {
   }
 };
 
+// GATED: a tile's 128 B rows are gate rows n0 .. n0 + 63 and the matching up rows (I + n0 ..),
+// so waves 0-1 hold g and waves 2-3 u of the same 64 output columns; after the K loop waves 2-3
+// pass u through LDS and waves 0-1 write act(g) * u (the values the ungated kernel followed by
+// the split would give, bit for bit).
+template <bool GATED>
 __global__ __launch_bounds__(256) void moe_gemm_kernel(MoeGemmArgs ma) {
   using T = GTile<32>;
   extern __shared__ __align__(16) uint8_t smem[];
@@ -500,11 +506,17 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(MoeGemmArgs ma) {
   a.w += (int64_t)e * ma.expert_bytes;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int wn = wave;  // 4 waves along N, 32 columns each
-  const int n0 = blockIdx.x * GBN;
+  const int n0 = blockIdx.x * (GATED ? GBN / 2 : GBN);
   const int ksteps = a.K / GBK;
   const int acol = t & 7, arow = t >> 3;  // A: 32 rows x 128 B per step, one 16-byte load per thread
   const int wr = t >> 1, wh = t & 1;
-  const int wrow = n0 + wr < a.N ? n0 + wr : a.N - 1;
+  int wrow;
+  if constexpr (GATED) {
+    const int I = ma.gated_I, c = n0 + (wr & (GBN / 2 - 1));
+    wrow = (wr >= GBN / 2 ? I : 0) + (c < I ? c : I - 1);
+  } else {
+    wrow = n0 + wr < a.N ? n0 + wr : a.N - 1;
+  }
   const int fr = lane & 31, fk = (lane >> 5) * 8;
 
   for (int c0 = seg0; c0 < seg1; c0 += 32) {
@@ -564,17 +576,43 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(MoeGemmArgs ma) {
     // The ring's last (clamped) loads land before its registers can be reused.
 #pragma unroll
     for (int d = 0; d < MD; d++) wait_ring<0>(ra[d], wp[d].q, wp[d].h);
-    const int col = n0 + wn * 32 + (lane & 31);
-    if (col < a.N) {
+    if constexpr (GATED) {
+      // The stage buffers are free (the last step ended with a barrier): waves 2-3 leave u.
+      float *ux = reinterpret_cast<float *>(smem);
+      if (wn >= 2) {
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int lr = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        const int i = c0 + lr;
-        if (i >= seg1) continue;
-        const int64_t p = ma.pairs[i];
-        if (p < 0 || p >= ma.size_m) continue;
-        const int64_t row = ma.rpp ? p : p / ma.topk;
-        ma.out[p * a.N + col] = acc[r] * ma.xscale[row] * (ma.topk_w ? ma.topk_w[p] : 1.f);
+        for (int r = 0; r < 16; r++) ux[((wn - 2) * 16 + r) * 64 + lane] = acc[r];
+      }
+      __syncthreads();
+      const int col = n0 + wn * 32 + (lane & 31);
+      if (wn < 2 && col < ma.gated_I) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const int lr = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+          const int i = c0 + lr;
+          if (i >= seg1) continue;
+          const int64_t p = ma.pairs[i];
+          if (p < 0 || p >= ma.size_m) continue;
+          const int64_t row = ma.rpp ? p : p / ma.topk;
+          const float sc = ma.xscale[row];
+          const float g = acc[r] * sc, u = ux[(wn * 16 + r) * 64 + lane] * sc;
+          ma.out[p * ma.gated_I + col] = gate_act(g, ma.act) * u;
+        }
+      }
+      __syncthreads();  // (u is read before the next chunk's stages overwrite it)
+    } else {
+      const int col = n0 + wn * 32 + (lane & 31);
+      if (col < a.N) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const int lr = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+          const int i = c0 + lr;
+          if (i >= seg1) continue;
+          const int64_t p = ma.pairs[i];
+          if (p < 0 || p >= ma.size_m) continue;
+          const int64_t row = ma.rpp ? p : p / ma.topk;
+          ma.out[p * a.N + col] = acc[r] * ma.xscale[row] * (ma.topk_w ? ma.topk_w[p] : 1.f);
+        }
       }
     }
   }
@@ -582,9 +620,11 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(MoeGemmArgs ma) {
 
 // x (rows, K) F32 in, xh = f16 rows (rows * K * 2 bytes, 16-byte aligned) and xs = row scales
 // (rows floats) in the workspace.
+// gated_I > 0: N = 2 gated_I stacked gate / up rows, out (size_m, gated_I) = act(g) * u.
 int launch_moe_gemm_q4k(const float *x, uint16_t *xh, float *xs, const void *w, const int64_t *pairs,
                         const int32_t *offsets, const float *topk_w, float *out, int topk, int64_t size_m,
-                        int64_t rows, int64_t E, int64_t N, int64_t K, int rpp, hipStream_t s) {
+                        int64_t rows, int64_t E, int64_t N, int64_t K, int rpp, hipStream_t s, int64_t gated_I,
+                        int act) {
   using T = GTile<32>;
   to_f16_rowscale_kernel<<<(unsigned)rows, 256, 0, s>>>(x, reinterpret_cast<_Float16 *>(xh), xs, K);
   if (int rc = check_launch("to_f16_rowscale")) return rc;
@@ -602,8 +642,15 @@ int launch_moe_gemm_q4k(const float *x, uint16_t *xh, float *xs, const void *w, 
   ma.expert_bytes = N * (K / 256) * 144;
   ma.topk = topk;
   ma.rpp = rpp;
-  dim3 grid((unsigned)cdiv(N, GBN), (unsigned)E);
-  moe_gemm_kernel<<<grid, 256, T::LDS, s>>>(ma);
+  ma.gated_I = (int)gated_I;
+  ma.act = act;
+  if (gated_I > 0) {
+    dim3 grid((unsigned)cdiv(gated_I, GBN / 2), (unsigned)E);
+    moe_gemm_kernel<true><<<grid, 256, T::LDS, s>>>(ma);
+  } else {
+    dim3 grid((unsigned)cdiv(N, GBN), (unsigned)E);
+    moe_gemm_kernel<false><<<grid, 256, T::LDS, s>>>(ma);
+  }
   return check_launch("moe_gemm_q4k");
 }
 

@@ -171,6 +171,7 @@ int launch_moe_gemv_q4k(const void *act, const void *w, const int64_t *pairs, co
 // xs (rows row scales) in the caller's workspace, then the grouped f16 MFMA kernel.
 int launch_moe_gemm_q4k(const float *x, uint16_t *xh, float *xs, const void *w, const int64_t *pairs,
                         const int32_t *offsets, const float *topk_w, float *out, int topk, int64_t size_m,
-                        int64_t rows, int64_t E, int64_t N, int64_t K, int rpp, hipStream_t s);
+                        int64_t rows, int64_t E, int64_t N, int64_t K, int rpp, hipStream_t s, int64_t gated_I = 0,
+                        int act = 0);
 
 }  // namespace hq

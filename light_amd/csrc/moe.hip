@@ -201,6 +201,22 @@ int launch_moe_q_gated(const float *x, const void *w, const int64_t *pairs, cons
   if (M > 0 && E <= 65535 && (dt == Q5_K || !moe_use_mfma(M, E)) && moe_x_ok(K, dt, w, x))
     return launch_moe_gemv_x(x, w, pairs, expts, counts, offsets, nullptr, out, topk, size_m, M, rows, E, I, K, rpp,
                              dt, act, s);
+  if (moe_q4k_fast(dt, K, w) && moe_use_mfma(M, E)) {
+    // The grouped GEMM with the gated epilogue: h straight from the gate / up tiles.  Rows of
+    // pairs outside every expert segment stay zero, as after the split of a zeroed output.
+    void *inner = static_cast<char *>(ws) + al256m(4 * size_m * 2 * I);
+    zero_f32_kernel<<<(unsigned)cdiv(size_m * I, 256), 256, 0, s>>>(out, size_m * I);
+    if (int rc = check_launch("zero")) return rc;
+    if (E + 1 <= 16384)
+      moe_offsets_wg_kernel<<<1, 1024, (size_t)(E + 1) * 4, s>>>(expts, M, (int)E, counts, offsets);
+    else
+      moe_offsets_kernel<<<(unsigned)cdiv(E + 1, 256), 256, 0, s>>>(expts, M, (int)E, counts, offsets);
+    if (int rc = check_launch("moe_offsets")) return rc;
+    auto *xh = static_cast<uint16_t *>(inner);
+    auto *xs = reinterpret_cast<float *>(static_cast<char *>(inner) + al256m(2 * rows * K));
+    return launch_moe_gemm_q4k(x, xh, xs, w, pairs, offsets, nullptr, out, topk, size_m, rows, E, 2 * I, K, rpp, s, I,
+                               act);
+  }
   float *gu = static_cast<float *>(ws);
   void *inner = static_cast<char *>(ws) + al256m(4 * size_m * 2 * I);
   zero_f32_kernel<<<(unsigned)cdiv(size_m * 2 * I, 256), 256, 0, s>>>(gu, size_m * 2 * I);

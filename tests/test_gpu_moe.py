@@ -227,7 +227,9 @@ def test_moe_gated_decode_config(dev, act):
 
 @pytest.mark.parametrize("dt,T,E,topk,I,K,rpp", [(hipq.Q4_K, 5, 16, 4, 96, 512, False),
                                                  (hipq.Q5_K, 3, 8, 2, 64, 1024, True),
-                                                 (hipq.Q4_K, 40, 4, 2, 64, 256, False),   # M > 4E: MFMA + split
+                                                 (hipq.Q4_K, 40, 4, 2, 64, 256, False),   # M > 4E: MFMA, gated epilogue
+                                                 (hipq.Q4_K, 60, 4, 2, 96, 512, True),    # ragged gate/up tile, rpp
+                                                 (hipq.Q4_K, 256, 32, 8, 768, 2048, False),  # configs[4] T = 256
                                                  (hipq.Q8_0, 4, 8, 2, 48, 256, False),    # generic + split
                                                  (hipq.Q4_K, 2, 4, 2, 32, 5120, False)])  # K > 4096: fallback
 def test_moe_gated_shapes(dev, dt, T, E, topk, I, K, rpp):
