@@ -116,7 +116,7 @@ size_t moe_ws_bytes(int64_t rows, int64_t K, int dt);
 int launch_moe_combine(const float *pair, float *out, int64_t T, int64_t N, int topk, hipStream_t s);
 int launch_moe_q(const float *x, const void *w, const int64_t *pairs, const int64_t *expts, int32_t *counts,
                  int32_t *offsets, const float *topk_w, float *out, int topk, int64_t size_m, int64_t M, int64_t rows,
-                 int64_t E, int64_t N, int64_t K, int rpp, int dt, void *ws, hipStream_t s);
+                 int64_t E, int64_t N, int64_t K, int rpp, int dt, void *ws, hipStream_t s, float *zero_out = nullptr);
 bool moe_x_ok(int64_t K, int dt, const void *w, const void *x);
 int launch_moe_gemv_x(const float *x, const void *w, const int64_t *pairs, const int64_t *expts, int32_t *counts,
                       int32_t *offsets, const float *topk_w, float *out, int topk, int64_t size_m, int64_t M,

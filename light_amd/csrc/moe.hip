@@ -40,16 +40,30 @@ __global__ __launch_bounds__(256) void moe_offsets_kernel(const int64_t *__restr
   if (e < E) counts[e] = (int32_t)(lower(e + 1) - a);
 }
 
+__global__ __launch_bounds__(256) void zero_f32_kernel(float *__restrict__ p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = 0.f;
+}
+
 // The same offsets / counts from one workgroup, for E + 1 offsets that fit in LDS: the sorted
 // ids are read once, coalesced (a binary search per expert is a chain of dependent loads),
 // and each segment start fills the offsets of the experts up to its own:
 // offsets[e] = i for e in (ids[i-1], ids[i]], and M after the last id -- the lower bound of e.
+// With zero_out: the rows r < size_m of zero_out (row_len floats each) that no pair of a valid
+// expert will write -- pairs routed nowhere, indices the pair list skips -- are zeroed here,
+// instead of the whole output before the grouped GEMM.
 __global__ __launch_bounds__(1024) void moe_offsets_wg_kernel(const int64_t *__restrict__ expts, int64_t M, int E,
                                                               int32_t *__restrict__ counts,
-                                                              int32_t *__restrict__ offsets) {
+                                                              int32_t *__restrict__ offsets,
+                                                              const int64_t *__restrict__ pairs,
+                                                              float *__restrict__ zero_out, int64_t size_m,
+                                                              int64_t row_len) {
   extern __shared__ int32_t lo[];
+  uint32_t *seen = reinterpret_cast<uint32_t *>(lo + E + 1);  // size_m bits (zero_out only)
   const int t = threadIdx.x, nt = blockDim.x;
   for (int e = t; e <= E; e += nt) lo[e] = (int32_t)M;  // experts past the last id
+  if (zero_out)
+    for (int64_t w = t; w < (size_m + 31) / 32; w += nt) seen[w] = 0u;
   __syncthreads();
   for (int64_t i = t; i < M; i += nt) {
     const int64_t v = expts[i], p = i > 0 ? expts[i - 1] : -1;
@@ -57,12 +71,41 @@ __global__ __launch_bounds__(1024) void moe_offsets_wg_kernel(const int64_t *__r
       const int64_t e0 = p + 1 > 0 ? p + 1 : 0, e1 = v < E ? v : E;
       for (int64_t e = e0; e <= e1; e++) lo[e] = (int32_t)i;
     }
+    if (zero_out && v >= 0 && v < E) {
+      const int64_t r = pairs[i];
+      if (r >= 0 && r < size_m) atomicOr(&seen[r >> 5], 1u << (r & 31));
+    }
   }
   __syncthreads();
   for (int e = t; e <= E; e += nt) {
     offsets[e] = lo[e];
     if (e < E) counts[e] = lo[e + 1] - lo[e];
   }
+  if (zero_out) {
+    for (int64_t r = t; r < size_m; r += nt) {  // a row to zero is rare: its thread does it alone
+      if (seen[r >> 5] & (1u << (r & 31))) continue;
+      for (int64_t c = 0; c < row_len; c++) zero_out[r * row_len + c] = 0.f;
+    }
+  }
+}
+
+// counts / offsets of the sorted expert ids; with zero_out, the rows no valid pair writes are
+// zeroed (the one-workgroup kernel when E + 1 offsets and size_m row bits fit in LDS, else a
+// whole-output zero first).
+static int moe_offsets(const int64_t *expts, int64_t M, int64_t E, int32_t *counts, int32_t *offsets,
+                       const int64_t *pairs, float *zero_out, int64_t size_m, int64_t row_len, hipStream_t s) {
+  const int64_t lds = 4 * (E + 1) + (zero_out ? 4 * ((size_m + 31) / 32) : 0);
+  if (lds <= 64 * 1024) {
+    moe_offsets_wg_kernel<<<1, 1024, (size_t)lds, s>>>(expts, M, (int)E, counts, offsets, pairs, zero_out, size_m,
+                                                      row_len);
+    return check_launch("moe_offsets");
+  }
+  if (zero_out) {
+    zero_f32_kernel<<<(unsigned)cdiv(size_m * row_len, 256), 256, 0, s>>>(zero_out, size_m * row_len);
+    if (int rc = check_launch("zero")) return rc;
+  }
+  moe_offsets_kernel<<<(unsigned)cdiv(E + 1, 256), 256, 0, s>>>(expts, M, (int)E, counts, offsets);
+  return check_launch("moe_offsets");
 }
 
 template <int DT>
@@ -130,20 +173,22 @@ size_t moe_ws_bytes(int64_t rows, int64_t K, int dt) {
   return dt == Q4_K ? (size_t)std::max<int64_t>(act_bytes(rows, K), al256m(2 * rows * K) + 4 * rows) : 0;
 }
 
+// zero_out (nullable; = out): rows of out that no valid pair writes are zeroed on the way.
 int launch_moe_q(const float *x, const void *w, const int64_t *pairs, const int64_t *expts, int32_t *counts,
                  int32_t *offsets, const float *topk_w, float *out, int topk, int64_t size_m, int64_t M, int64_t rows,
-                 int64_t E, int64_t N, int64_t K, int rpp, int dt, void *ws, hipStream_t s) {
+                 int64_t E, int64_t N, int64_t K, int rpp, int dt, void *ws, hipStream_t s, float *zero_out) {
   if (E > INT32_MAX - 1 || M > INT32_MAX || N > INT32_MAX) return fail(HQ_EUNSUPPORTED, "moe_gemm_q", "too large");
   // Decode: one launch finds the segments, writes counts / offsets, quantizes x and streams.
   // (Q5_K takes it at every M: it has no grouped MFMA kernel.)
-  if (M > 0 && E <= 65535 && (dt == Q5_K || !moe_use_mfma(M, E)) && moe_x_ok(K, dt, w, x))
+  if (M > 0 && E <= 65535 && (dt == Q5_K || !moe_use_mfma(M, E)) && moe_x_ok(K, dt, w, x)) {
+    if (zero_out) {
+      zero_f32_kernel<<<(unsigned)cdiv(size_m * N, 256), 256, 0, s>>>(zero_out, size_m * N);
+      if (int rc = check_launch("zero")) return rc;
+    }
     return launch_moe_gemv_x(x, w, pairs, expts, counts, offsets, topk_w, out, topk, size_m, M, rows, E, N, K, rpp,
                              dt, -1, s);
-  if (E + 1 <= 16384)
-    moe_offsets_wg_kernel<<<1, 1024, (size_t)(E + 1) * 4, s>>>(expts, M, (int)E, counts, offsets);
-  else
-    moe_offsets_kernel<<<(unsigned)cdiv(E + 1, 256), 256, 0, s>>>(expts, M, (int)E, counts, offsets);
-  if (int rc = check_launch("moe_offsets")) return rc;
+  }
+  if (int rc = moe_offsets(expts, M, E, counts, offsets, pairs, zero_out, size_m, N, s)) return rc;
   if (moe_q4k_fast(dt, K, w)) {
     if (moe_use_mfma(M, E)) {
       auto *xh = static_cast<uint16_t *>(ws);
@@ -182,10 +227,6 @@ __global__ __launch_bounds__(256) void moe_gated_split_kernel(const float *__res
   out[i] = gate_act(gu[r * 2 * I + n], act) * gu[r * 2 * I + I + n];
 }
 
-__global__ __launch_bounds__(256) void zero_f32_kernel(float *__restrict__ p, int64_t n) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i < n) p[i] = 0.f;
-}
 
 static int64_t al256m(int64_t b) { return (b + 255) & ~(int64_t)255; }
 
@@ -205,13 +246,7 @@ int launch_moe_q_gated(const float *x, const void *w, const int64_t *pairs, cons
     // The grouped GEMM with the gated epilogue: h straight from the gate / up tiles.  Rows of
     // pairs outside every expert segment stay zero, as after the split of a zeroed output.
     void *inner = static_cast<char *>(ws) + al256m(4 * size_m * 2 * I);
-    zero_f32_kernel<<<(unsigned)cdiv(size_m * I, 256), 256, 0, s>>>(out, size_m * I);
-    if (int rc = check_launch("zero")) return rc;
-    if (E + 1 <= 16384)
-      moe_offsets_wg_kernel<<<1, 1024, (size_t)(E + 1) * 4, s>>>(expts, M, (int)E, counts, offsets);
-    else
-      moe_offsets_kernel<<<(unsigned)cdiv(E + 1, 256), 256, 0, s>>>(expts, M, (int)E, counts, offsets);
-    if (int rc = check_launch("moe_offsets")) return rc;
+    if (int rc = moe_offsets(expts, M, E, counts, offsets, pairs, out, size_m, I, s)) return rc;
     auto *xh = static_cast<uint16_t *>(inner);
     auto *xs = reinterpret_cast<float *>(static_cast<char *>(inner) + al256m(2 * rows * K));
     return launch_moe_gemm_q4k(x, xh, xs, w, pairs, offsets, nullptr, out, topk, size_m, rows, E, 2 * I, K, rpp, s, I,
@@ -255,9 +290,10 @@ int launch_moe_q_combine(const float *h, const void *w, const int64_t *pairs, co
     counts = co;
     offsets = co + E;
   }
-  zero_f32_kernel<<<(unsigned)cdiv(M * N, 256), 256, 0, s>>>(po, M * N);
-  if (int rc = check_launch("zero")) return rc;
-  if (int rc = launch_moe_q(h, w, pairs, expts, counts, offsets, topk_w, po, topk, M, M, M, E, N, K, 1, dt, inner, s))
+  // The rows no valid pair writes are zeroed by launch_moe_q (zero_out = po), as Light's
+  // zeroed pair output would hold them.
+  if (int rc = launch_moe_q(h, w, pairs, expts, counts, offsets, topk_w, po, topk, M, M, M, E, N, K, 1, dt, inner, s,
+                            po))
     return rc;
   return launch_moe_combine(po, y, T, N, topk, s);
 }

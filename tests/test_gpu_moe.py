@@ -391,3 +391,37 @@ def test_moe_block_second_stream_and_changing_routes(dev):
         torch.cuda.synchronize()
         assert torch.equal(got, want), i
         assert torch.equal(got2, want), i
+
+
+def test_moe_grouped_gemm_pairs_routed_nowhere(dev):
+    """Pairs whose expert id is outside [0, E) contribute zero rows, in the grouped MFMA paths
+    that zero only the rows no valid pair writes: the gated gate/up (h rows of such pairs are
+    0 even in a NaN-filled output) and the down + combine (equal bit for bit to moe_gemm_q into
+    a zeroed output followed by moe_combine, with a NaN-filled workspace)."""
+    print("[case] moe grouped GEMM, pairs routed nowhere", flush=True)
+    g = synth.rng(2024)
+    T, E, topk, H, I = 48, 4, 2, 512, 256  # M = 96 > 4 E: the grouped MFMA GEMM
+    ids, tw = synth.moe_routing(T, E, topk, g)
+    ids = ids.copy()
+    bad = [3, 17, 50, 95]
+    ids.reshape(-1)[bad] = [E, -1, E + 5, E]
+    se, sp = synth.sort_pairs(ids)
+    wgu = _t(synth.gguf_weight(hipq.Q4_K, E * 2 * I, H, g), dev)
+    wdn = _t(synth.gguf_weight(hipq.Q4_K, E * H, I, g), dev)
+    x = _t(synth.activations(T, H, g), dev)
+    spt, set_, twt = _t(sp, dev), _t(se, dev), _t(tw, dev)
+    hz = hipq.moe_gemm_q_gated(x, wgu, spt, set_, E, I, H, hipq.Q4_K, topk,
+                               out=torch.zeros((T * topk, I), device=dev))
+    hn = hipq.moe_gemm_q_gated(x, wgu, spt, set_, E, I, H, hipq.Q4_K, topk,
+                               out=torch.full((T * topk, I), float("nan"), device=dev))
+    torch.cuda.synchronize()
+    assert torch.equal(hz, hn)
+    assert torch.all(hn[bad] == 0)
+    h = _t(synth.activations(T * topk, I, g), dev)
+    want = hipq.moe_combine(hipq.moe_gemm_q(h, wdn, spt, set_, E, H, I, hipq.Q4_K, topk, topk_w=twt,
+                                            out=torch.zeros((T * topk, H), device=dev)), topk)
+    nb = hipq.lib().hq_moe_gemm_q_combine_ws_bytes(T, topk, E, H, I, hipq.Q4_K)
+    ws = torch.full((nb // 4 + 1,), float("nan"), device=dev)
+    got = hipq.moe_gemm_q_combine(h, wdn, spt, set_, E, H, I, hipq.Q4_K, topk, topk_w=twt, ws=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
