@@ -410,17 +410,48 @@ __global__ __launch_bounds__(256) void to_f16_rowscale_kernel(const float *__res
   __shared__ float red[4];
   const int64_t r = blockIdx.x;
   const float *xr = x + r * K;
+  const int t = threadIdx.x;
+  // K <= 4096 (K % 256 == 0): the row stays in registers, four floats per load, so it is read
+  // once; longer rows are read twice.
+  constexpr int KV = 4;
+  const int64_t n4 = K / 4;
+  const bool reg = n4 <= KV * 256;
+  float4 v[KV];
   float m = 0.f;
-  for (int64_t k = threadIdx.x; k < K; k += 256) m = fmaxf(m, fabsf(xr[k]));
+  if (reg) {
+#pragma unroll
+    for (int j = 0; j < KV; j++) {
+      const int64_t i = t + 256 * j;
+      v[j] = i < n4 ? reinterpret_cast<const float4 *>(xr)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int j = 0; j < KV; j++)
+      m = fmaxf(m, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
+  } else {
+    for (int64_t k = t; k < K; k += 256) m = fmaxf(m, fabsf(xr[k]));
+  }
   for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  if ((t & 63) == 0) red[t >> 6] = m;
   __syncthreads();
   m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   int ex = 0;
   (void)frexpf(m, &ex);  // m < 2^ex
   const int e = ex > 15 && m == m && m < INFINITY ? ex - 15 : 0;
-  for (int64_t k = threadIdx.x; k < K; k += 256) y[r * K + k] = (_Float16)ldexpf(xr[k], -e);
-  if (threadIdx.x == 0) xscale[r] = ldexpf(1.f, e);
+  if (reg) {
+#pragma unroll
+    for (int j = 0; j < KV; j++) {
+      const int64_t i = t + 256 * j;
+      if (i < n4) {
+        typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+        const f16x4 h = {(_Float16)ldexpf(v[j].x, -e), (_Float16)ldexpf(v[j].y, -e), (_Float16)ldexpf(v[j].z, -e),
+                         (_Float16)ldexpf(v[j].w, -e)};
+        reinterpret_cast<f16x4 *>(y + r * K)[i] = h;
+      }
+    }
+  } else {
+    for (int64_t k = t; k < K; k += 256) y[r * K + k] = (_Float16)ldexpf(xr[k], -e);
+  }
+  if (t == 0) xscale[r] = ldexpf(1.f, e);
 }
 
 // The ring's loads are issued from inline asm and awaited with explicit counts: with plain
