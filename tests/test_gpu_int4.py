@@ -177,3 +177,27 @@ def test_moe_int4_vs_light_cpu(dev, T, E, topk, H, I, G, xdt):
         gg, uu = wg[:I] @ xw[0].astype(np.float64), wg[I:] @ xw[0].astype(np.float64)
         ref += float(w[j]) * (wd @ (gg / (1 + np.exp(-gg)) * uu))
     assert np.max(np.abs(got[0] - ref)) <= tol * (np.abs(ref).max() + 1e-30)
+
+
+@pytest.mark.parametrize("M,N,K,G", [(33, 1000, 1024, 128), (64, 18944, 3584, 128), (17, 300, 2048, 256)])
+def test_matmul_int4_f16_split_k_streams_and_repeats(dev, M, N, K, G):
+    """F16 x, 8 < M <= 64, split over K: matches the f64 reference, and repeated calls -- on the
+    default stream and on twenty other streams (each with its own library workspace) -- give
+    the same bits."""
+    rng = np.random.default_rng(M + N + K)
+    codes, s, z = light_int4(rng, N, K, G)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    _check(dev, x, codes, s, z, G, hipq.F16)
+    xt = torch.from_numpy(x).to(torch.float16).to(dev)
+    ct, st, zt = _t(codes, dev), _t(s, dev), _t(z, dev)
+    first = hipq.int4_matmul(xt, ct, st, zt, G)
+    again = [hipq.int4_matmul(xt, ct, st, zt, G) for _ in range(3)]
+    other = torch.cuda.Stream(device=dev)
+    outs = []
+    for i in range(20):
+        st2 = torch.cuda.Stream(device=dev) if i else other
+        with torch.cuda.stream(st2):
+            outs.append(hipq.int4_matmul(xt, ct, st, zt, G, stream=st2))
+    torch.cuda.synchronize()
+    for y in again + outs:
+        assert torch.equal(y, first)
