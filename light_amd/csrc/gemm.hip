@@ -385,9 +385,10 @@ __global__ __launch_bounds__(256) void gemm_small_int4_kernel(SmallI4Args a) {
 // d*sc and -dmin*m (one rounding), about 2 VALU instructions per weight.  x is converted to
 // f16 once per row with a power-of-two row scale (rows of |x| above 2^15 are scaled down, the
 // output row scaled back up exactly), so the f16 range never clips.
-// The raw loads of step s + MD go out while step s computes (a register ring).
+// The raw loads of step s + MD go out while step s computes (a register ring of one 256-k
+// block: the block header is loaded with its first step only).
 
-constexpr int MD = 3;
+constexpr int MD = 4;  // ring slots: one super-block of 256 k, so slot 0 starts each block
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2v __attribute__((ext_vector_type(2)));
 
@@ -469,20 +470,26 @@ template <int N>
 __device__ __forceinline__ void wait_ring(u32x4 &a, u32x4 &b, u32x4 &c) {
   asm volatile("s_waitcnt vmcnt(%3)" : "+v"(a), "+v"(b), "+v"(c) : "n"(N) : "memory");
 }
+template <int N>
+__device__ __forceinline__ void wait_ring(u32x4 &a, u32x4 &b) {
+  asm volatile("s_waitcnt vmcnt(%2)" : "+v"(a), "+v"(b) : "n"(N) : "memory");
+}
 #pragma clang diagnostic pop
 
 // Raw Q4_K bytes of one thread's B slot for one 64-k step: (row, half): quant bytes
 // 16 * half .. + 16 of the step's pair (low nibbles: sub-block 2p, k = 16 half + i; high:
-// sub-block 2p + 1, k = 32 + 16 half + i) and the block header.
+// sub-block 2p + 1, k = 32 + 16 half + i); the block header h (d, dmin, scales) is loaded
+// with the block's first step only and kept for the other three.
 struct Q4kF16Slot {
-  u32x4 q, h;
-  __device__ __forceinline__ void load(const GemmArgs &a, int row, int half, int k0) {
-    const uint8_t *bp = a.w + (int64_t)row * (a.K / 256) * 144 + (int64_t)(k0 >> 8) * 144;
-    const int p = (k0 >> 6) & 3;
-    q = ldg16(bp + 16 + 32 * p + 16 * half);
-    h = ldg16(bp);
+  u32x4 q;
+  __device__ __forceinline__ static const uint8_t *block(const GemmArgs &a, int row, int k0) {
+    return a.w + (int64_t)row * (a.K / 256) * 144 + (int64_t)(k0 >> 8) * 144;
   }
-  __device__ __forceinline__ void store(uint8_t *brow, int half, int k0) const {
+  __device__ __forceinline__ void load(const GemmArgs &a, int row, int half, int k0) {
+    const int p = (k0 >> 6) & 3;
+    q = ldg16(block(a, row, k0) + 16 + 32 * p + 16 * half);
+  }
+  __device__ __forceinline__ void store(uint8_t *brow, int half, int k0, const u32x4 &h) const {
     const int p = (k0 >> 6) & 3;
     const float d = h2f(h.x & 0xffffu), dmin = h2f(h.x >> 16);
     int scA, mnA, scB, mnB;
@@ -526,6 +533,12 @@ struct Q4kF16Slot {
 // so waves 0-1 hold g and waves 2-3 u of the same 64 output columns; after the K loop waves 2-3
 // pass u through LDS and waves 0-1 write act(g) * u (the values the ungated kernel followed by
 // the split would give, bit for bit).
+// f(integral_constant<int, I>) for I = 0, 1, ... while it returns true.
+template <class F, int... I>
+__device__ __forceinline__ void unroll_steps(F &&f, std::integer_sequence<int, I...>) {
+  (void)(... && f(std::integral_constant<int, I>{}));
+}
+
 template <bool GATED>
 __global__ __launch_bounds__(256) void moe_gemm_kernel(MoeGemmArgs ma) {
   using T = GTile<32>;
@@ -561,33 +574,43 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(MoeGemmArgs ma) {
     for (int r = 0; r < 16; r++) acc[r] = 0.f;
     // Ring slot i holds the raw loads of a step congruent to i mod MD; loads past the last step
     // are clamped to it (unconditional, so the compiler's per-register waits stay exact).
-    u32x4 ra[MD];
+    u32x4 ra[MD], hd, hcur;  // hd: slot 0's block header; hcur: the header being staged
     Q4kF16Slot wp[MD];
-    // Three loads per step and thread (x, the quant bytes, the header), in this order.
-    auto load = [&](int st, u32x4 &r, Q4kF16Slot &w) __attribute__((always_inline)) {
+    // Loads per step and thread: x and the quant bytes, plus the block header in slot 0 (whose
+    // steps start the 256-k blocks: K % 256 == 0), in this order.
+    auto load = [&](int st, u32x4 &r, Q4kF16Slot &w, auto SLOT) __attribute__((always_inline)) {
       const int k = (st < ksteps ? st : ksteps - 1) * GBK;
       r = ldg16(xrow + k);
       w.load(a, wrow, wh, k);
+      if constexpr (decltype(SLOT)::value == 0) hd = ldg16(Q4kF16Slot::block(a, wrow, k));
     };
-    auto stage_in = [&](int buf, int st, const u32x4 &r, const Q4kF16Slot &w) __attribute__((always_inline)) {
+    auto stage_in = [&](int buf, int st, const u32x4 &r, const Q4kF16Slot &w, auto SLOT) __attribute__((always_inline)) {
+      if constexpr (decltype(SLOT)::value == 0) hcur = hd;
       uint8_t *na = smem + buf * T::STAGE;
       *reinterpret_cast<u32x4 *>(na + (arow * GLD + acol * 8) * 2) = r;
-      w.store(na + T::A_BYTES + wr * GLD * 2, wh, (st < ksteps ? st : ksteps - 1) * GBK);
+      w.store(na + T::A_BYTES + wr * GLD * 2, wh, (st < ksteps ? st : ksteps - 1) * GBK, hcur);
     };
-#pragma unroll
-    for (int d = 0; d < MD; d++) load(d, ra[d], wp[d]);
-    // Loads issued after a slot's three when it is staged: the other MD - 1 slots' (one step
-    // each), at the prologue and in every step alike.
-    constexpr int NAFTER = 3 * (MD - 1);
-    wait_ring<NAFTER>(ra[0], wp[0].q, wp[0].h);
-    stage_in(0, 0, ra[0], wp[0]);
+    // The ring holds one step per slot, so when slot n is awaited the loads issued after its
+    // own are one step of every other slot: 2 MD + 1 in all, less slot n's.
+    auto wait_slot = [&](auto SLOT) __attribute__((always_inline)) {
+      constexpr int n = decltype(SLOT)::value;
+      if constexpr (n == 0)
+        wait_ring<2 * MD + 1 - 3>(ra[0], wp[0].q, hd);
+      else
+        wait_ring<2 * MD + 1 - 2>(ra[n], wp[n].q);
+    };
+    unroll_steps([&](auto I) { return load(decltype(I)::value, ra[decltype(I)::value], wp[decltype(I)::value], I), true; },
+                 std::make_integer_sequence<int, MD>{});
+    wait_slot(std::integral_constant<int, 0>{});
+    stage_in(0, 0, ra[0], wp[0], std::integral_constant<int, 0>{});
     __syncthreads();
     // Step s (ring slot s % MD, a compile-time constant): refill the slot with step s + MD,
     // multiply step s from LDS, stage step s + 1 (slot (s + 1) % MD) into the other buffer.
+    // Slot 0 is refilled after step s + 1 .. s + 3 no longer need its header: hcur holds it.
     auto step = [&](int s, auto SLOT) __attribute__((always_inline)) {
       constexpr int slot = decltype(SLOT)::value, nslot = (slot + 1) % MD;
-      load(s + MD, ra[slot], wp[slot]);
-      wait_ring<NAFTER>(ra[nslot], wp[nslot].q, wp[nslot].h);
+      load(s + MD, ra[slot], wp[slot], SLOT);
+      wait_slot(std::integral_constant<int, nslot>{});
       const uint8_t *sa = smem + (s & 1) * T::STAGE;
       const uint8_t *sb = sa + T::A_BYTES;
 #pragma unroll
@@ -596,17 +619,16 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(MoeGemmArgs ma) {
         const f16x8 bfr = *reinterpret_cast<const f16x8 *>(sb + ((wn * 32 + fr) * GLD + kk * 16 + fk) * 2);
         acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bfr, acc, 0, 0, 0);
       }
-      if (s + 1 < ksteps) stage_in((s + 1) & 1, s + 1, ra[nslot], wp[nslot]);
+      if (s + 1 < ksteps) stage_in((s + 1) & 1, s + 1, ra[nslot], wp[nslot], std::integral_constant<int, nslot>{});
       __syncthreads();
     };
-    for (int s = 0; s < ksteps; s += MD) {
-      step(s, std::integral_constant<int, 0>{});
-      if (s + 1 < ksteps) step(s + 1, std::integral_constant<int, 1>{});
-      if (s + 2 < ksteps) step(s + 2, std::integral_constant<int, 2>{});
-    }
+    for (int s = 0; s < ksteps; s += MD)
+      unroll_steps([&](auto I) { return s + decltype(I)::value < ksteps ? (step(s + decltype(I)::value, I), true) : false; },
+                   std::make_integer_sequence<int, MD>{});
     // The ring's last (clamped) loads land before its registers can be reused.
+    wait_ring<0>(ra[0], wp[0].q, hd);
 #pragma unroll
-    for (int d = 0; d < MD; d++) wait_ring<0>(ra[d], wp[d].q, wp[d].h);
+    for (int d = 1; d < MD; d++) wait_ring<0>(ra[d], wp[d].q);
     if constexpr (GATED) {
       // The stage buffers are free (the last step ended with a barrier): waves 2-3 leave u.
       float *ux = reinterpret_cast<float *>(smem);
