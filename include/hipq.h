@@ -335,7 +335,7 @@ size_t hq_moe_gemm_q_gated_ws_bytes(int64_t size_m, int64_t rows, int64_t I, int
  * out (size_m, I) F32 gets h[p] = act(x_row(p) . Wg[e(p)]) * (x_row(p) . Wu[e(p)]) -- the
  * MoEGemmQ, Narrow, SiLU / GeluErf and Mul of that function in one op (one kernel for
  * Q4_K / Q5_K decode).  Routing arguments as hq_moe_gemm_q; act HQ_ACT_SILU or
- * HQ_ACT_GELU_ERF.  No counterpart kernel in Light: the fusion of (f) row 4. */
+ * HQ_ACT_GELU_ERF.  No counterpart kernel in Light: these launches fused. */
 int hq_moe_gemm_q_gated(const float *x, const void *w, const int64_t *sorted_pairs, const int64_t *sorted_expts,
                         int32_t *counts, int32_t *offsets, float *out, int topk, int64_t size_m, int64_t M,
                         int64_t rows, int64_t E, int64_t I, int64_t K, int row_per_pair, int w_dtype, int act,
@@ -363,7 +363,7 @@ int hq_moe_route_gated(const float *probs, const float *x, const void *w, float 
  * one kernel runs the whole block, with a grid barrier between the gate/up and the down
  * projection; that kernel serves the first stream that calls this function on a device
  * (other streams get the two launches), and graph replays of it must not run beside one
- * another.  No counterpart kernel in Light: the fusion of (f) row 4. */
+ * another.  No counterpart kernel in Light: these launches fused. */
 size_t hq_moe_block_q_ws_bytes(int64_t T, int topk, int64_t E, int64_t H, int64_t I, int w_dtype);
 int hq_moe_block_q(const float *probs, const float *x, const void *w_gate_up, const void *w_down, float *h, float *y,
                    int64_t T, int64_t E, int topk, int normalize, int64_t H, int64_t I, int w_dtype, int act,

@@ -116,7 +116,8 @@ size_t moe_ws_bytes(int64_t rows, int64_t K, int dt);
 int launch_moe_combine(const float *pair, float *out, int64_t T, int64_t N, int topk, hipStream_t s);
 int launch_moe_q(const float *x, const void *w, const int64_t *pairs, const int64_t *expts, int32_t *counts,
                  int32_t *offsets, const float *topk_w, float *out, int topk, int64_t size_m, int64_t M, int64_t rows,
-                 int64_t E, int64_t N, int64_t K, int rpp, int dt, void *ws, hipStream_t s, float *zero_out = nullptr);
+                 int64_t E, int64_t N, int64_t K, int rpp, int dt, void *ws, hipStream_t s, float *zero_out = nullptr,
+                 bool routed = false);
 bool moe_x_ok(int64_t K, int dt, const void *w, const void *x);
 int launch_moe_gemv_x(const float *x, const void *w, const int64_t *pairs, const int64_t *expts, int32_t *counts,
                       int32_t *offsets, const float *topk_w, float *out, int topk, int64_t size_m, int64_t M,
@@ -130,11 +131,11 @@ int launch_moe_sort_ids(const int64_t *ids, int64_t M, int64_t E, int64_t *sorte
                         int32_t *counts, int32_t *offsets, hipStream_t s);
 int launch_moe_q_gated(const float *x, const void *w, const int64_t *pairs, const int64_t *expts, int32_t *counts,
                        int32_t *offsets, float *out, int topk, int64_t size_m, int64_t M, int64_t rows, int64_t E,
-                       int64_t I, int64_t K, int rpp, int dt, int act, void *ws, hipStream_t s);
+                       int64_t I, int64_t K, int rpp, int dt, int act, void *ws, hipStream_t s, bool routed = false);
 size_t moe_combine_ws_bytes(int64_t M, int64_t E, int64_t N, int64_t K, int dt);
 int launch_moe_q_combine(const float *h, const void *w, const int64_t *pairs, const int64_t *expts, int32_t *counts,
                          int32_t *offsets, const float *topk_w, float *y, int topk, int64_t T, int64_t E, int64_t N,
-                         int64_t K, int dt, void *ws, hipStream_t s);
+                         int64_t K, int dt, void *ws, hipStream_t s, bool routed = false);
 size_t moe_route_gated_ws_bytes(int64_t T, int topk, int64_t E, int64_t I, int64_t K, int dt);
 int launch_moe_route_gated_any(const float *probs, const float *x, const void *w, float *h, int64_t T, int64_t E,
                                int topk, int normalize, int64_t I, int64_t K, int dt, int act, int64_t *topk_ids,

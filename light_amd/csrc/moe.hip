@@ -174,21 +174,27 @@ size_t moe_ws_bytes(int64_t rows, int64_t K, int dt) {
 }
 
 // zero_out (nullable; = out): rows of out that no valid pair writes are zeroed on the way.
+// routed: pairs / expts / counts / offsets come from MoERoute over exactly the pairs [0, M)
+// with size_m == M (every pair in one valid expert segment, counts / offsets already written),
+// so the grouped GEMM writes every row: no offsets pass, nothing to zero.
 int launch_moe_q(const float *x, const void *w, const int64_t *pairs, const int64_t *expts, int32_t *counts,
                  int32_t *offsets, const float *topk_w, float *out, int topk, int64_t size_m, int64_t M, int64_t rows,
-                 int64_t E, int64_t N, int64_t K, int rpp, int dt, void *ws, hipStream_t s, float *zero_out) {
+                 int64_t E, int64_t N, int64_t K, int rpp, int dt, void *ws, hipStream_t s, float *zero_out,
+                 bool routed) {
+  if (routed && size_m != M) return fail(HQ_EINVAL, "moe_gemm_q", "routed pairs need size_m == M");
   if (E > INT32_MAX - 1 || M > INT32_MAX || N > INT32_MAX) return fail(HQ_EUNSUPPORTED, "moe_gemm_q", "too large");
   // Decode: one launch finds the segments, writes counts / offsets, quantizes x and streams.
   // (Q5_K takes it at every M: it has no grouped MFMA kernel.)
   if (M > 0 && E <= 65535 && (dt == Q5_K || !moe_use_mfma(M, E)) && moe_x_ok(K, dt, w, x)) {
-    if (zero_out) {
+    if (zero_out && !routed) {
       zero_f32_kernel<<<(unsigned)cdiv(size_m * N, 256), 256, 0, s>>>(zero_out, size_m * N);
       if (int rc = check_launch("zero")) return rc;
     }
     return launch_moe_gemv_x(x, w, pairs, expts, counts, offsets, topk_w, out, topk, size_m, M, rows, E, N, K, rpp,
                              dt, -1, s);
   }
-  if (int rc = moe_offsets(expts, M, E, counts, offsets, pairs, zero_out, size_m, N, s)) return rc;
+  if (!routed)
+    if (int rc = moe_offsets(expts, M, E, counts, offsets, pairs, zero_out, size_m, N, s)) return rc;
   if (moe_q4k_fast(dt, K, w)) {
     if (moe_use_mfma(M, E)) {
       auto *xh = static_cast<uint16_t *>(ws);
@@ -236,9 +242,10 @@ size_t moe_gated_ws_bytes(int64_t size_m, int64_t rows, int64_t I, int64_t K, in
 
 int launch_moe_q_gated(const float *x, const void *w, const int64_t *pairs, const int64_t *expts, int32_t *counts,
                        int32_t *offsets, float *out, int topk, int64_t size_m, int64_t M, int64_t rows, int64_t E,
-                       int64_t I, int64_t K, int rpp, int dt, int act, void *ws, hipStream_t s) {
+                       int64_t I, int64_t K, int rpp, int dt, int act, void *ws, hipStream_t s, bool routed) {
   if (E > INT32_MAX - 1 || M > INT32_MAX || 2 * I > INT32_MAX)
     return fail(HQ_EUNSUPPORTED, "moe_gemm_q_gated", "too large");
+  if (routed && size_m != M) return fail(HQ_EINVAL, "moe_gemm_q_gated", "routed pairs need size_m == M");
   if (M > 0 && E <= 65535 && (dt == Q5_K || !moe_use_mfma(M, E)) && moe_x_ok(K, dt, w, x))
     return launch_moe_gemv_x(x, w, pairs, expts, counts, offsets, nullptr, out, topk, size_m, M, rows, E, I, K, rpp,
                              dt, act, s);
@@ -246,7 +253,8 @@ int launch_moe_q_gated(const float *x, const void *w, const int64_t *pairs, cons
     // The grouped GEMM with the gated epilogue: h straight from the gate / up tiles.  Rows of
     // pairs outside every expert segment stay zero, as after the split of a zeroed output.
     void *inner = static_cast<char *>(ws) + al256m(4 * size_m * 2 * I);
-    if (int rc = moe_offsets(expts, M, E, counts, offsets, pairs, out, size_m, I, s)) return rc;
+    if (!routed)
+      if (int rc = moe_offsets(expts, M, E, counts, offsets, pairs, out, size_m, I, s)) return rc;
     auto *xh = static_cast<uint16_t *>(inner);
     auto *xs = reinterpret_cast<float *>(static_cast<char *>(inner) + al256m(2 * rows * K));
     return launch_moe_gemm_q4k(x, xh, xs, w, pairs, offsets, nullptr, out, topk, size_m, rows, E, 2 * I, K, rpp, s, I,
@@ -275,7 +283,7 @@ size_t moe_combine_ws_bytes(int64_t M, int64_t E, int64_t N, int64_t K, int dt) 
 // zeroed workspace and moe_combine follows.
 int launch_moe_q_combine(const float *h, const void *w, const int64_t *pairs, const int64_t *expts, int32_t *counts,
                          int32_t *offsets, const float *topk_w, float *y, int topk, int64_t T, int64_t E, int64_t N,
-                         int64_t K, int dt, void *ws, hipStream_t s) {
+                         int64_t K, int dt, void *ws, hipStream_t s, bool routed) {
   const int64_t M = T * topk;
   if (E > INT32_MAX - 1 || M > INT32_MAX || N > INT32_MAX)
     return fail(HQ_EUNSUPPORTED, "moe_gemm_q_combine", "too large");
@@ -285,7 +293,9 @@ int launch_moe_q_combine(const float *h, const void *w, const int64_t *pairs, co
   float *po = static_cast<float *>(ws);
   auto *co = reinterpret_cast<int32_t *>(static_cast<char *>(ws) + al256m(4 * M * N));
   void *inner = static_cast<char *>(ws) + al256m(4 * M * N) + al256m(4 * (2 * E + 1));
-  // moe_gemm_q writes counts / offsets; without caller buffers they go to the workspace.
+  // moe_gemm_q writes counts / offsets; without caller buffers they go to the workspace (and
+  // are not the route's: the offsets pass runs).
+  const bool caller_counts = counts && offsets;
   if (!counts || !offsets) {
     counts = co;
     offsets = co + E;
@@ -293,7 +303,7 @@ int launch_moe_q_combine(const float *h, const void *w, const int64_t *pairs, co
   // The rows no valid pair writes are zeroed by launch_moe_q (zero_out = po), as Light's
   // zeroed pair output would hold them.
   if (int rc = launch_moe_q(h, w, pairs, expts, counts, offsets, topk_w, po, topk, M, M, M, E, N, K, 1, dt, inner, s,
-                            po))
+                            po, routed && caller_counts))
     return rc;
   return launch_moe_combine(po, y, T, N, topk, s);
 }
@@ -323,11 +333,14 @@ int launch_moe_route_gated_any(const float *probs, const float *x, const void *w
     return rc;
   const int64_t M = T * topk;
   return launch_moe_q_gated(x, w, sorted_pairs, sorted_expts, counts, offsets, h, topk, M, M, T, E, I, K, 0, dt, act,
-                            inner, s);
+                            inner, s, /*routed=*/true);
 }
 
+// The two halves share the workspace (they do not overlap in time), followed by the counts /
+// offsets of the routing when the caller passes none: written by the route, read by both.
 size_t moe_block_ws_bytes(int64_t T, int topk, int64_t E, int64_t H, int64_t I, int dt) {
-  return std::max(moe_route_gated_ws_bytes(T, topk, E, I, H, dt), moe_combine_ws_bytes(T * topk, E, H, I, dt));
+  return std::max(moe_route_gated_ws_bytes(T, topk, E, I, H, dt), moe_combine_ws_bytes(T * topk, E, H, I, dt)) +
+         (size_t)al256m(4 * (2 * E + 1));
 }
 
 // The SparseMoE decode block: MoERoute, the routed gated gate/up into h, then the down
@@ -341,11 +354,18 @@ int launch_moe_block_any(const float *probs, const float *x, const void *wgu, co
   const int rc = launch_moe_block(probs, x, wgu, wdn, h, y, T, E, topk, normalize, H, I, dt, act, topk_ids, weights,
                                   sorted_pairs, sorted_expts, counts, offsets, s);
   if (rc != 1) return rc;
+  if (!counts || !offsets) {
+    const size_t tail = std::max(moe_route_gated_ws_bytes(T, topk, E, I, H, dt), moe_combine_ws_bytes(T * topk, E, H, I, dt));
+    counts = reinterpret_cast<int32_t *>(static_cast<char *>(ws) + tail);
+    offsets = counts + E;
+  }
   if (int r = launch_moe_route_gated_any(probs, x, wgu, h, T, E, topk, normalize, I, H, dt, act, topk_ids, weights,
                                          sorted_pairs, sorted_expts, counts, offsets, ws, s))
     return r;
+  // The route wrote counts / offsets for exactly the pairs [0, T topk): the down projection
+  // needs no offsets pass and no zeroing.
   return launch_moe_q_combine(h, wdn, sorted_pairs, sorted_expts, counts, offsets, weights, y, topk, T, E, H, I, dt,
-                              ws, s);
+                              ws, s, /*routed=*/true);
 }
 
 }  // namespace hq

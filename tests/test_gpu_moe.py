@@ -371,6 +371,42 @@ def test_moe_block_equals_route_gated_then_combine(dev, dt, T, E, topk, H, I):
             assert torch.equal(a, b), (name, rep)
 
 
+@pytest.mark.parametrize("caller_counts", [True, False])
+def test_moe_block_grouped_gemm_path_equals_separate_calls(dev, caller_counts):
+    """Past 4 E pairs the block runs the grouped MFMA GEMMs on the route's counts / offsets,
+    with no offsets pass and no zeroing (every pair of the route is in one expert segment).
+    Bit for bit equal to moe_route, moe_gemm_q_gated and moe_gemm_q_combine called separately
+    (each with its own offsets pass), with h and the workspace NaN-filled, with the caller's
+    counts / offsets and with the workspace's."""
+    dt, T, E, topk, H, I = hipq.Q4_K, 80, 128, 8, 2048, 768
+    print(f"[case] moe block grouped path T={T} E={E} caller_counts={caller_counts}", flush=True)
+    g = synth.rng(1790 + int(caller_counts))
+    wgu = _t(synth.gguf_weight(dt, E * 2 * I, H, g), dev)
+    wdn = _t(synth.gguf_weight(dt, E * H, I, g), dev)
+    x = _t(synth.activations(T, H, g), dev)
+    probs = _t(_probs(g, T, E, ties=False), dev)
+    ids, w, sp, se = hipq.moe_route(probs, topk)
+    h = hipq.moe_gemm_q_gated(x, wgu, sp, se, E, I, H, dt, topk)
+    y = hipq.moe_gemm_q_combine(h, wdn, sp, se, E, H, I, dt, topk, topk_w=w)
+    nb = hipq.lib().hq_moe_block_q_ws_bytes(T, topk, E, H, I, dt)
+    ws = torch.full((nb // 4 + 1,), float("nan"), dtype=torch.float32, device=dev)
+    for rep in range(2):
+        h1 = torch.full((T * topk, I), float("nan"), dtype=torch.float32, device=dev)
+        c1 = torch.full((E,), -5, dtype=torch.int32, device=dev) if caller_counts else None
+        o1 = torch.full((E + 1,), -5, dtype=torch.int32, device=dev) if caller_counts else None
+        y1, ids1, w1, sp1, se1, h1 = hipq.moe_block_q(probs, x, wgu, wdn, E, H, I, dt, topk, h=h1, counts=c1,
+                                                      offsets=o1, ws=ws)
+        torch.cuda.synchronize()
+        for a, b, name in ((y, y1, "y"), (h, h1, "h"), (ids, ids1, "ids"), (w, w1, "weights"),
+                           (sp, sp1, "sorted_pairs"), (se, se1, "sorted_expts")):
+            assert torch.equal(a, b), (name, rep)
+        if caller_counts:
+            cnt = torch.bincount(se, minlength=E).to(torch.int32)
+            assert torch.equal(c1, cnt)
+            assert torch.equal(o1, torch.cat([torch.zeros(1, dtype=torch.int32, device=dev),
+                                              torch.cumsum(cnt, 0).to(torch.int32)]))
+
+
 def test_moe_block_second_stream_and_changing_routes(dev):
     """The one-launch block on its stream and the two-launch path on another stream agree with
     the separate calls, for routings that change from call to call."""
