@@ -59,7 +59,7 @@ def check_block(block, report):
         is_load = is_vm and "_load" in op and "_lds" not in op  # direct-to-LDS: no VGPR result
         returns = is_load or (is_vm and "atomic" in op and " glc" in text)
         dst = list(vgprs(operands[0])) if operands and (returns or not is_vm) else []
-        srcs = [r for t in (operands[1:] if dst else operands) for r in vgprs(t)]
+        srcs = sorted({r for t in (operands[1:] if dst else operands) for r in vgprs(t)})
         for r in srcs:
             if r in pending:
                 report.append((ln, text, "reads v%d before its load has landed" % r))
