@@ -677,10 +677,12 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(MoeGemmArgs ma) {
 int launch_moe_gemm_q4k(const float *x, uint16_t *xh, float *xs, const void *w, const int64_t *pairs,
                         const int32_t *offsets, const float *topk_w, float *out, int topk, int64_t size_m,
                         int64_t rows, int64_t E, int64_t N, int64_t K, int rpp, hipStream_t s, int64_t gated_I,
-                        int act) {
+                        int act, bool x_ready) {
   using T = GTile<32>;
-  to_f16_rowscale_kernel<<<(unsigned)rows, 256, 0, s>>>(x, reinterpret_cast<_Float16 *>(xh), xs, K);
-  if (int rc = check_launch("to_f16_rowscale")) return rc;
+  if (!x_ready) {
+    to_f16_rowscale_kernel<<<(unsigned)rows, 256, 0, s>>>(x, reinterpret_cast<_Float16 *>(xh), xs, K);
+    if (int rc = check_launch("to_f16_rowscale")) return rc;
+  }
   MoeGemmArgs ma = {};
   ma.g.x = xh;
   ma.g.w = static_cast<const uint8_t *>(w);

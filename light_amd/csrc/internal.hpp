@@ -124,14 +124,18 @@ int launch_moe_gemv_x(const float *x, const void *w, const int64_t *pairs, const
                       int64_t rows, int64_t E, int64_t N, int64_t K, int rpp, int dt, int act, hipStream_t s);
 // On-device MoERoute / MoERouteFromIDs sort (moe_route.hip).
 bool moe_route_fits(int64_t M, int64_t E);
+// x_f32 / K / xh / xs (optional): each token's row of x is also converted to f16 with its
+// power-of-two row scale (what the grouped GEMM's to_f16_rowscale_kernel writes, bit for bit).
 int launch_moe_route(const float *probs, int64_t T, int64_t E, int topk, int normalize, int64_t *topk_ids,
                      float *weights, int64_t *sorted_pairs, int64_t *sorted_expts, int32_t *counts, int32_t *offsets,
-                     hipStream_t s);
+                     hipStream_t s, const float *x_f32 = nullptr, int64_t K = 0, uint16_t *xh = nullptr,
+                     float *xs = nullptr);
 int launch_moe_sort_ids(const int64_t *ids, int64_t M, int64_t E, int64_t *sorted_pairs, int64_t *sorted_expts,
                         int32_t *counts, int32_t *offsets, hipStream_t s);
 int launch_moe_q_gated(const float *x, const void *w, const int64_t *pairs, const int64_t *expts, int32_t *counts,
                        int32_t *offsets, float *out, int topk, int64_t size_m, int64_t M, int64_t rows, int64_t E,
-                       int64_t I, int64_t K, int rpp, int dt, int act, void *ws, hipStream_t s, bool routed = false);
+                       int64_t I, int64_t K, int rpp, int dt, int act, void *ws, hipStream_t s, bool routed = false,
+                       bool x_ready = false);
 size_t moe_combine_ws_bytes(int64_t M, int64_t E, int64_t N, int64_t K, int dt);
 int launch_moe_q_combine(const float *h, const void *w, const int64_t *pairs, const int64_t *expts, int32_t *counts,
                          int32_t *offsets, const float *topk_w, float *y, int topk, int64_t T, int64_t E, int64_t N,
@@ -170,9 +174,10 @@ int launch_moe_gemv_q4k(const void *act, const void *w, const int64_t *pairs, co
                         int64_t E, int64_t N, int64_t K, int rpp, hipStream_t s);
 // MoE grouped Q4_K GEMM: x (rows, K) F32 converted into xh (f16, rows * K * 2 bytes) and
 // xs (rows row scales) in the caller's workspace, then the grouped f16 MFMA kernel.
+// x_ready: xh / xs already hold that conversion (written by the routing launch).
 int launch_moe_gemm_q4k(const float *x, uint16_t *xh, float *xs, const void *w, const int64_t *pairs,
                         const int32_t *offsets, const float *topk_w, float *out, int topk, int64_t size_m,
                         int64_t rows, int64_t E, int64_t N, int64_t K, int rpp, hipStream_t s, int64_t gated_I = 0,
-                        int act = 0);
+                        int act = 0, bool x_ready = false);
 
 }  // namespace hq

@@ -242,7 +242,8 @@ size_t moe_gated_ws_bytes(int64_t size_m, int64_t rows, int64_t I, int64_t K, in
 
 int launch_moe_q_gated(const float *x, const void *w, const int64_t *pairs, const int64_t *expts, int32_t *counts,
                        int32_t *offsets, float *out, int topk, int64_t size_m, int64_t M, int64_t rows, int64_t E,
-                       int64_t I, int64_t K, int rpp, int dt, int act, void *ws, hipStream_t s, bool routed) {
+                       int64_t I, int64_t K, int rpp, int dt, int act, void *ws, hipStream_t s, bool routed,
+                       bool x_ready) {
   if (E > INT32_MAX - 1 || M > INT32_MAX || 2 * I > INT32_MAX)
     return fail(HQ_EUNSUPPORTED, "moe_gemm_q_gated", "too large");
   if (routed && size_m != M) return fail(HQ_EINVAL, "moe_gemm_q_gated", "routed pairs need size_m == M");
@@ -258,7 +259,7 @@ int launch_moe_q_gated(const float *x, const void *w, const int64_t *pairs, cons
     auto *xh = static_cast<uint16_t *>(inner);
     auto *xs = reinterpret_cast<float *>(static_cast<char *>(inner) + al256m(2 * rows * K));
     return launch_moe_gemm_q4k(x, xh, xs, w, pairs, offsets, nullptr, out, topk, size_m, rows, E, 2 * I, K, rpp, s, I,
-                               act);
+                               act, x_ready);
   }
   float *gu = static_cast<float *>(ws);
   void *inner = static_cast<char *>(ws) + al256m(4 * size_m * 2 * I);
@@ -328,12 +329,18 @@ int launch_moe_route_gated_any(const float *probs, const float *x, const void *w
     counts = co;
     offsets = co + E;
   }
-  if (int rc = launch_moe_route(probs, T, E, topk, normalize, topk_ids, weights, sorted_pairs, sorted_expts, counts,
-                                offsets, s))
-    return rc;
   const int64_t M = T * topk;
+  // The grouped-GEMM path converts x to f16 rows first: the routing launch does that on the
+  // way (one wave per token), into the places launch_moe_q_gated's grouped GEMM reads.
+  const bool fuse_x = moe_q4k_fast(dt, K, w) && moe_use_mfma(M, E) && ((uintptr_t)x & 15) == 0;
+  char *gemm_ws = static_cast<char *>(inner) + al256m(4 * M * 2 * I);
+  auto *xh = reinterpret_cast<uint16_t *>(gemm_ws);
+  auto *xs = reinterpret_cast<float *>(gemm_ws + al256m(2 * T * K));
+  if (int rc = launch_moe_route(probs, T, E, topk, normalize, topk_ids, weights, sorted_pairs, sorted_expts, counts,
+                                offsets, s, fuse_x ? x : nullptr, K, xh, xs))
+    return rc;
   return launch_moe_q_gated(x, w, sorted_pairs, sorted_expts, counts, offsets, h, topk, M, M, T, E, I, K, 0, dt, act,
-                            inner, s, /*routed=*/true);
+                            inner, s, /*routed=*/true, fuse_x);
 }
 
 // The two halves share the workspace (they do not overlap in time), followed by the counts /

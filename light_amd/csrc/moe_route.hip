@@ -36,7 +36,38 @@ struct RouteArgs {
   int64_t *sorted_pairs, *sorted_expts;
   int32_t *counts, *offsets;  // nullable
   int T, E, topk, normalize, M, W;
+  // Optional: x (T, K) F32 rows converted to f16 (xh) with their power-of-two scales (xs).
+  const float *x;
+  _Float16 *xh;
+  float *xs;
+  int64_t K;
 };
+
+// Row t of x to f16 divided by 2^e (e = 0 unless max |x| >= 2^15; then e brings the row's
+// maximum below 2^15) and xs[t] = 2^e, by one wave: what to_f16_rowscale_kernel writes for
+// the row, bit for bit (the same maximum, exponent and conversion).  K % 4 == 0, x 16-byte
+// aligned.
+__device__ void rowscale_wave(const RouteArgs &a, int t, int lane) {
+  const float4 *xr = reinterpret_cast<const float4 *>(a.x + (int64_t)t * a.K);
+  const int64_t n4 = a.K / 4;
+  float m = 0.f;
+  for (int64_t i = lane; i < n4; i += 64) {
+    const float4 v = xr[i];
+    m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+  }
+  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+  int ex = 0;
+  (void)frexpf(m, &ex);  // m < 2^ex
+  const int e = ex > 15 && m == m && m < INFINITY ? ex - 15 : 0;
+  typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+  f16x4 *yr = reinterpret_cast<f16x4 *>(a.xh + (int64_t)t * a.K);
+  for (int64_t i = lane; i < n4; i += 64) {
+    const float4 v = xr[i];
+    yr[i] = f16x4{(_Float16)ldexpf(v.x, -e), (_Float16)ldexpf(v.y, -e), (_Float16)ldexpf(v.z, -e),
+                  (_Float16)ldexpf(v.w, -e)};
+  }
+  if (lane == 0) a.xs[t] = ldexpf(1.f, e);
+}
 
 // Top-k of token t by one wave, renormalised if asked; writes topk_ids and weights.
 template <int VPL>
@@ -88,7 +119,10 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(RouteArgs a) {
 
   for (int64_t i = t; i < (int64_t)a.W * a.E; i += nthr) wcnt[i] = 0;
   if constexpr (TOPK) {
-    for (int tok = wave; tok < a.T; tok += nwav) route_token(a, tok, lane, lid);
+    for (int tok = wave; tok < a.T; tok += nwav) {
+      route_token(a, tok, lane, lid);
+      if (a.x) rowscale_wave(a, tok, lane);
+    }
   } else {
     for (int p = t; p < a.M; p += nthr) {
       int64_t id = a.ids_in[p];
@@ -160,7 +194,10 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(RouteArgs a) {
 // Top-k for many tokens: one wave per token, 8 tokens per workgroup.
 __global__ __launch_bounds__(512) void moe_topk_kernel(RouteArgs a) {
   const int tok = blockIdx.x * 8 + (threadIdx.x >> 6);
-  if (tok < a.T) route_token(a, tok, threadIdx.x & 63, nullptr);
+  if (tok < a.T) {
+    route_token(a, tok, threadIdx.x & 63, nullptr);
+    if (a.x) rowscale_wave(a, tok, threadIdx.x & 63);
+  }
 }
 
 size_t route_lds(int64_t M, int64_t E) {
@@ -194,9 +231,13 @@ bool moe_route_fits(int64_t M, int64_t E) {
 
 int launch_moe_route(const float *probs, int64_t T, int64_t E, int topk, int normalize, int64_t *topk_ids,
                      float *weights, int64_t *sorted_pairs, int64_t *sorted_expts, int32_t *counts, int32_t *offsets,
-                     hipStream_t s) {
+                     hipStream_t s, const float *x_f32, int64_t K, uint16_t *xh, float *xs) {
   RouteArgs a = {};
   a.probs = probs;
+  a.x = x_f32;
+  a.xh = reinterpret_cast<_Float16 *>(xh);
+  a.xs = xs;
+  a.K = K;
   a.topk_ids = topk_ids;
   a.weights = weights;
   a.sorted_pairs = sorted_pairs;
