@@ -17,11 +17,14 @@ shapes.  Both halves are measured in the default run.
   dense bf16 MFMA peak, with Light's CPU path beside it.
 * `cpu_baseline`: Light's AVX2 CPU path (the C restatement in oracle/: MatMulQ, MatMulQ,
   SiLU, Mul, MatMulQ) on the same step, on the host cores available to this process.
+* `table`: every named configuration (the GEMV / GEMM / int4 / MoE shapes and the added
+  formats): µs per call, GB/s, TFLOP/s and fraction of HBM peak, with Light's CPU path for
+  the same call beside it (a bounded sample where the whole call would take too long).
 
 Inputs are synthetic (seeded, BASELINE distributions) and resident in HBM; every weight is
 rotated over enough copies that the working set exceeds the 256 MB Infinity Cache.
 
-Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--table] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-table] [--no-cpu]
 """
 import argparse
 import json
@@ -44,7 +47,8 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--table", action="store_true", help="also time every config (printed to stderr)")
+    p.add_argument("--table", action="store_true", help="also print the per-config table to stderr")
+    p.add_argument("--no-table", action="store_true", help="leave the per-config table out of the line")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--launches", type=int, default=200, help="per-kernel timed launches for the roofline")
     p.add_argument("--gemm-launches", type=int, default=100, help="timed calls per M=512 GEMM shape")
@@ -394,9 +398,18 @@ def moe_rows(c, name, g, dev, cpu=False):
     used = float(np.mean([len(np.unique(torch.topk(p_, topk, dim=1).indices.cpu().numpy())) for p_ in probs]))
     nbytes = used * (ebytes_gu + ebytes_dn) + 4 * T * E + 4 * T * H * 2
     gbs = nbytes / (us * 1e-6) / 1e9
-    out.append(dict(config=f"{name}_block", us=round(us, 2), GBs=round(gbs, 1),
-                    TFLOPS=round(2.0 * M * (2 * I * H + H * I) / (us * 1e-6) / 1e12, 2),
-                    hbm_frac=round(gbs / HBM_PEAK_GBS, 3)))
+    brow = dict(config=f"{name}_block", us=round(us, 2), GBs=round(gbs, 1),
+                TFLOPS=round(2.0 * M * (2 * I * H + H * I) / (us * 1e-6) / 1e12, 2),
+                hbm_frac=round(gbs / HBM_PEAK_GBS, 3))
+    legs = [r for r in out if r["config"] in (f"{name}_gate_up", f"{name}_down") and "cpu_us" in r]
+    if cpu and len(legs) == 2:
+        # Light's CPU block is its routing (a top-k and a sort of T x E values, negligible here)
+        # plus the two MoEGemmQ legs (the SiLU * up and the combine are O(T topk I) adds): the
+        # sum of the two legs' CPU times above.
+        t = sum(r["cpu_us"] for r in legs)
+        brow.update(cpu_us=round(t, 1), cpu_threads=legs[0]["cpu_threads"],
+                    cpu_sample="sum of the gate_up and down rows' CPU times", gpu_over_cpu=round(t / us, 1))
+    out.append(brow)
     return out
 
 
@@ -598,8 +611,10 @@ def main():
     line["gemm"] = gemm_records(args, torch.device("cuda:0"), cpu=not args.no_cpu)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(res["inputs"])
-    if args.table:
-        print(json.dumps({"table": table(args, torch.device("cuda:0"))}), file=sys.stderr)
+    if args.table or not args.no_table:
+        line["table"] = table(args, torch.device("cuda:0"))
+        if args.table:
+            print(json.dumps({"table": line["table"]}), file=sys.stderr)
     print(json.dumps(line))
 
 
