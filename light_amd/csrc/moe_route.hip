@@ -46,26 +46,47 @@ struct RouteArgs {
 // Row t of x to f16 divided by 2^e (e = 0 unless max |x| >= 2^15; then e brings the row's
 // maximum below 2^15) and xs[t] = 2^e, by one wave: what to_f16_rowscale_kernel writes for
 // the row, bit for bit (the same maximum, exponent and conversion).  K % 4 == 0, x 16-byte
-// aligned.
+// aligned.  K <= 4096: the row is read once, into registers.
 __device__ void rowscale_wave(const RouteArgs &a, int t, int lane) {
   const float4 *xr = reinterpret_cast<const float4 *>(a.x + (int64_t)t * a.K);
   const int64_t n4 = a.K / 4;
-  float m = 0.f;
-  for (int64_t i = lane; i < n4; i += 64) {
-    const float4 v = xr[i];
-    m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-  }
-  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-  int ex = 0;
-  (void)frexpf(m, &ex);  // m < 2^ex
-  const int e = ex > 15 && m == m && m < INFINITY ? ex - 15 : 0;
   typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
   f16x4 *yr = reinterpret_cast<f16x4 *>(a.xh + (int64_t)t * a.K);
-  for (int64_t i = lane; i < n4; i += 64) {
-    const float4 v = xr[i];
-    yr[i] = f16x4{(_Float16)ldexpf(v.x, -e), (_Float16)ldexpf(v.y, -e), (_Float16)ldexpf(v.z, -e),
-                  (_Float16)ldexpf(v.w, -e)};
+  auto amax = [](const float4 v) { return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))); };
+  auto scale = [](float m) {
+    int ex = 0;
+    (void)frexpf(m, &ex);  // m < 2^ex
+    return ex > 15 && m == m && m < INFINITY ? ex - 15 : 0;
+  };
+  auto cvt = [](const float4 v, int e) {
+    return f16x4{(_Float16)ldexpf(v.x, -e), (_Float16)ldexpf(v.y, -e), (_Float16)ldexpf(v.z, -e),
+                 (_Float16)ldexpf(v.w, -e)};
+  };
+  constexpr int R = 16;  // float4 per lane held in registers
+  float m = 0.f;
+  if (n4 <= 64 * R) {
+    float4 v[R];
+#pragma unroll
+    for (int j = 0; j < R; j++) {
+      const int64_t i = lane + 64 * j;
+      v[j] = i < n4 ? xr[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int j = 0; j < R; j++) m = fmaxf(m, amax(v[j]));
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    const int e = scale(m);
+#pragma unroll
+    for (int j = 0; j < R; j++) {
+      const int64_t i = lane + 64 * j;
+      if (i < n4) yr[i] = cvt(v[j], e);
+    }
+    if (lane == 0) a.xs[t] = ldexpf(1.f, e);
+    return;
   }
+  for (int64_t i = lane; i < n4; i += 64) m = fmaxf(m, amax(xr[i]));
+  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+  const int e = scale(m);
+  for (int64_t i = lane; i < n4; i += 64) yr[i] = cvt(xr[i], e);
   if (lane == 0) a.xs[t] = ldexpf(1.f, e);
 }
 
@@ -96,6 +117,7 @@ __device__ __forceinline__ void route_token(const RouteArgs &a, int t, int lane,
   else
     route_token_v<16>(a, t, lane, lid);
 }
+
 
 // Mask of lanes holding the same id as this lane (among valid lanes).
 __device__ __forceinline__ uint64_t match_id(int id, bool valid, int nbits) {
@@ -191,9 +213,9 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(RouteArgs a) {
   }
 }
 
-// Top-k for many tokens: one wave per token, 8 tokens per workgroup.
+// Top-k for many tokens: one wave per token, blockDim / 64 tokens per workgroup.
 __global__ __launch_bounds__(512) void moe_topk_kernel(RouteArgs a) {
-  const int tok = blockIdx.x * 8 + (threadIdx.x >> 6);
+  const int tok = blockIdx.x * (int)(blockDim.x >> 6) + (int)(threadIdx.x >> 6);
   if (tok < a.T) {
     route_token(a, tok, threadIdx.x & 63, nullptr);
     if (a.x) rowscale_wave(a, tok, threadIdx.x & 63);
@@ -252,7 +274,9 @@ int launch_moe_route(const float *probs, int64_t T, int64_t E, int topk, int nor
   a.W = (a.M + 63) / 64;
   // Few tokens: top-k and sort in one workgroup; otherwise top-k over the grid first.
   if (T <= 4 * kRouteWaves) return run_route(true, a, s);
-  moe_topk_kernel<<<(unsigned)cdiv(T, 8), 512, 0, s>>>(a);
+  // Converting x too: one token per workgroup, so the rows spread over the CUs.
+  const int tpw = a.x ? 1 : 8;
+  moe_topk_kernel<<<(unsigned)cdiv(T, tpw), 64 * tpw, 0, s>>>(a);
   if (int rc = check_launch("moe_topk")) return rc;
   a.ids_in = topk_ids;
   return run_route(false, a, s);
