@@ -407,6 +407,19 @@ def test_moe_block_grouped_gemm_path_equals_separate_calls(dev, caller_counts):
                                               torch.cumsum(cnt, 0).to(torch.int32)]))
 
 
+@pytest.mark.parametrize("T,N,topk", [(256, 2048, 8), (3, 4096, 1), (5, 1024, 3), (2, 512, 9), (4, 1026, 8)])
+def test_moe_combine_bit_exact(dev, T, N, topk):
+    """MoECombine (ops/moe.go:209-240): y[t] = pair[t, 0] + pair[t, 1] + ... in slot order, bit
+    for bit against the oracle's sequential sum, for pair values spread over 2^-8 .. 2^8, at
+    the T = 256 shape and at small, odd and topk > 8 ones."""
+    print(f"[case] moe_combine T={T} N={N} topk={topk}", flush=True)
+    g = synth.rng(1900 + T + topk)
+    pr = (g.standard_normal((T * topk, N)) * np.exp(g.uniform(-8, 8, (T * topk, 1)))).astype(np.float32)
+    y = hipq.moe_combine(_t(pr, dev), topk).cpu().numpy()
+    want = oracle.moe_combine(pr, topk)
+    assert np.array_equal(y.view(np.uint32), np.asarray(want, dtype=np.float32).view(np.uint32))
+
+
 def test_moe_block_second_stream_and_changing_routes(dev):
     """The one-launch block on its stream and the two-launch path on another stream agree with
     the separate calls, for routings that change from call to call."""
