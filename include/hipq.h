@@ -43,6 +43,7 @@ enum {
   HQ_EINVAL = -1,       /* bad argument (shape, dtype, pointer) */
   HQ_EUNSUPPORTED = -2, /* dtype / layout not handled by this library */
   HQ_ENOMEM = -3,       /* workspace too small or allocation failed */
+  HQ_EBARRIER = -4,     /* a one-launch kernel's grid barrier gave up (hq_moe_block_q) */
 };
 
 /* dtype.DType codes (dtype/dtype.go:13-37). */
@@ -364,11 +365,26 @@ int hq_moe_route_gated(const float *probs, const float *x, const void *w, float 
  * projection; that kernel serves the first stream that calls this function on a device
  * (other streams get the two launches), and graph replays of it must not run beside one
  * another.  No counterpart kernel in Light: these launches fused. */
+/* The one-launch kernel needs its whole grid resident at once.  It is sized to the
+ * occupancy, but kernels of other streams or processes can hold CUs, so its grid barrier is
+ * a bounded wait (2^22 polls: 0.1 s to a few seconds).  A workgroup that gives up writes NaN
+ * to its rows of y and sets a flag in pinned host memory; the next hq_moe_block_q on the
+ * device then returns HQ_EBARRIER without launching anything (or hq_moe_block_q_check does,
+ * after synchronizing the stream), and from then on the device takes the two launches. */
 size_t hq_moe_block_q_ws_bytes(int64_t T, int topk, int64_t E, int64_t H, int64_t I, int w_dtype);
 int hq_moe_block_q(const float *probs, const float *x, const void *w_gate_up, const void *w_down, float *h, float *y,
                    int64_t T, int64_t E, int topk, int normalize, int64_t H, int64_t I, int w_dtype, int act,
                    int64_t *topk_ids, float *weights, int64_t *sorted_pairs, int64_t *sorted_expts, int32_t *counts,
                    int32_t *offsets, void *ws, size_t ws_bytes, hq_stream_t stream);
+/* Synchronizes `stream`, then returns HQ_EBARRIER (and clears the flag) if a one-launch MoE
+ * block on the current device gave up at its grid barrier since the last report, else HQ_OK.
+ * No counterpart in Light (its ops report every failure as an error, ops/moe.go:247-265). */
+int hq_moe_block_q_check(hq_stream_t stream);
+/* Test hook: the number of s_sleep(1) polls the one-launch block's barrier makes before it
+ * gives up (0: give up at once, so every workgroup fails and exits normally; the default is
+ * 2^22).  It also re-enables the one launch on the current device after a reported failure
+ * and hands the kernel to the next stream that runs the block. */
+void hq_debug_moe_block_spin_limit(uint32_t limit);
 
 /* ops.MoEInt4 (ops/int4.go:149-246): the routed gated-MLP expert block with canonical 4-bit
  * experts (GPTQ / AWQ MoE checkpoints):

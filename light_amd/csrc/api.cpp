@@ -760,6 +760,10 @@ int hq_moe_route_gated(const float *probs, const float *x, const void *w, float 
                                     sorted_pairs, sorted_expts, counts, offsets, ws, s);
 }
 
+int hq_moe_block_q_check(hq_stream_t stream) { return moe_block_check(resolve(stream), "hq_moe_block_q_check"); }
+
+void hq_debug_moe_block_spin_limit(uint32_t limit) { moe_block_set_spin_limit(limit); }
+
 size_t hq_moe_block_q_ws_bytes(int64_t T, int topk, int64_t E, int64_t H, int64_t I, int w_dtype) {
   if (T <= 0 || topk < 1 || E <= 0 || H <= 0 || I <= 0) return 0;
   return moe_block_ws_bytes(T, topk, E, H, I, w_dtype);

@@ -622,9 +622,11 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(MoeGemmArgs ma) {
       if (s + 1 < ksteps) stage_in((s + 1) & 1, s + 1, ra[nslot], wp[nslot], std::integral_constant<int, nslot>{});
       __syncthreads();
     };
+    // ksteps = K / 64 is a multiple of MD (Q4_K rows are whole 256-k blocks), so each trip runs
+    // all MD steps: the loop has no exit between its steps, and every path that reaches the
+    // loop head has issued the same loads.
     for (int s = 0; s < ksteps; s += MD)
-      unroll_steps([&](auto I) { return s + decltype(I)::value < ksteps ? (step(s + decltype(I)::value, I), true) : false; },
-                   std::make_integer_sequence<int, MD>{});
+      unroll_steps([&](auto I) { return step(s + decltype(I)::value, I), true; }, std::make_integer_sequence<int, MD>{});
     // The ring's last (clamped) loads land before its registers can be reused.
     wait_ring<0>(ra[0], wp[0].q, hd);
 #pragma unroll
@@ -679,6 +681,7 @@ int launch_moe_gemm_q4k(const float *x, uint16_t *xh, float *xs, const void *w, 
                         int64_t rows, int64_t E, int64_t N, int64_t K, int rpp, hipStream_t s, int64_t gated_I,
                         int act, bool x_ready) {
   using T = GTile<32>;
+  if (K % 256 || K <= 0) return fail(HQ_EINVAL, "moe_gemm_q4k", "K=%lld is not a multiple of 256", (long long)K);
   if (!x_ready) {
     to_f16_rowscale_kernel<<<(unsigned)rows, 256, 0, s>>>(x, reinterpret_cast<_Float16 *>(xh), xs, K);
     if (int rc = check_launch("to_f16_rowscale")) return rc;

@@ -1153,10 +1153,11 @@ struct MoeCombArgs {
 
 // The kernel body for workgroup bx of G (token tok).  FUSED (the one-launch MoE block): the
 // slots' experts and routing weights come from the workgroup's own routing (slot_e, slot_w),
-// the first weights go out before hook() -- which waits until h is complete -- and h is read
-// with agent-coherent loads after it.
+// the first weights go out before hook() -- which waits until h is complete and returns false
+// if it gave up -- and h is read with agent-coherent loads after it.  A workgroup whose hook
+// gave up writes NaN to its rows of y instead of sums over an h that may be incomplete.
 struct NoWait {
-  __device__ void operator()() const {}
+  __device__ bool operator()() const { return true; }
 };
 
 template <class U, bool FUSED = false, class Hook = NoWait>
@@ -1236,8 +1237,9 @@ __device__ __forceinline__ void moe_comb_body(const MoeCombArgs &ma, uint8_t *sm
     const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(hr, (uint32_t)task * 16u, 0, 16 /* sc1 */);
     return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3]));
   };
+  bool h_ok = true;
   if constexpr (FUSED) {
-    hook();
+    h_ok = hook();
 #pragma unroll
     for (int i = 0; i < XT; i++) xv[i] = hload(i * bd + t < ntask ? i * bd + t : ntask - 1);
   }
@@ -1298,7 +1300,7 @@ __device__ __forceinline__ void moe_comb_body(const MoeCombArgs &ma, uint8_t *sm
     if (t < RPW && row < a.N) {
       float acc = vb[t * topk];
       for (int s2 = 1; s2 < topk; s2++) acc = __fadd_rn(acc, vb[t * topk + s2]);
-      static_cast<float *>(a.out)[(int64_t)tok * a.N + row] = acc;
+      static_cast<float *>(a.out)[(int64_t)tok * a.N + row] = h_ok ? acc : __builtin_nanf("");
     }
   }
 }
@@ -1323,13 +1325,31 @@ __global__ __launch_bounds__(512) void moe_down_combine_kernel(MoeCombArgs ma) {
 // the generation at 64 * (17 + r).  A workgroup reads its copy of the generation before it
 // arrives; the last arrival at a counter resets it and arrives at the top counter; the last
 // arrival there resets it and bumps every copy; the others poll their copy.  The state
-// returns to zero counts after every launch, so graph replays work.  The wait needs the whole
-// grid resident at once (the host sizes the grid to the occupancy and serves one stream);
-// it is bounded all the same.
+// returns to zero counts after every launch, so graph replays work: a workgroup always
+// arrives before it waits, so the last one to arrive completes the barrier even when others
+// have already given up.
+//
+// The wait needs the whole grid resident at once.  The host sizes the grid to the occupancy
+// and serves one stream, but kernels of other streams or processes can hold CUs, so the wait
+// is bounded (`limit` polls, each a device-scope load and an s_sleep(1): by default 2^22,
+// at least 0.1 s and a few seconds at most, against a few microseconds for a normal wait).
+// A workgroup that gives up sets the failure word (64 * (17 + 16)) and the host-visible
+// flag, and writes NaN to its rows of y; the host reports the failure as an error
+// (hq_moe_block_q / hq_moe_block_q_check).
+//
+// Ordering is carried by the accesses to h themselves, not by release / acquire on the barrier
+// words: h goes out as device-scope (sc1) stores, every thread waits for its own stores to
+// complete (s_waitcnt vmcnt(0)) before the workgroup barrier that precedes thread 0's arrival
+// (so the compiler cannot move the arrival above them either), and after the poll and a
+// second workgroup barrier h is read back with device-scope (sc1) loads, which miss any stale
+// line of the reader's L2.  The counters and generation words are relaxed device-scope
+// atomics.  Agent-scope release / acquire on them instead (an L2 write-back per arrival and
+// an invalidate after the poll) measured 32.0 against 20.4 us per block.
 // ---------------------------------------------------------------------------
 constexpr int kBarSub = 16;
-constexpr int kBarWords = 64 * (17 + kBarSub);
-constexpr uint32_t kBarSpinLimit = 1u << 26;  // s_sleep(1) rounds, far beyond a normal wait
+constexpr int kBarFail = 64 * (17 + kBarSub);
+constexpr int kBarWords = kBarFail + 64;
+constexpr uint32_t kBarSpinLimit = 1u << 22;  // polls; a normal wait takes a few hundred
 
 __device__ __forceinline__ void bar_arrive(uint32_t *w, int bx, int G, uint32_t gen) {
   const int k = bx % kBarSub;
@@ -1343,27 +1363,41 @@ __device__ __forceinline__ void bar_arrive(uint32_t *w, int bx, int G, uint32_t 
     __hip_atomic_store(&w[64 * (17 + r)], gen + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Returns false (for the whole workgroup) if the generation did not change within `limit` polls.
 struct BarWait {
   uint32_t *w;
   uint32_t gen;
   int bx;
-  __device__ void operator()() const {
+  uint32_t limit;
+  uint32_t *host_flag;  // pinned host word, nullable
+  int *ok_lds;
+  __device__ bool operator()() const {
     if (threadIdx.x == 0) {
       uint32_t *g = &w[64 * (17 + bx % kBarSub)];
-      for (uint32_t n = 0; n < kBarSpinLimit; n++) {
-        if (__hip_atomic_load(g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != gen) break;
+      int ok = 0;
+      for (uint32_t n = 0; n < limit; n++) {
+        if (__hip_atomic_load(g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != gen) {
+          ok = 1;
+          break;
+        }
         __builtin_amdgcn_s_sleep(1);
       }
+      if (!ok) {
+        __hip_atomic_store(&w[kBarFail], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (host_flag) __hip_atomic_store(host_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      }
+      *ok_lds = ok;
     }
     __syncthreads();
+    return *ok_lds != 0;
   }
 };
 
 template <class U>
 __global__ __launch_bounds__(512) void moe_block_kernel(MoeXArgs ma1, MoeCombArgs ma2, uint32_t *bar, int per,
-                                                        int nseg) {
+                                                        int nseg, uint32_t limit, uint32_t *host_flag) {
   extern __shared__ __align__(16) uint8_t smem[];
-  __shared__ int r_e[64], r_se[64], r_sp[64];
+  __shared__ int r_e[64], r_se[64], r_sp[64], r_ok;
   __shared__ float r_w[64];
   const int id = (int)blockIdx.x, G = (int)gridDim.x;
   uint32_t gen = 0;
@@ -1374,7 +1408,7 @@ __global__ __launch_bounds__(512) void moe_block_kernel(MoeXArgs ma1, MoeCombArg
   __builtin_amdgcn_s_waitcnt(0);  // this wave's h stores are complete
   __syncthreads();
   if (threadIdx.x == 0) bar_arrive(bar, id, G, gen);
-  moe_comb_body<U, true>(ma2, smem, id, 0, G, r_e, r_w, BarWait{bar, gen, id});
+  moe_comb_body<U, true>(ma2, smem, id, 0, G, r_e, r_w, BarWait{bar, gen, id, limit, host_flag, &r_ok});
 }
 
 // ---------------------------------------------------------------------------
@@ -2062,30 +2096,76 @@ int launch_moe_route_gated(const float *probs, const float *x, const void *w, fl
 // The one-launch MoE block's barrier words: a file-scope device array (zero when the library
 // loads) that serves one stream per device -- the first to run the block; other streams take
 // the two launches (two such grids side by side could each hold CUs the other waits for).
+// Beside it, per device, a pinned host word that a workgroup giving up at the barrier sets
+// (system scope), so the host sees the failure without synchronizing; after a failure the
+// device takes the two launches until moe_block_set_spin_limit() re-enables the one launch.
 static __device__ __align__(256) uint32_t g_moe_bar[kBarWords];
 
-static uint32_t *moe_block_bar(hipStream_t s) {
-  static std::mutex mu;
-  static uint32_t *base[64] = {};
-  static hipStream_t owner[64] = {};
-  static bool init[64] = {};
+namespace {
+struct MoeBarState {
+  uint32_t *bar = nullptr;         // device address of g_moe_bar on this device
+  volatile uint32_t *flag = nullptr;  // pinned host word
+  hipStream_t owner = nullptr;
+  bool init = false, disabled = false;
+};
+std::mutex g_bar_mu;
+MoeBarState g_bar[64];
+uint32_t g_bar_limit = kBarSpinLimit;
+
+MoeBarState *moe_bar_state(int *dev_out) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
     (void)hipGetLastError();
     return nullptr;
   }
-  std::lock_guard<std::mutex> lk(mu);
-  if (!init[dev]) {
-    void *p = nullptr;
+  *dev_out = dev;
+  MoeBarState &st = g_bar[dev];
+  if (!st.init) {
+    void *p = nullptr, *h = nullptr;
     if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_moe_bar)) != hipSuccess || !p) {
       (void)hipGetLastError();
       return nullptr;
     }
-    base[dev] = static_cast<uint32_t *>(p);
-    owner[dev] = s;
-    init[dev] = true;
+    if (hipHostMalloc(&h, 256, hipHostMallocCoherent | hipHostMallocMapped) != hipSuccess || !h) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+    st.bar = static_cast<uint32_t *>(p);
+    st.flag = static_cast<volatile uint32_t *>(h);
+    *st.flag = 0;
+    st.init = true;
   }
-  return owner[dev] == s ? base[dev] : nullptr;
+  return &st;
+}
+
+// HQ_OK, or the error of a one-launch block on this device whose barrier gave up since the
+// last check (the flag is cleared and the device falls back to the two launches).
+int moe_bar_take_failure(MoeBarState &st, const char *call) {
+  if (!st.flag || *st.flag == 0) return HQ_OK;
+  *st.flag = 0;
+  st.disabled = true;
+  return fail(HQ_EBARRIER, call,
+              "an earlier one-launch MoE block on this device gave up at its grid barrier (the grid was "
+              "not resident at once); that call's y holds NaN, and later calls take the two launches");
+}
+}  // namespace
+
+int moe_block_check(hipStream_t s, const char *call) {
+  if (hipError_t e = hipStreamSynchronize(s)) return fail((int)e, call, "hipStreamSynchronize: %s", hipGetErrorString(e));
+  std::lock_guard<std::mutex> lk(g_bar_mu);
+  int dev = 0;
+  MoeBarState *st = moe_bar_state(&dev);
+  return st ? moe_bar_take_failure(*st, call) : HQ_OK;
+}
+
+void moe_block_set_spin_limit(uint32_t limit) {
+  std::lock_guard<std::mutex> lk(g_bar_mu);
+  g_bar_limit = limit;
+  int dev = 0;
+  if (MoeBarState *st = moe_bar_state(&dev)) {
+    st->disabled = false;
+    st->owner = nullptr;  // the next stream to run the block owns it
+  }
 }
 
 // MoERoute + gated gate/up + down + MoECombine for one token in one launch; returns 1 (and
@@ -2098,8 +2178,22 @@ int launch_moe_block(const float *probs, const float *x, const void *wgu, const 
   constexpr int kNo = 1;
   if (T != 1 || (dt != Q4_K && dt != Q5_K) || topk > 64) return kNo;
   if (!moe_route_gated_ok(T, E, topk, H, dt, wgu, x) || !moe_comb_ok(topk, T, topk, I, dt, wdn, h)) return kNo;
-  uint32_t *bar = moe_block_bar(s);
-  if (!bar) return kNo;
+  uint32_t *bar = nullptr;
+  uint32_t *host_flag = nullptr;
+  uint32_t limit = 0;
+  {
+    std::lock_guard<std::mutex> lk(g_bar_mu);
+    int dev = 0;
+    MoeBarState *st = moe_bar_state(&dev);
+    if (!st) return kNo;
+    if (int rc = moe_bar_take_failure(*st, "hq_moe_block_q")) return rc;
+    if (st->disabled) return kNo;
+    if (!st->owner) st->owner = s;
+    if (st->owner != s) return kNo;
+    bar = st->bar;
+    host_flag = const_cast<uint32_t *>(st->flag);
+    limit = g_bar_limit;
+  }
   MoeXArgs ma1;
   const int64_t rb1 = q4kx_row_bytes(dt, H), rb2 = q4kx_row_bytes(dt, I);
   if (q4kx_setup(ma1.g, 1, 2 * I, H, 256, rb1, "moe_block")) return kNo;
@@ -2168,7 +2262,7 @@ int launch_moe_block(const float *probs, const float *x, const void *wgu, const 
   const int64_t resident = (int64_t)device_cus() * (pc < 2 ? pc : 2);
   const int64_t G = std::max<int64_t>(per * nseg, device_cus() * 2);
   if (pc < 1 || G > resident) return kNo;
-  kern<<<(unsigned)G, 512, lds, s>>>(ma1, ma2, bar, (int)per, (int)nseg);
+  kern<<<(unsigned)G, 512, lds, s>>>(ma1, ma2, bar, (int)per, (int)nseg, limit, host_flag);
   if (int rc = check_launch("moe_block")) return rc;
   return HQ_OK;
 }

@@ -172,69 +172,74 @@ __global__ __launch_bounds__(512) void gemm_i4f16_small_kernel(I4F16Args a) {
     constexpr int slot = decltype(SLOT)::value, nslot = (slot + 1) % ID;
     const int buf = (c - c0) & 1;
     wait_w<4 * (ID - 1)>(cw[slot][0], cw[slot][1]);
-    const int gl = c * IK / a.G - g0, lr = wave * 32 + fr;
-    const float sgv = lsz[lr * ngl + gl], zgv = lsz[256 * ngl + lr * ngl + gl];
-    const uint16_t *xa = &xs[buf][0];
-    // Nibbles i = 0, 2 enter as 1024 + q, nibbles 1, 3 as 1024 + 16 q (masked in place, no
-    // shift; the x pairs they meet were staged / 16).  Integral zero points (every GPTQ / AWQ
-    // checkpoint's): one packed add of -(1024 + z) or -(1024 + 16 z) leaves q - z or 16 (q - z)
-    // exactly.  Otherwise (a wave-uniform test) -1024 first, exact, then -z or -16 z.
-    const bool zint = __all(zgv == rintf(zgv) && fabsf(zgv) <= 64.f);
-    const uint32_t magic = __builtin_amdgcn_readfirstlane(0x64006400u);
-    f32x16 cacc[2];
-    auto mfma_stage = [&](auto ZI) __attribute__((always_inline)) {
-      constexpr bool zi = decltype(ZI)::value;
-      const f16x2 c0v = {(_Float16)(zi ? -1024.f - zgv : -1024.f), (_Float16)(zi ? -1024.f - zgv : -1024.f)};
-      const f16x2 c0v16 = {(_Float16)(zi ? -1024.f - 16.f * zgv : -1024.f),
-                           (_Float16)(zi ? -1024.f - 16.f * zgv : -1024.f)};
-      const f16x2 zf = {(_Float16)-zgv, (_Float16)-zgv}, zf16 = {(_Float16)(-16.f * zgv), (_Float16)(-16.f * zgv)};
+    if (c < c1) {  // (uniform) a padding stage past the split only keeps the ring's loads and waits
+      const int gl = c * IK / a.G - g0, lr = wave * 32 + fr;
+      const float sgv = lsz[lr * ngl + gl], zgv = lsz[256 * ngl + lr * ngl + gl];
+      const uint16_t *xa = &xs[buf][0];
+      // Nibbles i = 0, 2 enter as 1024 + q, nibbles 1, 3 as 1024 + 16 q (masked in place, no
+      // shift; the x pairs they meet were staged / 16).  Integral zero points (every GPTQ / AWQ
+      // checkpoint's): one packed add of -(1024 + z) or -(1024 + 16 z) leaves q - z or 16 (q - z)
+      // exactly.  Otherwise (a wave-uniform test) -1024 first, exact, then -z or -16 z.
+      const bool zint = __all(zgv == rintf(zgv) && fabsf(zgv) <= 64.f);
+      const uint32_t magic = __builtin_amdgcn_readfirstlane(0x64006400u);
+      f32x16 cacc[2];
+      auto mfma_stage = [&](auto ZI) __attribute__((always_inline)) {
+        constexpr bool zi = decltype(ZI)::value;
+        const f16x2 c0v = {(_Float16)(zi ? -1024.f - zgv : -1024.f), (_Float16)(zi ? -1024.f - zgv : -1024.f)};
+        const f16x2 c0v16 = {(_Float16)(zi ? -1024.f - 16.f * zgv : -1024.f),
+                             (_Float16)(zi ? -1024.f - 16.f * zgv : -1024.f)};
+        const f16x2 zf = {(_Float16)-zgv, (_Float16)-zgv}, zf16 = {(_Float16)(-16.f * zgv), (_Float16)(-16.f * zgv)};
 #pragma unroll
-      for (int j = 0; j < 8; j++) {
-        const uint32_t w = cw[slot][j >> 2][j & 3], w8 = w >> 8;
-        const uint32_t pr[4] = {and_or_6400(w, 0x000F000Fu, magic), and_or_6400(w, 0x00F000F0u, magic),
-                                and_or_6400(w8, 0x000F000Fu, magic), and_or_6400(w8, 0x00F000F0u, magic)};
-        f16x8 b;
+        for (int j = 0; j < 8; j++) {
+          const uint32_t w = cw[slot][j >> 2][j & 3], w8 = w >> 8;
+          const uint32_t pr[4] = {and_or_6400(w, 0x000F000Fu, magic), and_or_6400(w, 0x00F000F0u, magic),
+                                  and_or_6400(w8, 0x000F000Fu, magic), and_or_6400(w8, 0x00F000F0u, magic)};
+          f16x8 b;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-          f16x2 h;
-          __builtin_memcpy(&h, &pr[i], 4);
-          h = h + ((i & 1) ? c0v16 : c0v);
-          if constexpr (!zi) h = h + ((i & 1) ? zf16 : zf);
-          b[2 * i] = h[0];
-          b[2 * i + 1] = h[1];
+          for (int i = 0; i < 4; i++) {
+            f16x2 h;
+            __builtin_memcpy(&h, &pr[i], 4);
+            h = h + ((i & 1) ? c0v16 : c0v);
+            if constexpr (!zi) h = h + ((i & 1) ? zf16 : zf);
+            b[2 * i] = h[0];
+            b[2 * i + 1] = h[1];
+          }
+          const int kx = 64 * kh + 8 * j;
+          const f16x8 a0 = *reinterpret_cast<const f16x8 *>(xa + fr * IXLD + kx);
+          const f16x8 a1 = *reinterpret_cast<const f16x8 *>(xa + (32 + fr) * IXLD + kx);
+          if (j == 0) {
+            const f32x16 zero = {};
+            cacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b, zero, 0, 0, 0);
+            cacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b, zero, 0, 0, 0);
+          } else {
+            cacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b, cacc[0], 0, 0, 0);
+            cacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b, cacc[1], 0, 0, 0);
+          }
         }
-        const int kx = 64 * kh + 8 * j;
-        const f16x8 a0 = *reinterpret_cast<const f16x8 *>(xa + fr * IXLD + kx);
-        const f16x8 a1 = *reinterpret_cast<const f16x8 *>(xa + (32 + fr) * IXLD + kx);
-        if (j == 0) {
-          const f32x16 zero = {};
-          cacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b, zero, 0, 0, 0);
-          cacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b, zero, 0, 0, 0);
-        } else {
-          cacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b, cacc[0], 0, 0, 0);
-          cacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b, cacc[1], 0, 0, 0);
-        }
-      }
-    };
-    if (zint)
-      mfma_stage(std::true_type{});
-    else
-      mfma_stage(std::false_type{});
-    const float sc = sgv;
+      };
+      if (zint)
+        mfma_stage(std::true_type{});
+      else
+        mfma_stage(std::false_type{});
+      const float sc = sgv;
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+      for (int i = 0; i < 2; i++)
 #pragma unroll
-      for (int r = 0; r < 16; r++) acc[i][r] = __fmaf_rn(sc, cacc[i][r], acc[i][r]);
+        for (int r = 0; r < 16; r++) acc[i][r] = __fmaf_rn(sc, cacc[i][r], acc[i][r]);
+    }
     load_x(c + ID, slot);
     load_w(c + ID, slot);
     wait_x<2 + 4 * (ID - 1)>(xv[nslot][0], xv[nslot][1]);
     store_x(buf ^ 1, nslot);
     __syncthreads();
   };
+  // Every trip runs all ID stages (the last trip's stages past c1 are padding), so each path
+  // to the loop head has issued the same loads and the hand-counted waits hold on all of them.
+  static_assert(ID == 3, "the trip below unrolls ID stages");
   for (int c = c0; c < c1; c += ID) {
     stage(c, std::integral_constant<int, 0>{});
-    if (c + 1 < c1) stage(c + 1, std::integral_constant<int, 1>{});
-    if (c + 2 < c1) stage(c + 2, std::integral_constant<int, 2>{});
+    stage(c + 1, std::integral_constant<int, 1>{});
+    stage(c + 2, std::integral_constant<int, 2>{});
   }
   // The last (clamped) prefetches land before their registers can be reused.
 #pragma unroll

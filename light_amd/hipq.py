@@ -21,7 +21,7 @@ BLOCK = {Q4_0: (32, 18), Q5_0: (32, 22), Q8_0: (32, 34), Q8_1: (32, 36), Q4_K: (
 NAMES = {F16: "F16", BF16: "BF16", F32: "F32", Q4_0: "Q4_0", Q5_0: "Q5_0", Q8_0: "Q8_0", Q8_1: "Q8_1",
          Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K", Q6_K_R: "Q6_K_R"}
 
-HQ_OK, HQ_EINVAL, HQ_EUNSUPPORTED, HQ_ENOMEM = 0, -1, -2, -3
+HQ_OK, HQ_EINVAL, HQ_EUNSUPPORTED, HQ_ENOMEM, HQ_EBARRIER = 0, -1, -2, -3, -4
 ACT_SILU, ACT_GELU_ERF = 0, 1
 
 
@@ -96,6 +96,8 @@ SIGNATURES = {
     "hq_moe_block_q_ws_bytes": (_SZ, [_I64, _I, _I64, _I64, _I64, _I]),
     "hq_moe_block_q": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I, _I, _I64, _I64, _I, _I, _P, _P, _P, _P, _P, _P,
                             _P, _SZ, _P]),
+    "hq_moe_block_q_check": (_I, [_P]),
+    "hq_debug_moe_block_spin_limit": (None, [ctypes.c_uint32]),
     "hq_moe_route_gated": (_I, [_P, _P, _P, _P, _I64, _I64, _I, _I, _I64, _I64, _I, _I, _P, _P, _P, _P, _P, _P, _P,
                                 _SZ, _P]),
     "hq_moe_gemm_q": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I,
@@ -434,6 +436,18 @@ def moe_block_q(probs, x, w_gate_up, w_down, E, H, I, w_dtype, topk, normalize=T
                                int(bool(normalize)), H, I, w_dtype, act, _ptr(ids), _ptr(wt), _ptr(sp), _ptr(se),
                                _ptr(counts), _ptr(offsets), _ptr(ws), ws_bytes, _stream(stream)))
     return out, ids, wt, sp, se, h
+
+
+def moe_block_q_check(stream=None):
+    """Synchronize the stream; raise HipqError(HQ_EBARRIER) if a one-launch MoE block on the
+    current device gave up at its grid barrier since the last report."""
+    check(lib().hq_moe_block_q_check(_stream(stream)))
+
+
+def debug_moe_block_spin_limit(limit=1 << 22):
+    """Test hook: polls before the one-launch block's barrier gives up (0: at once); also
+    re-enables the one launch after a reported failure."""
+    lib().hq_debug_moe_block_spin_limit(int(limit))
 
 
 def moe_int4(x, gate_up, down, topk_ids, weights, topk, G, act=ACT_SILU, out=None, ws=None, stream=None):

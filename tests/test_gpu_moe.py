@@ -474,3 +474,48 @@ def test_moe_grouped_gemm_pairs_routed_nowhere(dev):
     got = hipq.moe_gemm_q_combine(h, wdn, spt, set_, E, H, I, hipq.Q4_K, topk, topk_w=twt, ws=ws)
     torch.cuda.synchronize()
     assert torch.equal(got, want)
+
+
+def test_moe_block_barrier_gives_up_loudly(dev):
+    """The one-launch block's grid barrier is a bounded wait.  With the host's test hook set
+    to give up at once (every workgroup still arrives, gives up and exits normally), the
+    call's y is all NaN, the next hq_moe_block_q on the device returns HQ_EBARRIER without
+    launching, later calls take the two launches, and hq_moe_block_q_check reports a failure
+    after synchronizing.  Restoring the limit re-enables the one launch, whose results then
+    equal the separate calls bit for bit (the barrier state stayed consistent)."""
+    print("[case] moe block barrier give-up (spin limit 0)", flush=True)
+    dt, E, topk, H, I = hipq.Q4_K, 128, 8, 2048, 768
+    g = synth.rng(1811)
+    wgu = _t(synth.gguf_weight(dt, E * 2 * I, H, g), dev)
+    wdn = _t(synth.gguf_weight(dt, E * H, I, g), dev)
+    x = _t(synth.activations(1, H, g), dev)
+    probs = _t(_probs(g, 1, E, ties=False), dev)
+    ids, w, sp, se, h = hipq.moe_route_gated(probs, x, wgu, E, I, H, dt, topk)
+    want = hipq.moe_gemm_q_combine(h, wdn, sp, se, E, H, I, dt, topk, topk_w=w)
+    try:
+        hipq.debug_moe_block_spin_limit(0)
+        y0 = hipq.moe_block_q(probs, x, wgu, wdn, E, H, I, dt, topk)[0]
+        torch.cuda.synchronize()
+        assert bool(torch.isnan(y0).all()), "a block whose barrier gave up must not return numbers"
+        with pytest.raises(hipq.HipqError) as ei:
+            hipq.moe_block_q(probs, x, wgu, wdn, E, H, I, dt, topk)
+        assert ei.value.code == hipq.HQ_EBARRIER, ei.value
+        assert "grid barrier" in str(ei.value)
+        # Reported once; the device now takes the two launches (spin limit still 0).
+        y1 = hipq.moe_block_q(probs, x, wgu, wdn, E, H, I, dt, topk)[0]
+        hipq.moe_block_q_check()
+        assert torch.equal(y1, want)
+        # Re-enabled with the limit still 0: the failure is reported by the check call too.
+        hipq.debug_moe_block_spin_limit(0)
+        y2 = hipq.moe_block_q(probs, x, wgu, wdn, E, H, I, dt, topk)[0]
+        with pytest.raises(hipq.HipqError) as ei:
+            hipq.moe_block_q_check()
+        assert ei.value.code == hipq.HQ_EBARRIER
+        assert bool(torch.isnan(y2).all())
+        hipq.moe_block_q_check()  # reported once
+    finally:
+        hipq.debug_moe_block_spin_limit()
+    for _ in range(2):
+        y3 = hipq.moe_block_q(probs, x, wgu, wdn, E, H, I, dt, topk)[0]
+        hipq.moe_block_q_check()
+        assert torch.equal(y3, want)
