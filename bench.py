@@ -219,6 +219,57 @@ def down_kernel(args, down, h, dev):
             "traffic": measured_traffic(f"down act N={N} K={K} M=1")}
 
 
+def ceilings(args, dev, step_us, kernel_bytes):
+    """What the hardware sustains on this box, measured in this run (context for the roofline
+    fractions, never their denominator): hq_ceiling_read, a plain streaming read launch of the
+    step's kernel sizes and of the whole step's bytes, rotating over a 640 MB buffer (beyond
+    the 256 MB MALL), in two access orders with two 16-byte loads in flight per thread; and
+    hq_ceiling_mfma, back-to-back register-operand v_mfma_f32_32x32x16_bf16."""
+    import ctypes
+    import torch
+    from light_amd import hipq
+    L = hipq.lib()
+    big = torch.empty(640 << 20, dtype=torch.uint8, device=dev)
+    big.fill_(1)
+    sink = torch.zeros(64, dtype=torch.int32, device=dev)
+    base = big.data_ptr()
+
+    def read_us(nbytes, order, n=60):
+        nbytes = nbytes // 256 * 256
+        nwin = big.numel() // nbytes
+
+        def fn(i):
+            hipq.check(L.hq_ceiling_read(ctypes.c_void_p(base + (i % nwin) * nbytes), nbytes, order, 2,
+                                         ctypes.c_void_p(sink.data_ptr()), None))
+        return time_launches(fn, n, nwin)
+
+    sizes = sorted(set(kernel_bytes) | {sum(kernel_bytes), 268435456})
+    reads = []
+    for nb in sizes:
+        for order, name in ((0, "window"), (1, "slice")):
+            us = read_us(nb, order)
+            reads.append({"bytes": nb, "order": name, "loads_in_flight_per_thread": 2, "us": round(us, 2),
+                          "GBs": round(nb / us / 1e3, 1), "frac": round(nb / us / 1e3 / HBM_PEAK_GBS, 4)})
+    best = {nb: min(r["us"] for r in reads if r["bytes"] == nb) for nb in sizes}
+    two = sum(best[nb] for nb in kernel_bytes)
+    flops = ctypes.c_int64()
+    sf = torch.zeros(16, device=dev)
+    iters = 20000
+    hipq.check(L.hq_ceiling_mfma(iters, ctypes.c_void_p(sf.data_ptr()), ctypes.byref(flops), None))
+    us = time_launches(lambda i: hipq.check(L.hq_ceiling_mfma(iters, ctypes.c_void_p(sf.data_ptr()),
+                                                               ctypes.byref(flops), None)), 5, 1)
+    tf = flops.value / us / 1e6
+    del big
+    torch.cuda.empty_cache()
+    return {"read": reads,
+            "step_kernels_read_us": round(two, 2),
+            "step_vs_read_ceiling": round(two / step_us, 4),
+            "step_one_launch_read_us": best[sum(kernel_bytes)],
+            "mfma_bf16": {"TFLOPS": round(tf, 1), "frac_of_peak": round(tf / 2500.0, 4),
+                          "kernel": "4 independent v_mfma_f32_32x32x16_bf16 chains per wave, register operands, "
+                                    "2 waves per SIMD"}}
+
+
 GEMM_SHAPES = ((512, 14336, 4096), (512, 4096, 14336))
 
 
@@ -608,6 +659,8 @@ def main():
         "second_kernel": res["down"],
     }
     import torch
+    line["ceilings"] = ceilings(args, torch.device("cuda:0"), res["ms_per_step"] * 1e3,
+                                [res["roofline"]["alg_bytes_per_launch"], res["down"]["alg_bytes_per_launch"]])
     line["gemm"] = gemm_records(args, torch.device("cuda:0"), cpu=not args.no_cpu)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(res["inputs"])

@@ -409,6 +409,19 @@ int hq_moe_int4(const void *x, int x_dtype, const void *const *expert_tab, int64
 int hq_gather_cols(const void *x, const int64_t *idx, void *y, int64_t M, int64_t K, int elem_bytes,
                    hq_stream_t stream);
 
+/* ---- ceilings (measurement only; no counterpart in Light) ----------------
+ * What the hardware sustains, reported beside the roofline fractions.
+ * hq_ceiling_read: one launch that reads `bytes` (16-byte aligned) of `buf` with 16-byte
+ * loads, `depth` (1, 2, 4 or 8) in flight per thread, two 512-thread workgroups per CU;
+ * order 0 reads a contiguous window that moves through the buffer (grid stride), order 1
+ * gives each workgroup its own contiguous slice.  `sink`: one device word (almost never
+ * written).
+ * hq_ceiling_mfma: one launch of `iters` rounds of four independent
+ * v_mfma_f32_32x32x16_bf16 per wave on register operands, two 256-thread workgroups per CU
+ * (two waves per SIMD); *flops receives the launch's flop count. */
+int hq_ceiling_read(const void *buf, int64_t bytes, int order, int depth, uint32_t *sink, hq_stream_t stream);
+int hq_ceiling_mfma(int64_t iters, float *sink, int64_t *flops, hq_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -152,6 +152,15 @@ extern "C" {
 const char *hq_last_error(void) { return g_err; }
 int hq_version(void) { return 100; }
 
+int hq_ceiling_read(const void *buf, int64_t bytes, int order, int depth, uint32_t *sink, hq_stream_t stream) {
+  return launch_ceiling_read(buf, bytes, order, depth, sink, resolve(stream));
+}
+
+int hq_ceiling_mfma(int64_t iters, float *sink, int64_t *flops, hq_stream_t stream) {
+  if (flops) *flops = ceiling_mfma_flops(iters);
+  return launch_ceiling_mfma(iters, sink, resolve(stream));
+}
+
 int hq_device_count(int *count) {
   if (!count) return fail(HQ_EINVAL, "hq_device_count", "count is NULL");
   return check(hipGetDeviceCount(count), "hipGetDeviceCount");

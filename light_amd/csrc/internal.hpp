@@ -73,6 +73,10 @@ size_t gemm_partial_bytes(int64_t M, int64_t N, int64_t K, bool f32_out);
 int launch_gemm_int4_bf16(const uint16_t *xb, const uint32_t *codes, const float *sc, const float *zr, void *out,
                           int out_dtype, float *partials, int64_t M, int64_t N, int64_t K, int G, hipStream_t s);
 int device_cus();
+// Ceiling measurements (ceiling.hip).
+int launch_ceiling_read(const void *buf, int64_t bytes, int order, int depth, uint32_t *sink, hipStream_t s);
+int launch_ceiling_mfma(int64_t iters, float *sink, hipStream_t s);
+int64_t ceiling_mfma_flops(int64_t iters);
 // Q4_K GEMV on F32 x quantized in LDS (M <= kGemvMaxRows); w1 != NULL: gated pair,
 // out = act(x.w0) * (x.w1), act 0 = SiLU, 1 = GELU (erf).
 // x: F32 x or prepared activations (16-byte aligned); w1 may be NULL.

@@ -148,9 +148,9 @@ def _int4_experts(g, E, N, K, G, dev):
 ])
 def test_moe_int4_vs_light_cpu(dev, T, E, topk, H, I, G, xdt):
     """hq_moe_int4 against the restated CPU MoEInt4 (oracle.moe_int4, ops/int4.go:284-343) and
-    an f64 dense block on the dequantized experts.  Bar: |y - y_ref| <= 5e-3 max_n |y_ref[t]|
-    per token (x and h are quantized to two-level int8 on the GPU; BF16 / F16 outputs add their
-    rounding)."""
+    an f64 dense block on the dequantized experts.  Bar (the north star's, for a combined MoE
+    output): |y[t, n] - ref[t, n]| <= 1e-3 * sum_j |w_j| ||W_dn[e_j]_n|| ||h_j|| for every
+    token and output, with h_j the f64 gated activations of slot j."""
     print(f"[case] moe_int4 T={T} E={E} topk={topk} H={H} I={I} G={G} x={xdt}", flush=True)
     g = synth.rng(3000 + T + H + I)
     gu_h, gu_d = _int4_experts(g, E, 2 * I, H, G, dev)
@@ -164,19 +164,25 @@ def test_moe_int4_vs_light_cpu(dev, T, E, topk, H, I, G, xdt):
     torch.cuda.synchronize()
     got = got.float().cpu().numpy()
     want = oracle.moe_int4(xw, gu_h, dn_h, ids, w, topk, G)
-    tol = 5e-3 if xdt == torch.float32 else 8e-3
+    # f64 dense on the dequantized experts, and the normaliser
+    ref = np.zeros((T, H))
+    norm = np.zeros((T, H))
+    wdn = {}
     for t in range(T):
-        scale = np.abs(want[t]).max() + 1e-30
-        assert np.max(np.abs(got[t] - want[t])) <= tol * scale, t
-    # f64 dense on the dequantized experts (first token)
-    ref = np.zeros(H)
-    for j in range(topk):
-        e = ids[j]
-        wg = oracle.int4_dequant(*gu_h[e], 2 * I, H, G).astype(np.float64)
-        wd = oracle.int4_dequant(*dn_h[e], H, I, G).astype(np.float64)
-        gg, uu = wg[:I] @ xw[0].astype(np.float64), wg[I:] @ xw[0].astype(np.float64)
-        ref += float(w[j]) * (wd @ (gg / (1 + np.exp(-gg)) * uu))
-    assert np.max(np.abs(got[0] - ref)) <= tol * (np.abs(ref).max() + 1e-30)
+        for j in range(topk):
+            e = ids[t * topk + j]
+            wg = oracle.int4_dequant(*gu_h[e], 2 * I, H, G).astype(np.float64)
+            if e not in wdn:
+                wdn[e] = oracle.int4_dequant(*dn_h[e], H, I, G).astype(np.float64)
+            gg, uu = wg[:I] @ xw[t].astype(np.float64), wg[I:] @ xw[t].astype(np.float64)
+            hj = gg / (1 + np.exp(-gg)) * uu
+            ref[t] += float(w[t * topk + j]) * (wdn[e] @ hj)
+            norm[t] += abs(float(w[t * topk + j])) * np.linalg.norm(wdn[e], axis=1) * np.linalg.norm(hj)
+    norm += 1e-30
+    err_cpu = np.max(np.abs(got - want) / norm)
+    err_f64 = np.max(np.abs(got - ref) / norm)
+    assert err_cpu <= 1e-3, f"vs Light CPU: {err_cpu:.3g}"
+    assert err_f64 <= 1e-3, f"vs f64: {err_f64:.3g}"
 
 
 @pytest.mark.parametrize("M,N,K,G", [(33, 1000, 1024, 128), (64, 18944, 3584, 128), (17, 300, 2048, 256)])
