@@ -1767,6 +1767,81 @@ int launch_gemv_q4kx(const float *x, const void *w0, const void *w1, float *out,
   });
 }
 
+// ---------------------------------------------------------------------------
+// Long-row GEMV on prepared activations at one token (the MLP's down projection, K = 14336):
+// one workgroup per CU, its rows requested early.
+//
+// A CU serves the memory requests of its workgroups roughly in issue order.  With two
+// persistent workgroups per CU (gemv_q4kx_kernel) the second one's first rows arrive only
+// after the first one's (per-workgroup clock stamps: first data at 2.5 us for workgroups
+// 0-255, 5.5 us for 256-511), and each later row group is requested only after a dot, so the
+// launch ends several latencies after its first data.  Here one workgroup per CU holds RW
+// teams of R rows each: every lane requests its unit's activations first (they gate every
+// dot), then D rows, and each dot refills its slot with the row D ahead (straight-line code:
+// the compiler's wait before each dot covers that row's loads only).  The teams' 16-lane sums
+// meet in LDS once, at the end.  Arithmetic and summation order are gemv_q4kx_kernel's (unit
+// dots, 16-lane sums, a team's rows added in order from zero), so the results are the same
+// bits.  4096 x 14336: 10.2 -> 8.8 us.
+// ---------------------------------------------------------------------------
+template <class U, int R, int D>
+__global__ __launch_bounds__(512) void gemv_rows_kernel(Q4kxArgs a) {
+  static_assert(D >= 1 && D <= R, "ring depth");
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int t = threadIdx.x, lane = t & 63;
+  const int team = t / a.TP, u = t - team * a.TP;
+  const bool active = u < a.P;
+  const typename U::Lane L = unit_lane<U>(active ? u : 0, a.G);
+  const int hpt = a.TP >> 4;
+  const int row0 = (blockIdx.x * a.RW + team) * R;
+  typename U::X xr[1];
+  U::load_x(a.ain, a.ain + a.in_q2, a.ain + a.in_d, a.ain + a.in_s, (int64_t)L.ja, xr[0]);
+  typename U::W wr[D];
+  auto load_row = [&](int r) __attribute__((always_inline)) {
+    int row = row0 + r;
+    row = row < a.N ? row : a.N;  // past the end: zeros, no traffic
+    U::load(a.w0, a.s0, a.z0, a, row, L, wr[r % D]);
+  };
+#pragma unroll
+  for (int r = 0; r < D; r++) load_row(r);
+  float *pp = reinterpret_cast<float *>(smem);  // [RW][R][hpt] 16-lane sums
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    float c[1];
+    U::template dot<1>(wr[r % D], xr, L, c);
+    if (r + D < R) load_row(r + D);
+    const float s16 = rsum16(active ? c[0] : 0.f);
+    if ((lane & 15) == 0) pp[(team * R + r) * hpt + (u >> 4)] = s16;
+  }
+  __syncthreads();
+  if (t < a.RW * R) {
+    const int tm = t / R, r = t - tm * R;
+    float acc = 0.f;
+    for (int k = 0; k < hpt; k++) acc += pp[(tm * R + r) * hpt + k];
+    const int row = (blockIdx.x * a.RW + tm) * R + r;
+    if (row < a.N) static_cast<float *>(a.out)[row] = acc;
+  }
+}
+
+// One token, teams wider than a wave (K > 4096) that fill a workgroup.
+static bool gemv_rows_ok(const Q4kxArgs &a) { return a.M == 1 && a.TP > 64 && a.TP * a.RW <= 512; }
+
+// R rows per team: as many as put one workgroup on every CU, at most 8 (4 in flight).
+template <class U>
+static int run_gemv_rows(const Q4kxArgs &a, hipStream_t s) {
+  const int64_t per = cdiv(a.N, (int64_t)a.RW * device_cus());
+  const int R = per >= 8 ? 8 : per >= 4 ? 4 : per >= 2 ? 2 : 1;
+  const size_t lds = (size_t)a.RW * R * (a.TP >> 4) * 4;
+  const dim3 grid((unsigned)cdiv(a.N, (int64_t)a.RW * R));
+  const int nt = a.TP * a.RW;
+  switch (R) {
+    case 8: gemv_rows_kernel<U, 8, 4><<<grid, nt, lds, s>>>(a); break;
+    case 4: gemv_rows_kernel<U, 4, 4><<<grid, nt, lds, s>>>(a); break;
+    case 2: gemv_rows_kernel<U, 2, 2><<<grid, nt, lds, s>>>(a); break;
+    default: gemv_rows_kernel<U, 1, 1><<<grid, nt, lds, s>>>(a); break;
+  }
+  return check_launch("gemv_rows");
+}
+
 int launch_gemv_q4kx_act(const void *act_in, const void *w, float *out, int64_t M, int64_t N, int64_t K, int dt,
                          hipStream_t s) {
   Q4kxArgs a;
@@ -1778,6 +1853,7 @@ int launch_gemv_q4kx_act(const void *act_in, const void *w, float *out, int64_t 
   // 10.6 us at 4096 x 14336; four rows, 130 registers, measured 12.2 us).
   return with_qk_unit(dt, K, [&](auto unit) {
     using U = decltype(unit);
+    if (gemv_rows_ok(a)) return run_gemv_rows<U>(a, s);
     if (a.TP > 64) return dispatch_q4kx<U, false, false, false, F32, F32, 2>(a, s);
     return dispatch_q4kx<U, false, false, false>(a, s);
   });
@@ -1900,6 +1976,135 @@ size_t matmul_q_gated_act_ws_bytes(int64_t M, int64_t N, int64_t K, int dt) {
   return (size_t)al256(4 * M * N) + matmul_q_gated_ws_bytes(M, N, K, dt);
 }
 
+// ---------------------------------------------------------------------------
+// The gated gate/up launch of the decode MLP at one token, K in (2048, 4096] (one wave per
+// row), with the quantized-h epilogue: one workgroup per CU owning whole 32-row chunks --
+// chunk bx and, with NCH = 2, chunk bx + G.
+//
+// Each wave reads rows 8 i + wave of its chunks, gate and up together.  x is requested first
+// (every dot waits for it), then the first row pair, and x is quantized into LDS while the
+// weights stream.  One row pair is in flight per wave while every CU streams its first chunk
+// and two during the second chunk (only the CUs that own two chunks are still streaming then):
+// measured against one, two, four, six and eight row pairs in flight throughout, this was the
+// fastest -- more requests in flight at once lengthen every request's latency more than they
+// add bandwidth, as a plain read shows too (hq_ceiling_read, depth 1-2 against 4-8).  The code
+// is straight-line, so the compiler's wait before each dot covers that row pair's loads only.
+// The arithmetic -- unit dots, 16-lane sums, the row sum order, act(g) * u, the chunk's
+// quantization -- is gemv_q4kx_kernel<U, 1, GATED, XIN, AOUT>'s, bit for bit.
+// 14336 x 4096: 15.2 -> 14.2-14.6 us.
+// ---------------------------------------------------------------------------
+template <class U, int NCH>
+__global__ __launch_bounds__(512) void gate_cu_kernel(Q4kxArgs a) {
+  constexpr int RC = 4, R = RC * NCH;  // row pairs per wave: 4 per chunk
+  static_assert(NCH == 1 || NCH == 2, "one or two chunks");
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int KB = a.K >> 5;
+  const bool active = lane < a.P;
+  const typename U::Lane L = unit_lane<U>(active ? lane : 0, a.G);
+  const int nch = a.N / 32;
+  const int c0 = blockIdx.x, c1 = NCH > 1 ? blockIdx.x + (int)gridDim.x : nch;
+  auto row_of = [&](int i) __attribute__((always_inline)) {
+    const int c = i < RC ? c0 : c1;
+    return c < nch ? c * 32 + 8 * (i % RC) + wave : a.N;  // past the end: zeros, no traffic
+  };
+  typename U::W wg[2], wu[2];
+  auto load_row = [&](int i) __attribute__((always_inline)) {
+    const int row = row_of(i);
+    U::load(a.w0, a.s0, a.z0, a, row, L, wg[i & 1]);
+    U::load(a.w1, a.s1, a.z1, a, row, L, wu[i & 1]);
+  };
+
+  // x: one 16-element task per thread (K <= 4096: at most 256 tasks).
+  uint8_t *lq1 = smem, *lq2 = smem + a.K;
+  float2 *lde = reinterpret_cast<float2 *>(smem + 2 * a.K);
+  float *lsx = reinterpret_cast<float *>(smem + 2 * a.K + 8 * KB);
+  const int ntask = KB * 2;
+  const int task = t < ntask ? t : ntask - 1;
+  float v[16];
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const float4 f = reinterpret_cast<const float4 *>(static_cast<const float *>(a.x) + (int64_t)task * 16)[r];
+    v[4 * r] = f.x, v[4 * r + 1] = f.y, v[4 * r + 2] = f.z, v[4 * r + 3] = f.w;
+  }
+  load_row(0);
+  {
+    const ActQ16 q = act_quant16_fast(v);
+    if (t < ntask) {
+      const int blk = task >> 1, half = task & 1;
+      *reinterpret_cast<u32x4_t *>(lq1 + blk * 32 + half * 16) = u32x4_t{q.q1[0], q.q1[1], q.q1[2], q.q1[3]};
+      if constexpr (U::kX2)
+        *reinterpret_cast<u32x4_t *>(lq2 + blk * 32 + half * 16) = u32x4_t{q.q2[0], q.q2[1], q.q2[2], q.q2[3]};
+      if (half == 0) {
+        lde[blk] = make_float2(q.d, q.e);
+        lsx[blk] = q.sum;
+      }
+    }
+  }
+  __syncthreads();
+  typename U::X xr[1];
+  U::load_x(lq1, lq2, reinterpret_cast<const uint8_t *>(lde), reinterpret_cast<const uint8_t *>(lsx), L.ja, xr[0]);
+
+  float *hb = reinterpret_cast<float *>(smem + q4kx_act_lds(1, a.K));  // [NCH][32]
+#pragma unroll
+  for (int i = 0; i < R; i++) {
+    float cg[1], cu[1];
+    U::template dot<1>(wg[i & 1], xr, L, cg);
+    U::template dot<1>(wu[i & 1], xr, L, cu);
+    // Refill: the next row pair during the first chunk, the one after it (two in flight)
+    // from the first chunk's last row on.
+    if (i < RC - 1) {
+      load_row(i + 1);
+    } else if (i == RC - 1 && NCH > 1) {
+      load_row(RC);
+      load_row(RC + 1);
+    } else if (i + 2 < R) {
+      load_row(i + 2);
+    }
+    const float g16 = rsum16(active ? cg[0] : 0.f), u16 = rsum16(active ? cu[0] : 0.f);
+    const float tg = ((rl(g16, 0) + rl(g16, 16)) + rl(g16, 32)) + rl(g16, 48);
+    const float tu = ((rl(u16, 0) + rl(u16, 16)) + rl(u16, 32)) + rl(u16, 48);
+    const int row = row_of(i);
+    if (lane == 0 && row < a.N) {
+      const float y = gate_act(tg, a.act) * tu;
+      if (a.out) static_cast<float *>(a.out)[row] = y;
+      hb[(i / RC) * 32 + 8 * (i % RC) + wave] = y;
+    }
+  }
+  __syncthreads();
+  // Each chunk's 32 values into the act layout of (1, N): eight lanes per chunk.
+  if (t < 8 * NCH) {
+    const int ch = t >> 3, sub = t & 7, c = ch ? c1 : c0;
+    const float hv[4] = {hb[ch * 32 + sub * 4], hb[ch * 32 + sub * 4 + 1], hb[ch * 32 + sub * 4 + 2],
+                         hb[ch * 32 + sub * 4 + 3]};
+    const ActQ q = act_quant8_fast(hv);
+    if (c < nch) {
+      reinterpret_cast<uint32_t *>(a.aout + (int64_t)c * 32)[sub] = q.q1;
+      reinterpret_cast<uint32_t *>(a.aout + a.out_q2 + (int64_t)c * 32)[sub] = q.q2;
+      if (sub == 0) {
+        reinterpret_cast<float2 *>(a.aout + a.out_d)[c] = make_float2(q.d, q.e);
+        reinterpret_cast<float *>(a.aout + a.out_s)[c] = q.sum;
+      }
+    }
+  }
+}
+
+// One token, one wave per row, 8 teams (K in (2048, 4096]), whole chunks, at most two per CU.
+static bool gate_cu_ok(const Q4kxArgs &a) {
+  return a.M == 1 && a.TP == 64 && a.RW == 8 && a.P > 32 && a.N % 32 == 0 && a.N / 32 <= 2 * device_cus();
+}
+
+template <class U>
+static int run_gate_cu(const Q4kxArgs &a, hipStream_t s) {
+  const int nch = (int)(a.N / 32), cus = device_cus();
+  const size_t lds = (size_t)q4kx_act_lds(1, a.K) + 64 * 4;
+  if (nch > cus)
+    gate_cu_kernel<U, 2><<<(unsigned)cus, 512, lds, s>>>(a);
+  else
+    gate_cu_kernel<U, 1><<<(unsigned)nch, 512, lds, s>>>(a);
+  return check_launch("gate_cu");
+}
+
 // Gated projection whose output is written as prepared activations (act layout of (M, N)).
 // Q4_K / Q5_K, M <= 8, aligned, with teams that tile 32-row chunks: one kernel (the gated
 // GEMV quantizes its own 32-row output chunks in the epilogue).  Otherwise the gated
@@ -1915,7 +2120,11 @@ int launch_matmul_q_gated_act(const float *x, const void *wg, const void *wu, ui
     a.w1 = static_cast<const uint8_t *>(wu);
     a.aout = aout;
     a.act = act;
-    return with_qk_unit(dt, K, [&](auto unit) { return dispatch_q4kx<decltype(unit), true, true, true>(a, s); });
+    return with_qk_unit(dt, K, [&](auto unit) {
+      using U = decltype(unit);
+      if (gate_cu_ok(a)) return run_gate_cu<U>(a, s);
+      return dispatch_q4kx<U, true, true, true>(a, s);
+    });
   }
   float *h = static_cast<float *>(ws);
   void *inner = static_cast<char *>(ws) + al256(4 * M * N);
@@ -2353,3 +2562,4 @@ int launch_moe_int4(const void *x, int x_dtype, const void *const *tab, int64_t 
 }
 
 }  // namespace hq
+
