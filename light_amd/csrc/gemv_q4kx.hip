@@ -1412,6 +1412,250 @@ __global__ __launch_bounds__(512) void moe_block_kernel(MoeXArgs ma1, MoeCombArg
 }
 
 // ---------------------------------------------------------------------------
+// The MoE decode block for one token in one launch, one workgroup per CU (moe_block1_kernel):
+//  * every workgroup loads the router probabilities and x, routes the token (the top-k and
+//    the expert sort of route_in_workgroup) and quantizes x into LDS;
+//  * gate/up: workgroup b < topk * I / 32 owns slot b / (I / 32) and the 32-row block
+//    b % (I / 32) of that slot's gated rows -- all of its row loads go out right after the
+//    routing, R1 = 32 / RW1 rows per team -- writes act(g) * u as F32 h and quantizes the
+//    block into the act layout (agent-coherent stores: read by other workgroups);
+//  * down + MoECombine: workgroup b owns RPW output rows for all topk slots, as (row, slot)
+//    team tasks; their weights are requested before the grid barrier (the routing names the
+//    experts), h's act blocks are read agent-coherently after it into LDS, and each row's
+//    slot values are added in slot order.
+// With the previous layout (one 16-row group per workgroup, 384 of them on 256 CUs) the
+// second workgroup of a CU got its rows only after the first's, and h went out as F32 to be
+// quantized by every down workgroup after the barrier (per-workgroup clock stamps: gate/up
+// done at 6.5-11.4 us, h quantized 2.6 us after the barrier).  The arithmetic -- unit dots,
+// team sums, act(g) * u, h's quantization (act_quant8_fast on eight lanes per block), pair
+// values times the routing weight, the slot-order adds -- is that of hq_moe_route_gated
+// followed by hq_moe_gemm_q_combine, so every output is the same bits.  The grid barrier is
+// moe_block_kernel's (bounded wait; a workgroup that gives up writes NaN and raises the flag).
+// ---------------------------------------------------------------------------
+struct MoeBlock1Args {
+  Q4kxArgs ga;       // gate/up geometry: K = H, N = 2I (an expert's gate rows then up rows)
+  Q4kxArgs da;       // down geometry: K = I, N = H
+  MoeXArgs ra;       // routing (probs, E, topk, normalize, outputs)
+  const uint8_t *wgu, *wdn;
+  float *h;          // (topk, I) F32
+  uint8_t *hact;     // act layout of (topk, I), agent-coherent
+  float *y;          // (1, H)
+  int64_t gu_bytes, dn_bytes;  // bytes per expert
+  int I, H, topk, act, rpw;
+};
+
+template <class U, int R1, int NR>
+__global__ __launch_bounds__(512) void moe_block1_kernel(MoeBlock1Args b, uint32_t *bar, uint32_t limit,
+                                                         uint32_t *host_flag) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  __shared__ int r_e[64], r_se[64], r_sp[64], r_ok;
+  __shared__ float r_w[64];
+  const int t = threadIdx.x, lane = t & 63;
+  const int id = (int)blockIdx.x, G = (int)gridDim.x;
+  const int topk = b.topk, I = b.I;
+  uint32_t gen = 0;
+  if (t == 0) gen = __hip_atomic_load(&bar[64 * (17 + id % kBarSub)], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+  // x (one row of H) requested first; quantized into LDS after the gate/up loads go out.
+  const Q4kxArgs &ga = b.ga;
+  const int KB1 = ga.K >> 5, ntask1 = KB1 * 8;  // eight lanes per 32-block (act_quant8_fast)
+  constexpr int XT = 2;
+  float4 xv[XT];
+#pragma unroll
+  for (int i = 0; i < XT; i++) {
+    const int task = i * 512 + t < ntask1 ? i * 512 + t : ntask1 - 1;
+    xv[i] = reinterpret_cast<const float4 *>(ga.x)[task];
+  }
+  route_in_workgroup(b.ra, r_e, r_w, r_se, r_sp);
+  if (id == 0) {
+    for (int i = t; i < topk; i += 512) {
+      b.ra.topk_ids[i] = r_e[i];
+      b.ra.weights_out[i] = r_w[i];
+      b.ra.sorted_pairs_out[i] = r_sp[i];
+      b.ra.sorted_expts_out[i] = r_se[i];
+    }
+    if (b.ra.counts && b.ra.offsets) {
+      // counts / offsets of the expert-sorted pairs: an exclusive scan over the sorted ids.
+      for (int e = t; e <= b.ra.E; e += 512) {
+        int lo = 0, cnt = 0;
+        for (int i = 0; i < topk; i++) {
+          lo += r_se[i] < e ? 1 : 0;
+          cnt += r_se[i] == e ? 1 : 0;
+        }
+        b.ra.offsets[e] = lo;
+        if (e < b.ra.E) b.ra.counts[e] = cnt;
+      }
+    }
+  }
+
+  // ---- gate / up: slot s, 32-row block j ----
+  const int nblk = I / 32, gwg = topk * nblk;
+  const int team1 = t / ga.TP, u1 = t - team1 * ga.TP;
+  const bool act1 = u1 < ga.P;
+  const typename U::Lane L1 = unit_lane<U>(act1 ? u1 : 0, ga.G);
+  const bool gwork = id < gwg;
+  const int gs = gwork ? id / nblk : 0, gj = gwork ? id % nblk : 0;
+  int ge = r_e[gs];
+  const bool gok = gwork && ge >= 0 && ge < b.ra.E;
+  ge = gok ? ge : 0;
+  const uint8_t *wgu = b.wgu + (int64_t)ge * b.gu_bytes;
+  typename U::W wg[R1], wu[R1];
+#pragma unroll
+  for (int i = 0; i < R1; i++) {
+    int row = gj * 32 + team1 + ga.RW * i;
+    row = gok && team1 < ga.RW ? row : ga.N;  // no work: row N, zeros, no traffic
+    U::load(wgu, ga.s0, ga.z0, ga, row, L1, wg[i]);
+    U::load(wgu, ga.s0, ga.z0, ga, row < ga.N ? row + I : ga.N, L1, wu[i]);
+  }
+  // x into LDS (two-level act layout of one row)
+  uint8_t *lq1 = smem, *lq2 = smem + ga.K;
+  float2 *lde = reinterpret_cast<float2 *>(smem + 2 * ga.K);
+  float *lsx = reinterpret_cast<float *>(smem + 2 * ga.K + 8 * KB1);
+#pragma unroll
+  for (int i = 0; i < XT; i++) {
+    const int task = i * 512 + t;
+    if (i * 512 >= ntask1) break;
+    const int tc = task < ntask1 ? task : ntask1 - 1;
+    const int blk = tc >> 3, sub = tc & 7;
+    const float v[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
+    const ActQ q = act_quant8_fast(v);
+    if (task < ntask1) {
+      reinterpret_cast<uint32_t *>(lq1 + blk * 32)[sub] = q.q1;
+      reinterpret_cast<uint32_t *>(lq2 + blk * 32)[sub] = q.q2;
+      if (sub == 0) {
+        lde[blk] = make_float2(q.d, q.e);
+        lsx[blk] = q.sum;
+      }
+    }
+  }
+  __syncthreads();
+  float *hb = reinterpret_cast<float *>(smem + q4kx_act_lds(1, ga.K));  // [32]
+  if (gwork) {
+    typename U::X xr[1];
+    U::load_x(lq1, lq2, reinterpret_cast<const uint8_t *>(lde), reinterpret_cast<const uint8_t *>(lsx), L1.ja, xr[0]);
+#pragma unroll
+    for (int i = 0; i < R1; i++) {
+      float cg[1], cu[1];
+      U::template dot<1>(wg[i], xr, L1, cg);
+      U::template dot<1>(wu[i], xr, L1, cu);
+      const float g16 = rsum16(act1 ? cg[0] : 0.f), u16 = rsum16(act1 ? cu[0] : 0.f);
+      const float g0 = rl(g16, 0), g1 = rl(g16, 16), g2 = rl(g16, 32), g3 = rl(g16, 48);
+      const float v0 = rl(u16, 0), v1 = rl(u16, 16), v2 = rl(u16, 32), v3 = rl(u16, 48);
+      float tg, tu;
+      if (ga.TP == 64) {
+        tg = ((g0 + g1) + g2) + g3;
+        tu = ((v0 + v1) + v2) + v3;
+      } else if (ga.TP == 32) {
+        tg = lane < 32 ? g0 + g1 : g2 + g3;
+        tu = lane < 32 ? v0 + v1 : v2 + v3;
+      } else {
+        tg = lane < 16 ? g0 : (lane < 32 ? g1 : (lane < 48 ? g2 : g3));
+        tu = lane < 16 ? v0 : (lane < 32 ? v1 : (lane < 48 ? v2 : v3));
+      }
+      const int r = team1 + ga.RW * i;
+      if (u1 == 0 && team1 < ga.RW && r < 32) hb[r] = gok ? gate_act(tg, b.act) * tu : 0.f;
+    }
+  }
+  __syncthreads();
+  if (gwork && t < 8) {
+    const float v[4] = {hb[t * 4], hb[t * 4 + 1], hb[t * 4 + 2], hb[t * 4 + 3]};
+    const ActQ q = act_quant8_fast(v);
+    const int64_t blk = (int64_t)gs * nblk + gj;
+    const int64_t q2 = act_q2_off(topk, I), dof = act_d_off(topk, I), sof = act_s_off(topk, I);
+    auto st = [&](int64_t off, uint32_t val) __attribute__((always_inline)) {
+      __hip_atomic_store(reinterpret_cast<uint32_t *>(b.hact + off), val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+    st(blk * 32 + 4 * t, q.q1);
+    st(q2 + blk * 32 + 4 * t, q.q2);
+    if (t == 0) {
+      st(dof + 8 * blk, __float_as_uint(q.d));
+      st(dof + 8 * blk + 4, __float_as_uint(q.e));
+      st(sof + 4 * blk, __float_as_uint(q.sum));
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's act stores are complete
+  __syncthreads();
+  if (t == 0) bar_arrive(bar, id, G, gen);
+  // F32 h (an output of the call, read by no other workgroup) after the arrival.
+  if (gwork && t < 32) b.h[(int64_t)gs * I + gj * 32 + t] = hb[t];
+
+  // ---- down + combine: rows id * rpw .. + rpw, every slot ----
+  const Q4kxArgs &da = b.da;
+  const int team2 = t / da.TP, u2 = t - team2 * da.TP;
+  const bool act2 = u2 < da.P;
+  const typename U::Lane L2 = unit_lane<U>(act2 ? u2 : 0, da.G);
+  const int slot = team2 % topk;
+  int de_ = r_e[slot];
+  const bool dok = de_ >= 0 && de_ < b.ra.E;
+  de_ = dok ? de_ : 0;
+  const uint8_t *wdn = b.wdn + (int64_t)de_ * b.dn_bytes;
+  const int ntasks = b.rpw * topk;
+  typename U::W wd[NR];
+#pragma unroll
+  for (int i = 0; i < NR; i++) {
+    const int k = team2 + da.RW * i;  // task: (row k / topk, slot k % topk)
+    int row = id * b.rpw + k / topk;
+    row = k < ntasks && team2 < da.RW && row < da.N ? row : da.N;
+    U::load(wdn, da.s0, da.z0, da, row, L2, wd[i]);
+  }
+  const bool h_ok = BarWait{bar, gen, id, limit, host_flag, &r_ok}();
+  // h's act blocks of every slot into LDS (the LDS act layout of (topk, I)), agent-coherently.
+  {
+    const int KB2 = I >> 5;
+    const int64_t gq2 = act_q2_off(topk, I), gd = act_d_off(topk, I), gsx = act_s_off(topk, I);
+    const int nq = topk * I / 16;  // 16-byte pieces of q1 (and of q2)
+    const __amdgpu_buffer_rsrc_t hr = span_rsrc(b.hact, (uint32_t)act_bytes(topk, I));
+    uint8_t *d1 = smem, *d2 = smem + (int64_t)topk * I;
+    uint8_t *dd = smem + 2 * (int64_t)topk * I, *ds = dd + 8 * (int64_t)topk * KB2;
+    for (int i = t; i < nq; i += 512) {
+      *reinterpret_cast<u32x4_t *>(d1 + 16 * i) = __builtin_amdgcn_raw_buffer_load_b128(hr, (uint32_t)(16 * i), 0, 16);
+      *reinterpret_cast<u32x4_t *>(d2 + 16 * i) =
+          __builtin_amdgcn_raw_buffer_load_b128(hr, (uint32_t)(gq2 + 16 * i), 0, 16);
+    }
+    for (int i = t; i < topk * KB2; i += 512) {
+      reinterpret_cast<uint32_t *>(dd)[2 * i] = __builtin_amdgcn_raw_buffer_load_b32(hr, (uint32_t)(gd + 8 * i), 0, 16);
+      reinterpret_cast<uint32_t *>(dd)[2 * i + 1] =
+          __builtin_amdgcn_raw_buffer_load_b32(hr, (uint32_t)(gd + 8 * i + 4), 0, 16);
+      reinterpret_cast<uint32_t *>(ds)[i] = __builtin_amdgcn_raw_buffer_load_b32(hr, (uint32_t)(gsx + 4 * i), 0, 16);
+    }
+  }
+  __syncthreads();
+  typename U::X xr2[1];
+  {
+    const int KB2 = I >> 5;
+    U::load_x(smem, smem + (int64_t)topk * I, smem + 2 * (int64_t)topk * I,
+              smem + 2 * (int64_t)topk * I + 8 * (int64_t)topk * KB2, (int64_t)slot * KB2 + L2.ja, xr2[0]);
+  }
+  float *vb = reinterpret_cast<float *>(smem + q4kx_act_lds(topk, I));  // [rpw][topk]
+  const float wp = r_w[slot];
+#pragma unroll
+  for (int i = 0; i < NR; i++) {
+    float c[1];
+    U::template dot<1>(wd[i], xr2, L2, c);
+    const float r16 = rsum16(act2 ? c[0] : 0.f);
+    const float r0 = rl(r16, 0), r1 = rl(r16, 16), r2 = rl(r16, 32), r3 = rl(r16, 48);
+    float tot;
+    if (da.TP == 64)
+      tot = ((r0 + r1) + r2) + r3;
+    else if (da.TP == 32)
+      tot = lane < 32 ? r0 + r1 : r2 + r3;
+    else
+      tot = lane < 16 ? r0 : (lane < 32 ? r1 : (lane < 48 ? r2 : r3));
+    const int k = team2 + da.RW * i;
+    if (u2 == 0 && team2 < da.RW && k < ntasks) vb[k] = dok ? tot * wp : 0.f;
+  }
+  __syncthreads();
+  if (t < b.rpw) {
+    const int row = id * b.rpw + t;
+    if (row < da.N) {
+      float acc = vb[t * topk];
+      for (int s2 = 1; s2 < topk; s2++) acc = __fadd_rn(acc, vb[t * topk + s2]);
+      b.y[row] = h_ok ? acc : __builtin_nanf("");
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // MoEInt4 (ops/int4.go:149-300): the routed gated-MLP expert block with 4-bit (GPTQ / AWQ,
 // canonical quant.Int4) experts.  Each expert is a separate quant.Int4, so the kernels read
 // per-expert (codes, scales, zeros) pointers from device tables, and only the routed experts'
@@ -2380,10 +2624,59 @@ void moe_block_set_spin_limit(uint32_t limit) {
 // MoERoute + gated gate/up + down + MoECombine for one token in one launch; returns 1 (and
 // launches nothing) where it does not apply: Q4_K / Q5_K, T = 1, the route_gated and
 // down-combine geometries, and a grid that fits the device at once.
+// The one-workgroup-per-CU block (moe_block1_kernel); returns 1 where it does not apply.
+static int launch_moe_block1(const MoeXArgs &ra, const Q4kxArgs &da0, const uint8_t *wgu, const uint8_t *wdn, float *h,
+                             uint8_t *hact, float *y, int64_t H, int64_t I, int topk, int act, int dt, uint32_t *bar,
+                             uint32_t limit, uint32_t *host_flag, hipStream_t s) {
+  constexpr int kNo = 1;
+  MoeBlock1Args b;
+  b.ra = ra;
+  b.ga = ra.g;
+  b.ga.N = (int)(2 * I);  // an expert's gate rows then its up rows
+  b.da = da0;
+  const int G = device_cus();
+  const int TP1 = b.ga.TP, RW1 = b.ga.RW, TP2 = b.da.TP, RW2 = b.da.RW;
+  if (TP1 > 64 || 32 % RW1 || I % 32 || TP2 > 64 || RW2 % topk || H > 4096) return kNo;
+  if (topk * (I / 32) > G || ((uintptr_t)ra.g.x & 15)) return kNo;
+  const int rpw = (int)cdiv(H, G);
+  const int nr = (int)cdiv((int64_t)rpw * topk, RW2), r1 = 32 / RW1;
+  if (nr > 4 || nr == 3) return kNo;
+  const size_t lds = std::max((size_t)q4kx_act_lds(1, H) + 32 * 4, (size_t)q4kx_act_lds(topk, I) + 4 * (size_t)rpw * topk);
+  if (lds > 64 * 1024) return kNo;
+  b.wgu = wgu;
+  b.wdn = wdn;
+  b.h = h;
+  b.hact = hact;
+  b.y = y;
+  b.gu_bytes = 2 * I * b.ga.row_bytes;
+  b.dn_bytes = H * b.da.row_bytes;
+  b.I = (int)I;
+  b.H = (int)H;
+  b.topk = topk;
+  b.act = act;
+  b.rpw = rpw;
+  auto launch = [&](auto unit) {
+    using U = decltype(unit);
+    auto go = [&](auto R1c, auto NRc) {
+      moe_block1_kernel<U, decltype(R1c)::value, decltype(NRc)::value><<<(unsigned)G, 512, lds, s>>>(b, bar, limit,
+                                                                                                     host_flag);
+      return check_launch("moe_block1");
+    };
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I4 = std::integral_constant<int, 4>;
+    if (r1 == 1) return nr == 1 ? go(I1{}, I1{}) : nr == 2 ? go(I1{}, I2{}) : go(I1{}, I4{});
+    if (r1 == 2) return nr == 1 ? go(I2{}, I1{}) : nr == 2 ? go(I2{}, I2{}) : go(I2{}, I4{});
+    if (r1 == 4) return nr == 1 ? go(I4{}, I1{}) : nr == 2 ? go(I4{}, I2{}) : go(I4{}, I4{});
+    return kNo;
+  };
+  return dt == Q5_K ? launch(Q5kUnit{}) : launch(Q4kUnit{});
+}
+
 int launch_moe_block(const float *probs, const float *x, const void *wgu, const void *wdn, float *h, float *y,
                      int64_t T, int64_t E, int topk, int normalize, int64_t H, int64_t I, int dt, int act,
                      int64_t *topk_ids, float *weights, int64_t *sorted_pairs, int64_t *sorted_expts,
-                     int32_t *counts, int32_t *offsets, hipStream_t s) {
+                     int32_t *counts, int32_t *offsets, uint8_t *hact, hipStream_t s) {
   constexpr int kNo = 1;
   if (T != 1 || (dt != Q4_K && dt != Q5_K) || topk > 64) return kNo;
   if (!moe_route_gated_ok(T, E, topk, H, dt, wgu, x) || !moe_comb_ok(topk, T, topk, I, dt, wdn, h)) return kNo;
@@ -2447,6 +2740,11 @@ int launch_moe_block(const float *probs, const float *x, const void *wgu, const 
   ma2.E = (int)E;
   ma2.topk = topk;
   if (ma1.g.TP * ma1.g.RW > 512 || ma2.g.TP * ma2.g.RW > 512) return kNo;
+  if (hact) {
+    const int rc1 = launch_moe_block1(ma1, ma2.g, static_cast<const uint8_t *>(wgu), static_cast<const uint8_t *>(wdn),
+                                      h, hact, y, H, I, topk, act, dt, bar, limit, host_flag, s);
+    if (rc1 != kNo) return rc1;
+  }
   // Gate/up grid as run_moe_x sizes it; the down projection's row groups over the same grid.
   const int64_t nseg = M < E ? M : E;
   const int ngroups1 = (ma1.g.N + ma1.g.RW - 1) / ma1.g.RW;

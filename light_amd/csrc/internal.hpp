@@ -157,7 +157,7 @@ int launch_moe_route_gated(const float *probs, const float *x, const void *w, fl
 int launch_moe_block(const float *probs, const float *x, const void *wgu, const void *wdn, float *h, float *y,
                      int64_t T, int64_t E, int topk, int normalize, int64_t H, int64_t I, int dt, int act,
                      int64_t *topk_ids, float *weights, int64_t *sorted_pairs, int64_t *sorted_expts,
-                     int32_t *counts, int32_t *offsets, hipStream_t s);
+                     int32_t *counts, int32_t *offsets, uint8_t *hact, hipStream_t s);
 size_t moe_block_ws_bytes(int64_t T, int topk, int64_t E, int64_t H, int64_t I, int dt);
 int moe_block_check(hipStream_t s, const char *call);
 void moe_block_set_spin_limit(uint32_t limit);

@@ -358,8 +358,12 @@ int launch_moe_block_any(const float *probs, const float *x, const void *wgu, co
                          int64_t T, int64_t E, int topk, int normalize, int64_t H, int64_t I, int dt, int act,
                          int64_t *topk_ids, float *weights, int64_t *sorted_pairs, int64_t *sorted_expts,
                          int32_t *counts, int32_t *offsets, void *ws, hipStream_t s) {
+  // The one-launch kernels use the front of the workspace for h's act blocks (act_bytes(topk, I),
+  // well inside the two-launch path's share).
+  uint8_t *hact = moe_block_ws_bytes(T, topk, E, H, I, dt) >= (size_t)act_bytes(T * topk, I) + 256
+                      ? static_cast<uint8_t *>(ws) : nullptr;
   const int rc = launch_moe_block(probs, x, wgu, wdn, h, y, T, E, topk, normalize, H, I, dt, act, topk_ids, weights,
-                                  sorted_pairs, sorted_expts, counts, offsets, s);
+                                  sorted_pairs, sorted_expts, counts, offsets, hact, s);
   if (rc != 1) return rc;
   if (!counts || !offsets) {
     const size_t tail = std::max(moe_route_gated_ws_bytes(T, topk, E, I, H, dt), moe_combine_ws_bytes(T * topk, E, H, I, dt));
