@@ -1996,6 +1996,113 @@ static int q4kx_setup(Q4kxArgs &a, int64_t M, int64_t N, int64_t K, int kblock, 
   return 0;
 }
 
+// ---------------------------------------------------------------------------
+// One-token GEMV (plain, or gated with F32 output) on x quantized in the kernel, K in
+// (2048, 4096] (one wave per row): one workgroup per CU over a contiguous range of
+// N / C rows, x requested first and quantized into LDS while the first rows stream, D rows
+// (pairs, gated) in flight per wave, straight-line code.  The arithmetic is
+// gemv_q4kx_kernel<U, 1, GATED, XIN = true, AOUT = false, XDT, ODT>'s, bit for bit.
+// ---------------------------------------------------------------------------
+template <class U, bool GATED, int R, int D, int XDT, int ODT>
+__global__ __launch_bounds__(512) void gemv_cu_kernel(Q4kxArgs a) {
+  static_assert(D >= 1 && D <= R, "ring depth");
+  constexpr int NW = GATED ? 2 : 1;
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int KB = a.K >> 5;
+  const bool active = lane < a.P;
+  const typename U::Lane L = unit_lane<U>(active ? lane : 0, a.G);
+  const int C = (int)gridDim.x, b = (int)blockIdx.x;
+  const int rs = (int)((int64_t)b * a.N / C), re = (int)((int64_t)(b + 1) * a.N / C);
+  auto row_of = [&](int i) __attribute__((always_inline)) {
+    const int r = rs + 8 * i + wave;
+    return r < re ? r : a.N;  // past the range: row N, zeros, no traffic
+  };
+  typename U::W wr[D][NW];
+  auto load_row = [&](int i) __attribute__((always_inline)) {
+    const int row = row_of(i);
+    U::load(a.w0, a.s0, a.z0, a, row, L, wr[i % D][0]);
+    if constexpr (GATED) U::load(a.w1, a.s1, a.z1, a, row, L, wr[i % D][NW - 1]);
+  };
+  // x: one 16-element task per thread (K <= 4096: at most 256 tasks).
+  const int ntask = KB * 2;
+  const int task = t < ntask ? t : ntask - 1;
+  constexpr int XR = XDT == F32 ? 4 : 2;
+  u32x4_t raw[XR];
+  {
+    const uint8_t *xp = static_cast<const uint8_t *>(a.x) + (int64_t)task * 16 * (XDT == F32 ? 4 : 2);
+#pragma unroll
+    for (int r = 0; r < XR; r++) raw[r] = *reinterpret_cast<const u32x4_t *>(xp + 16 * r);
+  }
+#pragma unroll
+  for (int i = 0; i < D; i++) load_row(i);
+  uint8_t *lq1 = smem, *lq2 = smem + a.K;
+  float2 *lde = reinterpret_cast<float2 *>(smem + 2 * a.K);
+  float *lsx = reinterpret_cast<float *>(smem + 2 * a.K + 8 * KB);
+  {
+    float v[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+      const uint32_t w32 = raw[XDT == F32 ? j / 4 : j / 8][XDT == F32 ? j % 4 : (j % 8) / 2];
+      if constexpr (XDT == F32)
+        v[j] = __uint_as_float(w32);
+      else
+        v[j] = XDT == BF16 ? bf2f((j & 1) ? w32 >> 16 : w32 & 0xffffu) : h2f((j & 1) ? w32 >> 16 : w32 & 0xffffu);
+    }
+    const ActQ16 q = act_quant16_fast(v);
+    if (t < ntask) {
+      const int blk = task >> 1, half = task & 1;
+      *reinterpret_cast<u32x4_t *>(lq1 + blk * 32 + half * 16) = u32x4_t{q.q1[0], q.q1[1], q.q1[2], q.q1[3]};
+      if constexpr (U::kX2)
+        *reinterpret_cast<u32x4_t *>(lq2 + blk * 32 + half * 16) = u32x4_t{q.q2[0], q.q2[1], q.q2[2], q.q2[3]};
+      if (half == 0) {
+        lde[blk] = make_float2(q.d, q.e);
+        lsx[blk] = q.sum;
+      }
+    }
+  }
+  __syncthreads();
+  typename U::X xr[1];
+  U::load_x(lq1, lq2, reinterpret_cast<const uint8_t *>(lde), reinterpret_cast<const uint8_t *>(lsx), L.ja, xr[0]);
+#pragma unroll
+  for (int i = 0; i < R; i++) {
+    float tot[NW];
+#pragma unroll
+    for (int j = 0; j < NW; j++) {
+      float c[1];
+      U::template dot<1>(wr[i % D][j], xr, L, c);
+      const float r16 = rsum16(active ? c[0] : 0.f);
+      tot[j] = ((rl(r16, 0) + rl(r16, 16)) + rl(r16, 32)) + rl(r16, 48);
+    }
+    if (i + D < R) load_row(i + D);
+    const int row = row_of(i);
+    if (lane == 0 && row < a.N) {
+      const float y = GATED ? gate_act(tot[0], a.act) * tot[NW - 1] : tot[0];
+      store_out<ODT>(a.out, row, y);
+    }
+  }
+}
+
+// One token, one wave per row (K in (2048, 4096]), 8 to 16 rows per CU.  (At 56 rows per CU,
+// 14336 x 4096, the persistent kernel was measured faster: 8.6 against 8.9-9.9 us with one to
+// three rows in flight per wave; at 16 rows per CU, Q6_K_R 4096 x 4096, this one: 6.5 -> 5.8 us.)
+static bool gemv_cu_ok(const Q4kxArgs &a) {
+  return a.M == 1 && a.TP == 64 && a.RW == 8 && a.P > 32 && a.N >= 8 * device_cus() && a.N <= 16 * device_cus();
+}
+
+template <class U, bool GATED, int XDT, int ODT>
+static int run_gemv_cu(const Q4kxArgs &a, hipStream_t s) {
+  const int C = device_cus();
+  const int R = (int)cdiv(cdiv(a.N, C), 8);
+  const size_t lds = (size_t)q4kx_act_lds(1, a.K);
+  const dim3 grid((unsigned)C);
+  if (R <= 1)
+    gemv_cu_kernel<U, GATED, 1, 1, XDT, ODT><<<grid, 512, lds, s>>>(a);
+  else
+    gemv_cu_kernel<U, GATED, 2, 2, XDT, ODT><<<grid, 512, lds, s>>>(a);
+  return check_launch(GATED ? "gemv_cu_gated" : "gemv_cu");
+}
+
 int launch_gemv_q4kx(const float *x, const void *w0, const void *w1, float *out, int64_t M, int64_t N, int64_t K,
                      int act, int dt, hipStream_t s) {
   Q4kxArgs a;
@@ -2007,6 +2114,7 @@ int launch_gemv_q4kx(const float *x, const void *w0, const void *w1, float *out,
   a.act = act;
   return with_qk_unit(dt, K, [&](auto unit) {
     using U = decltype(unit);
+    if (gemv_cu_ok(a)) return w1 ? run_gemv_cu<U, true, F32, F32>(a, s) : run_gemv_cu<U, false, F32, F32>(a, s);
     return w1 ? dispatch_q4kx<U, true, true, false>(a, s) : dispatch_q4kx<U, false, true, false>(a, s);
   });
 }
@@ -2147,6 +2255,12 @@ int launch_gemv_int4x(const void *x, int x_dtype, const uint32_t *codes, const f
     }
   }
   a.x = x;
+  if (gemv_cu_ok(a)) switch (x_dtype) {
+      case F32: return run_gemv_cu<Int4Unit, false, F32, F32>(a, s);
+      case BF16: return run_gemv_cu<Int4Unit, false, BF16, BF16>(a, s);
+      case F16: return run_gemv_cu<Int4Unit, false, F16, F16>(a, s);
+      default: return fail(HQ_EUNSUPPORTED, "int4_gemv", "x dtype %d", x_dtype);
+    }
   switch (x_dtype) {
     case F32: return dispatch_q4kx<Int4Unit, false, true, false, F32, F32>(a, s);
     case BF16: return dispatch_q4kx<Int4Unit, false, true, false, BF16, BF16>(a, s);
