@@ -81,6 +81,9 @@ int hq_memcpy_d2d(void *dst, const void *src, size_t bytes, hq_stream_t stream);
 int hq_memset(void *dst, int value, size_t bytes, hq_stream_t stream);
 /* cudart stream helpers (internal/cudart/stream.go:12-60). */
 int hq_stream_create(hq_stream_t *stream);
+/* hq_stream_destroy waits for the stream to drain, frees the library workspace it used for
+ * calls with ws == NULL (graphs captured on it with ws == NULL must not be replayed after
+ * this), and destroys it. */
 int hq_stream_destroy(hq_stream_t stream);
 int hq_stream_synchronize(hq_stream_t stream);
 int hq_stream_set_current(hq_stream_t stream);

@@ -42,7 +42,12 @@ hipStream_t resolve(hq_stream_t s) { return s ? (hipStream_t)s : g_current; }
 // hq_workspace_release() (after a device synchronisation) or at process exit.
 static std::mutex g_ws_mu;
 static std::map<std::pair<int, hipStream_t>, std::pair<void *, size_t>> g_ws;
-static std::vector<std::pair<int, void *>> g_ws_retired;
+struct Retired {
+  int dev;
+  hipStream_t stream;
+  void *p;
+};
+static std::vector<Retired> g_ws_retired;
 
 int workspace(size_t bytes, hipStream_t stream, void **out, const char *call) {
   int dev = 0;
@@ -57,7 +62,7 @@ int workspace(size_t bytes, hipStream_t stream, void **out, const char *call) {
     size_t cap = bytes < (1u << 20) ? (1u << 20) : bytes + bytes / 4;
     void *p = nullptr;
     if (hipMalloc(&p, cap) != hipSuccess) return fail(HQ_ENOMEM, call, "workspace of %zu bytes", cap);
-    if (slot.first) g_ws_retired.push_back({dev, slot.first});
+    if (slot.first) g_ws_retired.push_back({dev, stream, slot.first});
     slot = {p, cap};
   }
   *out = slot.first;
@@ -74,7 +79,7 @@ int workspace_release() {
     if (!rc) rc = check(hipDeviceSynchronize(), "hipDeviceSynchronize");
     if (!rc) rc = check(hipFree(p), "hipFree");
   };
-  for (auto &r : g_ws_retired) drop(r.first, r.second);
+  for (auto &r : g_ws_retired) drop(r.dev, r.p);
   for (auto &kv : g_ws)
     if (kv.second.first) drop(kv.first.first, kv.second.first);
   if (!rc) {
@@ -82,6 +87,30 @@ int workspace_release() {
     g_ws.clear();
   }
   (void)hipSetDevice(cur);
+  return rc;
+}
+
+// Frees the workspace buffers (current and retired, on every device) of a stream that is
+// being destroyed, after the stream has drained.
+static int workspace_forget_stream(hipStream_t stream) {
+  std::lock_guard<std::mutex> lk(g_ws_mu);
+  int rc = HQ_OK;
+  for (auto it = g_ws.begin(); it != g_ws.end();) {
+    if (it->first.second == stream) {
+      if (it->second.first && !rc) rc = check(hipFree(it->second.first), "hipFree");
+      it = g_ws.erase(it);
+    } else {
+      ++it;
+    }
+  }
+  for (auto it = g_ws_retired.begin(); it != g_ws_retired.end();) {
+    if (it->stream == stream) {
+      if (!rc) rc = check(hipFree(it->p), "hipFree");
+      it = g_ws_retired.erase(it);
+    } else {
+      ++it;
+    }
+  }
   return rc;
 }
 
@@ -218,8 +247,13 @@ int hq_stream_create(hq_stream_t *stream) {
 
 int hq_stream_destroy(hq_stream_t stream) {
   if (!stream) return HQ_OK;
-  if ((hipStream_t)stream == g_current) g_current = nullptr;
-  return check(hipStreamDestroy((hipStream_t)stream), "hipStreamDestroy");
+  hipStream_t s = (hipStream_t)stream;
+  if (s == g_current) g_current = nullptr;
+  // The stream's library workspace goes with it (its last kernels have finished first).
+  if (int rc = check(hipStreamSynchronize(s), "hipStreamSynchronize")) return rc;
+  if (int rc = workspace_forget_stream(s)) return rc;
+  moe_block_forget_stream(s);
+  return check(hipStreamDestroy(s), "hipStreamDestroy");
 }
 
 int hq_stream_synchronize(hq_stream_t stream) {

@@ -2725,6 +2725,12 @@ int moe_block_check(hipStream_t s, const char *call) {
   return st ? moe_bar_take_failure(*st, call) : HQ_OK;
 }
 
+void moe_block_forget_stream(hipStream_t s) {
+  std::lock_guard<std::mutex> lk(g_bar_mu);
+  for (auto &st : g_bar)
+    if (st.init && st.owner == s) st.owner = nullptr;
+}
+
 void moe_block_set_spin_limit(uint32_t limit) {
   std::lock_guard<std::mutex> lk(g_bar_mu);
   g_bar_limit = limit;

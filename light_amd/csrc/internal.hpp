@@ -161,6 +161,8 @@ int launch_moe_block(const float *probs, const float *x, const void *wgu, const 
 size_t moe_block_ws_bytes(int64_t T, int topk, int64_t E, int64_t H, int64_t I, int dt);
 int moe_block_check(hipStream_t s, const char *call);
 void moe_block_set_spin_limit(uint32_t limit);
+// A stream that is being destroyed stops owning the one-launch MoE block's barrier.
+void moe_block_forget_stream(hipStream_t s);
 int launch_moe_block_any(const float *probs, const float *x, const void *wgu, const void *wdn, float *h, float *y,
                          int64_t T, int64_t E, int topk, int normalize, int64_t H, int64_t I, int dt, int act,
                          int64_t *topk_ids, float *weights, int64_t *sorted_pairs, int64_t *sorted_expts,

@@ -34,6 +34,10 @@ def _noalloc(x, w, N, K, dt):
     (hipq.Q8_0, (3, 4096, 4096), (1, 512, 10240)),        # staged GEMV, K > 8192: quantize into scratch
     (hipq.Q4_K, (512, 4096, 14336), (64, 2048, 4096)),    # MFMA GEMM: bf16 x and split-K partials in scratch
     (hipq.Q6_K, (96, 1024, 4096), (16, 512, 2048)),       # bf16 weight copy in scratch, then the GEMM
+    (hipq.Q5_K, (1, 4096, 4096), (12, 1024, 2048)),       # Q5_K GEMV, then the GEMM on a bf16 copy
+    (hipq.Q4_0, (2, 2048, 4096), (32, 512, 1024)),        # staged Q4_0 GEMV, then the GEMM
+    (hipq.Q4_K, (2, 1024, 12288), (1, 512, 9216)),        # K > 8192 at small M: x quantized into scratch
+    (hipq.Q5_K, (1, 2048, 10240), (3, 512, 8448)),
 ])
 def test_noalloc_matches_matmul_q(dev, dt, big, small):
     for i, (M, N, K) in enumerate((big, small)):
@@ -41,6 +45,18 @@ def test_noalloc_matches_matmul_q(dev, dt, big, small):
         x, w = _pair(dev, dt, M, N, K, 100 + i)
         want = hipq.matmul_q(x, w, N, K, dt)
         got = _noalloc(x, w, N, K, dt)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"call {i}: max diff {(got - want).abs().max().item():.3g}"
+
+
+def test_noalloc_q6k_r_matches_matmul_q(dev):
+    """Q6_K_R (repacked once by hq_repack_q6k) at decode and prefill sizes, two calls in a row."""
+    for i, (M, N, K) in enumerate(((1, 4096, 4096), (24, 1024, 2048))):
+        print(f"[case] noalloc dt=Q6_K_R M={M} N={N} K={K} call {i}", flush=True)
+        x, raw = _pair(dev, hipq.Q6_K, M, N, K, 200 + i)
+        w = hipq.repack_q6k(raw, N, K)
+        want = hipq.matmul_q(x, w, N, K, hipq.Q6_K_R)
+        got = _noalloc(x, w, N, K, hipq.Q6_K_R)
         torch.cuda.synchronize()
         assert torch.equal(got, want), f"call {i}: max diff {(got - want).abs().max().item():.3g}"
 
