@@ -2135,7 +2135,7 @@ int launch_gemv_q4kx(const float *x, const void *w0, const void *w1, float *out,
 // dots, 16-lane sums, a team's rows added in order from zero), so the results are the same
 // bits.  4096 x 14336: 10.2 -> 8.8 us.
 // ---------------------------------------------------------------------------
-template <class U, int R, int D>
+template <class U, int R, int D, int ODT = F32>
 __global__ __launch_bounds__(512) void gemv_rows_kernel(Q4kxArgs a) {
   static_assert(D >= 1 && D <= R, "ring depth");
   extern __shared__ __align__(16) uint8_t smem[];
@@ -2170,7 +2170,7 @@ __global__ __launch_bounds__(512) void gemv_rows_kernel(Q4kxArgs a) {
     float acc = 0.f;
     for (int k = 0; k < hpt; k++) acc += pp[(tm * R + r) * hpt + k];
     const int row = (blockIdx.x * a.RW + tm) * R + r;
-    if (row < a.N) static_cast<float *>(a.out)[row] = acc;
+    if (row < a.N) store_out<ODT>(a.out, row, acc);
   }
 }
 
@@ -2178,7 +2178,7 @@ __global__ __launch_bounds__(512) void gemv_rows_kernel(Q4kxArgs a) {
 static bool gemv_rows_ok(const Q4kxArgs &a) { return a.M == 1 && a.TP > 64 && a.TP * a.RW <= 512; }
 
 // R rows per team: as many as put one workgroup on every CU, at most 8 (4 in flight).
-template <class U>
+template <class U, int ODT = F32>
 static int run_gemv_rows(const Q4kxArgs &a, hipStream_t s) {
   const int64_t per = cdiv(a.N, (int64_t)a.RW * device_cus());
   const int R = per >= 8 ? 8 : per >= 4 ? 4 : per >= 2 ? 2 : 1;
@@ -2186,10 +2186,10 @@ static int run_gemv_rows(const Q4kxArgs &a, hipStream_t s) {
   const dim3 grid((unsigned)cdiv(a.N, (int64_t)a.RW * R));
   const int nt = a.TP * a.RW;
   switch (R) {
-    case 8: gemv_rows_kernel<U, 8, 4><<<grid, nt, lds, s>>>(a); break;
-    case 4: gemv_rows_kernel<U, 4, 4><<<grid, nt, lds, s>>>(a); break;
-    case 2: gemv_rows_kernel<U, 2, 2><<<grid, nt, lds, s>>>(a); break;
-    default: gemv_rows_kernel<U, 1, 1><<<grid, nt, lds, s>>>(a); break;
+    case 8: gemv_rows_kernel<U, 8, 4, ODT><<<grid, nt, lds, s>>>(a); break;
+    case 4: gemv_rows_kernel<U, 4, 4, ODT><<<grid, nt, lds, s>>>(a); break;
+    case 2: gemv_rows_kernel<U, 2, 2, ODT><<<grid, nt, lds, s>>>(a); break;
+    default: gemv_rows_kernel<U, 1, 1, ODT><<<grid, nt, lds, s>>>(a); break;
   }
   return check_launch("gemv_rows");
 }
@@ -2235,12 +2235,24 @@ int launch_gemv_int4x(const void *x, int x_dtype, const uint32_t *codes, const f
     a.ain = static_cast<const uint8_t *>(ws);
     // Two rows per team (15.0 -> 13.8 us at 3584 x 18944); rows of at least kX1MinK take
     // single-level activations.
+    if (a.TP > 64 && K >= kX1MinK && gemv_rows_ok(a)) switch (x_dtype) {
+        case F32: return run_gemv_rows<Int4UnitT<false>, F32>(a, s);
+        case BF16: return run_gemv_rows<Int4UnitT<false>, BF16>(a, s);
+        case F16: return run_gemv_rows<Int4UnitT<false>, F16>(a, s);
+        default: return fail(HQ_EUNSUPPORTED, "int4_gemv", "x dtype %d", x_dtype);
+      }
     if (a.TP > 64 && K >= kX1MinK) switch (x_dtype) {
       case F32: return dispatch_q4kx<Int4UnitT<false>, false, false, false, F32, F32, 2>(a, s);
       case BF16: return dispatch_q4kx<Int4UnitT<false>, false, false, false, F32, BF16, 2>(a, s);
       case F16: return dispatch_q4kx<Int4UnitT<false>, false, false, false, F32, F16, 2>(a, s);
       default: return fail(HQ_EUNSUPPORTED, "int4_gemv", "x dtype %d", x_dtype);
     }
+    if (a.TP > 64 && gemv_rows_ok(a)) switch (x_dtype) {
+        case F32: return run_gemv_rows<Int4Unit, F32>(a, s);
+        case BF16: return run_gemv_rows<Int4Unit, BF16>(a, s);
+        case F16: return run_gemv_rows<Int4Unit, F16>(a, s);
+        default: return fail(HQ_EUNSUPPORTED, "int4_gemv", "x dtype %d", x_dtype);
+      }
     if (a.TP > 64) switch (x_dtype) {
       case F32: return dispatch_q4kx<Int4Unit, false, false, false, F32, F32, 2>(a, s);
       case BF16: return dispatch_q4kx<Int4Unit, false, false, false, F32, BF16, 2>(a, s);

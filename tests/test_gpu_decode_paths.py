@@ -80,9 +80,13 @@ def test_cu_kernel_equals_persistent(dev, dt, N, K):
 
 
 @pytest.mark.parametrize("N,K,xdt", [(3584, 3584, torch.float16), (2048, 4096, torch.float32),
-                                     (4096, 2560, torch.bfloat16)])
+                                     (4096, 2560, torch.bfloat16),
+                                     # rows longer than a wave: gemv_rows_kernel (one and two levels)
+                                     (3584, 18944, torch.float16), (1000, 10240, torch.float32),
+                                     (2048, 6144, torch.bfloat16)])
 def test_int4_cu_kernel_equals_persistent(dev, N, K, xdt):
-    """int4 GEMV with x quantized in the kernel at 8-16 rows per CU: M = 1 against row 0 of M = 2."""
+    """int4 GEMV at one token (8-16 rows per CU with x quantized in the kernel, or rows longer
+    than a wave on prepared activations): M = 1 against row 0 of M = 2."""
     print(f"[case] decode paths int4 N={N} K={K} x={xdt}", flush=True)
     g = synth.rng(7400 + N + K)
     G = 128
