@@ -285,6 +285,11 @@ size_t int4_ws_bytes(int64_t M, int64_t N, int64_t K, int G, int x_dtype) {
 int launch_int4_matmul(const void *x, int x_dtype, const uint32_t *codes, const float *s, const float *z, void *y,
                        int64_t M, int64_t N, int64_t K, int G, void *ws, hipStream_t st) {
   if (N > INT32_MAX || K > INT32_MAX) return fail(HQ_EUNSUPPORTED, "int4_matmul", "N or K too large");
+  if (int4_gemm_ok(M, G) && i4cu_ok(M, N, K, G, x_dtype, x, codes)) {
+    // F16 x at M <= 64 with enough column tiles to fill the chip: one workgroup per CU over
+    // all of K, no split-K partials.
+    return launch_i4cu(static_cast<const uint16_t *>(x), codes, s, z, y, M, N, K, G, st);
+  }
   if (int4_gemm_ok(M, G) && i4f16_small_ok(M, N, K, G, x_dtype, x, codes)) {
     // F16 x at M <= 64: the exact-weight f16 MFMA kernel reads x as given.
     return launch_i4f16_small(static_cast<const uint16_t *>(x), codes, s, z, y,

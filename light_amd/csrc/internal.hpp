@@ -112,6 +112,9 @@ int launch_int4_from_gptq(const uint32_t *qw, const uint32_t *qz, const float *s
                           int64_t N, int group, bool v2, uint32_t *codes, float *s_out, float *z_out, hipStream_t s);
 int launch_int4_from_awq(const uint32_t *qw, const uint32_t *qz, const float *sc, int64_t K, int64_t N, int group,
                          uint32_t *codes, float *s_out, float *z_out, hipStream_t s);
+bool i4cu_ok(int64_t M, int64_t N, int64_t K, int G, int x_dtype, const void *x, const void *codes);
+int launch_i4cu(const uint16_t *x, const uint32_t *codes, const float *s, const float *z, void *y, int64_t M, int64_t N,
+                int64_t K, int G, hipStream_t st);
 bool i4f16_small_ok(int64_t M, int64_t N, int64_t K, int G, int x_dtype, const void *x, const void *codes);
 int launch_i4f16_small(const uint16_t *x, const uint32_t *codes, const float *s, const float *z, void *y,
                        float *partials, int64_t M, int64_t N, int64_t K, int G, hipStream_t st);

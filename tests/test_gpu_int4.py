@@ -184,6 +184,29 @@ def test_moe_int4_vs_light_cpu(dev, T, E, topk, H, I, G, xdt):
     assert err_f64 <= 1e-3, f"vs f64: {err_f64:.3g}"
 
 
+@pytest.mark.parametrize("M,N,K,G,kind", [
+    (24, 15400, 1024, 128, "light"),   # two 16-row x tiles, a 40-row last column tile
+    (40, 16000, 512, 256, "light"),    # four chunks over eight waves (some own none), G > 128
+    (9, 20480, 2048, 128, "light"),    # one x tile, rows past M clamped
+    (64, 15400, 768, 128, "frac"),     # non-integral zero points: the second FMA subtracts z s'
+    (64, 15400, 768, 128, "wide"),     # integral zero points beyond 64
+    (48, 15400, 1536, 128, "tiny"),    # scales 1e-7 .. 1e-4 in a row: the per-row exponent
+])
+def test_matmul_int4_f16_one_launch(dev, M, N, K, G, kind):
+    """F16 x, 8 < M <= 64, 80-row column tiles filling the chip: the one-launch kernel (one
+    workgroup per CU over all of K) against the f64 reference and Light's CPU path."""
+    rng = np.random.default_rng(M * 3 + N + K + G)
+    codes, s, z = light_int4(rng, N, K, G)
+    if kind == "frac":
+        z = (rng.random((N, K // G)) * 15).astype(np.float32)
+    elif kind == "wide":
+        z = rng.integers(60, 100, size=(N, K // G)).astype(np.float32)
+    elif kind == "tiny":
+        s = (10.0 ** rng.uniform(-7, -4, size=(N, K // G))).astype(np.float32)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    _check(dev, x, codes, s, z, G, hipq.F16)
+
+
 @pytest.mark.parametrize("M,N,K,G", [(33, 1000, 1024, 128), (64, 18944, 3584, 128), (17, 300, 2048, 256)])
 def test_matmul_int4_f16_split_k_streams_and_repeats(dev, M, N, K, G):
     """F16 x, 8 < M <= 64, split over K: matches the f64 reference, and repeated calls -- on the
