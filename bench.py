@@ -223,8 +223,10 @@ def ceilings(args, dev, step_us, kernel_bytes):
     """What the hardware sustains on this box, measured in this run (context for the roofline
     fractions, never their denominator): hq_ceiling_read, a plain streaming read launch of the
     step's kernel sizes and of the whole step's bytes, rotating over a 640 MB buffer (beyond
-    the 256 MB MALL), in two access orders with two 16-byte loads in flight per thread; and
-    hq_ceiling_mfma, back-to-back register-operand v_mfma_f32_32x32x16_bf16."""
+    the 256 MB MALL), in two access orders with two 16-byte loads in flight per thread, and
+    the 268 MB read once more as half cache lines; hq_ceiling_mfma, back-to-back
+    register-operand v_mfma_f32_32x32x16_bf16; and hq_ceiling_mix, how far a SIMD overlaps
+    MFMA and VALU work."""
     import ctypes
     import torch
     from light_amd import hipq
@@ -234,9 +236,9 @@ def ceilings(args, dev, step_us, kernel_bytes):
     sink = torch.zeros(64, dtype=torch.int32, device=dev)
     base = big.data_ptr()
 
-    def read_us(nbytes, order, n=60):
-        nbytes = nbytes // 256 * 256
-        nwin = big.numel() // nbytes
+    def read_us(nbytes, order, n=60, rotate=True):
+        nbytes = nbytes // 2048 * 2048
+        nwin = big.numel() // nbytes if rotate else 1
 
         def fn(i):
             hipq.check(L.hq_ceiling_read(ctypes.c_void_p(base + (i % nwin) * nbytes), nbytes, order, 2,
@@ -250,7 +252,16 @@ def ceilings(args, dev, step_us, kernel_bytes):
             us = read_us(nb, order)
             reads.append({"bytes": nb, "order": name, "loads_in_flight_per_thread": 2, "us": round(us, 2),
                           "GBs": round(nb / us / 1e3, 1), "frac": round(nb / us / 1e3 / HBM_PEAK_GBS, 4)})
-    best = {nb: min(r["us"] for r in reads if r["bytes"] == nb) for nb in sizes}
+    half = read_us(268435456, 2)
+    reads.append({"bytes": 268435456, "order": "half_lines", "loads_in_flight_per_thread": 2, "us": round(half, 2),
+                  "GBs": round(268435456 / half / 1e3, 1), "frac": round(268435456 / half / 1e3 / HBM_PEAK_GBS, 4)})
+    best = {nb: min(r["us"] for r in reads if r["bytes"] == nb and r["order"] != "half_lines") for nb in sizes}
+    # The same 16 MB read again and again: after the first launch it sits in the XCDs' L2s, so
+    # the CUs' request rate, not HBM, bounds it -- whole lines against half lines.
+    l2 = []
+    for order, name in ((0, "window"), (2, "half_lines")):
+        us = read_us(16 << 20, order, rotate=False)
+        l2.append({"bytes": 16 << 20, "order": name, "us": round(us, 2), "GBs": round((16 << 20) / us / 1e3, 1)})
     two = sum(best[nb] for nb in kernel_bytes)
     flops = ctypes.c_int64()
     sf = torch.zeros(16, device=dev)
@@ -259,15 +270,23 @@ def ceilings(args, dev, step_us, kernel_bytes):
     us = time_launches(lambda i: hipq.check(L.hq_ceiling_mfma(iters, ctypes.c_void_p(sf.data_ptr()),
                                                                ctypes.byref(flops), None)), 5, 1)
     tf = flops.value / us / 1e6
+    mix_iters = 4000
+    mix = [time_launches(lambda i, m=m: hipq.check(L.hq_ceiling_mix(m, mix_iters, ctypes.c_void_p(sf.data_ptr()), None)),
+                         5, 1) * 1e3 / mix_iters for m in (0, 1, 2)]
     del big
     torch.cuda.empty_cache()
     return {"read": reads,
+            "read_l2_resident": l2,
             "step_kernels_read_us": round(two, 2),
             "step_vs_read_ceiling": round(two / step_us, 4),
             "step_one_launch_read_us": best[sum(kernel_bytes)],
             "mfma_bf16": {"TFLOPS": round(tf, 1), "frac_of_peak": round(tf / 2500.0, 4),
                           "kernel": "4 independent v_mfma_f32_32x32x16_bf16 chains per wave, register operands, "
-                                    "2 waves per SIMD"}}
+                                    "2 waves per SIMD"},
+            "mfma_valu_mix": {"ns_per_round": {"mfma": round(mix[0], 2), "valu": round(mix[1], 2), "both": round(mix[2], 2)},
+                              "overlap": round((mix[0] + mix[1] - mix[2]) / min(mix[0], mix[1]), 3),
+                              "round": "20 v_mfma_f32_16x16x32_f16 and/or 80 v_pk_fma_f16 per wave, 2 waves per SIMD; "
+                                       "overlap 1 = the shorter hidden entirely, 0 = none"}}
 
 
 GEMM_SHAPES = ((512, 14336, 4096), (512, 4096, 14336))

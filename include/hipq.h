@@ -417,13 +417,18 @@ int hq_gather_cols(const void *x, const int64_t *idx, void *y, int64_t M, int64_
  * hq_ceiling_read: one launch that reads `bytes` (16-byte aligned) of `buf` with 16-byte
  * loads, `depth` (1, 2, 4 or 8) in flight per thread, two 512-thread workgroups per CU;
  * order 0 reads a contiguous window that moves through the buffer (grid stride), order 1
- * gives each workgroup its own contiguous slice.  `sink`: one device word (almost never
- * written).
+ * gives each workgroup its own contiguous slice, order 2 reads order 0's bytes as half cache
+ * lines (each load 16 rows x 64 bytes, the other halves a trip later; `bytes` a multiple of
+ * 2048).  `sink`: one device word (almost never written).
  * hq_ceiling_mfma: one launch of `iters` rounds of four independent
  * v_mfma_f32_32x32x16_bf16 per wave on register operands, two 256-thread workgroups per CU
- * (two waves per SIMD); *flops receives the launch's flop count. */
+ * (two waves per SIMD); *flops receives the launch's flop count.
+ * hq_ceiling_mix: one launch of `iters` rounds, one 512-thread workgroup per CU, of
+ * mode 0: 20 v_mfma_f32_16x16x32_f16, mode 1: 80 v_pk_fma_f16, mode 2: both (VALU block,
+ * then MFMA block) -- time(2) against time(0) + time(1) is how far a SIMD overlaps them. */
 int hq_ceiling_read(const void *buf, int64_t bytes, int order, int depth, uint32_t *sink, hq_stream_t stream);
 int hq_ceiling_mfma(int64_t iters, float *sink, int64_t *flops, hq_stream_t stream);
+int hq_ceiling_mix(int mode, int64_t iters, float *sink, hq_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -185,6 +185,10 @@ int hq_ceiling_read(const void *buf, int64_t bytes, int order, int depth, uint32
   return launch_ceiling_read(buf, bytes, order, depth, sink, resolve(stream));
 }
 
+int hq_ceiling_mix(int mode, int64_t iters, float *sink, hq_stream_t stream) {
+  return launch_ceiling_mix(mode, iters, sink, resolve(stream));
+}
+
 int hq_ceiling_mfma(int64_t iters, float *sink, int64_t *flops, hq_stream_t stream) {
   if (flops) *flops = ceiling_mfma_flops(iters);
   return launch_ceiling_mfma(iters, sink, resolve(stream));

@@ -77,6 +77,7 @@ int device_cus();
 int launch_ceiling_read(const void *buf, int64_t bytes, int order, int depth, uint32_t *sink, hipStream_t s);
 int launch_ceiling_mfma(int64_t iters, float *sink, hipStream_t s);
 int64_t ceiling_mfma_flops(int64_t iters);
+int launch_ceiling_mix(int mode, int64_t iters, float *sink, hipStream_t s);
 // Q4_K GEMV on F32 x quantized in LDS (M <= kGemvMaxRows); w1 != NULL: gated pair,
 // out = act(x.w0) * (x.w1), act 0 = SiLU, 1 = GELU (erf).
 // x: F32 x or prepared activations (16-byte aligned); w1 may be NULL.

@@ -99,6 +99,7 @@ SIGNATURES = {
     "hq_moe_block_q_check": (_I, [_P]),
     "hq_ceiling_read": (_I, [_P, _I64, _I, _I, _P, _P]),
     "hq_ceiling_mfma": (_I, [_I64, _P, _P, _P]),
+    "hq_ceiling_mix": (_I, [_I, _I64, _P, _P]),
     "hq_debug_moe_block_spin_limit": (None, [ctypes.c_uint32]),
     "hq_moe_route_gated": (_I, [_P, _P, _P, _P, _I64, _I64, _I, _I, _I64, _I64, _I, _I, _P, _P, _P, _P, _P, _P, _P,
                                 _SZ, _P]),
