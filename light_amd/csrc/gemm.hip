@@ -686,6 +686,8 @@ int launch_moe_gemm_q4k(const float *x, uint16_t *xh, float *xs, const void *w, 
     to_f16_rowscale_kernel<<<(unsigned)rows, 256, 0, s>>>(x, reinterpret_cast<_Float16 *>(xh), xs, K);
     if (int rc = check_launch("to_f16_rowscale")) return rc;
   }
+  if (moe_stream_ok(rows, size_m, N, K, gated_I))
+    return launch_moe_stream_q4k(xh, xs, w, pairs, offsets, topk_w, out, topk, size_m, E, N, K, rpp, gated_I, act, s);
   MoeGemmArgs ma = {};
   ma.g.x = xh;
   ma.g.w = static_cast<const uint8_t *>(w);

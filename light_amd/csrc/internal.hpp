@@ -78,6 +78,10 @@ int launch_ceiling_read(const void *buf, int64_t bytes, int order, int depth, ui
 int launch_ceiling_mfma(int64_t iters, float *sink, hipStream_t s);
 int64_t ceiling_mfma_flops(int64_t iters);
 int launch_ceiling_mix(int mode, int64_t iters, float *sink, hipStream_t s);
+bool moe_stream_ok(int64_t rows, int64_t size_m, int64_t N, int64_t K, int64_t gated_I);
+int launch_moe_stream_q4k(const uint16_t *xh, const float *xs, const void *w, const int64_t *pairs,
+                          const int32_t *offsets, const float *topk_w, float *out, int topk, int64_t size_m, int64_t E,
+                          int64_t N, int64_t K, int rpp, int64_t gated_I, int act, hipStream_t s);
 // Q4_K GEMV on F32 x quantized in LDS (M <= kGemvMaxRows); w1 != NULL: gated pair,
 // out = act(x.w0) * (x.w1), act 0 = SiLU, 1 = GELU (erf).
 // x: F32 x or prepared activations (16-byte aligned); w1 may be NULL.

@@ -94,7 +94,9 @@ def test_moe_gemm_q_light_shapes(dev, dt, E, weighted):
                                           (33, 64, 8, 256, 768), (200, 8, 2, 96, 256),
                                           # decode kernel: several chunks of pairs per expert; K=4096
                                           # (one-wave teams); K=5120 (falls back to the act GEMV)
-                                          (13, 4, 1, 72, 512), (3, 8, 2, 128, 4096), (2, 4, 2, 40, 5120)])
+                                          (13, 4, 1, 72, 512), (3, 8, 2, 128, 4096), (2, 4, 2, 40, 5120),
+                                          # MFMA path with N % 16 != 0: the tiled grouped GEMM
+                                          (64, 4, 2, 200, 512)])
 def test_moe_gemm_q4_k_shapes(dev, T, E, topk, N, K):
     g = synth.rng(T * 13 + E + N + K)
     w = synth.gguf_weight(hipq.Q4_K, E * N, K, g)
@@ -250,7 +252,8 @@ def test_moe_gated_decode_config(dev, act):
                                                  (hipq.Q4_K, 60, 4, 2, 96, 512, True),    # ragged gate/up tile, rpp
                                                  (hipq.Q4_K, 256, 32, 8, 768, 2048, False),  # configs[4] T = 256
                                                  (hipq.Q8_0, 4, 8, 2, 48, 256, False),    # generic + split
-                                                 (hipq.Q4_K, 2, 4, 2, 32, 5120, False)])  # K > 4096: fallback
+                                                 (hipq.Q4_K, 2, 4, 2, 32, 5120, False),  # K > 4096: fallback
+                                                 (hipq.Q4_K, 64, 4, 2, 40, 512, False)])  # I % 16 != 0: tiled GEMM
 def test_moe_gated_shapes(dev, dt, T, E, topk, I, K, rpp):
     _check_gated(dev, dt, T, E, topk, I, K, hipq.ACT_SILU, rpp)
 

@@ -110,7 +110,7 @@ def test_vgpr_operands(line, regs):
 
 
 @pytest.mark.skipif(not os.path.exists(vc.HIPCC), reason="hipcc not installed")
-@pytest.mark.parametrize("src", ["int4_small.hip", "gemm.hip", "int4_cu.hip"])
+@pytest.mark.parametrize("src", ["int4_small.hip", "gemm.hip", "int4_cu.hip", "moe_stream.hip"])
 def test_real_sources_are_clean(src):
     """The kernels that load from inline asm with hand-counted waits, compiled as the library
     is: no in-flight destination is touched, across blocks and loop back edges."""
