@@ -59,7 +59,7 @@ constexpr int NTH = 64 * NW;
 constexpr int DB = 2;              // weight chunks in each wave's register ring
 constexpr int XU = 2;              // x units (64 k) in each wave's LDS ring
 constexpr int RP = NR + 4;         // reduction row pitch (floats)
-constexpr int MAXSZ = 4096 / NTH;  // scale / zero loads per thread and array (NR * groups <= 4096)
+constexpr int RPW = NR / NW;       // weight rows per wave whose scales / zeros it stages
 
 struct I4CuArgs {
   const uint16_t *x;      // f16 (M, K)
@@ -135,16 +135,16 @@ __global__ __launch_bounds__(NTH) void int4_cu_kernel(I4CuArgs a) {
   const int clast = n > 0 ? ce - 1 : 0;  // loads past the range are clamped here
   auto chunk = [&](int k) { return k < n ? cb + k : clast; };
 
-  // Scales / zeros of the workgroup's rows, issued by every wave ahead of any ring load.
-  const int nsz = NR * ng;
-  uint32_t sv[MAXSZ], zv[MAXSZ];
+  // Scales / zeros of the workgroup's rows, issued by every wave ahead of any ring load: wave w
+  // stages rows w, w + NW, ..., one row per load with the lane as the group (K / G <= 64).
+  const int gl = lane < ng ? lane : ng - 1;
+  uint32_t sv[RPW], zv[RPW];
 #pragma unroll
-  for (int i = 0; i < MAXSZ; i++) {
-    const int e = t + NTH * i < nsz ? t + NTH * i : 0;
-    const int r = e / ng, gg = e - r * ng;
+  for (int i = 0; i < RPW; i++) {
+    const int r = wave + NW * i;
     const int wr = n0 + r < a.N ? n0 + r : a.N - 1;
-    sv[i] = ld4(a.s + (int64_t)wr * ng + gg);
-    zv[i] = ld4(a.z + (int64_t)wr * ng + gg);
+    sv[i] = ld4(a.s + (int64_t)wr * ng + gl);
+    zv[i] = ld4(a.z + (int64_t)wr * ng + gl);
   }
   __syncthreads();
 
@@ -190,18 +190,17 @@ __global__ __launch_bounds__(NTH) void int4_cu_kernel(I4CuArgs a) {
   load_xu(0, ic<0>{}, ic<0>{});
   wait_vmem<XIN + NT>();  // the scales / zeros have landed
 #pragma unroll
-  for (int i = 0; i < MAXSZ; i++) asm volatile("" : "+v"(sv[i]), "+v"(zv[i]));  // defined only here
+  for (int i = 0; i < RPW; i++) asm volatile("" : "+v"(sv[i]), "+v"(zv[i]));  // defined only here
   bool zok = true;
+  if (lane < ng) {
 #pragma unroll
-  for (int i = 0; i < MAXSZ; i++) {
-    const int e = t + NTH * i;
-    if (e < nsz) {
-      const int r = e / ng, gg = e - r * ng;
+    for (int i = 0; i < RPW; i++) {
+      const int r = wave + NW * i;
       float sf, zf;
       __builtin_memcpy(&sf, &sv[i], 4);
       __builtin_memcpy(&zf, &zv[i], 4);
-      ls[r * sp + gg] = sf;
-      lz[r * sp + gg] = zf;
+      ls[r * sp + lane] = sf;
+      lz[r * sp + lane] = zf;
       zok = zok && zf == rintf(zf) && fabsf(zf) <= 64.f;
     }
   }
@@ -394,12 +393,12 @@ static size_t i4cu_lds(int64_t K, int G, int mt) {
 }
 
 // One workgroup per CU over all of K: taken when the 80-row column tiles fill at least three
-// quarters of the CUs (below that, the K-split kernel keeps the chip busy), and the tile's
-// scales fit the staging (80 (K / G) <= 4096).
+// quarters of the CUs (below that, the K-split kernel keeps the chip busy), and the row's
+// groups fit one wave's lanes (K / G <= 64).
 bool i4cu_ok(int64_t M, int64_t N, int64_t K, int G, int x_dtype, const void *x, const void *codes) {
   return x_dtype == F16 && M > 8 && M <= 64 && K % CK == 0 && G % CK == 0 && K % G == 0 && N >= 1 &&
          ((uintptr_t)x & 15) == 0 && ((uintptr_t)codes & 15) == 0 && N * K / 2 < ((int64_t)1 << 31) &&
-         M * K * 2 < ((int64_t)1 << 31) && 4 * cdiv(N, NR) >= 3 * (int64_t)device_cus() && NR * (K / G) <= NTH * MAXSZ &&
+         M * K * 2 < ((int64_t)1 << 31) && 4 * cdiv(N, NR) >= 3 * (int64_t)device_cus() && K / G <= 64 &&
          i4cu_lds(K, G, 4) <= 160 * 1024;
 }
 
