@@ -23,7 +23,10 @@ def _t(a, dev):
 
 
 @pytest.mark.parametrize("dt,H,I", [(hipq.Q4_K, 4096, 14336), (hipq.Q4_K, 4096, 4096), (hipq.Q5_K, 4096, 8192),
-                                    (hipq.Q4_K, 3072, 8192), (hipq.Q4_K, 4096, 2048)])
+                                    (hipq.Q4_K, 3072, 8192), (hipq.Q4_K, 4096, 2048),
+                                    # more 32-row chunks than CUs, at most two per CU (gate_cu_kernel<2>)
+                                    (hipq.Q5_K, 4096, 12288), (hipq.Q4_K, 3840, 14336), (hipq.Q4_K, 3072, 16384),
+                                    (hipq.Q4_K, 2048, 10240)])
 def test_mlp_one_token_kernels_equal_persistent(dev, dt, H, I):
     """gated gate/up (quantized h) then the down projection: M = 1 against row 0 of M = 2."""
     print(f"[case] decode paths mlp dt={hipq.NAMES[dt]} H={H} I={I}", flush=True)
@@ -39,6 +42,21 @@ def test_mlp_one_token_kernels_equal_persistent(dev, dt, H, I):
     torch.cuda.synchronize()
     assert torch.equal(y1[0], y2[0])
     assert torch.equal(m1[0], y2[0])
+    # Graph replays of the call reproduce it.
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    out = torch.empty_like(m1)
+    ws = torch.empty(hipq.mlp_q_ws_bytes(1, H, I, dt), dtype=torch.uint8, device=dev)
+    with torch.cuda.stream(s):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            hipq.mlp_q(x1, wg, wu, wd, H, I, dt, out=out, ws=ws)
+    torch.cuda.current_stream().wait_stream(s)
+    for _ in range(3):
+        out.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out[0], y2[0])
 
 
 @pytest.mark.parametrize("dt,N,K", [(hipq.Q4_K, 4096, 14336), (hipq.Q4_K, 1024, 14336), (hipq.Q5_K, 4096, 8192),
