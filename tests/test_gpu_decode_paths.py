@@ -115,3 +115,35 @@ def test_int4_cu_kernel_equals_persistent(dev, N, K, xdt):
     y2 = hipq.int4_matmul(x2, ct, st, zt, G)
     torch.cuda.synchronize()
     assert torch.equal(y1[0], y2[0])
+
+
+@pytest.mark.parametrize("dt,N,K", [(hipq.Q4_K, 4096, 14336), (hipq.Q5_K, 1000, 12288), (hipq.Q4_K, 300, 16384),
+                                    (hipq.Q4_K, 2048, 8448), (hipq.Q5_K, 700, 28672)])
+def test_long_rows_f32_x_equals_prepared_activations(dev, dt, N, K):
+    """hq_matmul_q at one token with rows longer than 8192 (past the kernels that quantize x
+    themselves) equals hq_quantize_act followed by hq_matmul_q_act bit for bit."""
+    print(f"[case] long rows f32 x dt={hipq.NAMES[dt]} N={N} K={K}", flush=True)
+    g = synth.rng(7500 + N + dt)
+    w = _t(synth.gguf_weight(dt, N, K, g), dev)
+    x = _t(synth.activations(1, K, g), dev)
+    want = hipq.matmul_q_act(hipq.quantize_act(x), w, 1, N, K, dt)
+    got = hipq.matmul_q(x, w, N, K, dt)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("N,K,xdt", [(3584, 18944, torch.float16), (1000, 10240, torch.float32),
+                                     (2048, 8192, torch.bfloat16)])
+def test_int4_long_rows_one_token_equals_two(dev, N, K, xdt):
+    """int4 GEMV with K >= 8192 (a quantize launch, then the long-row kernel on single-level
+    activations): M = 1 equals row 0 of M = 2 bit for bit."""
+    print(f"[case] int4 long rows N={N} K={K} x={xdt}", flush=True)
+    g = synth.rng(7600 + N + K)
+    G = 128
+    codes, s, z = synth.int4_weight(N, K, G, g)
+    ct, st, zt = (_t(a, dev) for a in (codes, s, z))
+    x2 = torch.from_numpy(synth.activations(2, K, g)).to(xdt).to(dev)
+    y1 = hipq.int4_matmul(x2[:1].contiguous(), ct, st, zt, G)
+    y2 = hipq.int4_matmul(x2, ct, st, zt, G)
+    torch.cuda.synchronize()
+    assert torch.equal(y1[0], y2[0])
