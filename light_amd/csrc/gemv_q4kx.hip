@@ -106,8 +106,10 @@ __device__ __forceinline__ uint32_t bload_u32(__amdgpu_buffer_rsrc_t r, uint32_t
 // the fifth bit of the pair's low / high element l.
 //
 // X2 = false: single-level activations (q1 with its step d only -- exactly q8_1), for rows of
-// at least kX1MinK elements, where the int8 rounding noise of x averages out below the error
-// bar; the q2 loads and dots are skipped (4096 x 14336: 10.9 -> 9.8 us).
+// at least kX1MinK = 4096 elements, where the int8 rounding noise of x averages out below the
+// error bar (K = 4096, N(0,1) x: at most ~3.6e-4 of |w| |x| per output against f32 x, a third
+// of the 1e-3 bar); the q2 loads and dots are skipped (4096 x 14336: 10.9 -> 9.8 us; the MLP
+// step's gate/up at K = 4096: 23.0 -> 22.3 us per step).  Shorter rows keep both levels.
 template <bool Q5, bool X2 = true>
 struct QkUnit {
   static constexpr int BB = Q5 ? 176 : 144, QO = Q5 ? 48 : 16;
@@ -462,7 +464,7 @@ struct Q6kUnit {
 };
 
 // Rows of at least this many elements take single-level activations.
-constexpr int64_t kX1MinK = 8192;
+constexpr int64_t kX1MinK = 4096;
 
 // Calls f with a default-constructed unit policy for (dt in {Q4_K, Q5_K, Q6_K_R}, K).
 template <class F>

@@ -137,7 +137,7 @@ def test_mlp_repeated_calls_agree(dev):
 
 @pytest.mark.parametrize("dt,M,H,I", [(hipq.Q4_K, 1, 4096, 14336), (hipq.Q4_K, 3, 1024, 2816),
                                       (hipq.Q5_K, 2, 1024, 2816), (hipq.Q8_0, 1, 512, 768),
-                                      # both unit variants (two-level x below 8192, one level
+                                      # both unit variants (two-level x below 4096, one level
                                       # from it) on each side; fewer chunks than workgroups
                                       (hipq.Q5_K, 1, 1024, 2816), (hipq.Q4_K, 1, 8192, 1024),
                                       (hipq.Q4_K, 1, 256, 256), (hipq.Q4_K, 1, 2048, 768)])
