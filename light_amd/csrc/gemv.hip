@@ -519,7 +519,7 @@ __device__ __forceinline__ void b32_quants(const uint8_t *lds, int o, uint32_t (
   }
 }
 
-template <int DT, int CPL, int R, int MM, bool XIN>
+template <int DT, int CPL, int R, int MM, bool XIN, bool X1>
 __global__ __launch_bounds__(256) void gemv_q80_kernel(StagedArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   constexpr int BB = DT == Q8_0 ? 34 : DT == Q4_0 ? 18 : 22;
@@ -552,7 +552,8 @@ __global__ __launch_bounds__(256) void gemv_q80_kernel(StagedArgs a) {
       const int64_t blk = (int64_t)m * a.nb + (ok ? bl : 0);
       const uint4 *xs = reinterpret_cast<const uint4 *>(av.p + blk * 32);
       const uint4 *x2 = reinterpret_cast<const uint4 *>(av.p + av.q2 + blk * 32);
-      const uint4 v0 = xs[0], v1 = xs[1], u0 = x2[0], u1 = x2[1];
+      const uint4 v0 = xs[0], v1 = xs[1];
+      const uint4 u0 = X1 ? make_uint4(0, 0, 0, 0) : x2[0], u1 = X1 ? make_uint4(0, 0, 0, 0) : x2[1];
       const int V[8] = {(int)v0.x, (int)v0.y, (int)v0.z, (int)v0.w, (int)v1.x, (int)v1.y, (int)v1.z, (int)v1.w};
       const int U[8] = {(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w, (int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
 #pragma unroll
@@ -599,9 +600,9 @@ __global__ __launch_bounds__(256) void gemv_q80_kernel(StagedArgs a) {
 #pragma unroll
           for (int k = 0; k < 8; k++) {
             dot = dot4((int)qd[k], xv[mm][i][k], dot);
-            dot2 = dot4((int)qd[k], yv[mm][i][k], dot2);
+            if constexpr (!X1) dot2 = dot4((int)qd[k], yv[mm][i][k], dot2);
           }
-          float v = dx[mm][i].x * (float)dot + dx[mm][i].y * (float)dot2;
+          float v = X1 ? dx[mm][i].x * (float)dot : dx[mm][i].x * (float)dot + dx[mm][i].y * (float)dot2;
           if constexpr (DT != Q8_0) v -= ox[mm][i];
           acc[mm] += d * v;
         }
@@ -618,7 +619,7 @@ __global__ __launch_bounds__(256) void gemv_q80_kernel(StagedArgs a) {
 
 // Q6_K lane unit = (block b, l8): half h = l8 >> 2, l0 = (l8 & 3) * 8; the unit covers
 // elements h*128 + g*32 + l0 + [0, 8) for g = 0..3 (quant/q6_k.go:18-27).
-template <int CPL, int R, int MM, bool XIN>
+template <int CPL, int R, int MM, bool XIN, bool X1>
 __global__ __launch_bounds__(256) void gemv_q6k_kernel(StagedArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   const int lane = threadIdx.x & 63;
@@ -655,12 +656,13 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(StagedArgs a) {
       for (int g = 0; g < 4; g++) {
         const int64_t blk = (int64_t)m * (a.K / 32) + bl * 8 + h * 4 + g;
         const uint2 v = *reinterpret_cast<const uint2 *>(av.p + blk * 32 + l0);
-        const uint2 v2 = *reinterpret_cast<const uint2 *>(av.p + av.q2 + blk * 32 + l0);
+        const uint2 v2 = X1 ? make_uint2(0, 0) : *reinterpret_cast<const uint2 *>(av.p + av.q2 + blk * 32 + l0);
         xv[mm][i][2 * g] = ok ? (int)v.x : 0;
         xv[mm][i][2 * g + 1] = ok ? (int)v.y : 0;
         yv[mm][i][2 * g] = ok ? (int)v2.x : 0;
         yv[mm][i][2 * g + 1] = ok ? (int)v2.y : 0;
-        fs[mm][i][g] = ok ? reinterpret_cast<const float2 *>(av.p + av.d)[blk].x * (1.0f / 254.0f) : 0.f;
+        const float dxb = reinterpret_cast<const float2 *>(av.p + av.d)[blk].x;
+        fs[mm][i][g] = ok ? (X1 ? dxb : dxb * (1.0f / 254.0f)) : 0.f;
         s32[mm][i][g] = -32 * byte_sum(&xv[mm][i][2 * g], 2);
         t32[mm][i][g] = -32 * byte_sum(&yv[mm][i][2 * g], 2);
       }
@@ -722,9 +724,14 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(StagedArgs a) {
             // 254 dot + dot2 stays below 2^23 and sc * (254 dot + dot2) below 2^31.
             int dot = dot4((int)qv[g][0], xv[mm][i][2 * g], s32[mm][i][g]);
             dot = dot4((int)qv[g][1], xv[mm][i][2 * g + 1], dot);
-            int dot2 = dot4((int)qv[g][0], yv[mm][i][2 * g], t32[mm][i][g]);
-            dot2 = dot4((int)qv[g][1], yv[mm][i][2 * g + 1], dot2);
-            const int c = __mul24(sc[g], __mul24(254, dot) + dot2);
+            int c;
+            if constexpr (X1) {
+              c = __mul24(sc[g], dot);
+            } else {
+              int dot2 = dot4((int)qv[g][0], yv[mm][i][2 * g], t32[mm][i][g]);
+              dot2 = dot4((int)qv[g][1], yv[mm][i][2 * g + 1], dot2);
+              c = __mul24(sc[g], __mul24(254, dot) + dot2);
+            }
             v = __fmaf_rn((float)c, fs[mm][i][g], v);
           }
           acc[mm] += d * v;
@@ -822,18 +829,18 @@ static void allow_big_lds(K *kern) {
 // Bytes of one LDS slice: R rows (+16 bytes read past the last block), whole KB.
 static int staged_slice(int R, int64_t row_bytes) { return (int)((R * row_bytes + 16 + 1023) & ~(int64_t)1023); }
 
-template <int CPL, int R, int MM, bool XIN>
-static void run_staged(int dt, StagedArgs a, int ns, hipStream_t s) {
+template <int CPL, int R, int MM, bool XIN, bool X1>
+static void run_staged_x(int dt, StagedArgs a, int ns, hipStream_t s) {
   // ns slices per wave; XIN adds the workgroup's quantized x rows.
   a.lds_wave = staged_slice(R, a.row_bytes);
   a.ns = ns;
   const int lds = 4 * ns * a.lds_wave + (XIN ? (int)staged_xin_lds(MM, a.K) : 0);
   static bool attr_done = false;
   if (!attr_done) {
-    allow_big_lds(&gemv_q80_kernel<Q8_0, CPL, R, MM, XIN>);
-    allow_big_lds(&gemv_q80_kernel<Q4_0, CPL, R, MM, XIN>);
-    allow_big_lds(&gemv_q80_kernel<Q5_0, CPL, R, MM, XIN>);
-    allow_big_lds(&gemv_q6k_kernel<CPL, R, MM, XIN>);
+    allow_big_lds(&gemv_q80_kernel<Q8_0, CPL, R, MM, XIN, X1>);
+    allow_big_lds(&gemv_q80_kernel<Q4_0, CPL, R, MM, XIN, X1>);
+    allow_big_lds(&gemv_q80_kernel<Q5_0, CPL, R, MM, XIN, X1>);
+    allow_big_lds(&gemv_q6k_kernel<CPL, R, MM, XIN, X1>);
     attr_done = true;
   }
   const int per_cu = (160 * 1024) / lds;
@@ -842,10 +849,28 @@ static void run_staged(int dt, StagedArgs a, int ns, hipStream_t s) {
   int64_t wgs = cdiv(cdiv(a.N, R), 4 * 2), cap = (int64_t)device_cus() * (per_cu < 2 ? per_cu : 2);
   dim3 g((unsigned)(wgs < cap ? wgs : cap), (unsigned)cdiv(a.M, MM));
   switch (dt) {
-    case Q8_0: gemv_q80_kernel<Q8_0, CPL, R, MM, XIN><<<g, 256, lds, s>>>(a); break;
-    case Q4_0: gemv_q80_kernel<Q4_0, CPL, R, MM, XIN><<<g, 256, lds, s>>>(a); break;
-    case Q5_0: gemv_q80_kernel<Q5_0, CPL, R, MM, XIN><<<g, 256, lds, s>>>(a); break;
-    default: gemv_q6k_kernel<CPL, R, MM, XIN><<<g, 256, lds, s>>>(a); break;
+    case Q8_0: gemv_q80_kernel<Q8_0, CPL, R, MM, XIN, X1><<<g, 256, lds, s>>>(a); break;
+    case Q4_0: gemv_q80_kernel<Q4_0, CPL, R, MM, XIN, X1><<<g, 256, lds, s>>>(a); break;
+    case Q5_0: gemv_q80_kernel<Q5_0, CPL, R, MM, XIN, X1><<<g, 256, lds, s>>>(a); break;
+    default: gemv_q6k_kernel<CPL, R, MM, XIN, X1><<<g, 256, lds, s>>>(a); break;
+  }
+}
+
+// Rows of at least kStagedX1MinK elements take single-level activations (q1 alone, exactly
+// q8_1), as the Q4_K / Q5_K / int4 GEMVs do from the same length: the second level's loads
+// and dots are skipped.
+constexpr int64_t kStagedX1MinK = 4096;
+// (Three or more units per lane means more than 128 units, i.e. K > 4096: those widths
+// exist only with one level.)
+template <int CPL, int R, int MM, bool XIN>
+static void run_staged(int dt, StagedArgs a, int ns, hipStream_t s) {
+  if constexpr (CPL > 2) {
+    run_staged_x<CPL, R, MM, XIN, true>(dt, a, ns, s);
+  } else {
+    if (a.K >= kStagedX1MinK)
+      run_staged_x<CPL, R, MM, XIN, true>(dt, a, ns, s);
+    else
+      run_staged_x<CPL, R, MM, XIN, false>(dt, a, ns, s);
   }
 }
 

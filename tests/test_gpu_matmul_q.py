@@ -207,9 +207,13 @@ def test_matmul_q_act_equals_matmul_q(dev, dt, M):
     y2 = hipq.matmul_q_act(act, w, M, N, K, dt)
     torch.cuda.synchronize()
     # At K <= 8192 the decode GEMVs quantize x inside their workgroups (reciprocal-based
-    # scales): the two paths agree to the activation quantization's own error, far inside the bar.
+    # scales), hq_quantize_act with IEEE divisions: a q1 that rounds the other way at a tie
+    # moves its element by one step d (no second level to absorb it from K = 4096), so the two
+    # paths agree to a few such steps, far inside the bar (each is checked against it below).
     ref = torch.from_numpy(oracle.matmul_q(x.cpu().numpy(), w.cpu().numpy(), N, K, dt)).to(dev)
-    assert ((y1 - y2).abs().max() <= 1e-4 * ref.abs().max()).item()
+    ratio = ((y1 - y2).abs().max() / ref.abs().max()).item()
+    print(f"[diff] {hipq.NAMES[dt]} M={M}: max |y1 - y2| / max |y| = {ratio:.3g}", flush=True)
+    assert ratio <= (1e-4 if K < 4096 else 1e-3)
     _check_matmul(dev, dt, x.cpu().numpy(), w.cpu().numpy(), N, K, "act")
     _check_matmul(dev, dt, x.cpu().numpy(), w.cpu().numpy(), N, K, "act", got=y2.cpu().numpy())
 
