@@ -8,8 +8,9 @@ shapes.  Both halves are measured in the default run.
       h = SiLU(x . Wgate^T) * (x . Wup^T)   gate/up 14336x4096 Q4_K (h emitted quantized)
       y = h . Wdown^T                        down 4096x14336 Q4_K
   value = algorithmic bytes of a step (the three weights as stored + F32 x in + F32 y out)
-  / wall time of the K timed steps, run back to back (`graph_us_per_step`: the same steps
-  replayed from a captured HIP graph, for reference).
+  / GPU time of the K timed steps, run back to back (HIP events around them, the host's
+  enqueueing hidden behind a spin kernel; `graph_us_per_step`: the same steps replayed from a
+  captured HIP graph, for reference).
 * `roofline`: the step's dominant kernel, its first launch (hq_matmul_q_gated_act: the gated
   GEMV with the quantized-h epilogue), timed per launch with HIP events on its stream.
   `second_kernel` is the step's down GEMV, timed the same way.
@@ -119,18 +120,23 @@ def run_gpu(args):
     torch.cuda.synchronize()
     eager = y.clone()
 
-    # The timed steps: back-to-back hq_mlp_q calls (the host queues them faster than the GPU
-    # runs them), rotating over the weight copies.
+    # The timed steps: back-to-back hq_mlp_q calls rotating over the weight copies, timed by a
+    # HIP event pair on the stream.  A spin kernel queued first keeps the GPU busy while the
+    # host enqueues all K calls, so the interval is the K steps' own GPU time whatever the
+    # host's per-call cost (a profiler's, say).
     def run_steps(n):
         for i in range(n):
             step(i % rot)
 
     run_steps(args.warmup)
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(int(3e5 * args.steps))
+    e0.record()
     run_steps(args.steps)
+    e1.record()
     torch.cuda.synchronize()
-    dt = time.perf_counter() - t0
+    dt = e0.elapsed_time(e1) * 1e-3
     if not torch.equal(y, eager):  # copies hold identical bytes
         raise RuntimeError("a timed step differs from the eager step")
     nbytes = step_bytes(gate, up, down)
