@@ -188,10 +188,9 @@ int hq_mlp_q(const float *x, const void *wg, const void *wu, const void *wd, flo
  *   (d, e) f32 pairs [M][K/32] (d before q8_1's f16 rounding)
  *   sx f32 [M][K/32]          the block sum of x
  * so x = d*q1 + e*q2 to within e/2 (about 2^-15 of the block's amax); offsets are
- * rounded up to 256 bytes.  The Q4_K / Q5_K / int4 decode GEMVs read q1 alone (exactly
- * q8_1) for rows of K >= 8192, where the rounding averages out below the 1e-3 bar; shorter
- * rows and the other formats use both levels.  The layout is internal and may change with
- * the version. */
+ * rounded up to 256 bytes.  The decode GEMVs read q1 alone (exactly q8_1) for rows of
+ * K >= 4096, where the rounding averages out below the 1e-3 bar; shorter rows and the MoE
+ * GEMVs use both levels.  The layout is internal and may change with the version. */
 size_t hq_act_bytes(int64_t M, int64_t K);
 int hq_quantize_act(const void *x, int x_dtype, void *act, int64_t M, int64_t K, hq_stream_t stream);
 /* Workspace hq_matmul_q_act needs beyond the act buffer (0 for the GEMV). */
