@@ -394,12 +394,12 @@ static size_t i4cu_lds(int64_t K, int G, int mt) {
 
 // One workgroup per CU over all of K: taken when the 80-row column tiles fill at least three
 // quarters of the CUs (below that, the K-split kernel keeps the chip busy), and the row's
-// groups fit one wave's lanes (K / G <= 64).
+// groups fit one wave's lanes (K / G <= 64), and the LDS of the launch's x tiles fits.
 bool i4cu_ok(int64_t M, int64_t N, int64_t K, int G, int x_dtype, const void *x, const void *codes) {
   return x_dtype == F16 && M > 8 && M <= 64 && K % CK == 0 && G % CK == 0 && K % G == 0 && N >= 1 &&
          ((uintptr_t)x & 15) == 0 && ((uintptr_t)codes & 15) == 0 && N * K / 2 < ((int64_t)1 << 31) &&
          M * K * 2 < ((int64_t)1 << 31) && 4 * cdiv(N, NR) >= 3 * (int64_t)device_cus() && K / G <= 64 &&
-         i4cu_lds(K, G, 4) <= 160 * 1024;
+         i4cu_lds(K, G, (int)cdiv(M, 16)) <= 160 * 1024;
 }
 
 int launch_i4cu(const uint16_t *x, const uint32_t *codes, const float *s, const float *z, void *y, int64_t M, int64_t N,

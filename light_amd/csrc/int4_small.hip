@@ -261,12 +261,23 @@ __global__ __launch_bounds__(512) void gemm_i4f16_small_kernel(I4F16Args a) {
     }
 }
 
-bool i4f16_small_ok(int64_t M, int64_t N, int64_t K, int G, int x_dtype, const void *x, const void *codes) {
-  return x_dtype == F16 && M > 8 && M <= 64 && K % IK == 0 && G % IK == 0 && K % G == 0 && N >= 1 &&
-         ((uintptr_t)x & 15) == 0 && ((uintptr_t)codes & 15) == 0;
+int launch_splitk_reduce(const float *part, void *out, int out_dtype, int64_t n, int splits, hipStream_t s);
+int i4f16_splits(int64_t N, int64_t K);
+
+// LDS of one workgroup: the double-buffered x stage, then the scales and zeros of the 256
+// weight rows over the groups one split can touch (its stages' span of K / G, plus one for a
+// group boundary).
+static size_t i4f16_lds(int64_t N, int64_t K, int G) {
+  const int64_t nst = K / IK, maxst = cdiv(nst, i4f16_splits(N, K));
+  const int64_t ngl = (maxst * IK + G - 1) / G + 1;
+  return 2 * 64 * IXLD * 2 + 2 * 256 * (size_t)ngl * 4;
 }
 
-int launch_splitk_reduce(const float *part, void *out, int out_dtype, int64_t n, int splits, hipStream_t s);
+// Shapes past the LDS (many groups per split) take the bf16 GEMM instead.
+bool i4f16_small_ok(int64_t M, int64_t N, int64_t K, int G, int x_dtype, const void *x, const void *codes) {
+  return x_dtype == F16 && M > 8 && M <= 64 && K % IK == 0 && G % IK == 0 && K % G == 0 && N >= 1 &&
+         ((uintptr_t)x & 15) == 0 && ((uintptr_t)codes & 15) == 0 && i4f16_lds(N, K, G) <= 160 * 1024;
+}
 
 // K split: one workgroup fits a CU (133 registers, eight waves), so the split minimising
 // (rounds of workgroups over the CUs) x (stages per split) wins, with a 2% charge per split
@@ -300,11 +311,8 @@ int launch_i4f16_small(const uint16_t *x, const uint32_t *codes, const float *s,
   a.G = G;
   a.splits = i4f16_splits(N, K);
   dim3 grid((unsigned)cdiv(N, 256), 1, (unsigned)a.splits);
-  // Groups one split can touch: its stages' span of K / G, plus one for a group boundary.
-  const int64_t nst = K / IK, maxst = cdiv(nst, a.splits);
-  const int64_t ngl = (maxst * IK + G - 1) / G + 1;
-  const size_t lds = 2 * 64 * IXLD * 2 + 2 * 256 * (size_t)ngl * 4;
-  if (lds > 64 * 1024) return fail(HQ_EUNSUPPORTED, "int4_matmul", "%lld groups per split", (long long)ngl);
+  const size_t lds = i4f16_lds(N, K, G);
+  if (lds > 160 * 1024) return fail(HQ_EUNSUPPORTED, "int4_matmul", "LDS %zu bytes", lds);
   gemm_i4f16_small_kernel<<<grid, 512, lds, st>>>(a);
   if (int rc = check_launch("gemm_i4f16_small")) return rc;
   return launch_splitk_reduce(partials, y, F16, M * N, a.splits, st);

@@ -191,6 +191,7 @@ def test_moe_int4_vs_light_cpu(dev, T, E, topk, H, I, G, xdt):
     (64, 15400, 768, 128, "frac"),     # non-integral zero points: the second FMA subtracts z s'
     (64, 15400, 768, 128, "wide"),     # integral zero points beyond 64
     (48, 15400, 1536, 128, "tiny"),    # scales 1e-7 .. 1e-4 in a row: the per-row exponent
+    (40, 15400, 8192, 128, "light"),   # K / G = 64 groups: every lane stages one group's scale
 ])
 def test_matmul_int4_f16_one_launch(dev, M, N, K, G, kind):
     """F16 x, 8 < M <= 64, 80-row column tiles filling the chip: the one-launch kernel (one
@@ -207,7 +208,10 @@ def test_matmul_int4_f16_one_launch(dev, M, N, K, G, kind):
     _check(dev, x, codes, s, z, G, hipq.F16)
 
 
-@pytest.mark.parametrize("M,N,K,G", [(33, 1000, 1024, 128), (64, 18944, 3584, 128), (17, 300, 2048, 256)])
+@pytest.mark.parametrize("M,N,K,G", [
+    (33, 1000, 1024, 128), (64, 18944, 3584, 128), (17, 300, 2048, 256),
+    (64, 15400, 8192, 128),  # 17 groups per split: scales / zeros past 64 KB of LDS
+])
 def test_matmul_int4_f16_split_k_streams_and_repeats(dev, M, N, K, G):
     """F16 x, 8 < M <= 64, split over K: matches the f64 reference, and repeated calls -- on the
     default stream and on twenty other streams (each with its own library workspace) -- give
