@@ -1,0 +1,122 @@
+"""Seeded random shapes through every dispatch path of MatMulQ, MatMulInt4 and MoEGemmQ.
+
+Each entry point picks among several kernels by M, N, K, the group size and the x dtype
+(decode GEMVs, staged GEMVs, the one-launch and split-K int4 kernels, the MFMA GEMMs).  The
+shapes below are drawn once from a fixed seed over ragged N, K up to 16-20 K and M from 1 to
+100 (and, for the int4 kernels that need the chip filled, N up to 24 K with sampled rows;
+for MoEGemmQ, random expert counts, top-k and token counts), so every path meets shapes its
+own tests do not name; each call must succeed and stay within the north-star bar of Light's
+CPU path and the f64 oracle (ops/matmul_q_test.go:105-146, ops/int4_test.go:15-31 and
+ops/moe_test.go for the input distributions).
+"""
+import numpy as np
+import pytest
+
+from _util import random_blocks
+from light_amd import hipq, synth
+from test_gpu_int4 import _check as check_int4, light_int4
+from test_gpu_matmul_q import _check_matmul
+from test_gpu_moe import _check as check_moe
+
+pytestmark = pytest.mark.gpu
+
+_MS = (1, 2, 3, 5, 8, 9, 12, 16, 17, 24, 33, 40, 48, 64, 65, 100)
+_GGUF = (hipq.Q4_0, hipq.Q5_0, hipq.Q8_0, hipq.Q4_K, hipq.Q5_K, hipq.Q6_K)
+_BLOCK = {hipq.Q4_0: 32, hipq.Q5_0: 32, hipq.Q8_0: 32, hipq.Q4_K: 256, hipq.Q5_K: 256, hipq.Q6_K: 256}
+_WORK = 2.5e8  # M * N * K per case: the CPU oracle finishes each in about a second
+
+
+def _gguf_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        dt = _GGUF[i % len(_GGUF)]
+        M = int(rng.choice(_MS))
+        K = _BLOCK[dt] * int(rng.integers(1, 20480 // _BLOCK[dt] + 1))
+        N = int(rng.integers(1, 6000))
+        while M * N * K > _WORK and N > 1:
+            N //= 2
+        out.append((dt, M, N, K))
+    return out
+
+
+def _int4_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        xdt = (hipq.F32, hipq.F16, hipq.BF16)[i % 3]
+        G = int(rng.choice((32, 64, 128, 256)))
+        M = int(rng.choice(_MS))
+        K = G * int(rng.integers(1, 16384 // G + 1))
+        N = int(rng.integers(1, 20000))
+        while M * N * K > _WORK and N > 1:
+            N //= 2
+        out.append((xdt, M, N, K, G))
+    return out
+
+
+@pytest.mark.parametrize("dt,M,N,K", _gguf_cases(36, 2024))
+def test_matmul_q_random_shape(dev, dt, M, N, K):
+    rng = np.random.default_rng(M * 7919 + N * 31 + K + dt)
+    w = random_blocks(rng, dt, N, K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    _check_matmul(dev, dt, x, w, N, K, "random shape")
+
+
+@pytest.mark.parametrize("xdt,M,N,K,G", _int4_cases(30, 4048))
+def test_int4_matmul_random_shape(dev, xdt, M, N, K, G):
+    rng = np.random.default_rng(M * 7919 + N * 31 + K + G)
+    codes, s, z = light_int4(rng, N, K, G)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    check_int4(dev, x, codes, s, z, G, xdt)
+
+
+def _int4_wide_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        xdt = (hipq.F16, hipq.F32, hipq.BF16, hipq.F16)[i % 4]
+        G = int(rng.choice((64, 128, 256)))
+        M = int(rng.integers(9, 65))
+        K = G * int(rng.integers(1, 8192 // G + 1))
+        N = int(rng.integers(15000, 24000))
+        out.append((xdt, M, N, K, G))
+    return out
+
+
+@pytest.mark.parametrize("xdt,M,N,K,G", _int4_wide_cases(12, 8096))
+def test_int4_matmul_random_wide_shape(dev, xdt, M, N, K, G):
+    """N large enough for the one-launch F16 kernel; four rows checked (first, last, two inside)."""
+    rng = np.random.default_rng(M * 7919 + N * 31 + K + G)
+    codes, s, z = light_int4(rng, N, K, G)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    rows = sorted({0, M - 1, int(rng.integers(0, M)), int(rng.integers(0, M))})
+    check_int4(dev, x, codes, s, z, G, xdt, rows=rows)
+
+
+def _moe_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        dt = _GGUF[i % len(_GGUF)]
+        E = int(rng.integers(2, 65))
+        topk = int(rng.integers(1, min(E, 8) + 1))
+        T = int(rng.choice((1, 2, 3, 7, 16, 33, 64, 100, 256)))
+        K = _BLOCK[dt] * int(rng.integers(1, 6144 // _BLOCK[dt] + 1))
+        N = int(rng.integers(1, 700))
+        while (T * topk * N * K > _WORK or E * N * K > 6e7) and N > 1:  # oracle time and memory
+            N //= 2
+        out.append((dt, T, E, topk, N, K, bool(i % 2)))
+    return out
+
+
+@pytest.mark.parametrize("dt,T,E,topk,N,K,weighted", _moe_cases(24, 6072))
+def test_moe_gemm_q_random_shape(dev, dt, T, E, topk, N, K, weighted):
+    g = synth.rng(T * 131 + E * 17 + topk + N + K + dt)
+    w = synth.gguf_weight(dt, E * N, K, g)
+    ids, tw = synth.moe_routing(T, E, topk, g)
+    rows = T * topk if weighted else T
+    x = g.standard_normal((rows, K)).astype(np.float32)
+    M = T * topk
+    sample = None if M <= 64 else list(range(0, M, max(1, M // 64))) + [M - 1]
+    check_moe(dev, x, w, dt, E, N, K, ids, tw, topk, weighted, sample=sample)
