@@ -1,4 +1,5 @@
-"""Seeded random shapes through every dispatch path of MatMulQ, MatMulInt4 and MoEGemmQ.
+"""Seeded random shapes through every dispatch path of MatMulQ, MatMulInt4, MoEGemmQ and
+the fused gated projection and MLP.
 
 Each entry point picks among several kernels by M, N, K, the group size and the x dtype
 (decode GEMVs, staged GEMVs, the one-launch and split-K int4 kernels, the MFMA GEMMs).  The
@@ -14,6 +15,7 @@ import pytest
 
 from _util import random_blocks
 from light_amd import hipq, synth
+from test_gpu_gated import _check as check_gated, _check_mlp as check_mlp
 from test_gpu_int4 import _check as check_int4, light_int4
 from test_gpu_matmul_q import _check_matmul
 from test_gpu_moe import _check as check_moe
@@ -120,3 +122,41 @@ def test_moe_gemm_q_random_shape(dev, dt, T, E, topk, N, K, weighted):
     M = T * topk
     sample = None if M <= 64 else list(range(0, M, max(1, M // 64))) + [M - 1]
     check_moe(dev, x, w, dt, E, N, K, ids, tw, topk, weighted, sample=sample)
+
+
+def _gated_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        dt = _GGUF[i % len(_GGUF)]
+        M = int(rng.choice(_MS))
+        K = _BLOCK[dt] * int(rng.integers(1, 16384 // _BLOCK[dt] + 1))
+        N = int(rng.integers(1, 6000))
+        while 2 * M * N * K > _WORK and N > 1:
+            N //= 2
+        out.append((dt, M, N, K, (hipq.ACT_SILU, hipq.ACT_GELU_ERF)[i % 2]))
+    return out
+
+
+@pytest.mark.parametrize("dt,M,N,K,act", _gated_cases(24, 9120))
+def test_gated_random_shape(dev, dt, M, N, K, act):
+    check_gated(dev, dt, M, N, K, act, seed=M * 7919 + N * 31 + K + dt)
+
+
+def _mlp_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        dt = _GGUF[i % len(_GGUF)]
+        M = int(rng.choice(_MS))
+        H = _BLOCK[dt] * int(rng.integers(1, 6144 // _BLOCK[dt] + 1))
+        I = _BLOCK[dt] * int(rng.integers(1, 16384 // _BLOCK[dt] + 1))
+        while 3 * M * H * I > _WORK and I > _BLOCK[dt]:
+            I = max(_BLOCK[dt], (I // 2) // _BLOCK[dt] * _BLOCK[dt])
+        out.append((dt, M, H, I, (hipq.ACT_SILU, hipq.ACT_GELU_ERF)[i % 2]))
+    return out
+
+
+@pytest.mark.parametrize("dt,M,H,I,act", _mlp_cases(18, 10144))
+def test_mlp_random_shape(dev, dt, M, H, I, act):
+    check_mlp(dev, dt, M, H, I, act, seed=M * 7919 + H * 31 + I + dt)
