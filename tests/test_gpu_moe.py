@@ -162,7 +162,7 @@ def _probs(g, T, E, ties):
     logits = g.standard_normal((T, E)).astype(np.float32)
     p = np.exp(logits - logits.max(axis=1, keepdims=True))
     p = (p / p.sum(axis=1, keepdims=True)).astype(np.float32)
-    if ties:
+    if ties and E > 1:  # (one expert: nothing to tie)
         p[:, E // 2] = p[:, 0]
         p[:, E - 1] = p[:, 1]
     return p

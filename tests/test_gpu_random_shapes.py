@@ -1,5 +1,5 @@
-"""Seeded random shapes through every dispatch path of MatMulQ, MatMulInt4, MoEGemmQ and
-the fused gated projection and MLP.
+"""Seeded random shapes through every dispatch path of MatMulQ, MatMulInt4, MoEGemmQ, the
+fused gated projection and MLP, MoERoute, the fused MoE blocks and MoEInt4.
 
 Each entry point picks among several kernels by M, N, K, the group size and the x dtype
 (decode GEMVs, staged GEMVs, the one-launch and split-K int4 kernels, the MFMA GEMMs).  The
@@ -12,13 +12,18 @@ ops/moe_test.go for the input distributions).
 """
 import numpy as np
 import pytest
+import torch
 
 from _util import random_blocks
 from light_amd import hipq, synth
 from test_gpu_gated import _check as check_gated, _check_mlp as check_mlp
 from test_gpu_int4 import _check as check_int4, light_int4
 from test_gpu_matmul_q import _check_matmul
+from test_gpu_int4 import test_moe_int4_vs_light_cpu as check_moe_int4
 from test_gpu_moe import _check as check_moe
+from test_gpu_moe import test_moe_block_equals_route_gated_then_combine as check_moe_block
+from test_gpu_moe import test_moe_route_bit_exact as check_route
+from test_gpu_moe import test_moe_route_gated_bit_exact as check_route_gated
 
 pytestmark = pytest.mark.gpu
 
@@ -160,3 +165,64 @@ def _mlp_cases(n, seed):
 @pytest.mark.parametrize("dt,M,H,I,act", _mlp_cases(18, 10144))
 def test_mlp_random_shape(dev, dt, M, H, I, act):
     check_mlp(dev, dt, M, H, I, act, seed=M * 7919 + H * 31 + I + dt)
+
+
+def _route_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        E = int(rng.choice((1, 2, 7, 16, 60, 64, 65, 128, 200, 256, 513, 1024)))
+        topk = int(rng.integers(1, min(E, 64) + 1))
+        # the one-workgroup sort holds a 16-bit count per (64-pair chunk, expert) in LDS
+        T = int(rng.integers(1, max(2, min(3000, 4_000_000 // (topk * E)))))
+        out.append((T, E, topk, bool(i % 2)))
+    return out
+
+
+@pytest.mark.parametrize("T,E,topk,normalize", _route_cases(16, 11168))
+def test_moe_route_random_shape(dev, T, E, topk, normalize):
+    check_route(dev, T, E, topk, normalize)
+
+
+def _moe_fused_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        dt = (hipq.Q4_K, hipq.Q5_K, hipq.Q4_K, hipq.Q8_0, hipq.Q6_K, hipq.Q4_0)[i % 6]
+        T = int(rng.choice((1, 1, 1, 2, 3, 5, 16, 40)))
+        E = int(rng.integers(2, 161))
+        topk = int(rng.integers(1, min(E, 8) + 1))
+        H = _BLOCK[dt] * int(rng.integers(1, 4096 // _BLOCK[dt] + 1))
+        I = _BLOCK[dt] * int(rng.integers(1, 2048 // _BLOCK[dt] + 1))
+        while E * 3 * I * H > 1.2e8 and E > 2:
+            E = max(2, E // 2)
+        topk = min(topk, E)
+        out.append((dt, T, E, topk, H, I))
+    return out
+
+
+@pytest.mark.parametrize("dt,T,E,topk,H,I", _moe_fused_cases(18, 12192))
+def test_moe_fused_random_shape(dev, dt, T, E, topk, H, I):
+    """Route + gated equals the separate calls, and the whole block equals route + gated +
+    combine, bit for bit (the separate calls are held to the oracle by their own tests)."""
+    check_route_gated(dev, dt, T, E, topk, H, I, False)
+    check_moe_block(dev, dt, T, E, topk, H, I)
+
+
+def _moe_int4_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        G = int(rng.choice((32, 64, 128)))
+        T = int(rng.choice((1, 2, 3, 7)))
+        E = int(rng.integers(2, 33))
+        topk = int(rng.integers(1, min(E, 8) + 1))
+        H = G * int(rng.integers(1, 2048 // G + 1))
+        I = G * int(rng.integers(1, 1536 // G + 1))
+        out.append((T, E, topk, H, I, G, (torch.float32, torch.float16, torch.bfloat16)[i % 3]))
+    return out
+
+
+@pytest.mark.parametrize("T,E,topk,H,I,G,xdt", _moe_int4_cases(9, 13216))
+def test_moe_int4_random_shape(dev, T, E, topk, H, I, G, xdt):
+    check_moe_int4(dev, T, E, topk, H, I, G, xdt)
