@@ -195,9 +195,10 @@ size_t hq_act_bytes(int64_t M, int64_t K);
 int hq_quantize_act(const void *x, int x_dtype, void *act, int64_t M, int64_t K, hq_stream_t stream);
 /* Workspace hq_matmul_q_act needs beyond the act buffer (0 for the GEMV). */
 size_t hq_matmul_q_act_ws_bytes(int64_t M, int64_t N, int64_t K, int w_dtype);
-/* out (M, N) F32 = x @ dequant(w)^T from prepared activations.  For M <= 8 the
- * weight must take the int8 GEMV (16-byte aligned, rows a multiple of 16 bytes;
- * HQ_EUNSUPPORTED otherwise). */
+/* out (M, N) F32 = x @ dequant(w)^T from prepared activations.  For M <= 8, and for
+ * any M when K is not a multiple of 64, the weight must take the int8 GEMV (16-byte
+ * aligned, rows a multiple of 16 bytes; HQ_EUNSUPPORTED otherwise -- hq_matmul_q takes
+ * every layout). */
 int hq_matmul_q_act(const void *act, const void *w, float *out, int64_t M, int64_t N, int64_t K, int w_dtype,
                     void *ws, size_t ws_bytes, hq_stream_t stream);
 

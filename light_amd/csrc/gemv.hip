@@ -1018,6 +1018,8 @@ bool use_gemm(int64_t M, int dt) { return M > kGemvMaxRows; }
 
 static bool gemm_k_ok(int64_t K) { return K % 64 == 0; }
 
+bool matmul_act_takes_gemm(int64_t M, int64_t K, int dt) { return use_gemm(M, dt) && gemm_k_ok(K); }
+
 static int64_t al256(int64_t b) { return (b + 255) & ~(int64_t)255; }
 
 static size_t gemm_ws(int64_t M, int64_t N, int64_t K, int dt) {
@@ -1053,7 +1055,7 @@ static int run_gemm(const void *src, bool from_act, const void *w, float *out, i
 
 int launch_matmul_act(const void *act, const void *w, float *out, int64_t M, int64_t N, int64_t K, int dt, void *ws,
                       hipStream_t s) {
-  if (use_gemm(M, dt) && gemm_k_ok(K)) return run_gemm(act, true, w, out, M, N, K, dt, ws, s);
+  if (matmul_act_takes_gemm(M, K, dt)) return run_gemm(act, true, w, out, M, N, K, dt, ws, s);
   return launch_gemv_act(act, w, out, M, N, K, dt, s);
 }
 

@@ -42,6 +42,8 @@ int launch_dequant_q6kr(const void *src, void *dst, int64_t N, int64_t K, int ou
 // in ws, then runs the kernel.
 constexpr int64_t kGemvMaxRows = 8;
 bool use_gemm(int64_t M, int dt);
+// hq_matmul_q_act runs the MFMA GEMM (else the int8 GEMV on the prepared activations).
+bool matmul_act_takes_gemm(int64_t M, int64_t K, int dt);
 int launch_gemm_ws_bf16(const uint16_t *xb, const uint16_t *wb, float *out, float *partials, int64_t M, int64_t N,
                         int64_t K, hipStream_t s);
 size_t matmul_q_ws_bytes(int64_t M, int64_t N, int64_t K, int dt);

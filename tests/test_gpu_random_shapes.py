@@ -1,5 +1,6 @@
-"""Seeded random shapes through every dispatch path of MatMulQ, MatMulInt4, MoEGemmQ, the
-fused gated projection and MLP, MoERoute, the fused MoE blocks and MoEInt4.
+"""Seeded random shapes through every dispatch path of MatMulQ (GGUF bytes, the Q6_K_R layout
+and prepared activations), dequant, MatMulInt4, MoEGemmQ, the fused gated projection and MLP,
+MoERoute, the fused MoE blocks and MoEInt4.
 
 Each entry point picks among several kernels by M, N, K, the group size and the x dtype
 (decode GEMVs, staged GEMVs, the one-launch and split-K int4 kernels, the MFMA GEMMs).  The
@@ -14,7 +15,8 @@ import numpy as np
 import pytest
 import torch
 
-from _util import random_blocks
+import oracle
+from _util import norm_err, random_blocks
 from light_amd import hipq, synth
 from test_gpu_gated import _check as check_gated, _check_mlp as check_mlp
 from test_gpu_int4 import _check as check_int4, light_int4
@@ -24,6 +26,7 @@ from test_gpu_moe import _check as check_moe
 from test_gpu_moe import test_moe_block_equals_route_gated_then_combine as check_moe_block
 from test_gpu_moe import test_moe_route_bit_exact as check_route
 from test_gpu_moe import test_moe_route_gated_bit_exact as check_route_gated
+from test_gpu_q6k_repack import _check as check_q6kr
 
 pytestmark = pytest.mark.gpu
 
@@ -226,3 +229,55 @@ def _moe_int4_cases(n, seed):
 @pytest.mark.parametrize("T,E,topk,H,I,G,xdt", _moe_int4_cases(9, 13216))
 def test_moe_int4_random_shape(dev, T, E, topk, H, I, G, xdt):
     check_moe_int4(dev, T, E, topk, H, I, G, xdt)
+
+
+def _t(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+@pytest.mark.parametrize("dt,M,N,K", [(hipq.Q6_K, M, N, K) for (_, M, N, K) in _gguf_cases(18, 14240)])
+def test_matmul_q6kr_random_shape(dev, dt, M, N, K):
+    """The Q6_K_R layout (repacked on the device) against Light's CPU path on the GGUF bytes."""
+    rng = np.random.default_rng(M * 7919 + N * 31 + K)
+    K = 256 * max(1, K // 256)
+    w = random_blocks(rng, hipq.Q6_K, N, K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    check_q6kr(dev, x, w, N, K, "random shape")
+
+
+@pytest.mark.parametrize("dt,M,N,K", _gguf_cases(24, 15264))
+@pytest.mark.parametrize("odt", [hipq.F32, hipq.BF16])
+def test_dequant_random_shape(dev, dt, M, N, K, odt):
+    """Bit-exact dequant of N rows of K at random sizes (M unused)."""
+    print(f"[case] dequant dt={hipq.NAMES[dt]} N={N} K={K} odt={odt}", flush=True)
+    raw = random_blocks(np.random.default_rng(N * 31 + K + dt), dt, N, K)
+    got = hipq.dequant(_t(raw, dev), N * K, dt, odt)
+    want = oracle.dequant(dt, raw, N * K)
+    if odt == hipq.F32:
+        assert np.array_equal(got.cpu().numpy().view(np.uint32), want.view(np.uint32))
+    else:
+        assert torch.equal(got.cpu().view(torch.int16), torch.from_numpy(want).to(torch.bfloat16).view(torch.int16))
+
+
+@pytest.mark.parametrize("dt,M,N,K", _gguf_cases(24, 16288))
+def test_matmul_q_act_random_shape(dev, dt, M, N, K):
+    """Prepared activations (hq_quantize_act, then hq_matmul_q_act) against the f64 oracle.
+    Calls that take the GEMV (M <= 8, or K not a multiple of 64) need a weight layout the int8
+    GEMV reads (rows of whole 16-byte pieces); any other is refused with HQ_EUNSUPPORTED, never
+    run (hq_matmul_q takes those, and test_matmul_q_random_shape covers it)."""
+    print(f"[case] matmul_q_act dt={hipq.NAMES[dt]} M={M} N={N} K={K}", flush=True)
+    rng = np.random.default_rng(M * 7919 + N * 31 + K + dt + 1)
+    w = random_blocks(rng, dt, N, K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    act = hipq.quantize_act(_t(x, dev))
+    ws = torch.empty(max(1, hipq.lib().hq_matmul_q_act_ws_bytes(M, N, K, dt)), dtype=torch.uint8, device=dev)
+    takes_gemv = M <= 8 or K % 64 != 0
+    try:
+        got = hipq.matmul_q_act(act, _t(w, dev), M, N, K, dt, ws=ws).cpu().numpy()
+    except hipq.HipqError as e:
+        assert e.code == hipq.HQ_EUNSUPPORTED and takes_gemv, str(e)
+        return
+    wd = oracle.dequant(dt, w, N * K).reshape(N, K)
+    ref, _, wn, xn = oracle.matmul_f64(x, wd)
+    assert np.all(np.isfinite(got))
+    assert norm_err(got, ref, wn, xn) <= 1e-3
