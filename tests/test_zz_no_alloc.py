@@ -11,6 +11,7 @@ import numpy as np
 import pytest
 import torch
 
+from _util import random_blocks
 from light_amd import hipq, synth
 
 pytestmark = pytest.mark.gpu
@@ -57,6 +58,45 @@ def test_noalloc_q6k_r_matches_matmul_q(dev):
         w = hipq.repack_q6k(raw, N, K)
         want = hipq.matmul_q(x, w, N, K, hipq.Q6_K_R)
         got = _noalloc(x, w, N, K, hipq.Q6_K_R)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"call {i}: max diff {(got - want).abs().max().item():.3g}"
+
+
+def _random_pairs(n, seed):
+    rng = np.random.default_rng(seed)
+    fmts = (hipq.Q4_0, hipq.Q5_0, hipq.Q8_0, hipq.Q4_K, hipq.Q5_K, hipq.Q6_K)
+    block = {hipq.Q4_0: 32, hipq.Q5_0: 32, hipq.Q8_0: 32, hipq.Q4_K: 256, hipq.Q5_K: 256, hipq.Q6_K: 256}
+    ms = (1, 2, 3, 5, 8, 9, 16, 24, 33, 64, 100)
+    out = []
+    for i in range(n):
+        dt = fmts[i % len(fmts)]
+        shapes = []
+        for _ in range(2):
+            M = int(rng.choice(ms))
+            K = block[dt] * int(rng.integers(1, 16384 // block[dt] + 1))
+            N = int(rng.integers(1, 4000))
+            shapes.append((M, N, K))
+        out.append((dt, shapes[0], shapes[1]))
+    return out
+
+
+@pytest.mark.parametrize("dt,first,second", _random_pairs(18, 5151))
+def test_noalloc_random_shape_pairs(dev, dt, first, second):
+    """Two calls in a row at random shapes: each equals hq_matmul_q bit for bit, or is refused
+    with HQ_ENOMEM exactly when its workspace exceeds the scratch array."""
+    for i, (M, N, K) in enumerate((first, second)):
+        print(f"[case] noalloc random dt={hipq.NAMES[dt]} M={M} N={N} K={K} call {i}", flush=True)
+        rng = np.random.default_rng(M * 7919 + N * 31 + K + dt + i)
+        w = torch.from_numpy(random_blocks(rng, dt, N, K)).to(dev)
+        x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).to(dev)
+        need = hipq.lib().hq_matmul_q_ws_bytes(M, N, K, dt)
+        want = hipq.matmul_q(x, w, N, K, dt)
+        if need > hipq.NOALLOC_SCRATCH_BYTES:
+            with pytest.raises(hipq.HipqError) as ei:
+                _noalloc(x, w, N, K, dt)
+            assert ei.value.code == hipq.HQ_ENOMEM
+            continue
+        got = _noalloc(x, w, N, K, dt)
         torch.cuda.synchronize()
         assert torch.equal(got, want), f"call {i}: max diff {(got - want).abs().max().item():.3g}"
 
