@@ -281,3 +281,27 @@ def test_matmul_q_act_random_shape(dev, dt, M, N, K):
     ref, _, wn, xn = oracle.matmul_f64(x, wd)
     assert np.all(np.isfinite(got))
     assert norm_err(got, ref, wn, xn) <= 1e-3
+
+
+@pytest.mark.parametrize("dt,M,N,K,act", [(dt, M, 32 * max(1, N // 32), K, a)
+                                          for (dt, M, N, K, a) in _gated_cases(24, 17312)])
+def test_gated_act_random_shape(dev, dt, M, N, K, act):
+    """hq_matmul_q_gated_act writes what hq_quantize_act writes for hq_matmul_q_gated's F32
+    output: the same bytes (N % 32 == 0)."""
+    print(f"[case] gated_act dt={hipq.NAMES[dt]} M={M} N={N} K={K} act={act}", flush=True)
+    rng = np.random.default_rng(M * 7919 + N * 31 + K + dt + 2)
+    wg = _t(random_blocks(rng, dt, N, K), dev)
+    wu = _t(random_blocks(rng, dt, N, K), dev)
+    x = _t(rng.standard_normal((M, K)).astype(np.float32), dev)
+    got = hipq.matmul_q_gated_act(x, wg, wu, N, K, dt, act=act)
+    h = hipq.matmul_q_gated(x, wg, wu, N, K, dt, act=act)
+    want = hipq.quantize_act(h)
+    torch.cuda.synchronize()
+    assert got.shape == want.shape
+    # The defined regions of the act layout (q1, q2, (d, e), sx); the rounding gaps between
+    # them are not written.
+    q2o = (M * N + 255) & ~255
+    do = 2 * q2o
+    so = do + 8 * M * (N // 32)
+    for name, a, b in (("q1", 0, M * N), ("q2", q2o, q2o + M * N), ("de", do, so), ("sx", so, so + 4 * M * (N // 32))):
+        assert torch.equal(got[a:b], want[a:b]), name
