@@ -1,6 +1,7 @@
 """Seeded random shapes through every dispatch path of MatMulQ (GGUF bytes, the Q6_K_R layout
-and prepared activations), dequant, MatMulInt4, MoEGemmQ, the fused gated projection and MLP,
-MoERoute, the fused MoE blocks and MoEInt4.
+and prepared activations), dequant, MatMulInt4 (with DequantizeInt4 and the GPTQ / AWQ
+conversions), MoEGemmQ, the fused gated projection and MLP, MoERoute, the fused MoE blocks and
+MoEInt4.
 
 Each entry point picks among several kernels by M, N, K, the group size and the x dtype
 (decode GEMVs, staged GEMVs, the one-launch and split-K int4 kernels, the MFMA GEMMs).  The
@@ -22,6 +23,8 @@ from test_gpu_gated import _check as check_gated, _check_mlp as check_mlp
 from test_gpu_int4 import _check as check_int4, light_int4
 from test_gpu_matmul_q import _check_matmul
 from test_gpu_int4 import test_moe_int4_vs_light_cpu as check_moe_int4
+from test_gpu_int4_convert import test_from_awq_bit_exact as check_awq
+from test_gpu_int4_convert import test_from_gptq_bit_exact as check_gptq
 from test_gpu_moe import _check as check_moe
 from test_gpu_moe import test_moe_block_equals_route_gated_then_combine as check_moe_block
 from test_gpu_moe import test_moe_route_bit_exact as check_route
@@ -305,3 +308,39 @@ def test_gated_act_random_shape(dev, dt, M, N, K, act):
     so = do + 8 * M * (N // 32)
     for name, a, b in (("q1", 0, M * N), ("q2", q2o, q2o + M * N), ("de", do, so), ("sx", so, so + 4 * M * (N // 32))):
         assert torch.equal(got[a:b], want[a:b]), name
+
+
+def _int4_layout_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        G = int(rng.choice((32, 64, 128)))
+        K = G * int(rng.integers(1, 12288 // G + 1))
+        N = 8 * int(rng.integers(1, 3000))
+        out.append((K, N, G, bool(i % 2), bool((i // 2) % 2)))
+    return out
+
+
+@pytest.mark.parametrize("K,N,G,v2,act_order", _int4_layout_cases(12, 18336))
+def test_from_gptq_random_shape(dev, K, N, G, v2, act_order):
+    check_gptq(dev, K, N, G, v2, act_order)
+
+
+@pytest.mark.parametrize("K,N,G,v2,act_order", _int4_layout_cases(8, 19360))
+def test_from_awq_random_shape(dev, K, N, G, v2, act_order):
+    check_awq(dev, K, N, G)
+
+
+@pytest.mark.parametrize("K,N,G,v2,act_order", _int4_layout_cases(10, 20384))
+@pytest.mark.parametrize("odt", [hipq.F32, hipq.BF16])
+def test_dequantize_int4_random_shape(dev, K, N, G, v2, act_order, odt):
+    """Bit-exact DequantizeInt4 at random sizes (v2 / act_order unused)."""
+    print(f"[case] int4_dequant N={N} K={K} G={G} odt={odt}", flush=True)
+    rng = np.random.default_rng(N * 31 + K + G)
+    codes, sc, z = light_int4(rng, N, K, G)
+    got = hipq.int4_dequant(_t(codes, dev), _t(sc, dev), _t(z, dev), G, odt).cpu()
+    want = oracle.int4_dequant(codes, sc, z, N, K, G, odt)
+    if odt == hipq.F32:
+        assert np.array_equal(got.numpy().view(np.uint32), want.view(np.uint32))
+    else:
+        assert np.array_equal(got.view(torch.int16).numpy().view(np.uint16), want)
