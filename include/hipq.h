@@ -98,6 +98,12 @@ int hq_trace_stop(char *names, int *calls, double *total_us, int n_max);
 
 /* ---- ops ----------------------------------------------------------------- */
 
+/* Pointers: activations (x, act, h) and GGUF weight buffers start 16-byte aligned, F32 outputs
+ * 4-byte aligned (hipMalloc and torch allocations are 256-byte aligned); a misaligned base
+ * pointer is HQ_EINVAL, never a silent misread.  Row lengths need no alignment: rows whose
+ * byte length is not a multiple of 16 take the generic paths named below.  Empty operands
+ * (M, N or T = 0) return HQ_OK and launch nothing. */
+
 /* Workspace bytes hq_matmul_q needs for x (M, K), a weight (N, K) and w_dtype. */
 size_t hq_matmul_q_ws_bytes(int64_t M, int64_t N, int64_t K, int w_dtype);
 
@@ -111,7 +117,8 @@ size_t hq_matmul_q_ws_bytes(int64_t M, int64_t N, int64_t K, int w_dtype);
  *    workgroups up to K = 8192, into ws above).
  *  - M > 8 (K % 64 == 0): the bf16 MFMA GEMM; x is rounded to bf16 in ws; Q4_K tiles are
  *    dequantized inside the GEMM, the other formats once to a bf16 copy in ws.
- *  - Rows that are not 16-byte aligned: a generic F32 GEMV with the bit-exact decoder.
+ *  - Rows whose byte length is not a multiple of 16: a generic F32 GEMV with the bit-exact
+ *    decoder.
  * Replaces registry kernel "matmul_q" (ops/matmul_q.go:61-75; CUDA launcher
  * kernels/cuda/matmul_q.go:44-91) and, since it serves every M, the M >= 8
  * dequant + cuBLAS fallback (ops/matmul_q.go:52-59, 85-95). */
