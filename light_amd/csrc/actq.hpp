@@ -6,6 +6,11 @@
 // d = amax / 127, id = 1 / d, q1 = RoundToEven(v * id).  Level 2 quantizes the residual
 // r = v - d*q1 at step e = d / 254 (|q2| <= 127).  sum is the block's f32 sum, reduced
 // pairwise in lane order so every caller gets the same bits.
+//
+// Non-finite x: fmaxf drops a NaN from amax, so a block holding one would quantize to
+// finite codes.  A NaN block sum (a NaN, or +Inf with -Inf, in the block) sets d and e to
+// NaN instead, and an Inf sets d to Inf: either way every dot over the block is NaN, as
+// Light's F32 arithmetic gives a non-finite result for that row.
 #pragma once
 
 #include "common.hpp"
@@ -28,6 +33,12 @@ __device__ __forceinline__ float dpp8f(float v) {
 template <int CTRL>
 __device__ __forceinline__ int dpp8i(int v) {
   return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+
+// d and e of a block whose sum is NaN become NaN (see the header).
+template <class Q>
+__device__ __forceinline__ void poison_nan_block(Q &r) {
+  if (r.sum != r.sum) r.d = r.e = r.sum;
 }
 
 __device__ __forceinline__ ActQ act_quant8(const float v[4]) {
@@ -63,6 +74,7 @@ __device__ __forceinline__ ActQ act_quant8(const float v[4]) {
   qs += dpp8i<0x141>(qs);
   r.sum = bsum;
   r.qsum = qs;
+  poison_nan_block(r);
   return r;
 }
 
@@ -96,6 +108,7 @@ __device__ __forceinline__ ActQ act_quant8_fast(const float v[4]) {
   bsum += dpp8f<0x141>(bsum);
   r.sum = bsum;
   r.qsum = 0;
+  poison_nan_block(r);
   return r;
 }
 
@@ -143,6 +156,7 @@ __device__ __forceinline__ ActQ16 act_quant16_fast(const float (&v)[16]) {
 #pragma unroll
   for (int j = 0; j < 16; j += 4) s += (v[j] + v[j + 1]) + (v[j + 2] + v[j + 3]);
   r.sum = s + dpp8f<0xB1>(s);
+  poison_nan_block(r);
   return r;
 }
 
