@@ -6,6 +6,7 @@
 
 #include <algorithm>
 #include <map>
+#include <atomic>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -15,7 +16,7 @@
 namespace hq {
 
 static thread_local char g_err[512] = "";
-static hipStream_t g_current = nullptr;
+static std::atomic<hipStream_t> g_current{nullptr};  // hq_stream_set_current, from any thread
 
 int fail(int code, const char *call, const char *fmt, ...) {
   char msg[400];
@@ -32,7 +33,7 @@ int check(hipError_t e, const char *call) {
   return fail((int)e, call, "%s", hipGetErrorString(e));
 }
 
-hipStream_t resolve(hq_stream_t s) { return s ? (hipStream_t)s : g_current; }
+hipStream_t resolve(hq_stream_t s) { return s ? (hipStream_t)s : g_current.load(); }
 
 // Library-owned workspace for calls made with ws == NULL, one buffer per (device, stream):
 // work on one stream runs in order, so a stream's buffer is never used by two kernels at
@@ -252,7 +253,8 @@ int hq_stream_create(hq_stream_t *stream) {
 int hq_stream_destroy(hq_stream_t stream) {
   if (!stream) return HQ_OK;
   hipStream_t s = (hipStream_t)stream;
-  if (s == g_current) g_current = nullptr;
+  hipStream_t cur = s;
+  g_current.compare_exchange_strong(cur, nullptr);
   // The stream's library workspace goes with it (its last kernels have finished first).
   if (int rc = check(hipStreamSynchronize(s), "hipStreamSynchronize")) return rc;
   if (int rc = workspace_forget_stream(s)) return rc;
@@ -269,7 +271,7 @@ int hq_stream_set_current(hq_stream_t stream) {
   return HQ_OK;
 }
 
-hq_stream_t hq_stream_get_current(void) { return (hq_stream_t)g_current; }
+hq_stream_t hq_stream_get_current(void) { return (hq_stream_t)g_current.load(); }
 
 int hq_trace_start(void) {
   std::lock_guard<std::mutex> lk(g_tr_mu);

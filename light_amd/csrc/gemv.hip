@@ -32,6 +32,7 @@
 #include "decode.hpp"
 #include "internal.hpp"
 
+#include <atomic>
 #include <mutex>
 
 namespace hq {
@@ -835,13 +836,13 @@ static void run_staged_x(int dt, StagedArgs a, int ns, hipStream_t s) {
   a.lds_wave = staged_slice(R, a.row_bytes);
   a.ns = ns;
   const int lds = 4 * ns * a.lds_wave + (XIN ? (int)staged_xin_lds(MM, a.K) : 0);
-  static bool attr_done = false;
-  if (!attr_done) {
+  static std::atomic<bool> attr_done{false};  // (idempotent: racing callers both set it)
+  if (!attr_done.load(std::memory_order_acquire)) {
     allow_big_lds(&gemv_q80_kernel<Q8_0, CPL, R, MM, XIN, X1>);
     allow_big_lds(&gemv_q80_kernel<Q4_0, CPL, R, MM, XIN, X1>);
     allow_big_lds(&gemv_q80_kernel<Q5_0, CPL, R, MM, XIN, X1>);
     allow_big_lds(&gemv_q6k_kernel<CPL, R, MM, XIN, X1>);
-    attr_done = true;
+    attr_done.store(true, std::memory_order_release);
   }
   const int per_cu = (160 * 1024) / lds;
   // At least two row groups per wave where N allows (the workgroup's x quantization and the

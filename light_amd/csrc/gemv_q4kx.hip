@@ -37,6 +37,7 @@
 #include "route.hpp"
 
 #include <algorithm>
+#include <atomic>
 #include <mutex>
 
 namespace hq {
@@ -1946,12 +1947,12 @@ static int run_q4kx(const Q4kxArgs &a, hipStream_t s) {
   auto *kern = &gemv_q4kx_kernel<U, MM, GATED, XIN, AOUT, XDT, ODT, ROWS>;
   const size_t lds = q4kx_lds(MM, a.K, a.TP, a.RW, GATED ? 2 : ROWS, XIN, AOUT);
   if (lds > 64 * 1024) {
-    static bool attr_done = false;
-    if (!attr_done) {
+    static std::atomic<bool> attr_done{false};  // (idempotent: racing callers both set it)
+    if (!attr_done.load(std::memory_order_acquire)) {
       if (hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                               160 * 1024) != hipSuccess)
         return fail(HQ_EUNSUPPORTED, "gemv_q4kx", "LDS %zu bytes not available", lds);
-      attr_done = true;
+      attr_done.store(true, std::memory_order_release);
     }
   }
   const int span = ROWS * a.RW;

@@ -17,6 +17,8 @@
 // giving each pair its rank among equal ids of lower lanes.  Per-chunk counts [W][E] (u16
 // in LDS) are turned into exclusive offsets along the chunk axis per expert, the expert
 // totals are scanned, and every pair lands at base[e] + chunk offset + rank.
+#include <atomic>
+
 #include "internal.hpp"
 #include "route.hpp"
 
@@ -230,13 +232,13 @@ size_t route_lds(int64_t M, int64_t E) {
 int run_route(bool topk, const RouteArgs &a, hipStream_t s) {
   const size_t lds = route_lds(a.M, a.E);
   auto *kern = topk ? &moe_route_kernel<true> : &moe_route_kernel<false>;
-  static bool attr_done[2] = {false, false};
-  if (lds > 64 * 1024 && !attr_done[topk]) {
+  static std::atomic<bool> attr_done[2] = {false, false};  // (idempotent: racing callers both set it)
+  if (lds > 64 * 1024 && !attr_done[topk].load(std::memory_order_acquire)) {
     if (int rc = check(hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024),
                        "hipFuncSetAttribute"))
       return rc;
-    attr_done[topk] = true;
+    attr_done[topk].store(true, std::memory_order_release);
   }
   // One wave per chunk of 64 pairs (and per token for the top-k), up to 16 waves.
   int64_t waves = a.W > a.T ? a.W : a.T;
