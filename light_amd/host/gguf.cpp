@@ -381,8 +381,26 @@ const TensorInfo &File::Info(const std::string &name) const {
   return it->second;
 }
 
+// Before anything is allocated for a tensor's data: its byte range must be addressable and
+// its last byte readable.  A sized input was checked at Open; on an unsized one (a stream)
+// a header that lies about the size then fails as the short read Light's TensorBytes would
+// meet (gguf/reader.go:254-264), not as an allocation of the claimed size first.
+void File::ProbeData(const TensorInfo &ti, const std::string &name) const {
+  if (ti.bytes <= 0) return;
+  const uint64_t room = (uint64_t)INT64_MAX - (uint64_t)data_base;
+  if (ti.offset > room || (uint64_t)ti.bytes > room - ti.offset)
+    throw Error("gguf: read tensor " + q(name) + ": offset out of range");
+  uint8_t last;
+  try {
+    src_->ReadAt(&last, 1, data_base + (int64_t)(ti.offset + (uint64_t)ti.bytes - 1));
+  } catch (const Error &e) {
+    wrap("gguf: read tensor " + q(name), e);
+  }
+}
+
 std::vector<uint8_t> File::TensorBytes(const std::string &name) const {
   const TensorInfo &ti = Info(name);
+  ProbeData(ti, name);
   std::vector<uint8_t> buf((size_t)ti.bytes);
   try {
     src_->ReadAt(buf.data(), buf.size(), data_base + (int64_t)ti.offset);
@@ -413,6 +431,7 @@ void File::CopyTensorTo(const std::string &name, void *dst, Device dev) const {
 
 Tensor File::LoadTensor(const std::string &name, Device dev) const {
   const TensorInfo &ti = Info(name);
+  ProbeData(ti, name);
   Tensor t = Tensor::Empty(ti.dtype, ti.dims, dev);
   CopyTensorTo(name, t.data(), dev);
   return t;
@@ -420,6 +439,7 @@ Tensor File::LoadTensor(const std::string &name, Device dev) const {
 
 Tensor File::TensorRowMajor(const std::string &name, Device dev) const {
   const TensorInfo &ti = Info(name);
+  ProbeData(ti, name);
   std::vector<int64_t> dims(ti.dims.rbegin(), ti.dims.rend());
   Tensor t = Tensor::Empty(ti.dtype, dims, dev);
   CopyTensorTo(name, t.data(), dev);
@@ -513,11 +533,12 @@ ExpertStacks LoadExperts(const File &f, const std::string &p, Device dev) {
   const DType odt = widen ? DType::F32 : dt;
   const int64_t slab = ByteSize(dt, I * H), oslab = ByteSize(odt, I * H);  // one expert's (I, H) block
   ExpertStacks out;
-  out.gate_up = Tensor::Empty(odt, {E, 2 * I, H}, dev);
   // Expert e: its I gate rows, then its I up rows (models/llama_gguf.go:186-191), copied
-  // from the file's payloads straight into place.
+  // from the file's payloads straight into place (payloads read, or probed, before the
+  // stacks are allocated).
   std::vector<uint8_t> gt, ut;
   const uint8_t *gb = f.Payload(gi->first, &gt), *ub = f.Payload(ui->first, &ut);
+  out.gate_up = Tensor::Empty(odt, {E, 2 * I, H}, dev);
   for (int64_t e = 0; e < E; e++) {
     uint8_t *dst = static_cast<uint8_t *>(out.gate_up.data()) + 2 * e * oslab;
     put_slab(gb + e * slab, dt, I * H, dst, dev);
@@ -526,11 +547,12 @@ ExpertStacks LoadExperts(const File &f, const std::string &p, Device dev) {
   const TensorInfo &di = f.Info(p + "ffn_down_exps.weight");
   if (di.dtype == DType::F16 || di.dtype == DType::BF16) {
     std::vector<int64_t> dims(di.dims.rbegin(), di.dims.rend());
-    out.down = Tensor::Empty(DType::F32, dims, dev);
     std::vector<uint8_t> dt_;
+    const uint8_t *db = f.Payload(di.name, &dt_);
+    out.down = Tensor::Empty(DType::F32, dims, dev);
     int64_t n = 1;
     for (int64_t d : dims) n *= d;
-    put_slab(f.Payload(di.name, &dt_), di.dtype, n, static_cast<uint8_t *>(out.down.data()), dev);
+    put_slab(db, di.dtype, n, static_cast<uint8_t *>(out.down.data()), dev);
   } else {
     out.down = f.TensorRowMajor(p + "ffn_down_exps.weight", dev);
   }

@@ -96,6 +96,8 @@ class File {
   bool Float64(const std::string &key, double *out) const;
 
  private:
+  // The tensor's byte range is addressable and its last byte readable (before allocation).
+  void ProbeData(const TensorInfo &ti, const std::string &name) const;
   std::shared_ptr<Source> src_;
 };
 

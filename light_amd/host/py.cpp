@@ -101,6 +101,21 @@ py::str gguf_str(const std::string &s) {
   return py::reinterpret_steal<py::str>(o);
 }
 
+// The inverse, for names and keys passed in: a str (surrogateescape bytes kept) or bytes.
+std::string gguf_name(const py::object &o) {
+  if (py::isinstance<py::bytes>(o)) return o.cast<std::string>();
+  PyObject *b = PyUnicode_AsEncodedString(o.ptr(), "utf-8", "surrogateescape");
+  if (!b) throw py::error_already_set();
+  py::bytes bb = py::reinterpret_steal<py::bytes>(b);
+  return bb.cast<std::string>();
+}
+
+py::list gguf_strs(const std::vector<std::string> &v) {
+  py::list l;
+  for (const auto &x : v) l.append(gguf_str(x));
+  return l;
+}
+
 py::object value_to_py(const gguf::Value &v) {
   switch (v.type) {
     case gguf::TypeUInt8: case gguf::TypeUInt16: case gguf::TypeUInt32: case gguf::TypeUInt64:
@@ -246,15 +261,15 @@ PYBIND11_MODULE(_light, m) {
 
   // GGUF byte path
   py::class_<gguf::TensorInfo>(m, "GGUFTensorInfo")
-      .def_readonly("name", &gguf::TensorInfo::name)
+      .def_property_readonly("name", [](const gguf::TensorInfo &t) { return gguf_str(t.name); })
       .def_property_readonly("dtype", [](const gguf::TensorInfo &t) { return std::string(DTypeName(t.dtype)); })
       .def_readonly("dims", &gguf::TensorInfo::dims)
       .def_readonly("offset", &gguf::TensorInfo::offset)
       .def_readonly("bytes", &gguf::TensorInfo::bytes);
   py::class_<gguf::File, std::shared_ptr<gguf::File>>(m, "GGUFFile")
       .def_readonly("version", &gguf::File::version)
-      .def_readonly("order", &gguf::File::order)
-      .def_readonly("key_order", &gguf::File::key_order)
+      .def_property_readonly("order", [](const gguf::File &f) { return gguf_strs(f.order); })
+      .def_property_readonly("key_order", [](const gguf::File &f) { return gguf_strs(f.key_order); })
       .def_readonly("data_base", &gguf::File::data_base)
       .def_property_readonly("meta",
                              [](const gguf::File &f) {
@@ -262,31 +277,31 @@ PYBIND11_MODULE(_light, m) {
                                for (const auto &kv : f.meta) d[gguf_str(kv.first)] = value_to_py(kv.second);
                                return d;
                              })
-      .def("info", &gguf::File::Info, py::return_value_policy::copy)
+      .def("info", [](const gguf::File &f, const py::object &n) { return f.Info(gguf_name(n)); })
       .def("tensor_bytes",
-           [](const gguf::File &f, const std::string &n) {
-             std::vector<uint8_t> b = f.TensorBytes(n);
+           [](const gguf::File &f, const py::object &n) {
+             std::vector<uint8_t> b = f.TensorBytes(gguf_name(n));
              return py::bytes((const char *)b.data(), b.size());
            })
-      .def("load_tensor", [](const gguf::File &f, const std::string &n,
-                             const std::string &dev) { return f.LoadTensor(n, parse_device(dev)); },
+      .def("load_tensor", [](const gguf::File &f, const py::object &n,
+                             const std::string &dev) { return f.LoadTensor(gguf_name(n), parse_device(dev)); },
            py::arg("name"), py::arg("device") = "cpu")
-      .def("tensor_row_major", [](const gguf::File &f, const std::string &n,
-                                  const std::string &dev) { return f.TensorRowMajor(n, parse_device(dev)); },
+      .def("tensor_row_major", [](const gguf::File &f, const py::object &n,
+                                  const std::string &dev) { return f.TensorRowMajor(gguf_name(n), parse_device(dev)); },
            py::arg("name"), py::arg("device") = "cpu")
-      .def("string", [](const gguf::File &f, const std::string &k) -> py::object {
+      .def("string", [](const gguf::File &f, const py::object &k) -> py::object {
         std::string s;
-        if (!f.String(k, &s)) return py::none();
-        return py::str(s);
+        if (!f.String(gguf_name(k), &s)) return py::none();
+        return gguf_str(s);
       })
-      .def("int64", [](const gguf::File &f, const std::string &k) -> py::object {
+      .def("int64", [](const gguf::File &f, const py::object &k) -> py::object {
         int64_t v;
-        if (!f.Int64(k, &v)) return py::none();
+        if (!f.Int64(gguf_name(k), &v)) return py::none();
         return py::int_(v);
       })
-      .def("float64", [](const gguf::File &f, const std::string &k) -> py::object {
+      .def("float64", [](const gguf::File &f, const py::object &k) -> py::object {
         double v;
-        if (!f.Float64(k, &v)) return py::none();
+        if (!f.Float64(gguf_name(k), &v)) return py::none();
         return py::float_(v);
       });
   m.def(

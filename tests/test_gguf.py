@@ -278,3 +278,77 @@ def test_ggml_type_codes():
         assert L.dtype_from_ggml(code) == name
     with pytest.raises(L.Error, match="unsupported ggml type 99"):
         L.dtype_from_ggml(99)
+
+
+def test_unsized_lying_size_is_an_error_not_an_allocation():
+    """On an unsized input a tensor may claim more data than exists; loading it fails as the
+    short read of gguf/reader.go:254-264 before anything of the claimed size is allocated."""
+    w = Writer()
+    w.add_tensor("t", [1 << 44], 0, f32b(1, 2))  # 64 TiB claimed, 8 bytes present
+    f = L.gguf_open_bytes(w.bytes(), False)
+    for load in (f.load_tensor, f.tensor_row_major, f.tensor_bytes):
+        with pytest.raises(L.Error, match="read tensor"):
+            load("t")
+
+
+def test_non_utf8_names_round_trip():
+    """GGUF strings are bytes (Go strings): a name that is not UTF-8 is listed and loads."""
+    w = Writer()
+    name = b"blk.\xff\x80.w"
+    w.add_tensor(name, [2], 0, f32b(3, 4))
+    f = L.gguf_open_bytes(w.bytes())
+    (listed,) = f.order
+    assert listed.encode("utf-8", "surrogateescape") == name
+    assert f.load_tensor(listed).numpy().tolist() == [3, 4]
+    assert f.load_tensor(name).numpy().tolist() == [3, 4]
+    assert f.info(listed).name == listed
+
+
+_FUZZ = r"""
+import random, resource, sys
+resource.setrlimit(resource.RLIMIT_AS, (4 << 30, 4 << 30))
+import numpy as np
+from _gguf import ARR, STR, U32, Writer
+from light_amd import _light as L
+w = Writer()
+w.add("general.name", STR, "toy")
+w.add("tokenizer.tokens", ARR, (STR, ["a", "bb", "ccc"]))
+w.add("n", U32, 7)
+w.add_tensor("a", [8], 0, np.arange(8, dtype="<f4").tobytes())
+w.add_tensor("b", [32, 2], 2, bytes(range(36)))
+w.add_tensor("c", [4], 1, np.arange(4, dtype="<f2").tobytes())
+data = bytearray(w.bytes())
+rng = random.Random(int(sys.argv[1]))
+for it in range(int(sys.argv[2])):
+    d = bytearray(data)
+    for _ in range(rng.choice((1, 1, 2, 4, 8))):
+        i = rng.randrange(len(d)) if rng.random() < 0.5 else rng.randrange(min(len(d), 160))
+        d[i] = rng.choice((0, 0xFF, 0x7F, 0x80, rng.randrange(256)))
+    for sized in (True, False):
+        try:
+            f = L.gguf_open_bytes(bytes(d), sized)
+        except L.Error:
+            continue
+        for n in f.order:
+            f.info(n)
+            try:
+                f.load_tensor(n)
+            except L.Error:
+                pass
+print("done")
+"""
+
+
+@pytest.mark.parametrize("seed", [1, 2])
+def test_mutated_inputs_never_crash(seed):
+    """Random byte mutations of a valid file (header, metadata, tensor table, data): every one
+    opens or raises gguf's Error, and every listed tensor loads or raises it -- no crash, no
+    other exception and no allocation beyond a 4 GiB address-space cap (run in a child)."""
+    import os
+    import subprocess
+    import sys
+    here = os.path.dirname(os.path.abspath(__file__))
+    env = dict(os.environ, PYTHONPATH=os.pathsep.join([here, os.path.dirname(here), os.environ.get("PYTHONPATH", "")]))
+    r = subprocess.run([sys.executable, "-c", _FUZZ, str(seed), "5000"], capture_output=True, text=True, env=env,
+                       timeout=300)
+    assert r.returncode == 0 and r.stdout.strip() == "done", r.stderr[-2000:]
