@@ -274,28 +274,30 @@ static void run_i4_m(const I4Args &a, int mm, hipStream_t s) {
   }
 }
 
-static bool int4_gemm_ok(int64_t M, int G) { return M > 8 && G % 64 == 0; }
+// The MFMA GEMMs: M > 8, and rows too long for the int8 GEMV (K / 32 > 2048) at any M (their
+// x rows past M are clamped and their stores masked).
+static bool int4_gemm_ok(int64_t M, int64_t K, int G) { return (M > 8 || K / 32 > 2048) && G % 64 == 0; }
 
 size_t int4_ws_bytes(int64_t M, int64_t N, int64_t K, int G, int x_dtype) {
   if (M <= 0 || K <= 0 || K % 32) return 0;
-  if (!int4_gemm_ok(M, G)) return (size_t)act_bytes(M, K);
+  if (!int4_gemm_ok(M, K, G)) return (size_t)act_bytes(M, K);
   return (x_dtype == BF16 ? 0 : gemm_x_bytes(M, K)) + gemm_partial_bytes(M, N, K, x_dtype == F32);
 }
 
 int launch_int4_matmul(const void *x, int x_dtype, const uint32_t *codes, const float *s, const float *z, void *y,
                        int64_t M, int64_t N, int64_t K, int G, void *ws, hipStream_t st) {
   if (N > INT32_MAX || K > INT32_MAX) return fail(HQ_EUNSUPPORTED, "int4_matmul", "N or K too large");
-  if (int4_gemm_ok(M, G) && i4cu_ok(M, N, K, G, x_dtype, x, codes)) {
+  if (int4_gemm_ok(M, K, G) && i4cu_ok(M, N, K, G, x_dtype, x, codes)) {
     // F16 x at M <= 64 with enough column tiles to fill the chip: one workgroup per CU over
     // all of K, no split-K partials.
     return launch_i4cu(static_cast<const uint16_t *>(x), codes, s, z, y, M, N, K, G, st);
   }
-  if (int4_gemm_ok(M, G) && i4f16_small_ok(M, N, K, G, x_dtype, x, codes)) {
+  if (int4_gemm_ok(M, K, G) && i4f16_small_ok(M, N, K, G, x_dtype, x, codes)) {
     // F16 x at M <= 64: the exact-weight f16 MFMA kernel reads x as given.
     return launch_i4f16_small(static_cast<const uint16_t *>(x), codes, s, z, y,
                               reinterpret_cast<float *>(static_cast<char *>(ws) + gemm_x_bytes(M, K)), M, N, K, G, st);
   }
-  if (int4_gemm_ok(M, G)) {
+  if (int4_gemm_ok(M, K, G)) {
     const uint16_t *xb = static_cast<const uint16_t *>(x);
     char *rest = static_cast<char *>(ws);
     if (x_dtype != BF16) {

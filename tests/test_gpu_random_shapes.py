@@ -344,3 +344,26 @@ def test_dequantize_int4_random_shape(dev, K, N, G, v2, act_order, odt):
         assert np.array_equal(got.numpy().view(np.uint32), want.view(np.uint32))
     else:
         assert np.array_equal(got.view(torch.int16).numpy().view(np.uint16), want)
+
+
+@pytest.mark.parametrize("dt", _GGUF)
+@pytest.mark.parametrize("K", [32768, 53248, 73728])
+@pytest.mark.parametrize("M", [1, 3, 16])
+def test_matmul_q_long_rows(dev, dt, K, M):
+    """Rows past the decode kernels' team sizes (Llama-3-405B's FFN is K = 53248): each path
+    takes a kernel that covers them, within the bar."""
+    rng = np.random.default_rng(M * 7919 + K + dt)
+    N = 64
+    w = random_blocks(rng, dt, N, K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    _check_matmul(dev, dt, x, w, N, K, "long rows")
+
+
+@pytest.mark.parametrize("K", [53248, 73728])
+@pytest.mark.parametrize("M", [1, 3, 16])
+@pytest.mark.parametrize("xdt", [hipq.F32, hipq.F16])
+def test_int4_long_rows(dev, K, M, xdt):
+    rng = np.random.default_rng(M + K + xdt)
+    codes, s, z = light_int4(rng, 64, K, 128)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    check_int4(dev, x, codes, s, z, 128, xdt)
