@@ -367,3 +367,21 @@ def test_int4_long_rows(dev, K, M, xdt):
     codes, s, z = light_int4(rng, 64, K, 128)
     x = rng.standard_normal((M, K)).astype(np.float32)
     check_int4(dev, x, codes, s, z, 128, xdt)
+
+
+@pytest.mark.parametrize("dt", [hipq.Q4_K, hipq.Q6_K, hipq.Q8_0])
+@pytest.mark.parametrize("K", [32768, 53248])
+@pytest.mark.parametrize("T", [1, 3, 64])
+def test_moe_gemm_q_long_rows(dev, dt, K, T):
+    g = synth.rng(T + K + dt)
+    E, topk, N = 4, 2, 64
+    w = synth.gguf_weight(dt, E * N, K, g)
+    ids, tw = synth.moe_routing(T, E, topk, g)
+    x = g.standard_normal((T, K)).astype(np.float32)
+    check_moe(dev, x, w, dt, E, N, K, ids, tw, topk, False)
+
+
+@pytest.mark.parametrize("H,I", [(32768, 256), (256, 53248)])
+@pytest.mark.parametrize("T", [1, 3])
+def test_moe_int4_long_rows(dev, H, I, T):
+    check_moe_int4(dev, T, 4, 2, H, I, 128, torch.float32)
