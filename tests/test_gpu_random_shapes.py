@@ -385,3 +385,11 @@ def test_moe_gemm_q_long_rows(dev, dt, K, T):
 @pytest.mark.parametrize("T", [1, 3])
 def test_moe_int4_long_rows(dev, H, I, T):
     check_moe_int4(dev, T, 4, 2, H, I, 128, torch.float32)
+
+
+@pytest.mark.parametrize("dt,M,H,I", [(hipq.Q4_K, 1, 4096, 53248), (hipq.Q4_K, 3, 16384, 2048),
+                                      (hipq.Q6_K, 1, 16384, 4096), (hipq.Q8_0, 2, 2048, 40960)])
+def test_mlp_long_rows(dev, dt, M, H, I):
+    """Llama-3-405B-sized rows (H = 16384, I = 53248) through the gated projection and the MLP."""
+    check_gated(dev, dt, M, min(I, 8192), H, hipq.ACT_SILU, seed=M + H + I)
+    check_mlp(dev, dt, M, H, I, hipq.ACT_SILU, seed=M + H + I)
