@@ -1030,7 +1030,11 @@ static size_t gemm_ws(int64_t M, int64_t N, int64_t K, int dt) {
 
 size_t matmul_q_ws_bytes(int64_t M, int64_t N, int64_t K, int dt) {
   if (M <= 0 || K <= 0 || K % 32) return 0;
-  return use_gemm(M, dt) && gemm_k_ok(K) ? gemm_ws(M, N, K, dt) : (size_t)act_bytes(M, K);
+  if (use_gemm(M, dt) && gemm_k_ok(K)) return gemm_ws(M, N, K, dt);
+  // Long Q4_K / Q5_K rows: x quantized once, then the second K half's outputs.
+  if ((dt == Q4_K || dt == Q5_K) && K > 32768 && K <= 65536 && K % 256 == 0)
+    return (size_t)(al256(act_bytes(M, K)) + 4 * M * N);
+  return (size_t)act_bytes(M, K);
 }
 
 size_t matmul_act_ws_bytes(int64_t M, int64_t N, int64_t K, int dt) {
@@ -1074,6 +1078,12 @@ int launch_matmul_q(const float *x, const void *w, float *out, int64_t M, int64_
   }
   if ((dt == Q4_K || dt == Q5_K) && q4kx_ok(M, N, K, w, nullptr, x, dt) && q4kx_xin(K))
     return launch_gemv_q4kx(x, w, nullptr, out, M, N, K, 0, dt, s);
+  if (q4kx_halves_ok(M, N, K, dt, w, x)) {
+    // Rows longer than one team: x quantized once, then the two K halves and their sum.
+    if (int rc = launch_quantize_act(x, F32, ws, M, K, s)) return rc;
+    float *tmp = reinterpret_cast<float *>(static_cast<char *>(ws) + al256(act_bytes(M, K)));
+    return launch_gemv_q4kx_act_halves(ws, w, out, tmp, M, N, K, dt, s);
+  }
   if (!gemv_fast_ok(dt, K, w) || (dt == Q5_K && !q4kx_ok(1, N, K, w, nullptr, x, dt)))
     return launch_gemv_generic(x, w, out, M, N, K, dt, s);
   if (dt != Q4_K && dt != Q5_K && K <= kStagedXinMaxK && ((uintptr_t)x & 15) == 0)

@@ -2214,6 +2214,52 @@ int launch_gemv_q4kx_act(const void *act_in, const void *w, float *out, int64_t 
   });
 }
 
+// Rows longer than one team (Q4_K / Q5_K, 32768 < K <= 65536, e.g. Llama-3-405B's down
+// projection, K = 53248): each x row's dot runs as two launches of the act GEMV above, one
+// per K half, on the full rows' stride -- the weight base moves by the first half's blocks
+// and the activation bases by its elements, so both halves read the same buffers in place --
+// then one launch adds the second half's outputs (in tmp) to the first's.
+__global__ void add_rows_kernel(float *out, const float *tmp, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] += tmp[i];
+}
+
+bool q4kx_halves_ok(int64_t M, int64_t N, int64_t K, int dt, const void *w, const void *act) {
+  if ((dt != Q4_K && dt != Q5_K) || M < 1 || M > kGemvMaxRows || K <= 32768 || K > 65536 || K % 256) return false;
+  const int64_t kh = (K / 2 + 255) / 256 * 256;
+  return q4kx_ok(1, N, kh, w, nullptr, act, dt) && (N + 1) * q4kx_row_bytes(dt, K) <= UINT32_MAX;
+}
+
+int launch_gemv_q4kx_act_halves(const void *act_in, const void *w, float *out, float *tmp, int64_t M, int64_t N,
+                                int64_t K, int dt, hipStream_t s) {
+  const int64_t kh = (K / 2 + 255) / 256 * 256;
+  const int64_t bb = dt == Q4_K ? 144 : 176;  // bytes per 256-element block
+  const int64_t q2 = act_q2_off(M, K), d = act_d_off(M, K), so = act_s_off(M, K);
+  const uint8_t *act = static_cast<const uint8_t *>(act_in);
+  for (int64_t m = 0; m < M; m++) {
+    for (int h = 0; h < 2; h++) {
+      const int64_t k0 = h ? kh : 0, kn = h ? K - kh : kh, e0 = m * K + k0;  // first element
+      Q4kxArgs a;
+      if (int rc = q4kx_setup(a, 1, N, kn, 256, q4kx_row_bytes(dt, K), "gemv_q4kx")) return rc;
+      a.ain = act + e0;
+      a.in_q2 = q2;                      // q2 base: act + q2 + e0
+      a.in_d = d + 8 * (e0 / 32) - e0;   // (d, e) base: act + d + 8 e0 / 32
+      a.in_s = so + 4 * (e0 / 32) - e0;  // sx base: act + s + 4 e0 / 32
+      a.w0 = static_cast<const uint8_t *>(w) + k0 / 256 * bb;
+      a.out = (h ? tmp : out) + m * N;
+      const int rc = with_qk_unit(dt, kn, [&](auto unit) {
+        using U = decltype(unit);
+        if (gemv_rows_ok(a)) return run_gemv_rows<U>(a, s);
+        return dispatch_q4kx<U, false, false, false, F32, F32, 2>(a, s);
+      });
+      if (rc) return rc;
+    }
+  }
+  const int64_t n = M * N;
+  add_rows_kernel<<<(unsigned)cdiv(n, 256), 256, 0, s>>>(out, tmp, n);
+  return check_launch("gemv_q4kx_halves");
+}
+
 // int4 GEMV on x (F32 / BF16 / F16) quantized in the kernel; y at x's dtype.
 bool int4x_ok(int64_t M, int64_t N, int64_t K, int G, const void *codes, const void *x) {
   int P, TP, RW;

@@ -92,6 +92,11 @@ int launch_gemv_q4kx(const float *x, const void *w0, const void *w1, float *out,
                      int act, int dt, hipStream_t s);
 int launch_gemv_q4kx_act(const void *act_in, const void *w, float *out, int64_t M, int64_t N, int64_t K, int dt,
                          hipStream_t s);
+// Q4_K / Q5_K rows of 32768 < K <= 65536 at M <= 8: the act GEMV on each K half, then an add
+// (tmp: M * N floats).
+bool q4kx_halves_ok(int64_t M, int64_t N, int64_t K, int dt, const void *w, const void *act);
+int launch_gemv_q4kx_act_halves(const void *act_in, const void *w, float *out, float *tmp, int64_t M, int64_t N,
+                                int64_t K, int dt, hipStream_t s);
 // int4 GEMV on x quantized in the kernel (M <= kGemvMaxRows, G % 32 == 0, K % 64 == 0).
 bool int4x_ok(int64_t M, int64_t N, int64_t K, int G, const void *codes, const void *x);
 int launch_gemv_int4x(const void *x, int x_dtype, const uint32_t *codes, const float *sc, const float *zr, void *y,

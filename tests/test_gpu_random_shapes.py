@@ -347,8 +347,8 @@ def test_dequantize_int4_random_shape(dev, K, N, G, v2, act_order, odt):
 
 
 @pytest.mark.parametrize("dt", _GGUF)
-@pytest.mark.parametrize("K", [32768, 53248, 73728])
-@pytest.mark.parametrize("M", [1, 3, 16])
+@pytest.mark.parametrize("K", [32768, 33024, 40960, 53248, 65536, 73728])
+@pytest.mark.parametrize("M", [1, 3, 8, 16])
 def test_matmul_q_long_rows(dev, dt, K, M):
     """Rows past the decode kernels' team sizes (Llama-3-405B's FFN is K = 53248): each path
     takes a kernel that covers them, within the bar."""
@@ -357,6 +357,18 @@ def test_matmul_q_long_rows(dev, dt, K, M):
     w = random_blocks(rng, dt, N, K)
     x = rng.standard_normal((M, K)).astype(np.float32)
     _check_matmul(dev, dt, x, w, N, K, "long rows")
+    # The prepared-activation entry: the same bar, or HQ_EUNSUPPORTED where the GEMV it would
+    # take cannot read the layout.
+    act = hipq.quantize_act(_t(x, dev))
+    ws = torch.empty(max(1, hipq.lib().hq_matmul_q_act_ws_bytes(M, N, K, dt)), dtype=torch.uint8, device=dev)
+    try:
+        got = hipq.matmul_q_act(act, _t(w, dev), M, N, K, dt, ws=ws).cpu().numpy()
+    except hipq.HipqError as e:
+        assert e.code == hipq.HQ_EUNSUPPORTED and M <= 8, str(e)
+        return
+    wd = oracle.dequant(dt, w, N * K).reshape(N, K)
+    ref, _, wn, xn = oracle.matmul_f64(x, wd)
+    assert norm_err(got, ref, wn, xn) <= 1e-3
 
 
 @pytest.mark.parametrize("K", [53248, 73728])
