@@ -417,6 +417,9 @@ struct StagedArgs {
   float *out;
   int M, N, K, nb;
   int64_t row_bytes, q2_off, d_off, s_off;
+  // Row stride in w and the byte offset of the staged part within each row: row_bytes and 0,
+  // except for a K part of rows too long to stage whole (then one row per group).
+  int64_t row_stride, k0_bytes;
   int lds_wave;  // bytes of one LDS slice (one row group)
   int ns;        // slices per wave: row groups are loaded ns - 1 ahead
 };
@@ -440,8 +443,10 @@ __device__ __forceinline__ void lds_unaligned(const uint8_t *lds, int o, uint32_
 // value is the number of loads issued (wave-uniform), for the wait that follows.
 __device__ __forceinline__ int staged_issue(const StagedArgs &a, uint8_t *slice, int64_t r0, int lane) {
   if (r0 >= a.N) return 0;
-  const int64_t total = (int64_t)a.N * a.row_bytes;
-  const int64_t base = r0 * a.row_bytes;
+  // Loads stay inside w (N rows of row_stride): lanes past the group's bytes re-read its last
+  // 16 bytes or read on into later bytes of w, landing in the slice's slack, which no dot reads.
+  const int64_t total = (int64_t)a.N * a.row_stride;
+  const int64_t base = r0 * a.row_stride + a.k0_bytes;
   const uint32_t dst = (uint32_t)(uintptr_t)slice;
   const int ni = a.lds_wave >> 10;
   for (int i = 0; i < ni; i++) {
@@ -929,6 +934,8 @@ static int launch_staged(const void *act, const float *x, const uint8_t *w, floa
   a.K = (int)K;
   a.nb = (int)(K / block_info(dt).elems);
   a.row_bytes = staged_row_bytes(dt, K);
+  a.row_stride = a.row_bytes;
+  a.k0_bytes = 0;
   a.q2_off = act_q2_off(M, K);
   a.d_off = act_d_off(M, K);
   a.s_off = act_s_off(M, K);
@@ -954,6 +961,76 @@ static int launch_staged(const void *act, const float *x, const uint8_t *w, floa
       run_staged_m<4, false>(dt, a, cpl, s);
   }
   return check_launch(dt == Q6_K ? "gemv_q6k" : "gemv_q80");
+}
+
+// Rows too long to stage whole (a Q6_K row of K = 53248 is 43,680 bytes; a slice holds at most
+// 16 KB): K parts of whole 8-block groups (16-byte aligned in every row), each staged one row
+// per group on the full row stride, for one x row at a time; the parts' outputs are summed.
+// Every part is longer than 4088 bytes, so the launcher's row-group choice is one row
+// (a group of several rows would need them contiguous).
+static bool staged_plan(int dt, int64_t nb, int64_t *size, int *parts) {
+  const BlockInfo bi = block_info(dt);
+  const int64_t upb = dt == Q6_K ? 8 : 1;  // lane units per block; at most 512 units per row part
+  const int64_t bmax = std::min<int64_t>((16384 - 16) / bi.bytes, 512 / upb) / 8 * 8;
+  if (bmax < 8 || nb % 8) return false;
+  const int p = (int)cdiv(nb, bmax);
+  if (p < 2 || p > 64) return false;
+  const int64_t sz = cdiv(cdiv(nb, p), 8) * 8, last = nb - (p - 1) * sz;
+  if (sz > bmax || last <= 0 || last * bi.bytes <= 4088 || sz * bi.bytes <= 4088) return false;
+  *size = sz;
+  *parts = p;
+  return true;
+}
+
+bool staged_parts_ok(int64_t M, int64_t N, int64_t K, int dt, const void *w, const void *x) {
+  if ((dt != Q8_0 && dt != Q4_0 && dt != Q5_0 && dt != Q6_K) || M < 1 || M > kGemvMaxRows || N < 1 ||
+      N > INT32_MAX || K <= 0 || K > INT32_MAX)
+    return false;
+  if (((uintptr_t)w & 15) || ((uintptr_t)x & 15)) return false;
+  const BlockInfo bi = block_info(dt);
+  if (K % bi.elems || gemv_fast_ok(dt, K, w)) return false;
+  const int64_t nb = K / bi.elems;
+  if ((nb * bi.bytes) % 16) return false;
+  int64_t sz;
+  int p;
+  return staged_plan(dt, nb, &sz, &p);
+}
+
+int launch_staged_parts(const void *act, const void *w, float *out, float *tmp, int64_t M, int64_t N, int64_t K,
+                        int dt, hipStream_t s) {
+  const BlockInfo bi = block_info(dt);
+  const int64_t nb = K / bi.elems, full = nb * bi.bytes;
+  int64_t sz;
+  int parts;
+  if (!staged_plan(dt, nb, &sz, &parts)) return fail(HQ_EUNSUPPORTED, "gemv", "K=%lld", (long long)K);
+  const int64_t q2 = act_q2_off(M, K), d = act_d_off(M, K), so = act_s_off(M, K);
+  for (int64_t m = 0; m < M; m++) {
+    for (int i = 0; i < parts; i++) {
+      const int64_t b0 = i * sz, nbp = std::min<int64_t>(sz, nb - b0), e0 = m * K + b0 * bi.elems;
+      StagedArgs a;
+      a.act = static_cast<const uint8_t *>(act) + e0;
+      a.x = nullptr;
+      a.w = static_cast<const uint8_t *>(w);
+      a.out = (i ? tmp : out) + m * N;
+      a.M = 1;
+      a.N = (int)N;
+      a.K = (int)(nbp * bi.elems);
+      a.nb = (int)nbp;
+      a.row_bytes = nbp * bi.bytes;
+      a.row_stride = full;
+      a.k0_bytes = b0 * bi.bytes;
+      a.q2_off = q2;                      // q2 base: act + q2 + e0
+      a.d_off = d + 8 * (e0 / 32) - e0;   // (d, e) base
+      a.s_off = so + 4 * (e0 / 32) - e0;  // sx base
+      a.lds_wave = 0;
+      a.ns = 2;
+      run_staged_m<1, false>(dt, a, pick_cpl(dt == Q6_K ? nbp * 8 : nbp), s);
+      if (int rc = check_launch(dt == Q6_K ? "gemv_q6k_parts" : "gemv_q80_parts")) return rc;
+      if (i)
+        if (int rc = launch_add_rows(out + m * N, tmp + m * N, N, s)) return rc;
+    }
+  }
+  return HQ_OK;
 }
 
 int launch_gemv_act(const void *act, const void *wv, float *out, int64_t M, int64_t N, int64_t K, int dt,
@@ -1034,6 +1111,9 @@ size_t matmul_q_ws_bytes(int64_t M, int64_t N, int64_t K, int dt) {
   // Long Q4_K / Q5_K rows: x quantized once, then the second K half's outputs.
   if ((dt == Q4_K || dt == Q5_K) && K > 32768 && K <= 65536 && K % 256 == 0)
     return (size_t)(al256(act_bytes(M, K)) + 4 * M * N);
+  // Long staged rows (split into K parts): the parts' outputs as well.
+  if ((dt == Q8_0 || dt == Q4_0 || dt == Q5_0 || dt == Q6_K) && staged_row_bytes(dt, K) + 16 > 16384)
+    return (size_t)(al256(act_bytes(M, K)) + 4 * M * N);
   return (size_t)act_bytes(M, K);
 }
 
@@ -1078,6 +1158,12 @@ int launch_matmul_q(const float *x, const void *w, float *out, int64_t M, int64_
   }
   if ((dt == Q4_K || dt == Q5_K) && q4kx_ok(M, N, K, w, nullptr, x, dt) && q4kx_xin(K))
     return launch_gemv_q4kx(x, w, nullptr, out, M, N, K, 0, dt, s);
+  if (staged_parts_ok(M, N, K, dt, w, x)) {
+    // Staged rows too long for one slice: x quantized once, then the K parts and their sum.
+    if (int rc = launch_quantize_act(x, F32, ws, M, K, s)) return rc;
+    float *tmp = reinterpret_cast<float *>(static_cast<char *>(ws) + al256(act_bytes(M, K)));
+    return launch_staged_parts(ws, w, out, tmp, M, N, K, dt, s);
+  }
   if (q4kx_halves_ok(M, N, K, dt, w, x)) {
     // Rows longer than one team: x quantized once, then the two K halves and their sum.
     if (int rc = launch_quantize_act(x, F32, ws, M, K, s)) return rc;

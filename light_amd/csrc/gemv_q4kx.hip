@@ -2255,9 +2255,12 @@ int launch_gemv_q4kx_act_halves(const void *act_in, const void *w, float *out, f
       if (rc) return rc;
     }
   }
-  const int64_t n = M * N;
+  return launch_add_rows(out, tmp, M * N, s);
+}
+
+int launch_add_rows(float *out, const float *tmp, int64_t n, hipStream_t s) {
   add_rows_kernel<<<(unsigned)cdiv(n, 256), 256, 0, s>>>(out, tmp, n);
-  return check_launch("gemv_q4kx_halves");
+  return check_launch("add_rows");
 }
 
 // int4 GEMV on x (F32 / BF16 / F16) quantized in the kernel; y at x's dtype.
