@@ -117,6 +117,9 @@ size_t hq_matmul_q_ws_bytes(int64_t M, int64_t N, int64_t K, int w_dtype);
  *    workgroups up to K = 8192, into ws above).
  *  - M > 8 (K % 64 == 0): the bf16 MFMA GEMM; x is rounded to bf16 in ws; Q4_K tiles are
  *    dequantized inside the GEMM, the other formats once to a bf16 copy in ws.
+ *  - M <= 8, rows longer than one GEMV team (Q4_K / Q5_K, 32768 < K <= 65536) or one LDS
+ *    slice (the staged formats past 16 KB per row): x quantized into ws once, the GEMV over
+ *    K parts on the full row stride, the parts' outputs summed in ws.
  *  - Rows whose byte length is not a multiple of 16: a generic F32 GEMV with the bit-exact
  *    decoder.
  * Replaces registry kernel "matmul_q" (ops/matmul_q.go:61-75; CUDA launcher
