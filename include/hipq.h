@@ -208,7 +208,8 @@ size_t hq_matmul_q_act_ws_bytes(int64_t M, int64_t N, int64_t K, int w_dtype);
 /* out (M, N) F32 = x @ dequant(w)^T from prepared activations.  For M <= 8, and for
  * any M when K is not a multiple of 64, the weight must take the int8 GEMV (16-byte
  * aligned, rows a multiple of 16 bytes; HQ_EUNSUPPORTED otherwise -- hq_matmul_q takes
- * every layout). */
+ * every layout); rows longer than one GEMV team or LDS slice run as K parts, summed in ws
+ * (M * N floats). */
 int hq_matmul_q_act(const void *act, const void *w, float *out, int64_t M, int64_t N, int64_t K, int w_dtype,
                     void *ws, size_t ws_bytes, hq_stream_t stream);
 

@@ -496,8 +496,10 @@ int hq_matmul_q_act(const void *act, const void *w, float *out, int64_t M, int64
   if (!act || !w || !out) return fail(HQ_EINVAL, call, "NULL pointer");
   if (((uintptr_t)act & 15) || ((uintptr_t)out & 3)) return fail(HQ_EINVAL, call, "act must be 16-byte aligned");
   // Calls that take the GEMV (M <= 8, or K not a multiple of the GEMM's 64-k step) read the
-  // weight through the int8 GEMV, whose rows must be whole 16-byte pieces.
-  if (!matmul_act_takes_gemm(M, K, w_dtype) && !gemv_fast_ok(w_dtype, K, w))
+  // weight through the int8 GEMV, whose rows must be whole 16-byte pieces (rows longer than
+  // one team or slice run as K parts).
+  if (!matmul_act_takes_gemm(M, K, w_dtype) && !gemv_fast_ok(w_dtype, K, w) &&
+      !act_long_rows_ok(M, N, K, w_dtype, w, act))
     return fail(HQ_EUNSUPPORTED, call, "weight layout needs the F32 path (hq_matmul_q)");
   hipStream_t s = resolve(stream);
   size_t need = hq_matmul_q_act_ws_bytes(M, N, K, w_dtype);

@@ -1117,9 +1117,21 @@ size_t matmul_q_ws_bytes(int64_t M, int64_t N, int64_t K, int dt) {
   return (size_t)act_bytes(M, K);
 }
 
+// Long rows split into K parts (act_long_rows_ok) need the later parts' outputs.
+static bool long_rows_dt(int64_t K, int dt) {
+  return ((dt == Q4_K || dt == Q5_K) && K > 32768 && K <= 65536 && K % 256 == 0) ||
+         ((dt == Q8_0 || dt == Q4_0 || dt == Q5_0 || dt == Q6_K) && staged_row_bytes(dt, K) + 16 > 16384);
+}
+
 size_t matmul_act_ws_bytes(int64_t M, int64_t N, int64_t K, int dt) {
   if (M <= 0 || K <= 0 || K % 32) return 0;
-  return use_gemm(M, dt) && gemm_k_ok(K) ? gemm_ws(M, N, K, dt) : 0;
+  if (use_gemm(M, dt) && gemm_k_ok(K)) return gemm_ws(M, N, K, dt);
+  return long_rows_dt(K, dt) && N > 0 ? (size_t)(4 * M * N) : 0;
+}
+
+bool act_long_rows_ok(int64_t M, int64_t N, int64_t K, int dt, const void *w, const void *act) {
+  return !matmul_act_takes_gemm(M, K, dt) &&
+         (q4kx_halves_ok(M, N, K, dt, w, act) || staged_parts_ok(M, N, K, dt, w, act));
 }
 
 const char *matmul_q_kernel_name(int64_t M, int dt) { return use_gemm(M, dt) ? "matmul_q.gemm" : "matmul_q.gemv"; }
@@ -1141,6 +1153,10 @@ static int run_gemm(const void *src, bool from_act, const void *w, float *out, i
 int launch_matmul_act(const void *act, const void *w, float *out, int64_t M, int64_t N, int64_t K, int dt, void *ws,
                       hipStream_t s) {
   if (matmul_act_takes_gemm(M, K, dt)) return run_gemm(act, true, w, out, M, N, K, dt, ws, s);
+  if (staged_parts_ok(M, N, K, dt, w, act))
+    return launch_staged_parts(act, w, out, static_cast<float *>(ws), M, N, K, dt, s);
+  if (q4kx_halves_ok(M, N, K, dt, w, act))
+    return launch_gemv_q4kx_act_halves(act, w, out, static_cast<float *>(ws), M, N, K, dt, s);
   return launch_gemv_act(act, w, out, M, N, K, dt, s);
 }
 

@@ -44,6 +44,8 @@ constexpr int64_t kGemvMaxRows = 8;
 bool use_gemm(int64_t M, int dt);
 // hq_matmul_q_act runs the MFMA GEMM (else the int8 GEMV on the prepared activations).
 bool matmul_act_takes_gemm(int64_t M, int64_t K, int dt);
+// hq_matmul_q_act runs long rows as K parts (ws: M * N floats).
+bool act_long_rows_ok(int64_t M, int64_t N, int64_t K, int dt, const void *w, const void *act);
 int launch_gemm_ws_bf16(const uint16_t *xb, const uint16_t *wb, float *out, float *partials, int64_t M, int64_t N,
                         int64_t K, hipStream_t s);
 size_t matmul_q_ws_bytes(int64_t M, int64_t N, int64_t K, int dt);

@@ -357,14 +357,17 @@ def test_matmul_q_long_rows(dev, dt, K, M):
     w = random_blocks(rng, dt, N, K)
     x = rng.standard_normal((M, K)).astype(np.float32)
     _check_matmul(dev, dt, x, w, N, K, "long rows")
-    # The prepared-activation entry: the same bar, or HQ_EUNSUPPORTED where the GEMV it would
-    # take cannot read the layout.
+    # The prepared-activation entry: the same bar (long rows run as K parts), HQ_EUNSUPPORTED
+    # only at M <= 8 for rows the int8 GEMV cannot read: Q4_K / Q5_K past two teams, or a row
+    # whose byte length is not a multiple of 16.
+    bpb = {hipq.Q4_0: 18, hipq.Q5_0: 22, hipq.Q8_0: 34, hipq.Q4_K: 144, hipq.Q5_K: 176, hipq.Q6_K: 210}[dt]
+    refusable = (K // _BLOCK[dt] * bpb) % 16 != 0 or (dt in (hipq.Q4_K, hipq.Q5_K) and K > 65536)
     act = hipq.quantize_act(_t(x, dev))
     ws = torch.empty(max(1, hipq.lib().hq_matmul_q_act_ws_bytes(M, N, K, dt)), dtype=torch.uint8, device=dev)
     try:
         got = hipq.matmul_q_act(act, _t(w, dev), M, N, K, dt, ws=ws).cpu().numpy()
     except hipq.HipqError as e:
-        assert e.code == hipq.HQ_EUNSUPPORTED and M <= 8, str(e)
+        assert e.code == hipq.HQ_EUNSUPPORTED and M <= 8 and refusable, str(e)
         return
     wd = oracle.dequant(dt, w, N * K).reshape(N, K)
     ref, _, wn, xn = oracle.matmul_f64(x, wd)
