@@ -542,3 +542,31 @@ def test_moe_block_barrier_gives_up_loudly(dev):
         y3 = hipq.moe_block_q(probs, x, wgu, wdn, E, H, I, dt, topk)[0]
         hipq.moe_block_q_check()
         assert torch.equal(y3, want)
+
+
+@pytest.mark.parametrize("dt", [hipq.Q4_K, hipq.Q8_0])
+@pytest.mark.parametrize("T", [3, 64])
+def test_moe_out_of_range_expert_ids_are_skipped(dev, dt, T):
+    """Expert ids outside [0, E) in a sorted routing (-1 before, E after the valid ones) form no
+    expert segment: those pairs read no weights, and every valid pair's row equals the run
+    without them (the grouped kernels index experts only through the counts / offsets of
+    [0, E), and the segment-search GEMV skips a segment whose expert is out of range)."""
+    print(f"[case] moe out-of-range ids dt={hipq.NAMES[dt]} T={T}", flush=True)
+    g = synth.rng(40 + T + dt)
+    E, topk, N, K = 8, 2, 64, 512
+    w = _t(synth.gguf_weight(dt, E * N, K, g), dev)
+    ids, tw = synth.moe_routing(T, E, topk, g)
+    x = _t(g.standard_normal((T, K)).astype(np.float32), dev)
+    se, sp = synth.sort_pairs(ids)
+    M = ids.size
+    se_bad = se.copy()
+    se_bad[0], se_bad[1], se_bad[-1] = -1, -1, E
+    se_bad = np.sort(se_bad, kind="stable")  # still sorted: -1s first, E last
+    ref = torch.zeros((M, N), device=dev)
+    hipq.moe_gemm_q(x, w, _t(sp, dev), _t(se, dev), E, N, K, dt, topk, out=ref)
+    out = torch.zeros((M, N), device=dev)
+    hipq.moe_gemm_q(x, w, _t(sp, dev), _t(se_bad, dev), E, N, K, dt, topk, out=out)
+    torch.cuda.synchronize()
+    pos_bad = {0, 1, M - 1}  # sorted positions given out-of-range experts
+    good_pairs = [int(sp[i]) for i in range(M) if i not in pos_bad]
+    assert torch.equal(out[good_pairs], ref[good_pairs])
