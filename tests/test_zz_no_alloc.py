@@ -39,6 +39,8 @@ def _noalloc(x, w, N, K, dt):
     (hipq.Q4_0, (2, 2048, 4096), (32, 512, 1024)),        # staged Q4_0 GEMV, then the GEMM
     (hipq.Q4_K, (2, 1024, 12288), (1, 512, 9216)),        # K > 8192 at small M: x quantized into scratch
     (hipq.Q5_K, (1, 2048, 10240), (3, 512, 8448)),
+    (hipq.Q4_K, (1, 4096, 53248), (3, 512, 40960)),       # long rows: two K halves + their sum in scratch
+    (hipq.Q6_K, (1, 2048, 53248), (2, 256, 20480)),       # staged K parts + their sums in scratch
 ])
 def test_noalloc_matches_matmul_q(dev, dt, big, small):
     for i, (M, N, K) in enumerate((big, small)):
