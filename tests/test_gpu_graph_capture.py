@@ -56,6 +56,8 @@ def _w(dt, N, K, seed, dev):
     (hipq.Q4_K, 512, 4096, 14336),   # MFMA GEMM, K split + reduce
     (hipq.Q8_0, 40, 1024, 2048),     # bf16 weight copy + GEMM
     (hipq.Q4_0, 24, 300, 2784),      # generic GEMV (rows of 1566 bytes)
+    (hipq.Q4_K, 1, 2048, 53248),     # long rows: two K halves + an add
+    (hipq.Q6_K, 2, 1024, 53248),     # staged K parts + adds, per x row
 ])
 def test_matmul_q_graph(dev, dt, M, N, K):
     print(f"[case] graph matmul_q dt={hipq.NAMES[dt]} M={M} N={N} K={K}", flush=True)
