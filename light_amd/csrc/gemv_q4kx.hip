@@ -53,6 +53,7 @@ struct Q4kxArgs {
   uint8_t *aout;           // AOUT: act layout of the (M, N) output
   int M, N, K, P, TP, RW;  // P: units per row (K/64); TP: team lanes; RW: teams per workgroup
   int G;                   // int4 group size
+  int gpr = 0;             // int4 scale / zero groups per row of s0 / z0 (0: K / G; a K part: the full row's)
   int64_t row_bytes;
   int64_t in_q2, in_d, in_s;     // act offsets of (M, K)
   int64_t out_q2, out_d, out_s;  // act offsets of (M, N)
@@ -266,12 +267,13 @@ struct Int4UnitT {
   __device__ static void load(const uint8_t *w, const float *s, const float *z, const Q4kxArgs &a, int row,
                               const Lane &L, W &r) {
     const __amdgpu_buffer_rsrc_t rs = span_rsrc(w, (uint32_t)a.N * (uint32_t)a.row_bytes);
-    const uint32_t gbytes = (uint32_t)a.N * (uint32_t)(a.K / a.G) * 4u;
+    const uint32_t gpr = (uint32_t)(a.gpr ? a.gpr : a.K / a.G);
+    const uint32_t gbytes = (uint32_t)a.N * gpr * 4u;
     const __amdgpu_buffer_rsrc_t rsc = span_rsrc(s, gbytes), rz = span_rsrc(z, gbytes);
     const uint32_t ro = (uint32_t)row * (uint32_t)a.row_bytes;
     r.q0 = bload16(rs, ro + L.coff);
     r.q1 = bload16(rs, ro + L.coff + 16);
-    const uint32_t go = (uint32_t)row * (uint32_t)(a.K / a.G) * 4u;
+    const uint32_t go = (uint32_t)row * gpr * 4u;
     r.sA = bload_f32(rsc, go + 4u * L.gA);
     r.zA = bload_f32(rz, go + 4u * L.gA);
     r.sB = bload_f32(rsc, go + 4u * L.gB);
@@ -2331,6 +2333,62 @@ int launch_gemv_int4x(const void *x, int x_dtype, const uint32_t *codes, const f
     case F16: return dispatch_q4kx<Int4Unit, false, true, false, F16, F16>(a, s);
     default: return fail(HQ_EUNSUPPORTED, "int4_gemv", "x dtype %d", x_dtype);
   }
+}
+
+// int4 rows past one team (32768 < K <= 65536, 256 % G == 0) at M <= 8: x quantized once,
+// the act GEMV over each K half on the full rows' strides (codes, scales and zeros bases moved
+// to the half; the scales' row stride is the full row's groups), both halves to F32 partials,
+// then one launch adds them and rounds once to y's dtype.
+template <int ODT>
+__global__ void add_halves_kernel(void *y, const float *t0, const float *t1, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) store_out<ODT>(y, i, t0[i] + t1[i]);
+}
+
+bool int4_halves_ok(int64_t M, int64_t N, int64_t K, int G, const void *codes, const void *x) {
+  if (M < 1 || M > kGemvMaxRows || K <= 32768 || K > 65536 || K % 256 || G <= 0 || 256 % G) return false;
+  const int64_t kh = (K / 2 + 255) / 256 * 256;
+  return int4x_ok(1, N, kh, G, codes, x) && (N + 1) * (K / 2) <= UINT32_MAX &&
+         N * (K / G) * 4 <= (int64_t)UINT32_MAX;
+}
+
+int launch_int4_halves(const void *x, int x_dtype, const uint32_t *codes, const float *sc, const float *zr, void *y,
+                       int64_t M, int64_t N, int64_t K, int G, void *ws, hipStream_t s) {
+  const int64_t kh = (K / 2 + 255) / 256 * 256;
+  if (int rc = launch_quantize_act(x, x_dtype, ws, M, K, s)) return rc;
+  const uint8_t *act = static_cast<const uint8_t *>(ws);
+  float *t0 = reinterpret_cast<float *>(static_cast<uint8_t *>(ws) + ((act_bytes(M, K) + 255) & ~(int64_t)255));
+  float *t1 = t0 + M * N;
+  const int64_t q2 = act_q2_off(M, K), d = act_d_off(M, K), so = act_s_off(M, K);
+  for (int64_t m = 0; m < M; m++) {
+    for (int h = 0; h < 2; h++) {
+      const int64_t k0 = h ? kh : 0, kn = h ? K - kh : kh, e0 = m * K + k0;
+      Q4kxArgs a;
+      if (int rc = q4kx_setup(a, 1, N, kn, 64, K / 2, "int4_gemv")) return rc;
+      a.ain = act + e0;
+      a.in_q2 = q2;
+      a.in_d = d + 8 * (e0 / 32) - e0;
+      a.in_s = so + 4 * (e0 / 32) - e0;
+      a.w0 = reinterpret_cast<const uint8_t *>(codes) + k0 / 2;
+      a.s0 = sc + k0 / G;
+      a.z0 = zr + k0 / G;
+      a.G = G;
+      a.gpr = (int)(K / G);
+      a.out = (h ? t1 : t0) + m * N;
+      const int rc = gemv_rows_ok(a) ? run_gemv_rows<Int4UnitT<false>, F32>(a, s)
+                                     : dispatch_q4kx<Int4UnitT<false>, false, false, false, F32, F32, 2>(a, s);
+      if (rc) return rc;
+    }
+  }
+  const int64_t n = M * N;
+  const unsigned g = (unsigned)cdiv(n, 256);
+  switch (x_dtype) {
+    case F32: add_halves_kernel<F32><<<g, 256, 0, s>>>(y, t0, t1, n); break;
+    case BF16: add_halves_kernel<BF16><<<g, 256, 0, s>>>(y, t0, t1, n); break;
+    case F16: add_halves_kernel<F16><<<g, 256, 0, s>>>(y, t0, t1, n); break;
+    default: return fail(HQ_EUNSUPPORTED, "int4_gemv", "x dtype %d", x_dtype);
+  }
+  return check_launch("int4_halves");
 }
 
 // ---------------------------------------------------------------------------

@@ -280,7 +280,11 @@ static bool int4_gemm_ok(int64_t M, int64_t K, int G) { return (M > 8 || K / 32 
 
 size_t int4_ws_bytes(int64_t M, int64_t N, int64_t K, int G, int x_dtype) {
   if (M <= 0 || K <= 0 || K % 32) return 0;
-  if (!int4_gemm_ok(M, K, G)) return (size_t)act_bytes(M, K);
+  if (!int4_gemm_ok(M, K, G)) {
+    // Long rows (two K halves): the halves' F32 partials as well.
+    const bool halves = M <= 8 && K > 32768 && K <= 65536 && K % 256 == 0 && G > 0 && 256 % G == 0;
+    return (size_t)(halves ? ((act_bytes(M, K) + 255) & ~(int64_t)255) + 8 * M * N : act_bytes(M, K));
+  }
   return (x_dtype == BF16 ? 0 : gemm_x_bytes(M, K)) + gemm_partial_bytes(M, N, K, x_dtype == F32);
 }
 
@@ -307,6 +311,7 @@ int launch_int4_matmul(const void *x, int x_dtype, const uint32_t *codes, const 
     }
     return launch_gemm_int4_bf16(xb, codes, s, z, y, x_dtype, reinterpret_cast<float *>(rest), M, N, K, G, st);
   }
+  if (int4_halves_ok(M, N, K, G, codes, x)) return launch_int4_halves(x, x_dtype, codes, s, z, y, M, N, K, G, ws, st);
   if (int4x_ok(M, N, K, G, codes, x)) return launch_gemv_int4x(x, x_dtype, codes, s, z, y, M, N, K, G, ws, st);
   if (int rc = launch_quantize_act(x, x_dtype, ws, M, K, st)) return rc;
   I4Args a;

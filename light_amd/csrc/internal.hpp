@@ -108,6 +108,11 @@ int launch_gemv_q4kx_act_halves(const void *act_in, const void *w, float *out, f
                                 int64_t K, int dt, hipStream_t s);
 // int4 GEMV on x quantized in the kernel (M <= kGemvMaxRows, G % 32 == 0, K % 64 == 0).
 bool int4x_ok(int64_t M, int64_t N, int64_t K, int G, const void *codes, const void *x);
+// int4 rows of 32768 < K <= 65536 (256 % G == 0) at M <= 8: two K halves + a combine
+// (ws: the act layout of x, then 2 * M * N floats).
+bool int4_halves_ok(int64_t M, int64_t N, int64_t K, int G, const void *codes, const void *x);
+int launch_int4_halves(const void *x, int x_dtype, const uint32_t *codes, const float *sc, const float *zr, void *y,
+                       int64_t M, int64_t N, int64_t K, int G, void *ws, hipStream_t s);
 int launch_gemv_int4x(const void *x, int x_dtype, const uint32_t *codes, const float *sc, const float *zr, void *y,
                       int64_t M, int64_t N, int64_t K, int G, void *ws, hipStream_t s);
 // Whether the decode GEMVs quantize x inside their workgroups at this K.
