@@ -255,7 +255,8 @@ size_t hq_int4_matmul_ws_bytes(int64_t M, int64_t N, int64_t K, int G, int x_dty
  * scales / zeros F32 (N, K/G); W = s * (code - z).  x_dtype F32, BF16 or F16;
  * y has x's dtype (F16 is an extension: Light takes F32 or BF16, ops/int4.go:70-72).
  * K % 32 == 0 and G % 32 == 0.  M <= 8 (or G % 64 != 0): x is quantized to q8_1
- * into ws and the int8-dot GEMV runs (K <= 65536); otherwise -- and for longer rows at
+ * into ws and the int8-dot GEMV runs (K <= 65536; rows past 32768 with 256 % G == 0 as two
+ * K halves whose F32 partials are summed in ws); otherwise -- and for longer rows at
  * any M when G % 64 == 0 -- the MFMA GEMMs run (F16 x at 8 < M <= 64 as given, else
  * rounded to bf16 into ws).  G % 64 != 0 with K > 65536 is HQ_EUNSUPPORTED.
  * Replaces registry kernel "int4_gemv" (ops/int4.go:87-99; kernels/cuda/int4.go:76-101)
