@@ -1110,7 +1110,7 @@ size_t matmul_q_ws_bytes(int64_t M, int64_t N, int64_t K, int dt) {
   if (use_gemm(M, dt) && gemm_k_ok(K)) return gemm_ws(M, N, K, dt);
   // Long Q4_K / Q5_K rows: x quantized once, then the second K half's outputs.
   if ((dt == Q4_K || dt == Q5_K) && K > 32768 && K <= 65536 && K % 256 == 0)
-    return (size_t)(al256(act_bytes(M, K)) + 4 * M * N);
+    return std::max((size_t)(al256(act_bytes(M, K)) + 4 * M * N), q4kx_halves_x_ws_bytes(M, N, K));
   // Long staged rows (split into K parts): the parts' outputs as well.
   if ((dt == Q8_0 || dt == Q4_0 || dt == Q5_0 || dt == Q6_K) && staged_row_bytes(dt, K) + 16 > 16384)
     return (size_t)(al256(act_bytes(M, K)) + 4 * M * N);
@@ -1181,7 +1181,9 @@ int launch_matmul_q(const float *x, const void *w, float *out, int64_t M, int64_
     return launch_staged_parts(ws, w, out, tmp, M, N, K, dt, s);
   }
   if (q4kx_halves_ok(M, N, K, dt, w, x)) {
-    // Rows longer than one team: x quantized once, then the two K halves and their sum.
+    // Rows longer than one team: x quantized once, then the two K halves and their sum
+    // (several rows of x: each half's columns quantized on their own, one launch per half).
+    if (M > 1) return launch_gemv_q4kx_halves_x(x, w, out, ws, M, N, K, dt, s);
     if (int rc = launch_quantize_act(x, F32, ws, M, K, s)) return rc;
     float *tmp = reinterpret_cast<float *>(static_cast<char *>(ws) + al256(act_bytes(M, K)));
     return launch_gemv_q4kx_act_halves(ws, w, out, tmp, M, N, K, dt, s);

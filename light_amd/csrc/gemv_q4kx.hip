@@ -2260,6 +2260,45 @@ int launch_gemv_q4kx_act_halves(const void *act_in, const void *w, float *out, f
   return launch_add_rows(out, tmp, M * N, s);
 }
 
+// The same halves for M >= 2 rows of F32 x: each half's columns of x are copied out and
+// quantized as an (M, kn) activation, so one launch serves every row of x and the weights
+// are read once per half (not once per row).  ws: the half's x, its act layout, then M * N
+// floats (q4kx_halves_x_ws_bytes).
+size_t q4kx_halves_x_ws_bytes(int64_t M, int64_t N, int64_t K) {
+  const int64_t kh = (K / 2 + 255) / 256 * 256;
+  auto al = [](int64_t b) { return (b + 255) & ~(int64_t)255; };
+  return (size_t)(al(4 * M * kh) + al(act_bytes(M, kh)) + 4 * M * N);
+}
+
+int launch_gemv_q4kx_halves_x(const float *x, const void *w, float *out, void *ws, int64_t M, int64_t N, int64_t K,
+                              int dt, hipStream_t s) {
+  const int64_t kh = (K / 2 + 255) / 256 * 256;
+  const int64_t bb = dt == Q4_K ? 144 : 176;
+  auto al = [](int64_t b) { return (b + 255) & ~(int64_t)255; };
+  float *xb = static_cast<float *>(ws);
+  uint8_t *ab = reinterpret_cast<uint8_t *>(ws) + al(4 * M * kh);
+  float *tmp = reinterpret_cast<float *>(ab + al(act_bytes(M, kh)));
+  for (int h = 0; h < 2; h++) {
+    const int64_t k0 = h ? kh : 0, kn = h ? K - kh : kh;
+    if (hipError_t e = hipMemcpy2DAsync(xb, (size_t)kn * 4, x + k0, (size_t)K * 4, (size_t)kn * 4, (size_t)M,
+                                        hipMemcpyDeviceToDevice, s))
+      return fail((int)e, "gemv_q4kx", "hipMemcpy2DAsync: %s", hipGetErrorString(e));
+    if (int rc = launch_quantize_act(xb, F32, ab, M, kn, s)) return rc;
+    Q4kxArgs a;
+    if (int rc = q4kx_setup(a, M, N, kn, 256, q4kx_row_bytes(dt, K), "gemv_q4kx")) return rc;
+    a.ain = ab;
+    a.w0 = static_cast<const uint8_t *>(w) + k0 / 256 * bb;
+    a.out = h ? tmp : out;
+    const int rc = with_qk_unit(dt, kn, [&](auto unit) {
+      using U = decltype(unit);
+      if (gemv_rows_ok(a)) return run_gemv_rows<U>(a, s);
+      return dispatch_q4kx<U, false, false, false, F32, F32, 2>(a, s);
+    });
+    if (rc) return rc;
+  }
+  return launch_add_rows(out, tmp, M * N, s);
+}
+
 int launch_add_rows(float *out, const float *tmp, int64_t n, hipStream_t s) {
   add_rows_kernel<<<(unsigned)cdiv(n, 256), 256, 0, s>>>(out, tmp, n);
   return check_launch("add_rows");

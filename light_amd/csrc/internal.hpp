@@ -97,6 +97,10 @@ int launch_gemv_q4kx_act(const void *act_in, const void *w, float *out, int64_t 
 // Q4_K / Q5_K rows of 32768 < K <= 65536 at M <= 8: the act GEMV on each K half, then an add
 // (tmp: M * N floats).
 bool q4kx_halves_ok(int64_t M, int64_t N, int64_t K, int dt, const void *w, const void *act);
+// The Q4_K / Q5_K halves for M >= 2 rows of F32 x: one launch per half for every row of x.
+size_t q4kx_halves_x_ws_bytes(int64_t M, int64_t N, int64_t K);
+int launch_gemv_q4kx_halves_x(const float *x, const void *w, float *out, void *ws, int64_t M, int64_t N, int64_t K,
+                              int dt, hipStream_t s);
 // out[i] += tmp[i], i < n (the second and later K parts of a split row).
 int launch_add_rows(float *out, const float *tmp, int64_t n, hipStream_t s);
 // Q8_0 / Q4_0 / Q5_0 / Q6_K rows too long to stage whole, at M <= 8: the staged GEMV on

@@ -57,6 +57,7 @@ def _w(dt, N, K, seed, dev):
     (hipq.Q8_0, 40, 1024, 2048),     # bf16 weight copy + GEMM
     (hipq.Q4_0, 24, 300, 2784),      # generic GEMV (rows of 1566 bytes)
     (hipq.Q4_K, 1, 2048, 53248),     # long rows: two K halves + an add
+    (hipq.Q4_K, 3, 2048, 53248),     # long rows, several x rows: each half's x copied out (memcpy node)
     (hipq.Q6_K, 2, 1024, 53248),     # staged K parts + adds, per x row
 ])
 def test_matmul_q_graph(dev, dt, M, N, K):
