@@ -1033,6 +1033,69 @@ int launch_staged_parts(const void *act, const void *w, float *out, float *tmp, 
   return HQ_OK;
 }
 
+// The same parts for M >= 2 rows of F32 x: each part's columns of x are copied out and
+// quantized as an (M, kn) activation, so one launch (the launcher's row tiles) serves every
+// row of x.  ws: the part's x, its act layout, then M * N floats.
+size_t staged_parts_x_ws_bytes(int dt, int64_t M, int64_t N, int64_t K) {
+  const BlockInfo bi = block_info(dt);
+  int64_t sz = 0;
+  int parts = 0;
+  if (!bi.elems || K % bi.elems || !staged_plan(dt, K / bi.elems, &sz, &parts)) return 0;
+  const int64_t kmax = sz * bi.elems;
+  auto al = [](int64_t b) { return (b + 255) & ~(int64_t)255; };
+  return (size_t)(al(4 * M * kmax) + al(act_bytes(M, kmax)) + 4 * M * N);
+}
+
+int launch_staged_parts_x(const float *x, const void *w, float *out, void *ws, int64_t M, int64_t N, int64_t K,
+                          int dt, hipStream_t s) {
+  const BlockInfo bi = block_info(dt);
+  const int64_t nb = K / bi.elems, full = nb * bi.bytes;
+  int64_t sz;
+  int parts;
+  if (!staged_plan(dt, nb, &sz, &parts)) return fail(HQ_EUNSUPPORTED, "gemv", "K=%lld", (long long)K);
+  auto al = [](int64_t b) { return (b + 255) & ~(int64_t)255; };
+  const int64_t kmax = sz * bi.elems;
+  float *xb = static_cast<float *>(ws);
+  uint8_t *ab = reinterpret_cast<uint8_t *>(ws) + al(4 * M * kmax);
+  float *tmp = reinterpret_cast<float *>(ab + al(act_bytes(M, kmax)));
+  for (int i = 0; i < parts; i++) {
+    const int64_t b0 = i * sz, nbp = std::min<int64_t>(sz, nb - b0), k0 = b0 * bi.elems, kn = nbp * bi.elems;
+    if (hipError_t e = hipMemcpy2DAsync(xb, (size_t)kn * 4, x + k0, (size_t)K * 4, (size_t)kn * 4, (size_t)M,
+                                        hipMemcpyDeviceToDevice, s))
+      return fail((int)e, "gemv", "hipMemcpy2DAsync: %s", hipGetErrorString(e));
+    if (int rc = launch_quantize_act(xb, F32, ab, M, kn, s)) return rc;
+    StagedArgs a;
+    a.act = ab;
+    a.x = nullptr;
+    a.w = static_cast<const uint8_t *>(w);
+    a.out = i ? tmp : out;
+    a.M = (int)M;
+    a.N = (int)N;
+    a.K = (int)kn;
+    a.nb = (int)nbp;
+    a.row_bytes = nbp * bi.bytes;
+    a.row_stride = full;
+    a.k0_bytes = b0 * bi.bytes;
+    a.q2_off = act_q2_off(M, kn);
+    a.d_off = act_d_off(M, kn);
+    a.s_off = act_s_off(M, kn);
+    a.lds_wave = 0;
+    a.ns = 2;
+    const int mm = M >= 3 ? (dt == Q6_K ? 2 : 4) : (int)M;  // Q6_K: at most two rows of x per pass
+    const int cpl = pick_cpl(dt == Q6_K ? nbp * 8 : nbp);
+    if (mm == 1)
+      run_staged_m<1, false>(dt, a, cpl, s);
+    else if (mm == 2)
+      run_staged_m<2, false>(dt, a, cpl, s);
+    else
+      run_staged_m<4, false>(dt, a, cpl, s);
+    if (int rc = check_launch(dt == Q6_K ? "gemv_q6k_parts" : "gemv_q80_parts")) return rc;
+    if (i)
+      if (int rc = launch_add_rows(out, tmp, M * N, s)) return rc;
+  }
+  return HQ_OK;
+}
+
 int launch_gemv_act(const void *act, const void *wv, float *out, int64_t M, int64_t N, int64_t K, int dt,
                     hipStream_t s) {
   if (N > INT32_MAX || M > 65535 * 4 || K > INT32_MAX)
@@ -1113,7 +1176,7 @@ size_t matmul_q_ws_bytes(int64_t M, int64_t N, int64_t K, int dt) {
     return std::max((size_t)(al256(act_bytes(M, K)) + 4 * M * N), q4kx_halves_x_ws_bytes(M, N, K));
   // Long staged rows (split into K parts): the parts' outputs as well.
   if ((dt == Q8_0 || dt == Q4_0 || dt == Q5_0 || dt == Q6_K) && staged_row_bytes(dt, K) + 16 > 16384)
-    return (size_t)(al256(act_bytes(M, K)) + 4 * M * N);
+    return std::max((size_t)(al256(act_bytes(M, K)) + 4 * M * N), staged_parts_x_ws_bytes(dt, M, N, K));
   return (size_t)act_bytes(M, K);
 }
 
@@ -1175,7 +1238,9 @@ int launch_matmul_q(const float *x, const void *w, float *out, int64_t M, int64_
   if ((dt == Q4_K || dt == Q5_K) && q4kx_ok(M, N, K, w, nullptr, x, dt) && q4kx_xin(K))
     return launch_gemv_q4kx(x, w, nullptr, out, M, N, K, 0, dt, s);
   if (staged_parts_ok(M, N, K, dt, w, x)) {
-    // Staged rows too long for one slice: x quantized once, then the K parts and their sum.
+    // Staged rows too long for one slice: x quantized once, then the K parts and their sum
+    // (several rows of x: each part's columns quantized on their own, one launch per part).
+    if (M > 1) return launch_staged_parts_x(x, w, out, ws, M, N, K, dt, s);
     if (int rc = launch_quantize_act(x, F32, ws, M, K, s)) return rc;
     float *tmp = reinterpret_cast<float *>(static_cast<char *>(ws) + al256(act_bytes(M, K)));
     return launch_staged_parts(ws, w, out, tmp, M, N, K, dt, s);
