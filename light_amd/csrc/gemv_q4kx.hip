@@ -2394,6 +2394,40 @@ bool int4_halves_ok(int64_t M, int64_t N, int64_t K, int G, const void *codes, c
 int launch_int4_halves(const void *x, int x_dtype, const uint32_t *codes, const float *sc, const float *zr, void *y,
                        int64_t M, int64_t N, int64_t K, int G, void *ws, hipStream_t s) {
   const int64_t kh = (K / 2 + 255) / 256 * 256;
+  auto al = [](int64_t b) { return (b + 255) & ~(int64_t)255; };
+  if (M > 1) {
+    // Several rows of x: each half's columns copied out (x's dtype) and quantized as an
+    // (M, kn) activation, one launch per half for every row (weights read once per half).
+    const int64_t esz = x_dtype == F32 ? 4 : 2;
+    uint8_t *xb = static_cast<uint8_t *>(ws), *ab = xb + al(esz * M * kh);
+    float *t0 = reinterpret_cast<float *>(ab + al(act_bytes(M, kh))), *t1 = t0 + M * N;
+    for (int h = 0; h < 2; h++) {
+      const int64_t k0 = h ? kh : 0, kn = h ? K - kh : kh;
+      if (hipError_t e = hipMemcpy2DAsync(xb, (size_t)(kn * esz), static_cast<const uint8_t *>(x) + k0 * esz,
+                                          (size_t)(K * esz), (size_t)(kn * esz), (size_t)M, hipMemcpyDeviceToDevice, s))
+        return fail((int)e, "int4_gemv", "hipMemcpy2DAsync: %s", hipGetErrorString(e));
+      if (int rc = launch_quantize_act(xb, x_dtype, ab, M, kn, s)) return rc;
+      Q4kxArgs a;
+      if (int rc = q4kx_setup(a, M, N, kn, 64, K / 2, "int4_gemv")) return rc;
+      a.ain = ab;
+      a.w0 = reinterpret_cast<const uint8_t *>(codes) + k0 / 2;
+      a.s0 = sc + k0 / G;
+      a.z0 = zr + k0 / G;
+      a.G = G;
+      a.gpr = (int)(K / G);
+      a.out = h ? t1 : t0;
+      if (int rc = dispatch_q4kx<Int4UnitT<false>, false, false, false, F32, F32, 2>(a, s)) return rc;
+    }
+    const int64_t n = M * N;
+    const unsigned g = (unsigned)cdiv(n, 256);
+    switch (x_dtype) {
+      case F32: add_halves_kernel<F32><<<g, 256, 0, s>>>(y, t0, t1, n); break;
+      case BF16: add_halves_kernel<BF16><<<g, 256, 0, s>>>(y, t0, t1, n); break;
+      case F16: add_halves_kernel<F16><<<g, 256, 0, s>>>(y, t0, t1, n); break;
+      default: return fail(HQ_EUNSUPPORTED, "int4_gemv", "x dtype %d", x_dtype);
+    }
+    return check_launch("int4_halves");
+  }
   if (int rc = launch_quantize_act(x, x_dtype, ws, M, K, s)) return rc;
   const uint8_t *act = static_cast<const uint8_t *>(ws);
   float *t0 = reinterpret_cast<float *>(static_cast<uint8_t *>(ws) + ((act_bytes(M, K) + 255) & ~(int64_t)255));

@@ -283,7 +283,12 @@ size_t int4_ws_bytes(int64_t M, int64_t N, int64_t K, int G, int x_dtype) {
   if (!int4_gemm_ok(M, K, G)) {
     // Long rows (two K halves): the halves' F32 partials as well.
     const bool halves = M <= 8 && K > 32768 && K <= 65536 && K % 256 == 0 && G > 0 && 256 % G == 0;
-    return (size_t)(halves ? ((act_bytes(M, K) + 255) & ~(int64_t)255) + 8 * M * N : act_bytes(M, K));
+    if (!halves) return (size_t)act_bytes(M, K);
+    // One row: x's act layout + two F32 partials; several rows: a half's x (up to F32), its
+    // act layout + the partials.
+    auto al = [](int64_t b) { return (b + 255) & ~(int64_t)255; };
+    const int64_t kh = (K / 2 + 255) / 256 * 256;
+    return (size_t)std::max(al(act_bytes(M, K)) + 8 * M * N, al(4 * M * kh) + al(act_bytes(M, kh)) + 8 * M * N);
   }
   return (x_dtype == BF16 ? 0 : gemm_x_bytes(M, K)) + gemm_partial_bytes(M, N, K, x_dtype == F32);
 }
